@@ -1,0 +1,516 @@
+"""CPU restatement of the GPTQ+ per-linear quantization hot path (TEST INFRASTRUCTURE ONLY).
+
+This module is the parity oracle.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker (or as the
+timed CPU baseline) -- never as the thing that produces product results.  The product
+path lives in ``gptq_plus_mp_quant_amd`` and runs hand-written gfx950 HIP kernels.
+
+It restates, op for op and in the same torch call order on CPU tensors, the reference:
+
+* ``WeightQuantizer.configure / find_params / fake_quantize / ready``
+  -- ``utils/quant_utils.py:300-331, 390-457, 471-486``
+* ``compute_safe_beta_from_reference_loss`` -- ``gptq_utils/gptq_plus_utils.py:174-194``
+* ``GPTQPlus.__init__ / add_batch / finalize_hessian`` -- ``gptq_plus_utils.py:431-487, 798-908``
+* ``GPTQPlus._compute_hessian_inverse_with_fallback`` -- ``gptq_plus_utils.py:494-561``
+* ``GPTQPlus._compute_gradient_terms`` -- ``gptq_plus_utils.py:563-578``
+* ``GPTQPlus.fasterquant`` in the default ``g_update_mode="frozen"``: find_params,
+  static / dynamic groups, dead columns, act_order, per-subgroup state, the in-block
+  column loop, the block-atomic variant, the trailing (outer) update, un-permute and
+  write-back -- ``gptq_plus_utils.py:910-1396, 1500-1570, 1850-1896``.
+
+Deviations, all opt-in:
+
+* ``dtype`` lets the same sequence run in float64 (used by the closed-form pinning tests).
+* ``stable_ties=True`` replaces ``torch.argsort(act_square, descending=True)`` (unstable on
+  exact ties on CPU) by its stable variant.  Among exactly tied ``act_square`` values the
+  reference's order is implementation-defined; the stable order (ties by ascending column
+  index) is one of the orders that call may return and is the one the HIP kernel uses.
+
+Parity pinning (see ``tests/test_oracle_*.py``): golden vectors written by importing the
+reference (``tests/golden/make_golden.py``), fp64 brute-force Hessians, scipy fp64
+Cholesky/inverse, textbook sequential OBS on tiny inputs, RTN reduction at H = I,
+blocksize invariance of the frozen GPTQ+ update, and the atomic triangular-solve identity.
+"""
+from __future__ import annotations
+
+import copy
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional
+
+import torch
+
+
+# ---------------------------------------------------------------------------------------
+# WeightQuantizer  (utils/quant_utils.py:300-486)
+# ---------------------------------------------------------------------------------------
+class WeightQuantizerOracle:
+    """Per-channel min/max weight quantizer, restating ``WeightQuantizer``.
+
+    ``configure`` -> quant_utils.py:309-331; ``find_params`` -> :390-457 (the ``mse`` grid
+    search :422-448 included); ``fake_quantize`` -> :471-480 (note: it ignores ``zero`` and
+    clamps to ``[-(maxq+1), maxq]`` even for ``sym=False``); ``ready`` -> :485-486.
+    """
+
+    def __init__(self, shape: int = 1):
+        self.maxq = torch.tensor(0)
+        self.scale = torch.zeros(shape)
+        self.zero = torch.zeros(shape)
+        self.bits = 16
+
+    def configure(self, bits, perchannel=False, sym=True, mse=False, norm=2.4, grid=50,
+                  maxshrink=0.5, weight_groupsize=-1):
+        self.bits = bits
+        self.perchannel = perchannel
+        self.sym = sym
+        self.mse = mse
+        self.norm = norm
+        self.grid = grid
+        self.maxshrink = maxshrink
+        self.weight_groupsize = weight_groupsize
+        # quant_utils.py:327-331
+        self.maxq = torch.tensor(2 ** (bits - 1) - 1) if sym else torch.tensor(2 ** bits - 1)
+
+    def find_params(self, x: torch.Tensor) -> None:
+        # quant_utils.py:390-457 (per-channel / per-tensor branch)
+        if self.bits == 16:
+            return
+        if self.weight_groupsize > 0:
+            raise NotImplementedError("weight_groupsize>0 activation-style grouping is off the hot path")
+        self.maxq = self.maxq.to(x.device)
+        shape = x.shape
+        x = x.flatten(1) if self.perchannel else x.flatten().unsqueeze(0)
+        zeros = torch.zeros(x.shape[0], device=x.device, dtype=x.dtype)
+        xmin = torch.minimum(x.min(1)[0], zeros)
+        xmax = torch.maximum(x.max(1)[0], zeros)
+        if self.sym:
+            self.scale = torch.maximum(torch.abs(xmin), xmax).clamp(min=1e-5) / self.maxq
+            self.zero = torch.zeros_like(self.scale)
+        else:
+            both_zero = (xmin == 0) & (xmax == 0)
+            xmin[both_zero] = -1
+            xmax[both_zero] = +1
+            self.scale = (xmax - xmin).clamp(min=1e-5) / self.maxq
+            self.zero = torch.round(-xmin / self.scale)
+        if self.mse:
+            self._mse_search(x, xmin, xmax)
+        if not self.perchannel:
+            self.scale = self.scale.repeat(shape[0])
+            self.zero = self.zero.repeat(shape[0])
+        out_shape = [-1] + [1] * (len(shape) - 1)
+        self.scale = self.scale.reshape(out_shape)
+        self.zero = self.zero.reshape(out_shape)
+
+    def _mse_search(self, x, xmin, xmax):
+        # quant_utils.py:422-448: shrink grid over (xmin, xmax), |q - x|^norm row error.
+        best = torch.full([x.shape[0]], float("inf"), device=x.device, dtype=x.dtype)
+        steps = int(self.maxshrink * self.grid)
+        for i in range(steps):
+            for j in range(steps):
+                xmin1 = (1 - i / self.grid) * xmin
+                xmax1 = (1 - j / self.grid) * xmax
+                if self.sym:
+                    scale1 = torch.maximum(torch.abs(xmin1), xmax1).clamp(min=1e-5) / self.maxq
+                    zero1 = torch.zeros_like(scale1)
+                    s = scale1.unsqueeze(1)
+                    q = s * torch.clamp(torch.round(x / s), -(self.maxq + 1), self.maxq)
+                else:
+                    scale1 = (xmax1 - xmin1) / self.maxq
+                    zero1 = torch.round(-xmin1 / scale1)
+                    s, z = scale1.unsqueeze(1), zero1.unsqueeze(1)
+                    q = s * (torch.clamp(torch.round(x / s) + z, 0, self.maxq) - z)
+                q -= x
+                q.abs_()
+                q.pow_(self.norm)
+                err = torch.sum(q, 1)
+                better = err < best
+                if torch.any(better):
+                    best[better] = err[better]
+                    self.scale[better] = scale1[better]
+                    self.zero[better] = zero1[better]
+
+    def fake_quantize(self, x, st_idx=None, end_idx=None):
+        # quant_utils.py:471-480
+        if self.ready() and self.bits < 16:
+            scale = self.scale.to(x.device)
+            if st_idx is not None and end_idx is not None:
+                scale = scale[st_idx:end_idx]
+            q = torch.clamp(torch.round(x / scale), -(self.maxq + 1), self.maxq)
+            return (scale * q).to(x.dtype), q, scale
+        return None, None, None
+
+    def ready(self):
+        return torch.all(self.scale != 0)
+
+
+# ---------------------------------------------------------------------------------------
+# GPTQ+ first-order term helpers
+# ---------------------------------------------------------------------------------------
+def safe_beta_from_reference_loss(gradients_sub, hinv_init, reference_loss, alpha):
+    """gptq_plus_utils.py:174-194 (``compute_safe_beta_from_reference_loss``)."""
+    ghinv_init = gradients_sub.matmul(hinv_init)
+    if reference_loss <= 0:
+        return torch.zeros(gradients_sub.shape[0], dtype=gradients_sub.dtype), ghinv_init
+    c = (gradients_sub * ghinv_init).sum(dim=1) - (
+        (ghinv_init ** 2) / torch.diagonal(hinv_init).unsqueeze(0)).mean(1)
+    target = 2 * alpha * reference_loss
+    c = torch.clamp(c, min=target)
+    ratio = torch.where(c > 0, target / c, torch.zeros_like(c))
+    ratio = torch.clamp(ratio, min=0.0, max=1.0)
+    beta = 1 - torch.sqrt(torch.clamp(1 - ratio, min=0.0))
+    beta = torch.nan_to_num(beta, nan=0.0, posinf=1.0, neginf=0.0)
+    return beta, ghinv_init
+
+
+def hessian_inverse_with_fallback(H_sub, percdamp=0.01, damp_auto_increment=0.0015):
+    """gptq_plus_utils.py:494-561.  Returns (Hinv_init, Hinv_upper, damp_percent, identity_fallback, attempts).
+
+    Damping is cumulative across retries on the same working copy; ``damp_percent >= 1``
+    gives the identity fallback.
+    """
+    damp_percent = float(percdamp)
+    if damp_percent <= 0:
+        raise ValueError(f"`damp_percent` must be positive. current is {damp_percent}")
+    H_work = H_sub.clone()
+    idx = torch.arange(H_work.shape[0])
+    attempts = 0
+    while 1 > damp_percent > 0:
+        attempts += 1
+        try:
+            damp = damp_percent * torch.mean(torch.diag(H_work))
+            H_work[idx, idx] += damp
+            chol = torch.linalg.cholesky(H_work)
+            Hinv_init = torch.cholesky_inverse(chol)
+            Hinv = torch.linalg.cholesky(Hinv_init, upper=True)
+            if not torch.isfinite(Hinv_init).all() or not torch.isfinite(Hinv).all():
+                raise torch._C._LinAlgError("non-finite Hinv")
+            return Hinv_init, Hinv, damp_percent, False, attempts
+        except torch._C._LinAlgError:
+            damp_percent += damp_auto_increment
+    if damp_percent >= 1:
+        eye = torch.eye(H_sub.shape[0], dtype=H_sub.dtype)
+        return eye, eye, damp_percent, True, attempts
+    raise ValueError(f"`damp_percent` must between 0 and 1. current is {damp_percent}")
+
+
+def gradient_terms(gradients_sub, Hinv_init, Hinv, alpha, reference_loss, rows, columns,
+                   enable_gradient_update=True):
+    """gptq_plus_utils.py:563-578.  Returns (beta, Z, GHinv, GHinv_init)."""
+    if enable_gradient_update and alpha > 0:
+        a = alpha / (rows * columns)
+        beta, GHinv_init = safe_beta_from_reference_loss(gradients_sub, Hinv_init, reference_loss, a)
+    else:
+        beta = torch.zeros([1]).to(gradients_sub)
+        GHinv_init = gradients_sub.matmul(Hinv_init)
+    beta_view = beta.unsqueeze(1)
+    Z = gradients_sub.matmul(Hinv.T) * beta_view
+    GHinv = Z.matmul(Hinv)
+    return beta, Z, GHinv, GHinv_init
+
+
+# ---------------------------------------------------------------------------------------
+# GPTQPlus (frozen mode)
+# ---------------------------------------------------------------------------------------
+@dataclass
+class SubgroupRecord:
+    row_start: int
+    row_end: int
+    perm: Optional[torch.Tensor]
+    invperm: Optional[torch.Tensor]
+    Hinv_init: torch.Tensor
+    Hinv: torch.Tensor
+    damp_percent: float
+    identity_fallback: bool
+    attempts: int
+    beta: torch.Tensor
+    Z: torch.Tensor
+    GHinv: torch.Tensor
+    W_sub_initial: torch.Tensor
+
+
+@dataclass
+class FasterquantResult:
+    Q: torch.Tensor            # (R, C) dequantized weight in the layer dtype (natural order)
+    Q_fp32: torch.Tensor       # (R, C) same before the dtype cast
+    W_int: torch.Tensor        # (R, C) integer-valued codes (compute dtype), natural order
+    Scale: torch.Tensor        # (R, C) per-element scale, natural order
+    subgroups: List[SubgroupRecord] = field(default_factory=list)
+
+
+class GPTQPlusOracle:
+    """Restates ``GPTQPlus`` (gptq_plus_utils.py:430-1896) for the default frozen mode.
+
+    ``weight`` is the layer weight (R, C) (any float dtype); ``saliency`` (N, T, G);
+    ``gradient`` (R, C).  ``quantizer`` must be assigned and configured by the caller,
+    exactly as ``build_gptq_for_subset`` does (gptq_plus_utils.py:6981-6987).
+    """
+
+    def __init__(self, weight, saliency, gradient, num_groups, alpha, reference_loss,
+                 hessian_saliency_scale=1.0, dtype=torch.float32):
+        self.weight = weight.clone()
+        self.rows, self.columns = weight.shape
+        self.dtype = dtype
+        self.num_groups = num_groups
+        assert self.num_groups == saliency.shape[2], "Number of groups must match saliency shape"
+        self.alpha = alpha
+        self.reference_loss = max(reference_loss, 0)
+        self.hessian_saliency_scale = float(hessian_saliency_scale)
+        self.saliencies = saliency.to(dtype)
+        self.gradients = gradient.to(dtype)
+        self.H = torch.zeros((num_groups, self.columns, self.columns), dtype=dtype)
+        self.act_square = torch.zeros((self.columns,), dtype=dtype)
+        self.nsamples = saliency.shape[0]
+        self.index = 0
+        self.token_count = 0
+        self._finalized = False
+        self.quantizer: Optional[WeightQuantizerOracle] = None
+        assert self.rows % self.num_groups == 0, "rows must be divisible by num_groups"
+
+    # gptq_plus_utils.py:798-857
+    @torch.no_grad()
+    def add_batch(self, inp, out=None):
+        if self._finalized:
+            raise RuntimeError("add_batch called after finalize_hessian. Re-init GPTQPlus to reuse.")
+        if inp.dim() == 2:
+            inp = inp.unsqueeze(0)
+        assert inp.dim() == 3
+        bsz = inp.shape[0]
+        sal = self.saliencies[self.index:self.index + bsz]
+        self.index += bsz
+        if sal.dim() == 3 and inp.shape[1] > sal.shape[1]:
+            inp = inp[:, inp.shape[1] - sal.shape[1]:]
+        inp = inp.reshape(-1, inp.shape[-1]).to(self.dtype)
+        sal = sal.reshape(-1, sal.shape[-1]).to(self.dtype)
+        n_tokens = inp.shape[0]
+        weighted = inp.unsqueeze(0).mul(sal.transpose(0, 1).unsqueeze(-1))
+        block = torch.bmm(inp.transpose(0, 1).unsqueeze(0).expand(self.num_groups, -1, -1), weighted)
+        self.H.add_(block)
+        self.act_square.add_((inp ** 2).sum(0))
+        self.token_count += n_tokens
+
+    # gptq_plus_utils.py:859-908 (world size 1: the all-reduces are identities)
+    @torch.no_grad()
+    def finalize_hessian(self):
+        if self._finalized:
+            return
+        total_samples = float(self.index)
+        total_tokens = float(self.token_count)
+        if total_samples <= 0 or total_tokens <= 0:
+            raise RuntimeError("finalize_hessian called before any add_batch ran.")
+        seq_len = total_tokens / total_samples
+        self.H.div_(total_samples * seq_len)
+        if self.hessian_saliency_scale != 1.0:
+            self.H.div_(self.hessian_saliency_scale)
+        self.act_square.div_(seq_len)
+        self.H = 0.5 * (self.H + self.H.transpose(-1, -2))
+        if not torch.isfinite(self.H).all():
+            self.H = torch.nan_to_num(self.H, nan=0.0, posinf=0.0, neginf=0.0)
+        self._finalized = True
+
+    # gptq_plus_utils.py:910-1896, frozen mode only
+    @torch.no_grad()
+    def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
+                    static_groups=False, enable_gradient_update=True, g_update_mode="frozen",
+                    block_atomic_quant=False, stable_ties=False) -> FasterquantResult:
+        if g_update_mode != "frozen":
+            raise NotImplementedError("oracle covers g_update_mode='frozen' only")
+        dt = self.dtype
+        W = self.weight.clone().to(dt)
+        quantizer = self.quantizer
+        Q_final = torch.zeros_like(W)
+        W_int_final = torch.zeros_like(W)
+        Scale_final = torch.zeros_like(W)
+
+        if not quantizer.ready():
+            quantizer.find_params(W)                                   # :978-980
+
+        dynamic_groups = groupsize != -1 and not static_groups         # :982-987
+        if dynamic_groups and groupsize != blocksize:
+            raise ValueError("`groupsize` must equal `blocksize` when using dynamic groups in GPTQ+.")
+
+        shared_groups = None
+        if groupsize != -1 and static_groups:                          # :994-1002
+            shared_groups = []
+            for col_start in range(0, self.columns, groupsize):
+                col_end = min(col_start + groupsize, self.columns)
+                qz = copy.deepcopy(quantizer)
+                qz.find_params(W[:, col_start:col_end])
+                shared_groups.append(qz)
+
+        fast = groupsize == -1 and quantizer.bits < 16 and bool(quantizer.ready())   # :1008-1020
+        if fast:
+            fast_scale_full = quantizer.scale
+            fast_maxq = int(quantizer.maxq.item())
+            fast_lo = -(fast_maxq + 1)
+
+        rows_per_sub = self.rows // self.num_groups
+        states = []
+        records: List[SubgroupRecord] = []
+        for sub in range(self.num_groups):                             # :1027-1162
+            r0, r1 = sub * rows_per_sub, (sub + 1) * rows_per_sub
+            W_sub = W[r0:r1, :].clone()
+            H_sub = self.H[sub].clone()
+            G_sub = self.gradients[r0:r1, :].to(dt).clone()
+            dead = torch.diag(H_sub) == 0
+            H_sub[dead, dead] = 1
+            W_sub[:, dead] = 0
+            perm = invperm = None
+            if actorder:
+                perm = torch.argsort(self.act_square, descending=True, stable=stable_ties)
+                W_sub = W_sub[:, perm]
+                H_sub = H_sub[perm][:, perm]
+                G_sub = G_sub[:, perm]
+                invperm = torch.argsort(perm)
+            Hinv_init, Hinv, damp, fallback, attempts = hessian_inverse_with_fallback(H_sub, percdamp)
+            beta, Z, GHinv, _ = gradient_terms(G_sub, Hinv_init, Hinv, self.alpha, self.reference_loss,
+                                               self.rows, self.columns, enable_gradient_update)
+            records.append(SubgroupRecord(r0, r1, perm, invperm, Hinv_init, Hinv, damp, fallback,
+                                          attempts, beta, Z.clone(), GHinv.clone(), W_sub.clone()))
+            states.append(dict(r0=r0, r1=r1, W_sub=W_sub, Hinv=Hinv, Z=Z, GHinv=GHinv, perm=perm,
+                               invperm=invperm, Q=torch.zeros_like(W_sub),
+                               W_int=torch.zeros_like(W_sub), Scale=torch.zeros_like(W_sub),
+                               fast_scale=fast_scale_full[r0:r1] if fast else None))
+
+        for i1 in range(0, self.columns, blocksize):                   # :1169
+            i2 = min(i1 + blocksize, self.columns)
+            count = i2 - i1
+            atomic = block_atomic_quant and i2 < self.columns          # :1174
+            D = torch.arange(count - 1, -1, -1).to(W)
+            block_states = []
+            for st in states:
+                W1 = st["W_sub"][:, i1:i2].clone()
+                W_block_start = W1.clone()
+                Q1 = torch.zeros_like(W1)
+                W_int1 = torch.zeros_like(W1)
+                Scale1 = torch.zeros_like(W1)
+                Err1 = torch.zeros_like(W1)
+                Hinv1 = st["Hinv"][i1:i2, i1:i2]
+                GHinv1 = st["GHinv"][:, i1:i2].clone()
+                Z1 = st["Z"][:, i1:i2]
+                dyn_q = None
+                if dynamic_groups:                                     # :1202-1209
+                    dyn_q = copy.deepcopy(quantizer)
+                    dyn_q.find_params(W_block_start)
+                if st["fast_scale"] is not None:
+                    Scale1.copy_(st["fast_scale"].expand_as(Scale1))
+
+                def column_quantizer(i):
+                    if dyn_q is not None:
+                        return dyn_q, None, None
+                    if groupsize != -1:
+                        idx = i1 + i
+                        if actorder:
+                            idx = st["perm"][idx]
+                        return shared_groups[idx // groupsize], st["r0"], st["r1"]
+                    return quantizer, st["r0"], st["r1"]
+
+                if atomic:                                             # :1238-1288
+                    if groupsize == -1:
+                        q, iw, sc = quantizer.fake_quantize(W_block_start, st_idx=st["r0"], end_idx=st["r1"])
+                        Q1.copy_(q)
+                        W_int1.copy_(iw)
+                        Scale1.copy_(sc.expand_as(W_block_start))
+                    else:
+                        for i in range(count):
+                            qz, a, b = column_quantizer(i)
+                            q, iw, sc = qz.fake_quantize(W_block_start[:, i].unsqueeze(1), st_idx=a, end_idx=b)
+                            Q1[:, i] = q.flatten()
+                            W_int1[:, i] = iw.flatten()
+                            Scale1[:, i] = sc.flatten()
+                    residual = W_block_start - Q1 - GHinv1
+                    Err1.copy_(torch.linalg.solve_triangular(Hinv1.T, residual.T, upper=False).T)
+                else:                                                  # :1296-1367
+                    for i in range(count):
+                        w = W1[:, i]
+                        d = Hinv1[i, i]
+                        w_col = w.unsqueeze(1)
+                        if st["fast_scale"] is not None:
+                            fs = st["fast_scale"]
+                            iw = torch.clamp(torch.round(w_col / fs), fast_lo, fast_maxq)
+                            q_fake = (fs * iw).to(w_col.dtype)
+                            sc = fs
+                        else:
+                            qz, a, b = column_quantizer(i)
+                            q_fake, iw, sc = qz.fake_quantize(w_col, st_idx=a, end_idx=b)
+                        q = q_fake.flatten()
+                        Q1[:, i] = q
+                        W_int1[:, i] = iw.flatten()
+                        if st["fast_scale"] is None:
+                            Scale1[:, i] = sc.flatten()
+                        err1 = (w - q - GHinv1[:, i]) / d
+                        upd = err1.unsqueeze(1).matmul(Hinv1[i, i:].unsqueeze(0))
+                        W1[:, i:] -= upd + GHinv1[:, i:]
+                        Err1[:, i] = err1
+                        GHinv1[:, i:].sub_(Z1[:, i].unsqueeze(1).matmul(Hinv1[i, i:].unsqueeze(0)))
+                st["Q"][:, i1:i2] = Q1
+                st["W_int"][:, i1:i2] = W_int1
+                st["Scale"][:, i1:i2] = Scale1
+                block_states.append((st, Err1, Z1))
+
+            for st, Err1, Z1 in block_states:                          # :1500-1570 (frozen)
+                GHinv_rest = st["GHinv"][:, i2:]
+                G_Update = count * GHinv_rest - torch.einsum("ij,j,jk->ik", Z1, D, st["Hinv"][i1:i2, i2:])
+                second = Err1.matmul(st["Hinv"][i1:i2, i2:])
+                st["W_sub"][:, i2:] -= second + G_Update
+                st["GHinv"][:, i2:] -= st["Z"][:, i1:i2].matmul(st["Hinv"][i1:i2, i2:])
+
+        for st in states:                                              # :1850-1864
+            Q, W_int_sub, Scale_sub = st["Q"], st["W_int"], st["Scale"]
+            if actorder:
+                Q = Q[:, st["invperm"]]
+                W_int_sub = W_int_sub[:, st["invperm"]]
+                Scale_sub = Scale_sub[:, st["invperm"]]
+            Q_final[st["r0"]:st["r1"], :] = Q
+            W_int_final[st["r0"]:st["r1"], :] = W_int_sub
+            Scale_final[st["r0"]:st["r1"], :] = Scale_sub
+
+        Q_out = Q_final.reshape(self.weight.shape).to(self.weight.dtype)   # :1873-1875
+        if torch.any(torch.isnan(Q_out)):
+            raise ValueError("NaN in weights")
+        return FasterquantResult(Q=Q_out, Q_fp32=Q_final, W_int=W_int_final, Scale=Scale_final,
+                                 subgroups=records)
+
+
+# ---------------------------------------------------------------------------------------
+# Convenience drivers used by tests and the CPU baseline
+# ---------------------------------------------------------------------------------------
+def make_quantizer(bits, sym=True, mse=False) -> WeightQuantizerOracle:
+    q = WeightQuantizerOracle()
+    q.configure(bits, perchannel=True, sym=sym, mse=mse)
+    return q
+
+
+def run_linear(weight, X, saliency, gradient, num_groups, bits=4, sym=True, alpha=0.0,
+               reference_loss=0.0, accum_bsz=16, blocksize=128, percdamp=0.01, groupsize=-1,
+               actorder=True, static_groups=None, block_atomic_quant=False, stable_ties=False,
+               dtype=torch.float32):
+    """Drive one linear like ``build_gptq_for_subset`` + ``accumulate_hessian_for_gptq`` +
+    ``fasterquant`` (gptq_plus_utils.py:6954-7039, 7467-7502).  X is (N, T, C)."""
+    if static_groups is None:
+        static_groups = actorder
+    g = GPTQPlusOracle(weight, saliency, gradient, num_groups, alpha, reference_loss, dtype=dtype)
+    g.quantizer = make_quantizer(bits, sym)
+    for j in range(0, X.shape[0], accum_bsz):
+        g.add_batch(X[j:j + accum_bsz])
+    g.finalize_hessian()
+    res = g.fasterquant(blocksize=blocksize, percdamp=percdamp, groupsize=groupsize, actorder=actorder,
+                        static_groups=static_groups, block_atomic_quant=block_atomic_quant,
+                        stable_ties=stable_ties)
+    return g, res
+
+
+def reconstruction_error(W, Q, X):
+    """Layer reconstruction error ||(W - Q) X^T||^2 / ||W X^T||^2 over tokens X (n, C), in float64."""
+    W = W.double()
+    Q = Q.double()
+    X = X.reshape(-1, X.shape[-1]).double()
+    num = ((W - Q) @ X.T).pow(2).sum()
+    den = (W @ X.T).pow(2).sum()
+    return float(num / den)
+
+
+__all__ = [
+    "WeightQuantizerOracle", "GPTQPlusOracle", "FasterquantResult", "SubgroupRecord",
+    "safe_beta_from_reference_loss", "hessian_inverse_with_fallback", "gradient_terms",
+    "make_quantizer", "run_linear", "reconstruction_error",
+]

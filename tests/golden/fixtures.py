@@ -1,0 +1,75 @@
+"""Loader for the golden vectors written by ``make_golden.py`` (data only, no reference code)."""
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+import torch
+
+PATH = Path(__file__).resolve().parent / "golden_cases.npz"
+
+
+def unpack_upper(flat: np.ndarray, n: int, symmetric: bool) -> np.ndarray:
+    out = np.zeros((n, n), dtype=flat.dtype)
+    iu = np.triu_indices(n)
+    out[iu] = flat
+    if symmetric:
+        il = np.tril_indices(n, -1)
+        out[il] = out.T[il]
+    return out
+
+
+@dataclass
+class GoldenCase:
+    meta: dict
+    arrays: dict
+
+    @property
+    def name(self):
+        return self.meta["name"]
+
+    def t(self, key):
+        return torch.from_numpy(np.array(self.arrays[key]))
+
+    def H(self):
+        C, G = self.meta["C"], self.meta["G"]
+        flat = self.arrays["H_upper"]
+        return torch.from_numpy(np.stack([unpack_upper(flat[g], C, True) for g in range(G)]))
+
+    def sub(self, s, tag):
+        key = f"sub{s}_{tag}"
+        if key not in self.arrays:
+            return None
+        a = self.arrays[key]
+        C = self.meta["C"]
+        if tag == "Hinv_init":
+            a = unpack_upper(a, C, True)
+        elif tag == "Hinv_upper_cholesky":
+            a = unpack_upper(a, C, False)
+        return torch.from_numpy(np.array(a))
+
+
+class GoldenSet:
+    def __init__(self, cases, beta):
+        self.cases = cases
+        self.beta = beta
+
+    @classmethod
+    def load(cls):
+        z = np.load(PATH, allow_pickle=False)
+        meta = json.loads(bytes(z["__meta__"]).decode())
+        cases = []
+        for m in meta:
+            prefix = m["name"] + "__"
+            arrays = {k[len(prefix):]: z[k] for k in z.files if k.startswith(prefix)}
+            cases.append(GoldenCase(m, arrays))
+        beta = {k: z[k] for k in z.files if k.startswith("beta")}
+        return cls(cases, beta)
+
+    def by_name(self, name):
+        for c in self.cases:
+            if c.name == name:
+                return c
+        raise KeyError(name)
