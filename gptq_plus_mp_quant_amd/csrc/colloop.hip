@@ -1,0 +1,356 @@
+// The fasterquant block loop (gptq_utils/gptq_plus_utils.py:1169-1372) and the trailing
+// (outer) update (:1500-1570), frozen mode, all subgroups in one launch each.
+//
+// k_quant_block: rows are independent, so each row of the block is owned by a quad of 4
+// lanes; lane t of the quad holds columns t, t+4, t+8, ... of the row in registers (W1, GHinv1,
+// Z1), 64 rows per 256-thread workgroup, one subgroup per workgroup.  The B x B block of
+// Hinv (upper) sits in LDS.  Column i = 4m + r is quantised by lane r of every quad, its error
+// is broadcast inside the quad with a DPP quad_perm move, and every lane applies the rank-1
+// update to its own columns.  After each group of 4 columns the register slots rotate down
+// by one so every slot index is a compile-time constant.  Arithmetic follows the reference
+// op by op (no contraction, IEEE divide, round-half-even):
+//   code = clamp(rint(w / s), -(maxq+1), maxq); q = s * code
+//   err  = ((w - q) - gh_i) / Hinv1[i][i]
+//   w_j  = w_j - (err * Hinv1[i][j] + gh_j);   gh_j = gh_j - z_i * Hinv1[i][j]     (j >= i)
+// so with identical inputs codes and errors are bit-identical to the reference's CPU loop.
+// The atomic variant (:1238-1288) quantises the block start at once and solves
+// Err * Hinv1 = W - Q - GHinv1 by forward substitution with the same quad layout.
+//
+// k_trailing: W[:, i2:] -= Err Hinv[i1:i2, i2:] + (count GH[:, i2:] - (Z1 D) Hinv[i1:i2, i2:])
+// and GH[:, i2:] -= Z1 Hinv[i1:i2, i2:], 64x64 output tiles, fp32 16x16x4 MFMA, K = count
+// streamed through LDS in slabs of 32.  The Z terms are skipped when Z is identically zero.
+#include "rq_common.h"
+
+namespace {
+
+constexpr int QB_MAXB = 128;
+constexpr int16_t RQ_CODE_NAN = -32768;
+
+template <int CTRL>
+__device__ __forceinline__ float quad_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_lane(float v, int r) {
+  switch (r) {
+    case 0: return quad_bcast<0x00>(v);
+    case 1: return quad_bcast<0x55>(v);
+    case 2: return quad_bcast<0xAA>(v);
+    default: return quad_bcast<0xFF>(v);
+  }
+}
+
+struct QBArgs {
+  float* Wp;
+  int64_t ldw;
+  const float* Hinv;
+  int C;
+  const float* GH;
+  const float* Z;
+  int64_t ldgh;
+  int R, R_s, i1, count, qmode;
+  const float* scale;
+  const int32_t* col_group;
+  float* dyn_scale;
+  float maxq;
+  int sym, atomic;
+  const int* z_nonzero;
+  int16_t* codes;
+  float* err;
+};
+
+template <int SLOTS>
+__global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
+  __shared__ float Hl[QB_MAXB][QB_MAXB];
+  const int tid = threadIdx.x;
+  const int t = tid & 3;
+  const int sub = blockIdx.y;
+  const int row_local = blockIdx.x * 64 + (tid >> 2);
+  const bool valid = row_local < a.R_s;
+  const int row = sub * a.R_s + (valid ? row_local : 0);
+  const int count = a.count, i1 = a.i1;
+  const float* Hs = a.Hinv + (int64_t)sub * a.C * a.C;
+  const bool use_gh = (*a.z_nonzero != 0);
+
+  for (int e = tid; e < QB_MAXB * QB_MAXB; e += 256) {
+    const int i = e / QB_MAXB, j = e % QB_MAXB;
+    Hl[i][j] = (i < count && j < count && j >= i) ? Hs[(int64_t)(i1 + i) * a.C + (i1 + j)] : 0.0f;
+  }
+
+  float w[SLOTS], gh[SLOTS], zz[SLOTS], sc[SLOTS];
+#pragma unroll
+  for (int k = 0; k < SLOTS; ++k) {
+    const int col = 4 * k + t;
+    const bool in = valid && col < count;
+    const int64_t off = (int64_t)row * a.ldw + i1 + col;
+    w[k] = in ? a.Wp[off] : 0.0f;
+    const int64_t og = (int64_t)row * a.ldgh + i1 + col;
+    gh[k] = (in && use_gh) ? a.GH[og] : 0.0f;
+    zz[k] = (in && use_gh) ? a.Z[og] : 0.0f;
+    sc[k] = 0.0f;
+    if (a.qmode == RQ_QMODE_STATIC && in) sc[k] = a.scale[(int64_t)a.col_group[i1 + col] * a.R + row];
+  }
+  const float lo = -(a.maxq + 1.0f), hi = a.maxq;
+  float srow = 0.0f;
+  if (a.qmode == RQ_QMODE_CHANNEL) {
+    srow = a.scale[row];
+  } else if (a.qmode == RQ_QMODE_DYNAMIC) {
+    // find_params on the block start (gptq_plus_utils.py:1208-1209): per-row min/max
+    float mn = __builtin_inff(), mx = -__builtin_inff();
+#pragma unroll
+    for (int k = 0; k < SLOTS; ++k) {
+      if (4 * k + t < count) {
+        mn = rq_nan_min(mn, w[k]);
+        mx = rq_nan_max(mx, w[k]);
+      }
+    }
+    mn = rq_nan_min(mn, quad_bcast<0xB1>(mn));
+    mx = rq_nan_max(mx, quad_bcast<0xB1>(mx));
+    mn = rq_nan_min(mn, quad_bcast<0x4E>(mn));
+    mx = rq_nan_max(mx, quad_bcast<0x4E>(mx));
+    float z;
+    rq_params_from_minmax(mn, mx, a.maxq, a.sym, &srow, &z);
+    if (valid && t == 0) a.dyn_scale[row] = srow;
+  }
+  __syncthreads();
+
+  int16_t* crow = a.codes + (int64_t)row * a.C + i1;
+  float* erow = a.err + (int64_t)row * count;
+  const int nmacro = (count + 3) / 4;
+
+  if (a.atomic) {
+    // Q1 = quant(W_block_start); res = W_block_start - Q1 - GHinv1   (:1243-1282)
+#pragma unroll
+    for (int k = 0; k < SLOTS; ++k) {
+      const int col = 4 * k + t;
+      const float s = (a.qmode == RQ_QMODE_STATIC) ? sc[k] : srow;
+      const float code = rq_quant_code(w[k], s, lo, hi);
+      const float q = s * code;
+      if (valid && col < count) crow[col] = (code != code) ? RQ_CODE_NAN : (int16_t)code;
+      w[k] = (w[k] - q) - gh[k];
+    }
+    // Err1 * Hinv1 = res, forward substitution (:1283-1288)
+    for (int m = 0; m < nmacro; ++m) {
+      const int nlive = (count - 4 * m + 3) / 4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 4 * m + r;
+        if (i < count) {
+          const float d = Hl[i][i];
+          const float e_own = w[0] / d;
+          const float e = quad_lane(e_own, r);
+          if (valid && t == r) erow[i] = e;
+#pragma unroll
+          for (int k = 0; k < SLOTS; ++k) {
+            if (k < nlive) {
+              const float h = Hl[i][4 * (m + k) + t];
+              w[k] = w[k] - e * h;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k + 1 < SLOTS; ++k) w[k] = w[k + 1];
+      w[SLOTS - 1] = 0.0f;
+    }
+    return;
+  }
+
+  // column-serial loop (:1296-1367)
+  for (int m = 0; m < nmacro; ++m) {
+    const int nlive = (count - 4 * m + 3) / 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 4 * m + r;
+      if (i < count) {
+        const float d = Hl[i][i];
+        const float s = (a.qmode == RQ_QMODE_STATIC) ? sc[0] : srow;
+        const float x = w[0];
+        const float code = rq_quant_code(x, s, lo, hi);
+        const float q = s * code;
+        const float e_own = ((x - q) - gh[0]) / d;
+        const float e = quad_lane(e_own, r);
+        if (valid && t == r) {
+          crow[i] = (code != code) ? RQ_CODE_NAN : (int16_t)code;
+          erow[i] = e;
+        }
+        if (use_gh) {
+          const float zi = quad_lane(zz[0], r);
+#pragma unroll
+          for (int k = 0; k < SLOTS; ++k) {
+            if (k < nlive) {
+              const float h = Hl[i][4 * (m + k) + t];
+              const float upd = e * h;
+              w[k] = w[k] - (upd + gh[k]);
+              gh[k] = gh[k] - zi * h;
+            }
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < SLOTS; ++k) {
+            if (k < nlive) {
+              const float h = Hl[i][4 * (m + k) + t];
+              w[k] = w[k] - (e * h + gh[k]);
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k + 1 < SLOTS; ++k) {
+      w[k] = w[k + 1];
+      gh[k] = gh[k + 1];
+      zz[k] = zz[k + 1];
+      sc[k] = sc[k + 1];
+    }
+    w[SLOTS - 1] = 0.0f;
+    gh[SLOTS - 1] = 0.0f;
+    zz[SLOTS - 1] = 0.0f;
+    sc[SLOTS - 1] = 0.0f;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+struct TrArgs {
+  float* Wp;
+  int64_t ldw;
+  float* GH;
+  const float* Z;
+  int64_t ldgh;
+  const float* Hinv;
+  int C, R, R_s, i1, count;
+  const float* err;
+  const int* z_nonzero;
+};
+
+constexpr int TKS = 32;  // K slab
+constexpr int TPAD = 4;
+
+__global__ __launch_bounds__(256) void k_trailing(TrArgs a) {
+  __shared__ float Es[TKS][64 + TPAD];
+  __shared__ float Zs[TKS][64 + TPAD];
+  __shared__ float Hs[TKS][64 + TPAD];
+  const int i2 = a.i1 + a.count;
+  const int sub = blockIdx.z;
+  const int rl0 = blockIdx.y * 64;
+  const int c0 = i2 + blockIdx.x * 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const bool use_z = (*a.z_nonzero != 0);
+  const float* Hsub = a.Hinv + (int64_t)sub * a.C * a.C;
+  const int rbase = sub * a.R_s;
+
+  floatx4 acc1[2][2], acc2[2][2], acc3[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc1[x][y][e] = acc2[x][y][e] = acc3[x][y][e] = 0.0f;
+
+  for (int k0 = 0; k0 < a.count; k0 += TKS) {
+    __syncthreads();
+    // err / Z slabs: 64 rows x 32 k, stored k-major; H slab: 32 k x 64 cols
+    for (int e = tid; e < 64 * TKS; e += 256) {
+      const int rr = e / TKS, kk = e % TKS;
+      const int rl = rl0 + rr, k = k0 + kk;
+      const bool in = rl < a.R_s && k < a.count;
+      Es[kk][rr] = in ? a.err[(int64_t)(rbase + rl) * a.count + k] : 0.0f;
+      if (use_z) Zs[kk][rr] = in ? a.Z[(int64_t)(rbase + rl) * a.ldgh + a.i1 + k] : 0.0f;
+    }
+    for (int e = tid; e < TKS * 64; e += 256) {
+      const int kk = e / 64, cc = e % 64;
+      const int k = k0 + kk, c = c0 + cc;
+      Hs[kk][cc] = (k < a.count && c < a.C) ? Hsub[(int64_t)(a.i1 + k) * a.C + c] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < TKS / 4; ++kk) {
+      const int k = kk * 4 + (lane >> 4);
+      const float b0 = Hs[k][wc * 32 + (lane & 15)];
+      const float b1 = Hs[k][wc * 32 + 16 + (lane & 15)];
+      const float e0 = Es[k][wr * 32 + (lane & 15)];
+      const float e1 = Es[k][wr * 32 + 16 + (lane & 15)];
+      acc1[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(e0, b0, acc1[0][0], 0, 0, 0);
+      acc1[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(e0, b1, acc1[0][1], 0, 0, 0);
+      acc1[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(e1, b0, acc1[1][0], 0, 0, 0);
+      acc1[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(e1, b1, acc1[1][1], 0, 0, 0);
+      if (use_z) {
+        const float dk = (float)(a.count - 1 - (k0 + k));
+        const float z0 = Zs[k][wr * 32 + (lane & 15)];
+        const float z1 = Zs[k][wr * 32 + 16 + (lane & 15)];
+        const float zd0 = z0 * dk, zd1 = z1 * dk;
+        acc2[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(zd0, b0, acc2[0][0], 0, 0, 0);
+        acc2[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(zd0, b1, acc2[0][1], 0, 0, 0);
+        acc2[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(zd1, b0, acc2[1][0], 0, 0, 0);
+        acc2[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(zd1, b1, acc2[1][1], 0, 0, 0);
+        acc3[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(z0, b0, acc3[0][0], 0, 0, 0);
+        acc3[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(z0, b1, acc3[0][1], 0, 0, 0);
+        acc3[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(z1, b0, acc3[1][0], 0, 0, 0);
+        acc3[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(z1, b1, acc3[1][1], 0, 0, 0);
+      }
+    }
+  }
+
+  const float cnt = (float)a.count;
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int rl = rl0 + wr * 32 + x * 16 + 4 * (lane >> 4) + e;
+        const int c = c0 + wc * 32 + y * 16 + (lane & 15);
+        if (rl < a.R_s && c < a.C) {
+          const int64_t ow = (int64_t)(rbase + rl) * a.ldw + c;
+          if (use_z) {
+            const int64_t og = (int64_t)(rbase + rl) * a.ldgh + c;
+            const float g = a.GH[og];
+            const float gupd = cnt * g - acc2[x][y][e];
+            a.Wp[ow] = a.Wp[ow] - (acc1[x][y][e] + gupd);
+            a.GH[og] = g - acc3[x][y][e];
+          } else {
+            a.Wp[ow] = a.Wp[ow] - acc1[x][y][e];
+          }
+        }
+      }
+}
+
+}  // namespace
+
+extern "C" int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int C, const float* GH,
+                              const float* Z, int64_t ldgh, int R, int R_s, int i1, int count,
+                              int qmode, const float* scale, const int32_t* col_group,
+                              float* dyn_scale, int maxq, int sym, int atomic,
+                              const int* z_nonzero, int16_t* codes, float* err, void* stream) {
+  if (!Wp || !Hinv_all || !GH || !Z || !z_nonzero || !codes || !err) return RQ_EINVAL;
+  if (R <= 0 || R_s <= 0 || R % R_s != 0 || C <= 0 || ldw < C || ldgh < C) return RQ_EINVAL;
+  if (count <= 0 || count > QB_MAXB || i1 < 0 || i1 + count > C || maxq <= 0) return RQ_EINVAL;
+  if (qmode == RQ_QMODE_CHANNEL && !scale) return RQ_EINVAL;
+  if (qmode == RQ_QMODE_STATIC && (!scale || !col_group)) return RQ_EINVAL;
+  if (qmode == RQ_QMODE_DYNAMIC && !dyn_scale) return RQ_EINVAL;
+  if (qmode < 0 || qmode > 2) return RQ_EINVAL;
+  QBArgs a{Wp, ldw, Hinv_all, C, GH, Z, ldgh, R, R_s, i1, count, qmode, scale, col_group,
+           dyn_scale, (float)maxq, sym, atomic, z_nonzero, codes, err};
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid((R_s + 63) / 64, R / R_s), block(256);
+  if (count <= 32) hipLaunchKernelGGL(k_quant_block<8>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(k_quant_block<32>, grid, block, 0, s, a);
+  RQ_CHECK_LAUNCH();
+  return RQ_OK;
+}
+
+extern "C" int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float* Z, int64_t ldgh,
+                                  const float* Hinv_all, int C, int R, int R_s, int i1, int count,
+                                  const float* err, const int* z_nonzero, void* stream) {
+  if (!Wp || !GH || !Z || !Hinv_all || !err || !z_nonzero) return RQ_EINVAL;
+  if (R <= 0 || R_s <= 0 || R % R_s != 0 || C <= 0 || ldw < C || ldgh < C) return RQ_EINVAL;
+  if (count <= 0 || i1 < 0 || i1 + count > C) return RQ_EINVAL;
+  const int i2 = i1 + count;
+  if (i2 >= C) return RQ_OK;
+  TrArgs a{Wp, ldw, GH, Z, ldgh, Hinv_all, C, R, R_s, i1, count, err, z_nonzero};
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid((C - i2 + 63) / 64, (R_s + 63) / 64, R / R_s), block(256);
+  hipLaunchKernelGGL(k_trailing, grid, block, 0, s, a);
+  RQ_CHECK_LAUNCH();
+  return RQ_OK;
+}

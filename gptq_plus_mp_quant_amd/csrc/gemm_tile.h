@@ -1,0 +1,219 @@
+// 64x64-tile MFMA GEMM shared by the Cholesky chain (fp64) and the GPTQ+ setup GEMMs (fp32).
+//
+//   C[i, j] (op)= alpha * sum_k A(i, k) B(k, j)        i < M, j < N, k in [k_lo(tile), k_hi(tile))
+//   A(i, k) = TA ? A[k*lda + i] : A[i*lda + k]        B(k, j) = TB ? B[j*ldb + k] : B[k*ldb + j]
+//
+// 256 threads = 4 waves in a 2x2 arrangement, 32x32 per wave as 2x2 blocks of the 16x16x4
+// MFMA (v_mfma_f32_16x16x4f32 / v_mfma_f64_16x16x4f64).  K advances in slabs of 16 through
+// LDS; the next slab is fetched into registers while the current one is multiplied.
+// Triangular operands are handled by restricting the K range per output tile (the invalid
+// triangle of every operand used here is stored as explicit zeros).
+#pragma once
+#include "rq_common.h"
+
+namespace rq {
+
+template <typename T>
+struct Mfma16;
+template <>
+struct Mfma16<float> {
+  using acc_t = floatx4;
+  static __device__ __forceinline__ acc_t op(float a, float b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma16<double> {
+  using acc_t = doublex4;
+  static __device__ __forceinline__ acc_t op(double a, double b, acc_t c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+};
+
+// K-range restriction per output tile (tile origin i0, j0; 64 wide).
+enum KRange : int {
+  KR_FULL = 0,
+  KR_B_UPPER = 1,   // B(k, j) == 0 for k > j   -> k < j0 + 64
+  KR_B_LOWER = 2,   // B(k, j) == 0 for k < j   -> k >= j0
+  KR_AB_LOWER = 3,  // A(i,k)==0 for k<i and B(k,j)==0 for k<j -> k >= max(i0, j0)
+};
+
+// Epilogue modes.
+enum Epi : int {
+  EPI_STORE = 0,     // C = alpha * acc
+  EPI_ACCUM = 1,     // C = C + alpha * acc
+};
+
+template <typename T>
+struct GemmArgs {
+  const T* A;
+  int64_t lda;
+  const T* B;
+  int64_t ldb;
+  T* Cm;
+  int64_t ldc;
+  int M, N, K;
+  T alpha;
+  int epi;
+  int krange;
+  int lower_only;            // skip output tiles strictly above the diagonal
+  const T* row_scale;        // optional epilogue factor: row_scale[row_bcast ? 0 : i]
+  int row_bcast;
+  int* nz_flag;              // optional: set to 1 when any stored value is non-zero or NaN
+  const int* skip_if_zero;   // optional: when *skip_if_zero == 0 store zeros and return
+  const int* abort_flag;     // optional: when *abort_flag != 0 return immediately
+};
+
+constexpr int GT = 64;
+constexpr int GKT = 16;
+constexpr int GPAD = 4;
+
+template <typename T, bool TA, bool TB>
+__global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
+  using acc_t = typename Mfma16<T>::acc_t;
+  __shared__ T As[GKT][GT + GPAD];
+  __shared__ T Bs[GKT][GT + GPAD];
+
+  if (p.abort_flag && *p.abort_flag) return;
+  const int ti = blockIdx.y, tj = blockIdx.x;
+  if (p.lower_only && tj > ti) return;
+  const int i0 = ti * GT, j0 = tj * GT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+
+  if (p.skip_if_zero && *p.skip_if_zero == 0) {
+    for (int e = tid; e < GT * GT; e += 256) {
+      const int i = i0 + e / GT, j = j0 + e % GT;
+      if (i < p.M && j < p.N) p.Cm[(int64_t)i * p.ldc + j] = T(0);
+    }
+    return;
+  }
+
+  int k_lo = 0, k_hi = p.K;
+  if (p.krange == KR_B_UPPER) k_hi = min(p.K, j0 + GT);
+  else if (p.krange == KR_B_LOWER) k_lo = j0;
+  else if (p.krange == KR_AB_LOWER) k_lo = max(i0, j0);
+  k_lo = (k_lo / GKT) * GKT;
+
+  acc_t acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[a][b][e] = T(0);
+
+  T ra[4], rb[4];
+  // A slab: 64 (i) x 16 (k).  B slab: 16 (k) x 64 (j).
+  auto fetch = [&](int k0) {
+    if (!TA) {  // A[i][k]: 4 consecutive k per thread
+      const int i = i0 + (tid >> 2), kq = k0 + (tid & 3) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        ra[e] = (i < p.M && kq + e < k_hi) ? p.A[(int64_t)i * p.lda + kq + e] : T(0);
+    } else {    // A[k][i]: 4 consecutive i per thread
+      const int k = k0 + (tid >> 4), iq = i0 + (tid & 15) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        ra[e] = (k < k_hi && iq + e < p.M) ? p.A[(int64_t)k * p.lda + iq + e] : T(0);
+    }
+    if (!TB) {  // B[k][j]: 4 consecutive j
+      const int k = k0 + (tid >> 4), jq = j0 + (tid & 15) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        rb[e] = (k < k_hi && jq + e < p.N) ? p.B[(int64_t)k * p.ldb + jq + e] : T(0);
+    } else {    // B[j][k]: 4 consecutive k
+      const int j = j0 + (tid >> 2), kq = k0 + (tid & 3) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        rb[e] = (j < p.N && kq + e < k_hi) ? p.B[(int64_t)j * p.ldb + kq + e] : T(0);
+    }
+  };
+  auto stash = [&]() {
+    if (!TA) {
+      const int i = tid >> 2, kq = (tid & 3) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) As[kq + e][i] = ra[e];
+    } else {
+      const int k = tid >> 4, iq = (tid & 15) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) As[k][iq + e] = ra[e];
+    }
+    if (!TB) {
+      const int k = tid >> 4, jq = (tid & 15) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Bs[k][jq + e] = rb[e];
+    } else {
+      const int j = tid >> 2, kq = (tid & 3) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Bs[kq + e][j] = rb[e];
+    }
+  };
+
+  if (k_lo < k_hi) {
+    fetch(k_lo);
+    for (int k0 = k_lo; k0 < k_hi; k0 += GKT) {
+      __syncthreads();
+      stash();
+      __syncthreads();
+      if (k0 + GKT < k_hi) fetch(k0 + GKT);
+#pragma unroll
+      for (int kk = 0; kk < GKT / 4; ++kk) {
+        const int k = kk * 4 + (lane >> 4);
+        const T a0 = As[k][wr * 32 + (lane & 15)];
+        const T a1 = As[k][wr * 32 + 16 + (lane & 15)];
+        const T b0 = Bs[k][wc * 32 + (lane & 15)];
+        const T b1 = Bs[k][wc * 32 + 16 + (lane & 15)];
+        acc[0][0] = Mfma16<T>::op(a0, b0, acc[0][0]);
+        acc[0][1] = Mfma16<T>::op(a0, b1, acc[0][1]);
+        acc[1][0] = Mfma16<T>::op(a1, b0, acc[1][0]);
+        acc[1][1] = Mfma16<T>::op(a1, b1, acc[1][1]);
+      }
+    }
+  }
+
+  // 16x16 block layout: row = 4*(lane/16) + e, col = lane % 16.
+  int nz = 0;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = i0 + wr * 32 + a * 16 + 4 * (lane >> 4) + e;
+        const int j = j0 + wc * 32 + b * 16 + (lane & 15);
+        if (i < p.M && j < p.N) {
+          T v = p.alpha * acc[a][b][e];
+          if (p.row_scale) v = v * p.row_scale[p.row_bcast ? 0 : i];
+          T* c = p.Cm + (int64_t)i * p.ldc + j;
+          if (p.epi == EPI_ACCUM) v = *c + v;
+          *c = v;
+          nz |= (v != T(0)) || (v != v);
+        }
+      }
+  if (p.nz_flag && nz) atomicOr(p.nz_flag, 1);
+}
+
+template <typename T>
+inline int launch_gemm(const GemmArgs<T>& a, bool ta, bool tb, hipStream_t s) {
+  if (a.M <= 0 || a.N <= 0) return RQ_OK;
+  dim3 grid((a.N + GT - 1) / GT, (a.M + GT - 1) / GT), block(256);
+  if (!ta && !tb) hipLaunchKernelGGL((k_gemm_tile<T, false, false>), grid, block, 0, s, a);
+  else if (!ta && tb) hipLaunchKernelGGL((k_gemm_tile<T, false, true>), grid, block, 0, s, a);
+  else if (ta && !tb) hipLaunchKernelGGL((k_gemm_tile<T, true, false>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((k_gemm_tile<T, true, true>), grid, block, 0, s, a);
+  return hipGetLastError() == hipSuccess ? RQ_OK : RQ_EHIP;
+}
+
+template <typename T>
+inline GemmArgs<T> gemm_args(const T* A, int64_t lda, const T* B, int64_t ldb, T* Cm, int64_t ldc,
+                             int M, int N, int K, T alpha, int epi) {
+  GemmArgs<T> g{};
+  g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.Cm = Cm; g.ldc = ldc;
+  g.M = M; g.N = N; g.K = K; g.alpha = alpha; g.epi = epi;
+  g.krange = KR_FULL; g.lower_only = 0; g.row_scale = nullptr; g.row_bcast = 0;
+  g.nz_flag = nullptr; g.skip_if_zero = nullptr; g.abort_flag = nullptr;
+  return g;
+}
+
+}  // namespace rq

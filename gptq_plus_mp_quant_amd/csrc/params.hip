@@ -1,0 +1,252 @@
+// Quantizer parameters, act_order permutation, per-subgroup gathers and the final write-back.
+//  - rq_find_params:      WeightQuantizer.find_params, per-channel min/max (utils/quant_utils.py:390-421),
+//                         also per static column group (gptq_utils/gptq_plus_utils.py:994-1002)
+//  - rq_act_order_perm:   argsort(act_square, descending) + argsort(perm) (gptq_plus_utils.py:1046-1050)
+//  - rq_prepare_subgroup: row slice, dead columns, act_order gathers of W, G and H (:1033-1050)
+//  - rq_writeback:        un-permute, dequantize, cast to the layer dtype, export buffers (:1850-1896)
+// All of these are HBM-bound gathers / reductions.
+#include "rq_common.h"
+
+namespace {
+
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = rq_nan_min(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = rq_nan_max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// One wavefront per (row, group).
+template <typename TW>
+__global__ __launch_bounds__(256) void k_find_params(const TW* __restrict__ w, int R, int C,
+                                                     int64_t ldw, int gs, float maxq, int sym,
+                                                     float* __restrict__ scale,
+                                                     float* __restrict__ zero) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int grp = blockIdx.y;
+  if (r >= R) return;
+  const int c0 = grp * gs;
+  const int c1 = min(C, c0 + gs);
+  const TW* row = w + (int64_t)r * ldw;
+  float mn = __builtin_inff(), mx = -__builtin_inff();
+  for (int c = c0 + lane; c < c1; c += 64) {
+    const float v = rq_load_elem(row + c);
+    mn = rq_nan_min(mn, v);
+    mx = rq_nan_max(mx, v);
+  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  if (lane == 0) {
+    float s, z;
+    rq_params_from_minmax(mn, mx, maxq, sym, &s, &z);
+    scale[(int64_t)grp * R + r] = s;
+    zero[(int64_t)grp * R + r] = z;
+  }
+}
+
+// a sorts strictly before b in a descending sort with NaN first (torch orders NaN as largest).
+__device__ __forceinline__ bool desc_before(float a, float b) {
+  const bool na = (a != a), nb = (b != b);
+  if (na) return !nb;
+  if (nb) return false;
+  return a > b;
+}
+__device__ __forceinline__ bool same_key(float a, float b) {
+  return ((a != a) && (b != b)) || (a == b);
+}
+
+// Stable descending rank sort: rank_i = #{j : key_j before key_i, or tie and j < i}.
+__global__ __launch_bounds__(256) void k_rank_desc(const float* __restrict__ key, int C,
+                                                   int64_t* __restrict__ perm,
+                                                   int64_t* __restrict__ invperm) {
+  __shared__ float tilek[1024];
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const float ki = (i < C) ? key[i] : 0.0f;
+  int rank = 0;
+  for (int base = 0; base < C; base += 1024) {
+    __syncthreads();
+    for (int t = threadIdx.x; t < 1024; t += 256) tilek[t] = (base + t < C) ? key[base + t] : 0.0f;
+    __syncthreads();
+    const int n = min(1024, C - base);
+    for (int t = 0; t < n; ++t) {
+      const float kj = tilek[t];
+      const int j = base + t;
+      rank += (desc_before(kj, ki) || (same_key(kj, ki) && j < i)) ? 1 : 0;
+    }
+  }
+  if (i < C) {
+    perm[rank] = i;
+    invperm[i] = rank;
+  }
+}
+
+template <typename TW>
+__global__ __launch_bounds__(256) void k_gather_w(const TW* __restrict__ w, int64_t ldw,
+                                                  const float* __restrict__ Hg, int R_s, int C,
+                                                  const int64_t* __restrict__ perm,
+                                                  float* __restrict__ out, int64_t ldo) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= C) return;
+  const int64_t p = perm ? perm[j] : j;
+  const bool dead = Hg[p * C + p] == 0.0f;
+  for (int r = blockIdx.y; r < R_s; r += gridDim.y)
+    out[(int64_t)r * ldo + j] = dead ? 0.0f : rq_load_elem(w + (int64_t)r * ldw + p);
+}
+
+__global__ __launch_bounds__(256) void k_gather_g(const float* __restrict__ g, int64_t ldg, int R_s,
+                                                  int C, const int64_t* __restrict__ perm,
+                                                  float* __restrict__ out, int64_t ldo) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= C) return;
+  const int64_t p = perm ? perm[j] : j;
+  for (int r = blockIdx.y; r < R_s; r += gridDim.y) out[(int64_t)r * ldo + j] = g[(int64_t)r * ldg + p];
+}
+
+__global__ __launch_bounds__(256) void k_gather_h(const float* __restrict__ Hg, int C,
+                                                  const int64_t* __restrict__ perm,
+                                                  float* __restrict__ out) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= C) return;
+  const int64_t pj = perm ? perm[j] : j;
+  for (int i = blockIdx.y; i < C; i += gridDim.y) {
+    const int64_t pi = perm ? perm[i] : i;
+    float v = Hg[pi * C + pj];
+    if (i == j && v == 0.0f) v = 1.0f;            // H_sub[dead, dead] = 1
+    out[(int64_t)i * C + j] = v;
+  }
+}
+
+template <typename TQ>
+__device__ __forceinline__ TQ rq_cast(float v);
+template <>
+__device__ __forceinline__ __half rq_cast<__half>(float v) { return __float2half_rn(v); }
+template <>
+__device__ __forceinline__ __hip_bfloat16 rq_cast<__hip_bfloat16>(float v) { return __float2bfloat16(v); }
+template <>
+__device__ __forceinline__ float rq_cast<float>(float v) { return v; }
+
+template <typename TQ>
+__global__ __launch_bounds__(256) void k_writeback(const int16_t* __restrict__ codes, int R, int C,
+                                                   const int64_t* __restrict__ invperm, int qmode,
+                                                   const float* __restrict__ scale,
+                                                   const int32_t* __restrict__ col_group,
+                                                   const float* __restrict__ dyn_scale, int bs,
+                                                   TQ* __restrict__ q_out, int64_t ldq,
+                                                   float* __restrict__ w_int_out,
+                                                   float* __restrict__ scale_out,
+                                                   int* __restrict__ nan_flag) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  const int64_t j = invperm ? invperm[c] : c;
+  int nan_seen = 0;
+  for (int r = blockIdx.y; r < R; r += gridDim.y) {
+    const float code = (float)codes[(int64_t)r * C + j];
+    float s;
+    if (qmode == RQ_QMODE_CHANNEL) s = scale[r];
+    else if (qmode == RQ_QMODE_STATIC) s = scale[(int64_t)col_group[j] * R + r];
+    else s = dyn_scale[(j / bs) * (int64_t)R + r];
+    const TQ q = rq_cast<TQ>(s * code);
+    q_out[(int64_t)r * ldq + c] = q;
+    const float qf = (float)q;
+    nan_seen |= (qf != qf);
+    if (w_int_out) w_int_out[(int64_t)r * C + c] = code;
+    if (scale_out) scale_out[(int64_t)r * C + c] = s;
+  }
+  if (nan_seen && nan_flag) atomicOr(nan_flag, 1);
+}
+
+inline int rows_grid(int rows) { return rows < 1024 ? rows : 1024; }
+
+}  // namespace
+
+extern "C" int rq_find_params(const void* w, int w_dtype, int R, int C, int64_t ldw, int group_size,
+                              int maxq, int sym, float* scale, float* zero, void* stream) {
+  if (!w || !scale || !zero || R <= 0 || C <= 0 || ldw < C || maxq <= 0) return RQ_EINVAL;
+  const int gs = group_size > 0 ? group_size : C;
+  const int ng = (C + gs - 1) / gs;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid((R + 3) / 4, ng), block(256);
+  if (w_dtype == RQ_F16)
+    hipLaunchKernelGGL(k_find_params<__half>, grid, block, 0, s, (const __half*)w, R, C, ldw, gs,
+                       (float)maxq, sym, scale, zero);
+  else if (w_dtype == RQ_BF16)
+    hipLaunchKernelGGL(k_find_params<__hip_bfloat16>, grid, block, 0, s, (const __hip_bfloat16*)w, R,
+                       C, ldw, gs, (float)maxq, sym, scale, zero);
+  else if (w_dtype == RQ_F32)
+    hipLaunchKernelGGL(k_find_params<float>, grid, block, 0, s, (const float*)w, R, C, ldw, gs,
+                       (float)maxq, sym, scale, zero);
+  else
+    return RQ_EINVAL;
+  RQ_CHECK_LAUNCH();
+  return RQ_OK;
+}
+
+extern "C" int rq_act_order_perm(const float* act_sq, int C, int64_t* perm, int64_t* invperm,
+                                 void* stream) {
+  if (!act_sq || !perm || !invperm || C <= 0) return RQ_EINVAL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_rank_desc, dim3((C + 255) / 256), dim3(256), 0, s, act_sq, C, perm, invperm);
+  RQ_CHECK_LAUNCH();
+  return RQ_OK;
+}
+
+extern "C" int rq_prepare_subgroup(const void* w, int w_dtype, int64_t ldw, const float* grad,
+                                   int64_t ldg, const float* H_g, int R_s, int C,
+                                   const int64_t* perm, float* W_sub, int64_t ld_wsub, float* G_sub,
+                                   int64_t ld_gsub, float* H_sub, void* stream) {
+  if (!w || !H_g || !W_sub || !H_sub || R_s <= 0 || C <= 0 || ldw < C || ld_wsub < C) return RQ_EINVAL;
+  if (grad && (!G_sub || ldg < C || ld_gsub < C)) return RQ_EINVAL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 gw((C + 255) / 256, rows_grid(R_s)), block(256);
+  if (w_dtype == RQ_F16)
+    hipLaunchKernelGGL(k_gather_w<__half>, gw, block, 0, s, (const __half*)w, ldw, H_g, R_s, C, perm,
+                       W_sub, ld_wsub);
+  else if (w_dtype == RQ_BF16)
+    hipLaunchKernelGGL(k_gather_w<__hip_bfloat16>, gw, block, 0, s, (const __hip_bfloat16*)w, ldw, H_g,
+                       R_s, C, perm, W_sub, ld_wsub);
+  else if (w_dtype == RQ_F32)
+    hipLaunchKernelGGL(k_gather_w<float>, gw, block, 0, s, (const float*)w, ldw, H_g, R_s, C, perm,
+                       W_sub, ld_wsub);
+  else
+    return RQ_EINVAL;
+  RQ_CHECK_LAUNCH();
+  if (grad) {
+    hipLaunchKernelGGL(k_gather_g, gw, block, 0, s, grad, ldg, R_s, C, perm, G_sub, ld_gsub);
+    RQ_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(k_gather_h, dim3((C + 255) / 256, rows_grid(C)), block, 0, s, H_g, C, perm, H_sub);
+  RQ_CHECK_LAUNCH();
+  return RQ_OK;
+}
+
+extern "C" int rq_writeback(const int16_t* codes, int R, int C, const int64_t* invperm, int qmode,
+                            const float* scale, const int32_t* col_group, const float* dyn_scale,
+                            int blocksize, void* q_out, int q_dtype, int64_t ldq, float* w_int_out,
+                            float* scale_out, int* nan_flag, void* stream) {
+  if (!codes || !q_out || R <= 0 || C <= 0 || ldq < C) return RQ_EINVAL;
+  if (qmode == RQ_QMODE_CHANNEL && !scale) return RQ_EINVAL;
+  if (qmode == RQ_QMODE_STATIC && (!scale || !col_group)) return RQ_EINVAL;
+  if (qmode == RQ_QMODE_DYNAMIC && (!dyn_scale || blocksize <= 0)) return RQ_EINVAL;
+  if (qmode < 0 || qmode > 2) return RQ_EINVAL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid((C + 255) / 256, rows_grid(R)), block(256);
+  if (q_dtype == RQ_F16)
+    hipLaunchKernelGGL(k_writeback<__half>, grid, block, 0, s, codes, R, C, invperm, qmode, scale,
+                       col_group, dyn_scale, blocksize, (__half*)q_out, ldq, w_int_out, scale_out, nan_flag);
+  else if (q_dtype == RQ_BF16)
+    hipLaunchKernelGGL(k_writeback<__hip_bfloat16>, grid, block, 0, s, codes, R, C, invperm, qmode,
+                       scale, col_group, dyn_scale, blocksize, (__hip_bfloat16*)q_out, ldq, w_int_out,
+                       scale_out, nan_flag);
+  else if (q_dtype == RQ_F32)
+    hipLaunchKernelGGL(k_writeback<float>, grid, block, 0, s, codes, R, C, invperm, qmode, scale,
+                       col_group, dyn_scale, blocksize, (float*)q_out, ldq, w_int_out, scale_out, nan_flag);
+  else
+    return RQ_EINVAL;
+  RQ_CHECK_LAUNCH();
+  return RQ_OK;
+}

@@ -1,0 +1,62 @@
+// Shared definitions for the gfx950 GPTQ+ hot-path kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+#include "../../include/gptqplus_hip.h"
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef double doublex4 __attribute__((ext_vector_type(4)));
+
+#define RQ_CHECK_LAUNCH()                                   \
+  do {                                                      \
+    if (hipGetLastError() != hipSuccess) return RQ_EHIP;    \
+  } while (0)
+
+__device__ __forceinline__ float rq_load_elem(const __half* p) { return __half2float(*p); }
+__device__ __forceinline__ float rq_load_elem(const __hip_bfloat16* p) { return __bfloat162float(*p); }
+__device__ __forceinline__ float rq_load_elem(const float* p) { return *p; }
+
+// torch.minimum / torch.maximum semantics: NaN propagates.
+__device__ __forceinline__ float rq_nan_min(float a, float b) { return (a != a || a < b) ? a : b; }
+__device__ __forceinline__ float rq_nan_max(float a, float b) { return (a != a || a > b) ? a : b; }
+// torch.clamp(x, min=lo): NaN stays NaN.
+__device__ __forceinline__ float rq_clamp_min(float x, float lo) { return (x < lo) ? lo : x; }
+
+// One element of WeightQuantizer.fake_quantize (utils/quant_utils.py:471-480):
+// code = clamp(round_half_even(x / scale), -(maxq+1), maxq); q = scale * code.
+// Division is IEEE correctly rounded (hipcc default), no contraction (-ffp-contract=off).
+__device__ __forceinline__ float rq_quant_code(float x, float scale, float lo, float hi) {
+  float r = __builtin_rintf(x / scale);
+  // torch.clamp: NaN propagates; otherwise min/max.
+  r = (r < lo) ? lo : r;
+  r = (r > hi) ? hi : r;
+  return r;
+}
+
+// WeightQuantizer.find_params per-channel branch (utils/quant_utils.py:408-421) for one row,
+// given the row's NaN-propagating min and max.
+__device__ __forceinline__ void rq_params_from_minmax(float rmin, float rmax, float maxq, int sym,
+                                                      float* scale_out, float* zero_out) {
+  float xmin = rq_nan_min(rmin, 0.0f);
+  float xmax = rq_nan_max(rmax, 0.0f);
+  if (sym) {
+    float m = rq_nan_max(fabsf(xmin), xmax);
+    *scale_out = rq_clamp_min(m, 1e-5f) / maxq;
+    *zero_out = 0.0f;
+  } else {
+    if (xmin == 0.0f && xmax == 0.0f) {
+      xmin = -1.0f;
+      xmax = 1.0f;
+    }
+    float s = rq_clamp_min(xmax - xmin, 1e-5f) / maxq;
+    *scale_out = s;
+    *zero_out = __builtin_rintf(-xmin / s);
+  }
+}
+
+__device__ __forceinline__ int rq_isfinite(float x) { return (x == x) && (fabsf(x) <= 3.402823466e38f); }
+__device__ __forceinline__ int rq_isfinite(double x) { return (x == x) && (fabs(x) <= 1.7976931348623157e308); }

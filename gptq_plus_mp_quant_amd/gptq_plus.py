@@ -1,0 +1,338 @@
+"""Drop-in ``GPTQPlus`` (reference: gptq_utils/gptq_plus_utils.py:430-1896, frozen mode) whose
+arithmetic runs in the gfx950 HIP kernels of ``libgptqplus_hip.so``.
+
+The constructor, ``add_batch`` / ``finalize_hessian`` / ``fasterquant`` / ``free`` signatures,
+the public fields the layer-wise driver reads (``H``, ``act_square``, ``gradients``,
+``saliencies``, ``reference_loss``, ``token_count``, ``index``, ``quantizer``), the error
+behaviour and the side effects (``layer.weight.data`` replaced by the dequantized weight in
+the layer dtype, ``int_weight`` / ``scale`` buffers with ``export_to_et``) follow the
+reference.  Additionally exposed for inspection: ``perm``, ``invperm``, ``codes`` (natural
+column order), ``subgroup_info`` (damping, retries, identity fallback, beta).
+
+Modes whose work needs a layer backward or a clipping search (``g_update_mode`` other than
+``"frozen"``, ``WeightQuantizer(mse=True)``, ``diagnostic_recorder``) raise
+``NotImplementedError`` rather than silently running different arithmetic.
+"""
+from __future__ import annotations
+
+import contextlib
+import logging
+from typing import Optional
+
+import torch
+
+from . import _native as nat
+from . import kernels as K
+from .quant_utils import WeightQuantizer
+
+_NULL = contextlib.nullcontext()
+MAX_BLOCKSIZE = 128
+
+
+def _section(rec, name):
+    return rec.section(name) if rec is not None else _NULL
+
+
+class GPTQPlus:
+    # gptq_plus_utils.py:431-487
+    def __init__(self, layer, saliency: torch.Tensor, gradient: torch.Tensor, num_groups: int,
+                 alpha: float, reference_loss: float, hessian_saliency_scale: float = 1.0):
+        self.layer = layer
+        self.dev = layer.weight.device
+        nat.require_gpu(layer.weight, "layer.weight")
+        nat.load()
+        W = layer.weight.data
+        self.rows, self.columns = W.shape[0], W.shape[1]
+        self.num_groups = num_groups
+        assert self.num_groups == saliency.shape[2], "Number of groups for GuidedQuant must match saliency shape!"
+        self.alpha = alpha
+        self.reference_loss = max(reference_loss, 0)
+        self.hessian_saliency_scale = float(hessian_saliency_scale)
+        self.saliencies = saliency.float()
+        self.gradients = gradient.float()
+        self.H = torch.zeros((self.num_groups, self.columns, self.columns), device=self.dev)
+        self.act_square = torch.zeros((self.columns,), device=self.dev)
+        self.nsamples = saliency.shape[0]
+        self.index = 0
+        self.token_count = 0
+        self._finalized = False
+        self.profile_recorder = None
+        self.quantizer: Optional[WeightQuantizer] = None
+        self.perm = None
+        self.invperm = None
+        self.subgroup_info = []
+        self._codes_perm = None
+        assert self.rows % self.num_groups == 0, (
+            f"Number of rows ({self.rows}) must be divisible by num_groups ({self.num_groups})")
+
+    # gptq_plus_utils.py:798-857
+    @torch.no_grad()
+    def add_batch(self, inp: torch.Tensor, out=None):
+        if self._finalized:
+            raise RuntimeError("add_batch called after finalize_hessian. Re-init GPTQPlus to reuse.")
+        rec = self.profile_recorder
+        with _section(rec, "add_batch.total"):
+            if inp.dim() == 2:
+                inp = inp.unsqueeze(0)
+            else:
+                assert inp.dim() == 3, "Input must be 2D or 3D. Got %dD." % inp.dim()
+            nat.require_gpu(inp, "add_batch input")
+            bsz = inp.shape[0]
+            sal = self.saliencies[self.index:self.index + bsz]
+            self.index += bsz
+            if sal.dim() == 3 and inp.shape[1] > sal.shape[1]:
+                inp = inp[:, inp.shape[1] - sal.shape[1]:]
+            x = inp.reshape(-1, inp.shape[-1])
+            if x.stride(1) != 1 or x.stride(0) < x.shape[1]:
+                x = x.contiguous()
+            if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+                x = x.float()
+            s = sal.reshape(-1, sal.shape[-1]).to(self.dev, torch.float32).contiguous()
+            n_tokens = x.shape[0]
+            if s.shape[0] != n_tokens:
+                raise ValueError(f"saliency rows ({s.shape[0]}) do not match tokens ({n_tokens})")
+            K.hessian_accum(x, s, self.H, self.act_square)
+            self.token_count += n_tokens
+
+    # gptq_plus_utils.py:859-908 (single GPU: the all-reduces are identities)
+    @torch.no_grad()
+    def finalize_hessian(self):
+        if self._finalized:
+            return
+        total_samples = float(self.index)
+        total_tokens = float(self.token_count)
+        if total_samples <= 0 or total_tokens <= 0:
+            raise RuntimeError("finalize_hessian called before any add_batch ran.")
+        seq_len = total_tokens / total_samples
+        nonfinite = torch.zeros(1, dtype=torch.int32, device=self.dev)
+        K.hessian_finalize(self.H, self.act_square, total_samples * seq_len, self.hessian_saliency_scale,
+                           seq_len, nonfinite)
+        n_bad = int(nonfinite.item())
+        if n_bad:
+            logging.warning("finalize_hessian: %d non-finite entries in H sanitised to 0 (module=%s)",
+                            n_bad, self.layer.__class__.__name__)
+        self._finalized = True
+
+    # gptq_plus_utils.py:494-561
+    def _hessian_inverse(self, H_work, Hinv_out, Hinv_init_out, workspace, percdamp,
+                         damp_auto_increment=0.0015, log_context=""):
+        damp_percent = float(percdamp)
+        if damp_percent <= 0:
+            raise ValueError(f"Quantization{log_context}: `damp_percent` must be positive. current is {damp_percent}")
+        info = torch.zeros(1, dtype=torch.int32, device=self.dev)
+        C = self.columns
+        attempts = 0
+        while 1 > damp_percent > 0:
+            attempts += 1
+            K.chol_hinv_attempt(H_work, damp_percent, workspace, Hinv_out, Hinv_init_out, info)
+            if int(info.item()) == 0:
+                return damp_percent, False, attempts
+            logging.warning("Quantization%s: Current `damp_percent = %.5f` is too low, auto-incrementing by `%.5f`",
+                            log_context, damp_percent, damp_auto_increment)
+            damp_percent += damp_auto_increment
+        if damp_percent >= 1:
+            logging.warning("Quantization%s: `damp_percent` reached %.5f; falling back to identity "
+                            "Hessian inverse for this subgroup.", log_context, damp_percent)
+            eye = torch.eye(C, device=self.dev)
+            Hinv_out.copy_(eye)
+            if Hinv_init_out is not None:
+                Hinv_init_out.copy_(eye)
+            return damp_percent, True, attempts
+        raise ValueError(f"Quantization{log_context}: `damp_percent` must between 0 and 1. current is {damp_percent}")
+
+    # gptq_plus_utils.py:910-1896 (frozen mode)
+    @torch.no_grad()
+    def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
+                    static_groups=False, enable_gradient_update=True, g_update_mode="frozen",
+                    export_to_et=False, profile_recorder=None, gradient_refresh_fn=None,
+                    grad_lr=1e-3, grad_optimizer="sgd", curvature_damping=0.1,
+                    grad_reg_strategy="none", grad_reg_lambda=0.0, grad_gate_floor=0.1,
+                    grad_gate_sharpness=1.0, grad_gate_sine_amp=0.0, second_order_scale=1.0,
+                    block_atomic_quant=False, block_observer=None, grad_clip=1.0,
+                    diagnostic_recorder=None, slide_refresh_start=0, slide_refresh_block_total=None,
+                    refresh_full_metrics=False, keep_hinv=False, inject=None):
+        """Quantize ``layer.weight`` in place (gptq_plus_utils.py:910-1896, frozen mode).
+
+        Extra keyword arguments (not in the reference):
+          keep_hinv -- keep ``Hinv_all``, ``Hinv_init_all``, ``Z`` and ``GHinv`` on the object.
+          inject    -- parity-test hook: ``{"perm": LongTensor[C], "hinv": [(Hinv_init, Hinv), ...]}``
+                       replaces the act_order permutation and/or each subgroup's inverse factors
+                       so the block loop can be compared against another implementation on
+                       identical inputs.
+        """
+        rec = profile_recorder or self.profile_recorder
+        inject = inject or {}
+        inject_hinv = inject.get("hinv")
+        self._validate(grad_reg_strategy, grad_reg_lambda, grad_gate_floor, grad_gate_sharpness,
+                       grad_gate_sine_amp)
+        if g_update_mode != "frozen":
+            raise NotImplementedError(f"g_update_mode={g_update_mode!r} needs a layer backward; only "
+                                      "'frozen' runs on the HIP path")
+        if diagnostic_recorder is not None:
+            raise NotImplementedError("diagnostic_recorder dumps are not produced by the HIP path")
+        if not self._finalized:
+            raise RuntimeError("fasterquant called before finalize_hessian")
+        q = self.quantizer
+        if q is None or q.bits >= 16:
+            raise ValueError("fasterquant needs a configured WeightQuantizer with bits < 16")
+        if blocksize > MAX_BLOCKSIZE or blocksize <= 0:
+            raise NotImplementedError(f"blocksize must be in [1, {MAX_BLOCKSIZE}] on the HIP path")
+
+        dev, R, C, G = self.dev, self.rows, self.columns, self.num_groups
+        R_s = R // G
+        W = self.layer.weight.data
+        if W.stride(1) != 1:
+            W = W.contiguous()
+        maxq = int(q.maxq)
+        sym = int(bool(q.sym))
+        f32 = dict(device=dev, dtype=torch.float32)
+
+        with _section(rec, "fasterquant.total"):
+            if not q.ready():
+                with _section(rec, "fasterquant.quantizer_find_params_initial"):
+                    q.find_params(W)
+            dynamic_groups = groupsize != -1 and not static_groups
+            if dynamic_groups and groupsize != blocksize:
+                raise ValueError("`groupsize` must equal `blocksize` when using dynamic groups in GPTQ+. "
+                                 f"Got groupsize={groupsize}, blocksize={blocksize}.")
+            if dynamic_groups and grad_reg_strategy in {"quant_error_gate", "quant_error_gate_optimized"}:
+                raise ValueError("Dynamic weight groups are not supported with quant_error_gate regularization yet.")
+
+            if groupsize == -1:
+                qmode = nat.RQ_QMODE_CHANNEL
+                scale_tab = q.scale.reshape(-1).to(**f32).contiguous()
+                if scale_tab.numel() != R:
+                    raise ValueError("quantizer scale must hold one value per output row")
+            elif static_groups:
+                qmode = nat.RQ_QMODE_STATIC
+                with _section(rec, "fasterquant.quantizer_build_groups"):
+                    scale_tab, _ = q.params_on(W, groupsize)
+            else:
+                qmode = nat.RQ_QMODE_DYNAMIC
+                scale_tab = None
+
+            # act_order: one permutation, argsort(act_square, descending), for every subgroup
+            perm = invperm = None
+            if actorder:
+                if inject.get("perm") is not None:
+                    perm = inject["perm"].to(dev, torch.int64).contiguous()
+                    invperm = torch.argsort(perm)
+                else:
+                    perm, invperm = K.act_order_perm(self.act_square)
+            col_group = None
+            if qmode == nat.RQ_QMODE_STATIC:
+                cols = perm if perm is not None else torch.arange(C, device=dev)
+                col_group = (cols // groupsize).to(torch.int32).contiguous()
+
+            Wp = torch.empty((R, C), **f32)
+            Z = torch.empty((R, C), **f32)
+            GH = torch.empty((R, C), **f32)
+            Hinv_all = torch.empty((G, C, C), **f32)
+            H_work = torch.empty((C, C), **f32)
+            beta_mode = 1 if (enable_gradient_update and self.alpha > 0) else 0
+            want_init = beta_mode == 1 or keep_hinv
+            workspace = K.chol_workspace(C, dev) if inject_hinv is None else None
+            Gs = torch.empty((R_s, C), **f32)
+            GH0 = torch.empty((R_s, C), **f32) if beta_mode == 1 else None
+            z_flags = torch.zeros(G, dtype=torch.int32, device=dev)
+            grads = self.gradients.to(**f32)
+            if grads.stride(1) != 1:
+                grads = grads.contiguous()
+            alpha_eff = self.alpha / (R * C) if beta_mode == 1 else 0.0
+            self.subgroup_info = []
+            hinv_init_keep = []
+            for sub in range(G):
+                r0 = sub * R_s
+                Hinit = torch.empty((C, C), **f32) if want_init else None
+                with _section(rec, "fasterquant.subgroup.slice_inputs"):
+                    K.prepare_subgroup(W[r0:], grads[r0:], self.H[sub], perm, Wp[r0:r0 + R_s], Gs, H_work)
+                with _section(rec, "fasterquant.subgroup.compute_hinv"):
+                    if inject_hinv is None:
+                        damp, fallback, attempts = self._hessian_inverse(
+                            H_work, Hinv_all[sub], Hinit, workspace, percdamp, log_context=f" subgroup={sub}")
+                    else:   # test hook: use a given (Hinv_init, Hinv) pair for this subgroup
+                        Hinv_all[sub].copy_(inject_hinv[sub][1])
+                        if Hinit is not None:
+                            Hinit.copy_(inject_hinv[sub][0])
+                        damp, fallback, attempts = float(percdamp), False, 0
+                beta = torch.empty(R_s if beta_mode == 1 else 1, **f32)
+                with _section(rec, "fasterquant.subgroup.init_ghinv"):
+                    K.gptqplus_terms(Gs, Hinit, Hinv_all[sub], alpha_eff, float(self.reference_loss),
+                                     beta_mode, beta, Z[r0:r0 + R_s], GH[r0:r0 + R_s], GH0, z_flags[sub:sub + 1])
+                if beta_mode == 1 and self.reference_loss <= 0:
+                    beta = torch.zeros(R_s, **f32)
+                self.subgroup_info.append(dict(damp_percent=damp, identity_fallback=fallback,
+                                               attempts=attempts, beta=beta))
+                if keep_hinv:
+                    hinv_init_keep.append(Hinit)
+            del H_work, workspace, Gs, GH0
+            self.GHinv_initial = GH.clone() if keep_hinv else None
+            z_any = torch.amax(z_flags).reshape(1).contiguous()
+
+            codes = torch.empty((R, C), dtype=torch.int16, device=dev)
+            err = torch.empty((R, min(blocksize, C)), **f32)
+            nblocks = (C + blocksize - 1) // blocksize
+            dyn_scale = torch.empty((nblocks, R), **f32) if qmode == nat.RQ_QMODE_DYNAMIC else None
+            with _section(rec, "fasterquant.block_loop"):
+                for bidx, i1 in enumerate(range(0, C, blocksize)):
+                    i2 = min(i1 + blocksize, C)
+                    count = i2 - i1
+                    atomic = bool(block_atomic_quant) and i2 < C
+                    K.quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale_tab, col_group,
+                                  dyn_scale[bidx] if dyn_scale is not None else None, maxq, sym, atomic,
+                                  z_any, codes, err)
+                    if i2 < C:
+                        K.trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_any)
+
+            with _section(rec, "fasterquant.write_layer_weight"):
+                Q = torch.empty((R, C), dtype=W.dtype, device=dev)
+                w_int = torch.empty((R, C), **f32) if export_to_et else None
+                scale_full = torch.empty((R, C), **f32) if export_to_et else None
+                nan_flag = torch.zeros(1, dtype=torch.int32, device=dev)
+                K.writeback(codes, invperm, qmode, scale_tab, col_group, dyn_scale, blocksize, Q,
+                            w_int, scale_full, nan_flag)
+                if export_to_et:
+                    self.layer.register_buffer("int_weight", w_int.reshape(self.layer.weight.shape))
+                    self.layer.register_buffer("scale", scale_full)
+                self.layer.weight.data = Q.reshape(self.layer.weight.shape)
+
+        self.perm, self.invperm = perm, invperm
+        self._codes_perm = codes
+        self.qmode, self.scale_table, self.col_group, self.dyn_scale = qmode, scale_tab, col_group, dyn_scale
+        self.Hinv_all = Hinv_all if keep_hinv else None
+        self.Hinv_init_all = hinv_init_keep if keep_hinv else None
+        self.Z = Z if keep_hinv else None
+        if int(nan_flag.item()):
+            logging.warning("NaN in weights")
+            raise ValueError("NaN in weights")
+
+    @property
+    def codes(self):
+        """Integer codes (int16) in natural column order, shape (R, C)."""
+        if self._codes_perm is None:
+            return None
+        return self._codes_perm if self.invperm is None else self._codes_perm[:, self.invperm]
+
+    @staticmethod
+    def _validate(grad_reg_strategy, grad_reg_lambda=0.0, grad_gate_floor=0.1, grad_gate_sharpness=1.0,
+                  grad_gate_sine_amp=0.0):
+        # gptq_plus_utils.py:658-677
+        valid = {"none", "l2", "hessian", "quant_error_gate", "quant_error_gate_optimized"}
+        if grad_reg_strategy not in valid:
+            raise ValueError(f"Unsupported `grad_reg_strategy={grad_reg_strategy}`.")
+        if grad_reg_lambda < 0:
+            raise ValueError(f"`grad_reg_lambda` must be non-negative. Got {grad_reg_lambda}.")
+        if not (0.0 <= grad_gate_floor <= 1.0):
+            raise ValueError(f"`grad_gate_floor` must be in [0, 1]. Got {grad_gate_floor}.")
+        if grad_gate_sharpness < 0:
+            raise ValueError(f"`grad_gate_sharpness` must be non-negative. Got {grad_gate_sharpness}.")
+        if grad_gate_sine_amp < 0:
+            raise ValueError(f"`grad_gate_sine_amp` must be non-negative. Got {grad_gate_sine_amp}.")
+
+    # gptq_plus_utils.py:2357-2361
+    def free(self):
+        self.H = None
+        self.Losses = None
+        self._codes_perm = None
+        self.Hinv_all = None
+        torch.cuda.empty_cache()

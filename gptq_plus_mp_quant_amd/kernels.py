@@ -1,0 +1,120 @@
+"""Tensor-level wrappers of the C ABI (one function per entry point of include/gptqplus_hip.h).
+
+Each wrapper validates shapes/dtypes on the host, passes raw device pointers and the current
+HIP stream of the tensors' device, and raises ``RuntimeError`` on a non-zero status.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+_f32 = torch.float32
+
+
+def _stream(t):
+    return nat.stream_of(t.device)
+
+
+def _rowmajor(t, name):
+    nat.require_gpu(t, name)
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D tensor with unit column stride")
+    return t
+
+
+def hessian_accum(x, sal, H, act_sq):
+    """H[g] += X^T diag(sal[:, g]) X (upper tiles), act_sq += sum x^2.  x: [n, C], sal: [n, G]."""
+    _rowmajor(x, "x")
+    _rowmajor(sal, "sal")
+    G, C, C2 = H.shape
+    if C != C2 or x.shape[1] != C or sal.shape != (x.shape[0], G) or sal.dtype != _f32:
+        raise ValueError("hessian_accum: shape mismatch")
+    if not (H.is_contiguous() and H.dtype == _f32 and act_sq.is_contiguous() and act_sq.numel() == C):
+        raise ValueError("hessian_accum: H / act_sq must be contiguous fp32")
+    nat.call("rq_hessian_accum", nat.ptr(x), nat.dtype_code(x.dtype), x.shape[0], x.stride(0), C,
+             nat.ptr(sal), sal.stride(0), G, nat.ptr(H), nat.ptr(act_sq), _stream(x))
+
+
+def hessian_finalize(H, act_sq, h_div, sal_scale, seq_len, nonfinite=None):
+    G, C, _ = H.shape
+    nat.call("rq_hessian_finalize", nat.ptr(H), nat.ptr(act_sq), G, C, float(h_div), float(sal_scale),
+             float(seq_len), nat.ptr(nonfinite), _stream(H))
+
+
+def find_params(w, maxq, sym, group_size=-1):
+    """Per-row (or per column group) min/max scale and zero: returns ([ng, R], [ng, R])."""
+    _rowmajor(w, "w")
+    R, C = w.shape
+    gs = group_size if group_size > 0 else C
+    ng = (C + gs - 1) // gs
+    scale = torch.empty((ng, R), device=w.device, dtype=_f32)
+    zero = torch.empty((ng, R), device=w.device, dtype=_f32)
+    nat.call("rq_find_params", nat.ptr(w), nat.dtype_code(w.dtype), R, C, w.stride(0), gs, int(maxq),
+             int(bool(sym)), nat.ptr(scale), nat.ptr(zero), _stream(w))
+    return scale, zero
+
+
+def act_order_perm(act_sq):
+    C = act_sq.numel()
+    perm = torch.empty(C, dtype=torch.int64, device=act_sq.device)
+    invperm = torch.empty(C, dtype=torch.int64, device=act_sq.device)
+    nat.call("rq_act_order_perm", nat.ptr(act_sq), C, nat.ptr(perm), nat.ptr(invperm), _stream(act_sq))
+    return perm, invperm
+
+
+def prepare_subgroup(w, grad, H_g, perm, W_sub, G_sub, H_sub):
+    _rowmajor(w, "w")
+    R_s, C = W_sub.shape
+    nat.call("rq_prepare_subgroup", nat.ptr(w), nat.dtype_code(w.dtype), w.stride(0), nat.ptr(grad),
+             grad.stride(0) if grad is not None else 0, nat.ptr(H_g), R_s, C, nat.ptr(perm),
+             nat.ptr(W_sub), W_sub.stride(0), nat.ptr(G_sub), G_sub.stride(0) if G_sub is not None else 0,
+             nat.ptr(H_sub), _stream(w))
+
+
+def chol_workspace(C, device):
+    return torch.empty(int(nat.load().rq_chol_workspace_bytes(C)), dtype=torch.uint8, device=device)
+
+
+def chol_hinv_attempt(H_work, damp_percent, workspace, Hinv, Hinv_init=None, info=None):
+    C = H_work.shape[0]
+    if info is None:
+        info = torch.zeros(1, dtype=torch.int32, device=H_work.device)
+    nat.call("rq_chol_hinv_attempt", nat.ptr(H_work), C, float(damp_percent), nat.ptr(workspace),
+             nat.ptr(Hinv), nat.ptr(Hinv_init), nat.ptr(info), _stream(H_work))
+    return info
+
+
+def gptqplus_terms(G_sub, Hinv_init, Hinv, alpha_eff, reference_loss, beta_mode, beta, Z, GHinv,
+                   GH0, z_nonzero):
+    R_s, C = G_sub.shape
+    nat.call("rq_gptqplus_terms", nat.ptr(G_sub), G_sub.stride(0), nat.ptr(Hinv_init), nat.ptr(Hinv),
+             R_s, C, float(alpha_eff), float(reference_loss), int(beta_mode), nat.ptr(beta), nat.ptr(Z),
+             nat.ptr(GHinv), Z.stride(0), nat.ptr(GH0), nat.ptr(z_nonzero), _stream(G_sub))
+
+
+def quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale, col_group, dyn_scale, maxq, sym,
+                atomic, z_nonzero, codes, err):
+    R, C = Wp.shape
+    if Hinv_all.shape != (R // R_s, C, C):
+        raise ValueError("quant_block: Hinv_all must be [G, C, C]")
+    nat.call("rq_quant_block", nat.ptr(Wp), Wp.stride(0), nat.ptr(Hinv_all), C, nat.ptr(GH), nat.ptr(Z),
+             GH.stride(0), R, R_s, int(i1), int(count), int(qmode), nat.ptr(scale), nat.ptr(col_group),
+             nat.ptr(dyn_scale), int(maxq), int(bool(sym)), int(bool(atomic)), nat.ptr(z_nonzero),
+             nat.ptr(codes), nat.ptr(err), _stream(Wp))
+
+
+def trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_nonzero):
+    R, C = Wp.shape
+    nat.call("rq_trailing_update", nat.ptr(Wp), Wp.stride(0), nat.ptr(GH), nat.ptr(Z), GH.stride(0),
+             nat.ptr(Hinv_all), C, R, R_s, int(i1), int(count), nat.ptr(err), nat.ptr(z_nonzero),
+             _stream(Wp))
+
+
+def writeback(codes, invperm, qmode, scale, col_group, dyn_scale, blocksize, q_out, w_int_out=None,
+              scale_out=None, nan_flag=None):
+    R, C = codes.shape
+    nat.call("rq_writeback", nat.ptr(codes), R, C, nat.ptr(invperm), int(qmode), nat.ptr(scale),
+             nat.ptr(col_group), nat.ptr(dyn_scale), int(blocksize), nat.ptr(q_out),
+             nat.dtype_code(q_out.dtype), q_out.stride(0), nat.ptr(w_int_out), nat.ptr(scale_out),
+             nat.ptr(nan_flag), _stream(codes))

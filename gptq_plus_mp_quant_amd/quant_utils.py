@@ -1,0 +1,116 @@
+"""Drop-in ``WeightQuantizer`` (reference: utils/quant_utils.py:300-486) whose ``find_params``
+runs the gfx950 ``rq_find_params`` kernel.
+
+Same constructor, ``configure`` arguments, attributes (``maxq``, ``scale``, ``zero``, ``bits``,
+``perchannel``, ``sym``, ...) and method semantics as the reference.  ``find_params`` needs the
+tensor on the GPU.  The ``mse=True`` clipping grid search and ``weight_groupsize > 0`` are not
+implemented as kernels yet and raise ``NotImplementedError`` instead of diverging.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+
+def get_minq_maxq(bits, sym):
+    """utils/quant_utils.py:21-29."""
+    if sym:
+        maxq = torch.tensor(2 ** (bits - 1) - 1)
+        minq = -maxq - 1
+    else:
+        maxq = torch.tensor(2 ** bits - 1)
+        minq = 0
+    return minq, maxq
+
+
+class WeightQuantizer(torch.nn.Module):
+    def __init__(self, shape: int = 1) -> None:
+        super().__init__()
+        self.register_buffer("maxq", torch.tensor(0))
+        self.register_buffer("scale", torch.zeros(shape))
+        self.register_buffer("zero", torch.zeros(shape))
+        self.bits = 16
+
+    # utils/quant_utils.py:309-331
+    def configure(self, bits, perchannel: bool = False, sym: bool = True, mse: bool = False,
+                  norm: float = 2.4, grid: int = 50, maxshrink: float = 0.5,
+                  weight_groupsize: int = -1) -> None:
+        self.bits = bits
+        self.perchannel = perchannel
+        self.sym = sym
+        self.mse = mse
+        self.norm = norm
+        self.grid = grid
+        self.maxshrink = maxshrink
+        self.weight_groupsize = weight_groupsize
+        self.maxq = torch.tensor(2 ** (bits - 1) - 1) if sym else torch.tensor(2 ** bits - 1)
+
+    def _check_supported(self):
+        if self.mse:
+            raise NotImplementedError("WeightQuantizer(mse=True) clipping search has no HIP kernel yet")
+        if getattr(self, "weight_groupsize", -1) > 0:
+            raise NotImplementedError("weight_groupsize > 0 has no HIP kernel yet")
+
+    def params_on(self, w: torch.Tensor, group_size: int = -1):
+        """Return (scale [ngroups, R], zero [ngroups, R]) for a 2-D weight without touching self."""
+        self._check_supported()
+        nat.require_gpu(w, "weight")
+        if w.dim() != 2:
+            raise ValueError("expected a 2-D weight")
+        if w.stride(1) != 1:
+            w = w.contiguous()
+        R, C = w.shape
+        gs = group_size if group_size > 0 else C
+        ng = (C + gs - 1) // gs
+        scale = torch.empty((ng, R), device=w.device, dtype=torch.float32)
+        zero = torch.empty((ng, R), device=w.device, dtype=torch.float32)
+        nat.call("rq_find_params", nat.ptr(w), nat.dtype_code(w.dtype), R, C, w.stride(0), gs,
+                 int(self.maxq), int(bool(self.sym)), nat.ptr(scale), nat.ptr(zero),
+                 nat.stream_of(w.device))
+        return scale, zero
+
+    # utils/quant_utils.py:390-457
+    def find_params(self, x) -> None:
+        if self.bits == 16:
+            return
+        self._check_supported()
+        nat.require_gpu(x, "x")
+        self.maxq = self.maxq.to(x.device)
+        shape = x.shape
+        x2 = x.flatten(1) if self.perchannel else x.flatten().unsqueeze(0)
+        scale, zero = self.params_on(x2)
+        scale, zero = scale[0], zero[0]
+        if not self.perchannel:
+            scale = scale.repeat(shape[0])
+            zero = zero.repeat(shape[0])
+        out = [-1] + [1] * (len(shape) - 1)
+        self.scale = scale.reshape(out)
+        self.zero = zero.reshape(out)
+
+    # utils/quant_utils.py:462-469
+    def quantize(self, x):
+        if self.ready() and self.bits < 16:
+            scale = self.scale.to(x.device)
+            if self.sym:
+                return (scale * torch.clamp(torch.round(x / scale), -(self.maxq + 1), self.maxq)).to(x.dtype)
+            zero = self.zero.to(x.device)
+            q = torch.clamp(torch.round(x / scale) + zero, 0, self.maxq)
+            return (scale * (q - zero)).to(x.dtype)
+        return x
+
+    # utils/quant_utils.py:471-480 (zero ignored, signed range even when sym=False)
+    def fake_quantize(self, x, st_idx=None, end_idx=None):
+        if self.ready() and self.bits < 16:
+            scale = self.scale.to(x.device)
+            if st_idx is not None and end_idx is not None:
+                scale = scale[st_idx:end_idx]
+            q = torch.clamp(torch.round(x / scale), -(self.maxq + 1), self.maxq)
+            return (scale * q).to(x.dtype), q, scale
+        return None, None, None
+
+    def enabled(self):
+        return self.maxq > 0
+
+    def ready(self):
+        return torch.all(self.scale != 0)

@@ -1,0 +1,136 @@
+/*
+ * C ABI of the MI355X (gfx950) GPTQ+ per-linear quantization hot path.
+ *
+ * Every entry point takes device pointers allocated by the caller (no allocation happens
+ * inside the library), a hipStream_t passed as `void*`, launches asynchronously on that
+ * stream and returns an int status:  0 = ok, <0 = argument / HIP error (RQ_E*).  Shapes are
+ * validated on the host before any launch.  Matrices are row-major with explicit leading
+ * dimensions (in elements).  The reference implementation is Python; the citations name
+ * the reference code each call replaces (file:line in Mrluxianseng/gptq_plus_mp_quant).
+ */
+#ifndef GPTQPLUS_HIP_H
+#define GPTQPLUS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RQ_OK 0
+#define RQ_EINVAL (-1)
+#define RQ_EHIP (-2)
+#define RQ_ENOTSUP (-3)
+
+/* element types of caller tensors */
+#define RQ_F16 0
+#define RQ_BF16 1
+#define RQ_F32 2
+
+/* quantizer modes of rq_quant_block / rq_writeback */
+#define RQ_QMODE_CHANNEL 0 /* one scale per row            (gptq_plus_utils.py:1008-1020) */
+#define RQ_QMODE_STATIC 1  /* per column-group, act_order  (gptq_plus_utils.py:994-1002)  */
+#define RQ_QMODE_DYNAMIC 2 /* per block, from block start  (gptq_plus_utils.py:1202-1209) */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int rq_version(void);
+
+/* GPTQPlus.add_batch -- gptq_utils/gptq_plus_utils.py:798-857.
+ * H[g] (C x C, fp32, g < G) += X^T diag(sal[:, g]) X over `ntok` tokens, upper-triangle
+ * 128x128 tiles only (the lower triangle is filled by rq_hessian_finalize);
+ * act_sq[c] += sum_t x[t,c]^2.  X is [ntok, C] (row stride ldx) of type x_dtype,
+ * sal is [ntok, G] fp32 (row stride ld_sal).  fp32 MFMA, no atomics, deterministic. */
+int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
+                     const float* sal, int64_t ld_sal, int G, float* H, float* act_sq,
+                     void* stream);
+
+/* GPTQPlus.finalize_hessian -- gptq_plus_utils.py:859-908 (world size 1).
+ * H = sym(upper(H)) / h_div [/ sal_scale if != 1]; non-finite entries -> 0 and counted
+ * into *nonfinite (device int, accumulated); act_sq /= seq_len. */
+int rq_hessian_finalize(float* H, float* act_sq, int G, int C, double h_div, double sal_scale,
+                        double seq_len, int* nonfinite, void* stream);
+
+/* WeightQuantizer.find_params, per-channel min/max -- utils/quant_utils.py:390-421
+ * (static column groups: gptq_plus_utils.py:994-1002).  For each group k of `group_size`
+ * columns (group_size <= 0: one group of all C columns) and row r:
+ * scale[k*R + r], zero[k*R + r]. */
+int rq_find_params(const void* w, int w_dtype, int R, int C, int64_t ldw, int group_size,
+                   int maxq, int sym, float* scale, float* zero, void* stream);
+
+/* act_order permutation -- gptq_plus_utils.py:1046, 1050:
+ * perm = argsort(act_sq, descending) with ties broken by ascending index (NaN first),
+ * invperm = argsort(perm).  int64 outputs. */
+int rq_act_order_perm(const float* act_sq, int C, int64_t* perm, int64_t* invperm, void* stream);
+
+/* Per-subgroup slicing, dead columns and act_order gather -- gptq_plus_utils.py:1033-1050.
+ * dead[c] = (H_g[c,c] == 0).  W_sub[r,j] = dead[p_j] ? 0 : w[r, p_j] (fp32),
+ * G_sub[r,j] = grad[r, p_j] (skipped when grad == NULL), H_sub[i,j] = H_g[p_i, p_j] with
+ * H_sub[i,i] = 1 where dead[p_i]; p = perm (identity when perm == NULL).  w/grad point at the
+ * subgroup's first row. */
+int rq_prepare_subgroup(const void* w, int w_dtype, int64_t ldw, const float* grad, int64_t ldg,
+                        const float* H_g, int R_s, int C, const int64_t* perm, float* W_sub,
+                        int64_t ld_wsub, float* G_sub, int64_t ld_gsub, float* H_sub, void* stream);
+
+/* Bytes of device workspace rq_chol_hinv_attempt needs for a C x C Hessian. */
+int64_t rq_chol_workspace_bytes(int C);
+
+/* One attempt of GPTQPlus._compute_hessian_inverse_with_fallback -- gptq_plus_utils.py:519-533:
+ * H_work[i,i] += fl32(damp_percent) * mean(diag(H_work))   (in place: retries accumulate),
+ * then Hinv = upper Cholesky factor of H_work^-1 (Hinv^T Hinv = H_work^-1) and, when
+ * Hinv_init != NULL, Hinv_init = H_work^-1.  Factorisation in fp64 (blocked, MFMA).
+ * *info (device int) is set non-zero when H_work is not positive definite or the result is
+ * not finite; the caller reads it after the stream completes and retries. */
+int rq_chol_hinv_attempt(float* H_work, int C, double damp_percent, void* workspace, float* Hinv,
+                         float* Hinv_init, int* info, void* stream);
+
+/* GPTQPlus._compute_gradient_terms -- gptq_plus_utils.py:563-578 with
+ * compute_safe_beta_from_reference_loss -- :174-194.
+ * beta_mode 0: beta = 0 (alpha <= 0 or gradient update off; beta has 1 element);
+ * beta_mode 1: beta[r] from G_sub, Hinv_init (needs GH0 workspace [R_s, C]).
+ * Z = (G_sub Hinv^T) * beta, GHinv = Z Hinv.  *z_nonzero (device int) is set to 1 when any Z
+ * element is non-zero or NaN; 0 lets later kernels skip provably-zero first-order work. */
+int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* Hinv_init, const float* Hinv,
+                      int R_s, int C, double alpha_eff, double reference_loss, int beta_mode,
+                      float* beta, float* Z, float* GHinv, int64_t ldz, float* GH0,
+                      int* z_nonzero, void* stream);
+
+/* One block of the fasterquant loop for ALL subgroups -- gptq_plus_utils.py:1169-1372:
+ * columns [i1, i1+count) of the permuted working weight Wp [R, C] (row stride ldw),
+ * subgroup s = rows [s*R_s, (s+1)*R_s) with upper Hinv_all + s*C*C.
+ * Non-atomic: the column-serial quantize / error / rank-1 update (:1296-1367) incl. the
+ * GPTQ+ GHinv terms.  atomic != 0: quantize the block start at once and solve
+ * Err * Hinv1 = W - Q - GHinv1 (:1238-1288; the caller passes atomic = 0 for the last block).
+ * Writes int16 codes [R, C] (permuted order) and err [R, count] for rq_trailing_update.
+ * qmode: RQ_QMODE_CHANNEL scale[r]; RQ_QMODE_STATIC scale[col_group[i1+i]*R + r];
+ * RQ_QMODE_DYNAMIC computes scale from the block start into dyn_scale[r] (caller offsets it
+ * per block).  count <= 128. */
+int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int C, const float* GH,
+                   const float* Z, int64_t ldgh, int R, int R_s, int i1, int count, int qmode,
+                   const float* scale, const int32_t* col_group, float* dyn_scale, int maxq,
+                   int sym, int atomic, const int* z_nonzero, int16_t* codes, float* err,
+                   void* stream);
+
+/* Outer (trailing) update after a block, frozen mode -- gptq_plus_utils.py:1500-1570:
+ * Wp[:, i2:] -= err Hinv[i1:i2, i2:] + (count GH[:, i2:] - (Z[:, i1:i2] D) Hinv[i1:i2, i2:]),
+ * GH[:, i2:] -= Z[:, i1:i2] Hinv[i1:i2, i2:], D = [count-1, ..., 0], per subgroup; the Z
+ * terms are skipped when *z_nonzero == 0.  fp32 MFMA. */
+int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float* Z, int64_t ldgh,
+                       const float* Hinv_all, int C, int R, int R_s, int i1, int count,
+                       const float* err, const int* z_nonzero, void* stream);
+
+/* Un-permute and write back -- gptq_plus_utils.py:1850-1875:
+ * natural column c of row r takes permuted column j = invperm[c] (identity if NULL):
+ * Q = scale(r, j) * code[r, j]; q_out (layer dtype q_dtype, [R, C] row stride ldq) = Q;
+ * optional fp32 W_int / Scale (export_to_et, :1866-1871) when the pointers are non-NULL.
+ * *nan_flag (device int) is set to 1 if any written weight is NaN (:1882-1896).
+ * dynamic mode: dyn_scale[(j / blocksize) * R + r]. */
+int rq_writeback(const int16_t* codes, int R, int C, const int64_t* invperm, int qmode,
+                 const float* scale, const int32_t* col_group, const float* dyn_scale,
+                 int blocksize, void* q_out, int q_dtype, int64_t ldq, float* w_int_out,
+                 float* scale_out, int* nan_flag, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GPTQPLUS_HIP_H */

@@ -1,0 +1,68 @@
+"""CPU-only checks of the native boundary: the library loads and exports every symbol the
+header declares; the ctypes bindings cover them; host-side validation rejects bad calls
+before any device work; the drop-in classes refuse non-GPU tensors loudly."""
+import ctypes
+
+import pytest
+import torch
+
+from gptq_plus_mp_quant_amd import _native as nat
+
+
+def _lib():
+    if not nat.LIB_PATH.exists():
+        pytest.skip("library not built")
+    return nat.load()
+
+
+def test_header_symbols_are_exported_and_bound():
+    lib = _lib()
+    syms = nat.header_symbols()
+    assert len(syms) >= 12
+    for name in syms:
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in nat.SIGNATURES, f"{name} has no ctypes binding"
+    assert set(nat.SIGNATURES) == set(syms)
+
+
+def test_version_and_workspace_query():
+    lib = _lib()
+    assert lib.rq_version() == 100
+    assert lib.rq_chol_workspace_bytes(64) == 2 * 64 * 64 * 8 + 64 * 64 * 8
+    assert lib.rq_chol_workspace_bytes(0) < 0
+
+
+def test_argument_validation_needs_no_device():
+    lib = _lib()
+    null = ctypes.c_void_p(0)
+    assert lib.rq_hessian_accum(null, 0, 10, 8, 8, null, 1, 1, null, null, null) == nat.RQ_EINVAL
+    assert lib.rq_find_params(null, 0, 4, 4, 4, -1, 7, 1, null, null, null) == nat.RQ_EINVAL
+    assert lib.rq_act_order_perm(null, 4, null, null, null) == nat.RQ_EINVAL
+    assert lib.rq_chol_hinv_attempt(null, 4, 0.01, null, null, null, null, null) == nat.RQ_EINVAL
+    assert lib.rq_quant_block(null, 4, null, 4, null, null, 4, 4, 4, 0, 4, 0, null, null, null, 7, 1,
+                              0, null, null, null, null) == nat.RQ_EINVAL
+    assert lib.rq_trailing_update(null, 4, null, null, 4, null, 4, 4, 4, 0, 4, null, null, null) == nat.RQ_EINVAL
+    assert lib.rq_writeback(null, 4, 4, null, 0, null, null, null, 4, null, 0, 4, null, null, null,
+                            null) == nat.RQ_EINVAL
+
+
+def test_dropin_rejects_cpu_tensors():
+    _lib()
+    from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
+    layer = torch.nn.Linear(8, 4, bias=False)
+    with pytest.raises(RuntimeError, match="GPU"):
+        GPTQPlus(layer, torch.ones(1, 2, 1), torch.zeros(4, 8), 1, 0.0, 0.0)
+    q = WeightQuantizer()
+    q.configure(4, perchannel=True, sym=True)
+    with pytest.raises(RuntimeError, match="GPU"):
+        q.find_params(torch.ones(4, 8))
+    q.configure(4, perchannel=True, sym=True, mse=True)
+    with pytest.raises(NotImplementedError):
+        q.find_params(torch.ones(4, 8))
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(nat, "LIB_PATH", tmp_path / "absent.so")
+    monkeypatch.setattr(nat, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        nat.load()
