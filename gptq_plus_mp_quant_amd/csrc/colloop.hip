@@ -24,7 +24,6 @@
 namespace {
 
 constexpr int QB_MAXB = 128;
-constexpr int16_t RQ_CODE_NAN = -32768;
 
 template <int CTRL>
 __device__ __forceinline__ float quad_bcast(float v) {

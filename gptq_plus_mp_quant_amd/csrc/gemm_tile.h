@@ -15,9 +15,12 @@ namespace rq {
 
 template <typename T>
 struct Mfma16;
+// Output element e of a lane: column lane % 16, row row(lane, e).  The fp32 op returns four
+// consecutive rows per lane group, the fp64 op interleaves them (checked on gfx950).
 template <>
 struct Mfma16<float> {
   using acc_t = floatx4;
+  static __device__ __forceinline__ int row(int lane, int e) { return 4 * (lane >> 4) + e; }
   static __device__ __forceinline__ acc_t op(float a, float b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
@@ -25,6 +28,7 @@ struct Mfma16<float> {
 template <>
 struct Mfma16<double> {
   using acc_t = doublex4;
+  static __device__ __forceinline__ int row(int lane, int e) { return (lane >> 4) + 4 * e; }
   static __device__ __forceinline__ acc_t op(double a, double b, acc_t c) {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
   }
@@ -172,7 +176,7 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
     }
   }
 
-  // 16x16 block layout: row = 4*(lane/16) + e, col = lane % 16.
+  // 16x16 block layout: col = lane % 16, row = Mfma16<T>::row(lane, e).
   int nz = 0;
 #pragma unroll
   for (int a = 0; a < 2; ++a)
@@ -180,7 +184,7 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int i = i0 + wr * 32 + a * 16 + 4 * (lane >> 4) + e;
+        const int i = i0 + wr * 32 + a * 16 + Mfma16<T>::row(lane, e);
         const int j = j0 + wc * 32 + b * 16 + (lane & 15);
         if (i < p.M && j < p.N) {
           T v = p.alpha * acc[a][b][e];

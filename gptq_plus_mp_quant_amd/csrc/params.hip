@@ -145,15 +145,21 @@ __global__ __launch_bounds__(256) void k_writeback(const int16_t* __restrict__ c
   const int64_t j = invperm ? invperm[c] : c;
   int nan_seen = 0;
   for (int r = blockIdx.y; r < R; r += gridDim.y) {
-    const float code = (float)codes[(int64_t)r * C + j];
+    const int16_t ci = codes[(int64_t)r * C + j];
+    const float code = (ci == RQ_CODE_NAN) ? __builtin_nanf("") : (float)ci;   // NaN weight
     float s;
     if (qmode == RQ_QMODE_CHANNEL) s = scale[r];
     else if (qmode == RQ_QMODE_STATIC) s = scale[(int64_t)col_group[j] * R + r];
     else s = dyn_scale[(j / bs) * (int64_t)R + r];
-    const TQ q = rq_cast<TQ>(s * code);
+    float qf = s * code;
+    // Keep fl32(s * code) as its own rounding step: without the barrier the compiler folds
+    // the multiply and the fp16 conversion into v_fma_mixlo_f16 (a single rounding), which
+    // differs from torch's (scale * q).to(float16) on exact fp16 midpoints.
+    asm volatile("" : "+v"(qf));
+    const TQ q = rq_cast<TQ>(qf);
     q_out[(int64_t)r * ldq + c] = q;
-    const float qf = (float)q;
-    nan_seen |= (qf != qf);
+    const float qback = (float)q;
+    nan_seen |= (qback != qback);
     if (w_int_out) w_int_out[(int64_t)r * C + c] = code;
     if (scale_out) scale_out[(int64_t)r * C + c] = s;
   }

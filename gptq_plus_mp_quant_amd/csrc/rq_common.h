@@ -20,6 +20,9 @@ __device__ __forceinline__ float rq_load_elem(const __half* p) { return __half2f
 __device__ __forceinline__ float rq_load_elem(const __hip_bfloat16* p) { return __bfloat162float(*p); }
 __device__ __forceinline__ float rq_load_elem(const float* p) { return *p; }
 
+// int16 code written for a NaN weight (the reference keeps NaN in its float codes).
+constexpr int16_t RQ_CODE_NAN = -32768;
+
 // torch.minimum / torch.maximum semantics: NaN propagates.
 __device__ __forceinline__ float rq_nan_min(float a, float b) { return (a != a || a < b) ? a : b; }
 __device__ __forceinline__ float rq_nan_max(float a, float b) { return (a != a || a > b) ? a : b; }

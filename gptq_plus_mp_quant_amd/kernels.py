@@ -23,6 +23,27 @@ def _rowmajor(t, name):
     return t
 
 
+def _cin(t, name, dtype=_f32):
+    """Read-only operand: on the GPU, given dtype, dense row-major (copied if it is a view
+    with other strides, e.g. the transposed result of torch.linalg.cholesky(upper=True))."""
+    if t is None:
+        return None
+    nat.require_gpu(t, name)
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}")
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _cout(t, name, dtype=_f32):
+    """Written operand: must already be dense row-major (the kernel writes through it)."""
+    if t is None:
+        return None
+    nat.require_gpu(t, name)
+    if t.dtype != dtype or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous {dtype} tensor")
+    return t
+
+
 def hessian_accum(x, sal, H, act_sq):
     """H[g] += X^T diag(sal[:, g]) X (upper tiles), act_sq += sum x^2.  x: [n, C], sal: [n, G]."""
     _rowmajor(x, "x")
@@ -78,6 +99,7 @@ def chol_workspace(C, device):
 
 def chol_hinv_attempt(H_work, damp_percent, workspace, Hinv, Hinv_init=None, info=None):
     C = H_work.shape[0]
+    _cout(H_work, "H_work"), _cout(Hinv, "Hinv"), _cout(Hinv_init, "Hinv_init")
     if info is None:
         info = torch.zeros(1, dtype=torch.int32, device=H_work.device)
     nat.call("rq_chol_hinv_attempt", nat.ptr(H_work), C, float(damp_percent), nat.ptr(workspace),
@@ -88,6 +110,11 @@ def chol_hinv_attempt(H_work, damp_percent, workspace, Hinv, Hinv_init=None, inf
 def gptqplus_terms(G_sub, Hinv_init, Hinv, alpha_eff, reference_loss, beta_mode, beta, Z, GHinv,
                    GH0, z_nonzero):
     R_s, C = G_sub.shape
+    G_sub = _cin(G_sub, "G_sub")
+    Hinv_init = _cin(Hinv_init, "Hinv_init")
+    Hinv = _cin(Hinv, "Hinv")
+    for t, n in ((beta, "beta"), (Z, "Z"), (GHinv, "GHinv"), (GH0, "GH0")):
+        _cout(t, n)
     nat.call("rq_gptqplus_terms", nat.ptr(G_sub), G_sub.stride(0), nat.ptr(Hinv_init), nat.ptr(Hinv),
              R_s, C, float(alpha_eff), float(reference_loss), int(beta_mode), nat.ptr(beta), nat.ptr(Z),
              nat.ptr(GHinv), Z.stride(0), nat.ptr(GH0), nat.ptr(z_nonzero), _stream(G_sub))
@@ -98,6 +125,9 @@ def quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale, col_group, dy
     R, C = Wp.shape
     if Hinv_all.shape != (R // R_s, C, C):
         raise ValueError("quant_block: Hinv_all must be [G, C, C]")
+    _cout(Wp, "Wp"), _cin(Hinv_all, "Hinv_all"), _cin(GH, "GH"), _cin(Z, "Z")
+    if not (Hinv_all.is_contiguous() and GH.stride(1) == 1 and Z.stride(1) == 1):
+        raise ValueError("quant_block: Hinv_all must be contiguous, GH / Z row-major")
     nat.call("rq_quant_block", nat.ptr(Wp), Wp.stride(0), nat.ptr(Hinv_all), C, nat.ptr(GH), nat.ptr(Z),
              GH.stride(0), R, R_s, int(i1), int(count), int(qmode), nat.ptr(scale), nat.ptr(col_group),
              nat.ptr(dyn_scale), int(maxq), int(bool(sym)), int(bool(atomic)), nat.ptr(z_nonzero),
@@ -106,6 +136,9 @@ def quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale, col_group, dy
 
 def trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_nonzero):
     R, C = Wp.shape
+    _cout(Wp, "Wp"), _cout(GH, "GH"), _cout(err, "err")
+    if not (Hinv_all.is_contiguous() and Z.stride(1) == 1):
+        raise ValueError("trailing_update: Hinv_all must be contiguous, Z row-major")
     nat.call("rq_trailing_update", nat.ptr(Wp), Wp.stride(0), nat.ptr(GH), nat.ptr(Z), GH.stride(0),
              nat.ptr(Hinv_all), C, R, R_s, int(i1), int(count), nat.ptr(err), nat.ptr(z_nonzero),
              _stream(Wp))
