@@ -21,9 +21,25 @@ constexpr int NB = 64;
 __global__ void k_fill_i32(int* p, int v) { *p = v; }
 __global__ void k_fill_f32(float* p, float v) { *p = v; }
 
-// H_work[i,i] += fl32(p) * mean(diag(H_work)).  One workgroup.
-__global__ __launch_bounds__(256) void k_damp(float* __restrict__ H, int C, float p) {
+constexpr int MAXBATCH = 64;
+struct BatchCfg {
+  float damp[MAXBATCH];
+  int active[MAXBATCH];
+};
+
+__global__ void k_init_info(int* info, int nb, BatchCfg cfg) {
+  const int b = threadIdx.x;
+  if (b < nb) info[b] = cfg.active[b] ? 0 : -1;
+}
+
+// H_work[i,i] += fl32(p) * mean(diag(H_work)).  One workgroup per batch entry.
+__global__ __launch_bounds__(256) void k_damp(float* __restrict__ H, int C, BatchCfg cfg,
+                                              const int* __restrict__ info) {
   __shared__ double part[256];
+  const int b = blockIdx.x;
+  if (info[b]) return;
+  H += (int64_t)b * C * C;
+  const float p = cfg.damp[b];
   double s = 0.0;
   for (int i = threadIdx.x; i < C; i += 256) s += (double)H[(int64_t)i * C + i];
   part[threadIdx.x] = s;
@@ -40,10 +56,16 @@ __global__ __launch_bounds__(256) void k_damp(float* __restrict__ H, int C, floa
   }
 }
 
-// A = P H_work P in fp64 (full square), Linv = 0.
+// A = P H_work P in fp64 (full square), Linv = 0.  grid.z = batch entry.
 __global__ __launch_bounds__(256) void k_reverse_to_f64(const float* __restrict__ H, int C,
                                                         double* __restrict__ A,
-                                                        double* __restrict__ Linv) {
+                                                        double* __restrict__ Linv, int64_t ws,
+                                                        const int* __restrict__ info) {
+  const int b = blockIdx.z;
+  if (info[b]) return;
+  H += (int64_t)b * C * C;
+  A += b * ws;
+  Linv += b * ws;
   const int j = blockIdx.x * 256 + threadIdx.x;
   if (j >= C) return;
   for (int i = blockIdx.y; i < C; i += gridDim.y) {
@@ -54,69 +76,92 @@ __global__ __launch_bounds__(256) void k_reverse_to_f64(const float* __restrict_
 
 // Factor the nb x nb diagonal block of A at (k, k) and invert it.  One workgroup.
 // Writes T = L_kk^-1 (lower, explicit zeros above) to Tbuf and to Linv's diagonal block.
+// Factorisation: right-looking, one column per step; the 16x16 thread grid walks the
+// trailing triangle without integer division.  Inverse: four lanes per column of T, each
+// summing every fourth term of the forward substitution, combined with a quad reduction.
 __global__ __launch_bounds__(256) void k_chol_diag(const double* __restrict__ A, int C, int k,
                                                    int nb, double* __restrict__ Tbuf,
-                                                   double* __restrict__ Linv, int* info) {
+                                                   double* __restrict__ Linv, int64_t ws,
+                                                   int* info_all) {
   __shared__ double L[NB][NB + 1];
   __shared__ double T[NB][NB + 1];
+  __shared__ double rdiag[NB];
   __shared__ int fail;
+  const int b = blockIdx.x;
+  int* info = info_all + b;
   if (*info) return;
+  A += b * ws;
+  Tbuf += b * ws;
+  Linv += b * ws;
   const int tid = threadIdx.x;
+  const int tx = tid & 15, ty = tid >> 4;
   if (tid == 0) fail = 0;
-  for (int e = tid; e < NB * NB; e += 256) {
-    const int i = e / NB, j = e % NB;
-    double v = 0.0;
-    if (i < nb && j <= i) v = A[(int64_t)(k + i) * C + (k + j)];
-    L[i][j] = v;
-    T[i][j] = 0.0;
-  }
+  for (int i = ty; i < NB; i += 16)
+    for (int j = tx; j < NB; j += 16) {
+      L[i][j] = (i < nb && j <= i) ? A[(int64_t)(k + i) * C + (k + j)] : 0.0;
+      T[i][j] = 0.0;
+    }
   __syncthreads();
   for (int j = 0; j < nb; ++j) {
-    if (tid == 0) {
-      const double d = L[j][j];
-      if (!(d > 0.0) || !rq_isfinite(d)) fail = 1;
-      else L[j][j] = sqrt(d);
+    const double d = L[j][j];
+    if (!(d > 0.0) || !rq_isfinite(d)) {   // uniform: every thread reads the same pivot
+      if (tid == 0) fail = 1;
+      break;
+    }
+    const double rd = 1.0 / sqrt(d);
+    // trailing triangle: L[i][l] -= (L[i][j] rd) (L[l][j] rd), j < l <= i
+    for (int i = j + 1 + ty; i < nb; i += 16) {
+      const double lij = L[i][j] * rd;
+      for (int l = j + 1 + tx; l <= i; l += 16) L[i][l] = L[i][l] - lij * (L[l][j] * rd);
     }
     __syncthreads();
-    if (fail) break;
-    const double djj = L[j][j];
-    for (int i = j + 1 + tid; i < nb; i += 256) L[i][j] = L[i][j] / djj;
-    __syncthreads();
-    // trailing update of the lower triangle: L[i][l] -= L[i][j] * L[l][j], j < l <= i
-    const int m = nb - j - 1;
-    for (int e = tid; e < m * m; e += 256) {
-      const int i = j + 1 + e / m, l = j + 1 + e % m;
-      if (l <= i) L[i][l] = L[i][l] - L[i][j] * L[l][j];
+    // scale column j (nothing reads it during the update above)
+    if (tid < nb - j) {
+      const int i = j + tid;
+      L[i][j] = (i == j) ? sqrt(d) : L[i][j] * rd;
     }
     __syncthreads();
   }
+  __syncthreads();
   if (fail) {
     if (tid == 0) atomicExch(info, 1);
     return;
   }
-  // T = L^-1, column c by thread c: forward substitution.
-  if (tid < nb) {
-    const int c = tid;
-    T[c][c] = 1.0 / L[c][c];
-    for (int i = c + 1; i < nb; ++i) {
-      double s = 0.0;
-      for (int m2 = c; m2 < i; ++m2) s += L[i][m2] * T[m2][c];
-      T[i][c] = -s / L[i][i];
+  if (tid < nb) rdiag[tid] = 1.0 / L[tid][tid];
+  __syncthreads();
+  // T = L^-1: column c by the quad 4c..4c+3 (nb <= 64)
+  {
+    const int c = tid >> 2, part = tid & 3;
+    if (c < nb && part == 0) T[c][c] = rdiag[c];
+    for (int i = c + 1; i < NB; ++i) {
+      double sacc = 0.0;
+      if (c < nb && i < nb)
+        for (int m2 = c + part; m2 < i; m2 += 4) sacc += L[i][m2] * T[m2][c];
+      sacc += __shfl_xor(sacc, 1, 64);
+      sacc += __shfl_xor(sacc, 2, 64);
+      // T[i][c] is read only by this quad (same wavefront) in later iterations, and LDS
+      // accesses of one wavefront complete in program order
+      if (c < nb && i < nb && part == 0) T[i][c] = -sacc * rdiag[i];
     }
   }
   __syncthreads();
-  for (int e = tid; e < nb * nb; e += 256) {
-    const int i = e / nb, j = e % nb;
-    const double v = T[i][j];
-    Tbuf[i * NB + j] = v;
-    Linv[(int64_t)(k + i) * C + (k + j)] = v;
-  }
+  for (int i = ty; i < nb; i += 16)
+    for (int j = tx; j < nb; j += 16) {
+      const double v = T[i][j];
+      Tbuf[i * NB + j] = v;
+      Linv[(int64_t)(k + i) * C + (k + j)] = v;
+    }
 }
 
 // Hinv[i][j] = fl32(Linv[C-1-i][C-1-j]) for j >= i, 0 below; non-finite -> info.
 __global__ __launch_bounds__(256) void k_output_upper(const double* __restrict__ Linv, int C,
-                                                      float* __restrict__ Hinv, int* info) {
+                                                      float* __restrict__ Hinv, int64_t ws,
+                                                      int* info_all) {
+  const int b = blockIdx.z;
+  int* info = info_all + b;
   if (*info) return;
+  Linv += b * ws;
+  Hinv += (int64_t)b * C * C;
   const int j = blockIdx.x * 256 + threadIdx.x;
   if (j >= C) return;
   int bad = 0;
@@ -131,8 +176,13 @@ __global__ __launch_bounds__(256) void k_output_upper(const double* __restrict__
 
 // Hinv_init[i][j] = fl32(M[C-1-i][C-1-j]) with M = Linv^T Linv held in its lower triangle.
 __global__ __launch_bounds__(256) void k_output_full(const double* __restrict__ M, int C,
-                                                     float* __restrict__ Hinv_init, int* info) {
+                                                     float* __restrict__ Hinv_init, int64_t ws,
+                                                     int* info_all) {
+  const int b = blockIdx.z;
+  int* info = info_all + b;
   if (*info) return;
+  M += b * ws;
+  Hinv_init += (int64_t)b * C * C;
   const int j = blockIdx.x * 256 + threadIdx.x;
   if (j >= C) return;
   int bad = 0;
@@ -186,74 +236,99 @@ __global__ __launch_bounds__(256) void k_safe_beta(const float* __restrict__ G, 
 
 extern "C" int64_t rq_chol_workspace_bytes(int C) {
   if (C <= 0) return -1;
-  return (int64_t)2 * C * C * (int64_t)sizeof(double) + (int64_t)NB * NB * sizeof(double);
+  return ((int64_t)2 * C * C + (int64_t)NB * NB) * (int64_t)sizeof(double);
 }
 
-extern "C" int rq_chol_hinv_attempt(float* H_work, int C, double damp_percent, void* workspace,
-                                    float* Hinv, float* Hinv_init, int* info, void* stream) {
+extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* damp_percent,
+                                    void* workspace, float* Hinv, float* Hinv_init, int* info,
+                                    void* stream) {
   using namespace rq;
-  if (!H_work || !workspace || !Hinv || !info || C <= 0 || !(damp_percent > 0)) return RQ_EINVAL;
+  if (!H_work || !workspace || !Hinv || !info || !damp_percent || C <= 0 || nb <= 0 ||
+      nb > MAXBATCH)
+    return RQ_EINVAL;
+  BatchCfg cfg;
+  int n_active = 0;
+  for (int b = 0; b < MAXBATCH; ++b) {
+    cfg.damp[b] = 0.0f;
+    cfg.active[b] = 0;
+  }
+  for (int b = 0; b < nb; ++b) {
+    const double p = damp_percent[b];
+    if (p > 0) {
+      if (!(p < 1.0)) return RQ_EINVAL;
+      cfg.damp[b] = (float)p;   // torch multiplies the fp32 mean by the scalar in fp32
+      cfg.active[b] = 1;
+      ++n_active;
+    }
+  }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_init_info, dim3(1), dim3(MAXBATCH), 0, s, info, nb, cfg);
+  RQ_CHECK_LAUNCH();
+  if (n_active == 0) return RQ_OK;
+  const int64_t ws = 2 * (int64_t)C * C + (int64_t)NB * NB;   // doubles per batch entry
   double* A = reinterpret_cast<double*>(workspace);
   double* Linv = A + (int64_t)C * C;
   double* Tbuf = Linv + (int64_t)C * C;
   const dim3 blk(256);
-  const dim3 gcol((C + 255) / 256, C < 1024 ? C : 1024);
+  const dim3 gcol((C + 255) / 256, C < 1024 ? C : 1024, nb);
 
-  hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(1), 0, s, info, 0);
-  hipLaunchKernelGGL(k_damp, dim3(1), blk, 0, s, H_work, C, (float)damp_percent);
-  hipLaunchKernelGGL(k_reverse_to_f64, gcol, blk, 0, s, H_work, C, A, Linv);
+  hipLaunchKernelGGL(k_damp, dim3(nb), blk, 0, s, H_work, C, cfg, info);
+  hipLaunchKernelGGL(k_reverse_to_f64, gcol, blk, 0, s, H_work, C, A, Linv, ws, info);
   RQ_CHECK_LAUNCH();
 
+  auto batched = [&](GemmArgs<double> g) {
+    g.abort_flag = info;
+    g.sA = ws;
+    g.sB = ws;
+    g.sC = ws;
+    return g;
+  };
   for (int k = 0; k < C; k += NB) {
-    const int nb = (C - k < NB) ? (C - k) : NB;
-    const int rest = C - k - nb;
-    hipLaunchKernelGGL(k_chol_diag, dim3(1), blk, 0, s, A, C, k, nb, Tbuf, Linv, info);
+    const int kb = (C - k < NB) ? (C - k) : NB;
+    const int rest = C - k - kb;
+    hipLaunchKernelGGL(k_chol_diag, dim3(nb), blk, 0, s, A, C, k, kb, Tbuf, Linv, ws, info);
     RQ_CHECK_LAUNCH();
     int rc;
     if (rest > 0) {
       // L_ik = A_ik T^T  (in place, rows below the panel)
-      GemmArgs<double> g = gemm_args<double>(A + (int64_t)(k + nb) * C + k, C, Tbuf, NB,
-                                             A + (int64_t)(k + nb) * C + k, C, rest, nb, nb, 1.0,
-                                             EPI_STORE);
-      g.abort_flag = info;
-      if ((rc = launch_gemm(g, false, true, s))) return rc;
+      GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)(k + kb) * C + k, C, Tbuf, NB,
+                                                     A + (int64_t)(k + kb) * C + k, C, rest, kb, kb,
+                                                     1.0, EPI_STORE));
+      if ((rc = launch_gemm(g, false, true, s, nb))) return rc;
     }
     if (k > 0) {
       // X_k[:, 0:k] = T B_k[:, 0:k]  (in place, row block k of L^-1)
-      GemmArgs<double> g = gemm_args<double>(Tbuf, NB, Linv + (int64_t)k * C, C,
-                                             Linv + (int64_t)k * C, C, nb, k, nb, 1.0, EPI_STORE);
-      g.abort_flag = info;
-      if ((rc = launch_gemm(g, false, false, s))) return rc;
+      GemmArgs<double> g = batched(gemm_args<double>(Tbuf, NB, Linv + (int64_t)k * C, C,
+                                                     Linv + (int64_t)k * C, C, kb, k, kb, 1.0,
+                                                     EPI_STORE));
+      if ((rc = launch_gemm(g, false, false, s, nb))) return rc;
     }
     if (rest > 0) {
-      // B_i[:, 0:k+nb] -= L_ik X_k
-      GemmArgs<double> g = gemm_args<double>(A + (int64_t)(k + nb) * C + k, C, Linv + (int64_t)k * C,
-                                             C, Linv + (int64_t)(k + nb) * C, C, rest, k + nb, nb,
-                                             -1.0, EPI_ACCUM);
-      g.abort_flag = info;
-      if ((rc = launch_gemm(g, false, false, s))) return rc;
+      // B_i[:, 0:k+kb] -= L_ik X_k
+      GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)(k + kb) * C + k, C,
+                                                     Linv + (int64_t)k * C, C,
+                                                     Linv + (int64_t)(k + kb) * C, C, rest, k + kb,
+                                                     kb, -1.0, EPI_ACCUM));
+      if ((rc = launch_gemm(g, false, false, s, nb))) return rc;
       // A_ij -= L_ik L_jk^T on the lower tiles of the trailing matrix
-      GemmArgs<double> h = gemm_args<double>(A + (int64_t)(k + nb) * C + k, C,
-                                             A + (int64_t)(k + nb) * C + k, C,
-                                             A + (int64_t)(k + nb) * C + (k + nb), C, rest, rest, nb,
-                                             -1.0, EPI_ACCUM);
+      GemmArgs<double> h = batched(gemm_args<double>(A + (int64_t)(k + kb) * C + k, C,
+                                                     A + (int64_t)(k + kb) * C + k, C,
+                                                     A + (int64_t)(k + kb) * C + (k + kb), C, rest,
+                                                     rest, kb, -1.0, EPI_ACCUM));
       h.lower_only = 1;
-      h.abort_flag = info;
-      if ((rc = launch_gemm(h, false, true, s))) return rc;
+      if ((rc = launch_gemm(h, false, true, s, nb))) return rc;
     }
   }
-  hipLaunchKernelGGL(k_output_upper, gcol, blk, 0, s, Linv, C, Hinv, info);
+  hipLaunchKernelGGL(k_output_upper, gcol, blk, 0, s, Linv, C, Hinv, ws, info);
   RQ_CHECK_LAUNCH();
   if (Hinv_init) {
     // M = Linv^T Linv (lower tiles) into A, then Hinv_init = P M P.
-    GemmArgs<double> g = gemm_args<double>(Linv, C, Linv, C, A, C, C, C, C, 1.0, EPI_STORE);
+    GemmArgs<double> g = batched(gemm_args<double>(Linv, C, Linv, C, A, C, C, C, C, 1.0, EPI_STORE));
     g.krange = KR_AB_LOWER;
     g.lower_only = 1;
-    g.abort_flag = info;
-    int rc = launch_gemm(g, true, false, s);
+    int rc = launch_gemm(g, true, false, s, nb);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_output_full, gcol, blk, 0, s, A, C, Hinv_init, info);
+    hipLaunchKernelGGL(k_output_full, gcol, blk, 0, s, A, C, Hinv_init, ws, info);
     RQ_CHECK_LAUNCH();
   }
   return RQ_OK;

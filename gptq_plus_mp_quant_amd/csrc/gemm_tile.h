@@ -65,7 +65,8 @@ struct GemmArgs {
   int row_bcast;
   int* nz_flag;              // optional: set to 1 when any stored value is non-zero or NaN
   const int* skip_if_zero;   // optional: when *skip_if_zero == 0 store zeros and return
-  const int* abort_flag;     // optional: when *abort_flag != 0 return immediately
+  const int* abort_flag;     // optional: when abort_flag[batch] != 0 return immediately
+  int64_t sA, sB, sC;        // element strides between batch entries (grid z = batch)
 };
 
 constexpr int GT = 64;
@@ -78,7 +79,11 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
   __shared__ T As[GKT][GT + GPAD];
   __shared__ T Bs[GKT][GT + GPAD];
 
-  if (p.abort_flag && *p.abort_flag) return;
+  const int bz = blockIdx.z;
+  if (p.abort_flag && p.abort_flag[bz]) return;
+  p.A += bz * p.sA;
+  p.B += bz * p.sB;
+  p.Cm += bz * p.sC;
   const int ti = blockIdx.y, tj = blockIdx.x;
   if (p.lower_only && tj > ti) return;
   const int i0 = ti * GT, j0 = tj * GT;
@@ -199,9 +204,9 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
 }
 
 template <typename T>
-inline int launch_gemm(const GemmArgs<T>& a, bool ta, bool tb, hipStream_t s) {
-  if (a.M <= 0 || a.N <= 0) return RQ_OK;
-  dim3 grid((a.N + GT - 1) / GT, (a.M + GT - 1) / GT), block(256);
+inline int launch_gemm(const GemmArgs<T>& a, bool ta, bool tb, hipStream_t s, int batch = 1) {
+  if (a.M <= 0 || a.N <= 0 || batch <= 0) return RQ_OK;
+  dim3 grid((a.N + GT - 1) / GT, (a.M + GT - 1) / GT, batch), block(256);
   if (!ta && !tb) hipLaunchKernelGGL((k_gemm_tile<T, false, false>), grid, block, 0, s, a);
   else if (!ta && tb) hipLaunchKernelGGL((k_gemm_tile<T, false, true>), grid, block, 0, s, a);
   else if (ta && !tb) hipLaunchKernelGGL((k_gemm_tile<T, true, false>), grid, block, 0, s, a);
@@ -217,6 +222,7 @@ inline GemmArgs<T> gemm_args(const T* A, int64_t lda, const T* B, int64_t ldb, T
   g.M = M; g.N = N; g.K = K; g.alpha = alpha; g.epi = epi;
   g.krange = KR_FULL; g.lower_only = 0; g.row_scale = nullptr; g.row_bcast = 0;
   g.nz_flag = nullptr; g.skip_if_zero = nullptr; g.abort_flag = nullptr;
+  g.sA = 0; g.sB = 0; g.sC = 0;
   return g;
 }
 

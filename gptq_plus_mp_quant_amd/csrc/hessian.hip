@@ -3,66 +3,59 @@
 //
 // H[g] += X^T diag(s_g) X is computed as a symmetric rank-k update: only 128x128 tiles on or
 // above the diagonal are formed (the mirrored half is never computed), one workgroup per
-// (tile, group).  Each workgroup streams 32-token slabs of X[:, I] and X[:, J] (fp16/bf16/fp32)
-// through double-buffered LDS, converting to fp32 once; the per-token saliency s[t, g] is
-// folded into the B operand as it is written to LDS (the reference's `weighted` tensor,
-// fl32(x * s), is never materialised).  Products run on v_mfma_f32_32x32x2f32 with fp32
-// accumulation; each 64x64 quarter of the tile belongs to one wave (2x2 MFMA blocks).
-// The diagonal tiles of group 0 also accumulate act_square = sum_t x^2.  No atomics: every
-// output element has exactly one owner, so results are bitwise reproducible run to run.
+// (tile, group), three workgroups per CU.  Each workgroup streams 32-token slabs of X[:, I]
+// and X[:, J] (fp16/bf16/fp32, read in place): a slab is fetched into registers as raw
+// 16-byte vectors while the previous slab is multiplied, then converted to fp32 and written
+// to LDS token-minor ([column][token], row stride 36 floats, so each lane reads its 8 tokens
+// of one column with two conflict-free ds_read_b128).  The per-token saliency s[t, g] is folded
+// into the B operand as it is written (the reference's `weighted` = fl32(x * s) is never
+// materialised).  Products run on v_mfma_f32_32x32x2f32 with fp32 accumulation; each 64x64
+// quarter of the tile belongs to one wave (2x2 MFMA blocks of 32x32).  The diagonal tiles of
+// group 0 also accumulate act_square = sum_t x^2.  No atomics: every output element has
+// exactly one owner, so results are bitwise reproducible run to run.
 #include "rq_common.h"
 
 namespace {
 
-constexpr int HT = 128;      // output tile edge
-constexpr int HKC = 32;      // tokens per LDS slab
+constexpr int HT = 128;        // output tile edge
+constexpr int HKC = 32;        // tokens per slab
+constexpr int HS = HKC + 4;    // LDS row stride in floats (16-byte aligned, bank-spread)
 constexpr int HTHREADS = 256;
 
-struct XLoad {
-  float v[2][16];            // [side][16 consecutive columns]
+// Raw slab fragment of one thread: 16 consecutive columns of one token, per side.
+template <typename TX>
+struct RawSide {
+  static constexpr int NV = 16 * sizeof(TX) / 16;
+  union {
+    uint4 u[NV];
+    TX e[16];
+  };
 };
 
-template <typename TX>
-__device__ __forceinline__ void load_slab(const TX* __restrict__ X, int64_t ntok, int64_t ldx,
-                                          int C, int64_t t0, int I0, int J0, bool diag,
-                                          bool vec_ok, XLoad& r) {
-  const int tid = threadIdx.x;
-  const int k = tid >> 3;             // token within slab (0..31)
-  const int c0 = (tid & 7) * 16;      // first of 16 columns
-  const int64_t t = t0 + k;
+__device__ __forceinline__ float to_f32(__half v) { return __half2float(v); }
+__device__ __forceinline__ float to_f32(__hip_bfloat16 v) { return __bfloat162float(v); }
+__device__ __forceinline__ float to_f32(float v) { return v; }
+
+// Staging map: token k = tid & 31, column chunk = tid >> 5 (16 columns each).
+template <typename TX, bool EDGE>
+__device__ __forceinline__ void load_side(const TX* __restrict__ X, int64_t ntok, int64_t ldx, int C,
+                                          int64_t t, int col, RawSide<TX>& r) {
+  if (!EDGE) {
+    if (t < ntok) {
+      const uint4* q = reinterpret_cast<const uint4*>(X + t * ldx + col);
 #pragma unroll
-  for (int side = 0; side < 2; ++side) {
-    if (side == 1 && diag) break;
-    const int col = (side == 0 ? I0 : J0) + c0;
-    if (t < ntok && vec_ok && col + 16 <= C) {
-      const TX* p = X + t * ldx + col;
-      if constexpr (sizeof(TX) == 2) {
-        const uint4* q = reinterpret_cast<const uint4*>(p);
-        uint4 u0 = q[0], u1 = q[1];
-        const TX* h0 = reinterpret_cast<const TX*>(&u0);
-        const TX* h1 = reinterpret_cast<const TX*>(&u1);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          r.v[side][e] = rq_load_elem(h0 + e);
-          r.v[side][8 + e] = rq_load_elem(h1 + e);
-        }
-      } else {
-        const float4* q = reinterpret_cast<const float4*>(p);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float4 f = q[e];
-          r.v[side][4 * e + 0] = f.x;
-          r.v[side][4 * e + 1] = f.y;
-          r.v[side][4 * e + 2] = f.z;
-          r.v[side][4 * e + 3] = f.w;
-        }
-      }
+      for (int v = 0; v < RawSide<TX>::NV; ++v) r.u[v] = q[v];
     } else {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int cc = col + e;
-        r.v[side][e] = (t < ntok && cc < C) ? rq_load_elem(X + t * ldx + cc) : 0.0f;
-      }
+      for (int v = 0; v < RawSide<TX>::NV; ++v) r.u[v] = make_uint4(0, 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < RawSide<TX>::NV; ++v) r.u[v] = make_uint4(0, 0, 0, 0);
+    if (t < ntok) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (col + e < C) r.e[e] = X[t * ldx + col + e];
     }
   }
 }
@@ -79,13 +72,118 @@ __device__ __forceinline__ void upper_tile(int t, int nt, int& ti, int& tj) {
   tj = row + rem;
 }
 
+template <typename TX, bool EDGE>
+__device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t ntok, int64_t ldx,
+                                             int C, const float* __restrict__ sal, int64_t ld_sal,
+                                             int g, float* __restrict__ Hg,
+                                             float* __restrict__ act_sq, int I0, int J0, bool diag,
+                                             bool want_act, float (*As)[HS], float (*Bs)[HS]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int sk = tid & 31;            // staged token
+  const int sc = (tid >> 5) * 16;     // first staged column
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  float actp[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) actp[e] = 0.0f;
+
+  RawSide<TX> ra, rb;
+  const int64_t nslab = (ntok + HKC - 1) / HKC;
+  load_side<TX, EDGE>(X, ntok, ldx, C, sk, I0 + sc, ra);
+  if (!diag) load_side<TX, EDGE>(X, ntok, ldx, C, sk, J0 + sc, rb);
+
+  const int fi = lane & 31;           // fragment column within a 32-block
+  const int fk = (lane >> 5) * 16;    // this lane's first token in the slab
+
+  for (int64_t sidx = 0; sidx < nslab; ++sidx) {
+    const int64_t t = sidx * HKC + sk;
+    const float s = (t < ntok) ? sal[t * ld_sal + g] : 0.0f;
+    __syncthreads();                  // previous slab fully consumed
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float xa = to_f32(ra.e[e]);
+      const float xb = diag ? xa : to_f32(rb.e[e]);
+      As[sc + e][sk] = xa;
+      Bs[sc + e][sk] = xb * s;        // fl32(x * s): the reference's `weighted`
+      if (want_act) actp[e] += xa * xa;
+    }
+    __syncthreads();
+    if (sidx + 1 < nslab) {           // next slab in flight while this one is multiplied
+      load_side<TX, EDGE>(X, ntok, ldx, C, t + HKC, I0 + sc, ra);
+      if (!diag) load_side<TX, EDGE>(X, ntok, ldx, C, t + HKC, J0 + sc, rb);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kb = fk + h * 8;
+      const float4* pa0 = reinterpret_cast<const float4*>(&As[wr * 64 + fi][kb]);
+      const float4* pa1 = reinterpret_cast<const float4*>(&As[wr * 64 + 32 + fi][kb]);
+      const float4* pb0 = reinterpret_cast<const float4*>(&Bs[wc * 64 + fi][kb]);
+      const float4* pb1 = reinterpret_cast<const float4*>(&Bs[wc * 64 + 32 + fi][kb]);
+      float a0[8], a1[8], b0[8], b1[8];
+      *reinterpret_cast<float4*>(a0) = pa0[0];
+      *reinterpret_cast<float4*>(a0 + 4) = pa0[1];
+      *reinterpret_cast<float4*>(a1) = pa1[0];
+      *reinterpret_cast<float4*>(a1 + 4) = pa1[1];
+      *reinterpret_cast<float4*>(b0) = pb0[0];
+      *reinterpret_cast<float4*>(b0 + 4) = pb0[1];
+      *reinterpret_cast<float4*>(b1) = pb1[0];
+      *reinterpret_cast<float4*>(b1 + 4) = pb1[1];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        // MFMA step: lanes 0-31 contribute token kb+q, lanes 32-63 token 16+kb+q
+        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[q], b0[q], acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[q], b1[q], acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[q], b0[q], acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[q], b1[q], acc[1][1], 0, 0, 0);
+      }
+    }
+  }
+
+  // H[g][I0 + i][J0 + j] += acc   (32x32 block layout: i = 8*(e/4) + 4*(lane/32) + e%4, j = lane%32)
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int i = I0 + wr * 64 + bi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int j = J0 + wc * 64 + bj * 32 + (lane & 31);
+        if (!EDGE || (i < C && j < C)) {
+          float* p = Hg + (int64_t)i * C + j;
+          *p = *p + acc[bi][bj][e];
+        }
+      }
+
+  if (want_act) {
+    // Sum the 32 per-token partials of each column in a fixed order (As is free now).
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) As[sc + e][sk] = actp[e];
+    __syncthreads();
+    if (tid < HT && I0 + tid < C) {
+      float sum = 0.0f;
+      for (int q = 0; q < HKC; ++q) sum += As[tid][q];
+      act_sq[I0 + tid] += sum;
+    }
+  }
+}
+
 template <typename TX>
-__global__ __launch_bounds__(HTHREADS, 2) void k_hessian_accum(
+__global__ __launch_bounds__(HTHREADS, 3) void k_hessian_accum(
     const TX* __restrict__ X, int64_t ntok, int64_t ldx, int C, const float* __restrict__ sal,
     int64_t ld_sal, int G, float* __restrict__ H, float* __restrict__ act_sq, int nt, int ntiles,
     bool vec_ok) {
-  __shared__ float As[2][HKC][HT];
-  __shared__ float Bs[2][HKC][HT];
+  __shared__ __attribute__((aligned(16))) float As[HT][HS];
+  __shared__ __attribute__((aligned(16))) float Bs[HT][HS];
 
   // XCD-aware order: consecutive hardware workgroup ids land on different XCDs (round
   // robin over 8); give each XCD a contiguous run of logical ids so neighbouring tiles,
@@ -101,94 +199,12 @@ __global__ __launch_bounds__(HTHREADS, 2) void k_hessian_accum(
   const int I0 = ti * HT, J0 = tj * HT;
   const bool diag = (ti == tj);
   const bool want_act = diag && (g == 0) && (act_sq != nullptr);
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wr = wave >> 1, wc = wave & 1;
-  const int lk = tid >> 3;            // token row this thread stages
-  const int lc = (tid & 7) * 16;      // first column this thread stages
-
-  floatx16 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-  float actp[16];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) actp[e] = 0.0f;
-
-  const int64_t nslab = (ntok + HKC - 1) / HKC;
-  XLoad r;
-
-  auto stage = [&](int buf, int64_t t0) {
-    const int64_t t = t0 + lk;
-    const float s = (t < ntok) ? sal[t * ld_sal + g] : 0.0f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float xa = r.v[0][e];
-      As[buf][lk][lc + e] = xa;
-      const float xb = diag ? xa : r.v[1][e];
-      Bs[buf][lk][lc + e] = xb * s;       // fl32(x * s): the reference's `weighted`
-      if (want_act) actp[e] += xa * xa;
-    }
-  };
-
-  load_slab<TX>(X, ntok, ldx, C, 0, I0, J0, diag, vec_ok, r);
-  stage(0, 0);
-  __syncthreads();
-
-  for (int64_t sidx = 0; sidx < nslab; ++sidx) {
-    const int buf = (int)(sidx & 1);
-    const bool more = (sidx + 1) < nslab;
-    if (more) load_slab<TX>(X, ntok, ldx, C, (sidx + 1) * HKC, I0, J0, diag, vec_ok, r);
-#pragma unroll
-    for (int ks = 0; ks < HKC / 2; ++ks) {
-      const int k = 2 * ks + (lane >> 5);
-      const float a0 = As[buf][k][wr * 64 + (lane & 31)];
-      const float a1 = As[buf][k][wr * 64 + 32 + (lane & 31)];
-      const float b0 = Bs[buf][k][wc * 64 + (lane & 31)];
-      const float b1 = Bs[buf][k][wc * 64 + 32 + (lane & 31)];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
-    }
-    if (more) stage(buf ^ 1, (sidx + 1) * HKC);
-    __syncthreads();
-  }
-
-  // H[g][I0 + i][J0 + j] += acc   (32x32 block layout: i = 8*(e/4) + 4*(lane/32) + e%4, j = lane%32)
   float* Hg = H + (int64_t)g * C * C;
-#pragma unroll
-  for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-    for (int bj = 0; bj < 2; ++bj)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int i = I0 + wr * 64 + bi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const int j = J0 + wc * 64 + bj * 32 + (lane & 31);
-        if (i < C && j < C) {
-          float* p = Hg + (int64_t)i * C + j;
-          *p = *p + acc[bi][bj][e];
-        }
-      }
-
-  if (want_act) {
-    // Sum the 32 per-token-row partials of each column in a fixed order (As is free now).
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < 16; ++e) As[0][lk][lc + e] = actp[e];
-    __syncthreads();
-    if (tid < HT && I0 + tid < C) {
-      float s = 0.0f;
-      for (int q = 0; q < HKC; ++q) s += As[0][q][tid];
-      act_sq[I0 + tid] += s;
-    }
-  }
+  const bool interior = vec_ok && (J0 + HT <= C);   // I0 <= J0
+  if (interior)
+    hessian_tile<TX, false>(X, ntok, ldx, C, sal, ld_sal, g, Hg, act_sq, I0, J0, diag, want_act, As, Bs);
+  else
+    hessian_tile<TX, true>(X, ntok, ldx, C, sal, ld_sal, g, Hg, act_sq, I0, J0, diag, want_act, As, Bs);
 }
 
 }  // namespace

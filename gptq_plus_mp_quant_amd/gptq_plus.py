@@ -113,32 +113,54 @@ class GPTQPlus:
                             n_bad, self.layer.__class__.__name__)
         self._finalized = True
 
-    # gptq_plus_utils.py:494-561
+    # gptq_plus_utils.py:494-561, for a batch of subgroups (each with its own schedule)
     def _hessian_inverse(self, H_work, Hinv_out, Hinv_init_out, workspace, percdamp,
                          damp_auto_increment=0.0015, log_context=""):
-        damp_percent = float(percdamp)
-        if damp_percent <= 0:
-            raise ValueError(f"Quantization{log_context}: `damp_percent` must be positive. current is {damp_percent}")
-        info = torch.zeros(1, dtype=torch.int32, device=self.dev)
-        C = self.columns
-        attempts = 0
-        while 1 > damp_percent > 0:
-            attempts += 1
-            K.chol_hinv_attempt(H_work, damp_percent, workspace, Hinv_out, Hinv_init_out, info)
-            if int(info.item()) == 0:
-                return damp_percent, False, attempts
-            logging.warning("Quantization%s: Current `damp_percent = %.5f` is too low, auto-incrementing by `%.5f`",
-                            log_context, damp_percent, damp_auto_increment)
-            damp_percent += damp_auto_increment
-        if damp_percent >= 1:
-            logging.warning("Quantization%s: `damp_percent` reached %.5f; falling back to identity "
-                            "Hessian inverse for this subgroup.", log_context, damp_percent)
-            eye = torch.eye(C, device=self.dev)
-            Hinv_out.copy_(eye)
-            if Hinv_init_out is not None:
-                Hinv_init_out.copy_(eye)
-            return damp_percent, True, attempts
-        raise ValueError(f"Quantization{log_context}: `damp_percent` must between 0 and 1. current is {damp_percent}")
+        """H_work [nb, C, C] (or [C, C]) is damped in place; returns [(damp, fallback, attempts)]."""
+        damp0 = float(percdamp)
+        if damp0 <= 0:
+            raise ValueError(f"Quantization{log_context}: `damp_percent` must be positive. current is {damp0}")
+        if H_work.dim() == 2:
+            H_work, Hinv_out = H_work[None], Hinv_out[None]
+            Hinv_init_out = None if Hinv_init_out is None else Hinv_init_out[None]
+        nb, C = H_work.shape[0], H_work.shape[-1]
+        damp = [damp0] * nb
+        attempts = [0] * nb
+        status = ["run" if 1 > damp0 > 0 else "range"] * nb
+        info = torch.zeros(nb, dtype=torch.int32, device=self.dev)
+        while any(st == "run" for st in status):
+            todo = [damp[b] if status[b] == "run" else 0.0 for b in range(nb)]
+            for b in range(nb):
+                attempts[b] += status[b] == "run"
+            K.chol_hinv_attempt(H_work, todo, workspace, Hinv_out, Hinv_init_out, info)
+            codes = info.tolist()
+            for b in range(nb):
+                if status[b] != "run":
+                    continue
+                if codes[b] == 0:
+                    status[b] = "ok"
+                    continue
+                logging.warning("Quantization%s subgroup=%d: Current `damp_percent = %.5f` is too low, "
+                                "auto-incrementing by `%.5f`", log_context, b, damp[b], damp_auto_increment)
+                damp[b] += damp_auto_increment
+                if not (1 > damp[b] > 0):
+                    status[b] = "range"
+        out = []
+        for b in range(nb):
+            if status[b] == "ok":
+                out.append((damp[b], False, attempts[b]))
+            elif damp[b] >= 1:
+                logging.warning("Quantization%s subgroup=%d: `damp_percent` reached %.5f; falling back to "
+                                "identity Hessian inverse for this subgroup.", log_context, b, damp[b])
+                eye = torch.eye(C, device=self.dev)
+                Hinv_out[b].copy_(eye)
+                if Hinv_init_out is not None:
+                    Hinv_init_out[b].copy_(eye)
+                out.append((damp[b], True, attempts[b]))
+            else:
+                raise ValueError(f"Quantization{log_context}: `damp_percent` must between 0 and 1. "
+                                 f"current is {damp[b]}")
+        return out
 
     # gptq_plus_utils.py:910-1896 (frozen mode)
     @torch.no_grad()
@@ -227,45 +249,58 @@ class GPTQPlus:
             Wp = torch.empty((R, C), **f32)
             Z = torch.empty((R, C), **f32)
             GH = torch.empty((R, C), **f32)
+            Gs = torch.empty((R, C), **f32)
             Hinv_all = torch.empty((G, C, C), **f32)
-            H_work = torch.empty((C, C), **f32)
             beta_mode = 1 if (enable_gradient_update and self.alpha > 0) else 0
             want_init = beta_mode == 1 or keep_hinv
-            workspace = K.chol_workspace(C, dev) if inject_hinv is None else None
-            Gs = torch.empty((R_s, C), **f32)
-            GH0 = torch.empty((R_s, C), **f32) if beta_mode == 1 else None
-            z_flags = torch.zeros(G, dtype=torch.int32, device=dev)
+            Hinit_all = torch.empty((G, C, C), **f32) if want_init else None
             grads = self.gradients.to(**f32)
             if grads.stride(1) != 1:
                 grads = grads.contiguous()
+            # slice, dead-column fix and act_order gathers of every subgroup
+            H_work = torch.empty((G, C, C), **f32)
+            with _section(rec, "fasterquant.subgroup.slice_inputs"):
+                for sub in range(G):
+                    r0 = sub * R_s
+                    K.prepare_subgroup(W[r0:], grads[r0:], self.H[sub], perm, Wp[r0:r0 + R_s],
+                                       Gs[r0:r0 + R_s], H_work[sub])
+            # damped Cholesky chain, subgroups batched through every launch
+            with _section(rec, "fasterquant.subgroup.compute_hinv"):
+                if inject_hinv is None:
+                    nb = self._chol_batch(C, G, dev)
+                    workspace = K.chol_workspace(C, dev, nb)
+                    chain = []
+                    for b0 in range(0, G, nb):
+                        b1 = min(G, b0 + nb)
+                        chain += self._hessian_inverse(
+                            H_work[b0:b1], Hinv_all[b0:b1],
+                            None if Hinit_all is None else Hinit_all[b0:b1], workspace, percdamp)
+                    del workspace
+                else:   # test hook: use given (Hinv_init, Hinv) pairs
+                    chain = []
+                    for sub in range(G):
+                        Hinv_all[sub].copy_(inject_hinv[sub][1])
+                        if Hinit_all is not None:
+                            Hinit_all[sub].copy_(inject_hinv[sub][0])
+                        chain.append((float(percdamp), False, 0))
+            del H_work
+            GH0 = torch.empty((R_s, C), **f32) if beta_mode == 1 else None
+            z_flags = torch.zeros(G, dtype=torch.int32, device=dev)
             alpha_eff = self.alpha / (R * C) if beta_mode == 1 else 0.0
             self.subgroup_info = []
-            hinv_init_keep = []
             for sub in range(G):
                 r0 = sub * R_s
-                Hinit = torch.empty((C, C), **f32) if want_init else None
-                with _section(rec, "fasterquant.subgroup.slice_inputs"):
-                    K.prepare_subgroup(W[r0:], grads[r0:], self.H[sub], perm, Wp[r0:r0 + R_s], Gs, H_work)
-                with _section(rec, "fasterquant.subgroup.compute_hinv"):
-                    if inject_hinv is None:
-                        damp, fallback, attempts = self._hessian_inverse(
-                            H_work, Hinv_all[sub], Hinit, workspace, percdamp, log_context=f" subgroup={sub}")
-                    else:   # test hook: use a given (Hinv_init, Hinv) pair for this subgroup
-                        Hinv_all[sub].copy_(inject_hinv[sub][1])
-                        if Hinit is not None:
-                            Hinit.copy_(inject_hinv[sub][0])
-                        damp, fallback, attempts = float(percdamp), False, 0
                 beta = torch.empty(R_s if beta_mode == 1 else 1, **f32)
                 with _section(rec, "fasterquant.subgroup.init_ghinv"):
-                    K.gptqplus_terms(Gs, Hinit, Hinv_all[sub], alpha_eff, float(self.reference_loss),
-                                     beta_mode, beta, Z[r0:r0 + R_s], GH[r0:r0 + R_s], GH0, z_flags[sub:sub + 1])
+                    K.gptqplus_terms(Gs[r0:r0 + R_s], None if Hinit_all is None else Hinit_all[sub],
+                                     Hinv_all[sub], alpha_eff, float(self.reference_loss), beta_mode, beta,
+                                     Z[r0:r0 + R_s], GH[r0:r0 + R_s], GH0, z_flags[sub:sub + 1])
                 if beta_mode == 1 and self.reference_loss <= 0:
                     beta = torch.zeros(R_s, **f32)
+                damp, fallback, attempts = chain[sub]
                 self.subgroup_info.append(dict(damp_percent=damp, identity_fallback=fallback,
                                                attempts=attempts, beta=beta))
-                if keep_hinv:
-                    hinv_init_keep.append(Hinit)
-            del H_work, workspace, Gs, GH0
+            del Gs, GH0
             self.GHinv_initial = GH.clone() if keep_hinv else None
             z_any = torch.amax(z_flags).reshape(1).contiguous()
 
@@ -300,11 +335,19 @@ class GPTQPlus:
         self._codes_perm = codes
         self.qmode, self.scale_table, self.col_group, self.dyn_scale = qmode, scale_tab, col_group, dyn_scale
         self.Hinv_all = Hinv_all if keep_hinv else None
-        self.Hinv_init_all = hinv_init_keep if keep_hinv else None
+        self.Hinv_init_all = Hinit_all if keep_hinv else None
         self.Z = Z if keep_hinv else None
         if int(nan_flag.item()):
             logging.warning("NaN in weights")
             raise ValueError("NaN in weights")
+
+    @staticmethod
+    def _chol_batch(C, G, dev):
+        """How many subgroups to factorise per launch: all of them when their fp64 workspaces
+        fit in 40 % of the free device memory, fewer otherwise."""
+        per = int(nat.load().rq_chol_workspace_bytes(C))
+        free, _ = torch.cuda.mem_get_info(dev)
+        return max(1, min(G, int(0.4 * free) // per))
 
     @property
     def codes(self):

@@ -5,6 +5,8 @@ HIP stream of the tensors' device, and raises ``RuntimeError`` on a non-zero sta
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _native as nat
@@ -93,17 +95,29 @@ def prepare_subgroup(w, grad, H_g, perm, W_sub, G_sub, H_sub):
              nat.ptr(H_sub), _stream(w))
 
 
-def chol_workspace(C, device):
-    return torch.empty(int(nat.load().rq_chol_workspace_bytes(C)), dtype=torch.uint8, device=device)
+def chol_workspace(C, device, nb=1):
+    return torch.empty(nb * int(nat.load().rq_chol_workspace_bytes(C)), dtype=torch.uint8, device=device)
 
 
 def chol_hinv_attempt(H_work, damp_percent, workspace, Hinv, Hinv_init=None, info=None):
-    C = H_work.shape[0]
+    """One damping attempt for H_work [C, C] or a batch [nb, C, C]; damp_percent is a float or a
+    list (entries <= 0 skip that matrix).  Returns the device info tensor [nb]."""
+    batched = H_work.dim() == 3
+    nb = H_work.shape[0] if batched else 1
+    C = H_work.shape[-1]
     _cout(H_work, "H_work"), _cout(Hinv, "Hinv"), _cout(Hinv_init, "Hinv_init")
+    if Hinv.numel() != nb * C * C or (Hinv_init is not None and Hinv_init.numel() != nb * C * C):
+        raise ValueError("chol_hinv_attempt: output shape mismatch")
+    if workspace.numel() < nb * int(nat.load().rq_chol_workspace_bytes(C)):
+        raise ValueError("chol_hinv_attempt: workspace too small")
+    damps = list(damp_percent) if isinstance(damp_percent, (list, tuple)) else [float(damp_percent)] * nb
+    if len(damps) != nb:
+        raise ValueError("chol_hinv_attempt: one damp_percent per matrix")
     if info is None:
-        info = torch.zeros(1, dtype=torch.int32, device=H_work.device)
-    nat.call("rq_chol_hinv_attempt", nat.ptr(H_work), C, float(damp_percent), nat.ptr(workspace),
-             nat.ptr(Hinv), nat.ptr(Hinv_init), nat.ptr(info), _stream(H_work))
+        info = torch.zeros(nb, dtype=torch.int32, device=H_work.device)
+    arr = (ctypes.c_double * nb)(*[float(d) for d in damps])
+    nat.call("rq_chol_hinv_attempt", nat.ptr(H_work), C, nb, arr, nat.ptr(workspace), nat.ptr(Hinv),
+             nat.ptr(Hinv_init), nat.ptr(info), _stream(H_work))
     return info
 
 

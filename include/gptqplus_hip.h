@@ -71,17 +71,20 @@ int rq_prepare_subgroup(const void* w, int w_dtype, int64_t ldw, const float* gr
                         const float* H_g, int R_s, int C, const int64_t* perm, float* W_sub,
                         int64_t ld_wsub, float* G_sub, int64_t ld_gsub, float* H_sub, void* stream);
 
-/* Bytes of device workspace rq_chol_hinv_attempt needs for a C x C Hessian. */
+/* Bytes of device workspace rq_chol_hinv_attempt needs per C x C matrix. */
 int64_t rq_chol_workspace_bytes(int C);
 
-/* One attempt of GPTQPlus._compute_hessian_inverse_with_fallback -- gptq_plus_utils.py:519-533:
- * H_work[i,i] += fl32(damp_percent) * mean(diag(H_work))   (in place: retries accumulate),
- * then Hinv = upper Cholesky factor of H_work^-1 (Hinv^T Hinv = H_work^-1) and, when
- * Hinv_init != NULL, Hinv_init = H_work^-1.  Factorisation in fp64 (blocked, MFMA).
- * *info (device int) is set non-zero when H_work is not positive definite or the result is
- * not finite; the caller reads it after the stream completes and retries. */
-int rq_chol_hinv_attempt(float* H_work, int C, double damp_percent, void* workspace, float* Hinv,
-                         float* Hinv_init, int* info, void* stream);
+/* One attempt of GPTQPlus._compute_hessian_inverse_with_fallback -- gptq_plus_utils.py:519-533,
+ * for a batch of nb <= 64 subgroup matrices H_work[b] = H_work + b*C*C (one per row group):
+ * H_work[b][i,i] += fl32(damp_percent[b]) * mean(diag(H_work[b]))  (in place: retries
+ * accumulate, as in the reference), then Hinv[b] = upper Cholesky factor of H_work[b]^-1
+ * (Hinv^T Hinv = H_work^-1) and, when Hinv_init != NULL, Hinv_init[b] = H_work[b]^-1.
+ * damp_percent is a HOST array; entries <= 0 are skipped (left untouched).  Factorisation in
+ * fp64 (blocked, MFMA).  info (device int[nb]) is written per entry: 0 = done, > 0 = not
+ * positive definite or non-finite result (caller raises the damping and retries that entry),
+ * -1 = skipped.  workspace holds nb * rq_chol_workspace_bytes(C) bytes. */
+int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* damp_percent, void* workspace,
+                         float* Hinv, float* Hinv_init, int* info, void* stream);
 
 /* GPTQPlus._compute_gradient_terms -- gptq_plus_utils.py:563-578 with
  * compute_safe_beta_from_reference_loss -- :174-194.

@@ -152,6 +152,27 @@ def test_cholesky_chain(C):
     assert rel_fro(Hw, Hd_ref) <= 1e-7
 
 
+def test_cholesky_batch_independent_entries():
+    """Batched attempt: each matrix gets its own damping, skipped entries stay untouched, and a
+    non-positive-definite entry fails alone."""
+    C = 200
+    Hs = [_spd(7, C), _spd(8, C), -torch.eye(C), _spd(9, C)]
+    damps = [0.01, 0.02, 0.01, 0.0]          # last entry skipped
+    Hw = torch.stack(Hs).to(DEV).contiguous()
+    before = Hw.clone()
+    ws = K.chol_workspace(C, DEV, 4)
+    Hinv = torch.zeros(4, C, C, device=DEV)
+    Hinit = torch.zeros(4, C, C, device=DEV)
+    info = K.chol_hinv_attempt(Hw, damps, ws, Hinv, Hinit)
+    torch.cuda.synchronize()
+    codes = info.tolist()
+    assert codes[0] == 0 and codes[1] == 0 and codes[2] > 0 and codes[3] == -1
+    assert torch.equal(Hw[3], before[3]) and not Hinv[3].any()
+    for b in (0, 1):
+        Hi_o, Hv_o, *_ = hessian_inverse_with_fallback(Hs[b], damps[b])
+        assert rel_fro(Hinv[b], Hv_o) <= 1e-4 and rel_fro(Hinit[b], Hi_o) <= 1e-4
+
+
 @pytest.mark.parametrize("neg", [0.05, 0.3, 5.0])
 def test_cholesky_retry_schedule(neg):
     """Indefinite diagonal H: the damping retries (cumulative on the same working copy)
@@ -164,7 +185,7 @@ def test_cholesky_retry_schedule(neg):
     g = GPTQPlus(layer, torch.ones(1, 1, 1), torch.zeros(8, 80), 1, 0.0, 0.0)
     Hw = H.to(DEV).clone()
     Hinv = torch.empty(80, 80, device=DEV)
-    p, fb, att = g._hessian_inverse(Hw, Hinv, None, K.chol_workspace(80, DEV), 0.01)
+    (p, fb, att), = g._hessian_inverse(Hw, Hinv, None, K.chol_workspace(80, DEV), 0.01)
     assert (att, fb) == (att_o, fb_o) and abs(p - p_o) < 1e-12
     if fb:
         assert torch.equal(Hinv.cpu(), torch.eye(80))

@@ -28,7 +28,7 @@ def test_header_symbols_are_exported_and_bound():
 def test_version_and_workspace_query():
     lib = _lib()
     assert lib.rq_version() == 100
-    assert lib.rq_chol_workspace_bytes(64) == 2 * 64 * 64 * 8 + 64 * 64 * 8
+    assert lib.rq_chol_workspace_bytes(64) == (2 * 64 * 64 + 64 * 64) * 8
     assert lib.rq_chol_workspace_bytes(0) < 0
 
 
@@ -38,7 +38,9 @@ def test_argument_validation_needs_no_device():
     assert lib.rq_hessian_accum(null, 0, 10, 8, 8, null, 1, 1, null, null, null) == nat.RQ_EINVAL
     assert lib.rq_find_params(null, 0, 4, 4, 4, -1, 7, 1, null, null, null) == nat.RQ_EINVAL
     assert lib.rq_act_order_perm(null, 4, null, null, null) == nat.RQ_EINVAL
-    assert lib.rq_chol_hinv_attempt(null, 4, 0.01, null, null, null, null, null) == nat.RQ_EINVAL
+    damp = (ctypes.c_double * 1)(0.01)
+    assert lib.rq_chol_hinv_attempt(null, 4, 1, damp, null, null, null, null, null) == nat.RQ_EINVAL
+    assert lib.rq_chol_hinv_attempt(null, 4, 65, damp, null, null, null, null, null) == nat.RQ_EINVAL
     assert lib.rq_quant_block(null, 4, null, 4, null, null, 4, 4, 4, 0, 4, 0, null, null, null, 7, 1,
                               0, null, null, null, null) == nat.RQ_EINVAL
     assert lib.rq_trailing_update(null, 4, null, null, 4, null, 4, 4, 4, 0, 4, null, null, null) == nat.RQ_EINVAL
