@@ -120,6 +120,18 @@ def cpu_baseline(X, W, s, grad, cfg, chunks=2):
                         f"finalize_hessian+fasterquant ({t_fq:.1f} s); {platform.processor() or platform.machine()}"))
 
 
+def copy_calibration(dev, nbytes=1 << 30, reps=3):
+    """A plain device-to-device copy of known size, profiled with the same FETCH_SIZE /
+    WRITE_SIZE counters to calibrate them (bytes moved = nbytes read + nbytes written)."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "reps": reps}), flush=True)
+
+
 def load_traffic():
     path = os.path.join(ROOT, "profiles", "hessian_traffic.json")
     if os.path.exists(path):
@@ -135,6 +147,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-chunks", type=int, default=2)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (counter calibration for the traffic figure)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs the GPTQ+ hot path on one GPU only (asked for --gpus {args.gpus}); "
@@ -142,6 +156,9 @@ def main():
         sys.exit(2)
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        copy_calibration(dev)
+        return
     torch.backends.cuda.matmul.allow_tf32 = False
     cfg = dict(CFG)
     X, W, s, grad = make_inputs(dev, cfg)

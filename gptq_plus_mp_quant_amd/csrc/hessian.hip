@@ -60,6 +60,34 @@ __device__ __forceinline__ void load_side(const TX* __restrict__ X, int64_t ntok
   }
 }
 
+// Map a linear index to an upper-triangle tile (ti <= tj) in super-row order: rows are taken
+// HSR at a time and each super-row is walked column by column, so tiles that run at the same
+// time on one XCD share a few I strips and a few J strips of X (L2 reuse in both operands).
+constexpr int HSR = 4;
+__device__ __forceinline__ void upper_tile_blocked(int t, int nt, int& ti, int& tj) {
+  int r0 = 0;
+  int rem = t;
+  for (;;) {
+    const int h = min(HSR, nt - r0);
+    // tiles in this super-row: sum over tj >= r0 of min(h, tj - r0 + 1)
+    const int ncol = nt - r0;
+    const int cnt = (ncol >= h) ? (h * (h + 1) / 2 + (ncol - h) * h) : (ncol * (ncol + 1) / 2);
+    if (rem < cnt) break;
+    rem -= cnt;
+    r0 += h;
+  }
+  const int h = min(HSR, nt - r0);
+  for (int c = r0;; ++c) {
+    const int k = min(h, c - r0 + 1);
+    if (rem < k) {
+      ti = r0 + rem;
+      tj = c;
+      return;
+    }
+    rem -= k;
+  }
+}
+
 // Map a linear upper-triangle tile index to (ti, tj), ti <= tj, row-major.
 __device__ __forceinline__ void upper_tile(int t, int nt, int& ti, int& tj) {
   int row = 0;
@@ -195,7 +223,7 @@ __global__ __launch_bounds__(HTHREADS, 3) void k_hessian_accum(
   const int logical = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
   const int g = logical % G;
   int ti, tj;
-  upper_tile(logical / G, nt, ti, tj);
+  upper_tile_blocked(logical / G, nt, ti, tj);
   const int I0 = ti * HT, J0 = tj * HT;
   const bool diag = (ti == tj);
   const bool want_act = diag && (g == 0) && (act_sq != nullptr);
