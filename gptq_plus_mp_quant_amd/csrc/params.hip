@@ -49,6 +49,96 @@ __global__ __launch_bounds__(256) void k_find_params(const TW* __restrict__ w, i
   }
 }
 
+// WeightQuantizer.find_params with mse=True (utils/quant_utils.py:408-448): min/max start,
+// then a maxshrink*grid x maxshrink*grid shrink grid over (xmin, xmax); each candidate's row
+// error sum |q - x|^norm is reduced in a fixed order and the first strict minimum wins.
+// One 256-thread workgroup per (row, group).
+template <typename TW>
+__global__ __launch_bounds__(256) void k_find_params_mse(const TW* __restrict__ w, int R, int C,
+                                                         int64_t ldw, int gs, float maxq, int sym,
+                                                         float norm, int grid, int steps,
+                                                         float* __restrict__ scale,
+                                                         float* __restrict__ zero) {
+  __shared__ float red[256];
+  __shared__ float red2[256];
+  const int tid = threadIdx.x;
+  const int r = blockIdx.x, grp = blockIdx.y;
+  const int c0 = grp * gs;
+  const int c1 = min(C, c0 + gs);
+  const TW* row = w + (int64_t)r * ldw;
+  float mn = __builtin_inff(), mx = -__builtin_inff();
+  for (int c = c0 + tid; c < c1; c += 256) {
+    const float v = rq_load_elem(row + c);
+    mn = rq_nan_min(mn, v);
+    mx = rq_nan_max(mx, v);
+  }
+  red[tid] = mn;
+  red2[tid] = mx;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (tid < o) {
+      red[tid] = rq_nan_min(red[tid], red[tid + o]);
+      red2[tid] = rq_nan_max(red2[tid], red2[tid + o]);
+    }
+    __syncthreads();
+  }
+  float xmin = rq_nan_min(red[0], 0.0f);
+  float xmax = rq_nan_max(red2[0], 0.0f);
+  if (!sym && xmin == 0.0f && xmax == 0.0f) {
+    xmin = -1.0f;
+    xmax = 1.0f;
+  }
+  float bscale, bzero;
+  rq_params_from_minmax(red[0], red2[0], maxq, sym, &bscale, &bzero);
+  float best = __builtin_inff();
+  for (int i = 0; i < steps; ++i) {
+    const float fi = (float)(1.0 - (double)i / (double)grid);
+    for (int j = 0; j < steps; ++j) {
+      const float fj = (float)(1.0 - (double)j / (double)grid);
+      const float xmin1 = fi * xmin, xmax1 = fj * xmax;
+      float s1, z1;
+      if (sym) {
+        s1 = rq_clamp_min(rq_nan_max(fabsf(xmin1), xmax1), 1e-5f) / maxq;
+        z1 = 0.0f;
+      } else {
+        s1 = (xmax1 - xmin1) / maxq;
+        z1 = __builtin_rintf(-xmin1 / s1);
+      }
+      float part = 0.0f;
+      for (int c = c0 + tid; c < c1; c += 256) {
+        const float x = rq_load_elem(row + c);
+        float q;
+        if (sym) {
+          q = s1 * rq_quant_code(x, s1, -(maxq + 1.0f), maxq);
+        } else {
+          float t = __builtin_rintf(x / s1) + z1;
+          t = (t < 0.0f) ? 0.0f : t;
+          t = (t > maxq) ? maxq : t;
+          q = s1 * (t - z1);
+        }
+        part += powf(fabsf(q - x), norm);
+      }
+      __syncthreads();                  // red[] of the previous candidate fully read
+      red[tid] = part;
+      __syncthreads();
+      for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) red[tid] = red[tid] + red[tid + o];
+        __syncthreads();
+      }
+      const float err = red[0];
+      if (err < best) {                 // same value in every thread: uniform update
+        best = err;
+        bscale = s1;
+        bzero = z1;
+      }
+    }
+  }
+  if (tid == 0) {
+    scale[(int64_t)grp * R + r] = bscale;
+    zero[(int64_t)grp * R + r] = bzero;
+  }
+}
+
 // a sorts strictly before b in a descending sort with NaN first (torch orders NaN as largest).
 __device__ __forceinline__ bool desc_before(float a, float b) {
   const bool na = (a != a), nb = (b != b);
@@ -186,6 +276,31 @@ extern "C" int rq_find_params(const void* w, int w_dtype, int R, int C, int64_t 
   else if (w_dtype == RQ_F32)
     hipLaunchKernelGGL(k_find_params<float>, grid, block, 0, s, (const float*)w, R, C, ldw, gs,
                        (float)maxq, sym, scale, zero);
+  else
+    return RQ_EINVAL;
+  RQ_CHECK_LAUNCH();
+  return RQ_OK;
+}
+
+extern "C" int rq_find_params_mse(const void* w, int w_dtype, int R, int C, int64_t ldw,
+                                  int group_size, int maxq, int sym, double norm, int grid,
+                                  double maxshrink, float* scale, float* zero, void* stream) {
+  if (!w || !scale || !zero || R <= 0 || C <= 0 || ldw < C || maxq <= 0 || grid <= 0) return RQ_EINVAL;
+  const int gs = group_size > 0 ? group_size : C;
+  const int ng = (C + gs - 1) / gs;
+  const int steps = (int)(maxshrink * grid);   // int(self.maxshrink * self.grid)
+  if (steps <= 0) return RQ_EINVAL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 g(R, ng), block(256);
+  if (w_dtype == RQ_F16)
+    hipLaunchKernelGGL(k_find_params_mse<__half>, g, block, 0, s, (const __half*)w, R, C, ldw, gs,
+                       (float)maxq, sym, (float)norm, grid, steps, scale, zero);
+  else if (w_dtype == RQ_BF16)
+    hipLaunchKernelGGL(k_find_params_mse<__hip_bfloat16>, g, block, 0, s, (const __hip_bfloat16*)w, R,
+                       C, ldw, gs, (float)maxq, sym, (float)norm, grid, steps, scale, zero);
+  else if (w_dtype == RQ_F32)
+    hipLaunchKernelGGL(k_find_params_mse<float>, g, block, 0, s, (const float*)w, R, C, ldw, gs,
+                       (float)maxq, sym, (float)norm, grid, steps, scale, zero);
   else
     return RQ_EINVAL;
   RQ_CHECK_LAUNCH();

@@ -9,9 +9,9 @@ the layer dtype, ``int_weight`` / ``scale`` buffers with ``export_to_et``) follo
 reference.  Additionally exposed for inspection: ``perm``, ``invperm``, ``codes`` (natural
 column order), ``subgroup_info`` (damping, retries, identity fallback, beta).
 
-Modes whose work needs a layer backward or a clipping search (``g_update_mode`` other than
-``"frozen"``, ``WeightQuantizer(mse=True)``, ``diagnostic_recorder``) raise
-``NotImplementedError`` rather than silently running different arithmetic.
+Modes whose work needs a layer backward (``g_update_mode`` other than ``"frozen"``) and
+``diagnostic_recorder`` dumps raise ``NotImplementedError`` rather than silently running
+different arithmetic.
 """
 from __future__ import annotations
 
@@ -313,9 +313,17 @@ class GPTQPlus:
                     i2 = min(i1 + blocksize, C)
                     count = i2 - i1
                     atomic = bool(block_atomic_quant) and i2 < C
-                    K.quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale_tab, col_group,
-                                  dyn_scale[bidx] if dyn_scale is not None else None, maxq, sym, atomic,
-                                  z_any, codes, err)
+                    if qmode == nat.RQ_QMODE_DYNAMIC and q.mse:
+                        # dynamic groups + clip search: find_params on the block start
+                        # (gptq_plus_utils.py:1208-1209), then quantize with those row scales
+                        bscale, _ = q.params_on(Wp[:, i1:i2])
+                        dyn_scale[bidx].copy_(bscale[0])
+                        K.quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, nat.RQ_QMODE_CHANNEL,
+                                      dyn_scale[bidx], None, None, maxq, sym, atomic, z_any, codes, err)
+                    else:
+                        K.quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale_tab, col_group,
+                                      dyn_scale[bidx] if dyn_scale is not None else None, maxq, sym,
+                                      atomic, z_any, codes, err)
                     if i2 < C:
                         K.trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_any)
 

@@ -78,6 +78,20 @@ def find_params(w, maxq, sym, group_size=-1):
     return scale, zero
 
 
+def find_params_mse(w, maxq, sym, norm=2.4, grid=50, maxshrink=0.5, group_size=-1):
+    """find_params with the mse clip search: returns ([ng, R], [ng, R])."""
+    _rowmajor(w, "w")
+    R, C = w.shape
+    gs = group_size if group_size > 0 else C
+    ng = (C + gs - 1) // gs
+    scale = torch.empty((ng, R), device=w.device, dtype=_f32)
+    zero = torch.empty((ng, R), device=w.device, dtype=_f32)
+    nat.call("rq_find_params_mse", nat.ptr(w), nat.dtype_code(w.dtype), R, C, w.stride(0), gs, int(maxq),
+             int(bool(sym)), float(norm), int(grid), float(maxshrink), nat.ptr(scale), nat.ptr(zero),
+             _stream(w))
+    return scale, zero
+
+
 def act_order_perm(act_sq):
     C = act_sq.numel()
     perm = torch.empty(C, dtype=torch.int64, device=act_sq.device)

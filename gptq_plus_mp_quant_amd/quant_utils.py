@@ -3,8 +3,9 @@ runs the gfx950 ``rq_find_params`` kernel.
 
 Same constructor, ``configure`` arguments, attributes (``maxq``, ``scale``, ``zero``, ``bits``,
 ``perchannel``, ``sym``, ...) and method semantics as the reference.  ``find_params`` needs the
-tensor on the GPU.  The ``mse=True`` clipping grid search and ``weight_groupsize > 0`` are not
-implemented as kernels yet and raise ``NotImplementedError`` instead of diverging.
+tensor on the GPU; ``mse=True`` runs the clip grid search kernel (``rq_find_params_mse``).
+``weight_groupsize > 0`` (the activation-style grouping of ``find_params_weight_groupwise``,
+off the GPTQ+ path) raises ``NotImplementedError`` instead of diverging.
 """
 from __future__ import annotations
 
@@ -47,8 +48,6 @@ class WeightQuantizer(torch.nn.Module):
         self.maxq = torch.tensor(2 ** (bits - 1) - 1) if sym else torch.tensor(2 ** bits - 1)
 
     def _check_supported(self):
-        if self.mse:
-            raise NotImplementedError("WeightQuantizer(mse=True) clipping search has no HIP kernel yet")
         if getattr(self, "weight_groupsize", -1) > 0:
             raise NotImplementedError("weight_groupsize > 0 has no HIP kernel yet")
 
@@ -65,9 +64,14 @@ class WeightQuantizer(torch.nn.Module):
         ng = (C + gs - 1) // gs
         scale = torch.empty((ng, R), device=w.device, dtype=torch.float32)
         zero = torch.empty((ng, R), device=w.device, dtype=torch.float32)
-        nat.call("rq_find_params", nat.ptr(w), nat.dtype_code(w.dtype), R, C, w.stride(0), gs,
-                 int(self.maxq), int(bool(self.sym)), nat.ptr(scale), nat.ptr(zero),
-                 nat.stream_of(w.device))
+        if self.mse:
+            nat.call("rq_find_params_mse", nat.ptr(w), nat.dtype_code(w.dtype), R, C, w.stride(0), gs,
+                     int(self.maxq), int(bool(self.sym)), float(self.norm), int(self.grid),
+                     float(self.maxshrink), nat.ptr(scale), nat.ptr(zero), nat.stream_of(w.device))
+        else:
+            nat.call("rq_find_params", nat.ptr(w), nat.dtype_code(w.dtype), R, C, w.stride(0), gs,
+                     int(self.maxq), int(bool(self.sym)), nat.ptr(scale), nat.ptr(zero),
+                     nat.stream_of(w.device))
         return scale, zero
 
     # utils/quant_utils.py:390-457

@@ -57,6 +57,14 @@ int rq_hessian_finalize(float* H, float* act_sq, int G, int C, double h_div, dou
 int rq_find_params(const void* w, int w_dtype, int R, int C, int64_t ldw, int group_size,
                    int maxq, int sym, float* scale, float* zero, void* stream);
 
+/* WeightQuantizer.find_params with mse=True (the --w_clip grid search) -- utils/quant_utils.py:
+ * 408-448: per (row, group) min/max start, then int(maxshrink*grid)^2 shrunken (xmin, xmax)
+ * candidates scored by sum |q - x|^norm; the first strict minimum is kept.  Same layouts as
+ * rq_find_params. */
+int rq_find_params_mse(const void* w, int w_dtype, int R, int C, int64_t ldw, int group_size,
+                       int maxq, int sym, double norm, int grid, double maxshrink, float* scale,
+                       float* zero, void* stream);
+
 /* act_order permutation -- gptq_plus_utils.py:1046, 1050:
  * perm = argsort(act_sq, descending) with ties broken by ascending index (NaN first),
  * invperm = argsort(perm).  int64 outputs. */

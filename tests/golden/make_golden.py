@@ -42,6 +42,9 @@ CASES = [
     dict(name="g2_asym4_deadcols_zero_rows", R=32, C=64, G=2, N=8, T=16, bits=4, sym=False, gs=-1, act=True, B=16, atomic=False, alpha=0.0, ref_loss=0.0, dead=True),
     dict(name="g1_sym4_indefinite_retry", R=16, C=32, G=1, N=4, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=False, alpha=0.0, ref_loss=0.0, negsal=0.35),
     dict(name="g1_sym4_indefinite_identity", R=16, C=32, G=1, N=4, T=16, bits=4, sym=True, gs=-1, act=False, B=16, atomic=False, alpha=0.0, ref_loss=0.0, negsal=50.0),
+    dict(name="g2_sym4_mse_perchan_act", R=32, C=64, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=False, alpha=0.0, ref_loss=0.0, mse=True),
+    dict(name="g2_asym3_mse_static_groups", R=32, C=64, G=2, N=8, T=16, bits=3, sym=False, gs=16, act=True, B=16, atomic=False, alpha=0.0, ref_loss=0.0, mse=True),
+    dict(name="g1_sym4_mse_dynamic_atomic", R=32, C=48, G=1, N=8, T=16, bits=4, sym=True, gs=16, act=False, B=16, atomic=True, alpha=0.0, ref_loss=0.0, mse=True),
 ]
 
 
@@ -110,7 +113,7 @@ def run_case(gpu, qu, case, seed):
     g = gpu.GPTQPlus(layer, saliency=torch.from_numpy(s), gradient=torch.from_numpy(grad),
                      num_groups=case["G"], alpha=case["alpha"], reference_loss=case["ref_loss"])
     g.quantizer = qu.WeightQuantizer()
-    g.quantizer.configure(case["bits"], perchannel=True, sym=case["sym"], mse=False)
+    g.quantizer.configure(case["bits"], perchannel=True, sym=case["sym"], mse=case.get("mse", False))
     xs = torch.from_numpy(X)
     for j in range(0, xs.shape[0], 4):
         g.add_batch(xs[j:j + 4].data, None)

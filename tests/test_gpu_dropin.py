@@ -22,13 +22,13 @@ DEV = torch.device("cuda:0")
 GOLD = GoldenSet.load().cases
 
 
-def _gpu_obj(W, s, grad, G, alpha, ref_loss, bits, sym):
+def _gpu_obj(W, s, grad, G, alpha, ref_loss, bits, sym, mse=False):
     R, C = W.shape
     layer = torch.nn.Linear(C, R, bias=False).to(DEV, W.dtype)
     layer.weight.data.copy_(W.to(DEV))
     g = GPTQPlus(layer, saliency=s, gradient=grad, num_groups=G, alpha=alpha, reference_loss=ref_loss)
     g.quantizer = WeightQuantizer()
-    g.quantizer.configure(bits, perchannel=True, sym=sym, mse=False)
+    g.quantizer.configure(bits, perchannel=True, sym=sym, mse=mse)
     return g, layer
 
 
@@ -41,7 +41,8 @@ def _accumulate(g, X, bsz):
 @pytest.mark.parametrize("case", GOLD, ids=[c.name for c in GOLD])
 def test_golden_hessian(case):
     m = case.meta
-    g, _ = _gpu_obj(case.t("W"), case.t("s"), case.t("grad"), m["G"], m["alpha"], m["ref_loss"], m["bits"], m["sym"])
+    g, _ = _gpu_obj(case.t("W"), case.t("s"), case.t("grad"), m["G"], m["alpha"], m["ref_loss"], m["bits"], m["sym"],
+                    m.get("mse", False))
     _accumulate(g, case.t("X"), 4)
     torch.cuda.synchronize()
     assert rel_fro(g.H, case.H()) <= 1e-5
@@ -52,7 +53,8 @@ def test_golden_hessian(case):
 def test_golden_fasterquant_same_inverse(case):
     """Reference H, act_order perm and H^-1 factors injected: codes match the reference."""
     m = case.meta
-    g, layer = _gpu_obj(case.t("W"), case.t("s"), case.t("grad"), m["G"], m["alpha"], m["ref_loss"], m["bits"], m["sym"])
+    g, layer = _gpu_obj(case.t("W"), case.t("s"), case.t("grad"), m["G"], m["alpha"], m["ref_loss"], m["bits"], m["sym"],
+                    m.get("mse", False))
     _accumulate(g, case.t("X"), 4)
     g.H.copy_(case.H().to(DEV))
     g.act_square.copy_(case.t("act_square").to(DEV))
@@ -88,7 +90,8 @@ def test_golden_fasterquant_same_inverse(case):
 def test_golden_fasterquant_own_chain(case):
     """Every stage on the GPU (own Hessian, perm, fp64 Cholesky chain)."""
     m = case.meta
-    g, layer = _gpu_obj(case.t("W"), case.t("s"), case.t("grad"), m["G"], m["alpha"], m["ref_loss"], m["bits"], m["sym"])
+    g, layer = _gpu_obj(case.t("W"), case.t("s"), case.t("grad"), m["G"], m["alpha"], m["ref_loss"], m["bits"], m["sym"],
+                    m.get("mse", False))
     _accumulate(g, case.t("X"), 4)
     g.fasterquant(blocksize=m["B"], percdamp=0.01, groupsize=m["gs"], actorder=m["act"],
                   static_groups=m["act"], block_atomic_quant=m["atomic"], export_to_et=True, keep_hinv=True)
@@ -119,6 +122,8 @@ CFGS = [
     dict(name="g2_sym4_static_gplus", R=256, C=512, G=2, bits=4, sym=True, gs=128, act=True, B=128, atomic=False, alpha=0.05, ref_loss=3e4, gscale=1e-1),
     dict(name="g4_sym4_dynamic_atomic", R=256, C=512, G=4, bits=4, sym=True, gs=128, act=False, B=128, atomic=True, alpha=0.0),
     dict(name="g2_sym3_ragged", R=128, C=300, G=2, bits=3, sym=True, gs=-1, act=True, B=64, atomic=False, alpha=0.0),
+    dict(name="g2_asym4_mse_static", R=128, C=384, G=2, bits=4, sym=False, gs=128, act=True, B=128, atomic=False, alpha=0.0, mse=True),
+    dict(name="g2_sym4_mse_dynamic", R=128, C=384, G=2, bits=4, sym=True, gs=128, act=False, B=128, atomic=False, alpha=0.0, mse=True),
 ]
 
 
@@ -129,7 +134,7 @@ def test_dropin_vs_oracle(cfg):
     X, W, s, grad = synth(sum(map(ord, cfg["name"])), R, C, G, N, T, gscale=cfg.get("gscale", 1e-4))
     alpha, ref_loss = cfg["alpha"], cfg.get("ref_loss", 0.0)
     o = GPTQPlusOracle(W, s, grad, G, alpha, ref_loss)
-    o.quantizer = make_quantizer(cfg["bits"], cfg["sym"])
+    o.quantizer = make_quantizer(cfg["bits"], cfg["sym"], cfg.get("mse", False))
     for j in range(0, N, 4):
         o.add_batch(X[j:j + 4])
     o.finalize_hessian()
@@ -137,7 +142,7 @@ def test_dropin_vs_oracle(cfg):
               static_groups=cfg["act"], block_atomic_quant=cfg["atomic"])
     res = o.fasterquant(stable_ties=True, **fq)
 
-    g, layer = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"])
+    g, layer = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False))
     _accumulate(g, X, 4)
     assert rel_fro(g.H, o.H) <= 1e-5
     # (1) same H, same H^-1: codes bit-exact up to trailing-GEMM rounding ties
@@ -156,7 +161,7 @@ def test_dropin_vs_oracle(cfg):
     assert flips_same <= max(2, n // (1000 if alpha > 0 else 10000))
     # (2) own fp64 Cholesky chain
     layer.weight.data.copy_(W.to(DEV))
-    g2, layer2 = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"])
+    g2, layer2 = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False))
     g2.H = o.H.to(DEV).clone()
     g2.act_square = o.act_square.to(DEV).clone()
     g2._finalized = True

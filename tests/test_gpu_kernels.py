@@ -102,6 +102,28 @@ def test_find_params_bitexact(bits, sym, gs):
         assert torch.allclose(zero[k].cpu(), qo.zero.flatten(), rtol=0, atol=0, equal_nan=True)
 
 
+@pytest.mark.parametrize("bits,sym", [(4, True), (4, False), (3, True), (3, False)])
+@pytest.mark.parametrize("gs", [-1, 64])
+def test_find_params_mse_matches_oracle(bits, sym, gs):
+    """The --w_clip grid search: the chosen (scale, zero) must equal the oracle's, except
+    where two candidates' error sums tie to within summation-order rounding (reported)."""
+    r = rng(100 + bits * 10 + sym)
+    W = torch.from_numpy(r.standard_normal((96, 256)).astype(np.float32) * 0.03).to(torch.float16)
+    W[3] = 0
+    q = make_quantizer(bits, sym, mse=True)
+    scale, zero = K.find_params_mse(W.to(DEV), int(q.maxq), sym, group_size=gs)
+    groups = range(0, 256, gs) if gs > 0 else [0]
+    mism = 0
+    for k, c0 in enumerate(groups):
+        qo = make_quantizer(bits, sym, mse=True)
+        qo.find_params(W.float()[:, c0:c0 + gs] if gs > 0 else W.float())
+        diff = (scale[k].cpu() != qo.scale.flatten()) | (zero[k].cpu() != qo.zero.flatten())
+        mism += int(diff.sum())
+    n = 96 * len(groups)
+    print(f"mse search: {mism}/{n} (row, group) choices differ from the oracle")
+    assert mism <= max(1, n // 100)
+
+
 def test_act_order_perm_stable_desc():
     r = rng(3)
     a = torch.from_numpy(r.integers(0, 40, size=3000).astype(np.float32))

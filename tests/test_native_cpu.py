@@ -59,6 +59,9 @@ def test_dropin_rejects_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU"):
         q.find_params(torch.ones(4, 8))
     q.configure(4, perchannel=True, sym=True, mse=True)
+    with pytest.raises(RuntimeError, match="GPU"):
+        q.find_params(torch.ones(4, 8))
+    q.configure(4, perchannel=True, sym=True, weight_groupsize=4)
     with pytest.raises(NotImplementedError):
         q.find_params(torch.ones(4, 8))
 

@@ -18,7 +18,7 @@ def _run(case, inject_H=False):
     m = case.meta
     W = case.t("W")
     g = GPTQPlusOracle(W, case.t("s"), case.t("grad"), m["G"], m["alpha"], m["ref_loss"])
-    g.quantizer = make_quantizer(m["bits"], m["sym"])
+    g.quantizer = make_quantizer(m["bits"], m["sym"], m.get("mse", False))
     X = case.t("X")
     for j in range(0, X.shape[0], 4):
         g.add_batch(X[j:j + 4])
@@ -69,6 +69,7 @@ def test_golden_cover_the_branches():
     assert any(m["alpha"] > 0 for m in metas)                                       # beta != 0
     assert any(not m["sym"] for m in metas)                                         # asym quirk
     assert any(m["C"] % m["B"] for m in metas)                                      # ragged last block
+    assert sum(bool(m.get("mse")) for m in metas) >= 3                              # clip search
     assert "g1_sym4_indefinite_identity" in names
     ident = GoldenSet.load().by_name("g1_sym4_indefinite_identity")
     assert bool(ident.arrays["sub0_identity_fallback"])
