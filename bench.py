@@ -49,6 +49,134 @@ def make_inputs(dev, cfg):
     return X, W, s, grad
 
 
+# a full Llama-3-8B decoder layer; modules that read the same input share one X
+LAYER8B = [("q_proj", 4096, 4096, "attn"), ("k_proj", 1024, 4096, "attn"), ("v_proj", 1024, 4096, "attn"),
+           ("o_proj", 4096, 4096, "o"), ("gate_proj", 14336, 4096, "mlp"), ("up_proj", 14336, 4096, "mlp"),
+           ("down_proj", 4096, 14336, "down")]
+
+
+def make_layer_inputs(dev, cfg):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(cfg["seed"] + 1)
+    N, T, G = cfg["N"], cfg["T"], cfg["G"]
+    xs = {}
+    for key, C in (("attn", 4096), ("o", 4096), ("mlp", 4096), ("down", 14336)):
+        X = torch.empty((N, T, C), dtype=torch.float16, device=dev)
+        for i in range(N):
+            X[i] = torch.randn((T, C), generator=gen, device=dev, dtype=torch.float32).half()
+        X[:, :, torch.randperm(C, generator=gen, device=dev)[: cfg["outliers"]]] *= 20
+        xs[key] = X
+    mods = {}
+    for name, R, C, key in LAYER8B:
+        W = (torch.randn((R, C), generator=gen, device=dev) * 0.02).half()
+        s = torch.exp(torch.randn((N, T, G), generator=gen, device=dev))
+        for g in range(G):
+            s[..., g].clamp_(max=float(torch.quantile(s[..., g].flatten(), 0.99)))
+        grad = torch.randn((R, C), generator=gen, device=dev) * 1e-4
+        mods[name] = (W, s, grad, key)
+    return xs, mods
+
+
+def one_layer(xs, mods, cfg, layers, timer=None):
+    """Hessians of all 7 linears (shared inputs fused) + finalize + fasterquant of each."""
+    from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer, add_batch_shared
+    objs = {}
+    for name, (W, s, grad, key) in mods.items():
+        layers[name].weight.data.copy_(W)
+        g = GPTQPlus(layers[name], saliency=s, gradient=grad, num_groups=cfg["G"], alpha=cfg["alpha"],
+                     reference_loss=0.0)
+        g.quantizer = WeightQuantizer()
+        g.quantizer.configure(cfg["bits"], perchannel=True, sym=cfg["sym"], mse=False)
+        objs[name] = g
+    for key in ("attn", "o", "mlp", "down"):
+        group = [objs[n] for n, _, _, k in LAYER8B if k == key]
+        for j in range(0, cfg["N"], cfg["bsz"]):
+            if timer is not None:
+                timer.start()
+            add_batch_shared(group, xs[key][j:j + cfg["bsz"]])
+            if timer is not None:
+                timer.stop()
+    for g in objs.values():
+        g.finalize_hessian()
+    for g in objs.values():
+        g.fasterquant(blocksize=cfg["blocksize"], percdamp=cfg["percdamp"], groupsize=-1, actorder=True,
+                      static_groups=True)
+        g.free()
+    return objs
+
+
+def layer_hessian_flops(cfg):
+    ntok = cfg["N"] * cfg["T"]
+    return sum(cfg["G"] * ntok * C * (C + 1) for _, _, C, _ in LAYER8B)
+
+
+def cpu_baseline_layer(xs, mods, cfg):
+    """CPU oracle for configs[2]: per input width, one add_batch chunk is timed and scaled by
+    tokens (x N/bsz); every module's finalize_hessian + fasterquant is timed in full."""
+    from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
+    nchunks = cfg["N"] // cfg["bsz"]
+    total, parts = 0.0, []
+    for name, R, C, key in LAYER8B:
+        W, s, grad, _ = mods[name]
+        o = GPTQPlusOracle(W.cpu(), s.cpu(), grad.cpu(), cfg["G"], cfg["alpha"], 0.0)
+        o.quantizer = make_quantizer(cfg["bits"], cfg["sym"])
+        xc = xs[key][: cfg["bsz"]].cpu()
+        t0 = time.perf_counter()
+        o.add_batch(xc)
+        t_acc = time.perf_counter() - t0
+        o.index, o.token_count = cfg["N"], cfg["N"] * cfg["T"]
+        t1 = time.perf_counter()
+        o.finalize_hessian()
+        o.fasterquant(blocksize=cfg["blocksize"], percdamp=cfg["percdamp"], groupsize=-1, actorder=True,
+                      static_groups=True)
+        t_fq = time.perf_counter() - t1
+        total += t_acc * nchunks + t_fq
+        parts.append(f"{name}: 1/{nchunks} chunk {t_acc:.1f}s, fasterquant {t_fq:.1f}s")
+        print(f"cpu baseline {name}: add_batch chunk {t_acc:.1f} s, finalize+fasterquant {t_fq:.1f} s",
+              flush=True)
+    return dict(value=round(total * 1e3 / len(LAYER8B), 1), unit="ms per linear (layer / 7, extrapolated)",
+                cores=torch.get_num_threads(), kind="port",
+                sample="oracle on host CPU; " + "; ".join(parts) + f"; layer {total:.1f} s")
+
+
+def run_layer(args, dev):
+    cfg = dict(CFG)
+    xs, mods = make_layer_inputs(dev, cfg)
+    layers = {n: torch.nn.Linear(C, R, bias=False).to(dev, torch.float16) for n, R, C, _ in LAYER8B}
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        one_layer(xs, mods, cfg, layers)
+    timer = EventTimer()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_layer(xs, mods, cfg, layers, timer)
+    torch.cuda.synchronize()
+    layer_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    h_ms_mean, n_launch = timer.mean_ms()
+    h_ms_layer = h_ms_mean * n_launch / args.steps
+    achieved = layer_hessian_flops(cfg) / (h_ms_layer * 1e-3) / 1e12
+    line = {
+        "metric": "ms per linear (H-accum + fasterquant) at Llama-8B shapes; % fp32-MFMA peak",
+        "value": round(layer_ms / len(LAYER8B), 2), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(layer_ms, 2), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32 (fp16 inputs)",
+        "data": "synthetic (seeded, generated on the GPU)",
+        "config": {"workload": "configs[2]: Llama-3-8B decoder layer, 7 linears (q/k/v and gate/up Hessians "
+                               "fused over their shared input), NUM_GROUPS=4, 128x2048 tokens, w4 asym "
+                               "per-channel, act_order, B=128; value = layer time / 7, ms_per_step = layer",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "k_hessian_accum (all launches of the layer)",
+                     "hessian_ms_per_layer": round(h_ms_layer, 2), "launches_per_layer": n_launch // args.steps,
+                     "flops_per_layer": layer_hessian_flops(cfg)},
+    }
+    if args.cpu_baseline_layer:
+        line["cpu_baseline"] = cpu_baseline_layer(xs, mods, cfg)
+    print(json.dumps(line), flush=True)
+
+
 def one_linear(X, W, s, grad, cfg, layer, timer=None):
     from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
     layer.weight.data.copy_(W)
@@ -147,6 +275,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-chunks", type=int, default=2)
+    ap.add_argument("--config", choices=["cfg2", "cfg3"], default="cfg2",
+                    help="cfg2: one q_proj linear (default); cfg3: a full Llama-3-8B layer")
+    ap.add_argument("--cpu-baseline-layer", action="store_true",
+                    help="with --config cfg3: also time the CPU oracle on the layer (minutes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration for the traffic figure)")
     args = ap.parse_args()
@@ -158,6 +290,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.copy_calibration:
         copy_calibration(dev)
+        return
+    if args.config == "cfg3":
+        run_layer(args, dev)
         return
     torch.backends.cuda.matmul.allow_tf32 = False
     cfg = dict(CFG)

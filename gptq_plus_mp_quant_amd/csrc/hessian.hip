@@ -103,7 +103,7 @@ __device__ __forceinline__ void upper_tile(int t, int nt, int& ti, int& tj) {
 template <typename TX, bool EDGE>
 __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t ntok, int64_t ldx,
                                              int C, const float* __restrict__ sal, int64_t ld_sal,
-                                             int g, float* __restrict__ Hg,
+                                             float* __restrict__ Hg,
                                              float* __restrict__ act_sq, int I0, int J0, bool diag,
                                              bool want_act, float (*As)[HS], float (*Bs)[HS]) {
   const int tid = threadIdx.x;
@@ -134,7 +134,7 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
 
   for (int64_t sidx = 0; sidx < nslab; ++sidx) {
     const int64_t t = sidx * HKC + sk;
-    const float s = (t < ntok) ? sal[t * ld_sal + g] : 0.0f;
+    const float s = (t < ntok) ? sal[t * ld_sal] : 0.0f;
     __syncthreads();                  // previous slab fully consumed
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -205,34 +205,47 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
   }
 }
 
+// One output of a launch: the Hessian of one (module, saliency group) pair.  Modules that
+// read the same input (q/k/v, gate/up) are accumulated by one launch, so each X strip is
+// fetched once for all of them.
+constexpr int HMAXT = 32;
+struct HTargets {
+  const float* sal[HMAXT];   // saliency column of this target: sal[t * ld_sal]
+  int64_t ld_sal[HMAXT];
+  float* H[HMAXT];           // C x C output
+  float* act[HMAXT];         // act_square output (one target per module) or nullptr
+};
+
 template <typename TX>
 __global__ __launch_bounds__(HTHREADS, 3) void k_hessian_accum(
-    const TX* __restrict__ X, int64_t ntok, int64_t ldx, int C, const float* __restrict__ sal,
-    int64_t ld_sal, int G, float* __restrict__ H, float* __restrict__ act_sq, int nt, int ntiles,
-    bool vec_ok) {
+    const TX* __restrict__ X, int64_t ntok, int64_t ldx, int C, HTargets tg, int ntarg, int nt,
+    int ntiles, bool vec_ok) {
   __shared__ __attribute__((aligned(16))) float As[HT][HS];
   __shared__ __attribute__((aligned(16))) float Bs[HT][HS];
 
   // XCD-aware order: consecutive hardware workgroup ids land on different XCDs (round
   // robin over 8); give each XCD a contiguous run of logical ids so neighbouring tiles,
-  // which share X column strips, share that XCD's L2.
-  const int total = ntiles * G;
+  // which share X column strips, share that XCD's L2.  Targets of one tile are adjacent.
+  const int total = ntiles * ntarg;
   const int b = blockIdx.x;
   const int per = total / 8, rem8 = total % 8;
   const int xcd = b % 8, idx = b / 8;
   const int logical = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
-  const int g = logical % G;
+  const int g = logical % ntarg;
   int ti, tj;
-  upper_tile_blocked(logical / G, nt, ti, tj);
+  upper_tile_blocked(logical / ntarg, nt, ti, tj);
   const int I0 = ti * HT, J0 = tj * HT;
   const bool diag = (ti == tj);
-  const bool want_act = diag && (g == 0) && (act_sq != nullptr);
-  float* Hg = H + (int64_t)g * C * C;
+  float* act_sq = tg.act[g];
+  const bool want_act = diag && (act_sq != nullptr);
+  float* Hg = tg.H[g];
   const bool interior = vec_ok && (J0 + HT <= C);   // I0 <= J0
   if (interior)
-    hessian_tile<TX, false>(X, ntok, ldx, C, sal, ld_sal, g, Hg, act_sq, I0, J0, diag, want_act, As, Bs);
+    hessian_tile<TX, false>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], Hg, act_sq, I0, J0, diag,
+                            want_act, As, Bs);
   else
-    hessian_tile<TX, true>(X, ntok, ldx, C, sal, ld_sal, g, Hg, act_sq, I0, J0, diag, want_act, As, Bs);
+    hessian_tile<TX, true>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], Hg, act_sq, I0, J0, diag,
+                           want_act, As, Bs);
 }
 
 }  // namespace
@@ -296,32 +309,71 @@ __global__ void k_scale_vec(float* __restrict__ v, int n, float div) {
 
 extern "C" int rq_version(void) { return 100; }
 
+namespace {
+
+int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, const HTargets& tg,
+                   int ntarg, hipStream_t s) {
+  const int nt = (C + HT - 1) / HT;
+  const int ntiles = nt * (nt + 1) / 2;
+  const int64_t total = (int64_t)ntiles * ntarg;
+  if (total > 0x7fffffff) return RQ_EINVAL;
+  const size_t esz = (x_dtype == RQ_F32) ? 4 : 2;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (((size_t)ldx * esz) % 16 == 0);
+  dim3 grid((unsigned)total), block(HTHREADS);
+  if (x_dtype == RQ_F16)
+    hipLaunchKernelGGL(k_hessian_accum<__half>, grid, block, 0, s, (const __half*)x, ntok, ldx, C, tg,
+                       ntarg, nt, ntiles, vec_ok);
+  else if (x_dtype == RQ_BF16)
+    hipLaunchKernelGGL(k_hessian_accum<__hip_bfloat16>, grid, block, 0, s, (const __hip_bfloat16*)x,
+                       ntok, ldx, C, tg, ntarg, nt, ntiles, vec_ok);
+  else
+    hipLaunchKernelGGL(k_hessian_accum<float>, grid, block, 0, s, (const float*)x, ntok, ldx, C, tg,
+                       ntarg, nt, ntiles, vec_ok);
+  RQ_CHECK_LAUNCH();
+  return RQ_OK;
+}
+
+}  // namespace
+
 extern "C" int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
                                 const float* sal, int64_t ld_sal, int G, float* H, float* act_sq,
                                 void* stream) {
   if (!x || !sal || !H || C <= 0 || G <= 0 || ntok < 0 || ldx < C || ld_sal < G) return RQ_EINVAL;
   if (x_dtype != RQ_F16 && x_dtype != RQ_BF16 && x_dtype != RQ_F32) return RQ_EINVAL;
   if (ntok == 0) return RQ_OK;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int nt = (C + HT - 1) / HT;
-  const int ntiles = nt * (nt + 1) / 2;
-  const int64_t total = (int64_t)ntiles * G;
-  if (total > 0x7fffffff) return RQ_EINVAL;
-  const size_t esz = (x_dtype == RQ_F32) ? 4 : 2;
-  const bool vec_ok = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (((size_t)ldx * esz) % 16 == 0);
-  dim3 grid((unsigned)total), block(HTHREADS);
-  if (x_dtype == RQ_F16)
-    hipLaunchKernelGGL(k_hessian_accum<__half>, grid, block, 0, s, (const __half*)x, ntok, ldx, C,
-                       sal, ld_sal, G, H, act_sq, nt, ntiles, vec_ok);
-  else if (x_dtype == RQ_BF16)
-    hipLaunchKernelGGL(k_hessian_accum<__hip_bfloat16>, grid, block, 0, s,
-                       (const __hip_bfloat16*)x, ntok, ldx, C, sal, ld_sal, G, H, act_sq, nt,
-                       ntiles, vec_ok);
-  else
-    hipLaunchKernelGGL(k_hessian_accum<float>, grid, block, 0, s, (const float*)x, ntok, ldx, C,
-                       sal, ld_sal, G, H, act_sq, nt, ntiles, vec_ok);
-  RQ_CHECK_LAUNCH();
+  for (int g0 = 0; g0 < G; g0 += HMAXT) {     // up to 32 groups per launch
+    const int n = (G - g0 < HMAXT) ? (G - g0) : HMAXT;
+    HTargets tg{};
+    for (int t = 0; t < n; ++t) {
+      const int g = g0 + t;
+      tg.sal[t] = sal + g;
+      tg.ld_sal[t] = ld_sal;
+      tg.H[t] = H + (int64_t)g * C * C;
+      tg.act[t] = (g == 0) ? act_sq : nullptr;
+    }
+    const int rc = launch_hessian(x, x_dtype, ntok, ldx, C, tg, n, reinterpret_cast<hipStream_t>(stream));
+    if (rc) return rc;
+  }
   return RQ_OK;
+}
+
+extern "C" int rq_hessian_accum_multi(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
+                                      int ntargets, const float* const* sal, const int64_t* ld_sal,
+                                      float* const* H, float* const* act_sq, void* stream) {
+  if (!x || !sal || !ld_sal || !H || C <= 0 || ntargets <= 0 || ntargets > HMAXT || ntok < 0 ||
+      ldx < C)
+    return RQ_EINVAL;
+  if (x_dtype != RQ_F16 && x_dtype != RQ_BF16 && x_dtype != RQ_F32) return RQ_EINVAL;
+  HTargets tg{};
+  for (int t = 0; t < ntargets; ++t) {
+    if (!sal[t] || !H[t] || ld_sal[t] < 1) return RQ_EINVAL;
+    tg.sal[t] = sal[t];
+    tg.ld_sal[t] = ld_sal[t];
+    tg.H[t] = H[t];
+    tg.act[t] = act_sq ? act_sq[t] : nullptr;
+  }
+  if (ntok == 0) return RQ_OK;
+  return launch_hessian(x, x_dtype, ntok, ldx, C, tg, ntargets, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int rq_hessian_finalize(float* H, float* act_sq, int G, int C, double h_div,

@@ -76,23 +76,31 @@ class GPTQPlus:
                 inp = inp.unsqueeze(0)
             else:
                 assert inp.dim() == 3, "Input must be 2D or 3D. Got %dD." % inp.dim()
-            nat.require_gpu(inp, "add_batch input")
-            bsz = inp.shape[0]
-            sal = self.saliencies[self.index:self.index + bsz]
-            self.index += bsz
-            if sal.dim() == 3 and inp.shape[1] > sal.shape[1]:
-                inp = inp[:, inp.shape[1] - sal.shape[1]:]
-            x = inp.reshape(-1, inp.shape[-1])
-            if x.stride(1) != 1 or x.stride(0) < x.shape[1]:
-                x = x.contiguous()
-            if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-                x = x.float()
-            s = sal.reshape(-1, sal.shape[-1]).to(self.dev, torch.float32).contiguous()
-            n_tokens = x.shape[0]
-            if s.shape[0] != n_tokens:
-                raise ValueError(f"saliency rows ({s.shape[0]}) do not match tokens ({n_tokens})")
+            x, s = self._take_saliency(inp)
             K.hessian_accum(x, s, self.H, self.act_square)
-            self.token_count += n_tokens
+            self.token_count += x.shape[0]
+
+    def _take_saliency(self, inp):
+        """Advance the sample cursor like add_batch and return (x [n, C], sal [n, G])."""
+        if self._finalized:
+            raise RuntimeError("add_batch called after finalize_hessian. Re-init GPTQPlus to reuse.")
+        if inp.dim() == 2:
+            inp = inp.unsqueeze(0)
+        nat.require_gpu(inp, "add_batch input")
+        bsz = inp.shape[0]
+        sal = self.saliencies[self.index:self.index + bsz]
+        self.index += bsz
+        if sal.dim() == 3 and inp.shape[1] > sal.shape[1]:
+            inp = inp[:, inp.shape[1] - sal.shape[1]:]
+        x = inp.reshape(-1, inp.shape[-1])
+        if x.stride(1) != 1 or x.stride(0) < x.shape[1]:
+            x = x.contiguous()
+        if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            x = x.float()
+        s = sal.reshape(-1, sal.shape[-1]).to(self.dev, torch.float32).contiguous()
+        if s.shape[0] != x.shape[0]:
+            raise ValueError(f"saliency rows ({s.shape[0]}) do not match tokens ({x.shape[0]})")
+        return x, s
 
     # gptq_plus_utils.py:859-908 (single GPU: the all-reduces are identities)
     @torch.no_grad()
@@ -387,3 +395,41 @@ class GPTQPlus:
         self._codes_perm = None
         self.Hinv_all = None
         torch.cuda.empty_cache()
+
+
+@torch.no_grad()
+def add_batch_shared(gptqs, inp, out=None):
+    """``add_batch(inp, out)`` for several GPTQPlus objects whose modules receive the same input
+    (q/k/v, or gate/up: their forward hooks in gptq_plus_utils.py:6991-7003 see one tensor).
+
+    Each object advances its own saliency cursor and accumulates its own H / act_square exactly
+    as its own add_batch would (same kernel, same tile order, so the result is bitwise the
+    same), but X is streamed once for all of them: one launch for up to 32 (module, group)
+    Hessians.
+    """
+    gptqs = list(gptqs)
+    if not gptqs:
+        return
+    C = gptqs[0].columns
+    if any(g.columns != C or g.dev != gptqs[0].dev for g in gptqs):
+        raise ValueError("add_batch_shared: all modules must share in_features and device")
+    parts = [g._take_saliency(inp) for g in gptqs]
+    x0 = parts[0][0]
+    batch, used = [], 0
+    for g, (x, s) in zip(gptqs, parts):
+        if x.shape != x0.shape:
+            raise ValueError("add_batch_shared: the modules' saliencies keep different token counts")
+        if g.num_groups > 32:                  # its own launch(es)
+            K.hessian_accum(x0, s, g.H, g.act_square)
+            continue
+        if batch and used + g.num_groups > 32:
+            K.hessian_accum_multi(x0, [b[1] for b in batch], [b[0].H for b in batch],
+                                  [b[0].act_square for b in batch])
+            batch, used = [], 0
+        batch.append((g, s))
+        used += g.num_groups
+    if batch:
+        K.hessian_accum_multi(x0, [b[1] for b in batch], [b[0].H for b in batch],
+                              [b[0].act_square for b in batch])
+    for g in gptqs:
+        g.token_count += x0.shape[0]

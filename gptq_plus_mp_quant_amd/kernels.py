@@ -59,6 +59,30 @@ def hessian_accum(x, sal, H, act_sq):
              nat.ptr(sal), sal.stride(0), G, nat.ptr(H), nat.ptr(act_sq), _stream(x))
 
 
+def hessian_accum_multi(x, sals, Hs, acts):
+    """One launch for several (module, group) targets sharing x [n, C]: for module m,
+    Hs[m][g] += x^T diag(sals[m][:, g]) x and acts[m] += sum x^2 (acts[m] may be None)."""
+    _rowmajor(x, "x")
+    n, C = x.shape
+    sal_p, ld, H_p, act_p = [], [], [], []
+    for sal, H, act in zip(sals, Hs, acts):
+        _rowmajor(sal, "sal")
+        G = H.shape[0]
+        if sal.shape != (n, G) or sal.dtype != _f32 or H.shape != (G, C, C) or not H.is_contiguous():
+            raise ValueError("hessian_accum_multi: shape mismatch")
+        for g in range(G):
+            sal_p.append(sal.data_ptr() + 4 * g)
+            ld.append(sal.stride(0))
+            H_p.append(H[g].data_ptr())
+            act_p.append(act.data_ptr() if (act is not None and g == 0) else 0)
+    if len(H_p) > 32:
+        raise ValueError("hessian_accum_multi: at most 32 (module, group) targets per launch")
+    nt = len(H_p)
+    P = ctypes.c_void_p
+    nat.call("rq_hessian_accum_multi", nat.ptr(x), nat.dtype_code(x.dtype), n, x.stride(0), C, nt,
+             (P * nt)(*sal_p), (ctypes.c_int64 * nt)(*ld), (P * nt)(*H_p), (P * nt)(*act_p), _stream(x))
+
+
 def hessian_finalize(H, act_sq, h_div, sal_scale, seq_len, nonfinite=None):
     G, C, _ = H.shape
     nat.call("rq_hessian_finalize", nat.ptr(H), nat.ptr(act_sq), G, C, float(h_div), float(sal_scale),

@@ -44,6 +44,16 @@ int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int 
                      const float* sal, int64_t ld_sal, int G, float* H, float* act_sq,
                      void* stream);
 
+/* Cross-module fused accumulation: the add_batch of several GPTQPlus objects whose modules read
+ * the same input (q/k/v, gate/up; their forward hooks receive the same tensor,
+ * gptq_plus_utils.py:6991-7003) in one launch, so X is streamed once for all of them.
+ * Target t (< 32) accumulates H[t] (C x C) += X^T diag(s_t) X with s_t = sal[t][i * ld_sal[t]],
+ * and act_sq[t] (when act_sq and act_sq[t] are non-NULL) += sum_t x^2.  sal, ld_sal, H and
+ * act_sq are HOST arrays of device pointers / strides. */
+int rq_hessian_accum_multi(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
+                           int ntargets, const float* const* sal, const int64_t* ld_sal,
+                           float* const* H, float* const* act_sq, void* stream);
+
 /* GPTQPlus.finalize_hessian -- gptq_plus_utils.py:859-908 (world size 1).
  * H = sym(upper(H)) / h_div [/ sal_scale if != 1]; non-finite entries -> 0 and counted
  * into *nonfinite (device int, accumulated); act_sq /= seq_len. */

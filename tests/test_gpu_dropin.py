@@ -178,6 +178,32 @@ def test_dropin_vs_oracle(cfg):
     assert abs(e_gpu - e_ref) <= 0.005 * e_ref
 
 
+@pytest.mark.parametrize("groups", [(4, 4, 4), (12, 12, 12), (48, 1, 2)])
+def test_add_batch_shared_equals_separate(groups):
+    """q/k/v-style modules fed one input: the fused launch gives bitwise the add_batch results
+    (more than 32 (module, group) targets are split over launches)."""
+    from gptq_plus_mp_quant_amd import add_batch_shared
+    C, N, T = 256, 4, 64
+    X, _, _, _ = synth(31, 8, C, 1, N, T)
+    objs_sep, objs_fused = [], []
+    for m, (R, G) in enumerate(zip((96, 48, 48), groups)):
+        _, W, s, grad = synth(40 + m, R, C, G, N, T)
+        objs_sep.append(_gpu_obj(W, s, grad, G, 0.0, 0.0, 4, True)[0])
+        objs_fused.append(_gpu_obj(W, s, grad, G, 0.0, 0.0, 4, True)[0])
+    for j in range(0, N, 2):
+        xb = X[j:j + 2].to(DEV)
+        for g in objs_sep:
+            g.add_batch(xb)
+        add_batch_shared(objs_fused, xb)
+    for a, b in zip(objs_sep, objs_fused):
+        torch.cuda.synchronize()
+        assert torch.equal(a.H, b.H) and torch.equal(a.act_square, b.act_square)
+        assert (a.index, a.token_count) == (b.index, b.token_count)
+        a.finalize_hessian()
+        b.finalize_hessian()
+        assert torch.equal(a.H, b.H)
+
+
 def test_dropin_errors_and_side_effects():
     X, W, s, grad = synth(1, 64, 128, 2, 2, 64)
     g, layer = _gpu_obj(W, s, grad, 2, 0.0, 0.0, 4, True)
