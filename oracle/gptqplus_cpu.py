@@ -13,7 +13,8 @@ It restates, op for op and in the same torch call order on CPU tensors, the refe
 * ``GPTQPlus.__init__ / add_batch / finalize_hessian`` -- ``gptq_plus_utils.py:431-487, 798-908``
 * ``GPTQPlus._compute_hessian_inverse_with_fallback`` -- ``gptq_plus_utils.py:494-561``
 * ``GPTQPlus._compute_gradient_terms`` -- ``gptq_plus_utils.py:563-578``
-* ``GPTQPlus.fasterquant`` in the default ``g_update_mode="frozen"``: find_params,
+* ``GPTQPlus.fasterquant`` for ``g_update_mode`` in {frozen (default), surrogate_block,
+  surrogate_online} (``_current_ghinv`` :580-584): find_params,
   static / dynamic groups, dead columns, act_order, per-subgroup state, the in-block
   column loop, the block-atomic variant, the trailing (outer) update, un-permute and
   write-back -- ``gptq_plus_utils.py:910-1396, 1500-1570, 1850-1896``.
@@ -208,8 +209,15 @@ def gradient_terms(gradients_sub, Hinv_init, Hinv, alpha, reference_loss, rows, 
     return beta, Z, GHinv, GHinv_init
 
 
+def _current_ghinv(base, current_weight, ref_weight, beta_view, refresh_mode):
+    """gptq_plus_utils.py:580-584."""
+    if refresh_mode == "frozen":
+        return base
+    return base + beta_view * (current_weight - ref_weight)
+
+
 # ---------------------------------------------------------------------------------------
-# GPTQPlus (frozen mode)
+# GPTQPlus (frozen and surrogate modes)
 # ---------------------------------------------------------------------------------------
 @dataclass
 class SubgroupRecord:
@@ -312,8 +320,13 @@ class GPTQPlusOracle:
     def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
                     static_groups=False, enable_gradient_update=True, g_update_mode="frozen",
                     block_atomic_quant=False, stable_ties=False) -> FasterquantResult:
-        if g_update_mode != "frozen":
-            raise NotImplementedError("oracle covers g_update_mode='frozen' only")
+        # frozen and the two surrogate modes (no layer backward); gptq_plus_utils.py:1190-1199,
+        # 1360-1367 (inner) and 1500-1511 (outer)
+        if g_update_mode not in ("frozen", "surrogate_block", "surrogate_online"):
+            raise NotImplementedError("oracle covers g_update_mode in {frozen, surrogate_block, surrogate_online}")
+        inner_mode = g_update_mode
+        online = inner_mode == "surrogate_online"
+        outer_mode = "frozen" if g_update_mode == "frozen" else "surrogate_block"
         dt = self.dtype
         W = self.weight.clone().to(dt)
         quantizer = self.quantizer
@@ -367,6 +380,7 @@ class GPTQPlusOracle:
             records.append(SubgroupRecord(r0, r1, perm, invperm, Hinv_init, Hinv, damp, fallback,
                                           attempts, beta, Z.clone(), GHinv.clone(), W_sub.clone()))
             states.append(dict(r0=r0, r1=r1, W_sub=W_sub, Hinv=Hinv, Z=Z, GHinv=GHinv, perm=perm,
+                               anchor=W_sub.clone(), beta_view=beta.unsqueeze(1),
                                invperm=invperm, Q=torch.zeros_like(W_sub),
                                W_int=torch.zeros_like(W_sub), Scale=torch.zeros_like(W_sub),
                                fast_scale=fast_scale_full[r0:r1] if fast else None))
@@ -387,6 +401,9 @@ class GPTQPlusOracle:
                 Hinv1 = st["Hinv"][i1:i2, i1:i2]
                 GHinv1 = st["GHinv"][:, i1:i2].clone()
                 Z1 = st["Z"][:, i1:i2]
+                W_ref1 = st["anchor"][:, i1:i2]
+                GHinv1_eff = _current_ghinv(GHinv1, W1 if online else W_block_start, W_ref1,
+                                            st["beta_view"], inner_mode)
                 dyn_q = None
                 if dynamic_groups:                                     # :1202-1209
                     dyn_q = copy.deepcopy(quantizer)
@@ -417,7 +434,7 @@ class GPTQPlusOracle:
                             Q1[:, i] = q.flatten()
                             W_int1[:, i] = iw.flatten()
                             Scale1[:, i] = sc.flatten()
-                    residual = W_block_start - Q1 - GHinv1
+                    residual = W_block_start - Q1 - GHinv1_eff
                     Err1.copy_(torch.linalg.solve_triangular(Hinv1.T, residual.T, upper=False).T)
                 else:                                                  # :1296-1367
                     for i in range(count):
@@ -437,18 +454,22 @@ class GPTQPlusOracle:
                         W_int1[:, i] = iw.flatten()
                         if st["fast_scale"] is None:
                             Scale1[:, i] = sc.flatten()
-                        err1 = (w - q - GHinv1[:, i]) / d
+                        err1 = (w - q - GHinv1_eff[:, i]) / d
                         upd = err1.unsqueeze(1).matmul(Hinv1[i, i:].unsqueeze(0))
-                        W1[:, i:] -= upd + GHinv1[:, i:]
+                        W1[:, i:] -= upd + GHinv1_eff[:, i:]
                         Err1[:, i] = err1
                         GHinv1[:, i:].sub_(Z1[:, i].unsqueeze(1).matmul(Hinv1[i, i:].unsqueeze(0)))
+                        if inner_mode != "frozen":
+                            GHinv1_eff = _current_ghinv(GHinv1, W1 if online else W_block_start, W_ref1,
+                                                        st["beta_view"], inner_mode)
                 st["Q"][:, i1:i2] = Q1
                 st["W_int"][:, i1:i2] = W_int1
                 st["Scale"][:, i1:i2] = Scale1
                 block_states.append((st, Err1, Z1))
 
-            for st, Err1, Z1 in block_states:                          # :1500-1570 (frozen)
-                GHinv_rest = st["GHinv"][:, i2:]
+            for st, Err1, Z1 in block_states:                          # :1500-1570
+                GHinv_rest = _current_ghinv(st["GHinv"][:, i2:], st["W_sub"][:, i2:], st["anchor"][:, i2:],
+                                            st["beta_view"], outer_mode)
                 G_Update = count * GHinv_rest - torch.einsum("ij,j,jk->ik", Z1, D, st["Hinv"][i1:i2, i2:])
                 second = Err1.matmul(st["Hinv"][i1:i2, i2:])
                 st["W_sub"][:, i2:] -= second + G_Update
@@ -483,7 +504,7 @@ def make_quantizer(bits, sym=True, mse=False) -> WeightQuantizerOracle:
 def run_linear(weight, X, saliency, gradient, num_groups, bits=4, sym=True, alpha=0.0,
                reference_loss=0.0, accum_bsz=16, blocksize=128, percdamp=0.01, groupsize=-1,
                actorder=True, static_groups=None, block_atomic_quant=False, stable_ties=False,
-               dtype=torch.float32):
+               g_update_mode="frozen", dtype=torch.float32):
     """Drive one linear like ``build_gptq_for_subset`` + ``accumulate_hessian_for_gptq`` +
     ``fasterquant`` (gptq_plus_utils.py:6954-7039, 7467-7502).  X is (N, T, C)."""
     if static_groups is None:
@@ -495,7 +516,7 @@ def run_linear(weight, X, saliency, gradient, num_groups, bits=4, sym=True, alph
     g.finalize_hessian()
     res = g.fasterquant(blocksize=blocksize, percdamp=percdamp, groupsize=groupsize, actorder=actorder,
                         static_groups=static_groups, block_atomic_quant=block_atomic_quant,
-                        stable_ties=stable_ties)
+                        stable_ties=stable_ties, g_update_mode=g_update_mode)
     return g, res
 
 

@@ -45,6 +45,9 @@ CASES = [
     dict(name="g2_sym4_mse_perchan_act", R=32, C=64, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=False, alpha=0.0, ref_loss=0.0, mse=True),
     dict(name="g2_asym3_mse_static_groups", R=32, C=64, G=2, N=8, T=16, bits=3, sym=False, gs=16, act=True, B=16, atomic=False, alpha=0.0, ref_loss=0.0, mse=True),
     dict(name="g1_sym4_mse_dynamic_atomic", R=32, C=48, G=1, N=8, T=16, bits=4, sym=True, gs=16, act=False, B=16, atomic=True, alpha=0.0, ref_loss=0.0, mse=True),
+    dict(name="g2_sym4_surrogate_block_gplus", R=32, C=64, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=False, alpha=0.05, ref_loss=1e6, gscale=1.0, mode="surrogate_block"),
+    dict(name="g2_asym4_surrogate_online_gplus", R=32, C=64, G=2, N=8, T=16, bits=4, sym=False, gs=16, act=True, B=16, atomic=False, alpha=0.05, ref_loss=1e6, gscale=1.0, mode="surrogate_online"),
+    dict(name="g2_sym4_surrogate_online_atomic", R=32, C=48, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=True, alpha=0.05, ref_loss=1e6, gscale=1.0, mode="surrogate_online"),
 ]
 
 
@@ -122,7 +125,8 @@ def run_case(gpu, qu, case, seed):
     act = g.act_square.clone()
     cap = _Capture()
     g.fasterquant(blocksize=case["B"], percdamp=0.01, groupsize=case["gs"], actorder=case["act"],
-                  static_groups=case["act"], enable_gradient_update=True, g_update_mode="frozen",
+                  static_groups=case["act"], enable_gradient_update=True,
+                  g_update_mode=case.get("mode", "frozen"),
                   export_to_et=True, block_atomic_quant=case["atomic"], diagnostic_recorder=cap)
     out = {
         "X": X, "W": W, "s": s, "grad": grad,

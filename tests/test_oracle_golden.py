@@ -27,7 +27,8 @@ def _run(case, inject_H=False):
         g.H = case.H().clone()
         g.act_square = case.t("act_square").clone()
     res = g.fasterquant(blocksize=m["B"], percdamp=0.01, groupsize=m["gs"], actorder=m["act"],
-                        static_groups=m["act"], block_atomic_quant=m["atomic"])
+                        static_groups=m["act"], block_atomic_quant=m["atomic"],
+                        g_update_mode=m.get("mode", "frozen"))
     return g, res
 
 
@@ -70,6 +71,7 @@ def test_golden_cover_the_branches():
     assert any(not m["sym"] for m in metas)                                         # asym quirk
     assert any(m["C"] % m["B"] for m in metas)                                      # ragged last block
     assert sum(bool(m.get("mse")) for m in metas) >= 3                              # clip search
+    assert {m.get("mode") for m in metas} >= {"surrogate_block", "surrogate_online"}
     assert "g1_sym4_indefinite_identity" in names
     ident = GoldenSet.load().by_name("g1_sym4_indefinite_identity")
     assert bool(ident.arrays["sub0_identity_fallback"])
