@@ -17,6 +17,9 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "gptqplus_hip.h"
 RQ_OK, RQ_EINVAL, RQ_EHIP, RQ_ENOTSUP = 0, -1, -2, -3
 RQ_F16, RQ_BF16, RQ_F32 = 0, 1, 2
 RQ_QMODE_CHANNEL, RQ_QMODE_STATIC, RQ_QMODE_DYNAMIC = 0, 1, 2
+RQ_GMODE_FROZEN, RQ_GMODE_SURROGATE_BLOCK, RQ_GMODE_SURROGATE_ONLINE = 0, 1, 2
+GMODES = {"frozen": RQ_GMODE_FROZEN, "surrogate_block": RQ_GMODE_SURROGATE_BLOCK,
+          "surrogate_online": RQ_GMODE_SURROGATE_ONLINE}
 
 _P, _I, _L, _D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_double
 
@@ -34,8 +37,9 @@ SIGNATURES = {
     "rq_chol_hinv_attempt": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
     "rq_gptqplus_terms": (_I, [_P, _L, _P, _P, _I, _I, _D, _D, _I, _P, _P, _P, _L, _P, _P, _P]),
     "rq_quant_block": (_I, [_P, _L, _P, _I, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I,
-                            _I, _P, _P, _P, _P]),
-    "rq_trailing_update": (_I, [_P, _L, _P, _P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
+                            _I, _P, _P, _P, _I, _P, _L, _P, _P]),
+    "rq_trailing_update": (_I, [_P, _L, _P, _P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _L, _P,
+                                _P]),
     "rq_writeback": (_I, [_P, _I, _I, _P, _I, _P, _P, _P, _I, _P, _I, _L, _P, _P, _P, _P]),
 }
 

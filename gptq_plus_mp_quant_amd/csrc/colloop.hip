@@ -1,5 +1,6 @@
 // The fasterquant block loop (gptq_utils/gptq_plus_utils.py:1169-1372) and the trailing
-// (outer) update (:1500-1570), frozen mode, all subgroups in one launch each.
+// (outer) update (:1500-1570), all subgroups in one launch each, for the frozen and the two
+// surrogate g_update modes.
 //
 // k_quant_block: rows are independent, so each row of the block is owned by a quad of 4
 // lanes; lane t of the quad holds columns t, t+4, t+8, ... of the row in registers (W1, GHinv1,
@@ -16,9 +17,17 @@
 // The atomic variant (:1238-1288) quantises the block start at once and solves
 // Err * Hinv1 = W - Q - GHinv1 by forward substitution with the same quad layout.
 //
+// Surrogate modes (:580-584, :1190-1199, :1360-1367): the first-order term used in place of
+// gh is gh_eff = gh + beta_row * (W_cur - W_anchor), re-evaluated before every column, where
+// W_anchor is the permuted weight before the first block, W_cur the live W1 (surrogate_online)
+// or the block start (surrogate_block).  A fifth register array per row holds the anchor
+// (online) or the constant difference W_block_start - W_anchor (block).
+//
 // k_trailing: W[:, i2:] -= Err Hinv[i1:i2, i2:] + (count GH[:, i2:] - (Z1 D) Hinv[i1:i2, i2:])
 // and GH[:, i2:] -= Z1 Hinv[i1:i2, i2:], 64x64 output tiles, fp32 16x16x4 MFMA, K = count
 // streamed through LDS in slabs of 32.  The Z terms are skipped when Z is identically zero.
+// In the surrogate modes the GH[:, i2:] of the first term is GH + beta_row * (W - W_anchor)
+// (outer refresh "surrogate_block", :1500-1511), the GH update itself is unchanged.
 #include "rq_common.h"
 
 namespace {
@@ -55,9 +64,13 @@ struct QBArgs {
   const int* z_nonzero;
   int16_t* codes;
   float* err;
+  const float* anchor;
+  int64_t lda;
+  const float* beta;
 };
 
-template <int SLOTS>
+// GM: 0 frozen, 1 surrogate_block, 2 surrogate_online
+template <int SLOTS, int GM>
 __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
   __shared__ float Hl[QB_MAXB][QB_MAXB];
   const int tid = threadIdx.x;
@@ -75,19 +88,30 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
     Hl[i][j] = (i < count && j < count && j >= i) ? Hs[(int64_t)(i1 + i) * a.C + (i1 + j)] : 0.0f;
   }
 
-  float w[SLOTS], gh[SLOTS], zz[SLOTS], sc[SLOTS];
+  float w[SLOTS], gh[SLOTS], zz[SLOTS], sc[SLOTS], xr[GM ? SLOTS : 1];
+  const float brow = GM ? a.beta[row] : 0.0f;
 #pragma unroll
   for (int k = 0; k < SLOTS; ++k) {
     const int col = 4 * k + t;
     const bool in = valid && col < count;
     const int64_t off = (int64_t)row * a.ldw + i1 + col;
     w[k] = in ? a.Wp[off] : 0.0f;
+    if constexpr (GM != 0) {
+      const float wr = in ? a.anchor[(int64_t)row * a.lda + i1 + col] : 0.0f;
+      xr[k] = (GM == 1) ? (w[k] - wr) : wr;
+    }
     const int64_t og = (int64_t)row * a.ldgh + i1 + col;
     gh[k] = (in && use_gh) ? a.GH[og] : 0.0f;
     zz[k] = (in && use_gh) ? a.Z[og] : 0.0f;
     sc[k] = 0.0f;
     if (a.qmode == RQ_QMODE_STATIC && in) sc[k] = a.scale[(int64_t)a.col_group[i1 + col] * a.R + row];
   }
+  // gh_eff of slot k from the current registers: gh + beta * (W_cur - W_anchor)
+  auto geff = [&](int k) -> float {
+    if constexpr (GM == 0) return gh[k];
+    const float dw = (GM == 1) ? xr[k] : (w[k] - xr[k]);
+    return gh[k] + brow * dw;
+  };
   const float lo = -(a.maxq + 1.0f), hi = a.maxq;
   float srow = 0.0f;
   if (a.qmode == RQ_QMODE_CHANNEL) {
@@ -125,7 +149,8 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
       const float code = rq_quant_code(w[k], s, lo, hi);
       const float q = s * code;
       if (valid && col < count) crow[col] = (code != code) ? RQ_CODE_NAN : (int16_t)code;
-      w[k] = (w[k] - q) - gh[k];
+      const float ge = geff(k);
+      w[k] = (w[k] - q) - ge;
     }
     // Err1 * Hinv1 = res, forward substitution (:1283-1288)
     for (int m = 0; m < nmacro; ++m) {
@@ -166,13 +191,25 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
         const float x = w[0];
         const float code = rq_quant_code(x, s, lo, hi);
         const float q = s * code;
-        const float e_own = ((x - q) - gh[0]) / d;
+        const float e_own = ((x - q) - geff(0)) / d;
         const float e = quad_lane(e_own, r);
         if (valid && t == r) {
           crow[i] = (code != code) ? RQ_CODE_NAN : (int16_t)code;
           erow[i] = e;
         }
-        if (use_gh) {
+        if constexpr (GM != 0) {
+          const float zi = use_gh ? quad_lane(zz[0], r) : 0.0f;
+#pragma unroll
+          for (int k = 0; k < SLOTS; ++k) {
+            if (k < nlive) {
+              const float h = Hl[i][4 * (m + k) + t];
+              const float ge = geff(k);
+              const float upd = e * h;
+              w[k] = w[k] - (upd + ge);
+              gh[k] = gh[k] - zi * h;
+            }
+          }
+        } else if (use_gh) {
           const float zi = quad_lane(zz[0], r);
 #pragma unroll
           for (int k = 0; k < SLOTS; ++k) {
@@ -200,11 +237,13 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
       gh[k] = gh[k + 1];
       zz[k] = zz[k + 1];
       sc[k] = sc[k + 1];
+      if constexpr (GM != 0) xr[k] = xr[k + 1];
     }
     w[SLOTS - 1] = 0.0f;
     gh[SLOTS - 1] = 0.0f;
     zz[SLOTS - 1] = 0.0f;
     sc[SLOTS - 1] = 0.0f;
+    if constexpr (GM != 0) xr[SLOTS - 1] = 0.0f;
   }
 }
 
@@ -219,6 +258,10 @@ struct TrArgs {
   int C, R, R_s, i1, count;
   const float* err;
   const int* z_nonzero;
+  int gmode;
+  const float* anchor;
+  int64_t lda;
+  const float* beta;
 };
 
 constexpr int TKS = 32;  // K slab
@@ -301,7 +344,15 @@ __global__ __launch_bounds__(256) void k_trailing(TrArgs a) {
         const int c = c0 + wc * 32 + y * 16 + (lane & 15);
         if (rl < a.R_s && c < a.C) {
           const int64_t ow = (int64_t)(rbase + rl) * a.ldw + c;
-          if (use_z) {
+          if (a.gmode != 0) {
+            const float wv = a.Wp[ow];
+            const float g = use_z ? a.GH[(int64_t)(rbase + rl) * a.ldgh + c] : 0.0f;
+            const float dw = wv - a.anchor[(int64_t)(rbase + rl) * a.lda + c];
+            const float geff = g + a.beta[rbase + rl] * dw;
+            const float gupd = cnt * geff - acc2[x][y][e];
+            a.Wp[ow] = wv - (acc1[x][y][e] + gupd);
+            if (use_z) a.GH[(int64_t)(rbase + rl) * a.ldgh + c] = g - acc3[x][y][e];
+          } else if (use_z) {
             const int64_t og = (int64_t)(rbase + rl) * a.ldgh + c;
             const float g = a.GH[og];
             const float gupd = cnt * g - acc2[x][y][e];
@@ -320,8 +371,12 @@ extern "C" int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int
                               const float* Z, int64_t ldgh, int R, int R_s, int i1, int count,
                               int qmode, const float* scale, const int32_t* col_group,
                               float* dyn_scale, int maxq, int sym, int atomic,
-                              const int* z_nonzero, int16_t* codes, float* err, void* stream) {
+                              const int* z_nonzero, int16_t* codes, float* err, int gmode,
+                              const float* anchor, int64_t ld_anchor, const float* beta,
+                              void* stream) {
   if (!Wp || !Hinv_all || !GH || !Z || !z_nonzero || !codes || !err) return RQ_EINVAL;
+  if (gmode < 0 || gmode > 2) return RQ_EINVAL;
+  if (gmode != 0 && (!anchor || !beta || ld_anchor < C)) return RQ_EINVAL;
   if (R <= 0 || R_s <= 0 || R % R_s != 0 || C <= 0 || ldw < C || ldgh < C) return RQ_EINVAL;
   if (count <= 0 || count > QB_MAXB || i1 < 0 || i1 + count > C || maxq <= 0) return RQ_EINVAL;
   if (qmode == RQ_QMODE_CHANNEL && !scale) return RQ_EINVAL;
@@ -329,24 +384,41 @@ extern "C" int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int
   if (qmode == RQ_QMODE_DYNAMIC && !dyn_scale) return RQ_EINVAL;
   if (qmode < 0 || qmode > 2) return RQ_EINVAL;
   QBArgs a{Wp, ldw, Hinv_all, C, GH, Z, ldgh, R, R_s, i1, count, qmode, scale, col_group,
-           dyn_scale, (float)maxq, sym, atomic, z_nonzero, codes, err};
+           dyn_scale, (float)maxq, sym, atomic, z_nonzero, codes, err, anchor, ld_anchor, beta};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   dim3 grid((R_s + 63) / 64, R / R_s), block(256);
-  if (count <= 32) hipLaunchKernelGGL(k_quant_block<8>, grid, block, 0, s, a);
-  else hipLaunchKernelGGL(k_quant_block<32>, grid, block, 0, s, a);
+  const bool small = count <= 32;
+  switch (gmode) {
+    case 0:
+      if (small) hipLaunchKernelGGL((k_quant_block<8, 0>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_quant_block<32, 0>), grid, block, 0, s, a);
+      break;
+    case 1:
+      if (small) hipLaunchKernelGGL((k_quant_block<8, 1>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_quant_block<32, 1>), grid, block, 0, s, a);
+      break;
+    default:
+      if (small) hipLaunchKernelGGL((k_quant_block<8, 2>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_quant_block<32, 2>), grid, block, 0, s, a);
+  }
   RQ_CHECK_LAUNCH();
   return RQ_OK;
 }
 
 extern "C" int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float* Z, int64_t ldgh,
                                   const float* Hinv_all, int C, int R, int R_s, int i1, int count,
-                                  const float* err, const int* z_nonzero, void* stream) {
+                                  const float* err, const int* z_nonzero, int gmode,
+                                  const float* anchor, int64_t ld_anchor, const float* beta,
+                                  void* stream) {
   if (!Wp || !GH || !Z || !Hinv_all || !err || !z_nonzero) return RQ_EINVAL;
+  if (gmode < 0 || gmode > 2) return RQ_EINVAL;
+  if (gmode != 0 && (!anchor || !beta || ld_anchor < C)) return RQ_EINVAL;
   if (R <= 0 || R_s <= 0 || R % R_s != 0 || C <= 0 || ldw < C || ldgh < C) return RQ_EINVAL;
   if (count <= 0 || i1 < 0 || i1 + count > C) return RQ_EINVAL;
   const int i2 = i1 + count;
   if (i2 >= C) return RQ_OK;
-  TrArgs a{Wp, ldw, GH, Z, ldgh, Hinv_all, C, R, R_s, i1, count, err, z_nonzero};
+  TrArgs a{Wp, ldw, GH, Z, ldgh, Hinv_all, C, R, R_s, i1, count, err, z_nonzero, gmode,
+           anchor, ld_anchor, beta};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   dim3 grid((C - i2 + 63) / 64, (R_s + 63) / 64, R / R_s), block(256);
   hipLaunchKernelGGL(k_trailing, grid, block, 0, s, a);

@@ -1,4 +1,4 @@
-"""Drop-in ``GPTQPlus`` (reference: gptq_utils/gptq_plus_utils.py:430-1896, frozen mode) whose
+"""Drop-in ``GPTQPlus`` (reference: gptq_utils/gptq_plus_utils.py:430-1896) whose
 arithmetic runs in the gfx950 HIP kernels of ``libgptqplus_hip.so``.
 
 The constructor, ``add_batch`` / ``finalize_hessian`` / ``fasterquant`` / ``free`` signatures,
@@ -9,9 +9,10 @@ the layer dtype, ``int_weight`` / ``scale`` buffers with ``export_to_et``) follo
 reference.  Additionally exposed for inspection: ``perm``, ``invperm``, ``codes`` (natural
 column order), ``subgroup_info`` (damping, retries, identity fallback, beta).
 
-Modes whose work needs a layer backward (``g_update_mode`` other than ``"frozen"``) and
-``diagnostic_recorder`` dumps raise ``NotImplementedError`` rather than silently running
-different arithmetic.
+``g_update_mode`` ``"frozen"`` (default), ``"surrogate_block"`` and ``"surrogate_online"`` run
+on the HIP path.  Modes whose work needs a layer backward (``"block_gd"``, ``"block_backward"``,
+``"online"``, ...) and ``diagnostic_recorder`` dumps raise ``NotImplementedError`` rather than
+silently running different arithmetic.
 """
 from __future__ import annotations
 
@@ -181,7 +182,7 @@ class GPTQPlus:
                     block_atomic_quant=False, block_observer=None, grad_clip=1.0,
                     diagnostic_recorder=None, slide_refresh_start=0, slide_refresh_block_total=None,
                     refresh_full_metrics=False, keep_hinv=False, inject=None):
-        """Quantize ``layer.weight`` in place (gptq_plus_utils.py:910-1896, frozen mode).
+        """Quantize ``layer.weight`` in place (gptq_plus_utils.py:910-1896).
 
         Extra keyword arguments (not in the reference):
           keep_hinv -- keep ``Hinv_all``, ``Hinv_init_all``, ``Z`` and ``GHinv`` on the object.
@@ -195,9 +196,10 @@ class GPTQPlus:
         inject_hinv = inject.get("hinv")
         self._validate(grad_reg_strategy, grad_reg_lambda, grad_gate_floor, grad_gate_sharpness,
                        grad_gate_sine_amp)
-        if g_update_mode != "frozen":
-            raise NotImplementedError(f"g_update_mode={g_update_mode!r} needs a layer backward; only "
-                                      "'frozen' runs on the HIP path")
+        if g_update_mode not in nat.GMODES:
+            raise NotImplementedError(f"g_update_mode={g_update_mode!r} needs a layer backward; "
+                                      f"the HIP path runs {sorted(nat.GMODES)}")
+        gmode = nat.GMODES[g_update_mode]
         if diagnostic_recorder is not None:
             raise NotImplementedError("diagnostic_recorder dumps are not produced by the HIP path")
         if not self._finalized:
@@ -272,6 +274,8 @@ class GPTQPlus:
                     r0 = sub * R_s
                     K.prepare_subgroup(W[r0:], grads[r0:], self.H[sub], perm, Wp[r0:r0 + R_s],
                                        Gs[r0:r0 + R_s], H_work[sub])
+            # surrogate modes refresh GHinv against the weight before the first block
+            anchor = Wp.clone() if gmode != nat.RQ_GMODE_FROZEN else None
             # damped Cholesky chain, subgroups batched through every launch
             with _section(rec, "fasterquant.subgroup.compute_hinv"):
                 if inject_hinv is None:
@@ -309,6 +313,12 @@ class GPTQPlus:
                 self.subgroup_info.append(dict(damp_percent=damp, identity_fallback=fallback,
                                                attempts=attempts, beta=beta))
             del Gs, GH0
+            beta_rows = None
+            if gmode != nat.RQ_GMODE_FROZEN:
+                beta_rows = torch.zeros(R, **f32)
+                if beta_mode == 1:
+                    for sub, info in enumerate(self.subgroup_info):
+                        beta_rows[sub * R_s:(sub + 1) * R_s].copy_(info["beta"])
             self.GHinv_initial = GH.clone() if keep_hinv else None
             z_any = torch.amax(z_flags).reshape(1).contiguous()
 
@@ -327,13 +337,15 @@ class GPTQPlus:
                         bscale, _ = q.params_on(Wp[:, i1:i2])
                         dyn_scale[bidx].copy_(bscale[0])
                         K.quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, nat.RQ_QMODE_CHANNEL,
-                                      dyn_scale[bidx], None, None, maxq, sym, atomic, z_any, codes, err)
+                                      dyn_scale[bidx], None, None, maxq, sym, atomic, z_any, codes, err,
+                                      gmode, anchor, beta_rows)
                     else:
                         K.quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale_tab, col_group,
                                       dyn_scale[bidx] if dyn_scale is not None else None, maxq, sym,
-                                      atomic, z_any, codes, err)
+                                      atomic, z_any, codes, err, gmode, anchor, beta_rows)
                     if i2 < C:
-                        K.trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_any)
+                        K.trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_any, gmode,
+                                          anchor, beta_rows)
 
             with _section(rec, "fasterquant.write_layer_weight"):
                 Q = torch.empty((R, C), dtype=W.dtype, device=dev)

@@ -172,28 +172,43 @@ def gptqplus_terms(G_sub, Hinv_init, Hinv, alpha_eff, reference_loss, beta_mode,
              nat.ptr(GHinv), Z.stride(0), nat.ptr(GH0), nat.ptr(z_nonzero), _stream(G_sub))
 
 
+def _surrogate(gmode, anchor, beta, R, C):
+    if gmode == nat.RQ_GMODE_FROZEN:
+        return 0
+    if anchor is None or beta is None:
+        raise ValueError("surrogate g_update modes need anchor and beta")
+    if anchor.shape != (R, C) or anchor.stride(1) != 1 or beta.numel() != R or not beta.is_contiguous():
+        raise ValueError("anchor must be row-major [R, C] and beta a contiguous [R] vector")
+    if anchor.dtype != torch.float32 or beta.dtype != torch.float32:
+        raise ValueError("anchor and beta must be float32")
+    return anchor.stride(0)
+
+
 def quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale, col_group, dyn_scale, maxq, sym,
-                atomic, z_nonzero, codes, err):
+                atomic, z_nonzero, codes, err, gmode=nat.RQ_GMODE_FROZEN, anchor=None, beta=None):
     R, C = Wp.shape
     if Hinv_all.shape != (R // R_s, C, C):
         raise ValueError("quant_block: Hinv_all must be [G, C, C]")
+    lda = _surrogate(gmode, anchor, beta, R, C)
     _cout(Wp, "Wp"), _cin(Hinv_all, "Hinv_all"), _cin(GH, "GH"), _cin(Z, "Z")
     if not (Hinv_all.is_contiguous() and GH.stride(1) == 1 and Z.stride(1) == 1):
         raise ValueError("quant_block: Hinv_all must be contiguous, GH / Z row-major")
     nat.call("rq_quant_block", nat.ptr(Wp), Wp.stride(0), nat.ptr(Hinv_all), C, nat.ptr(GH), nat.ptr(Z),
              GH.stride(0), R, R_s, int(i1), int(count), int(qmode), nat.ptr(scale), nat.ptr(col_group),
              nat.ptr(dyn_scale), int(maxq), int(bool(sym)), int(bool(atomic)), nat.ptr(z_nonzero),
-             nat.ptr(codes), nat.ptr(err), _stream(Wp))
+             nat.ptr(codes), nat.ptr(err), int(gmode), nat.ptr(anchor), lda, nat.ptr(beta), _stream(Wp))
 
 
-def trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_nonzero):
+def trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_nonzero, gmode=nat.RQ_GMODE_FROZEN,
+                    anchor=None, beta=None):
     R, C = Wp.shape
+    lda = _surrogate(gmode, anchor, beta, R, C)
     _cout(Wp, "Wp"), _cout(GH, "GH"), _cout(err, "err")
     if not (Hinv_all.is_contiguous() and Z.stride(1) == 1):
         raise ValueError("trailing_update: Hinv_all must be contiguous, Z row-major")
     nat.call("rq_trailing_update", nat.ptr(Wp), Wp.stride(0), nat.ptr(GH), nat.ptr(Z), GH.stride(0),
              nat.ptr(Hinv_all), C, R, R_s, int(i1), int(count), nat.ptr(err), nat.ptr(z_nonzero),
-             _stream(Wp))
+             int(gmode), nat.ptr(anchor), lda, nat.ptr(beta), _stream(Wp))
 
 
 def writeback(codes, invperm, qmode, scale, col_group, dyn_scale, blocksize, q_out, w_int_out=None,

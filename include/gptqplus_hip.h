@@ -27,6 +27,11 @@ extern "C" {
 #define RQ_BF16 1
 #define RQ_F32 2
 
+/* g_update modes of rq_quant_block / rq_trailing_update (gptq_plus_utils.py:580-584) */
+#define RQ_GMODE_FROZEN 0           /* gh_eff = GH                                          */
+#define RQ_GMODE_SURROGATE_BLOCK 1  /* gh_eff = GH + beta_r (W_block_start - anchor)          */
+#define RQ_GMODE_SURROGATE_ONLINE 2 /* gh_eff = GH + beta_r (W_live - anchor), per column      */
+
 /* quantizer modes of rq_quant_block / rq_writeback */
 #define RQ_QMODE_CHANNEL 0 /* one scale per row            (gptq_plus_utils.py:1008-1020) */
 #define RQ_QMODE_STATIC 1  /* per column-group, act_order  (gptq_plus_utils.py:994-1002)  */
@@ -124,20 +129,28 @@ int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* Hinv_init, c
  * Writes int16 codes [R, C] (permuted order) and err [R, count] for rq_trailing_update.
  * qmode: RQ_QMODE_CHANNEL scale[r]; RQ_QMODE_STATIC scale[col_group[i1+i]*R + r];
  * RQ_QMODE_DYNAMIC computes scale from the block start into dyn_scale[r] (caller offsets it
- * per block).  count <= 128. */
+ * per block).  count <= 128.
+ * gmode (RQ_GMODE_*): in the surrogate modes the GHinv term is refreshed before every
+ * column (:1190-1199, :1360-1367) from anchor (the permuted weight before the first block,
+ * [R, C] row stride ld_anchor) and beta[r] (fp32, one per row of all subgroups); both may be
+ * NULL for RQ_GMODE_FROZEN. */
 int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int C, const float* GH,
                    const float* Z, int64_t ldgh, int R, int R_s, int i1, int count, int qmode,
                    const float* scale, const int32_t* col_group, float* dyn_scale, int maxq,
                    int sym, int atomic, const int* z_nonzero, int16_t* codes, float* err,
+                   int gmode, const float* anchor, int64_t ld_anchor, const float* beta,
                    void* stream);
 
-/* Outer (trailing) update after a block, frozen mode -- gptq_plus_utils.py:1500-1570:
+/* Outer (trailing) update after a block -- gptq_plus_utils.py:1500-1570:
  * Wp[:, i2:] -= err Hinv[i1:i2, i2:] + (count GH[:, i2:] - (Z[:, i1:i2] D) Hinv[i1:i2, i2:]),
  * GH[:, i2:] -= Z[:, i1:i2] Hinv[i1:i2, i2:], D = [count-1, ..., 0], per subgroup; the Z
- * terms are skipped when *z_nonzero == 0.  fp32 MFMA. */
+ * terms are skipped when *z_nonzero == 0.  fp32 MFMA.  For gmode != RQ_GMODE_FROZEN the GH
+ * of the first term is GH + beta[r] (Wp - anchor) (outer refresh "surrogate_block",
+ * :1500-1511); the GH update is unchanged. */
 int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float* Z, int64_t ldgh,
                        const float* Hinv_all, int C, int R, int R_s, int i1, int count,
-                       const float* err, const int* z_nonzero, void* stream);
+                       const float* err, const int* z_nonzero, int gmode, const float* anchor,
+                       int64_t ld_anchor, const float* beta, void* stream);
 
 /* Un-permute and write back -- gptq_plus_utils.py:1850-1875:
  * natural column c of row r takes permuted column j = invperm[c] (identity if NULL):

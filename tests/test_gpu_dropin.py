@@ -64,7 +64,7 @@ def test_golden_fasterquant_same_inverse(case):
         inject["perm"] = case.sub(0, "perm")
     g.fasterquant(blocksize=m["B"], percdamp=0.01, groupsize=m["gs"], actorder=m["act"],
                   static_groups=m["act"], block_atomic_quant=m["atomic"], export_to_et=True,
-                  inject=inject, keep_hinv=True)
+                  inject=inject, keep_hinv=True, g_update_mode=m.get("mode", "frozen"))
     torch.cuda.synchronize()
     assert torch.equal(g.quantizer.scale.cpu(), case.t("qscale"))
     for s, info in enumerate(g.subgroup_info):
@@ -94,7 +94,8 @@ def test_golden_fasterquant_own_chain(case):
                     m.get("mse", False))
     _accumulate(g, case.t("X"), 4)
     g.fasterquant(blocksize=m["B"], percdamp=0.01, groupsize=m["gs"], actorder=m["act"],
-                  static_groups=m["act"], block_atomic_quant=m["atomic"], export_to_et=True, keep_hinv=True)
+                  static_groups=m["act"], block_atomic_quant=m["atomic"], export_to_et=True, keep_hinv=True,
+                  g_update_mode=m.get("mode", "frozen"))
     torch.cuda.synchronize()
     for s, info in enumerate(g.subgroup_info):
         assert info["identity_fallback"] == bool(case.arrays[f"sub{s}_identity_fallback"])
@@ -124,6 +125,9 @@ CFGS = [
     dict(name="g2_sym3_ragged", R=128, C=300, G=2, bits=3, sym=True, gs=-1, act=True, B=64, atomic=False, alpha=0.0),
     dict(name="g2_asym4_mse_static", R=128, C=384, G=2, bits=4, sym=False, gs=128, act=True, B=128, atomic=False, alpha=0.0, mse=True),
     dict(name="g2_sym4_mse_dynamic", R=128, C=384, G=2, bits=4, sym=True, gs=128, act=False, B=128, atomic=False, alpha=0.0, mse=True),
+    dict(name="g2_sym4_surrogate_block_static", R=256, C=512, G=2, bits=4, sym=True, gs=128, act=True, B=128, atomic=False, alpha=0.05, ref_loss=3e4, gscale=1e-1, mode="surrogate_block"),
+    dict(name="g4_asym4_surrogate_online", R=256, C=512, G=4, bits=4, sym=False, gs=-1, act=True, B=128, atomic=False, alpha=0.05, ref_loss=3e4, gscale=1e-1, mode="surrogate_online"),
+    dict(name="g2_sym4_surrogate_online_dyn_atomic", R=128, C=384, G=2, bits=4, sym=True, gs=64, act=False, B=64, atomic=True, alpha=0.05, ref_loss=3e4, gscale=1e-1, mode="surrogate_online"),
 ]
 
 
@@ -139,7 +143,8 @@ def test_dropin_vs_oracle(cfg):
         o.add_batch(X[j:j + 4])
     o.finalize_hessian()
     fq = dict(blocksize=cfg["B"], percdamp=0.01, groupsize=cfg["gs"], actorder=cfg["act"],
-              static_groups=cfg["act"], block_atomic_quant=cfg["atomic"])
+              static_groups=cfg["act"], block_atomic_quant=cfg["atomic"],
+              g_update_mode=cfg.get("mode", "frozen"))
     res = o.fasterquant(stable_ties=True, **fq)
 
     g, layer = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False))
