@@ -113,12 +113,29 @@ def test_find_params_mse_matches_oracle(bits, sym, gs):
     q = make_quantizer(bits, sym, mse=True)
     scale, zero = K.find_params_mse(W.to(DEV), int(q.maxq), sym, group_size=gs)
     groups = range(0, 256, gs) if gs > 0 else [0]
+    maxq = float(q.maxq)
+
+    def clip_err(x, s_, z_):
+        # the search's objective (quant_utils.py:431-444) in fp64
+        x, s_, z_ = x.double(), float(s_), float(z_)
+        if sym:
+            qv = s_ * torch.clamp(torch.round(x / s_), -(maxq + 1), maxq)
+        else:
+            qv = s_ * (torch.clamp(torch.round(x / s_) + z_, 0, maxq) - z_)
+        return float(((qv - x).abs() ** 2.4).sum())
+
     mism = 0
     for k, c0 in enumerate(groups):
+        Wg = W.float()[:, c0:c0 + gs] if gs > 0 else W.float()
         qo = make_quantizer(bits, sym, mse=True)
-        qo.find_params(W.float()[:, c0:c0 + gs] if gs > 0 else W.float())
+        qo.find_params(Wg)
         diff = (scale[k].cpu() != qo.scale.flatten()) | (zero[k].cpu() != qo.zero.flatten())
         mism += int(diff.sum())
+        for r_ in torch.nonzero(diff).flatten().tolist():
+            # a different choice is allowed only between candidates of equal error
+            e_gpu = clip_err(Wg[r_], scale[k, r_].cpu(), zero[k, r_].cpu())
+            e_ora = clip_err(Wg[r_], qo.scale.flatten()[r_], qo.zero.flatten()[r_])
+            assert abs(e_gpu - e_ora) <= 1e-5 * e_ora, (r_, e_gpu, e_ora)
     n = 96 * len(groups)
     print(f"mse search: {mism}/{n} (row, group) choices differ from the oracle")
     assert mism <= max(1, n // 100)
