@@ -212,15 +212,6 @@ __global__ __launch_bounds__(256) void k_gather_h(const float* __restrict__ Hg, 
 }
 
 template <typename TQ>
-__device__ __forceinline__ TQ rq_cast(float v);
-template <>
-__device__ __forceinline__ __half rq_cast<__half>(float v) { return __float2half_rn(v); }
-template <>
-__device__ __forceinline__ __hip_bfloat16 rq_cast<__hip_bfloat16>(float v) { return __float2bfloat16(v); }
-template <>
-__device__ __forceinline__ float rq_cast<float>(float v) { return v; }
-
-template <typename TQ>
 __global__ __launch_bounds__(256) void k_writeback(const int16_t* __restrict__ codes, int R, int C,
                                                    const int64_t* __restrict__ invperm, int qmode,
                                                    const float* __restrict__ scale,

@@ -63,3 +63,13 @@ __device__ __forceinline__ void rq_params_from_minmax(float rmin, float rmax, fl
 
 __device__ __forceinline__ int rq_isfinite(float x) { return (x == x) && (fabsf(x) <= 3.402823466e38f); }
 __device__ __forceinline__ int rq_isfinite(double x) { return (x == x) && (fabs(x) <= 1.7976931348623157e308); }
+
+// fp32 -> output dtype, round to nearest even (torch's .to(dtype))
+template <typename TQ>
+__device__ __forceinline__ TQ rq_cast(float v);
+template <>
+__device__ __forceinline__ __half rq_cast<__half>(float v) { return __float2half_rn(v); }
+template <>
+__device__ __forceinline__ __hip_bfloat16 rq_cast<__hip_bfloat16>(float v) { return __float2bfloat16(v); }
+template <>
+__device__ __forceinline__ float rq_cast<float>(float v) { return v; }

@@ -362,6 +362,7 @@ class GPTQPlus:
         self.perm, self.invperm = perm, invperm
         self._codes_perm = codes
         self.qmode, self.scale_table, self.col_group, self.dyn_scale = qmode, scale_tab, col_group, dyn_scale
+        self.blocksize_used, self.groupsize_used = blocksize, groupsize
         self.Hinv_all = Hinv_all if keep_hinv else None
         self.Hinv_init_all = Hinit_all if keep_hinv else None
         self.Z = Z if keep_hinv else None
@@ -401,6 +402,12 @@ class GPTQPlus:
             raise ValueError(f"`grad_gate_sine_amp` must be non-negative. Got {grad_gate_sine_amp}.")
 
     # gptq_plus_utils.py:2357-2361
+    def export_packed(self):
+        """Packed form of the quantized weight (call after ``fasterquant``, before ``free``):
+        see ``gptq_plus_mp_quant_amd.export.export_packed``."""
+        from .export import export_packed
+        return export_packed(self)
+
     def free(self):
         self.H = None
         self.Losses = None

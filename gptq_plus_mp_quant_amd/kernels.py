@@ -218,3 +218,61 @@ def writeback(codes, invperm, qmode, scale, col_group, dyn_scale, blocksize, q_o
              nat.ptr(col_group), nat.ptr(dyn_scale), int(blocksize), nat.ptr(q_out),
              nat.dtype_code(q_out.dtype), q_out.stride(0), nat.ptr(w_int_out), nat.ptr(scale_out),
              nat.ptr(nan_flag), _stream(codes))
+
+
+def packed_words(C, nbits):
+    n = nat.load().rq_packed_words_per_row(int(C), int(nbits))
+    if n < 0:
+        raise ValueError(f"packed_words: bad C={C} / nbits={nbits}")
+    return int(n)
+
+
+def pack_codes(codes, nbits, invperm=None, out=None, range_flag=None):
+    """int16 codes [R, C] (permuted order when invperm is given) -> [R, ceil(C*nbits/32)] words
+    (uint32 bit patterns held in an int32 tensor)."""
+    nat.require_gpu(codes, "codes")
+    if codes.dtype != torch.int16 or codes.dim() != 2 or codes.stride(1) != 1:
+        raise ValueError("pack_codes: codes must be row-major int16 [R, C]")
+    R, C = codes.shape
+    words = packed_words(C, nbits)
+    if out is None:
+        out = torch.empty((R, words), dtype=torch.int32, device=codes.device)
+    if out.dtype != torch.int32 or out.shape != (R, words) or out.stride(1) != 1:
+        raise ValueError("pack_codes: out must be row-major int32 [R, words]")
+    if invperm is not None:
+        invperm = _cin(invperm, "invperm", torch.int64)
+        if invperm.numel() != C:
+            raise ValueError("pack_codes: invperm must be int64 [C]")
+    nat.call("rq_pack_codes", nat.ptr(codes), R, C, codes.stride(0), nat.ptr(invperm), int(nbits),
+             nat.ptr(out), out.stride(0), nat.ptr(range_flag), _stream(codes))
+    return out
+
+
+def unpack_dequant(packed, C, nbits, scales=None, g_idx=None, q_dtype=torch.float16, want_codes=False):
+    """Inverse of pack_codes: returns (Q [R, C] in q_dtype or None, codes int16 [R, C] or None)."""
+    nat.require_gpu(packed, "packed")
+    R = packed.shape[0]
+    if packed.dtype != torch.int32 or packed.stride(1) != 1 or packed.shape[1] < packed_words(C, nbits):
+        raise ValueError("unpack_dequant: packed must be row-major int32 [R, >= words]")
+    q = codes = None
+    if scales is not None:
+        scales = _cin(scales, "scales")
+        if scales.dtype != torch.float32 or scales.dim() != 2 or scales.shape[1] != R:
+            raise ValueError("unpack_dequant: scales must be float32 [ngroups, R]")
+        if g_idx is not None:
+            g_idx = _cin(g_idx, "g_idx", torch.int32)
+            if g_idx.numel() != C:
+                raise ValueError("unpack_dequant: g_idx must be int32 [C]")
+            if int(g_idx.min()) < 0 or int(g_idx.max()) >= scales.shape[0]:
+                raise ValueError("unpack_dequant: g_idx out of range of the scale table")
+        elif scales.shape[0] != 1:
+            raise ValueError("unpack_dequant: several scale groups need g_idx")
+        q = torch.empty((R, C), dtype=q_dtype, device=packed.device)
+    if want_codes:
+        codes = torch.empty((R, C), dtype=torch.int16, device=packed.device)
+    if q is None and codes is None:
+        raise ValueError("unpack_dequant: nothing to produce")
+    nat.call("rq_unpack_dequant", nat.ptr(packed), R, C, packed.stride(0), int(nbits), nat.ptr(scales),
+             R, nat.ptr(g_idx), nat.ptr(q), nat.dtype_code(q_dtype) if q is not None else 0,
+             C, nat.ptr(codes), _stream(packed))
+    return q, codes

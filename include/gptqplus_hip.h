@@ -163,6 +163,30 @@ int rq_writeback(const int16_t* codes, int R, int C, const int64_t* invperm, int
                  int blocksize, void* q_out, int q_dtype, int64_t ldq, float* w_int_out,
                  float* scale_out, int* nan_flag, void* stream);
 
+/* Packed export.  The reference's export_to_et keeps codes and scales as two fp32 [R, C]
+ * tensors (gptq_plus_utils.py:1866-1871) and saves the `quantizers` dict next to the
+ * fake-quantized state_dict (gptq_utils/main.py:68-71); this is the compact form of the
+ * same information.  Row r of `out` is a little-endian bitstream of C fields of nbits bits:
+ * field c = code[r, invperm ? invperm[c] : c] + 2^(nbits-1), at bits [c*nbits, (c+1)*nbits),
+ * bit b in bit (b & 31) of 32-bit word (b >> 5); trailing bits are zero.
+ * nbits = bits for sym, bits + 1 for asym (codes lie in [-(maxq+1), maxq],
+ * quant_utils.py:477).  Returns the words per row (ceil(C*nbits/32)), or RQ_EINVAL. */
+int64_t rq_packed_words_per_row(int C, int nbits);
+
+/* Pack int16 codes [R, C] (row stride ldc; permuted order when invperm != NULL) into
+ * out [R, ldo] uint32.  A code outside [-2^(nbits-1), 2^(nbits-1)) (incl. the NaN marker)
+ * sets *range_flag (device int, optional) and is stored masked.  2 <= nbits <= 16. */
+int rq_pack_codes(const int16_t* codes, int R, int C, int64_t ldc, const int64_t* invperm,
+                  int nbits, uint32_t* out, int64_t ldo, int* range_flag, void* stream);
+
+/* Inverse of rq_pack_codes, optionally dequantizing: codes_out[r, c] (int16 [R, C], optional)
+ * and q_out[r, c] = scales[g_idx[c] * lds + r] * code (fp32 product, then cast to q_dtype,
+ * [R, C] row stride ldq), g_idx NULL = one group.  Equal, bit for bit, to the weight
+ * fasterquant wrote (rq_writeback) when scales / g_idx describe its scale table. */
+int rq_unpack_dequant(const uint32_t* packed, int R, int C, int64_t ldp, int nbits,
+                      const float* scales, int64_t lds, const int32_t* g_idx, void* q_out,
+                      int q_dtype, int64_t ldq, int16_t* codes_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

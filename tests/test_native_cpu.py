@@ -18,7 +18,7 @@ def _lib():
 def test_header_symbols_are_exported_and_bound():
     lib = _lib()
     syms = nat.header_symbols()
-    assert len(syms) >= 12
+    assert len(syms) >= 17
     for name in syms:
         assert hasattr(lib, name), f"{name} not exported"
         assert name in nat.SIGNATURES, f"{name} has no ctypes binding"
@@ -55,6 +55,14 @@ def test_argument_validation_needs_no_device():
                                   fake, null) == nat.RQ_EINVAL
     assert lib.rq_writeback(null, 4, 4, null, 0, null, null, null, 4, null, 0, 4, null, null, null,
                             null) == nat.RQ_EINVAL
+    # packed export: word count, and refusal of bad widths / short rows before any launch
+    assert lib.rq_packed_words_per_row(33, 3) == 4 and lib.rq_packed_words_per_row(32, 4) == 4
+    assert lib.rq_packed_words_per_row(8, 1) < 0
+    fake = ctypes.c_void_p(16)
+    assert lib.rq_pack_codes(fake, 2, 8, 8, null, 1, fake, 4, null, null) == nat.RQ_EINVAL
+    assert lib.rq_pack_codes(fake, 2, 33, 33, null, 3, fake, 3, null, null) == nat.RQ_EINVAL
+    assert lib.rq_unpack_dequant(fake, 2, 33, 4, 3, null, 2, null, null, 0, 33, null, null) == nat.RQ_EINVAL
+    assert lib.rq_unpack_dequant(fake, 2, 33, 4, 3, null, 2, null, fake, 0, 33, null, null) == nat.RQ_EINVAL
 
 
 def test_dropin_rejects_cpu_tensors():
