@@ -13,8 +13,10 @@ It restates, op for op and in the same torch call order on CPU tensors, the refe
 * ``GPTQPlus.__init__ / add_batch / finalize_hessian`` -- ``gptq_plus_utils.py:431-487, 798-908``
 * ``GPTQPlus._compute_hessian_inverse_with_fallback`` -- ``gptq_plus_utils.py:494-561``
 * ``GPTQPlus._compute_gradient_terms`` -- ``gptq_plus_utils.py:563-578``
-* ``GPTQPlus.fasterquant`` for ``g_update_mode`` in {frozen (default), surrogate_block,
-  surrogate_online} (``_current_ghinv`` :580-584): find_params,
+* ``GPTQPlus.fasterquant`` for every ``g_update_mode``: frozen (default), surrogate_block,
+  surrogate_online (``_current_ghinv`` :580-584), block_backward and block_gd (the optimizer
+  step and regularizers :587-796, refresh :1408-1448, :1572-1848; the layer backward is the
+  caller's ``gradient_refresh_fn``): find_params,
   static / dynamic groups, dead columns, act_order, per-subgroup state, the in-block
   column loop, the block-atomic variant, the trailing (outer) update, un-permute and
   write-back -- ``gptq_plus_utils.py:910-1396, 1500-1570, 1850-1896``.
@@ -217,7 +219,152 @@ def _current_ghinv(base, current_weight, ref_weight, beta_view, refresh_mode):
 
 
 # ---------------------------------------------------------------------------------------
-# GPTQPlus (frozen and surrogate modes)
+# block_gd: optimizer step and first-order regularizers on the trailing columns
+# ---------------------------------------------------------------------------------------
+def kfac_curvature_diag(in_features, input_sq, damping=0.1):
+    """gptq_utils/gptq_plus_utils.py:4601-4640 without an output factor (the call at :1148
+    passes None): the mean-normalised input diagonal as a [1, C] row, plus ``damping``."""
+    a = input_sq.to(dtype=torch.float32).clamp_min(0.0)
+    a = a / a.mean().clamp_min(1e-12)
+    curvature = a.view(1, in_features)
+    if damping and damping > 0:
+        curvature = curvature + float(damping)
+    return curvature
+
+
+def make_opt_state(weight_sub, grad_optimizer, curvature_full=None):
+    """gptq_plus_utils.py:587-605."""
+    if grad_optimizer not in {"sgd", "adam", "h_adam"}:
+        raise ValueError(f"Unsupported `grad_optimizer={grad_optimizer}`.")
+    st = {"type": grad_optimizer, "step": 0}
+    if grad_optimizer in ("adam", "h_adam"):
+        st["exp_avg"] = torch.zeros_like(weight_sub)
+    if grad_optimizer == "adam":
+        st["exp_avg_sq"] = torch.zeros_like(weight_sub)
+    if grad_optimizer == "h_adam":
+        if curvature_full is None:
+            raise ValueError("h_adam requires `curvature_full` (KFAC curvature diagonal).")
+        st["curvature"] = curvature_full
+    return st
+
+
+def clear_opt_state(opt, c0, c1):
+    """gptq_plus_utils.py:607-614."""
+    if opt is None or c1 <= c0:
+        return
+    if opt["type"] in ("adam", "h_adam"):
+        opt["exp_avg"][:, c0:c1].zero_()
+    if opt["type"] == "adam":
+        opt["exp_avg_sq"][:, c0:c1].zero_()
+
+
+def opt_update(opt, grad_sub, c0, lr, grad_clip=1.0, b1=0.9, b2=0.999, eps=1e-8):
+    """gptq_plus_utils.py:616-655: the step for columns [c0, C)."""
+    g = grad_sub[:, c0:]
+    if g.numel() == 0:
+        return g
+    if grad_clip is not None and grad_clip > 0:
+        g = g.clamp(min=-grad_clip, max=grad_clip)
+    if opt["type"] == "sgd":
+        return lr * g
+    opt["step"] += 1
+    m = opt["exp_avg"][:, c0:]
+    m.mul_(b1).add_(g, alpha=1 - b1)
+    bc1 = 1 - b1 ** opt["step"]
+    if opt["type"] == "h_adam":
+        denom = opt["curvature"][:, c0:].sqrt() + eps
+        return (lr / bc1) * (m / denom)
+    v = opt["exp_avg_sq"][:, c0:]
+    v.mul_(b2).addcmul_(g, g, value=1 - b2)
+    bc2 = 1 - b2 ** opt["step"]
+    denom = v.sqrt() / math.sqrt(bc2)
+    denom.add_(eps)
+    return (lr / bc1) * (m / denom)
+
+
+def validate_regularizer(strategy, lam=0.0, floor=0.1, sharp=1.0, sine_amp=0.0):
+    """gptq_plus_utils.py:657-678."""
+    valid = {"none", "l2", "hessian", "quant_error_gate", "quant_error_gate_optimized"}
+    if strategy not in valid:
+        raise ValueError(f"Unsupported `grad_reg_strategy={strategy}`.")
+    if lam < 0:
+        raise ValueError(f"`grad_reg_lambda` must be non-negative. Got {lam}.")
+    if not (0.0 <= floor <= 1.0):
+        raise ValueError(f"`grad_gate_floor` must be in [0, 1]. Got {floor}.")
+    if sharp < 0:
+        raise ValueError(f"`grad_gate_sharpness` must be non-negative. Got {sharp}.")
+    if sine_amp < 0:
+        raise ValueError(f"`grad_gate_sine_amp` must be non-negative. Got {sine_amp}.")
+
+
+def gate_quant_maps(base_q, weight_sub, groupsize, r0, r1, groups=None, perm=None):
+    """gptq_plus_utils.py:680-710: per-element (scale, zero) of the quantizer grid."""
+    gs = torch.zeros_like(weight_sub)
+    gz = torch.zeros_like(weight_sub)
+    if groupsize == -1:
+        gs.copy_(base_q.scale[r0:r1].expand_as(weight_sub))
+        gz.copy_(base_q.zero[r0:r1].expand_as(weight_sub))
+        return gs, gz
+    if groups is None:
+        raise ValueError("`groups` must be provided when groupsize != -1.")
+    ids = (torch.arange(weight_sub.shape[1]) if perm is None else perm) // groupsize
+    for gid, gq in enumerate(groups):
+        mask = ids == gid
+        n = int(mask.sum().item())
+        if n == 0:
+            continue
+        gs[:, mask] = gq.scale[r0:r1].expand(-1, n)
+        gz[:, mask] = gq.zero[r0:r1].expand(-1, n)
+    return gs, gz
+
+
+def nearest_quant_grid(w, scale, zero, maxq, sym):
+    """gptq_plus_utils.py:712-719."""
+    scale = scale.clamp(min=1e-8)
+    if sym:
+        return scale * torch.clamp(torch.round(w / scale), -(maxq + 1), maxq)
+    q = torch.clamp(torch.round(w / scale) + zero, 0, maxq)
+    return scale * (q - zero)
+
+
+def sine_regularizer_update(w, scale, zero, sym, amp):
+    """gptq_plus_utils.py:721-728."""
+    scale = scale.clamp(min=1e-8)
+    phase = 2 * math.pi * (w / scale) if sym else 2 * math.pi * ((w / scale) + zero)
+    return amp * (2 * math.pi / scale) * torch.sin(phase)
+
+
+def apply_regularizer(st, current, upd, c0, lr, strategy, lam, floor, sharp, sine_amp, maxq, sym):
+    """gptq_plus_utils.py:730-796: returns (update, gate part, sine part)."""
+    if upd.numel() == 0:
+        return upd, upd, torch.zeros_like(upd)
+    validate_regularizer(strategy, lam, floor, sharp, sine_amp)
+    cur = current[:, c0:]
+    if strategy == "none":
+        z = torch.zeros_like(upd)
+        return upd, z, z
+    if strategy == "l2":
+        reg = lr * lam * (cur - st["full_precision_weight"][:, c0:])
+        return upd + reg, reg, torch.zeros_like(reg)
+    if strategy == "hessian":
+        diff = current - st["full_precision_weight"]
+        reg = lr * lam * diff.matmul(st["hessian_reg"][:, c0:])
+        return upd + reg, reg, torch.zeros_like(reg)
+    sc = st["gate_scale"][:, c0:]
+    zr = st["gate_zero"][:, c0:]
+    qn = nearest_quant_grid(cur, sc, zr, maxq, sym)
+    dist = (cur - qn).abs() / sc.clamp(min=1e-8)
+    gate = floor + (1.0 - floor) * (1.0 - torch.exp(-sharp * dist))
+    gated = upd * gate
+    gate_part = gated - upd
+    if strategy == "quant_error_gate":
+        return gated, gate_part, torch.zeros_like(gate_part)
+    sine = lr * sine_regularizer_update(cur, sc, zr, sym, sine_amp)
+    return gated + sine, gate_part, sine
+
+
+# ---------------------------------------------------------------------------------------
+# GPTQPlus (all g_update modes; the layer backward comes from the caller's refresh fn)
 # ---------------------------------------------------------------------------------------
 @dataclass
 class SubgroupRecord:
@@ -319,14 +466,26 @@ class GPTQPlusOracle:
     @torch.no_grad()
     def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
                     static_groups=False, enable_gradient_update=True, g_update_mode="frozen",
-                    block_atomic_quant=False, stable_ties=False) -> FasterquantResult:
-        # frozen and the two surrogate modes (no layer backward); gptq_plus_utils.py:1190-1199,
-        # 1360-1367 (inner) and 1500-1511 (outer)
-        if g_update_mode not in ("frozen", "surrogate_block", "surrogate_online"):
-            raise NotImplementedError("oracle covers g_update_mode in {frozen, surrogate_block, surrogate_online}")
-        inner_mode = g_update_mode
+                    block_atomic_quant=False, stable_ties=False, gradient_refresh_fn=None,
+                    grad_lr=1e-3, grad_optimizer="sgd", curvature_damping=0.1,
+                    grad_reg_strategy="none", grad_reg_lambda=0.0, grad_gate_floor=0.1,
+                    grad_gate_sharpness=1.0, grad_gate_sine_amp=0.0, second_order_scale=1.0,
+                    grad_clip=1.0, slide_refresh_start=0,
+                    slide_refresh_block_total=None) -> FasterquantResult:
+        # g_update modes: gptq_plus_utils.py:1190-1199, 1360-1367 (inner), 1408-1448
+        # (block_backward refresh), 1500-1570 (outer), 1572-1848 (block_gd step)
+        if g_update_mode not in ("frozen", "surrogate_block", "surrogate_online", "block_gd",
+                                 "block_backward"):
+            raise NotImplementedError(f"g_update_mode={g_update_mode!r}")
+        validate_regularizer(grad_reg_strategy, grad_reg_lambda, grad_gate_floor,   # :942-948
+                             grad_gate_sharpness, grad_gate_sine_amp)
+        block_gd = g_update_mode == "block_gd"
+        block_bw = g_update_mode == "block_backward"
+        inner_mode = "surrogate_online" if block_bw else "frozen" if block_gd else g_update_mode
         online = inner_mode == "surrogate_online"
-        outer_mode = "frozen" if g_update_mode == "frozen" else "surrogate_block"
+        outer_mode = ("frozen" if g_update_mode in ("frozen", "block_backward", "block_gd")
+                      else "surrogate_block")                          # :1500
+        sos = second_order_scale
         dt = self.dtype
         W = self.weight.clone().to(dt)
         quantizer = self.quantizer
@@ -337,9 +496,14 @@ class GPTQPlusOracle:
         if not quantizer.ready():
             quantizer.find_params(W)                                   # :978-980
 
-        dynamic_groups = groupsize != -1 and not static_groups         # :982-987
+        dynamic_groups = groupsize != -1 and not static_groups         # :982-992
         if dynamic_groups and groupsize != blocksize:
             raise ValueError("`groupsize` must equal `blocksize` when using dynamic groups in GPTQ+.")
+        if dynamic_groups and grad_reg_strategy in {"quant_error_gate", "quant_error_gate_optimized"}:
+            raise ValueError("Dynamic weight groups are not supported with quant_error_gate regularization yet.")
+        need_hreg = grad_reg_strategy == "hessian"                     # :1024-1026
+        need_fp = grad_reg_strategy in {"l2", "hessian"}
+        need_gate = grad_reg_strategy in {"quant_error_gate", "quant_error_gate_optimized"}
 
         shared_groups = None
         if groupsize != -1 and static_groups:                          # :994-1002
@@ -374,16 +538,40 @@ class GPTQPlusOracle:
                 H_sub = H_sub[perm][:, perm]
                 G_sub = G_sub[:, perm]
                 invperm = torch.argsort(perm)
+            h_diag = torch.diagonal(H_sub).clone() if (block_gd and grad_optimizer == "h_adam") else None
+            hessian_reg = H_sub.clone() if need_hreg else None         # :1061-1065
+            gate_scale = gate_zero = None
+            if need_gate:                                              # :1066-1078
+                gate_scale, gate_zero = gate_quant_maps(quantizer, W_sub, groupsize, r0, r1,
+                                                        shared_groups, perm)
             Hinv_init, Hinv, damp, fallback, attempts = hessian_inverse_with_fallback(H_sub, percdamp)
             beta, Z, GHinv, _ = gradient_terms(G_sub, Hinv_init, Hinv, self.alpha, self.reference_loss,
                                                self.rows, self.columns, enable_gradient_update)
             records.append(SubgroupRecord(r0, r1, perm, invperm, Hinv_init, Hinv, damp, fallback,
                                           attempts, beta, Z.clone(), GHinv.clone(), W_sub.clone()))
             states.append(dict(r0=r0, r1=r1, W_sub=W_sub, Hinv=Hinv, Z=Z, GHinv=GHinv, perm=perm,
-                               anchor=W_sub.clone(), beta_view=beta.unsqueeze(1),
+                               anchor=W_sub.clone(), beta_view=beta.unsqueeze(1), Hinv_init=Hinv_init,
+                               full_precision_weight=W_sub.clone() if need_fp else None,
+                               hessian_reg=hessian_reg, gate_scale=gate_scale, gate_zero=gate_zero,
+                               opt=make_opt_state(W_sub, grad_optimizer,
+                                                  kfac_curvature_diag(self.columns, h_diag, curvature_damping)
+                                                  if grad_optimizer == "h_adam" else None)
+                               if block_gd else None,
                                invperm=invperm, Q=torch.zeros_like(W_sub),
                                W_int=torch.zeros_like(W_sub), Scale=torch.zeros_like(W_sub),
                                fast_scale=fast_scale_full[r0:r1] if fast else None))
+
+        n_blocks = (self.columns + blocksize - 1) // blocksize         # :1165-1167
+        n_refresh_total = max(n_blocks - 1, 0)
+        maxq_int = int(quantizer.maxq.item())
+
+        def snapshot(cur_of):
+            # weight_snapshot rows = each subgroup's current weight, un-permuted (:1412-1420)
+            snap = self.weight.clone().to(dt)
+            for st in states:
+                cur = cur_of(st)
+                snap[st["r0"]:st["r1"], :] = cur[:, st["invperm"]] if actorder else cur
+            return snap
 
         for i1 in range(0, self.columns, blocksize):                   # :1169
             i2 = min(i1 + blocksize, self.columns)
@@ -456,7 +644,10 @@ class GPTQPlusOracle:
                             Scale1[:, i] = sc.flatten()
                         err1 = (w - q - GHinv1_eff[:, i]) / d
                         upd = err1.unsqueeze(1).matmul(Hinv1[i, i:].unsqueeze(0))
-                        W1[:, i:] -= upd + GHinv1_eff[:, i:]
+                        if block_gd:                                   # :1344-1349
+                            W1[:, i:] -= sos * (upd + GHinv1_eff[:, i:])
+                        else:
+                            W1[:, i:] -= upd + GHinv1_eff[:, i:]
                         Err1[:, i] = err1
                         GHinv1[:, i:].sub_(Z1[:, i].unsqueeze(1).matmul(Hinv1[i, i:].unsqueeze(0)))
                         if inner_mode != "frozen":
@@ -465,15 +656,72 @@ class GPTQPlusOracle:
                 st["Q"][:, i1:i2] = Q1
                 st["W_int"][:, i1:i2] = W_int1
                 st["Scale"][:, i1:i2] = Scale1
-                block_states.append((st, Err1, Z1))
+                if block_bw:                                           # :1389-1396
+                    cur = st["W_sub"].clone()
+                    if i1 > 0:
+                        cur[:, :i1] = st["Q"][:, :i1]
+                    cur[:, i1:i2] = Q1
+                    st["current"] = cur
+                block_states.append([st, Err1, Z1])
+
+            if block_bw and enable_gradient_update:                     # :1408-1448
+                if gradient_refresh_fn is None:
+                    raise ValueError("`gradient_refresh_fn` must be provided for g_update_mode='block_backward'.")
+                grad, _meta = gradient_refresh_fn(snapshot(lambda st: st["current"]))
+                grad = grad.to(dt)
+                for bs in block_states:
+                    st = bs[0]
+                    g_sub = grad[st["r0"]:st["r1"], :]
+                    if actorder:
+                        g_sub = g_sub[:, st["perm"]]
+                    beta, Z, GHinv, _ = gradient_terms(g_sub, st["Hinv_init"], st["Hinv"], self.alpha,
+                                                       self.reference_loss, self.rows, self.columns,
+                                                       enable_gradient_update)
+                    st["beta_view"] = beta.unsqueeze(1)
+                    st["Z"], st["GHinv"] = Z, GHinv
+                    st["anchor"] = st["current"].clone()
+                    bs[2] = Z[:, i1:i2]
 
             for st, Err1, Z1 in block_states:                          # :1500-1570
                 GHinv_rest = _current_ghinv(st["GHinv"][:, i2:], st["W_sub"][:, i2:], st["anchor"][:, i2:],
                                             st["beta_view"], outer_mode)
                 G_Update = count * GHinv_rest - torch.einsum("ij,j,jk->ik", Z1, D, st["Hinv"][i1:i2, i2:])
                 second = Err1.matmul(st["Hinv"][i1:i2, i2:])
-                st["W_sub"][:, i2:] -= second + G_Update
+                if block_gd:
+                    st["W_sub"][:, i2:] -= sos * (second + G_Update)
+                else:
+                    st["W_sub"][:, i2:] -= second + G_Update
                 st["GHinv"][:, i2:] -= st["Z"][:, i1:i2].matmul(st["Hinv"][i1:i2, i2:])
+                if block_gd:
+                    clear_opt_state(st["opt"], i1, i2)
+
+            if block_gd and enable_gradient_update and i2 < self.columns:   # :1572-1848
+                if gradient_refresh_fn is None:
+                    raise ValueError("`gradient_refresh_fn` must be provided for g_update_mode='block_gd'.")
+
+                def effective(st):
+                    cur = st["W_sub"].clone()
+                    cur[:, :i2] = st["Q"][:, :i2]
+                    return cur
+                refresh_idx = i1 // blocksize                          # :1600-1610
+                total = slide_refresh_block_total if slide_refresh_block_total is not None else n_refresh_total
+                idx = slide_refresh_start + refresh_idx
+                slide_alpha = 1.0 - idx / max(total - 1, 1) if total > 1 else 1.0
+                grad, _meta = gradient_refresh_fn(snapshot(effective), slide_alpha=slide_alpha)
+                grad = grad.to(dt)
+                for st in states:                                      # :1688-1711
+                    g_sub = grad[st["r0"]:st["r1"], :]
+                    if actorder:
+                        g_sub = g_sub[:, st["perm"]]
+                    raw = opt_update(st["opt"], g_sub, i2, grad_lr, grad_clip=grad_clip)
+                    upd, _, _ = apply_regularizer(st, effective(st), raw, i2, grad_lr, grad_reg_strategy,
+                                                  grad_reg_lambda, grad_gate_floor, grad_gate_sharpness,
+                                                  grad_gate_sine_amp, maxq_int, quantizer.sym)
+                    st["pending"] = upd
+                for st in states:                                      # :1828-1834
+                    upd = st.pop("pending")
+                    if upd.numel() > 0:
+                        st["W_sub"][:, i2:] -= upd
 
         for st in states:                                              # :1850-1864
             Q, W_int_sub, Scale_sub = st["Q"], st["W_int"], st["Scale"]
@@ -533,5 +781,6 @@ def reconstruction_error(W, Q, X):
 __all__ = [
     "WeightQuantizerOracle", "GPTQPlusOracle", "FasterquantResult", "SubgroupRecord",
     "safe_beta_from_reference_loss", "hessian_inverse_with_fallback", "gradient_terms",
-    "make_quantizer", "run_linear", "reconstruction_error",
+    "make_quantizer", "run_linear", "reconstruction_error", "kfac_curvature_diag",
+    "make_opt_state", "opt_update", "apply_regularizer", "gate_quant_maps", "nearest_quant_grid",
 ]

@@ -51,6 +51,27 @@ class GoldenCase:
         return torch.from_numpy(np.array(a))
 
 
+def quadratic_refresh(X, W0, G0):
+    """Deterministic stand-in for a layer backward (``gradient_refresh_fn``), shared by the
+    golden-vector script, the oracle tests and the GPU tests: the gradient of
+    0.5 tr((W - W0) A (W - W0)^T) + <G0, W> with A = X^T X / n, scaled by (1 + slide_alpha) / 2
+    when the caller passes ``slide_alpha`` (block_gd).  Computed in float64, returned float32."""
+    Xf = torch.as_tensor(X).double().reshape(-1, torch.as_tensor(X).shape[-1])
+    A = (Xf.T @ Xf) / Xf.shape[0]
+    W0 = torch.as_tensor(W0).double()
+    G0 = torch.as_tensor(G0).double()
+
+    def fn(weight_snapshot, slide_alpha=None):
+        dev = weight_snapshot.device
+        D = weight_snapshot.double() - W0.to(dev)
+        grad = D @ A.to(dev) + G0.to(dev)
+        if slide_alpha is not None:
+            grad = grad * (0.5 + 0.5 * float(slide_alpha))
+        loss = float(0.5 * (D * (D @ A.to(dev))).sum())
+        return grad.float(), {"mean_refresh_loss": loss, "slide_alpha": slide_alpha}
+    return fn
+
+
 class GoldenSet:
     def __init__(self, cases, beta):
         self.cases = cases

@@ -27,12 +27,14 @@ import torch
 
 HERE = Path(__file__).resolve().parent
 OUT = HERE / "golden_cases.npz"
+sys.path.insert(0, str(HERE))
+from fixtures import quadratic_refresh  # noqa: E402  (data helper, no reference code)
 
 # Case table.  R rows, C columns, G groups, N samples x T tokens, bits/sym, groupsize,
 # act_order, blocksize, atomic, alpha/ref_loss, special input shaping.
 CASES = [
     dict(name="g1_sym4_perchan_act", R=32, C=128, G=1, N=8, T=32, bits=4, sym=True, gs=-1, act=True, B=32, atomic=False, alpha=0.0, ref_loss=0.0),
-    dict(name="g4_asym4_perchan_act_gplus", R=64, C=64, G=4, N=8, T=16, bits=4, sym=False, gs=-1, act=True, B=16, atomic=False, alpha=0.05, ref_loss=1e6, gscale=1.0),
+    dict(name="g4_asym4_perchan_act_gplus", R=64, C=64, G=4, N=8, T=16, bits=4, sym=False, gs=-1, act=True, B=16, atomic=False, alpha=0.05, ref_loss=100.0, gscale=0.1),
     dict(name="g2_sym3_static_groups_act", R=32, C=64, G=2, N=8, T=16, bits=3, sym=True, gs=16, act=True, B=16, atomic=False, alpha=0.0, ref_loss=0.0),
     dict(name="g1_sym4_dynamic_groups", R=32, C=64, G=1, N=8, T=16, bits=4, sym=True, gs=16, act=False, B=16, atomic=False, alpha=0.0, ref_loss=0.0),
     dict(name="g4_sym4_atomic_perchan_act", R=64, C=64, G=4, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=True, alpha=0.0, ref_loss=0.0),
@@ -45,9 +47,22 @@ CASES = [
     dict(name="g2_sym4_mse_perchan_act", R=32, C=64, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=False, alpha=0.0, ref_loss=0.0, mse=True),
     dict(name="g2_asym3_mse_static_groups", R=32, C=64, G=2, N=8, T=16, bits=3, sym=False, gs=16, act=True, B=16, atomic=False, alpha=0.0, ref_loss=0.0, mse=True),
     dict(name="g1_sym4_mse_dynamic_atomic", R=32, C=48, G=1, N=8, T=16, bits=4, sym=True, gs=16, act=False, B=16, atomic=True, alpha=0.0, ref_loss=0.0, mse=True),
-    dict(name="g2_sym4_surrogate_block_gplus", R=32, C=64, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=False, alpha=0.05, ref_loss=1e6, gscale=1.0, mode="surrogate_block"),
-    dict(name="g2_asym4_surrogate_online_gplus", R=32, C=64, G=2, N=8, T=16, bits=4, sym=False, gs=16, act=True, B=16, atomic=False, alpha=0.05, ref_loss=1e6, gscale=1.0, mode="surrogate_online"),
-    dict(name="g2_sym4_surrogate_online_atomic", R=32, C=48, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=True, alpha=0.05, ref_loss=1e6, gscale=1.0, mode="surrogate_online"),
+    dict(name="g2_sym4_surrogate_block_gplus", R=32, C=64, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=False, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="surrogate_block"),
+    dict(name="g2_asym4_surrogate_online_gplus", R=32, C=64, G=2, N=8, T=16, bits=4, sym=False, gs=16, act=True, B=16, atomic=False, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="surrogate_online"),
+    dict(name="g2_sym4_surrogate_online_atomic", R=32, C=48, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=True, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="surrogate_online"),
+    # block_gd / block_backward with a deterministic quadratic refresh (fixtures.quadratic_refresh)
+    dict(name="g2_sym4_block_gd_sgd", R=32, C=64, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=False, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="block_gd",
+         fq=dict(grad_optimizer="sgd", grad_lr=8e-3, grad_reg_strategy="none", second_order_scale=1.0, grad_clip=1.0)),
+    dict(name="g2_asym4_block_gd_adam_l2", R=32, C=64, G=2, N=8, T=16, bits=4, sym=False, gs=-1, act=True, B=16, atomic=False, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="block_gd",
+         fq=dict(grad_optimizer="adam", grad_lr=4e-3, grad_reg_strategy="l2", grad_reg_lambda=0.5, second_order_scale=0.9, grad_clip=0.5, slide_refresh_start=1, slide_refresh_block_total=6)),
+    dict(name="g2_sym4_block_gd_hadam_hessian", R=32, C=64, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=False, B=16, atomic=False, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="block_gd",
+         fq=dict(grad_optimizer="h_adam", grad_lr=4e-3, grad_reg_strategy="hessian", grad_reg_lambda=0.1, curvature_damping=0.1, grad_clip=1.0)),
+    dict(name="g2_sym4_block_gd_adam_gateopt_static", R=32, C=64, G=2, N=8, T=16, bits=4, sym=True, gs=16, act=True, B=16, atomic=False, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="block_gd",
+         fq=dict(grad_optimizer="adam", grad_lr=4e-3, grad_reg_strategy="quant_error_gate_optimized", grad_gate_floor=0.2, grad_gate_sharpness=2.0, grad_gate_sine_amp=0.001, grad_clip=1.0)),
+    dict(name="g2_asym4_block_gd_sgd_gate_atomic", R=32, C=48, G=2, N=8, T=16, bits=4, sym=False, gs=-1, act=True, B=16, atomic=True, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="block_gd",
+         fq=dict(grad_optimizer="sgd", grad_lr=8e-3, grad_reg_strategy="quant_error_gate", grad_gate_floor=0.1, grad_gate_sharpness=1.0, second_order_scale=0.8, grad_clip=1.0)),
+    dict(name="g2_sym4_block_backward", R=32, C=64, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=False, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="block_backward"),
+    dict(name="g2_asym4_block_backward_dyn_atomic", R=32, C=48, G=2, N=8, T=16, bits=4, sym=False, gs=16, act=False, B=16, atomic=True, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="block_backward"),
 ]
 
 
@@ -90,6 +105,9 @@ class _Capture:
     def save_block(self, *a, **k):
         return None
 
+    def record_loss(self, *a, **k):
+        return None
+
 
 def _upper(a):
     """Row-major upper triangle (incl. diagonal) of a square matrix: H, Hinv_init are exactly
@@ -124,10 +142,14 @@ def run_case(gpu, qu, case, seed):
     H = g.H.clone()
     act = g.act_square.clone()
     cap = _Capture()
+    extra = dict(case.get("fq", {}))
+    if case.get("mode") in ("block_gd", "block_backward"):
+        extra["gradient_refresh_fn"] = quadratic_refresh(X, W, grad)
     g.fasterquant(blocksize=case["B"], percdamp=0.01, groupsize=case["gs"], actorder=case["act"],
                   static_groups=case["act"], enable_gradient_update=True,
                   g_update_mode=case.get("mode", "frozen"),
-                  export_to_et=True, block_atomic_quant=case["atomic"], diagnostic_recorder=cap)
+                  export_to_et=True, block_atomic_quant=case["atomic"], diagnostic_recorder=cap,
+                  **extra)
     out = {
         "X": X, "W": W, "s": s, "grad": grad,
         "H_upper": np.stack([_upper(h) for h in H.numpy()]), "act_square": act.numpy(),

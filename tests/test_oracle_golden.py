@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer, safe_beta_from_reference_loss
-from tests.golden.fixtures import GoldenSet
+from tests.golden.fixtures import GoldenSet, quadratic_refresh
 
 CASES = GoldenSet.load().cases
 
@@ -26,9 +26,12 @@ def _run(case, inject_H=False):
     if inject_H:
         g.H = case.H().clone()
         g.act_square = case.t("act_square").clone()
+    extra = dict(m.get("fq", {}))
+    if m.get("mode") in ("block_gd", "block_backward"):
+        extra["gradient_refresh_fn"] = quadratic_refresh(case.t("X"), W, case.t("grad"))
     res = g.fasterquant(blocksize=m["B"], percdamp=0.01, groupsize=m["gs"], actorder=m["act"],
                         static_groups=m["act"], block_atomic_quant=m["atomic"],
-                        g_update_mode=m.get("mode", "frozen"))
+                        g_update_mode=m.get("mode", "frozen"), **extra)
     return g, res
 
 
@@ -71,13 +74,21 @@ def test_golden_cover_the_branches():
     assert any(not m["sym"] for m in metas)                                         # asym quirk
     assert any(m["C"] % m["B"] for m in metas)                                      # ragged last block
     assert sum(bool(m.get("mse")) for m in metas) >= 3                              # clip search
-    assert {m.get("mode") for m in metas} >= {"surrogate_block", "surrogate_online"}
+    assert {m.get("mode") for m in metas} >= {"surrogate_block", "surrogate_online", "block_gd",
+                                              "block_backward"}
+    fq = [m.get("fq", {}) for m in metas]
+    assert {f.get("grad_optimizer") for f in fq} >= {"sgd", "adam", "h_adam"}
+    assert {f.get("grad_reg_strategy") for f in fq} >= {"none", "l2", "hessian", "quant_error_gate",
+                                                        "quant_error_gate_optimized"}
     assert "g1_sym4_indefinite_identity" in names
     ident = GoldenSet.load().by_name("g1_sym4_indefinite_identity")
     assert bool(ident.arrays["sub0_identity_fallback"])
     gp = GoldenSet.load().by_name("g4_asym4_perchan_act_gplus")
     b = np.concatenate([gp.arrays[f"sub{s}_beta"] for s in range(4)])
-    assert b.min() > 0.05 and b.max() < 1.0                # non-trivial first-order term
+    assert b.min() > 0 and b.max() < 0.1                   # small, non-zero first-order term
+    big = GoldenSet.load().by_name("g2_sym4_atomic_static_gplus")
+    b = np.concatenate([big.arrays[f"sub{s}_beta"] for s in range(2)])
+    assert b.max() > 0.9                                   # the ratio clamp near beta = 1
 
 
 def test_safe_beta_vectors(golden):
