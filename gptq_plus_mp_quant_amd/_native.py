@@ -17,9 +17,14 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "gptqplus_hip.h"
 RQ_OK, RQ_EINVAL, RQ_EHIP, RQ_ENOTSUP = 0, -1, -2, -3
 RQ_F16, RQ_BF16, RQ_F32 = 0, 1, 2
 RQ_QMODE_CHANNEL, RQ_QMODE_STATIC, RQ_QMODE_DYNAMIC = 0, 1, 2
-RQ_GMODE_FROZEN, RQ_GMODE_SURROGATE_BLOCK, RQ_GMODE_SURROGATE_ONLINE = 0, 1, 2
-GMODES = {"frozen": RQ_GMODE_FROZEN, "surrogate_block": RQ_GMODE_SURROGATE_BLOCK,
-          "surrogate_online": RQ_GMODE_SURROGATE_ONLINE}
+RQ_GMODE_FROZEN, RQ_GMODE_SURROGATE_BLOCK, RQ_GMODE_SURROGATE_ONLINE, RQ_GMODE_BLOCK_GD = 0, 1, 2, 3
+# g_update_mode -> (kernel mode of the in-block loop, kernel mode of the trailing update);
+# gptq_plus_utils.py:1190 (inner) and :1500 (outer)
+GMODES = {"frozen": (RQ_GMODE_FROZEN, RQ_GMODE_FROZEN),
+          "surrogate_block": (RQ_GMODE_SURROGATE_BLOCK, RQ_GMODE_SURROGATE_BLOCK),
+          "surrogate_online": (RQ_GMODE_SURROGATE_ONLINE, RQ_GMODE_SURROGATE_BLOCK),
+          "block_gd": (RQ_GMODE_BLOCK_GD, RQ_GMODE_BLOCK_GD),
+          "block_backward": (RQ_GMODE_SURROGATE_ONLINE, RQ_GMODE_FROZEN)}
 
 _P, _I, _L, _D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_double
 
@@ -37,13 +42,19 @@ SIGNATURES = {
     "rq_chol_hinv_attempt": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
     "rq_gptqplus_terms": (_I, [_P, _L, _P, _P, _I, _I, _D, _D, _I, _P, _P, _P, _L, _P, _P, _P]),
     "rq_quant_block": (_I, [_P, _L, _P, _I, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I,
-                            _I, _P, _P, _P, _I, _P, _L, _P, _P]),
+                            _I, _P, _P, _P, _I, _P, _L, _P, _D, _P]),
     "rq_trailing_update": (_I, [_P, _L, _P, _P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _L, _P,
-                                _P]),
+                                _D, _P]),
     "rq_writeback": (_I, [_P, _I, _I, _P, _I, _P, _P, _P, _I, _P, _I, _L, _P, _P, _P, _P]),
     "rq_packed_words_per_row": (_L, [_I, _I]),
     "rq_pack_codes": (_I, [_P, _I, _I, _L, _P, _I, _P, _L, _P, _P]),
     "rq_unpack_dequant": (_I, [_P, _I, _I, _L, _I, _P, _L, _P, _P, _I, _L, _P, _P]),
+    "rq_current_weight": (_I, [_P, _L, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _L, _P, _L, _P]),
+    "rq_gather_cols": (_I, [_P, _L, _P, _I, _I, _P, _L, _P]),
+    "rq_kfac_curvature": (_I, [_P, _I, _I, _D, _P, _P]),
+    "rq_hessian_reg_gemm": (_I, [_P, _L, _P, _I, _I, _I, _I, _P, _L, _P]),
+    "rq_block_gd_step": (_I, [_P, _L, _I, _I, _I, _I, _P, _L, _P, _I, _I, _D, _D, _P, _P, _P, _I, _D,
+                              _P, _L, _P, _L, _I, _P, _P, _P, _I, _I, _D, _D, _D, _P]),
 }
 
 _lib = None

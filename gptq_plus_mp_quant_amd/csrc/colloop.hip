@@ -27,7 +27,8 @@
 // and GH[:, i2:] -= Z1 Hinv[i1:i2, i2:], 64x64 output tiles, fp32 16x16x4 MFMA, K = count
 // streamed through LDS in slabs of 32.  The Z terms are skipped when Z is identically zero.
 // In the surrogate modes the GH[:, i2:] of the first term is GH + beta_row * (W - W_anchor)
-// (outer refresh "surrogate_block", :1500-1511), the GH update itself is unchanged.
+// (outer refresh "surrogate_block", :1500-1511), the GH update itself is unchanged; in
+// block_gd the whole W update is scaled by second_order_scale (:1546-1549).
 #include "rq_common.h"
 
 namespace {
@@ -67,9 +68,11 @@ struct QBArgs {
   const float* anchor;
   int64_t lda;
   const float* beta;
+  float sos;
 };
 
-// GM: 0 frozen, 1 surrogate_block, 2 surrogate_online
+// GM: 0 frozen, 1 surrogate_block, 2 surrogate_online, 3 frozen with every in-block update
+// scaled by second_order_scale (block_gd, :1344-1349)
 template <int SLOTS, int GM>
 __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
   __shared__ float Hl[QB_MAXB][QB_MAXB];
@@ -88,15 +91,16 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
     Hl[i][j] = (i < count && j < count && j >= i) ? Hs[(int64_t)(i1 + i) * a.C + (i1 + j)] : 0.0f;
   }
 
-  float w[SLOTS], gh[SLOTS], zz[SLOTS], sc[SLOTS], xr[GM ? SLOTS : 1];
-  const float brow = GM ? a.beta[row] : 0.0f;
+  constexpr bool SURR = (GM == 1 || GM == 2);
+  float w[SLOTS], gh[SLOTS], zz[SLOTS], sc[SLOTS], xr[SURR ? SLOTS : 1];
+  const float brow = SURR ? a.beta[row] : 0.0f;
 #pragma unroll
   for (int k = 0; k < SLOTS; ++k) {
     const int col = 4 * k + t;
     const bool in = valid && col < count;
     const int64_t off = (int64_t)row * a.ldw + i1 + col;
     w[k] = in ? a.Wp[off] : 0.0f;
-    if constexpr (GM != 0) {
+    if constexpr (SURR) {
       const float wr = in ? a.anchor[(int64_t)row * a.lda + i1 + col] : 0.0f;
       xr[k] = (GM == 1) ? (w[k] - wr) : wr;
     }
@@ -108,7 +112,7 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
   }
   // gh_eff of slot k from the current registers: gh + beta * (W_cur - W_anchor)
   auto geff = [&](int k) -> float {
-    if constexpr (GM == 0) return gh[k];
+    if constexpr (!SURR) return gh[k];
     const float dw = (GM == 1) ? xr[k] : (w[k] - xr[k]);
     return gh[k] + brow * dw;
   };
@@ -197,7 +201,7 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
           crow[i] = (code != code) ? RQ_CODE_NAN : (int16_t)code;
           erow[i] = e;
         }
-        if constexpr (GM != 0) {
+        if constexpr (SURR) {
           const float zi = use_gh ? quad_lane(zz[0], r) : 0.0f;
 #pragma unroll
           for (int k = 0; k < SLOTS; ++k) {
@@ -216,7 +220,8 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
             if (k < nlive) {
               const float h = Hl[i][4 * (m + k) + t];
               const float upd = e * h;
-              w[k] = w[k] - (upd + gh[k]);
+              if constexpr (GM == 3) w[k] = w[k] - a.sos * (upd + gh[k]);
+              else w[k] = w[k] - (upd + gh[k]);
               gh[k] = gh[k] - zi * h;
             }
           }
@@ -225,7 +230,8 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
           for (int k = 0; k < SLOTS; ++k) {
             if (k < nlive) {
               const float h = Hl[i][4 * (m + k) + t];
-              w[k] = w[k] - (e * h + gh[k]);
+              if constexpr (GM == 3) w[k] = w[k] - a.sos * (e * h + gh[k]);
+              else w[k] = w[k] - (e * h + gh[k]);
             }
           }
         }
@@ -237,13 +243,13 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
       gh[k] = gh[k + 1];
       zz[k] = zz[k + 1];
       sc[k] = sc[k + 1];
-      if constexpr (GM != 0) xr[k] = xr[k + 1];
+      if constexpr (SURR) xr[k] = xr[k + 1];
     }
     w[SLOTS - 1] = 0.0f;
     gh[SLOTS - 1] = 0.0f;
     zz[SLOTS - 1] = 0.0f;
     sc[SLOTS - 1] = 0.0f;
-    if constexpr (GM != 0) xr[SLOTS - 1] = 0.0f;
+    if constexpr (SURR) xr[SLOTS - 1] = 0.0f;
   }
 }
 
@@ -262,6 +268,7 @@ struct TrArgs {
   const float* anchor;
   int64_t lda;
   const float* beta;
+  float sos;
 };
 
 constexpr int TKS = 32;  // K slab
@@ -344,7 +351,7 @@ __global__ __launch_bounds__(256) void k_trailing(TrArgs a) {
         const int c = c0 + wc * 32 + y * 16 + (lane & 15);
         if (rl < a.R_s && c < a.C) {
           const int64_t ow = (int64_t)(rbase + rl) * a.ldw + c;
-          if (a.gmode != 0) {
+          if (a.gmode == 1 || a.gmode == 2) {
             const float wv = a.Wp[ow];
             const float g = use_z ? a.GH[(int64_t)(rbase + rl) * a.ldgh + c] : 0.0f;
             const float dw = wv - a.anchor[(int64_t)(rbase + rl) * a.lda + c];
@@ -356,10 +363,12 @@ __global__ __launch_bounds__(256) void k_trailing(TrArgs a) {
             const int64_t og = (int64_t)(rbase + rl) * a.ldgh + c;
             const float g = a.GH[og];
             const float gupd = cnt * g - acc2[x][y][e];
-            a.Wp[ow] = a.Wp[ow] - (acc1[x][y][e] + gupd);
+            const float tot = acc1[x][y][e] + gupd;
+            a.Wp[ow] = a.Wp[ow] - (a.gmode == 3 ? a.sos * tot : tot);
             a.GH[og] = g - acc3[x][y][e];
           } else {
-            a.Wp[ow] = a.Wp[ow] - acc1[x][y][e];
+            const float tot = acc1[x][y][e];
+            a.Wp[ow] = a.Wp[ow] - (a.gmode == 3 ? a.sos * tot : tot);
           }
         }
       }
@@ -373,10 +382,10 @@ extern "C" int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int
                               float* dyn_scale, int maxq, int sym, int atomic,
                               const int* z_nonzero, int16_t* codes, float* err, int gmode,
                               const float* anchor, int64_t ld_anchor, const float* beta,
-                              void* stream) {
+                              double second_order_scale, void* stream) {
   if (!Wp || !Hinv_all || !GH || !Z || !z_nonzero || !codes || !err) return RQ_EINVAL;
-  if (gmode < 0 || gmode > 2) return RQ_EINVAL;
-  if (gmode != 0 && (!anchor || !beta || ld_anchor < C)) return RQ_EINVAL;
+  if (gmode < 0 || gmode > 3) return RQ_EINVAL;
+  if ((gmode == 1 || gmode == 2) && (!anchor || !beta || ld_anchor < C)) return RQ_EINVAL;
   if (R <= 0 || R_s <= 0 || R % R_s != 0 || C <= 0 || ldw < C || ldgh < C) return RQ_EINVAL;
   if (count <= 0 || count > QB_MAXB || i1 < 0 || i1 + count > C || maxq <= 0) return RQ_EINVAL;
   if (qmode == RQ_QMODE_CHANNEL && !scale) return RQ_EINVAL;
@@ -384,7 +393,8 @@ extern "C" int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int
   if (qmode == RQ_QMODE_DYNAMIC && !dyn_scale) return RQ_EINVAL;
   if (qmode < 0 || qmode > 2) return RQ_EINVAL;
   QBArgs a{Wp, ldw, Hinv_all, C, GH, Z, ldgh, R, R_s, i1, count, qmode, scale, col_group,
-           dyn_scale, (float)maxq, sym, atomic, z_nonzero, codes, err, anchor, ld_anchor, beta};
+           dyn_scale, (float)maxq, sym, atomic, z_nonzero, codes, err, anchor, ld_anchor, beta,
+           (float)second_order_scale};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   dim3 grid((R_s + 63) / 64, R / R_s), block(256);
   const bool small = count <= 32;
@@ -397,9 +407,13 @@ extern "C" int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int
       if (small) hipLaunchKernelGGL((k_quant_block<8, 1>), grid, block, 0, s, a);
       else hipLaunchKernelGGL((k_quant_block<32, 1>), grid, block, 0, s, a);
       break;
-    default:
+    case 2:
       if (small) hipLaunchKernelGGL((k_quant_block<8, 2>), grid, block, 0, s, a);
       else hipLaunchKernelGGL((k_quant_block<32, 2>), grid, block, 0, s, a);
+      break;
+    default:
+      if (small) hipLaunchKernelGGL((k_quant_block<8, 3>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_quant_block<32, 3>), grid, block, 0, s, a);
   }
   RQ_CHECK_LAUNCH();
   return RQ_OK;
@@ -409,16 +423,16 @@ extern "C" int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float
                                   const float* Hinv_all, int C, int R, int R_s, int i1, int count,
                                   const float* err, const int* z_nonzero, int gmode,
                                   const float* anchor, int64_t ld_anchor, const float* beta,
-                                  void* stream) {
+                                  double second_order_scale, void* stream) {
   if (!Wp || !GH || !Z || !Hinv_all || !err || !z_nonzero) return RQ_EINVAL;
-  if (gmode < 0 || gmode > 2) return RQ_EINVAL;
-  if (gmode != 0 && (!anchor || !beta || ld_anchor < C)) return RQ_EINVAL;
+  if (gmode < 0 || gmode > 3) return RQ_EINVAL;
+  if ((gmode == 1 || gmode == 2) && (!anchor || !beta || ld_anchor < C)) return RQ_EINVAL;
   if (R <= 0 || R_s <= 0 || R % R_s != 0 || C <= 0 || ldw < C || ldgh < C) return RQ_EINVAL;
   if (count <= 0 || i1 < 0 || i1 + count > C) return RQ_EINVAL;
   const int i2 = i1 + count;
   if (i2 >= C) return RQ_OK;
   TrArgs a{Wp, ldw, GH, Z, ldgh, Hinv_all, C, R, R_s, i1, count, err, z_nonzero, gmode,
-           anchor, ld_anchor, beta};
+           anchor, ld_anchor, beta, (float)second_order_scale};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   dim3 grid((C - i2 + 63) / 64, (R_s + 63) / 64, R / R_s), block(256);
   hipLaunchKernelGGL(k_trailing, grid, block, 0, s, a);

@@ -9,10 +9,13 @@ the layer dtype, ``int_weight`` / ``scale`` buffers with ``export_to_et``) follo
 reference.  Additionally exposed for inspection: ``perm``, ``invperm``, ``codes`` (natural
 column order), ``subgroup_info`` (damping, retries, identity fallback, beta).
 
-``g_update_mode`` ``"frozen"`` (default), ``"surrogate_block"`` and ``"surrogate_online"`` run
-on the HIP path.  Modes whose work needs a layer backward (``"block_gd"``, ``"block_backward"``,
-``"online"``, ...) and ``diagnostic_recorder`` dumps raise ``NotImplementedError`` rather than
-silently running different arithmetic.
+Every ``g_update_mode`` of the reference runs on the HIP path: ``"frozen"`` (default),
+``"surrogate_block"``, ``"surrogate_online"``, and the refresh modes ``"block_gd"`` /
+``"block_backward"``, whose layer backward is the caller's ``gradient_refresh_fn`` (called
+with the current weight, on the GPU, like the reference does); the optimizer step,
+regularizers and GPTQ+ term refresh around it are kernels.  ``diagnostic_recorder`` dumps and
+``refresh_full_metrics`` statistics raise ``NotImplementedError`` rather than silently
+differing.
 """
 from __future__ import annotations
 
@@ -197,9 +200,14 @@ class GPTQPlus:
         self._validate(grad_reg_strategy, grad_reg_lambda, grad_gate_floor, grad_gate_sharpness,
                        grad_gate_sine_amp)
         if g_update_mode not in nat.GMODES:
-            raise NotImplementedError(f"g_update_mode={g_update_mode!r} needs a layer backward; "
-                                      f"the HIP path runs {sorted(nat.GMODES)}")
-        gmode = nat.GMODES[g_update_mode]
+            raise NotImplementedError(f"g_update_mode={g_update_mode!r} is not one of {sorted(nat.GMODES)}")
+        gm_in, gm_out = nat.GMODES[g_update_mode]
+        block_gd = g_update_mode == "block_gd"
+        block_bw = g_update_mode == "block_backward"
+        if (block_gd or block_bw) and refresh_full_metrics:
+            raise NotImplementedError("refresh_full_metrics statistics are not produced by the HIP path")
+        if block_gd and grad_optimizer not in K.OPTIMIZERS:
+            raise ValueError(f"Unsupported `grad_optimizer={grad_optimizer}`. Expected one of: sgd, adam, h_adam.")
         if diagnostic_recorder is not None:
             raise NotImplementedError("diagnostic_recorder dumps are not produced by the HIP path")
         if not self._finalized:
@@ -238,7 +246,7 @@ class GPTQPlus:
             elif static_groups:
                 qmode = nat.RQ_QMODE_STATIC
                 with _section(rec, "fasterquant.quantizer_build_groups"):
-                    scale_tab, _ = q.params_on(W, groupsize)
+                    scale_tab, zero_tab = q.params_on(W, groupsize)
             else:
                 qmode = nat.RQ_QMODE_DYNAMIC
                 scale_tab = None
@@ -274,8 +282,28 @@ class GPTQPlus:
                     r0 = sub * R_s
                     K.prepare_subgroup(W[r0:], grads[r0:], self.H[sub], perm, Wp[r0:r0 + R_s],
                                        Gs[r0:r0 + R_s], H_work[sub])
-            # surrogate modes refresh GHinv against the weight before the first block
-            anchor = Wp.clone() if gmode != nat.RQ_GMODE_FROZEN else None
+            # surrogate inner loops refresh GHinv against the weight before the first block
+            surrogate = gm_in in (nat.RQ_GMODE_SURROGATE_BLOCK, nat.RQ_GMODE_SURROGATE_ONLINE) or \
+                gm_out in (nat.RQ_GMODE_SURROGATE_BLOCK, nat.RQ_GMODE_SURROGATE_ONLINE)
+            anchor = Wp.clone() if surrogate else None
+            # block_gd state (gptq_plus_utils.py:1024-1151): W_fp for l2 / hessian, the undamped
+            # H_sub for hessian, H-Adam's curvature, the optimizer moments, the gate maps
+            reg = grad_reg_strategy if block_gd else "none"
+            W_fp = Wp.clone() if reg in ("l2", "hessian") else None
+            H_reg = H_work.clone() if reg == "hessian" else None
+            curvature = (K.kfac_curvature(H_work, curvature_damping)
+                         if block_gd and grad_optimizer == "h_adam" else None)
+            exp_avg = torch.zeros((R, C), **f32) if block_gd and grad_optimizer in ("adam", "h_adam") else None
+            exp_avg_sq = torch.zeros((R, C), **f32) if block_gd and grad_optimizer == "adam" else None
+            opt_step = 0
+            gate_q = gate_s = gate_z = None
+            if reg in ("quant_error_gate", "quant_error_gate_optimized"):
+                if qmode == nat.RQ_QMODE_STATIC:
+                    gate_q, gate_s, gate_z = nat.RQ_QMODE_STATIC, scale_tab, zero_tab
+                else:
+                    gate_q = nat.RQ_QMODE_CHANNEL
+                    gate_s = q.scale.reshape(-1).to(**f32).contiguous()
+                    gate_z = q.zero.reshape(-1).to(**f32).contiguous()
             # damped Cholesky chain, subgroups batched through every launch
             with _section(rec, "fasterquant.subgroup.compute_hinv"):
                 if inject_hinv is None:
@@ -312,9 +340,10 @@ class GPTQPlus:
                 damp, fallback, attempts = chain[sub]
                 self.subgroup_info.append(dict(damp_percent=damp, identity_fallback=fallback,
                                                attempts=attempts, beta=beta))
-            del Gs, GH0
+            if not block_bw:
+                del Gs, GH0
             beta_rows = None
-            if gmode != nat.RQ_GMODE_FROZEN:
+            if surrogate:
                 beta_rows = torch.zeros(R, **f32)
                 if beta_mode == 1:
                     for sub, info in enumerate(self.subgroup_info):
@@ -326,6 +355,19 @@ class GPTQPlus:
             err = torch.empty((R, min(blocksize, C)), **f32)
             nblocks = (C + blocksize - 1) // blocksize
             dyn_scale = torch.empty((nblocks, R), **f32) if qmode == nat.RQ_QMODE_DYNAMIC else None
+            n_refresh_total = max(nblocks - 1, 0)
+            sos = float(second_order_scale) if block_gd else 1.0
+
+            def snapshot(i_q):
+                # the caller's layer sees each subgroup's current weight, quantized columns
+                # replaced by Q, in the layer's own column order (:1412-1420, :1578-1588)
+                return K.current_weight(Wp, codes, i_q, qmode, scale_tab, col_group, dyn_scale,
+                                        blocksize, invperm=invperm).reshape(self.layer.weight.shape)
+
+            def refreshed(grad):
+                grad = grad.to(dev).float().reshape(R, C)
+                return grad if grad.is_contiguous() else grad.contiguous()
+
             with _section(rec, "fasterquant.block_loop"):
                 for bidx, i1 in enumerate(range(0, C, blocksize)):
                     i2 = min(i1 + blocksize, C)
@@ -338,14 +380,64 @@ class GPTQPlus:
                         dyn_scale[bidx].copy_(bscale[0])
                         K.quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, nat.RQ_QMODE_CHANNEL,
                                       dyn_scale[bidx], None, None, maxq, sym, atomic, z_any, codes, err,
-                                      gmode, anchor, beta_rows)
+                                      gm_in, anchor, beta_rows, sos)
                     else:
                         K.quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale_tab, col_group,
                                       dyn_scale[bidx] if dyn_scale is not None else None, maxq, sym,
-                                      atomic, z_any, codes, err, gmode, anchor, beta_rows)
+                                      atomic, z_any, codes, err, gm_in, anchor, beta_rows, sos)
+                    if block_bw and enable_gradient_update:
+                        # block_backward (:1408-1448): gradient at the current weight, then
+                        # beta / Z / GHinv recomputed and the anchor moved to the current weight
+                        if gradient_refresh_fn is None:
+                            raise ValueError("`gradient_refresh_fn` must be provided for g_update_mode='block_backward'.")
+                        with _section(rec, "fasterquant.block.true_gradient_refresh"):
+                            grad, meta = gradient_refresh_fn(snapshot(i2))
+                            K.gather_cols(refreshed(grad), perm, out=Gs)
+                            z_flags.zero_()
+                            for sub in range(G):
+                                r0 = sub * R_s
+                                beta = torch.empty(R_s if beta_mode == 1 else 1, **f32)
+                                K.gptqplus_terms(Gs[r0:r0 + R_s], None if Hinit_all is None else Hinit_all[sub],
+                                                 Hinv_all[sub], alpha_eff, float(self.reference_loss),
+                                                 beta_mode, beta, Z[r0:r0 + R_s], GH[r0:r0 + R_s], GH0,
+                                                 z_flags[sub:sub + 1])
+                                if beta_mode == 1 and self.reference_loss > 0:
+                                    beta_rows[r0:r0 + R_s].copy_(beta)
+                            z_any = torch.amax(z_flags).reshape(1).contiguous()
+                            K.current_weight(Wp, codes, i2, qmode, scale_tab, col_group, dyn_scale,
+                                             blocksize, out=anchor)
+                        if block_observer is not None:
+                            block_observer(self._observer_record(i1, i2, blocksize, meta, block_gd=False))
                     if i2 < C:
-                        K.trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_any, gmode,
-                                          anchor, beta_rows)
+                        K.trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_any, gm_out,
+                                          anchor, beta_rows, sos)
+                    if block_gd and enable_gradient_update and i2 < C:
+                        # block_gd (:1572-1834): one optimizer step on the trailing columns
+                        if gradient_refresh_fn is None:
+                            raise ValueError("`gradient_refresh_fn` must be provided for g_update_mode='block_gd'.")
+                        with _section(rec, "fasterquant.block.true_gradient_refresh"):
+                            total = (slide_refresh_block_total if slide_refresh_block_total is not None
+                                     else n_refresh_total)
+                            idx = slide_refresh_start + i1 // blocksize
+                            slide_alpha = 1.0 - idx / max(total - 1, 1) if total > 1 else 1.0
+                            grad, meta = gradient_refresh_fn(snapshot(i2), slide_alpha=slide_alpha)
+                            grad = refreshed(grad)
+                        with _section(rec, "fasterquant.block.outer_update_grad_descent"):
+                            hreg = None
+                            if reg == "hessian":
+                                diff = K.current_weight(Wp, codes, i2, qmode, scale_tab, col_group,
+                                                        dyn_scale, blocksize, sub_ref=W_fp)
+                                hreg = K.hessian_reg_gemm(diff, H_reg, R_s, i2)
+                                del diff
+                            if grad_optimizer != "sgd":
+                                opt_step += 1
+                            K.block_gd_step(Wp, R_s, i2, grad, perm, grad_optimizer, opt_step, grad_lr,
+                                            grad_clip, exp_avg, exp_avg_sq, curvature, reg,
+                                            grad_reg_lambda, W_fp, hreg, gate_q or 0, gate_s, gate_z,
+                                            col_group, maxq, sym, grad_gate_floor, grad_gate_sharpness,
+                                            grad_gate_sine_amp)
+                        if block_observer is not None:
+                            block_observer(self._observer_record(i1, i2, blocksize, meta, block_gd=True))
 
             with _section(rec, "fasterquant.write_layer_weight"):
                 Q = torch.empty((R, C), dtype=W.dtype, device=dev)
@@ -384,6 +476,28 @@ class GPTQPlus:
         if self._codes_perm is None:
             return None
         return self._codes_perm if self.invperm is None else self._codes_perm[:, self.invperm]
+
+    def _observer_record(self, i1, i2, blocksize, meta, block_gd):
+        """The per-block dict the reference hands to ``block_observer`` (:1462-1496,
+        :1784-1817) without the refresh_full_metrics statistics (all None)."""
+        rec = {"block_idx": i1 // blocksize, "col_start": i1, "col_end": i2,
+               "remaining_columns": self.columns - i2}
+        for k in ("remaining_grad_abs_mean", "remaining_grad_clipped_abs_mean", "remaining_grad_mean_row_l2",
+                  "second_order_update_abs_mean", "second_order_update_mean_row_l2",
+                  "second_order_update_abs_max", "second_order_update_abs_q99", "first_order_raw_abs_mean",
+                  "first_order_raw_mean_row_l2", "first_order_update_abs_mean",
+                  "first_order_update_mean_row_l2", "first_order_update_abs_max",
+                  "first_order_update_abs_q99", "regularizer_update_abs_mean",
+                  "regularizer_update_mean_row_l2", "sine_regularizer_update_abs_mean",
+                  "sine_regularizer_update_mean_row_l2"):
+            rec[k] = None
+        keys = ["mean_refresh_loss", "train_mean_refresh_loss", "val_mean_refresh_loss",
+                "refresh_subset_mean_refresh_loss"]
+        if block_gd:
+            keys += ["slide_alpha", "mean_refresh_loss_current", "mean_refresh_loss_next"]
+        for k in keys:
+            rec[k] = None if meta is None else meta.get(k)
+        return rec
 
     @staticmethod
     def _validate(grad_reg_strategy, grad_reg_lambda=0.0, grad_gate_floor=0.1, grad_gate_sharpness=1.0,

@@ -173,7 +173,7 @@ def gptqplus_terms(G_sub, Hinv_init, Hinv, alpha_eff, reference_loss, beta_mode,
 
 
 def _surrogate(gmode, anchor, beta, R, C):
-    if gmode == nat.RQ_GMODE_FROZEN:
+    if gmode not in (nat.RQ_GMODE_SURROGATE_BLOCK, nat.RQ_GMODE_SURROGATE_ONLINE):
         return 0
     if anchor is None or beta is None:
         raise ValueError("surrogate g_update modes need anchor and beta")
@@ -185,7 +185,8 @@ def _surrogate(gmode, anchor, beta, R, C):
 
 
 def quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale, col_group, dyn_scale, maxq, sym,
-                atomic, z_nonzero, codes, err, gmode=nat.RQ_GMODE_FROZEN, anchor=None, beta=None):
+                atomic, z_nonzero, codes, err, gmode=nat.RQ_GMODE_FROZEN, anchor=None, beta=None,
+                second_order_scale=1.0):
     R, C = Wp.shape
     if Hinv_all.shape != (R // R_s, C, C):
         raise ValueError("quant_block: Hinv_all must be [G, C, C]")
@@ -196,11 +197,12 @@ def quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale, col_group, dy
     nat.call("rq_quant_block", nat.ptr(Wp), Wp.stride(0), nat.ptr(Hinv_all), C, nat.ptr(GH), nat.ptr(Z),
              GH.stride(0), R, R_s, int(i1), int(count), int(qmode), nat.ptr(scale), nat.ptr(col_group),
              nat.ptr(dyn_scale), int(maxq), int(bool(sym)), int(bool(atomic)), nat.ptr(z_nonzero),
-             nat.ptr(codes), nat.ptr(err), int(gmode), nat.ptr(anchor), lda, nat.ptr(beta), _stream(Wp))
+             nat.ptr(codes), nat.ptr(err), int(gmode), nat.ptr(anchor), lda, nat.ptr(beta),
+             float(second_order_scale), _stream(Wp))
 
 
 def trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_nonzero, gmode=nat.RQ_GMODE_FROZEN,
-                    anchor=None, beta=None):
+                    anchor=None, beta=None, second_order_scale=1.0):
     R, C = Wp.shape
     lda = _surrogate(gmode, anchor, beta, R, C)
     _cout(Wp, "Wp"), _cout(GH, "GH"), _cout(err, "err")
@@ -208,7 +210,7 @@ def trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_nonzero, gmode=n
         raise ValueError("trailing_update: Hinv_all must be contiguous, Z row-major")
     nat.call("rq_trailing_update", nat.ptr(Wp), Wp.stride(0), nat.ptr(GH), nat.ptr(Z), GH.stride(0),
              nat.ptr(Hinv_all), C, R, R_s, int(i1), int(count), nat.ptr(err), nat.ptr(z_nonzero),
-             int(gmode), nat.ptr(anchor), lda, nat.ptr(beta), _stream(Wp))
+             int(gmode), nat.ptr(anchor), lda, nat.ptr(beta), float(second_order_scale), _stream(Wp))
 
 
 def writeback(codes, invperm, qmode, scale, col_group, dyn_scale, blocksize, q_out, w_int_out=None,
@@ -276,3 +278,91 @@ def unpack_dequant(packed, C, nbits, scales=None, g_idx=None, q_dtype=torch.floa
              R, nat.ptr(g_idx), nat.ptr(q), nat.dtype_code(q_dtype) if q is not None else 0,
              C, nat.ptr(codes), _stream(packed))
     return q, codes
+
+
+# --- refresh g_update modes (block_gd / block_backward) ---------------------------------
+OPTIMIZERS = {"sgd": 0, "adam": 1, "h_adam": 2}
+REGULARIZERS = {"none": 0, "l2": 1, "hessian": 2, "quant_error_gate": 3, "quant_error_gate_optimized": 4}
+
+
+def current_weight(Wp, codes, i_q, qmode, scale, col_group, dyn_scale, blocksize, invperm=None,
+                   sub_ref=None, out=None):
+    """Quantized columns (permuted j < i_q) as fl32(scale * code), the rest from Wp; natural
+    column order when invperm is given; minus sub_ref when given."""
+    R, C = Wp.shape
+    _rowmajor(Wp, "Wp")
+    if codes.shape != (R, C) or codes.dtype != torch.int16 or not codes.is_contiguous():
+        raise ValueError("current_weight: codes must be contiguous int16 [R, C]")
+    if invperm is not None:
+        invperm = _cin(invperm, "invperm", torch.int64)
+    if sub_ref is not None:
+        _rowmajor(sub_ref, "sub_ref")
+    if out is None:
+        out = torch.empty((R, C), dtype=torch.float32, device=Wp.device)
+    _cout(out, "out")
+    nat.call("rq_current_weight", nat.ptr(Wp), Wp.stride(0), nat.ptr(codes), R, C, int(i_q), int(qmode),
+             nat.ptr(scale), nat.ptr(col_group), nat.ptr(dyn_scale), int(blocksize), nat.ptr(invperm),
+             nat.ptr(sub_ref), sub_ref.stride(0) if sub_ref is not None else 0, nat.ptr(out),
+             out.stride(0), _stream(Wp))
+    return out
+
+
+def gather_cols(src, perm, out=None):
+    R, C = src.shape
+    src = _cin(src, "src")
+    if perm is not None:
+        perm = _cin(perm, "perm", torch.int64)
+    if out is None:
+        out = torch.empty((R, C), dtype=torch.float32, device=src.device)
+    _cout(out, "out")
+    nat.call("rq_gather_cols", nat.ptr(src), src.stride(0), nat.ptr(perm), R, C, nat.ptr(out),
+             out.stride(0), _stream(src))
+    return out
+
+
+def kfac_curvature(H_work, damping):
+    G, C, _ = H_work.shape
+    H_work = _cin(H_work, "H_work")
+    curv = torch.empty((G, C), dtype=torch.float32, device=H_work.device)
+    nat.call("rq_kfac_curvature", nat.ptr(H_work), C, G, float(damping), nat.ptr(curv), _stream(H_work))
+    return curv
+
+
+def hessian_reg_gemm(diff, H_reg, R_s, i2):
+    R, C = diff.shape
+    diff = _cin(diff, "diff")
+    H_reg = _cin(H_reg, "H_reg")
+    if H_reg.shape != (R // R_s, C, C):
+        raise ValueError("hessian_reg_gemm: H_reg must be [G, C, C]")
+    out = torch.empty((R, C - i2), dtype=torch.float32, device=diff.device)
+    nat.call("rq_hessian_reg_gemm", nat.ptr(diff), diff.stride(0), nat.ptr(H_reg), C, R, R_s, int(i2),
+             nat.ptr(out), out.stride(0), _stream(diff))
+    return out
+
+
+def block_gd_step(Wp, R_s, i2, grad, perm, optimizer, step, lr, grad_clip, exp_avg=None,
+                  exp_avg_sq=None, curvature=None, reg="none", reg_lambda=0.0, w_fp=None, hreg=None,
+                  gate_qmode=0, gate_scale=None, gate_zero=None, col_group=None, maxq=0, sym=True,
+                  gate_floor=0.1, gate_sharpness=1.0, sine_amp=0.0):
+    R, C = Wp.shape
+    _cout(Wp, "Wp")
+    grad = _cin(grad, "grad")
+    if grad.shape != (R, C):
+        raise ValueError("block_gd_step: grad must be [R, C]")
+    if perm is not None:
+        perm = _cin(perm, "perm", torch.int64)
+    for t, n in ((exp_avg, "exp_avg"), (exp_avg_sq, "exp_avg_sq"), (w_fp, "w_fp")):
+        if t is not None and (t.shape != (R, C) or not t.is_contiguous() or t.dtype != torch.float32):
+            raise ValueError(f"block_gd_step: {n} must be contiguous float32 [R, C]")
+    if curvature is not None and (curvature.shape != (R // R_s, C) or not curvature.is_contiguous()):
+        raise ValueError("block_gd_step: curvature must be contiguous [G, C]")
+    if hreg is not None and (hreg.shape != (R, C - i2) or hreg.stride(1) != 1):
+        raise ValueError("block_gd_step: hreg must be row-major [R, C - i2]")
+    nat.call("rq_block_gd_step", nat.ptr(Wp), Wp.stride(0), R, R_s, C, int(i2), nat.ptr(grad),
+             grad.stride(0), nat.ptr(perm), OPTIMIZERS[optimizer], int(step), float(lr),
+             float(grad_clip if grad_clip is not None else 0.0), nat.ptr(exp_avg), nat.ptr(exp_avg_sq),
+             nat.ptr(curvature), REGULARIZERS[reg], float(reg_lambda), nat.ptr(w_fp),
+             w_fp.stride(0) if w_fp is not None else 0, nat.ptr(hreg),
+             hreg.stride(0) if hreg is not None else 0, int(gate_qmode), nat.ptr(gate_scale),
+             nat.ptr(gate_zero), nat.ptr(col_group), int(maxq), int(bool(sym)), float(gate_floor),
+             float(gate_sharpness), float(sine_amp), _stream(Wp))

@@ -31,6 +31,7 @@ extern "C" {
 #define RQ_GMODE_FROZEN 0           /* gh_eff = GH                                          */
 #define RQ_GMODE_SURROGATE_BLOCK 1  /* gh_eff = GH + beta_r (W_block_start - anchor)          */
 #define RQ_GMODE_SURROGATE_ONLINE 2 /* gh_eff = GH + beta_r (W_live - anchor), per column      */
+#define RQ_GMODE_BLOCK_GD 3         /* gh_eff = GH, W updates scaled by second_order_scale      */
 
 /* quantizer modes of rq_quant_block / rq_writeback */
 #define RQ_QMODE_CHANNEL 0 /* one scale per row            (gptq_plus_utils.py:1008-1020) */
@@ -133,24 +134,28 @@ int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* Hinv_init, c
  * gmode (RQ_GMODE_*): in the surrogate modes the GHinv term is refreshed before every
  * column (:1190-1199, :1360-1367) from anchor (the permuted weight before the first block,
  * [R, C] row stride ld_anchor) and beta[r] (fp32, one per row of all subgroups); both may be
- * NULL for RQ_GMODE_FROZEN. */
+ * NULL for RQ_GMODE_FROZEN / RQ_GMODE_BLOCK_GD.  RQ_GMODE_BLOCK_GD scales every in-block
+ * weight update by second_order_scale (:1344-1349; ignored by the other modes).
+ * block_backward's inner loop is RQ_GMODE_SURROGATE_ONLINE (:1190). */
 int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int C, const float* GH,
                    const float* Z, int64_t ldgh, int R, int R_s, int i1, int count, int qmode,
                    const float* scale, const int32_t* col_group, float* dyn_scale, int maxq,
                    int sym, int atomic, const int* z_nonzero, int16_t* codes, float* err,
                    int gmode, const float* anchor, int64_t ld_anchor, const float* beta,
-                   void* stream);
+                   double second_order_scale, void* stream);
 
 /* Outer (trailing) update after a block -- gptq_plus_utils.py:1500-1570:
  * Wp[:, i2:] -= err Hinv[i1:i2, i2:] + (count GH[:, i2:] - (Z[:, i1:i2] D) Hinv[i1:i2, i2:]),
  * GH[:, i2:] -= Z[:, i1:i2] Hinv[i1:i2, i2:], D = [count-1, ..., 0], per subgroup; the Z
- * terms are skipped when *z_nonzero == 0.  fp32 MFMA.  For gmode != RQ_GMODE_FROZEN the GH
- * of the first term is GH + beta[r] (Wp - anchor) (outer refresh "surrogate_block",
- * :1500-1511); the GH update is unchanged. */
+ * terms are skipped when *z_nonzero == 0.  fp32 MFMA.  For the surrogate gmodes the GH of
+ * the first term is GH + beta[r] (Wp - anchor) (outer refresh "surrogate_block",
+ * :1500-1511); the GH update is unchanged.  RQ_GMODE_BLOCK_GD scales the whole W update by
+ * second_order_scale (:1546-1549); block_backward's outer update is RQ_GMODE_FROZEN. */
 int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float* Z, int64_t ldgh,
                        const float* Hinv_all, int C, int R, int R_s, int i1, int count,
                        const float* err, const int* z_nonzero, int gmode, const float* anchor,
-                       int64_t ld_anchor, const float* beta, void* stream);
+                       int64_t ld_anchor, const float* beta, double second_order_scale,
+                       void* stream);
 
 /* Un-permute and write back -- gptq_plus_utils.py:1850-1875:
  * natural column c of row r takes permuted column j = invperm[c] (identity if NULL):
@@ -186,6 +191,54 @@ int rq_pack_codes(const int16_t* codes, int R, int C, int64_t ldc, const int64_t
 int rq_unpack_dequant(const uint32_t* packed, int R, int C, int64_t ldp, int nbits,
                       const float* scales, int64_t lds, const int32_t* g_idx, void* q_out,
                       int q_dtype, int64_t ldq, int16_t* codes_out, void* stream);
+
+/* The refresh g_update modes (block_gd, block_backward): the caller's layer backward runs
+ * between blocks on the current weight; these entry points prepare its input and apply its
+ * output.
+ *
+ * Current effective weight -- gptq_plus_utils.py:1389-1396, 1412-1420, 1578-1588, 1690-1692:
+ * value(r, j) = j < i_q ? fl32(scale(r, j) * code[r, j]) : Wp[r, j] (permuted column j, scale
+ * by qmode as in rq_writeback); out[r, c] = value(r, invperm ? invperm[c] : c)
+ * - (sub_ref ? sub_ref[r, c] : 0).  invperm un-permutes (the snapshot handed to the caller);
+ * without it the output stays in the permuted order (block_backward's new anchor, or with
+ * sub_ref = W_fp the hessian regularizer's difference, :766). */
+int rq_current_weight(const float* Wp, int64_t ldw, const int16_t* codes, int R, int C, int i_q,
+                      int qmode, const float* scale, const int32_t* col_group,
+                      const float* dyn_scale, int blocksize, const int64_t* invperm,
+                      const float* sub_ref, int64_t ld_ref, float* out, int64_t ldo, void* stream);
+
+/* dst[r, j] = src[r, perm[j]] (perm NULL = copy): the refreshed gradient in act_order's
+ * column order (:1430-1432, 1688-1690). */
+int rq_gather_cols(const float* src, int64_t lds, const int64_t* perm, int R, int C, float* dst,
+                   int64_t ldd, void* stream);
+
+/* H-Adam curvature -- build_kfac_curvature_diag :4601-4640 as called at :1144-1151: for each
+ * of nsub matrices H_work[s] (dead-fixed, permuted, undamped), curv[s][j] =
+ * max(d_j, 0) / max(mean(max(d, 0)), 1e-12) + damping (damping added only when > 0). */
+int rq_kfac_curvature(const float* H_work, int C, int nsub, double damping, float* curv,
+                      void* stream);
+
+/* Hessian regularizer product -- :765-768: out[s] = diff[s] (R_s x C, row stride ldd) times
+ * H_reg[s][:, i2:] (H_reg [G, C, C]), out [R, C - i2] row stride ldo.  fp32 MFMA. */
+int rq_hessian_reg_gemm(const float* diff, int64_t ldd, const float* H_reg, int C, int R, int R_s,
+                        int i2, float* out, int64_t ldo, void* stream);
+
+/* One block_gd optimizer step on the trailing permuted columns [i2, C) of all rows --
+ * _compute_grad_optimizer_update :616-655 + _apply_first_order_regularizer :730-796 +
+ * W_sub[:, i2:] -= update :1828-1834.  grad: natural order [R, C] (row stride ldg), read
+ * through perm.  optimizer 0 sgd, 1 adam (exp_avg, exp_avg_sq [R, C]), 2 h_adam (exp_avg,
+ * curvature [G, C]); step = the optimizer's step count after its increment; betas 0.9 /
+ * 0.999, eps 1e-8.  reg_strategy 0 none, 1 l2 (w_fp [R, C]), 2 hessian (hreg from
+ * rq_hessian_reg_gemm), 3 quant_error_gate, 4 quant_error_gate_optimized (gate maps:
+ * gate_qmode RQ_QMODE_CHANNEL -> gate_scale[r] / gate_zero[r], RQ_QMODE_STATIC ->
+ * [col_group[j] * R + r]). */
+int rq_block_gd_step(float* Wp, int64_t ldw, int R, int R_s, int C, int i2, const float* grad,
+                     int64_t ldg, const int64_t* perm, int optimizer, int step, double lr,
+                     double grad_clip, float* exp_avg, float* exp_avg_sq, const float* curvature,
+                     int reg_strategy, double reg_lambda, const float* w_fp, int64_t ld_fp,
+                     const float* hreg, int64_t ld_hreg, int gate_qmode, const float* gate_scale,
+                     const float* gate_zero, const int32_t* col_group, int maxq, int sym,
+                     double gate_floor, double gate_sharpness, double sine_amp, void* stream);
 
 #ifdef __cplusplus
 }

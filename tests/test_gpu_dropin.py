@@ -15,7 +15,7 @@ import torch
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer, reconstruction_error
 from tests._util import code_flips, rel_fro, synth
-from tests.golden.fixtures import GoldenSet
+from tests.golden.fixtures import GoldenSet, quadratic_refresh
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -30,6 +30,16 @@ def _gpu_obj(W, s, grad, G, alpha, ref_loss, bits, sym, mse=False):
     g.quantizer = WeightQuantizer()
     g.quantizer.configure(bits, perchannel=True, sym=sym, mse=mse)
     return g, layer
+
+
+def _mode_kwargs(meta, X, W, grad):
+    """g_update_mode and its extra fasterquant arguments; the refresh modes get the shared
+    deterministic quadratic refresh as their layer backward."""
+    kw = dict(meta.get("fq", {}))
+    kw["g_update_mode"] = meta.get("mode", "frozen")
+    if kw["g_update_mode"] in ("block_gd", "block_backward"):
+        kw["gradient_refresh_fn"] = quadratic_refresh(X, W, grad)
+    return kw
 
 
 def _accumulate(g, X, bsz):
@@ -64,7 +74,7 @@ def test_golden_fasterquant_same_inverse(case):
         inject["perm"] = case.sub(0, "perm")
     g.fasterquant(blocksize=m["B"], percdamp=0.01, groupsize=m["gs"], actorder=m["act"],
                   static_groups=m["act"], block_atomic_quant=m["atomic"], export_to_et=True,
-                  inject=inject, keep_hinv=True, g_update_mode=m.get("mode", "frozen"))
+                  inject=inject, keep_hinv=True, **_mode_kwargs(m, case.t("X"), case.t("W"), case.t("grad")))
     torch.cuda.synchronize()
     assert torch.equal(g.quantizer.scale.cpu(), case.t("qscale"))
     for s, info in enumerate(g.subgroup_info):
@@ -95,7 +105,7 @@ def test_golden_fasterquant_own_chain(case):
     _accumulate(g, case.t("X"), 4)
     g.fasterquant(blocksize=m["B"], percdamp=0.01, groupsize=m["gs"], actorder=m["act"],
                   static_groups=m["act"], block_atomic_quant=m["atomic"], export_to_et=True, keep_hinv=True,
-                  g_update_mode=m.get("mode", "frozen"))
+                  **_mode_kwargs(m, case.t("X"), case.t("W"), case.t("grad")))
     torch.cuda.synchronize()
     for s, info in enumerate(g.subgroup_info):
         assert info["identity_fallback"] == bool(case.arrays[f"sub{s}_identity_fallback"])
@@ -128,6 +138,13 @@ CFGS = [
     dict(name="g2_sym4_surrogate_block_static", R=256, C=512, G=2, bits=4, sym=True, gs=128, act=True, B=128, atomic=False, alpha=0.05, ref_loss=3e4, gscale=1e-1, mode="surrogate_block"),
     dict(name="g4_asym4_surrogate_online", R=256, C=512, G=4, bits=4, sym=False, gs=-1, act=True, B=128, atomic=False, alpha=0.05, ref_loss=3e4, gscale=1e-1, mode="surrogate_online"),
     dict(name="g2_sym4_surrogate_online_dyn_atomic", R=128, C=384, G=2, bits=4, sym=True, gs=64, act=False, B=64, atomic=True, alpha=0.05, ref_loss=3e4, gscale=1e-1, mode="surrogate_online"),
+    dict(name="g2_sym4_block_gd_adam_l2", R=256, C=512, G=2, bits=4, sym=True, gs=-1, act=True, B=128, atomic=False, alpha=0.05, ref_loss=100.0, gscale=1e-1, mode="block_gd",
+         fq=dict(grad_optimizer="adam", grad_lr=2e-3, grad_reg_strategy="l2", grad_reg_lambda=0.5, second_order_scale=0.9)),
+    dict(name="g2_asym4_block_gd_hadam_hessian_static", R=128, C=384, G=2, bits=4, sym=False, gs=128, act=True, B=128, atomic=False, alpha=0.05, ref_loss=100.0, gscale=1e-1, mode="block_gd",
+         fq=dict(grad_optimizer="h_adam", grad_lr=2e-3, grad_reg_strategy="hessian", grad_reg_lambda=0.1)),
+    dict(name="g2_sym4_block_gd_sgd_gateopt_static", R=128, C=384, G=2, bits=4, sym=True, gs=128, act=True, B=128, atomic=False, alpha=0.05, ref_loss=100.0, gscale=1e-1, mode="block_gd",
+         fq=dict(grad_optimizer="sgd", grad_lr=4e-3, grad_reg_strategy="quant_error_gate_optimized", grad_gate_floor=0.2, grad_gate_sharpness=2.0, grad_gate_sine_amp=0.001)),
+    dict(name="g4_sym4_block_backward", R=256, C=512, G=4, bits=4, sym=True, gs=-1, act=True, B=128, atomic=False, alpha=0.05, ref_loss=100.0, gscale=1e-1, mode="block_backward"),
 ]
 
 
@@ -144,7 +161,7 @@ def test_dropin_vs_oracle(cfg):
     o.finalize_hessian()
     fq = dict(blocksize=cfg["B"], percdamp=0.01, groupsize=cfg["gs"], actorder=cfg["act"],
               static_groups=cfg["act"], block_atomic_quant=cfg["atomic"],
-              g_update_mode=cfg.get("mode", "frozen"))
+              **_mode_kwargs(cfg, X, W, grad))
     res = o.fasterquant(stable_ties=True, **fq)
 
     g, layer = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False))
@@ -220,7 +237,18 @@ def test_dropin_errors_and_side_effects():
     with pytest.raises(ValueError):
         g.fasterquant(blocksize=64, groupsize=32, actorder=False, static_groups=False)
     with pytest.raises(NotImplementedError):
-        g.fasterquant(g_update_mode="block_gd")
+        g.fasterquant(g_update_mode="online")                       # not a mode of the reference
+    with pytest.raises(NotImplementedError):
+        g.fasterquant(blocksize=64, g_update_mode="block_gd", refresh_full_metrics=True)
+    # a refresh mode without its layer backward fails at the first refresh, like the
+    # reference (:1573-1574, :1409-1410), before the layer weight is touched
+    w_before = layer.weight.data.clone()
+    for mode in ("block_gd", "block_backward"):
+        with pytest.raises(ValueError, match="gradient_refresh_fn"):
+            g.fasterquant(blocksize=64, g_update_mode=mode)
+    assert torch.equal(layer.weight.data, w_before)
+    with pytest.raises(ValueError, match="grad_optimizer"):
+        g.fasterquant(blocksize=64, g_update_mode="block_gd", grad_optimizer="lion")
     g.fasterquant(blocksize=64, actorder=True, static_groups=True, export_to_et=True)
     assert layer.weight.dtype == torch.float16 and layer.int_weight.dtype == torch.float32
     assert layer.scale.shape == (64, 128)

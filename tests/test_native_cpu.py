@@ -18,7 +18,7 @@ def _lib():
 def test_header_symbols_are_exported_and_bound():
     lib = _lib()
     syms = nat.header_symbols()
-    assert len(syms) >= 17
+    assert len(syms) >= 22
     for name in syms:
         assert hasattr(lib, name), f"{name} not exported"
         assert name in nat.SIGNATURES, f"{name} has no ctypes binding"
@@ -42,17 +42,28 @@ def test_argument_validation_needs_no_device():
     assert lib.rq_chol_hinv_attempt(null, 4, 1, damp, null, null, null, null, null) == nat.RQ_EINVAL
     assert lib.rq_chol_hinv_attempt(null, 4, 65, damp, null, null, null, null, null) == nat.RQ_EINVAL
     assert lib.rq_quant_block(null, 4, null, 4, null, null, 4, 4, 4, 0, 4, 0, null, null, null, 7, 1,
-                              0, null, null, null, 0, null, 4, null, null) == nat.RQ_EINVAL
+                              0, null, null, null, 0, null, 4, null, 1.0, null) == nat.RQ_EINVAL
     assert lib.rq_trailing_update(null, 4, null, null, 4, null, 4, 4, 4, 0, 4, null, null, 0, null, 4,
-                                  null, null) == nat.RQ_EINVAL
+                                  null, 1.0, null) == nat.RQ_EINVAL
     # a surrogate g_update mode without its anchor / beta is refused before any launch
     fake = ctypes.c_void_p(16)
     assert lib.rq_quant_block(fake, 4, fake, 4, fake, fake, 4, 4, 4, 0, 4, 0, fake, null, null, 7, 1,
-                              0, fake, fake, fake, 1, null, 4, null, null) == nat.RQ_EINVAL
+                              0, fake, fake, fake, 1, null, 4, null, 1.0, null) == nat.RQ_EINVAL
     assert lib.rq_trailing_update(fake, 4, fake, fake, 4, fake, 4, 4, 4, 0, 2, fake, fake, 2, fake, 4,
-                                  null, null) == nat.RQ_EINVAL
-    assert lib.rq_trailing_update(fake, 4, fake, fake, 4, fake, 4, 4, 4, 0, 2, fake, fake, 3, fake, 4,
-                                  fake, null) == nat.RQ_EINVAL
+                                  null, 1.0, null) == nat.RQ_EINVAL
+    assert lib.rq_trailing_update(fake, 4, fake, fake, 4, fake, 4, 4, 4, 0, 2, fake, fake, 4, fake, 4,
+                                  fake, 1.0, null) == nat.RQ_EINVAL
+    # refresh-mode entry points: missing optimizer state / regularizer inputs are refused
+    D = ctypes.c_double
+    assert lib.rq_block_gd_step(fake, 8, 4, 4, 8, 4, fake, 8, null, 1, 1, D(1e-3), D(1.0), null, null,
+                                null, 0, D(0.0), null, 0, null, 0, 0, null, null, null, 7, 1, D(0.1),
+                                D(1.0), D(0.0), null) == nat.RQ_EINVAL
+    assert lib.rq_block_gd_step(fake, 8, 4, 4, 8, 4, fake, 8, null, 0, 0, D(1e-3), D(1.0), null, null,
+                                null, 2, D(0.1), null, 0, null, 0, 0, null, null, null, 7, 1, D(0.1),
+                                D(1.0), D(0.0), null) == nat.RQ_EINVAL
+    assert lib.rq_current_weight(fake, 8, fake, 4, 8, 4, 1, fake, null, null, 8, null, null, 0, fake, 8,
+                                 null) == nat.RQ_EINVAL
+    assert lib.rq_hessian_reg_gemm(fake, 8, fake, 8, 4, 3, 0, fake, 8, null) == nat.RQ_EINVAL
     assert lib.rq_writeback(null, 4, 4, null, 0, null, null, null, 4, null, 0, 4, null, null, null,
                             null) == nat.RQ_EINVAL
     # packed export: word count, and refusal of bad widths / short rows before any launch
