@@ -31,8 +31,9 @@ _P, _I, _L, _D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_double
 # name -> (restype, argtypes); mirrors include/gptqplus_hip.h
 SIGNATURES = {
     "rq_version": (_I, []),
-    "rq_hessian_accum": (_I, [_P, _I, _L, _L, _I, _P, _L, _I, _P, _P, _P]),
-    "rq_hessian_accum_multi": (_I, [_P, _I, _L, _L, _I, _I, _P, _P, _P, _P, _P]),
+    "rq_hessian_accum": (_I, [_P, _I, _L, _L, _I, _P, _L, _I, _P, _P, _P, _L, _P]),
+    "rq_hessian_workspace_bytes": (_L, [_L, _I, _I]),
+    "rq_hessian_accum_multi": (_I, [_P, _I, _L, _L, _I, _I, _P, _P, _P, _P, _P, _L, _P]),
     "rq_hessian_finalize": (_I, [_P, _P, _I, _I, _D, _D, _D, _P, _P]),
     "rq_find_params": (_I, [_P, _I, _I, _I, _L, _I, _I, _I, _P, _P, _P]),
     "rq_find_params_mse": (_I, [_P, _I, _I, _I, _L, _I, _I, _I, _D, _I, _D, _P, _P, _P]),

@@ -11,8 +11,14 @@
 // into the B operand as it is written (the reference's `weighted` = fl32(x * s) is never
 // materialised).  Products run on v_mfma_f32_32x32x2f32 with fp32 accumulation; each 64x64
 // quarter of the tile belongs to one wave (2x2 MFMA blocks of 32x32).  The diagonal tiles of
-// group 0 also accumulate act_square = sum_t x^2.  No atomics: every output element has
-// exactly one owner, so results are bitwise reproducible run to run.
+// group 0 also accumulate act_square = sum_t x^2.
+//
+// Tail balancing: the (tile, target) items of a launch run in rounds of (CUs x 3) workgroups;
+// when the last round would be partly empty, its items are split along the tokens into S
+// slices (chosen so that the split work fills whole rounds).  A slice writes its partial
+// tile to a caller-provided workspace; the last slice to finish (an integer counter per item)
+// adds the S partials to H in slice order.  Every output element therefore still has one
+// fixed summation order, and results are bitwise reproducible run to run.
 #include "rq_common.h"
 
 namespace {
@@ -100,12 +106,17 @@ __device__ __forceinline__ void upper_tile(int t, int nt, int& ti, int& tj) {
   tj = row + rem;
 }
 
+// Partial tile of one token slice: 64 accumulator floats per thread, stored e-major so each
+// store instruction of the workgroup writes 1 KB contiguously, then 128 act_square partials.
+constexpr int HPART = HT * HT + HT;
+
 template <typename TX, bool EDGE>
 __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t ntok, int64_t ldx,
                                              int C, const float* __restrict__ sal, int64_t ld_sal,
                                              float* __restrict__ Hg,
                                              float* __restrict__ act_sq, int I0, int J0, bool diag,
-                                             bool want_act, float (*As)[HS], float (*Bs)[HS]) {
+                                             bool want_act, float (*As)[HS], float (*Bs)[HS],
+                                             int64_t sbeg, int64_t send, float* __restrict__ part) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -125,14 +136,13 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
   for (int e = 0; e < 16; ++e) actp[e] = 0.0f;
 
   RawSide<TX> ra, rb;
-  const int64_t nslab = (ntok + HKC - 1) / HKC;
-  load_side<TX, EDGE>(X, ntok, ldx, C, sk, I0 + sc, ra);
-  if (!diag) load_side<TX, EDGE>(X, ntok, ldx, C, sk, J0 + sc, rb);
+  load_side<TX, EDGE>(X, ntok, ldx, C, sbeg * HKC + sk, I0 + sc, ra);
+  if (!diag) load_side<TX, EDGE>(X, ntok, ldx, C, sbeg * HKC + sk, J0 + sc, rb);
 
   const int fi = lane & 31;           // fragment column within a 32-block
   const int fk = (lane >> 5) * 16;    // this lane's first token in the slab
 
-  for (int64_t sidx = 0; sidx < nslab; ++sidx) {
+  for (int64_t sidx = sbeg; sidx < send; ++sidx) {
     const int64_t t = sidx * HKC + sk;
     const float s = (t < ntok) ? sal[t * ld_sal] : 0.0f;
     __syncthreads();                  // previous slab fully consumed
@@ -145,7 +155,7 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
       if (want_act) actp[e] += xa * xa;
     }
     __syncthreads();
-    if (sidx + 1 < nslab) {           // next slab in flight while this one is multiplied
+    if (sidx + 1 < send) {            // next slab in flight while this one is multiplied
       load_side<TX, EDGE>(X, ntok, ldx, C, t + HKC, I0 + sc, ra);
       if (!diag) load_side<TX, EDGE>(X, ntok, ldx, C, t + HKC, J0 + sc, rb);
     }
@@ -174,6 +184,28 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
         acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[q], b1[q], acc[1][1], 0, 0, 0);
       }
     }
+  }
+
+  if (part) {
+    // token slice: hand the partial tile to the workspace (summed into H by the last slice)
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) part[(bi * 32 + bj * 16 + e) * HTHREADS + tid] = acc[bi][bj][e];
+    if (want_act) {
+      __syncthreads();
+#pragma unroll
+      for (int e = 0; e < 16; ++e) As[sc + e][sk] = actp[e];
+      __syncthreads();
+      if (tid < HT) {
+        float sum = 0.0f;
+        for (int q = 0; q < HKC; ++q) sum += As[tid][q];
+        part[HT * HT + tid] = sum;
+      }
+    }
+    return;
   }
 
   // H[g][I0 + i][J0 + j] += acc   (32x32 block layout: i = 8*(e/4) + 4*(lane/32) + e%4, j = lane%32)
@@ -216,21 +248,72 @@ struct HTargets {
   float* act[HMAXT];         // act_square output (one target per module) or nullptr
 };
 
+// The last slice of a split item adds the S partials (in slice order) to H and act_square.
+__device__ __forceinline__ void reduce_slices(const float* __restrict__ part0, int S, float* __restrict__ Hg,
+                                              float* __restrict__ act_sq, int I0, int J0, int C,
+                                              bool want_act) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll 4
+      for (int e = 0; e < 16; ++e) {
+        const int slot = (bi * 32 + bj * 16 + e) * HTHREADS + tid;
+        // partials of other workgroups: coherent (L1-bypassing) loads
+        float sum = __hip_atomic_load(part0 + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int q = 1; q < S; ++q)
+          sum += __hip_atomic_load(part0 + (int64_t)q * HPART + slot, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        const int i = I0 + wr * 64 + bi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int j = J0 + wc * 64 + bj * 32 + (lane & 31);
+        if (i < C && j < C) {
+          float* p = Hg + (int64_t)i * C + j;
+          *p = *p + sum;
+        }
+      }
+  if (want_act && tid < HT && I0 + tid < C) {
+    float sum = __hip_atomic_load(part0 + HT * HT + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int q = 1; q < S; ++q)
+      sum += __hip_atomic_load(part0 + (int64_t)q * HPART + HT * HT + tid, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    act_sq[I0 + tid] += sum;
+  }
+}
+
 template <typename TX>
 __global__ __launch_bounds__(HTHREADS, 3) void k_hessian_accum(
     const TX* __restrict__ X, int64_t ntok, int64_t ldx, int C, HTargets tg, int ntarg, int nt,
-    int ntiles, bool vec_ok) {
+    int ntiles, bool vec_ok, int full, int S, float* __restrict__ ws, int* __restrict__ cnt) {
   __shared__ __attribute__((aligned(16))) float As[HT][HS];
   __shared__ __attribute__((aligned(16))) float Bs[HT][HS];
+  __shared__ int last_slice;
 
-  // XCD-aware order: consecutive hardware workgroup ids land on different XCDs (round
-  // robin over 8); give each XCD a contiguous run of logical ids so neighbouring tiles,
-  // which share X column strips, share that XCD's L2.  Targets of one tile are adjacent.
+  // Blocks [0, full) run whole items.  XCD-aware order: consecutive hardware workgroup ids
+  // land on different XCDs (round robin over 8); give each XCD a contiguous run of logical
+  // ids so neighbouring tiles, which share X column strips, share that XCD's L2.  Targets of
+  // one tile are adjacent.  Blocks [full, full + S * (total - full)) are the token slices of
+  // the remaining items, slice-minor.
   const int total = ntiles * ntarg;
   const int b = blockIdx.x;
-  const int per = total / 8, rem8 = total % 8;
-  const int xcd = b % 8, idx = b / 8;
-  const int logical = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
+  const int64_t nslab = (ntok + HKC - 1) / HKC;
+  int logical, slice = -1;
+  int64_t sbeg = 0, send = nslab;
+  if (b < full) {
+    const int per = full / 8, rem8 = full % 8;
+    const int xcd = b % 8, idx = b / 8;
+    logical = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
+  } else {
+    const int tb = b - full;
+    logical = full + tb / S;
+    slice = tb % S;
+    sbeg = nslab * slice / S;
+    send = nslab * (slice + 1) / S;
+  }
+  if (logical >= total) return;
   const int g = logical % ntarg;
   int ti, tj;
   upper_tile_blocked(logical / ntarg, nt, ti, tj);
@@ -240,12 +323,28 @@ __global__ __launch_bounds__(HTHREADS, 3) void k_hessian_accum(
   const bool want_act = diag && (act_sq != nullptr);
   float* Hg = tg.H[g];
   const bool interior = vec_ok && (J0 + HT <= C);   // I0 <= J0
+  float* part0 = (slice >= 0) ? ws + (int64_t)(logical - full) * S * HPART : nullptr;
+  float* part = part0 ? part0 + (int64_t)slice * HPART : nullptr;
   if (interior)
     hessian_tile<TX, false>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], Hg, act_sq, I0, J0, diag,
-                            want_act, As, Bs);
+                            want_act, As, Bs, sbeg, send, part);
   else
     hessian_tile<TX, true>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], Hg, act_sq, I0, J0, diag,
-                           want_act, As, Bs);
+                           want_act, As, Bs, sbeg, send, part);
+  if (!part) return;
+  // publish this slice, and let the last of the S slices sum them in slice order
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int* c = cnt + (logical - full);
+    const int prev = atomicAdd(c, 1);
+    last_slice = (prev == S - 1);
+    if (last_slice) atomicExch(c, 0);              // leave the counter zero for the next call
+  }
+  __syncthreads();
+  if (!last_slice) return;
+  __threadfence();
+  reduce_slices(part0, S, Hg, act_sq, I0, J0, C, want_act);
 }
 
 }  // namespace
@@ -311,33 +410,108 @@ extern "C" int rq_version(void) { return 100; }
 
 namespace {
 
+// Concurrent workgroups of k_hessian_accum on the current device (CUs x occupancy).
+int hessian_slots() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] > 0) return cache[dev];
+  int cus = 0, occ = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_hessian_accum<__half>, HTHREADS, 0) !=
+      hipSuccess)
+    return 0;
+  cache[dev] = cus * occ;
+  return cache[dev];
+}
+
+// Items of the last, partly filled round and the slice count that fills rounds best
+// (the finishing time of the tail in rounds is ceil(tail * S / slots) / S).
+void tail_split(int64_t total, int64_t nslab, int slots, int* tail, int* S) {
+  *tail = 0;
+  *S = 1;
+  if (slots <= 0 || total <= 0) return;
+  const int64_t t = total % slots;
+  if (t == 0) return;
+  double best = 1.0;
+  int bestS = 1;
+  for (int cand = 2; cand <= 8; cand *= 2) {
+    if (nslab < 4 * cand) break;                  // keep >= 4 slabs per slice
+    const double rounds = (double)((t * cand + slots - 1) / slots) / cand;
+    if (rounds < best - 0.05) {
+      best = rounds;
+      bestS = cand;
+    }
+  }
+  if (bestS > 1) {
+    *tail = (int)t;
+    *S = bestS;
+  }
+}
+
+// Workspace layout: one int counter per possible tail item at a fixed place (the start), so
+// launches with different tails can share one workspace, then the partial tiles.
+int64_t hessian_cnt_bytes(int slots) { return (((int64_t)slots * 4 + 255) / 256) * 256; }
+
+int64_t hessian_ws_bytes(int64_t tail, int S, int slots) {
+  if (tail <= 0) return 0;
+  return hessian_cnt_bytes(slots) + tail * S * (int64_t)HPART * 4;
+}
+
 int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, const HTargets& tg,
-                   int ntarg, hipStream_t s) {
+                   int ntarg, void* ws, int64_t ws_bytes, hipStream_t s) {
   const int nt = (C + HT - 1) / HT;
   const int ntiles = nt * (nt + 1) / 2;
   const int64_t total = (int64_t)ntiles * ntarg;
-  if (total > 0x7fffffff) return RQ_EINVAL;
+  if (total > 0x7fffffff / 8) return RQ_EINVAL;
   const size_t esz = (x_dtype == RQ_F32) ? 4 : 2;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (((size_t)ldx * esz) % 16 == 0);
-  dim3 grid((unsigned)total), block(HTHREADS);
+  int tail = 0, S = 1;
+  const int slots = hessian_slots();
+  if (ws) tail_split(total, (ntok + HKC - 1) / HKC, slots, &tail, &S);
+  const int64_t need = hessian_ws_bytes(tail, S, slots);
+  if (tail > 0 && (ws_bytes < need || (reinterpret_cast<uintptr_t>(ws) & 255))) {
+    tail = 0;                                     // no room: whole items only
+    S = 1;
+  }
+  const int full = (int)(total - tail);
+  int* cnt = tail > 0 ? reinterpret_cast<int*>(ws) : nullptr;
+  float* wsf = tail > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + hessian_cnt_bytes(slots))
+                        : nullptr;
+  dim3 grid((unsigned)(full + (int64_t)tail * S)), block(HTHREADS);
   if (x_dtype == RQ_F16)
     hipLaunchKernelGGL(k_hessian_accum<__half>, grid, block, 0, s, (const __half*)x, ntok, ldx, C, tg,
-                       ntarg, nt, ntiles, vec_ok);
+                       ntarg, nt, ntiles, vec_ok, full, S, wsf, cnt);
   else if (x_dtype == RQ_BF16)
     hipLaunchKernelGGL(k_hessian_accum<__hip_bfloat16>, grid, block, 0, s, (const __hip_bfloat16*)x,
-                       ntok, ldx, C, tg, ntarg, nt, ntiles, vec_ok);
+                       ntok, ldx, C, tg, ntarg, nt, ntiles, vec_ok, full, S, wsf, cnt);
   else
     hipLaunchKernelGGL(k_hessian_accum<float>, grid, block, 0, s, (const float*)x, ntok, ldx, C, tg,
-                       ntarg, nt, ntiles, vec_ok);
+                       ntarg, nt, ntiles, vec_ok, full, S, wsf, cnt);
   RQ_CHECK_LAUNCH();
   return RQ_OK;
 }
 
 }  // namespace
 
+extern "C" int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets) {
+  if (ntok < 0 || C <= 0 || ntargets <= 0) return RQ_EINVAL;
+  const int nt = (C + HT - 1) / HT;
+  int64_t need = 0;
+  for (int t0 = 0; t0 < ntargets; t0 += HMAXT) {   // per launch of at most 32 targets
+    const int n = (ntargets - t0 < HMAXT) ? (ntargets - t0) : HMAXT;
+    int tail = 0, S = 1;
+    const int slots = hessian_slots();
+    tail_split((int64_t)nt * (nt + 1) / 2 * n, (ntok + HKC - 1) / HKC, slots, &tail, &S);
+    const int64_t b = hessian_ws_bytes(tail, S, slots);
+    if (b > need) need = b;
+  }
+  return need;
+}
+
 extern "C" int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
                                 const float* sal, int64_t ld_sal, int G, float* H, float* act_sq,
-                                void* stream) {
+                                void* workspace, int64_t workspace_bytes, void* stream) {
   if (!x || !sal || !H || C <= 0 || G <= 0 || ntok < 0 || ldx < C || ld_sal < G) return RQ_EINVAL;
   if (x_dtype != RQ_F16 && x_dtype != RQ_BF16 && x_dtype != RQ_F32) return RQ_EINVAL;
   if (ntok == 0) return RQ_OK;
@@ -351,7 +525,8 @@ extern "C" int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_
       tg.H[t] = H + (int64_t)g * C * C;
       tg.act[t] = (g == 0) ? act_sq : nullptr;
     }
-    const int rc = launch_hessian(x, x_dtype, ntok, ldx, C, tg, n, reinterpret_cast<hipStream_t>(stream));
+    const int rc = launch_hessian(x, x_dtype, ntok, ldx, C, tg, n, workspace, workspace_bytes,
+                                  reinterpret_cast<hipStream_t>(stream));
     if (rc) return rc;
   }
   return RQ_OK;
@@ -359,7 +534,8 @@ extern "C" int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_
 
 extern "C" int rq_hessian_accum_multi(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
                                       int ntargets, const float* const* sal, const int64_t* ld_sal,
-                                      float* const* H, float* const* act_sq, void* stream) {
+                                      float* const* H, float* const* act_sq, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
   if (!x || !sal || !ld_sal || !H || C <= 0 || ntargets <= 0 || ntargets > HMAXT || ntok < 0 ||
       ldx < C)
     return RQ_EINVAL;
@@ -373,7 +549,8 @@ extern "C" int rq_hessian_accum_multi(const void* x, int x_dtype, int64_t ntok, 
     tg.act[t] = act_sq ? act_sq[t] : nullptr;
   }
   if (ntok == 0) return RQ_OK;
-  return launch_hessian(x, x_dtype, ntok, ldx, C, tg, ntargets, reinterpret_cast<hipStream_t>(stream));
+  return launch_hessian(x, x_dtype, ntok, ldx, C, tg, ntargets, workspace, workspace_bytes,
+                        reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int rq_hessian_finalize(float* H, float* act_sq, int G, int C, double h_div,

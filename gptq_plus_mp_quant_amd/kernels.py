@@ -46,6 +46,24 @@ def _cout(t, name, dtype=_f32):
     return t
 
 
+_HWS = {}
+
+
+def hessian_workspace(x, ntargets):
+    """Per-device, grow-only workspace for the Hessian launches' tail slices (zero-filled on
+    allocation; the kernels leave their counters zero).  Launches are stream-ordered, so the
+    calls of one process on one device share it."""
+    need = int(nat.load().rq_hessian_workspace_bytes(x.shape[0], x.shape[1], int(ntargets)))
+    if need <= 0:
+        return None, 0
+    key = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    ws = _HWS.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=x.device)
+        _HWS[key] = ws
+    return ws, ws.numel()
+
+
 def hessian_accum(x, sal, H, act_sq):
     """H[g] += X^T diag(sal[:, g]) X (upper tiles), act_sq += sum x^2.  x: [n, C], sal: [n, G]."""
     _rowmajor(x, "x")
@@ -55,8 +73,9 @@ def hessian_accum(x, sal, H, act_sq):
         raise ValueError("hessian_accum: shape mismatch")
     if not (H.is_contiguous() and H.dtype == _f32 and act_sq.is_contiguous() and act_sq.numel() == C):
         raise ValueError("hessian_accum: H / act_sq must be contiguous fp32")
+    ws, nbytes = hessian_workspace(x, G)
     nat.call("rq_hessian_accum", nat.ptr(x), nat.dtype_code(x.dtype), x.shape[0], x.stride(0), C,
-             nat.ptr(sal), sal.stride(0), G, nat.ptr(H), nat.ptr(act_sq), _stream(x))
+             nat.ptr(sal), sal.stride(0), G, nat.ptr(H), nat.ptr(act_sq), nat.ptr(ws), nbytes, _stream(x))
 
 
 def hessian_accum_multi(x, sals, Hs, acts):
@@ -79,8 +98,10 @@ def hessian_accum_multi(x, sals, Hs, acts):
         raise ValueError("hessian_accum_multi: at most 32 (module, group) targets per launch")
     nt = len(H_p)
     P = ctypes.c_void_p
+    ws, nbytes = hessian_workspace(x, nt)
     nat.call("rq_hessian_accum_multi", nat.ptr(x), nat.dtype_code(x.dtype), n, x.stride(0), C, nt,
-             (P * nt)(*sal_p), (ctypes.c_int64 * nt)(*ld), (P * nt)(*H_p), (P * nt)(*act_p), _stream(x))
+             (P * nt)(*sal_p), (ctypes.c_int64 * nt)(*ld), (P * nt)(*H_p), (P * nt)(*act_p), nat.ptr(ws),
+             nbytes, _stream(x))
 
 
 def hessian_finalize(H, act_sq, h_div, sal_scale, seq_len, nonfinite=None):

@@ -45,10 +45,16 @@ int rq_version(void);
  * H[g] (C x C, fp32, g < G) += X^T diag(sal[:, g]) X over `ntok` tokens, upper-triangle
  * 128x128 tiles only (the lower triangle is filled by rq_hessian_finalize);
  * act_sq[c] += sum_t x[t,c]^2.  X is [ntok, C] (row stride ldx) of type x_dtype,
- * sal is [ntok, G] fp32 (row stride ld_sal).  fp32 MFMA, no atomics, deterministic. */
+ * sal is [ntok, G] fp32 (row stride ld_sal).  fp32 MFMA, deterministic (bitwise
+ * reproducible).  workspace (optional, device, 256-byte aligned, zero-filled when first
+ * allocated; the library leaves it reusable): with at least rq_hessian_workspace_bytes
+ * bytes the items of a partly filled last round are split along the tokens so the launch
+ * ends with full rounds; NULL runs whole items only.  Calls that overlap in time on one
+ * device need separate workspaces. */
+int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets);
 int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
                      const float* sal, int64_t ld_sal, int G, float* H, float* act_sq,
-                     void* stream);
+                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Cross-module fused accumulation: the add_batch of several GPTQPlus objects whose modules read
  * the same input (q/k/v, gate/up; their forward hooks receive the same tensor,
@@ -58,7 +64,8 @@ int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int 
  * act_sq are HOST arrays of device pointers / strides. */
 int rq_hessian_accum_multi(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
                            int ntargets, const float* const* sal, const int64_t* ld_sal,
-                           float* const* H, float* const* act_sq, void* stream);
+                           float* const* H, float* const* act_sq, void* workspace, int64_t workspace_bytes,
+                           void* stream);
 
 /* GPTQPlus.finalize_hessian -- gptq_plus_utils.py:859-908 (world size 1).
  * H = sym(upper(H)) / h_div [/ sal_scale if != 1]; non-finite entries -> 0 and counted

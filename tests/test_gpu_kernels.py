@@ -70,6 +70,36 @@ def test_hessian_is_deterministic_and_scaled():
     assert rel_fro(outs[0][0], o.H) <= 1e-5
 
 
+@pytest.mark.parametrize("C,G", [(1000, 3), (384, 2)])   # larger first: the second reuses its workspace
+def test_hessian_tail_slices_match_whole_items(C, G):
+    """The split of a partly filled last round into token slices (workspace given) changes
+    only the summation order: same result as whole items to fp32 rounding, and bitwise
+    reproducible from call to call."""
+    r = rng(40 + C)
+    n = 4096
+    x = torch.from_numpy(r.standard_normal((n, C), dtype=np.float32)).half().to(DEV)
+    sal = torch.from_numpy(r.lognormal(size=(n, G)).astype(np.float32)).to(DEV)
+    ws, nbytes = K.hessian_workspace(x, G)
+    assert nbytes > 0                                  # this shape has a partial last round
+    outs = []
+    for use_ws in (False, True, True):
+        H = torch.zeros(G, C, C, device=DEV)
+        act = torch.zeros(C, device=DEV)
+        nat.call("rq_hessian_accum", nat.ptr(x), nat.RQ_F16, n, C, C, nat.ptr(sal), G, G, nat.ptr(H),
+                 nat.ptr(act), nat.ptr(ws) if use_ws else None, nbytes if use_ws else 0,
+                 nat.stream_of(x.device))
+        outs.append((H, act))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[1][0], outs[2][0]) and torch.equal(outs[1][1], outs[2][1])
+    iu = torch.triu_indices(C, C)
+    for g in range(G):
+        a, b = outs[0][0][g][iu[0], iu[1]], outs[1][0][g][iu[0], iu[1]]
+        assert rel_fro(b, a) <= 1e-5      # the Hessian bar: fp32 sums of 4096 terms, other order
+    assert rel_fro(outs[1][1], outs[0][1]) <= 1e-5
+    # (the second split call reuses the workspace: equal results show the per-item counters
+    # were left zero by the first)
+
+
 def test_finalize_sanitises_nonfinite():
     H = torch.eye(70, device=DEV).repeat(2, 1, 1)
     H[1, 3, 40] = float("nan")
