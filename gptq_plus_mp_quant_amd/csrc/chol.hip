@@ -5,18 +5,21 @@
 // The reference computes chol(H) -> cholesky_inverse -> chol(H^-1, upper) in fp32.  Here the
 // upper factor U of H^-1 (U^T U = H^-1) is obtained with ONE factorisation: with P the
 // index-reversal permutation and L L^T = P H P,  U = P L^-1 P.  The factorisation and the
-// inverse L^-1 run together in one right-looking blocked pass in fp64 (64-wide panels):
-//   per panel k:  L_kk = chol(A_kk) and T = L_kk^-1 in LDS (one workgroup),
+// inverse L^-1 run together in one right-looking blocked pass in fp64 (64-wide blocks
+// inside 256-wide panels):
+//   per block k:  L_kk = chol(A_kk) and T = L_kk^-1 in LDS (one workgroup),
 //                 L_ik = A_ik T^T,  X_k = T B_k  (row block k of L^-1),
 //                 A_ij -= L_ik L_jk^T (lower tiles),  B_i -= L_ik X_k   (fp64 MFMA GEMMs),
-// where B accumulates I - sum_m L_im X_m.  H^-1 itself (Hinv_init) is P (L^-T L^-1) P and is
+// where B accumulates I - sum_m L_im X_m; the updates of the trailing matrix and of the
+// rows of B below a panel are applied once per panel (rank 256) instead of once per block.  H^-1 itself (Hinv_init) is P (L^-T L^-1) P and is
 // only formed when asked for.  A non-positive or non-finite pivot, or a non-finite result,
 // raises the device `info` flag; later kernels of the same attempt exit early.
 #include "gemm_tile.h"
 
 namespace {
 
-constexpr int NB = 64;
+constexpr int NB = 64;     // diagonal block (factored and inverted in LDS)
+constexpr int NBW = 256;   // outer panel width
 
 __global__ void k_fill_i32(int* p, int v) { *p = v; }
 __global__ void k_fill_f32(float* p, float v) { *p = v; }
@@ -283,40 +286,64 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
     g.sC = ws;
     return g;
   };
-  for (int k = 0; k < C; k += NB) {
-    const int kb = (C - k < NB) ? (C - k) : NB;
-    const int rest = C - k - kb;
-    hipLaunchKernelGGL(k_chol_diag, dim3(nb), blk, 0, s, A, C, k, kb, Tbuf, Linv, ws, info);
-    RQ_CHECK_LAUNCH();
-    int rc;
-    if (rest > 0) {
-      // L_ik = A_ik T^T  (in place, rows below the panel)
-      GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)(k + kb) * C + k, C, Tbuf, NB,
-                                                     A + (int64_t)(k + kb) * C + k, C, rest, kb, kb,
-                                                     1.0, EPI_STORE));
-      if ((rc = launch_gemm(g, false, true, s, nb))) return rc;
+  // Two-level blocking: outer panels of NBW columns, factored in NB-wide steps whose updates
+  // stay inside the panel; the trailing matrix (and the rows of L^-1 below the panel) get
+  // one rank-NBW update per panel, so the big updates read and write the trailing matrix
+  // NBW / NB times less often.
+  for (int k = 0; k < C; k += NBW) {
+    const int kw = (C - k < NBW) ? (C - k) : NBW;
+    const int pe = k + kw;                               // panel end
+    for (int j = k; j < pe; j += NB) {
+      const int jb = (pe - j < NB) ? (pe - j) : NB;
+      const int below = C - j - jb;                      // rows below this block (whole matrix)
+      const int pend = pe - j - jb;                      // panel columns right of this block
+      hipLaunchKernelGGL(k_chol_diag, dim3(nb), blk, 0, s, A, C, j, jb, Tbuf, Linv, ws, info);
+      RQ_CHECK_LAUNCH();
+      int rc;
+      if (below > 0) {
+        // L_ij = A_ij T^T  (in place, every row below the block)
+        GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)(j + jb) * C + j, C, Tbuf, NB,
+                                                       A + (int64_t)(j + jb) * C + j, C, below, jb,
+                                                       jb, 1.0, EPI_STORE));
+        if ((rc = launch_gemm(g, false, true, s, nb))) return rc;
+      }
+      if (j > 0) {
+        // X_j[:, 0:j] = T B_j[:, 0:j]  (in place, row block j of L^-1)
+        GemmArgs<double> g = batched(gemm_args<double>(Tbuf, NB, Linv + (int64_t)j * C, C,
+                                                       Linv + (int64_t)j * C, C, jb, j, jb, 1.0,
+                                                       EPI_STORE));
+        if ((rc = launch_gemm(g, false, false, s, nb))) return rc;
+      }
+      if (pend > 0) {
+        // inside the panel: A[j+jb:, j+jb:pe] -= L[j+jb:, j] L[j+jb:pe, j]^T (lower tiles)
+        GemmArgs<double> h = batched(gemm_args<double>(A + (int64_t)(j + jb) * C + j, C,
+                                                       A + (int64_t)(j + jb) * C + j, C,
+                                                       A + (int64_t)(j + jb) * C + (j + jb), C, below,
+                                                       pend, jb, -1.0, EPI_ACCUM));
+        h.lower_only = 1;
+        if ((rc = launch_gemm(h, false, true, s, nb))) return rc;
+        // and the panel rows of L^-1: B[j+jb:pe, 0:j+jb] -= L[j+jb:pe, j] X_j
+        GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)(j + jb) * C + j, C,
+                                                       Linv + (int64_t)j * C, C,
+                                                       Linv + (int64_t)(j + jb) * C, C, pend, j + jb,
+                                                       jb, -1.0, EPI_ACCUM));
+        if ((rc = launch_gemm(g, false, false, s, nb))) return rc;
+      }
     }
-    if (k > 0) {
-      // X_k[:, 0:k] = T B_k[:, 0:k]  (in place, row block k of L^-1)
-      GemmArgs<double> g = batched(gemm_args<double>(Tbuf, NB, Linv + (int64_t)k * C, C,
-                                                     Linv + (int64_t)k * C, C, kb, k, kb, 1.0,
-                                                     EPI_STORE));
-      if ((rc = launch_gemm(g, false, false, s, nb))) return rc;
-    }
+    const int rest = C - pe;
     if (rest > 0) {
-      // B_i[:, 0:k+kb] -= L_ik X_k
-      GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)(k + kb) * C + k, C,
-                                                     Linv + (int64_t)k * C, C,
-                                                     Linv + (int64_t)(k + kb) * C, C, rest, k + kb,
-                                                     kb, -1.0, EPI_ACCUM));
-      if ((rc = launch_gemm(g, false, false, s, nb))) return rc;
-      // A_ij -= L_ik L_jk^T on the lower tiles of the trailing matrix
-      GemmArgs<double> h = batched(gemm_args<double>(A + (int64_t)(k + kb) * C + k, C,
-                                                     A + (int64_t)(k + kb) * C + k, C,
-                                                     A + (int64_t)(k + kb) * C + (k + kb), C, rest,
-                                                     rest, kb, -1.0, EPI_ACCUM));
+      int rc;
+      // trailing matrix: A[pe:, pe:] -= L[pe:, k:pe] L[pe:, k:pe]^T (lower tiles, K = kw)
+      GemmArgs<double> h = batched(gemm_args<double>(A + (int64_t)pe * C + k, C, A + (int64_t)pe * C + k,
+                                                     C, A + (int64_t)pe * C + pe, C, rest, rest, kw,
+                                                     -1.0, EPI_ACCUM));
       h.lower_only = 1;
       if ((rc = launch_gemm(h, false, true, s, nb))) return rc;
+      // rows of L^-1 below the panel: B[pe:, 0:pe] -= L[pe:, k:pe] X[k:pe, 0:pe]
+      GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)pe * C + k, C, Linv + (int64_t)k * C,
+                                                     C, Linv + (int64_t)pe * C, C, rest, pe, kw, -1.0,
+                                                     EPI_ACCUM));
+      if ((rc = launch_gemm(g, false, false, s, nb))) return rc;
     }
   }
   hipLaunchKernelGGL(k_output_upper, gcol, blk, 0, s, Linv, C, Hinv, ws, info);
