@@ -4,8 +4,9 @@
 //   A(i, k) = TA ? A[k*lda + i] : A[i*lda + k]        B(k, j) = TB ? B[j*ldb + k] : B[k*ldb + j]
 //
 // 256 threads = 4 waves in a 2x2 arrangement, 32x32 per wave as 2x2 blocks of the 16x16x4
-// MFMA (v_mfma_f32_16x16x4f32 / v_mfma_f64_16x16x4f64).  K advances in slabs of 16 through
-// LDS; the next slab is fetched into registers while the current one is multiplied.
+// MFMA (v_mfma_f32_16x16x4f32 / v_mfma_f64_16x16x4f64).  K advances in slabs of 32 through
+// LDS; the next slab is fetched into registers (16-byte loads inside the matrix) while the
+// current one is multiplied.
 // Triangular operands are handled by restricting the K range per output tile (the invalid
 // triangle of every operand used here is stored as explicit zeros).
 #pragma once
@@ -67,11 +68,26 @@ struct GemmArgs {
   const int* skip_if_zero;   // optional: when *skip_if_zero == 0 store zeros and return
   const int* abort_flag;     // optional: when abort_flag[batch] != 0 return immediately
   int64_t sA, sB, sC;        // element strides between batch entries (grid z = batch)
+  int vec;                   // set by launch_gemm: A / B rows and batch strides 16-byte aligned
 };
 
 constexpr int GT = 64;
-constexpr int GKT = 16;
+constexpr int GKT = 32;
 constexpr int GPAD = 4;
+constexpr int GCH = 8;   // consecutive elements per thread in a slab fetch
+
+template <typename T>
+__device__ __forceinline__ void load_chunk(const T* __restrict__ src, bool vec, T (&r)[GCH]) {
+  if (vec) {   // 16-byte aligned, fully in bounds
+    const uint4* q = reinterpret_cast<const uint4*>(src);
+    constexpr int NV = GCH * sizeof(T) / 16;
+    uint4 v[NV];
+#pragma unroll
+    for (int e = 0; e < NV; ++e) v[e] = q[e];
+#pragma unroll
+    for (int e = 0; e < GCH; ++e) r[e] = reinterpret_cast<const T*>(v)[e];
+  }
+}
 
 template <typename T, bool TA, bool TB>
 __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
@@ -112,50 +128,61 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[a][b][e] = T(0);
 
-  T ra[4], rb[4];
-  // A slab: 64 (i) x 16 (k).  B slab: 16 (k) x 64 (j).
+  // Slab fetch: A 64 (i) x 32 (k), B 32 (k) x 64 (j), 8 consecutive elements per thread,
+  // as 16-byte loads when the slab is inside the matrix and rows are 16-byte aligned.
+  const bool rows_in = (i0 + GT <= p.M) && (j0 + GT <= p.N);
+  T ra[GCH], rb[GCH];
   auto fetch = [&](int k0) {
-    if (!TA) {  // A[i][k]: 4 consecutive k per thread
-      const int i = i0 + (tid >> 2), kq = k0 + (tid & 3) * 4;
+    const bool vec = p.vec && rows_in && (k0 + GKT <= k_hi);
+    if (!TA) {  // A[i][k]: row i = tid / 4, k chunk (tid % 4) * 8
+      const int i = i0 + (tid >> 2), kq = k0 + (tid & 3) * GCH;
+      const T* src = p.A + (int64_t)i * p.lda + kq;
+      load_chunk<T>(src, vec, ra);
+      if (!vec)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        ra[e] = (i < p.M && kq + e < k_hi) ? p.A[(int64_t)i * p.lda + kq + e] : T(0);
-    } else {    // A[k][i]: 4 consecutive i per thread
-      const int k = k0 + (tid >> 4), iq = i0 + (tid & 15) * 4;
+        for (int e = 0; e < GCH; ++e) ra[e] = (i < p.M && kq + e < k_hi) ? src[e] : T(0);
+    } else {    // A[k][i]: k = tid / 8, i chunk (tid % 8) * 8
+      const int k = k0 + (tid >> 3), iq = i0 + (tid & 7) * GCH;
+      const T* src = p.A + (int64_t)k * p.lda + iq;
+      load_chunk<T>(src, vec, ra);
+      if (!vec)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        ra[e] = (k < k_hi && iq + e < p.M) ? p.A[(int64_t)k * p.lda + iq + e] : T(0);
+        for (int e = 0; e < GCH; ++e) ra[e] = (k < k_hi && iq + e < p.M) ? src[e] : T(0);
     }
-    if (!TB) {  // B[k][j]: 4 consecutive j
-      const int k = k0 + (tid >> 4), jq = j0 + (tid & 15) * 4;
+    if (!TB) {  // B[k][j]: k = tid / 8, j chunk (tid % 8) * 8
+      const int k = k0 + (tid >> 3), jq = j0 + (tid & 7) * GCH;
+      const T* src = p.B + (int64_t)k * p.ldb + jq;
+      load_chunk<T>(src, vec, rb);
+      if (!vec)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        rb[e] = (k < k_hi && jq + e < p.N) ? p.B[(int64_t)k * p.ldb + jq + e] : T(0);
-    } else {    // B[j][k]: 4 consecutive k
-      const int j = j0 + (tid >> 2), kq = k0 + (tid & 3) * 4;
+        for (int e = 0; e < GCH; ++e) rb[e] = (k < k_hi && jq + e < p.N) ? src[e] : T(0);
+    } else {    // B[j][k]: j = tid / 4, k chunk (tid % 4) * 8
+      const int j = j0 + (tid >> 2), kq = k0 + (tid & 3) * GCH;
+      const T* src = p.B + (int64_t)j * p.ldb + kq;
+      load_chunk<T>(src, vec, rb);
+      if (!vec)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        rb[e] = (j < p.N && kq + e < k_hi) ? p.B[(int64_t)j * p.ldb + kq + e] : T(0);
+        for (int e = 0; e < GCH; ++e) rb[e] = (j < p.N && kq + e < k_hi) ? src[e] : T(0);
     }
   };
   auto stash = [&]() {
     if (!TA) {
-      const int i = tid >> 2, kq = (tid & 3) * 4;
+      const int i = tid >> 2, kq = (tid & 3) * GCH;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) As[kq + e][i] = ra[e];
+      for (int e = 0; e < GCH; ++e) As[kq + e][i] = ra[e];
     } else {
-      const int k = tid >> 4, iq = (tid & 15) * 4;
+      const int k = tid >> 3, iq = (tid & 7) * GCH;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) As[k][iq + e] = ra[e];
+      for (int e = 0; e < GCH; ++e) As[k][iq + e] = ra[e];
     }
     if (!TB) {
-      const int k = tid >> 4, jq = (tid & 15) * 4;
+      const int k = tid >> 3, jq = (tid & 7) * GCH;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) Bs[k][jq + e] = rb[e];
+      for (int e = 0; e < GCH; ++e) Bs[k][jq + e] = rb[e];
     } else {
-      const int j = tid >> 2, kq = (tid & 3) * 4;
+      const int j = tid >> 2, kq = (tid & 3) * GCH;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) Bs[kq + e][j] = rb[e];
+      for (int e = 0; e < GCH; ++e) Bs[kq + e][j] = rb[e];
     }
   };
 
@@ -204,8 +231,11 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
 }
 
 template <typename T>
-inline int launch_gemm(const GemmArgs<T>& a, bool ta, bool tb, hipStream_t s, int batch = 1) {
+inline int launch_gemm(GemmArgs<T> a, bool ta, bool tb, hipStream_t s, int batch = 1) {
   if (a.M <= 0 || a.N <= 0 || batch <= 0) return RQ_OK;
+  auto al = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  auto ld_ok = [](int64_t ld) { return ((ld * (int64_t)sizeof(T)) & 15) == 0; };
+  a.vec = al(a.A) && al(a.B) && ld_ok(a.lda) && ld_ok(a.ldb) && ld_ok(a.sA) && ld_ok(a.sB);
   dim3 grid((a.N + GT - 1) / GT, (a.M + GT - 1) / GT, batch), block(256);
   if (!ta && !tb) hipLaunchKernelGGL((k_gemm_tile<T, false, false>), grid, block, 0, s, a);
   else if (!ta && tb) hipLaunchKernelGGL((k_gemm_tile<T, false, true>), grid, block, 0, s, a);
@@ -222,7 +252,7 @@ inline GemmArgs<T> gemm_args(const T* A, int64_t lda, const T* B, int64_t ldb, T
   g.M = M; g.N = N; g.K = K; g.alpha = alpha; g.epi = epi;
   g.krange = KR_FULL; g.lower_only = 0; g.row_scale = nullptr; g.row_bcast = 0;
   g.nz_flag = nullptr; g.skip_if_zero = nullptr; g.abort_flag = nullptr;
-  g.sA = 0; g.sB = 0; g.sC = 0;
+  g.sA = 0; g.sB = 0; g.sC = 0; g.vec = 0;
   return g;
 }
 
