@@ -3,17 +3,18 @@
 //
 // H[g] += X^T diag(s_g) X is computed as a symmetric rank-k update: only 128x128 tiles on or
 // above the diagonal are formed (the mirrored half is never computed), one workgroup per
-// (tile, group), three workgroups per CU.  Each workgroup streams 32-token slabs of X[:, I]
+// (tile, group).  Each workgroup streams 32-token slabs of X[:, I]
 // and X[:, J] (fp16/bf16/fp32, read in place): a slab is fetched into registers as raw
 // 16-byte vectors while the previous slab is multiplied, then converted to fp32 and written
 // to LDS token-minor ([column][token], row stride 36 floats, so each lane reads its 8 tokens
 // of one column with two conflict-free ds_read_b128).  The per-token saliency s[t, g] is folded
 // into the B operand as it is written (the reference's `weighted` = fl32(x * s) is never
 // materialised).  Products run on v_mfma_f32_32x32x2f32 with fp32 accumulation; each 64x64
-// quarter of the tile belongs to one wave (2x2 MFMA blocks of 32x32).  The diagonal tiles of
-// group 0 also accumulate act_square = sum_t x^2.
+// quarter of the tile belongs to one wave (2x2 MFMA blocks of 32x32); four workgroups share a
+// CU (<= 128 VGPRs, 37 KB LDS each).  The diagonal tiles of group 0 also accumulate
+// act_square = sum_t x^2, read back from the staged slab by the first 128 threads.
 //
-// Tail balancing: the (tile, target) items of a launch run in rounds of (CUs x 3) workgroups;
+// Tail balancing: the (tile, target) items of a launch run in rounds of (CUs x 4) workgroups;
 // when the last round would be partly empty, its items are split along the tokens into S
 // slices (chosen so that the split work fills whole rounds).  A slice writes its partial
 // tile to a caller-provided workspace; the last slice to finish (an integer counter per item)
@@ -131,9 +132,7 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-  float actp[16];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) actp[e] = 0.0f;
+  float actr = 0.0f;                  // act_square partial of column I0 + tid (tid < 128)
 
   RawSide<TX> ra, rb;
   load_side<TX, EDGE>(X, ntok, ldx, C, sbeg * HKC + sk, I0 + sc, ra);
@@ -152,36 +151,40 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
       const float xb = diag ? xa : to_f32(rb.e[e]);
       As[sc + e][sk] = xa;
       Bs[sc + e][sk] = xb * s;        // fl32(x * s): the reference's `weighted`
-      if (want_act) actp[e] += xa * xa;
     }
     __syncthreads();
+    if (want_act && tid < HT) {       // diagonal tiles: sum_t x^2 from the staged slab
+#pragma unroll
+      for (int q = 0; q < HKC; q += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(&As[tid][q]);
+        actr += v.x * v.x;
+        actr += v.y * v.y;
+        actr += v.z * v.z;
+        actr += v.w * v.w;
+      }
+    }
     if (sidx + 1 < send) {            // next slab in flight while this one is multiplied
       load_side<TX, EDGE>(X, ntok, ldx, C, t + HKC, I0 + sc, ra);
       if (!diag) load_side<TX, EDGE>(X, ntok, ldx, C, t + HKC, J0 + sc, rb);
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int kb = fk + h * 8;
-      const float4* pa0 = reinterpret_cast<const float4*>(&As[wr * 64 + fi][kb]);
-      const float4* pa1 = reinterpret_cast<const float4*>(&As[wr * 64 + 32 + fi][kb]);
-      const float4* pb0 = reinterpret_cast<const float4*>(&Bs[wc * 64 + fi][kb]);
-      const float4* pb1 = reinterpret_cast<const float4*>(&Bs[wc * 64 + 32 + fi][kb]);
-      float a0[8], a1[8], b0[8], b1[8];
-      *reinterpret_cast<float4*>(a0) = pa0[0];
-      *reinterpret_cast<float4*>(a0 + 4) = pa0[1];
-      *reinterpret_cast<float4*>(a1) = pa1[0];
-      *reinterpret_cast<float4*>(a1 + 4) = pa1[1];
-      *reinterpret_cast<float4*>(b0) = pb0[0];
-      *reinterpret_cast<float4*>(b0 + 4) = pb0[1];
-      *reinterpret_cast<float4*>(b1) = pb1[0];
-      *reinterpret_cast<float4*>(b1 + 4) = pb1[1];
+    for (int h = 0; h < 4; ++h) {     // four tokens per ds_read_b128 fragment
+      const int kb = fk + h * 4;
+      const float4 a0 = *reinterpret_cast<const float4*>(&As[wr * 64 + fi][kb]);
+      const float4 a1 = *reinterpret_cast<const float4*>(&As[wr * 64 + 32 + fi][kb]);
+      const float4 b0 = *reinterpret_cast<const float4*>(&Bs[wc * 64 + fi][kb]);
+      const float4 b1 = *reinterpret_cast<const float4*>(&Bs[wc * 64 + 32 + fi][kb]);
+      const float* pa0 = reinterpret_cast<const float*>(&a0);
+      const float* pa1 = reinterpret_cast<const float*>(&a1);
+      const float* pb0 = reinterpret_cast<const float*>(&b0);
+      const float* pb1 = reinterpret_cast<const float*>(&b1);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
+      for (int q = 0; q < 4; ++q) {
         // MFMA step: lanes 0-31 contribute token kb+q, lanes 32-63 token 16+kb+q
-        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[q], b0[q], acc[0][0], 0, 0, 0);
-        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[q], b1[q], acc[0][1], 0, 0, 0);
-        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[q], b0[q], acc[1][0], 0, 0, 0);
-        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[q], b1[q], acc[1][1], 0, 0, 0);
+        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(pa0[q], pb0[q], acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(pa0[q], pb1[q], acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(pa1[q], pb0[q], acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(pa1[q], pb1[q], acc[1][1], 0, 0, 0);
       }
     }
   }
@@ -194,17 +197,7 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
       for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
         for (int e = 0; e < 16; ++e) part[(bi * 32 + bj * 16 + e) * HTHREADS + tid] = acc[bi][bj][e];
-    if (want_act) {
-      __syncthreads();
-#pragma unroll
-      for (int e = 0; e < 16; ++e) As[sc + e][sk] = actp[e];
-      __syncthreads();
-      if (tid < HT) {
-        float sum = 0.0f;
-        for (int q = 0; q < HKC; ++q) sum += As[tid][q];
-        part[HT * HT + tid] = sum;
-      }
-    }
+    if (want_act && tid < HT) part[HT * HT + tid] = actr;
     return;
   }
 
@@ -223,18 +216,7 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
         }
       }
 
-  if (want_act) {
-    // Sum the 32 per-token partials of each column in a fixed order (As is free now).
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < 16; ++e) As[sc + e][sk] = actp[e];
-    __syncthreads();
-    if (tid < HT && I0 + tid < C) {
-      float sum = 0.0f;
-      for (int q = 0; q < HKC; ++q) sum += As[tid][q];
-      act_sq[I0 + tid] += sum;
-    }
-  }
+  if (want_act && tid < HT && I0 + tid < C) act_sq[I0 + tid] += actr;
 }
 
 // One output of a launch: the Hessian of one (module, saliency group) pair.  Modules that
@@ -285,7 +267,7 @@ __device__ __forceinline__ void reduce_slices(const float* __restrict__ part0, i
 }
 
 template <typename TX>
-__global__ __launch_bounds__(HTHREADS, 3) void k_hessian_accum(
+__global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
     const TX* __restrict__ X, int64_t ntok, int64_t ldx, int C, HTargets tg, int ntarg, int nt,
     int ntiles, bool vec_ok, int full, int S, float* __restrict__ ws, int* __restrict__ cnt) {
   __shared__ __attribute__((aligned(16))) float As[HT][HS];
