@@ -7,7 +7,7 @@
 // index-reversal permutation and L L^T = P H P,  U = P L^-1 P.  The factorisation and the
 // inverse L^-1 run together in one right-looking blocked pass in fp64 (64-wide blocks
 // inside 256-wide panels):
-//   per block k:  L_kk = chol(A_kk) and T = L_kk^-1 in LDS (one workgroup),
+//   per block k:  L_kk = chol(A_kk) and T = L_kk^-1 (one wavefront, rows in registers),
 //                 L_ik = A_ik T^T,  X_k = T B_k  (row block k of L^-1),
 //                 A_ij -= L_ik L_jk^T (lower tiles),  B_i -= L_ik X_k   (fp64 MFMA GEMMs),
 // where B accumulates I - sum_m L_im X_m; the updates of the trailing matrix and of the
@@ -18,7 +18,7 @@
 
 namespace {
 
-constexpr int NB = 64;     // diagonal block (factored and inverted in LDS)
+constexpr int NB = 64;     // diagonal block (factored and inverted by one wavefront)
 constexpr int NBW = 256;   // outer panel width
 
 __global__ void k_fill_i32(int* p, int v) { *p = v; }
@@ -77,83 +77,82 @@ __global__ __launch_bounds__(256) void k_reverse_to_f64(const float* __restrict_
   }
 }
 
-// Factor the nb x nb diagonal block of A at (k, k) and invert it.  One workgroup.
-// Writes T = L_kk^-1 (lower, explicit zeros above) to Tbuf and to Linv's diagonal block.
-// Factorisation: right-looking, one column per step; the 16x16 thread grid walks the
-// trailing triangle without integer division.  Inverse: four lanes per column of T, each
-// summing every fourth term of the forward substitution, combined with a quad reduction.
-__global__ __launch_bounds__(256) void k_chol_diag(const double* __restrict__ A, int C, int k,
-                                                   int nb, double* __restrict__ Tbuf,
-                                                   double* __restrict__ Linv, int64_t ws,
-                                                   int* info_all) {
-  __shared__ double L[NB][NB + 1];
-  __shared__ double T[NB][NB + 1];
-  __shared__ double rdiag[NB];
-  __shared__ int fail;
+// Factor the nb x nb diagonal block of A at (k, k) and invert it: one wavefront, lane r owns
+// row r of the block in registers (rows >= nb are identity padding).  Step j broadcasts the
+// pivot and the scaled column through LDS; the inverse T = L^-1 is formed the same way row by
+// row (forward substitution).  Fully unrolled, so every register index is static.  Writes T
+// (lower, explicit zeros above) to Tbuf and to Linv's diagonal block.
+__global__ __launch_bounds__(64) void k_chol_diag(const double* __restrict__ A, int C, int k,
+                                                  int nb, double* __restrict__ Tbuf,
+                                                  double* __restrict__ Linv, int64_t ws,
+                                                  int* info_all) {
+  __shared__ __attribute__((aligned(16))) double buf[NB];
+  __shared__ double piv;
   const int b = blockIdx.x;
   int* info = info_all + b;
   if (*info) return;
   A += b * ws;
   Tbuf += b * ws;
   Linv += b * ws;
-  const int tid = threadIdx.x;
-  const int tx = tid & 15, ty = tid >> 4;
-  if (tid == 0) fail = 0;
-  for (int i = ty; i < NB; i += 16)
-    for (int j = tx; j < NB; j += 16) {
-      L[i][j] = (i < nb && j <= i) ? A[(int64_t)(k + i) * C + (k + j)] : 0.0;
-      T[i][j] = 0.0;
-    }
-  __syncthreads();
-  for (int j = 0; j < nb; ++j) {
-    const double d = L[j][j];
-    if (!(d > 0.0) || !rq_isfinite(d)) {   // uniform: every thread reads the same pivot
-      if (tid == 0) fail = 1;
+  const int r = threadIdx.x;
+  double a[NB];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
+    double v = (r >= nb && c == r) ? 1.0 : 0.0;
+    if (r < nb && c <= r) v = A[(int64_t)(k + r) * C + (k + c)];
+    a[c] = v;
+  }
+  bool fail = false;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    if (r == j) piv = a[j];
+    __syncthreads();
+    const double d = piv;                           // uniform pivot
+    if (!(d > 0.0) || !rq_isfinite(d)) {
+      fail = true;
       break;
     }
-    const double rd = 1.0 / sqrt(d);
-    // trailing triangle: L[i][l] -= (L[i][j] rd) (L[l][j] rd), j < l <= i
-    for (int i = j + 1 + ty; i < nb; i += 16) {
-      const double lij = L[i][j] * rd;
-      for (int l = j + 1 + tx; l <= i; l += 16) L[i][l] = L[i][l] - lij * (L[l][j] * rd);
-    }
+    const double sq = sqrt(d);
+    const double rd = 1.0 / sq;
+    const double lrj = (r > j) ? a[j] * rd : 0.0;  // L[r][j]
+    a[j] = (r == j) ? sq : ((r > j) ? lrj : a[j]);
+    buf[r] = lrj;
     __syncthreads();
-    // scale column j (nothing reads it during the update above)
-    if (tid < nb - j) {
-      const int i = j + tid;
-      L[i][j] = (i == j) ? sqrt(d) : L[i][j] * rd;
-    }
+#pragma unroll
+    for (int l = j + 1; l < NB; ++l) a[l] = __builtin_fma(-lrj, buf[l], a[l]);
     __syncthreads();
   }
-  __syncthreads();
   if (fail) {
-    if (tid == 0) atomicExch(info, 1);
+    if (r == 0) atomicExch(info, 1);
     return;
   }
-  if (tid < nb) rdiag[tid] = 1.0 / L[tid][tid];
-  __syncthreads();
-  // T = L^-1: column c by the quad 4c..4c+3 (nb <= 64)
-  {
-    const int c = tid >> 2, part = tid & 3;
-    if (c < nb && part == 0) T[c][c] = rdiag[c];
-    for (int i = c + 1; i < NB; ++i) {
-      double sacc = 0.0;
-      if (c < nb && i < nb)
-        for (int m2 = c + part; m2 < i; m2 += 4) sacc += L[i][m2] * T[m2][c];
-      sacc += __shfl_xor(sacc, 1, 64);
-      sacc += __shfl_xor(sacc, 2, 64);
-      // T[i][c] is read only by this quad (same wavefront) in later iterations, and LDS
-      // accesses of one wavefront complete in program order
-      if (c < nb && i < nb && part == 0) T[i][c] = -sacc * rdiag[i];
+  // T = L^-1: t accumulates sum_{m < r} L[r][m] T[m][c]; row m is final at step m
+  double t[NB];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) t[c] = 0.0;
+#pragma unroll
+  for (int m = 0; m < NB; ++m) {
+    if (r == m) {
+      const double rdm = 1.0 / a[m];
+#pragma unroll
+      for (int c = 0; c < m; ++c) t[c] = -t[c] * rdm;
+      t[m] = rdm;
+#pragma unroll
+      for (int c = 0; c <= m; ++c) buf[c] = t[c];
     }
+    __syncthreads();
+    const double lrm = (r > m) ? a[m] : 0.0;
+#pragma unroll
+    for (int c = 0; c <= m; ++c) t[c] = __builtin_fma(lrm, buf[c], t[c]);
+    __syncthreads();
   }
-  __syncthreads();
-  for (int i = ty; i < nb; i += 16)
-    for (int j = tx; j < nb; j += 16) {
-      const double v = T[i][j];
-      Tbuf[i * NB + j] = v;
-      Linv[(int64_t)(k + i) * C + (k + j)] = v;
-    }
+#pragma unroll
+  for (int c = 0; c < NB; ++c) Tbuf[r * NB + c] = t[c];
+  if (r < nb) {
+#pragma unroll
+    for (int c = 0; c < NB; ++c)
+      if (c < nb) Linv[(int64_t)(k + r) * C + (k + c)] = t[c];
+  }
 }
 
 // Hinv[i][j] = fl32(Linv[C-1-i][C-1-j]) for j >= i, 0 below; non-finite -> info.
@@ -297,7 +296,7 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
       const int jb = (pe - j < NB) ? (pe - j) : NB;
       const int below = C - j - jb;                      // rows below this block (whole matrix)
       const int pend = pe - j - jb;                      // panel columns right of this block
-      hipLaunchKernelGGL(k_chol_diag, dim3(nb), blk, 0, s, A, C, j, jb, Tbuf, Linv, ws, info);
+      hipLaunchKernelGGL(k_chol_diag, dim3(nb), dim3(64), 0, s, A, C, j, jb, Tbuf, Linv, ws, info);
       RQ_CHECK_LAUNCH();
       int rc;
       if (below > 0) {
