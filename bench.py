@@ -9,6 +9,8 @@ A step = one linear: 8 add_batch calls + finalize_hessian + fasterquant, inputs 
 HBM.  Prints one JSON line.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+  python bench.py --config cfg3|cfg4 [--cpu-baseline-layer]   # a whole Llama-3-8B layer
+  python bench.py --config cfg5 [--cpu-baseline-sample]       # Llama-3-70B down_proj
 """
 from __future__ import annotations
 
@@ -27,7 +29,9 @@ sys.path.insert(0, ROOT)
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
 CFG = dict(R=4096, C=4096, G=4, N=128, T=2048, bsz=16, bits=4, sym=False, blocksize=128,
-           percdamp=0.01, alpha=0.0, outliers=8, seed=20251201)
+           percdamp=0.01, alpha=0.0, outliers=8, seed=20251201, wscale=0.02)
+# the Llama-3-70B down_proj, one GPU's full share (4 Hessians of 28672^2 fp32)
+CFG5 = dict(CFG, R=8192, C=28672, wscale=0.015)
 
 
 def make_inputs(dev, cfg):
@@ -40,7 +44,7 @@ def make_inputs(dev, cfg):
         X[i] = torch.randn((T, C), generator=gen, device=dev, dtype=torch.float32).half()
     out_ch = torch.randperm(C, generator=gen, device=dev)[: cfg["outliers"]]
     X[:, :, out_ch] *= 20
-    W = (torch.randn((R, C), generator=gen, device=dev) * 0.02).half()
+    W = (torch.randn((R, C), generator=gen, device=dev) * cfg["wscale"]).half()
     s = torch.exp(torch.randn((N, T, G), generator=gen, device=dev))
     for g in range(G):
         q = torch.quantile(s[..., g].flatten(), 0.99)          # linear interpolation
@@ -55,20 +59,54 @@ LAYER8B = [("q_proj", 4096, 4096, "attn"), ("k_proj", 1024, 4096, "attn"), ("v_p
            ("down_proj", 4096, 14336, "down")]
 
 
+def hadamard(n, dev):
+    """Sylvester Hadamard matrix of order n (a power of two), fp32."""
+    H = torch.ones((1, 1), device=dev)
+    while H.shape[0] < n:
+        H = torch.cat([torch.cat([H, H], 1), torch.cat([H, -H], 1)], 0)
+    return H
+
+
+def rotation(C, gen, dev):
+    """configs[3]'s seeded orthogonal rotation: diag(+-1) H_C / sqrt(C) for a power of two,
+    Q_k (x) (diag(+-1) H_m / sqrt(m)) for C = k * m (QuaRot-style; C = 14336 = 7 * 2048)."""
+    m = 1 << (C.bit_length() - 1)
+    while C % m:
+        m >>= 1
+    k = C // m
+    signs = torch.randint(0, 2, (m,), generator=gen, device=dev).float() * 2 - 1
+    Hm = signs[:, None] * hadamard(m, dev) / (m ** 0.5)
+    if k == 1:
+        return Hm
+    Qk, _ = torch.linalg.qr(torch.randn((k, k), generator=gen, device=dev).cpu())
+    return torch.kron(Qk.contiguous().to(dev), Hm.contiguous())
+
+
+def rotate_(X, Rm):
+    """X <- X R in place, one calibration sample at a time (fp32 product, fp16 result)."""
+    for i in range(X.shape[0]):
+        X[i] = (X[i].float() @ Rm).half()
+
+
 def make_layer_inputs(dev, cfg):
     gen = torch.Generator(device=dev)
     gen.manual_seed(cfg["seed"] + 1)
     N, T, G = cfg["N"], cfg["T"], cfg["G"]
-    xs = {}
+    xs, rots = {}, {}
     for key, C in (("attn", 4096), ("o", 4096), ("mlp", 4096), ("down", 14336)):
         X = torch.empty((N, T, C), dtype=torch.float16, device=dev)
         for i in range(N):
             X[i] = torch.randn((T, C), generator=gen, device=dev, dtype=torch.float32).half()
         X[:, :, torch.randperm(C, generator=gen, device=dev)[: cfg["outliers"]]] *= 20
+        if cfg.get("rotate"):
+            rots[key] = rotation(C, gen, dev)
+            rotate_(X, rots[key])
         xs[key] = X
     mods = {}
     for name, R, C, key in LAYER8B:
         W = (torch.randn((R, C), generator=gen, device=dev) * 0.02).half()
+        if cfg.get("rotate"):
+            W = (W.float() @ rots[key]).half()                 # W' = W R keeps X' W'^T = X W^T
         s = torch.exp(torch.randn((N, T, G), generator=gen, device=dev))
         for g in range(G):
             s[..., g].clamp_(max=float(torch.quantile(s[..., g].flatten(), 0.99)))
@@ -88,6 +126,7 @@ def one_layer(xs, mods, cfg, layers, timer=None):
         g.quantizer = WeightQuantizer()
         g.quantizer.configure(cfg["bits"], perchannel=True, sym=cfg["sym"], mse=False)
         objs[name] = g
+    fq = fq_kwargs(cfg)
     for key in ("attn", "o", "mlp", "down"):
         group = [objs[n] for n, _, _, k in LAYER8B if k == key]
         for j in range(0, cfg["N"], cfg["bsz"]):
@@ -99,10 +138,17 @@ def one_layer(xs, mods, cfg, layers, timer=None):
     for g in objs.values():
         g.finalize_hessian()
     for g in objs.values():
-        g.fasterquant(blocksize=cfg["blocksize"], percdamp=cfg["percdamp"], groupsize=-1, actorder=True,
-                      static_groups=True)
+        g.fasterquant(**fq)
         g.free()
     return objs
+
+
+def fq_kwargs(cfg):
+    """fasterquant arguments of a config: configs[1..2] per-channel + act_order (static_groups
+    follows act_order like the driver, :7472); configs[3] dynamic 128-column groups + atomic."""
+    act = cfg.get("actorder", True)
+    return dict(blocksize=cfg["blocksize"], percdamp=cfg["percdamp"], groupsize=cfg.get("groupsize", -1),
+                actorder=act, static_groups=act, block_atomic_quant=cfg.get("atomic", False))
 
 
 def layer_hessian_flops(cfg):
@@ -127,8 +173,7 @@ def cpu_baseline_layer(xs, mods, cfg):
         o.index, o.token_count = cfg["N"], cfg["N"] * cfg["T"]
         t1 = time.perf_counter()
         o.finalize_hessian()
-        o.fasterquant(blocksize=cfg["blocksize"], percdamp=cfg["percdamp"], groupsize=-1, actorder=True,
-                      static_groups=True)
+        o.fasterquant(**fq_kwargs(cfg))
         t_fq = time.perf_counter() - t1
         total += t_acc * nchunks + t_fq
         parts.append(f"{name}: 1/{nchunks} chunk {t_acc:.1f}s, fasterquant {t_fq:.1f}s")
@@ -139,8 +184,19 @@ def cpu_baseline_layer(xs, mods, cfg):
                 sample="oracle on host CPU; " + "; ".join(parts) + f"; layer {total:.1f} s")
 
 
+CFG4 = dict(CFG, sym=True, groupsize=128, actorder=False, atomic=True, rotate=True)
+WORKLOAD = {
+    "cfg3": "configs[2]: Llama-3-8B decoder layer, 7 linears (q/k/v and gate/up Hessians fused over "
+            "their shared input), NUM_GROUPS=4, 128x2048 tokens, w4 asym per-channel, act_order, B=128; "
+            "value = layer time / 7, ms_per_step = layer",
+    "cfg4": "configs[3]: Llama-3-8B decoder layer, seeded orthogonal (Hadamard-based) rotation of W and X, "
+            "w4 sym, 128-column dynamic groups, BLOCK_ATOMIC_QUANT, NUM_GROUPS=4, 128x2048 tokens; "
+            "value = layer time / 7, ms_per_step = layer",
+}
+
+
 def run_layer(args, dev):
-    cfg = dict(CFG)
+    cfg = dict(CFG4 if args.config == "cfg4" else CFG)
     xs, mods = make_layer_inputs(dev, cfg)
     layers = {n: torch.nn.Linear(C, R, bias=False).to(dev, torch.float16) for n, R, C, _ in LAYER8B}
     torch.cuda.synchronize()
@@ -162,10 +218,7 @@ def run_layer(args, dev):
         "warmup": args.warmup, "ms_per_step": round(layer_ms, 2), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32 (fp16 inputs)",
         "data": "synthetic (seeded, generated on the GPU)",
-        "config": {"workload": "configs[2]: Llama-3-8B decoder layer, 7 linears (q/k/v and gate/up Hessians "
-                               "fused over their shared input), NUM_GROUPS=4, 128x2048 tokens, w4 asym "
-                               "per-channel, act_order, B=128; value = layer time / 7, ms_per_step = layer",
-                   "parallelism": "single GPU"},
+        "config": {"workload": WORKLOAD[args.config], "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
                      "kernel": "k_hessian_accum (all launches of the layer)",
@@ -190,8 +243,7 @@ def one_linear(X, W, s, grad, cfg, layer, timer=None):
         if timer is not None:
             timer.stop()
     g.finalize_hessian()
-    g.fasterquant(blocksize=cfg["blocksize"], percdamp=cfg["percdamp"], groupsize=-1, actorder=True,
-                  static_groups=True)
+    g.fasterquant(**fq_kwargs(cfg))
     return g
 
 
@@ -236,8 +288,7 @@ def cpu_baseline(X, W, s, grad, cfg, chunks=2):
     o.token_count = cfg["N"] * cfg["T"]
     t1 = time.perf_counter()
     o.finalize_hessian()
-    o.fasterquant(blocksize=cfg["blocksize"], percdamp=cfg["percdamp"], groupsize=-1, actorder=True,
-                  static_groups=True)
+    o.fasterquant(**fq_kwargs(cfg))
     t_fq = time.perf_counter() - t1
     nchunks = cfg["N"] // cfg["bsz"]
     total_s = t_acc * nchunks / chunks + t_fq
@@ -246,6 +297,24 @@ def cpu_baseline(X, W, s, grad, cfg, chunks=2):
                 sample=(f"oracle (reference torch op sequence) on host CPU: {chunks}/{nchunks} add_batch "
                         f"chunks timed ({t_acc:.1f} s, x{nchunks // chunks} by tokens) + full "
                         f"finalize_hessian+fasterquant ({t_fq:.1f} s); {platform.processor() or platform.machine()}"))
+
+
+def cpu_baseline_hessian_sample(X, s, cfg, samples=1):
+    """configs[4] on the host is hours of work; time the oracle's add_batch on `samples` of the
+    128 calibration samples and extrapolate by tokens.  A lower bound of the CPU path: the
+    CPU finalize_hessian + fasterquant (four 28672^2 Cholesky chains, the block loop) are left out."""
+    from oracle.gptqplus_cpu import GPTQPlusOracle
+    C, G = cfg["C"], cfg["G"]
+    o = GPTQPlusOracle(torch.zeros(G, C), s[:samples].cpu(), torch.zeros(G, C), G, 0.0, 0.0)
+    xc = X[:samples].cpu()
+    t0 = time.perf_counter()
+    o.add_batch(xc)
+    t = time.perf_counter() - t0
+    scale = cfg["N"] // samples
+    return dict(value=round(t * scale * 1e3, 1), unit="ms per linear (Hessian accumulation only, extrapolated)",
+                cores=torch.get_num_threads(), kind="port",
+                sample=(f"oracle add_batch on {samples}/{cfg['N']} samples ({t:.1f} s, x{scale} by tokens); "
+                        "finalize_hessian + fasterquant not timed, so this is a lower bound"))
 
 
 def copy_calibration(dev, nbytes=1 << 30, reps=3):
@@ -275,10 +344,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-chunks", type=int, default=2)
-    ap.add_argument("--config", choices=["cfg2", "cfg3"], default="cfg2",
-                    help="cfg2: one q_proj linear (default); cfg3: a full Llama-3-8B layer")
+    ap.add_argument("--config", choices=["cfg2", "cfg3", "cfg4", "cfg5"], default="cfg2",
+                    help="cfg2: one q_proj linear (default); cfg3: a full Llama-3-8B layer; cfg4: the "
+                         "layer rotated, w4 sym, dynamic 128-column groups, atomic; cfg5: the Llama-3-70B "
+                         "down_proj 8192x28672")
     ap.add_argument("--cpu-baseline-layer", action="store_true",
-                    help="with --config cfg3: also time the CPU oracle on the layer (minutes)")
+                    help="with --config cfg3/cfg4: also time the CPU oracle on the layer (minutes)")
+    ap.add_argument("--cpu-baseline-sample", action="store_true",
+                    help="with --config cfg5: time the CPU oracle's Hessian accumulation on one sample")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration for the traffic figure)")
     args = ap.parse_args()
@@ -291,11 +364,11 @@ def main():
     if args.copy_calibration:
         copy_calibration(dev)
         return
-    if args.config == "cfg3":
+    if args.config in ("cfg3", "cfg4"):
         run_layer(args, dev)
         return
     torch.backends.cuda.matmul.allow_tf32 = False
-    cfg = dict(CFG)
+    cfg = dict(CFG5 if args.config == "cfg5" else CFG)
     X, W, s, grad = make_inputs(dev, cfg)
     layer = torch.nn.Linear(cfg["C"], cfg["R"], bias=False).to(dev, torch.float16)
     torch.cuda.synchronize()
@@ -331,16 +404,23 @@ def main():
         "vs_baseline": None,
         "dtype": "fp32 (fp16 inputs)",
         "data": "synthetic (seeded, generated on the GPU)",
-        "config": {"workload": "configs[1]: q_proj 4096x4096, NUM_GROUPS=4, 128x2048 tokens, w4 asym "
-                               "per-channel, act_order, B=128, GPTQ+ term on (alpha=0)",
+        "config": {"workload": ("configs[4]: Llama-3-70B down_proj 8192x28672, W ~ N(0, 0.015^2), "
+                                "NUM_GROUPS=4 (4 Hessians of 28672^2 fp32), 128x2048 tokens, w4 asym "
+                                "per-channel, act_order, B=128, GPTQ+ term on (alpha=0)")
+                   if args.config == "cfg5" else
+                   "configs[1]: q_proj 4096x4096, NUM_GROUPS=4, 128x2048 tokens, w4 asym "
+                   "per-channel, act_order, B=128, GPTQ+ term on (alpha=0)",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-                     "traffic": load_traffic(),
+                     "traffic": load_traffic() if args.config == "cfg2" else None,
                      "kernel": "k_hessian_accum", "launch_ms": round(h_ms, 3), "launches": n_launch,
                      "flops_per_launch": flops},
     }
-    if not args.no_cpu_baseline:
+    if args.config == "cfg5":
+        if args.cpu_baseline_sample:
+            line["cpu_baseline"] = cpu_baseline_hessian_sample(X, s, cfg)
+    elif not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(X, W, s, grad, cfg, args.cpu_chunks)
     print(json.dumps(line), flush=True)
 
