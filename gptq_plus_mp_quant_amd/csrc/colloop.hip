@@ -35,6 +35,12 @@ namespace {
 
 constexpr int QB_MAXB = 128;
 
+// LDS column of register slot s of lane t.  Every slot is updated every column, so the
+// compiler can batch the LDS reads without per-slot branches: slots past the block (column
+// >= count) hold zeros and meet zero Hinv entries, slots past column 127 (they only exist
+// late in the block, and never become live again) read a clamped, in-bounds column.
+__device__ __forceinline__ int hcol(int s, int t) { return min(4 * s + t, QB_MAXB - 1); }
+
 template <int CTRL>
 __device__ __forceinline__ float quad_bcast(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
@@ -158,7 +164,6 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
     }
     // Err1 * Hinv1 = res, forward substitution (:1283-1288)
     for (int m = 0; m < nmacro; ++m) {
-      const int nlive = (count - 4 * m + 3) / 4;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 4 * m + r;
@@ -169,8 +174,8 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
           if (valid && t == r) erow[i] = e;
 #pragma unroll
           for (int k = 0; k < SLOTS; ++k) {
-            if (k < nlive) {
-              const float h = Hl[i][4 * (m + k) + t];
+            {
+              const float h = Hl[i][hcol(m + k, t)];
               w[k] = w[k] - e * h;
             }
           }
@@ -185,7 +190,6 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
 
   // column-serial loop (:1296-1367)
   for (int m = 0; m < nmacro; ++m) {
-    const int nlive = (count - 4 * m + 3) / 4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = 4 * m + r;
@@ -205,8 +209,8 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
           const float zi = use_gh ? quad_lane(zz[0], r) : 0.0f;
 #pragma unroll
           for (int k = 0; k < SLOTS; ++k) {
-            if (k < nlive) {
-              const float h = Hl[i][4 * (m + k) + t];
+            {
+              const float h = Hl[i][hcol(m + k, t)];
               const float ge = geff(k);
               const float upd = e * h;
               w[k] = w[k] - (upd + ge);
@@ -217,8 +221,8 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
           const float zi = quad_lane(zz[0], r);
 #pragma unroll
           for (int k = 0; k < SLOTS; ++k) {
-            if (k < nlive) {
-              const float h = Hl[i][4 * (m + k) + t];
+            {
+              const float h = Hl[i][hcol(m + k, t)];
               const float upd = e * h;
               if constexpr (GM == 3) w[k] = w[k] - a.sos * (upd + gh[k]);
               else w[k] = w[k] - (upd + gh[k]);
@@ -228,8 +232,8 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
         } else {
 #pragma unroll
           for (int k = 0; k < SLOTS; ++k) {
-            if (k < nlive) {
-              const float h = Hl[i][4 * (m + k) + t];
+            {
+              const float h = Hl[i][hcol(m + k, t)];
               if constexpr (GM == 3) w[k] = w[k] - a.sos * (e * h + gh[k]);
               else w[k] = w[k] - (e * h + gh[k]);
             }
