@@ -74,7 +74,9 @@ def quadratic_refresh(X, W0, G0):
 
 class GoldenSet:
     def __init__(self, cases, beta):
-        self.cases = cases
+        self.all_cases = cases
+        self.cases = [c for c in cases if c.meta.get("kind") != "gptq"]      # GPTQPlus
+        self.gptq_cases = [c for c in cases if c.meta.get("kind") == "gptq"]  # classic GPTQ
         self.beta = beta
 
     @classmethod
@@ -90,7 +92,7 @@ class GoldenSet:
         return cls(cases, beta)
 
     def by_name(self, name):
-        for c in self.cases:
+        for c in self.all_cases:
             if c.name == name:
                 return c
         raise KeyError(name)

@@ -16,6 +16,7 @@ The vectors (inputs + outputs) are stored compressed in ``tests/golden/golden_ca
 """
 from __future__ import annotations
 
+import importlib
 import json
 import logging
 import sys
@@ -63,6 +64,20 @@ CASES = [
          fq=dict(grad_optimizer="sgd", grad_lr=8e-3, grad_reg_strategy="quant_error_gate", grad_gate_floor=0.1, grad_gate_sharpness=1.0, second_order_scale=0.8, grad_clip=1.0)),
     dict(name="g2_sym4_block_backward", R=32, C=64, G=2, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16, atomic=False, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="block_backward"),
     dict(name="g2_asym4_block_backward_dyn_atomic", R=32, C=48, G=2, N=8, T=16, bits=4, sym=False, gs=16, act=False, B=16, atomic=True, alpha=0.05, ref_loss=100.0, gscale=0.1, mode="block_backward"),
+]
+
+
+# Classic GPTQ (gptq_utils/gptq_utils.py:23-180), driven like gptq_fwrd (:236-284): one
+# add_batch per calibration sample, static_groups = act_order unless stated.
+GPTQ_CASES = [
+    dict(name="gptq_sym4_perchan_act", R=32, C=64, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=16),
+    dict(name="gptq_asym4_static_act", R=32, C=64, N=8, T=16, bits=4, sym=False, gs=16, act=True, B=16),
+    dict(name="gptq_sym3_dynamic_gs16_B32", R=32, C=64, N=8, T=16, bits=3, sym=True, gs=16, act=False, B=32),
+    dict(name="gptq_sym4_dynamic_gs32_B16", R=32, C=64, N=8, T=16, bits=4, sym=True, gs=32, act=False, B=16),
+    dict(name="gptq_asym4_dynamic_act", R=32, C=64, N=8, T=16, bits=4, sym=False, gs=16, act=True, B=16, static=False),
+    dict(name="gptq_sym4_deadcols_ragged", R=32, C=50, N=8, T=16, bits=4, sym=True, gs=-1, act=True, B=32, dead=True),
+    dict(name="gptq_asym4_mse_static", R=32, C=64, N=8, T=16, bits=4, sym=False, gs=32, act=True, B=16, mse=True),
+    dict(name="gptq_sym4_nodata", R=32, C=64, N=0, T=16, bits=4, sym=True, gs=-1, act=False, B=16),
 ]
 
 
@@ -171,6 +186,30 @@ def run_case(gpu, qu, case, seed):
     return out
 
 
+def run_gptq_case(gq, qu, case, seed):
+    c = dict(case, G=1, N=max(case["N"], 1))
+    X, W, s, grad = synth_inputs(c, seed)
+    layer = torch.nn.Linear(case["C"], case["R"], bias=False).to(torch.float16)
+    layer.weight.data.copy_(torch.from_numpy(W))
+    g = gq.GPTQ(layer)
+    g.quantizer = qu.WeightQuantizer()
+    g.quantizer.configure(case["bits"], perchannel=True, sym=case["sym"], mse=case.get("mse", False))
+    xs = torch.from_numpy(X)
+    for j in range(case["N"]):
+        g.add_batch(xs[j].unsqueeze(0).data, None)
+    H = g.H.clone()
+    sync = torch.cuda.synchronize
+    torch.cuda.synchronize = lambda *a, **k: None       # fasterquant synchronises CUDA
+    try:
+        g.fasterquant(blocksize=case["B"], percdamp=0.01, groupsize=case["gs"], actorder=case["act"],
+                      static_groups=case.get("static", case["act"]), export_to_et=True)
+    finally:
+        torch.cuda.synchronize = sync
+    return {"X": X[:case["N"]], "W": W, "H_upper": _upper(H.numpy())[None], "Q": layer.weight.data.numpy(),
+            "W_int": layer.int_weight.numpy().astype(np.int8), "Scale": layer.scale.numpy(),
+            "qscale": g.quantizer.scale.numpy(), "qzero": g.quantizer.zero.numpy()}
+
+
 def beta_vectors(gpu):
     """compute_safe_beta_from_reference_loss on seeded inputs incl. its clamp / where branches."""
     rng = np.random.Generator(np.random.PCG64(1234))
@@ -208,6 +247,14 @@ def main():
         print(f"case {case['name']}: codes={out['W_int'].size} "
               f"fallback={[out.get(f'sub{s}_identity_fallback') for s in range(case['G'])]}")
     arrays.update(beta_vectors(gpu))
+    gq = importlib.import_module("gptq_utils.gptq_utils")
+    for k, case in enumerate(GPTQ_CASES):
+        seed = 3000 + k
+        out = run_gptq_case(gq, qu, case, seed)
+        for key, val in out.items():
+            arrays[f"{case['name']}__{key}"] = val
+        meta.append(dict(case, G=1, kind="gptq", seed=seed))
+        print(f"gptq case {case['name']}: codes={out['W_int'].size}")
     arrays["__meta__"] = np.frombuffer(json.dumps(meta).encode(), dtype=np.uint8)
     arrays["__torch_version__"] = np.frombuffer(torch.__version__.encode(), dtype=np.uint8)
     np.savez_compressed(OUT, **arrays)
