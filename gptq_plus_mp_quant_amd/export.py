@@ -50,10 +50,11 @@ def export_packed(gptq) -> Dict[str, object]:
         scales = gptq.scale_table.reshape(1, R)
         g_idx = torch.zeros(C, dtype=torch.int32, device=dev)
     elif gptq.qmode == nat.RQ_QMODE_STATIC:
-        # static groups are cut from the unpermuted weight (gptq_plus_utils.py:994-1002), so the
-        # natural column c belongs to group c // groupsize
+        # a scale table indexed by col_group[j] for the (permuted) column j: natural column c
+        # reads col_group[invperm[c]] (GPTQ+ static groups give c // groupsize; classic GPTQ's
+        # dynamic groups follow the permuted order)
         scales = gptq.scale_table
-        g_idx = (torch.arange(C, device=dev) // gptq.groupsize_used).to(torch.int32)
+        g_idx = gptq.col_group[invperm] if invperm is not None else gptq.col_group
     else:
         # dynamic groups: one scale per block of the (permuted) column order
         scales = gptq.dyn_scale

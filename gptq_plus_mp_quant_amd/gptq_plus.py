@@ -37,6 +37,58 @@ def _section(rec, name):
     return rec.section(name) if rec is not None else _NULL
 
 
+def hessian_inverse_chain(dev, H_work, Hinv_out, Hinv_init_out, workspace, percdamp,
+                          damp_auto_increment=0.0015, log_context="", identity_fallback=True):
+    """The damped Cholesky chain with retries (gptq_plus_utils.py:494-561; classic GPTQ
+    gptq_utils.py:87-106 has the same schedule but raises instead of the identity fallback).
+    H_work [nb, C, C] (or [C, C]) is damped in place; returns [(damp, fallback, attempts)]."""
+    damp0 = float(percdamp)
+    if damp0 <= 0:
+        raise ValueError(f"Quantization{log_context}: `damp_percent` must be positive. current is {damp0}")
+    if H_work.dim() == 2:
+        H_work, Hinv_out = H_work[None], Hinv_out[None]
+        Hinv_init_out = None if Hinv_init_out is None else Hinv_init_out[None]
+    nb, C = H_work.shape[0], H_work.shape[-1]
+    damp = [damp0] * nb
+    attempts = [0] * nb
+    status = ["run" if 1 > damp0 > 0 else "range"] * nb
+    info = torch.zeros(nb, dtype=torch.int32, device=dev)
+    while any(st == "run" for st in status):
+        todo = [damp[b] if status[b] == "run" else 0.0 for b in range(nb)]
+        for b in range(nb):
+            attempts[b] += status[b] == "run"
+        K.chol_hinv_attempt(H_work, todo, workspace, Hinv_out, Hinv_init_out, info)
+        codes = info.tolist()
+        for b in range(nb):
+            if status[b] != "run":
+                continue
+            if codes[b] == 0:
+                status[b] = "ok"
+                continue
+            logging.warning("Quantization%s subgroup=%d: Current `damp_percent = %.5f` is too low, "
+                            "auto-incrementing by `%.5f`", log_context, b, damp[b], damp_auto_increment)
+            damp[b] += damp_auto_increment
+            if not (1 > damp[b] > 0):
+                status[b] = "range"
+    out = []
+    for b in range(nb):
+        if status[b] == "ok":
+            out.append((damp[b], False, attempts[b]))
+        elif damp[b] >= 1 and identity_fallback:
+            logging.warning("Quantization%s subgroup=%d: `damp_percent` reached %.5f; falling back to "
+                            "identity Hessian inverse for this subgroup.", log_context, b, damp[b])
+            eye = torch.eye(C, device=dev)
+            Hinv_out[b].copy_(eye)
+            if Hinv_init_out is not None:
+                Hinv_init_out[b].copy_(eye)
+            out.append((damp[b], True, attempts[b]))
+        else:
+            raise ValueError(f"Quantization{log_context}: `damp_percent` must between 0 and 1. "
+                             f"current is {damp[b]}")
+    return out
+
+
+
 class GPTQPlus:
     # gptq_plus_utils.py:431-487
     def __init__(self, layer, saliency: torch.Tensor, gradient: torch.Tensor, num_groups: int,
@@ -128,51 +180,8 @@ class GPTQPlus:
     # gptq_plus_utils.py:494-561, for a batch of subgroups (each with its own schedule)
     def _hessian_inverse(self, H_work, Hinv_out, Hinv_init_out, workspace, percdamp,
                          damp_auto_increment=0.0015, log_context=""):
-        """H_work [nb, C, C] (or [C, C]) is damped in place; returns [(damp, fallback, attempts)]."""
-        damp0 = float(percdamp)
-        if damp0 <= 0:
-            raise ValueError(f"Quantization{log_context}: `damp_percent` must be positive. current is {damp0}")
-        if H_work.dim() == 2:
-            H_work, Hinv_out = H_work[None], Hinv_out[None]
-            Hinv_init_out = None if Hinv_init_out is None else Hinv_init_out[None]
-        nb, C = H_work.shape[0], H_work.shape[-1]
-        damp = [damp0] * nb
-        attempts = [0] * nb
-        status = ["run" if 1 > damp0 > 0 else "range"] * nb
-        info = torch.zeros(nb, dtype=torch.int32, device=self.dev)
-        while any(st == "run" for st in status):
-            todo = [damp[b] if status[b] == "run" else 0.0 for b in range(nb)]
-            for b in range(nb):
-                attempts[b] += status[b] == "run"
-            K.chol_hinv_attempt(H_work, todo, workspace, Hinv_out, Hinv_init_out, info)
-            codes = info.tolist()
-            for b in range(nb):
-                if status[b] != "run":
-                    continue
-                if codes[b] == 0:
-                    status[b] = "ok"
-                    continue
-                logging.warning("Quantization%s subgroup=%d: Current `damp_percent = %.5f` is too low, "
-                                "auto-incrementing by `%.5f`", log_context, b, damp[b], damp_auto_increment)
-                damp[b] += damp_auto_increment
-                if not (1 > damp[b] > 0):
-                    status[b] = "range"
-        out = []
-        for b in range(nb):
-            if status[b] == "ok":
-                out.append((damp[b], False, attempts[b]))
-            elif damp[b] >= 1:
-                logging.warning("Quantization%s subgroup=%d: `damp_percent` reached %.5f; falling back to "
-                                "identity Hessian inverse for this subgroup.", log_context, b, damp[b])
-                eye = torch.eye(C, device=self.dev)
-                Hinv_out[b].copy_(eye)
-                if Hinv_init_out is not None:
-                    Hinv_init_out[b].copy_(eye)
-                out.append((damp[b], True, attempts[b]))
-            else:
-                raise ValueError(f"Quantization{log_context}: `damp_percent` must between 0 and 1. "
-                                 f"current is {damp[b]}")
-        return out
+        return hessian_inverse_chain(self.dev, H_work, Hinv_out, Hinv_init_out, workspace, percdamp,
+                                     damp_auto_increment, log_context)
 
     # gptq_plus_utils.py:910-1896 (frozen mode)
     @torch.no_grad()
