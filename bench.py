@@ -27,6 +27,29 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 FP32_MFMA_PEAK_TFLOPS = 157.3
+FP16_MFMA_PEAK_TFLOPS = 2500.0      # dense fp16 / bf16 MFMA
+SPLIT_PIECES = 3                    # fp16 MFMA products per exact fp32 product (split16 kernel)
+
+
+def hessian_roofline(flops, ms, math, extra):
+    """Roofline object for the Hessian accumulation.  `flops` counts 2 per (token, i <= j)
+    element of every Hessian.  split16 runs on the fp16 MFMA pipe and needs SPLIT_PIECES fp16
+    products per fp32 product, so its bound is the fp16 peak against SPLIT_PIECES x flops; the
+    fp32-equivalent rate (flops / time against the fp32 MFMA peak) is what the metric's
+    "% fp32-MFMA peak" reads."""
+    eq = flops / (ms * 1e-3) / 1e12
+    if math == "split16":
+        ach, peak = SPLIT_PIECES * eq, FP16_MFMA_PEAK_TFLOPS
+        kernel = "k_hessian_split<__half> (timed with its k_xstats + k_xfinish pre-pass)"
+    else:
+        ach, peak = eq, FP32_MFMA_PEAK_TFLOPS
+        kernel = "k_hessian_accum<__half>"
+    out = {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+           "frac": round(ach / peak, 4), "kernel": kernel, "math": math,
+           "fp32_equivalent": {"achieved": round(eq, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+                               "frac": round(eq / FP32_MFMA_PEAK_TFLOPS, 4)}}
+    out.update(extra)
+    return out
 
 CFG = dict(R=4096, C=4096, G=4, N=128, T=2048, bsz=16, bits=4, sym=False, blocksize=128,
            percdamp=0.01, alpha=0.0, outliers=8, seed=20251201, wscale=0.02)
@@ -211,19 +234,17 @@ def run_layer(args, dev):
     layer_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     h_ms_mean, n_launch = timer.mean_ms()
     h_ms_layer = h_ms_mean * n_launch / args.steps
-    achieved = layer_hessian_flops(cfg) / (h_ms_layer * 1e-3) / 1e12
     line = {
         "metric": "ms per linear (H-accum + fasterquant) at Llama-8B shapes; % fp32-MFMA peak",
         "value": round(layer_ms / len(LAYER8B), 2), "unit": "ms", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(layer_ms, 2), "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "fp32 (fp16 inputs)",
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32 (fp16 inputs; exact fp32 products)",
         "data": "synthetic (seeded, generated on the GPU)",
         "config": {"workload": WORKLOAD[args.config], "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "k_hessian_accum (all launches of the layer)",
-                     "hessian_ms_per_layer": round(h_ms_layer, 2), "launches_per_layer": n_launch // args.steps,
-                     "flops_per_layer": layer_hessian_flops(cfg)},
+        "roofline": hessian_roofline(layer_hessian_flops(cfg), h_ms_layer, args.hessian_math,
+                                     {"traffic": None, "hessian_ms_per_layer": round(h_ms_layer, 2),
+                                      "launches_per_layer": n_launch // args.steps,
+                                      "flops_per_layer": layer_hessian_flops(cfg)}),
     }
     if args.cpu_baseline_layer:
         line["cpu_baseline"] = cpu_baseline_layer(xs, mods, cfg)
@@ -329,11 +350,13 @@ def copy_calibration(dev, nbytes=1 << 30, reps=3):
     print(json.dumps({"copy_calibration_bytes": nbytes, "reps": reps}), flush=True)
 
 
-def load_traffic():
+def load_traffic(math):
+    """Calibrated HBM bytes per Hessian launch of the given kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE measurement (None until measured)."""
     path = os.path.join(ROOT, "profiles", "hessian_traffic.json")
     if os.path.exists(path):
         with open(path) as f:
-            return json.load(f).get("traffic_bytes_per_launch")
+            return (json.load(f).get(math) or {}).get("traffic_bytes_per_launch")
     return None
 
 
@@ -352,6 +375,9 @@ def main():
                     help="with --config cfg3/cfg4: also time the CPU oracle on the layer (minutes)")
     ap.add_argument("--cpu-baseline-sample", action="store_true",
                     help="with --config cfg5: time the CPU oracle's Hessian accumulation on one sample")
+    ap.add_argument("--hessian-math", choices=["split16", "fp32"], default="split16",
+                    help="Hessian kernel for the fp16 inputs (split16: exact fp32 products from three "
+                         "fp16 MFMA products; fp32: fp32 MFMA)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration for the traffic figure)")
     args = ap.parse_args()
@@ -361,6 +387,8 @@ def main():
         sys.exit(2)
 
     dev = torch.device("cuda:0")
+    from gptq_plus_mp_quant_amd import _native as nat
+    nat.load().rq_hessian_math(nat.RQ_HMATH_SPLIT16 if args.hessian_math == "split16" else nat.RQ_HMATH_FP32)
     if args.copy_calibration:
         copy_calibration(dev)
         return
@@ -389,7 +417,6 @@ def main():
     h_ms, n_launch = timer.mean_ms()
     ntok = cfg["bsz"] * cfg["T"]
     flops = cfg["G"] * ntok * cfg["C"] * (cfg["C"] + 1)       # upper triangle incl. diagonal
-    achieved = flops / (h_ms * 1e-3) / 1e12
 
     line = {
         "metric": "ms per linear (H-accum + fasterquant) at Llama-8B shapes; % fp32-MFMA peak",
@@ -402,7 +429,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32 (fp16 inputs)",
+        "dtype": "f32 (fp16 inputs; exact fp32 products)",
         "data": "synthetic (seeded, generated on the GPU)",
         "config": {"workload": ("configs[4]: Llama-3-70B down_proj 8192x28672, W ~ N(0, 0.015^2), "
                                 "NUM_GROUPS=4 (4 Hessians of 28672^2 fp32), 128x2048 tokens, w4 asym "
@@ -411,11 +438,10 @@ def main():
                    "configs[1]: q_proj 4096x4096, NUM_GROUPS=4, 128x2048 tokens, w4 asym "
                    "per-channel, act_order, B=128, GPTQ+ term on (alpha=0)",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-                     "traffic": load_traffic() if args.config == "cfg2" else None,
-                     "kernel": "k_hessian_accum", "launch_ms": round(h_ms, 3), "launches": n_launch,
-                     "flops_per_launch": flops},
+        "roofline": hessian_roofline(flops, h_ms, args.hessian_math,
+                                     {"traffic": load_traffic(args.hessian_math) if args.config == "cfg2" else None,
+                                      "launch_ms": round(h_ms, 3), "launches": n_launch,
+                                      "flops_per_launch": flops}),
     }
     if args.config == "cfg5":
         if args.cpu_baseline_sample:

@@ -22,6 +22,8 @@
 // fixed summation order, and results are bitwise reproducible run to run.
 #include "rq_common.h"
 
+#include <atomic>
+
 namespace {
 
 constexpr int HT = 128;        // output tile edge
@@ -329,6 +331,444 @@ __global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
   reduce_slices(part0, S, Hg, act_sq, I0, J0, C, want_act);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Split-operand kernel for 16-bit inputs (the default for fp16 / bf16 X).
+//
+// H_ij = sum_t x_ti * w_tj with w = fl32(x * s), the reference's `weighted`.  x is exact in
+// the input's 16-bit type.  w is multiplied by 2^e (one exponent per target and column,
+// exact) and written as the sum of three 16-bit pieces, w * 2^e = p0 + p1 + p2 with
+// p0 = rn(w), p1 = rn(w - p0), p2 = rn(w - p0 - p1) (round to nearest in the 16-bit type):
+// 11 + 11 + 2 (fp16) or 8 + 8 + 8 (bf16) significant bits cover w's 24, so the sum is exact.
+// Each product x * p_k (11 x 11 or 8 x 8 bits) is exact in fp32, so three
+// v_mfma_f32_32x32x16_{f16,bf16} per 16 tokens accumulate the reference's fp32 products
+// in fp32, at 16x the fp32 MFMA rate (three MFMAs of 16 tokens replace eight of 2).
+// The exponent e (k_xfinish) puts the column's largest |w| in [2^14, 2^15): p0 cannot
+// overflow fp16, and the pieces are exact for every |w| * 2^e >= 2^-1, i.e. down to 2^-15
+// of the column's largest entry; below that the residual is at most 2^-25 * 2^-e, 2^-40 of
+// the column's largest |w|.  bf16 pieces have fp32's exponent range; the same scaling is
+// applied, harmlessly.  The epilogue multiplies the tile by 2^-e (exact) before adding it
+// to H.
+//
+// Tiles are 256 rows (x side) x 128 columns (w side), four waves of 128 x 64 (4 x 2 MFMA
+// blocks of 32 x 32), two workgroups per CU.  A tile pair-row p (rows 256p..) meets column
+// block c (columns 128c..) when 2p <= c; on c == 2p the lower 128 rows lie below the
+// diagonal and their two waves skip the MFMAs.  Slabs of 32 tokens are staged token-minor in
+// LDS (80-byte rows: 64 B of tokens + 16 B pad; the 16-byte token chunk k of row r sits at
+// chunk k ^ ((r >> 4) & 3), which keeps the transposing 16-byte writes and the fragment reads
+// free of bank conflicts).  act_square and the per-column maxima come from a separate pass
+// over X (k_xstats / k_xfinish).
+constexpr int XR = 256;          // tile rows (exact x operand)
+constexpr int XC = 128;          // tile columns (split weighted operand)
+constexpr int XK = 32;           // tokens per slab
+constexpr int XRS = 80;          // LDS row stride in bytes
+constexpr int XNP = 3;           // pieces of the weighted operand
+constexpr int XTHREADS = 256;
+constexpr int XPART = XR * XC;   // floats of one partial tile
+constexpr int XSR = 2;           // pair rows per super-row (tile order)
+
+template <typename TX>
+struct XType;
+template <>
+struct XType<__half> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ floatx16 mfma(v8 a, v8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float lo(uint32_t u) { return (float)__builtin_bit_cast(v2, u).x; }
+  static __device__ __forceinline__ float hi(uint32_t u) { return (float)__builtin_bit_cast(v2, u).y; }
+  static __device__ __forceinline__ uint32_t pack(float a, float b) {
+    v2 v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+template <>
+struct XType<__hip_bfloat16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ floatx16 mfma(v8 a, v8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float lo(uint32_t u) { return __uint_as_float(u << 16); }
+  static __device__ __forceinline__ float hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+  static __device__ __forceinline__ uint32_t pack(float a, float b) {
+    v2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+// Map an item index to (pair row p, column block c), 2p <= c < nt, in super-row order: XSR
+// pair rows at a time, each super-row walked column by column.
+__device__ __forceinline__ int ramp_sum(int n) {   // sum_{v<n} (floor(v/2) + 1)
+  const int h = n >> 1;
+  return h * (h + 1) + ((n & 1) ? h + 1 : 0);
+}
+__device__ __forceinline__ void pair_tile(int idx, int nt, int npr, int& p, int& c) {
+  int P0 = 0, rem = idx;
+  for (;;) {
+    const int h = min(XSR, npr - P0);
+    const int V = nt - 2 * P0;                      // columns of this super-row
+    const int cnt = (V <= 2 * h) ? ramp_sum(V) : ramp_sum(2 * h) + (V - 2 * h) * h;
+    if (rem < cnt) break;
+    rem -= cnt;
+    P0 += h;
+  }
+  const int h = min(XSR, npr - P0);
+  const int ramp = ramp_sum(2 * h);
+  if (rem >= ramp) {
+    rem -= ramp;
+    c = 2 * P0 + 2 * h + rem / h;
+    p = P0 + rem % h;
+    return;
+  }
+  for (int v = 0;; ++v) {
+    const int k = (v >> 1) + 1;
+    if (rem < k) {
+      c = 2 * P0 + v;
+      p = P0 + rem;
+      return;
+    }
+    rem -= k;
+  }
+}
+
+// 16-bit element cc (0..3) of a raw 4-column group.
+__device__ __forceinline__ uint32_t elem4(uint2 r, int cc) {
+  const uint32_t w = (cc < 2) ? r.x : r.y;
+  return (cc & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+template <bool EDGE>
+__device__ __forceinline__ void xload_a(const uint16_t* __restrict__ X, int64_t ntok, int64_t ldx,
+                                        int C, int64_t t0, int c0, uint2 (&r)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int64_t t = t0 + k;
+    if (!EDGE) {
+      r[k] = (t < ntok) ? *reinterpret_cast<const uint2*>(X + t * ldx + c0) : make_uint2(0, 0);
+    } else {
+      uint32_t e[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) e[q] = (t < ntok && c0 + q < C) ? X[t * ldx + c0 + q] : 0u;
+      r[k] = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+    }
+  }
+}
+
+template <bool EDGE>
+__device__ __forceinline__ void xload_b(const uint16_t* __restrict__ X, int64_t ntok, int64_t ldx,
+                                        int C, int64_t t0, int c0, const float* __restrict__ sal,
+                                        int64_t ld_sal, uint32_t (&r)[8], float (&s)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int64_t t = t0 + k;
+    s[k] = (t < ntok) ? sal[t * ld_sal] : 0.0f;
+    if (!EDGE) {
+      r[k] = (t < ntok) ? *reinterpret_cast<const uint32_t*>(X + t * ldx + c0) : 0u;
+    } else {
+      const uint32_t e0 = (t < ntok && c0 < C) ? X[t * ldx + c0] : 0u;
+      const uint32_t e1 = (t < ntok && c0 + 1 < C) ? X[t * ldx + c0 + 1] : 0u;
+      r[k] = e0 | (e1 << 16);
+    }
+  }
+}
+
+__device__ __forceinline__ int xchunk(int row, int k) { return row * XRS + 16 * (k ^ ((row >> 4) & 3)); }
+
+template <typename TX, bool EDGE>
+__device__ __forceinline__ void split_tile(const uint16_t* __restrict__ X, int64_t ntok, int64_t ldx,
+                                           int C, const float* __restrict__ sal, int64_t ld_sal,
+                                           const float* __restrict__ scl, float* __restrict__ Hg,
+                                           int R0, int C0, bool lower_live, uint8_t* As, uint8_t* Bs,
+                                           int64_t sbeg, int64_t send, float* __restrict__ part) {
+  typedef XType<TX> T;
+  typedef typename T::v8 v8;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const bool live = (wr == 0) || lower_live;
+  const int q = tid & 63;          // staging: row side columns R0 + 4q.., w side C0 + 2q..
+  const int w8 = tid >> 6;         // staging: tokens 8 * w8 .. + 7 of the slab
+
+  float sc[2];
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc) sc[cc] = (C0 + 2 * q + cc < C) ? scl[C0 + 2 * q + cc] : 1.0f;
+
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  uint2 ra[8];
+  uint32_t rb[8];
+  float s[8];
+  xload_a<EDGE>(X, ntok, ldx, C, sbeg * XK + 8 * w8, R0 + 4 * q, ra);
+  xload_b<EDGE>(X, ntok, ldx, C, sbeg * XK + 8 * w8, C0 + 2 * q, sal, ld_sal, rb, s);
+
+  const int fr = lane & 31;
+  const int fh = lane >> 5;
+
+  for (int64_t sidx = sbeg; sidx < send; ++sidx) {
+    __syncthreads();                 // previous slab fully consumed
+    // x side: transpose 8 tokens x 4 columns into four 16-byte token runs
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      uint4 d;
+      d.x = elem4(ra[0], cc) | (elem4(ra[1], cc) << 16);
+      d.y = elem4(ra[2], cc) | (elem4(ra[3], cc) << 16);
+      d.z = elem4(ra[4], cc) | (elem4(ra[5], cc) << 16);
+      d.w = elem4(ra[6], cc) | (elem4(ra[7], cc) << 16);
+      *reinterpret_cast<uint4*>(As + xchunk(4 * q + cc, w8)) = d;
+    }
+    // w side: w = fl32(x * s) * 2^e, split into three exact 16-bit pieces
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+      float w[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float x = cc ? T::hi(rb[k]) : T::lo(rb[k]);
+        const float ws = x * s[k];
+        w[k] = ws * sc[cc];
+      }
+      uint32_t p[XNP][4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        float a = w[2 * m], b = w[2 * m + 1];
+#pragma unroll
+        for (int k = 0; k < XNP; ++k) {
+          const uint32_t u = T::pack(a, b);
+          p[k][m] = u;
+          if (k + 1 < XNP) {
+            a = a - T::lo(u);
+            b = b - T::hi(u);
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < XNP; ++k)
+        *reinterpret_cast<uint4*>(Bs + k * (XC * XRS) + xchunk(2 * q + cc, w8)) =
+            make_uint4(p[k][0], p[k][1], p[k][2], p[k][3]);
+    }
+    __syncthreads();
+    if (sidx + 1 < send) {           // next slab in flight while this one is multiplied
+      xload_a<EDGE>(X, ntok, ldx, C, (sidx + 1) * XK + 8 * w8, R0 + 4 * q, ra);
+      xload_b<EDGE>(X, ntok, ldx, C, (sidx + 1) * XK + 8 * w8, C0 + 2 * q, sal, ld_sal, rb, s);
+    }
+    if (live) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int kc = 2 * ks + fh;  // this lane's 8-token chunk
+        v8 a[4], b[XNP][2];
+#pragma unroll
+        for (int bi = 0; bi < 4; ++bi)
+          a[bi] = *reinterpret_cast<const v8*>(As + xchunk(128 * wr + 32 * bi + fr, kc));
+#pragma unroll
+        for (int k = 0; k < XNP; ++k)
+#pragma unroll
+          for (int bj = 0; bj < 2; ++bj)
+            b[k][bj] = *reinterpret_cast<const v8*>(Bs + k * (XC * XRS) + xchunk(64 * wc + 32 * bj + fr, kc));
+#pragma unroll
+        for (int k = XNP - 1; k >= 0; --k)
+#pragma unroll
+          for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+            for (int bj = 0; bj < 2; ++bj) acc[bi][bj] = T::mfma(a[bi], b[k][bj], acc[bi][bj]);
+      }
+    }
+  }
+
+  if (part) {
+    // token slice: hand the (still scaled) partial tile to the workspace
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) part[((bi * 2 + bj) * 16 + e) * XTHREADS + tid] = acc[bi][bj][e];
+    return;
+  }
+  if (!live) return;
+  // H[g][i][j] += acc * 2^-e_j   (32x32 block layout: i = 8*(e/4) + 4*(lane/32) + e%4, j = lane%32)
+#pragma unroll
+  for (int bj = 0; bj < 2; ++bj) {
+    const int j = C0 + 64 * wc + 32 * bj + fr;
+    const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int i = R0 + 128 * wr + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
+        if (!EDGE || (i < C && j < C)) {
+          float* ph = Hg + (int64_t)i * C + j;
+          *ph = *ph + acc[bi][bj][e] * inv;
+        }
+      }
+  }
+}
+
+// The last slice of a split item adds the S partials (in slice order) to H.
+__device__ __forceinline__ void reduce_split_slices(const float* __restrict__ part0, int S,
+                                                    float* __restrict__ Hg, const float* __restrict__ scl,
+                                                    int R0, int C0, int C, bool lower_live) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  if (wr == 1 && !lower_live) return;
+  const int fr = lane & 31, fh = lane >> 5;
+#pragma unroll
+  for (int bj = 0; bj < 2; ++bj) {
+    const int j = C0 + 64 * wc + 32 * bj + fr;
+    const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll 4
+      for (int e = 0; e < 16; ++e) {
+        const int slot = ((bi * 2 + bj) * 16 + e) * XTHREADS + tid;
+        float sum = __hip_atomic_load(part0 + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int qq = 1; qq < S; ++qq)
+          sum += __hip_atomic_load(part0 + (int64_t)qq * XPART + slot, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        const int i = R0 + 128 * wr + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
+        if (i < C && j < C) {
+          float* ph = Hg + (int64_t)i * C + j;
+          *ph = *ph + sum * inv;
+        }
+      }
+  }
+}
+
+template <typename TX>
+__global__ __launch_bounds__(XTHREADS, 2) void k_hessian_split(
+    const uint16_t* __restrict__ X, int64_t ntok, int64_t ldx, int C, HTargets tg,
+    const float* __restrict__ scale, int ntarg, int nt, int npr, int nitems, bool vec_ok, int full,
+    int S, float* __restrict__ ws, int* __restrict__ cnt) {
+  __shared__ __attribute__((aligned(16))) uint8_t As[XR * XRS];
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[XNP * XC * XRS];
+  __shared__ int last_slice;
+
+  // Same schedule as k_hessian_accum: XCD-aware order for whole items, then the token
+  // slices of the tail items.
+  const int total = nitems * ntarg;
+  const int b = blockIdx.x;
+  const int64_t nslab = (ntok + XK - 1) / XK;
+  int logical, slice = -1;
+  int64_t sbeg = 0, send = nslab;
+  if (b < full) {
+    const int per = full / 8, rem8 = full % 8;
+    const int xcd = b % 8, idx = b / 8;
+    logical = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
+  } else {
+    const int tb = b - full;
+    logical = full + tb / S;
+    slice = tb % S;
+    sbeg = nslab * slice / S;
+    send = nslab * (slice + 1) / S;
+  }
+  if (logical >= total) return;
+  const int g = logical % ntarg;
+  int p, c;
+  pair_tile(logical / ntarg, nt, npr, p, c);
+  const int R0 = p * XR, C0 = c * XC;
+  const bool lower_live = (2 * p + 1 <= c) && (R0 + XR / 2 < C);
+  float* Hg = tg.H[g];
+  const float* scl = scale + (int64_t)g * C;
+  const bool interior = vec_ok && (R0 + XR <= C) && (C0 + XC <= C);
+  float* part0 = (slice >= 0) ? ws + (int64_t)(logical - full) * S * XPART : nullptr;
+  float* part = part0 ? part0 + (int64_t)slice * XPART : nullptr;
+  if (interior)
+    split_tile<TX, false>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], scl, Hg, R0, C0, lower_live, As, Bs,
+                          sbeg, send, part);
+  else
+    split_tile<TX, true>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], scl, Hg, R0, C0, lower_live, As, Bs,
+                         sbeg, send, part);
+  if (!part) return;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int* cp = cnt + (logical - full);
+    const int prev = atomicAdd(cp, 1);
+    last_slice = (prev == S - 1);
+    if (last_slice) atomicExch(cp, 0);
+  }
+  __syncthreads();
+  if (!last_slice) return;
+  __threadfence();
+  reduce_split_slices(part0, S, Hg, scl, R0, C0, C, lower_live);
+}
+
+// Pass over X before the split kernel: per token chunk, each column's max |x| and
+// sum_t x^2 (in token order), and each target's max |s|.
+template <typename TX>
+__global__ __launch_bounds__(256) void k_xstats(const TX* __restrict__ X, int64_t ntok, int64_t ldx,
+                                                int C, int64_t tpc, HTargets tg, int ntarg,
+                                                float* __restrict__ mpart, float* __restrict__ apart,
+                                                float* __restrict__ spart) {
+  __shared__ unsigned smx[HMAXT];
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int ch = blockIdx.y;
+  const int64_t t0 = (int64_t)ch * tpc;
+  const int64_t t1 = (t0 + tpc < ntok) ? t0 + tpc : ntok;
+  if (c < C) {
+    float m = 0.0f, a = 0.0f;
+    for (int64_t t = t0; t < t1; ++t) {
+      const float v = to_f32(X[t * ldx + c]);
+      m = fmaxf(m, fabsf(v));
+      a = a + v * v;                  // (inp ** 2).sum(0): square, then add
+    }
+    mpart[(int64_t)ch * C + c] = m;
+    apart[(int64_t)ch * C + c] = a;
+  }
+  if (blockIdx.x != 0) return;
+  if (threadIdx.x < HMAXT) smx[threadIdx.x] = 0u;
+  __syncthreads();
+  for (int g = 0; g < ntarg; ++g) {
+    float m = 0.0f;
+    for (int64_t t = t0 + threadIdx.x; t < t1; t += 256) m = fmaxf(m, fabsf(tg.sal[g][t * tg.ld_sal[g]]));
+    atomicMax(&smx[g], __float_as_uint(m));
+  }
+  __syncthreads();
+  if (threadIdx.x < ntarg) spart[(int64_t)ch * HMAXT + threadIdx.x] = __uint_as_float(smx[threadIdx.x]);
+}
+
+// Reduce the chunks: act_square += sum_t x^2 (chunks in order), and the per (target, column)
+// scale 2^e with e = 15 - E for max|x_c| * max|s_g| = f * 2^E, f in [0.5, 1).
+__global__ __launch_bounds__(256) void k_xfinish(int C, int nchunk, HTargets tg, int ntarg,
+                                                 const float* __restrict__ mpart,
+                                                 const float* __restrict__ apart,
+                                                 const float* __restrict__ spart, float* __restrict__ scale) {
+  __shared__ float smax[HMAXT];
+  if (threadIdx.x < ntarg) {
+    float m = 0.0f;
+    for (int ch = 0; ch < nchunk; ++ch) m = fmaxf(m, spart[(int64_t)ch * HMAXT + threadIdx.x]);
+    smax[threadIdx.x] = m;
+  }
+  __syncthreads();
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  float m = 0.0f, a = 0.0f;
+  for (int ch = 0; ch < nchunk; ++ch) {
+    m = fmaxf(m, mpart[(int64_t)ch * C + c]);
+    a = a + apart[(int64_t)ch * C + c];
+  }
+  for (int g = 0; g < ntarg; ++g)
+    if (tg.act[g]) tg.act[g][c] += a;
+  for (int g = 0; g < ntarg; ++g) {
+    const float mm = m * smax[g];
+    int e = 0;
+    if (mm > 0.0f && mm <= 3.402823466e38f) {
+      int E = 0;
+      (void)frexpf(mm, &E);
+      e = 15 - E;
+      e = e < -100 ? -100 : (e > 100 ? 100 : e);
+    }
+    scale[(int64_t)g * C + c] = ldexpf(1.0f, e);
+  }
+}
 }  // namespace
 
 namespace {
@@ -392,20 +832,23 @@ extern "C" int rq_version(void) { return 100; }
 
 namespace {
 
-// Concurrent workgroups of k_hessian_accum on the current device (CUs x occupancy).
-int hessian_slots() {
-  static int cache[64];
+std::atomic<int> g_hmath{RQ_HMATH_SPLIT16};
+
+// Concurrent workgroups of a Hessian kernel on the current device (CUs x occupancy).
+template <typename K>
+int kernel_slots(K kfn, int threads, int which) {
+  static int cache[2][64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] > 0) return cache[dev];
+  if (cache[which][dev] > 0) return cache[which][dev];
   int cus = 0, occ = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_hessian_accum<__half>, HTHREADS, 0) !=
-      hipSuccess)
-    return 0;
-  cache[dev] = cus * occ;
-  return cache[dev];
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn, threads, 0) != hipSuccess) return 0;
+  cache[which][dev] = cus * occ;
+  return cache[which][dev];
 }
+int hessian_slots() { return kernel_slots(k_hessian_accum<__half>, HTHREADS, 0); }
+int split_slots() { return kernel_slots(k_hessian_split<__half>, XTHREADS, 1); }
 
 // Items of the last, partly filled round and the slice count that fills rounds best
 // (the finishing time of the tail in rounds is ceil(tail * S / slots) / S).
@@ -431,17 +874,110 @@ void tail_split(int64_t total, int64_t nslab, int slots, int* tail, int* S) {
   }
 }
 
-// Workspace layout: one int counter per possible tail item at a fixed place (the start), so
-// launches with different tails can share one workspace, then the partial tiles.
-int64_t hessian_cnt_bytes(int slots) { return (((int64_t)slots * 4 + 255) / 256) * 256; }
+int64_t align256(int64_t b) { return ((b + 255) / 256) * 256; }
 
-int64_t hessian_ws_bytes(int64_t tail, int S, int slots) {
+// Workspace layout: one int counter per possible tail item at a fixed place (the start, sized
+// for the larger slot count of the two kernels), so launches with different tails and either
+// kernel can share one workspace, then the partial tiles, then (split kernel) the X pass.
+int64_t hessian_cnt_bytes() {
+  const int a = hessian_slots(), b = split_slots();
+  return align256((int64_t)(a > b ? a : b) * 4);
+}
+
+int64_t hessian_ws_bytes(int64_t tail, int S) {
   if (tail <= 0) return 0;
-  return hessian_cnt_bytes(slots) + tail * S * (int64_t)HPART * 4;
+  return hessian_cnt_bytes() + tail * S * (int64_t)HPART * 4;
+}
+
+struct SplitLayout {
+  int nchunk;
+  int64_t tpc, off_part, off_m, off_a, off_s, off_scale, bytes;
+};
+
+SplitLayout split_layout(int64_t ntok, int C, int ntarg, int64_t tail, int S) {
+  SplitLayout L;
+  int64_t nch = (ntok + 63) / 64;
+  L.nchunk = (int)(nch < 1 ? 1 : (nch > 256 ? 256 : nch));
+  L.tpc = (ntok + L.nchunk - 1) / L.nchunk;
+  L.off_part = hessian_cnt_bytes();
+  L.off_m = L.off_part + align256(tail * S * (int64_t)XPART * 4);
+  L.off_a = L.off_m + align256((int64_t)L.nchunk * C * 4);
+  L.off_s = L.off_a + align256((int64_t)L.nchunk * C * 4);
+  L.off_scale = L.off_s + align256((int64_t)L.nchunk * HMAXT * 4);
+  L.bytes = L.off_scale + align256((int64_t)ntarg * C * 4);
+  return L;
+}
+
+int64_t split_pairs(int C, int* nt_out, int* npr_out) {
+  const int nt = (C + XC - 1) / XC;
+  const int npr = (nt + 1) / 2;
+  int64_t n = 0;
+  for (int c = 0; c < nt; ++c) n += c / 2 + 1;
+  *nt_out = nt;
+  *npr_out = npr;
+  return n;
+}
+
+// Workspace bytes the split kernel needs for one launch of `ntarg` targets.
+int64_t split_ws_need(int64_t ntok, int C, int ntarg) {
+  int nt, npr;
+  const int64_t total = split_pairs(C, &nt, &npr) * ntarg;
+  int tail = 0, S = 1;
+  tail_split(total, (ntok + XK - 1) / XK, split_slots(), &tail, &S);
+  return split_layout(ntok, C, ntarg, tail, S).bytes;
+}
+
+int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, const HTargets& tg,
+                 int ntarg, void* ws, int64_t ws_bytes, hipStream_t s) {
+  int nt, npr;
+  const int64_t npairs = split_pairs(C, &nt, &npr);
+  const int64_t total = npairs * ntarg;
+  if (total > 0x7fffffff / 8) return RQ_EINVAL;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(x) & 7) == 0) && (((size_t)ldx * 2) % 8 == 0);
+  const int slots = split_slots();
+  int tail = 0, S = 1;
+  tail_split(total, (ntok + XK - 1) / XK, slots, &tail, &S);
+  SplitLayout L = split_layout(ntok, C, ntarg, tail, S);
+  if (ws_bytes < L.bytes) {                       // no room for the slices: whole items only
+    tail = 0;
+    S = 1;
+    L = split_layout(ntok, C, ntarg, 0, 1);
+  }
+  char* wb = reinterpret_cast<char*>(ws);
+  float* mpart = reinterpret_cast<float*>(wb + L.off_m);
+  float* apart = reinterpret_cast<float*>(wb + L.off_a);
+  float* spart = reinterpret_cast<float*>(wb + L.off_s);
+  float* scale = reinterpret_cast<float*>(wb + L.off_scale);
+  dim3 sgrid((C + 255) / 256, L.nchunk), fgrid((C + 255) / 256);
+  if (x_dtype == RQ_F16)
+    hipLaunchKernelGGL(k_xstats<__half>, sgrid, dim3(256), 0, s, (const __half*)x, ntok, ldx, C, L.tpc,
+                       tg, ntarg, mpart, apart, spart);
+  else
+    hipLaunchKernelGGL(k_xstats<__hip_bfloat16>, sgrid, dim3(256), 0, s, (const __hip_bfloat16*)x, ntok,
+                       ldx, C, L.tpc, tg, ntarg, mpart, apart, spart);
+  RQ_CHECK_LAUNCH();
+  hipLaunchKernelGGL(k_xfinish, fgrid, dim3(256), 0, s, C, L.nchunk, tg, ntarg, mpart, apart, spart, scale);
+  RQ_CHECK_LAUNCH();
+  const int full = (int)(total - tail);
+  int* cnt = tail > 0 ? reinterpret_cast<int*>(ws) : nullptr;
+  float* wsf = tail > 0 ? reinterpret_cast<float*>(wb + L.off_part) : nullptr;
+  dim3 grid((unsigned)(full + (int64_t)tail * S)), block(XTHREADS);
+  if (x_dtype == RQ_F16)
+    hipLaunchKernelGGL(k_hessian_split<__half>, grid, block, 0, s, (const uint16_t*)x, ntok, ldx, C, tg,
+                       scale, ntarg, nt, npr, (int)npairs, vec_ok, full, S, wsf, cnt);
+  else
+    hipLaunchKernelGGL(k_hessian_split<__hip_bfloat16>, grid, block, 0, s, (const uint16_t*)x, ntok, ldx,
+                       C, tg, scale, ntarg, nt, npr, (int)npairs, vec_ok, full, S, wsf, cnt);
+  RQ_CHECK_LAUNCH();
+  return RQ_OK;
 }
 
 int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, const HTargets& tg,
                    int ntarg, void* ws, int64_t ws_bytes, hipStream_t s) {
+  const bool aligned = ws && ((reinterpret_cast<uintptr_t>(ws) & 255) == 0);
+  if (x_dtype != RQ_F32 && g_hmath.load() == RQ_HMATH_SPLIT16 && aligned &&
+      ws_bytes >= split_layout(ntok, C, ntarg, 0, 1).bytes)
+    return launch_split(x, x_dtype, ntok, ldx, C, tg, ntarg, ws, ws_bytes, s);
   const int nt = (C + HT - 1) / HT;
   const int ntiles = nt * (nt + 1) / 2;
   const int64_t total = (int64_t)ntiles * ntarg;
@@ -449,16 +985,14 @@ int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
   const size_t esz = (x_dtype == RQ_F32) ? 4 : 2;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (((size_t)ldx * esz) % 16 == 0);
   int tail = 0, S = 1;
-  const int slots = hessian_slots();
-  if (ws) tail_split(total, (ntok + HKC - 1) / HKC, slots, &tail, &S);
-  const int64_t need = hessian_ws_bytes(tail, S, slots);
-  if (tail > 0 && (ws_bytes < need || (reinterpret_cast<uintptr_t>(ws) & 255))) {
+  if (aligned) tail_split(total, (ntok + HKC - 1) / HKC, hessian_slots(), &tail, &S);
+  if (tail > 0 && ws_bytes < hessian_ws_bytes(tail, S)) {
     tail = 0;                                     // no room: whole items only
     S = 1;
   }
   const int full = (int)(total - tail);
   int* cnt = tail > 0 ? reinterpret_cast<int*>(ws) : nullptr;
-  float* wsf = tail > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + hessian_cnt_bytes(slots))
+  float* wsf = tail > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + hessian_cnt_bytes())
                         : nullptr;
   dim3 grid((unsigned)(full + (int64_t)tail * S)), block(HTHREADS);
   if (x_dtype == RQ_F16)
@@ -476,6 +1010,12 @@ int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
 
 }  // namespace
 
+extern "C" int rq_hessian_math(int mode) {
+  if (mode < 0) return g_hmath.load();
+  if (mode != RQ_HMATH_SPLIT16 && mode != RQ_HMATH_FP32) return RQ_EINVAL;
+  return g_hmath.exchange(mode);
+}
+
 extern "C" int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets) {
   if (ntok < 0 || C <= 0 || ntargets <= 0) return RQ_EINVAL;
   const int nt = (C + HT - 1) / HT;
@@ -483,9 +1023,10 @@ extern "C" int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets)
   for (int t0 = 0; t0 < ntargets; t0 += HMAXT) {   // per launch of at most 32 targets
     const int n = (ntargets - t0 < HMAXT) ? (ntargets - t0) : HMAXT;
     int tail = 0, S = 1;
-    const int slots = hessian_slots();
-    tail_split((int64_t)nt * (nt + 1) / 2 * n, (ntok + HKC - 1) / HKC, slots, &tail, &S);
-    const int64_t b = hessian_ws_bytes(tail, S, slots);
+    tail_split((int64_t)nt * (nt + 1) / 2 * n, (ntok + HKC - 1) / HKC, hessian_slots(), &tail, &S);
+    int64_t b = hessian_ws_bytes(tail, S);
+    const int64_t bs = split_ws_need(ntok, C, n);
+    if (bs > b) b = bs;
     if (b > need) need = b;
   }
   return need;

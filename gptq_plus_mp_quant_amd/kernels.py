@@ -5,6 +5,7 @@ HIP stream of the tensors' device, and raises ``RuntimeError`` on a non-zero sta
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import torch
@@ -62,6 +63,24 @@ def hessian_workspace(x, ntargets):
         ws = torch.zeros(need, dtype=torch.uint8, device=x.device)
         _HWS[key] = ws
     return ws, ws.numel()
+
+
+HESSIAN_MATH = {"split16": nat.RQ_HMATH_SPLIT16, "fp32": nat.RQ_HMATH_FP32}
+
+
+@contextlib.contextmanager
+def hessian_math(mode):
+    """Select the Hessian kernel for fp16 / bf16 inputs inside the block: "split16" (default;
+    exact fp32 products from three 16-bit MFMA products) or "fp32" (fp32 MFMA).  The choice is
+    process-wide; fp32 inputs always use the fp32 kernel."""
+    lib = nat.load()
+    prev = int(lib.rq_hessian_math(HESSIAN_MATH[mode]))
+    if prev < 0:
+        raise RuntimeError(f"rq_hessian_math failed with status {prev}")
+    try:
+        yield
+    finally:
+        lib.rq_hessian_math(prev)
 
 
 def hessian_accum(x, sal, H, act_sq):

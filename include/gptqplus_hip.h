@@ -45,13 +45,24 @@ int rq_version(void);
  * H[g] (C x C, fp32, g < G) += X^T diag(sal[:, g]) X over `ntok` tokens, upper-triangle
  * 128x128 tiles only (the lower triangle is filled by rq_hessian_finalize);
  * act_sq[c] += sum_t x[t,c]^2.  X is [ntok, C] (row stride ldx) of type x_dtype,
- * sal is [ntok, G] fp32 (row stride ld_sal).  fp32 MFMA, deterministic (bitwise
- * reproducible).  workspace (optional, device, 256-byte aligned, zero-filled when first
+ * sal is [ntok, G] fp32 (row stride ld_sal).  fp32 products accumulated in fp32
+ * (rq_hessian_math), deterministic (bitwise reproducible).  workspace (optional, device, 256-byte aligned, zero-filled when first
  * allocated; the library leaves it reusable): with at least rq_hessian_workspace_bytes
  * bytes the items of a partly filled last round are split along the tokens so the launch
  * ends with full rounds; NULL runs whole items only.  Calls that overlap in time on one
  * device need separate workspaces. */
 int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets);
+
+/* Kernel choice for fp16 / bf16 X (process-wide; fp32 X always uses the fp32 MFMA kernel).
+ * RQ_HMATH_SPLIT16 (default): each fp32 product x * fl32(x * s) is formed exactly from three
+ * 16-bit MFMA products (the weighted operand split into three 16-bit pieces after an exact
+ * power-of-two column scaling) and accumulated in fp32; it needs the workspace (with less
+ * than rq_hessian_workspace_bytes the fp32 kernel runs instead).  RQ_HMATH_FP32: fp32
+ * MFMA on converted operands.  mode < 0 queries.  Returns the previous mode, or RQ_EINVAL.
+ * No counterpart in the reference (its bmm runs in fp32, gptq_plus_utils.py:845-847). */
+#define RQ_HMATH_SPLIT16 0
+#define RQ_HMATH_FP32 1
+int rq_hessian_math(int mode);
 int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
                      const float* sal, int64_t ld_sal, int G, float* H, float* act_sq,
                      void* workspace, int64_t workspace_bytes, void* stream);

@@ -104,16 +104,38 @@ CFGS = [
 
 @pytest.mark.parametrize("cfg", CFGS, ids=[c["name"] for c in CFGS])
 def test_gptq_vs_oracle(cfg, tmp_path):
+    """H against the oracle's (fp32 rounding only).  act_order ranks diag(H), and on these
+    sizes the closest pair of diagonal entries can lie within that rounding, so the codes are
+    compared with the oracle run on the kernel's own H (the quantization chain isolated from
+    the summation order of H); any difference of the two orders must be such a near tie."""
     X, W, _, _ = synth(sum(map(ord, cfg["name"])), cfg["R"], cfg["C"], 1, 6, 256)
-    o = GPTQOracle(W)
-    o.quantizer = make_quantizer(cfg["bits"], cfg["sym"])
-    for j in range(X.shape[0]):
-        o.add_batch(X[j].unsqueeze(0))
-    H_o = o.H.clone()
-    res = o.fasterquant(blocksize=cfg["B"], groupsize=cfg["gs"], actorder=cfg["act"],
-                        static_groups=cfg["act"], stable_ties=True)
+
+    def oracle(H=None):
+        o = GPTQOracle(W)
+        o.quantizer = make_quantizer(cfg["bits"], cfg["sym"])
+        for j in range(X.shape[0]):
+            o.add_batch(X[j].unsqueeze(0))
+        H_own = o.H.clone()
+        if H is not None:
+            o.H = H.clone()
+        res = o.fasterquant(blocksize=cfg["B"], groupsize=cfg["gs"], actorder=cfg["act"],
+                            static_groups=cfg["act"], stable_ties=True)
+        return H_own, res
+
     g, layer = _drop_in(W, X, cfg["bits"], cfg["sym"])
-    assert rel_fro(_finalized_H(g), H_o) <= 1e-5
+    H_gpu = _finalized_H(g).cpu()
+    H_o, res_own = oracle()
+    assert rel_fro(H_gpu, H_o) <= 1e-5
+    if cfg["act"]:
+        d_o, d_g = torch.diagonal(H_o), torch.diagonal(H_gpu)
+        p_o = torch.argsort(d_o, descending=True, stable=True)
+        p_g = torch.argsort(d_g, descending=True, stable=True)
+        moved = p_o != p_g
+        if moved.any():                              # only near ties may change places
+            gap = (d_o[p_o[moved]] - d_o[p_g[moved]]).abs() / d_o[p_o[moved]]
+            print(f"{cfg['name']}: act_order differs at {int(moved.sum())} positions, rel gap {float(gap.max()):.2e}")
+            assert float(gap.max()) <= 1e-5
+    _, res = oracle(H_gpu)
     g.fasterquant(blocksize=cfg["B"], groupsize=cfg["gs"], actorder=cfg["act"], static_groups=cfg["act"],
                   export_to_et=True)
     torch.cuda.synchronize()
@@ -123,7 +145,7 @@ def test_gptq_vs_oracle(cfg, tmp_path):
     assert flips <= n // 1000
     Xf = X.float().reshape(-1, cfg["C"])
     e_gpu = reconstruction_error(W.float(), layer.weight.data.float().cpu(), Xf)
-    e_ref = reconstruction_error(W.float(), res.Q.float(), Xf)
+    e_ref = reconstruction_error(W.float(), res_own.Q.float(), Xf)
     assert abs(e_gpu - e_ref) <= 0.005 * e_ref
     # the packed export reproduces the layer weight for every group layout
     assert torch.equal(dequantize_packed(g.export_packed()).cpu(), layer.weight.data.cpu())

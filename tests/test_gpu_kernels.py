@@ -72,9 +72,10 @@ def test_hessian_is_deterministic_and_scaled():
 
 @pytest.mark.parametrize("C,G", [(1000, 3), (384, 2)])   # larger first: the second reuses its workspace
 def test_hessian_tail_slices_match_whole_items(C, G):
-    """The split of a partly filled last round into token slices (workspace given) changes
-    only the summation order: same result as whole items to fp32 rounding, and bitwise
-    reproducible from call to call."""
+    """fp32-MFMA kernel: the split of a partly filled last round into token slices (workspace
+    given) changes only the summation order: same result as whole items to fp32 rounding, and
+    bitwise reproducible from call to call.  (The split-operand kernel's slices are covered in
+    test_gpu_hessian_split.py.)"""
     r = rng(40 + C)
     n = 4096
     x = torch.from_numpy(r.standard_normal((n, C), dtype=np.float32)).half().to(DEV)
@@ -85,9 +86,10 @@ def test_hessian_tail_slices_match_whole_items(C, G):
     for use_ws in (False, True, True):
         H = torch.zeros(G, C, C, device=DEV)
         act = torch.zeros(C, device=DEV)
-        nat.call("rq_hessian_accum", nat.ptr(x), nat.RQ_F16, n, C, C, nat.ptr(sal), G, G, nat.ptr(H),
-                 nat.ptr(act), nat.ptr(ws) if use_ws else None, nbytes if use_ws else 0,
-                 nat.stream_of(x.device))
+        with K.hessian_math("fp32"):
+            nat.call("rq_hessian_accum", nat.ptr(x), nat.RQ_F16, n, C, C, nat.ptr(sal), G, G, nat.ptr(H),
+                     nat.ptr(act), nat.ptr(ws) if use_ws else None, nbytes if use_ws else 0,
+                     nat.stream_of(x.device))
         outs.append((H, act))
     torch.cuda.synchronize()
     assert torch.equal(outs[1][0], outs[2][0]) and torch.equal(outs[1][1], outs[2][1])
