@@ -349,22 +349,21 @@ __global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
 // applied, harmlessly.  The epilogue multiplies the tile by 2^-e (exact) before adding it
 // to H.
 //
-// Tiles are 256 rows (x side) x 128 columns (w side), four waves of 128 x 64 (4 x 2 MFMA
-// blocks of 32 x 32), two workgroups per CU.  A tile pair-row p (rows 256p..) meets column
-// block c (columns 128c..) when 2p <= c; on c == 2p the lower 128 rows lie below the
-// diagonal and their two waves skip the MFMAs.  Slabs of 32 tokens are staged token-minor in
-// LDS (80-byte rows: 64 B of tokens + 16 B pad; the 16-byte token chunk k of row r sits at
-// chunk k ^ ((r >> 4) & 3), which keeps the transposing 16-byte writes and the fragment reads
-// free of bank conflicts).  act_square and the per-column maxima come from a separate pass
-// over X (k_xstats / k_xfinish).
-constexpr int XR = 256;          // tile rows (exact x operand)
-constexpr int XC = 128;          // tile columns (split weighted operand)
-constexpr int XK = 32;           // tokens per slab
-constexpr int XRS = 80;          // LDS row stride in bytes
+// Operands come straight from global memory.  A pre-pass (k_xprep) writes the chunk
+// transposed, X^T [C][ntok_p] (ntok_p = ntok rounded up to 256, zero padded), and each
+// target's saliency as a contiguous zero-padded vector, and reduces act_square and the
+// per-column / per-target maxima.  With tokens contiguous, one lane's MFMA fragment -- 8
+// consecutive tokens of one column -- is a single 16-byte load, so the product kernel needs
+// no LDS staging and no barriers.  A workgroup (4 waves, one per SIMD, one workgroup per CU)
+// owns a 256 x 256 tile of the upper triangle; wave w owns columns 64w..64w+63 against all
+// 256 rows (8 x 2 blocks of 32 x 32: 256 accumulators per lane).  Per 16 tokens a wave loads
+// 8 row fragments, 2 column fragments and 8 saliencies, splits the column fragments in
+// registers and issues 3 x 16 = 48 MFMAs, with the next 16 tokens' loads in flight.
+constexpr int XT = 256;          // workgroup tile edge
 constexpr int XNP = 3;           // pieces of the weighted operand
 constexpr int XTHREADS = 256;
-constexpr int XPART = XR * XC;   // floats of one partial tile
-constexpr int XSR = 2;           // pair rows per super-row (tile order)
+constexpr int XPART = XT * XT;   // floats of one partial tile
+constexpr int XTOK = 256;        // token padding of the transposed chunk / pre-pass block
 
 template <typename TX>
 struct XType;
@@ -397,212 +396,212 @@ struct XType<__hip_bfloat16> {
   }
 };
 
-// Map an item index to (pair row p, column block c), 2p <= c < nt, in super-row order: XSR
-// pair rows at a time, each super-row walked column by column.
-__device__ __forceinline__ int ramp_sum(int n) {   // sum_{v<n} (floor(v/2) + 1)
-  const int h = n >> 1;
-  return h * (h + 1) + ((n & 1) ? h + 1 : 0);
-}
-__device__ __forceinline__ void pair_tile(int idx, int nt, int npr, int& p, int& c) {
-  int P0 = 0, rem = idx;
-  for (;;) {
-    const int h = min(XSR, npr - P0);
-    const int V = nt - 2 * P0;                      // columns of this super-row
-    const int cnt = (V <= 2 * h) ? ramp_sum(V) : ramp_sum(2 * h) + (V - 2 * h) * h;
-    if (rem < cnt) break;
-    rem -= cnt;
-    P0 += h;
-  }
-  const int h = min(XSR, npr - P0);
-  const int ramp = ramp_sum(2 * h);
-  if (rem >= ramp) {
-    rem -= ramp;
-    c = 2 * P0 + 2 * h + rem / h;
-    p = P0 + rem % h;
-    return;
-  }
-  for (int v = 0;; ++v) {
-    const int k = (v >> 1) + 1;
-    if (rem < k) {
-      c = 2 * P0 + v;
-      p = P0 + rem;
-      return;
-    }
-    rem -= k;
-  }
-}
-
-// 16-bit element cc (0..3) of a raw 4-column group.
-__device__ __forceinline__ uint32_t elem4(uint2 r, int cc) {
-  const uint32_t w = (cc < 2) ? r.x : r.y;
-  return (cc & 1) ? (w >> 16) : (w & 0xffffu);
-}
-
-template <bool EDGE>
-__device__ __forceinline__ void xload_a(const uint16_t* __restrict__ X, int64_t ntok, int64_t ldx,
-                                        int C, int64_t t0, int c0, uint2 (&r)[8]) {
+// 8 tokens of one column: w = fl32(x * s) * 2^e split into three 16-bit fragments.
+// (fma(x, s, 0) is rn(x * s); fma(-p, 1, w) is the exact w - p.  Written as fma so that the
+// fp16 -> fp32 conversions can fold into v_fma_mix.)
+template <typename TX>
+__device__ __forceinline__ void split8(uint4 x, float4 s0, float4 s1, float sc, uint4 (&p)[XNP]) {
+  typedef XType<TX> T;
+  const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+  uint32_t o[XNP][4];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int64_t t = t0 + k;
-    if (!EDGE) {
-      r[k] = (t < ntok) ? *reinterpret_cast<const uint2*>(X + t * ldx + c0) : make_uint2(0, 0);
-    } else {
-      uint32_t e[4];
+  for (int m = 0; m < 4; ++m) {
+    float a = __builtin_fmaf(T::lo(xw[m]), s[2 * m], 0.0f);
+    float b = __builtin_fmaf(T::hi(xw[m]), s[2 * m + 1], 0.0f);
+    a = a * sc;
+    b = b * sc;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) e[q] = (t < ntok && c0 + q < C) ? X[t * ldx + c0 + q] : 0u;
-      r[k] = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+    for (int k = 0; k < XNP; ++k) {
+      const uint32_t u = T::pack(a, b);
+      o[k][m] = u;
+      if (k + 1 < XNP) {
+        a = __builtin_fmaf(-T::lo(u), 1.0f, a);
+        b = __builtin_fmaf(-T::hi(u), 1.0f, b);
+      }
     }
   }
-}
-
-template <bool EDGE>
-__device__ __forceinline__ void xload_b(const uint16_t* __restrict__ X, int64_t ntok, int64_t ldx,
-                                        int C, int64_t t0, int c0, const float* __restrict__ sal,
-                                        int64_t ld_sal, uint32_t (&r)[8], float (&s)[8]) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int64_t t = t0 + k;
-    s[k] = (t < ntok) ? sal[t * ld_sal] : 0.0f;
-    if (!EDGE) {
-      r[k] = (t < ntok) ? *reinterpret_cast<const uint32_t*>(X + t * ldx + c0) : 0u;
-    } else {
-      const uint32_t e0 = (t < ntok && c0 < C) ? X[t * ldx + c0] : 0u;
-      const uint32_t e1 = (t < ntok && c0 + 1 < C) ? X[t * ldx + c0 + 1] : 0u;
-      r[k] = e0 | (e1 << 16);
-    }
-  }
+  for (int k = 0; k < XNP; ++k) p[k] = make_uint4(o[k][0], o[k][1], o[k][2], o[k][3]);
 }
 
-__device__ __forceinline__ int xchunk(int row, int k) { return row * XRS + 16 * (k ^ ((row >> 4) & 3)); }
+// LDS ring: XDEPTH stages (separate arrays) of one 16-token step each.  A stage holds the
+// workgroup's 8 row fragments (each wave fetches 2) and, per wave, its 2 raw column fragments
+// and its 8 saliencies (as two 16-byte loads per lane); every fragment is 64 lanes x 16 B,
+// placed by lane, so a lane reads back exactly its own MFMA operand.  Step k of a tile (or
+// token slice) starting at kbeg lives in stage (k - kbeg) % XDEPTH; the loop is unrolled by
+// XDEPTH so that every stage index is a compile-time constant: the LDS reads are ordinary
+// loads (the compiler places their lgkmcnt waits), and alias analysis can tell the staging
+// writes in flight to other stages from the stage being read.
+constexpr int XDEPTH = 4;
+constexpr int XA_BYTES = 8 * 1024;                  // row fragments of a stage
+constexpr int XW_BYTES = 4 * 1024;                  // per wave: 2 column fragments + 2 saliency blocks
+constexpr int XSTAGE = XA_BYTES + 4 * XW_BYTES;     // 24 KB
 
-template <typename TX, bool EDGE>
-__device__ __forceinline__ void split_tile(const uint16_t* __restrict__ X, int64_t ntok, int64_t ldx,
-                                           int C, const float* __restrict__ sal, int64_t ld_sal,
-                                           const float* __restrict__ scl, float* __restrict__ Hg,
-                                           int R0, int C0, bool lower_live, uint8_t* As, uint8_t* Bs,
-                                           int64_t sbeg, int64_t send, float* __restrict__ part) {
+struct XStages {
+  uint8_t* s[XDEPTH];
+};
+
+// s_waitcnt with only the vector-memory counter limited (gfx9 encoding).
+#define XWAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+__device__ __forceinline__ void lds_dma16(const void* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+}
+
+// Stage step k into `st`: row fragments 2w, 2w+1, this wave's column fragments and saliencies.
+__device__ __forceinline__ void stage_step(uint8_t* st, const uint16_t* baseA, const uint32_t (&oa)[2],
+                                           const uint16_t* baseB, const uint32_t (&ob)[2], const float* sbase,
+                                           int wave, int64_t k) {
+  asm volatile("" : "+s"(k));
+  const uint16_t* pA = baseA + 16 * k;
+  const uint16_t* pB = baseB + 16 * k;
+  uint8_t* w = st + XA_BYTES + wave * XW_BYTES;
+  lds_dma16(pA + oa[0], st + (2 * wave) * 1024);
+  lds_dma16(pA + oa[1], st + (2 * wave + 1) * 1024);
+  lds_dma16(pB + ob[0], w);
+  lds_dma16(pB + ob[1], w + 1024);
+  lds_dma16(sbase + 16 * k, w + 2048);
+  lds_dma16(sbase + 16 * k + 4, w + 3072);
+}
+
+// This wave's column fragments and saliencies of a staged step, split into pieces.
+template <typename TX>
+__device__ __forceinline__ void split_staged(const uint8_t* st, int wave, int lane, const float (&sc)[2],
+                                             uint4 (&p)[2][XNP]) {
+  const uint8_t* w = st + XA_BYTES + wave * XW_BYTES + lane * 16;
+  const uint4 b0 = *reinterpret_cast<const uint4*>(w);
+  const uint4 b1 = *reinterpret_cast<const uint4*>(w + 1024);
+  const float4 s0 = *reinterpret_cast<const float4*>(w + 2048);
+  const float4 s1 = *reinterpret_cast<const float4*>(w + 3072);
+  split8<TX>(b0, s0, s1, sc[0], p[0]);
+  split8<TX>(b1, s0, s1, sc[1], p[1]);
+}
+
+// One 16-token step k of a wave.  KP = (k - kbeg) % 2 selects the piece and row-fragment
+// buffers; CUR, NXT, FILL are the stages of steps k, k+1 and k+XDEPTH-1.  This wave's staging
+// of steps k and k+1 was issued XDEPTH-1 and XDEPTH-2 steps ago and is followed by the 6
+// staging loads of each step since, so vmcnt(6) covers both whatever the issue order within a
+// step; after the barrier the other waves' row fragments of steps k and k+1 are in LDS too (the
+// barrier also orders every read of the FILL stage, done in earlier steps, before its refill).
+// Then: stage step k+XDEPTH-1; read the row fragments of k+1 into the other buffer; split this
+// wave's column fragments of k+1 while the 48 MFMAs of step k run on the row fragments read one
+// step ago.  A bare s_barrier: the fence of __syncthreads would wait for every staging load in
+// flight.
+template <typename TX, int KP, int CUR, int NXT, int FILL>
+__device__ __forceinline__ void split_step(uint4 (&p)[2][2][XNP], uint4 (&a)[2][8], floatx16 (&acc)[8][2],
+                                           const XStages& L, const uint16_t* baseA, const uint32_t (&oa)[2],
+                                           const uint16_t* baseB, const uint32_t (&ob)[2], const float* sbase,
+                                           const float (&sc)[2], int wave, int lane, int64_t k, int64_t last) {
   typedef XType<TX> T;
   typedef typename T::v8 v8;
+  constexpr int NP = 1 - KP;
+  XWAIT_VM(6);
+  __builtin_amdgcn_s_barrier();
+  stage_step(L.s[FILL], baseA, oa, baseB, ob, sbase, wave, min(k + XDEPTH - 1, last));
+  const uint8_t* nx = L.s[NXT] + lane * 16;
+#pragma unroll
+  for (int bi = 0; bi < 8; ++bi) a[NP][bi] = *reinterpret_cast<const uint4*>(nx + bi * 1024);
+  split_staged<TX>(L.s[NXT], wave, lane, sc, p[NP]);
+#pragma unroll
+  for (int q = XNP - 1; q >= 0; --q)
+#pragma unroll
+    for (int bi = 0; bi < 8; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < 2; ++bj)
+        acc[bi][bj] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][bj][q]), acc[bi][bj]);
+}
+
+template <typename TX>
+__device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XTr, int64_t ldt, int C,
+                                           const float* __restrict__ sg, const float* __restrict__ scl,
+                                           float* __restrict__ Hg, int R0, int C0, int64_t kbeg,
+                                           int64_t kend, float* __restrict__ part, const XStages& L) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wr = wave >> 1, wc = wave & 1;
-  const bool live = (wr == 0) || lower_live;
-  const int q = tid & 63;          // staging: row side columns R0 + 4q.., w side C0 + 2q..
-  const int w8 = tid >> 6;         // staging: tokens 8 * w8 .. + 7 of the slab
+  const int fr = lane & 31, fh = lane >> 5;
+  const int Cw = C0 + 64 * wave;
+  const int Cb = min(Cw, C - 1);
 
+  // Fragment sources: a uniform base per side plus a 32-bit lane offset (in elements, below
+  // 256 * ldt).  Rows / columns past C read column C-1; their products are discarded.
+  const uint16_t* baseA = XTr + (int64_t)R0 * ldt;
+  const uint16_t* baseB = XTr + (int64_t)Cb * ldt;
+  uint32_t oa[2], ob[2];
   float sc[2];
 #pragma unroll
-  for (int cc = 0; cc < 2; ++cc) sc[cc] = (C0 + 2 * q + cc < C) ? scl[C0 + 2 * q + cc] : 1.0f;
-
-  floatx16 acc[4][2];
+  for (int h = 0; h < 2; ++h)
+    oa[h] = (uint32_t)((min(R0 + 32 * (2 * wave + h) + fr, C - 1) - R0) * ldt + 8 * fh);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int bj = 0; bj < 2; ++bj) {
+    const int c = min(Cw + 32 * bj + fr, C - 1);
+    ob[bj] = (uint32_t)((c - Cb) * ldt + 8 * fh);
+    sc[bj] = scl[c];
+  }
+  const float* sbase = sg + 8 * fh;
+
+  floatx16 acc[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  uint2 ra[8];
-  uint32_t rb[8];
-  float s[8];
-  xload_a<EDGE>(X, ntok, ldx, C, sbeg * XK + 8 * w8, R0 + 4 * q, ra);
-  xload_b<EDGE>(X, ntok, ldx, C, sbeg * XK + 8 * w8, C0 + 2 * q, sal, ld_sal, rb, s);
-
-  const int fr = lane & 31;
-  const int fh = lane >> 5;
-
-  for (int64_t sidx = sbeg; sidx < send; ++sidx) {
-    __syncthreads();                 // previous slab fully consumed
-    // x side: transpose 8 tokens x 4 columns into four 16-byte token runs
+  // Prologue: stage steps kbeg .. kbeg+XDEPTH-2 into stages 0 .. XDEPTH-2, read the row
+  // fragments and split the column fragments of kbeg.  Steps past the end re-read the last one;
+  // their values are never used.
+  const int64_t last = kend - 1;
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      uint4 d;
-      d.x = elem4(ra[0], cc) | (elem4(ra[1], cc) << 16);
-      d.y = elem4(ra[2], cc) | (elem4(ra[3], cc) << 16);
-      d.z = elem4(ra[4], cc) | (elem4(ra[5], cc) << 16);
-      d.w = elem4(ra[6], cc) | (elem4(ra[7], cc) << 16);
-      *reinterpret_cast<uint4*>(As + xchunk(4 * q + cc, w8)) = d;
-    }
-    // w side: w = fl32(x * s) * 2^e, split into three exact 16-bit pieces
+  for (int h = 0; h < XDEPTH - 1; ++h) stage_step(L.s[h], baseA, oa, baseB, ob, sbase, wave, min(kbeg + h, last));
+  uint4 p[2][2][XNP];
+  uint4 a[2][8];
+  XWAIT_VM(6 * (XDEPTH - 2));         // this wave's staging of step kbeg
+  __builtin_amdgcn_s_barrier();       // and the other waves'
+  {
+    const uint8_t* c0 = L.s[0] + lane * 16;
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-      float w[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float x = cc ? T::hi(rb[k]) : T::lo(rb[k]);
-        const float ws = x * s[k];
-        w[k] = ws * sc[cc];
-      }
-      uint32_t p[XNP][4];
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        float a = w[2 * m], b = w[2 * m + 1];
-#pragma unroll
-        for (int k = 0; k < XNP; ++k) {
-          const uint32_t u = T::pack(a, b);
-          p[k][m] = u;
-          if (k + 1 < XNP) {
-            a = a - T::lo(u);
-            b = b - T::hi(u);
-          }
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < XNP; ++k)
-        *reinterpret_cast<uint4*>(Bs + k * (XC * XRS) + xchunk(2 * q + cc, w8)) =
-            make_uint4(p[k][0], p[k][1], p[k][2], p[k][3]);
-    }
-    __syncthreads();
-    if (sidx + 1 < send) {           // next slab in flight while this one is multiplied
-      xload_a<EDGE>(X, ntok, ldx, C, (sidx + 1) * XK + 8 * w8, R0 + 4 * q, ra);
-      xload_b<EDGE>(X, ntok, ldx, C, (sidx + 1) * XK + 8 * w8, C0 + 2 * q, sal, ld_sal, rb, s);
-    }
-    if (live) {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int kc = 2 * ks + fh;  // this lane's 8-token chunk
-        v8 a[4], b[XNP][2];
-#pragma unroll
-        for (int bi = 0; bi < 4; ++bi)
-          a[bi] = *reinterpret_cast<const v8*>(As + xchunk(128 * wr + 32 * bi + fr, kc));
-#pragma unroll
-        for (int k = 0; k < XNP; ++k)
-#pragma unroll
-          for (int bj = 0; bj < 2; ++bj)
-            b[k][bj] = *reinterpret_cast<const v8*>(Bs + k * (XC * XRS) + xchunk(64 * wc + 32 * bj + fr, kc));
-#pragma unroll
-        for (int k = XNP - 1; k >= 0; --k)
-#pragma unroll
-          for (int bi = 0; bi < 4; ++bi)
-#pragma unroll
-            for (int bj = 0; bj < 2; ++bj) acc[bi][bj] = T::mfma(a[bi], b[k][bj], acc[bi][bj]);
-      }
-    }
+    for (int bi = 0; bi < 8; ++bi) a[0][bi] = *reinterpret_cast<const uint4*>(c0 + bi * 1024);
+    split_staged<TX>(L.s[0], wave, lane, sc, p[0]);
   }
+
+  const int64_t n = kend - kbeg;
+  int64_t k = kbeg;
+  for (; k + 4 <= kend; k += 4) {
+    split_step<TX, 0, 0, 1, 3>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k, last);
+    split_step<TX, 1, 1, 2, 0>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k + 1, last);
+    split_step<TX, 0, 2, 3, 1>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k + 2, last);
+    split_step<TX, 1, 3, 0, 2>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k + 3, last);
+  }
+  const int rem = (int)(n & 3);
+  if (rem > 0) split_step<TX, 0, 0, 1, 3>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k, last);
+  if (rem > 1) split_step<TX, 1, 1, 2, 0>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k + 1, last);
+  if (rem > 2) split_step<TX, 0, 2, 3, 1>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k + 2, last);
+  XWAIT_VM(0);                        // no staging left in flight when the workgroup moves on
+
 
   if (part) {
     // token slice: hand the (still scaled) partial tile to the workspace
 #pragma unroll
-    for (int bi = 0; bi < 4; ++bi)
+    for (int bi = 0; bi < 8; ++bi)
 #pragma unroll
       for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
         for (int e = 0; e < 16; ++e) part[((bi * 2 + bj) * 16 + e) * XTHREADS + tid] = acc[bi][bj][e];
     return;
   }
-  if (!live) return;
   // H[g][i][j] += acc * 2^-e_j   (32x32 block layout: i = 8*(e/4) + 4*(lane/32) + e%4, j = lane%32)
 #pragma unroll
   for (int bj = 0; bj < 2; ++bj) {
-    const int j = C0 + 64 * wc + 32 * bj + fr;
+    const int j = Cw + 32 * bj + fr;
     const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
 #pragma unroll
-    for (int bi = 0; bi < 4; ++bi)
+    for (int bi = 0; bi < 8; ++bi)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int i = R0 + 128 * wr + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
-        if (!EDGE || (i < C && j < C)) {
+        const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
+        if (i < C && j < C) {
           float* ph = Hg + (int64_t)i * C + j;
           *ph = *ph + acc[bi][bj][e] * inv;
         }
@@ -613,19 +612,17 @@ __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ X, int64
 // The last slice of a split item adds the S partials (in slice order) to H.
 __device__ __forceinline__ void reduce_split_slices(const float* __restrict__ part0, int S,
                                                     float* __restrict__ Hg, const float* __restrict__ scl,
-                                                    int R0, int C0, int C, bool lower_live) {
+                                                    int R0, int C0, int C) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wr = wave >> 1, wc = wave & 1;
-  if (wr == 1 && !lower_live) return;
   const int fr = lane & 31, fh = lane >> 5;
 #pragma unroll
   for (int bj = 0; bj < 2; ++bj) {
-    const int j = C0 + 64 * wc + 32 * bj + fr;
+    const int j = C0 + 64 * wave + 32 * bj + fr;
     const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
-#pragma unroll
-    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll 1
+    for (int bi = 0; bi < 8; ++bi)
 #pragma unroll 4
       for (int e = 0; e < 16; ++e) {
         const int slot = ((bi * 2 + bj) * 16 + e) * XTHREADS + tid;
@@ -633,7 +630,7 @@ __device__ __forceinline__ void reduce_split_slices(const float* __restrict__ pa
         for (int qq = 1; qq < S; ++qq)
           sum += __hip_atomic_load(part0 + (int64_t)qq * XPART + slot, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
-        const int i = R0 + 128 * wr + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
+        const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
         if (i < C && j < C) {
           float* ph = Hg + (int64_t)i * C + j;
           *ph = *ph + sum * inv;
@@ -643,21 +640,23 @@ __device__ __forceinline__ void reduce_split_slices(const float* __restrict__ pa
 }
 
 template <typename TX>
-__global__ __launch_bounds__(XTHREADS, 2) void k_hessian_split(
-    const uint16_t* __restrict__ X, int64_t ntok, int64_t ldx, int C, HTargets tg,
-    const float* __restrict__ scale, int ntarg, int nt, int npr, int nitems, bool vec_ok, int full,
+__global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
+    const uint16_t* __restrict__ XTr, int64_t ldt, int C, const float* __restrict__ sT, int64_t lds_stride,
+    const float* __restrict__ scale, HTargets tg, int ntarg, int nt, int ntiles, int64_t nks, int full,
     int S, float* __restrict__ ws, int* __restrict__ cnt) {
-  __shared__ __attribute__((aligned(16))) uint8_t As[XR * XRS];
-  __shared__ __attribute__((aligned(16))) uint8_t Bs[XNP * XC * XRS];
+  __shared__ __attribute__((aligned(16))) uint8_t lds0[XSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds1[XSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds2[XSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds3[XSTAGE];
   __shared__ int last_slice;
-
+  static_assert(XDEPTH == 4, "stage arrays");
+  const XStages L{{lds0, lds1, lds2, lds3}};
   // Same schedule as k_hessian_accum: XCD-aware order for whole items, then the token
   // slices of the tail items.
-  const int total = nitems * ntarg;
+  const int total = ntiles * ntarg;
   const int b = blockIdx.x;
-  const int64_t nslab = (ntok + XK - 1) / XK;
   int logical, slice = -1;
-  int64_t sbeg = 0, send = nslab;
+  int64_t kbeg = 0, kend = nks;
   if (b < full) {
     const int per = full / 8, rem8 = full % 8;
     const int xcd = b % 8, idx = b / 8;
@@ -666,26 +665,19 @@ __global__ __launch_bounds__(XTHREADS, 2) void k_hessian_split(
     const int tb = b - full;
     logical = full + tb / S;
     slice = tb % S;
-    sbeg = nslab * slice / S;
-    send = nslab * (slice + 1) / S;
+    kbeg = nks * slice / S;
+    kend = nks * (slice + 1) / S;
   }
   if (logical >= total) return;
   const int g = logical % ntarg;
-  int p, c;
-  pair_tile(logical / ntarg, nt, npr, p, c);
-  const int R0 = p * XR, C0 = c * XC;
-  const bool lower_live = (2 * p + 1 <= c) && (R0 + XR / 2 < C);
+  int ti, tj;
+  upper_tile_blocked(logical / ntarg, nt, ti, tj);
+  const int R0 = ti * XT, C0 = tj * XT;
   float* Hg = tg.H[g];
   const float* scl = scale + (int64_t)g * C;
-  const bool interior = vec_ok && (R0 + XR <= C) && (C0 + XC <= C);
   float* part0 = (slice >= 0) ? ws + (int64_t)(logical - full) * S * XPART : nullptr;
   float* part = part0 ? part0 + (int64_t)slice * XPART : nullptr;
-  if (interior)
-    split_tile<TX, false>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], scl, Hg, R0, C0, lower_live, As, Bs,
-                          sbeg, send, part);
-  else
-    split_tile<TX, true>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], scl, Hg, R0, C0, lower_live, As, Bs,
-                         sbeg, send, part);
+  split_tile<TX>(XTr, ldt, C, sT + (int64_t)g * lds_stride, scl, Hg, R0, C0, kbeg, kend, part, L);
   if (!part) return;
   __threadfence();
   __syncthreads();
@@ -698,45 +690,88 @@ __global__ __launch_bounds__(XTHREADS, 2) void k_hessian_split(
   __syncthreads();
   if (!last_slice) return;
   __threadfence();
-  reduce_split_slices(part0, S, Hg, scl, R0, C0, C, lower_live);
+  reduce_split_slices(part0, S, Hg, scl, R0, C0, C);
 }
 
-// Pass over X before the split kernel: per token chunk, each column's max |x| and
-// sum_t x^2 (in token order), and each target's max |s|.
+// Pre-pass over one 64-column x 256-token block of X: the transposed block into X^T (zeros
+// past ntok), each column's max |x| and sum_t x^2 (in token order) for this token block, and
+// (first column block only) each target's saliency, contiguous and zero padded, with its
+// max |s|.  Two tokens of one column share a 32-bit LDS word; the row stride of 129 words
+// keeps the transposing writes free of bank conflicts.
+constexpr int XPC = 64;            // columns per pre-pass block
+constexpr int XPRS = XTOK / 2 + 1; // LDS row stride in words
 template <typename TX>
-__global__ __launch_bounds__(256) void k_xstats(const TX* __restrict__ X, int64_t ntok, int64_t ldx,
-                                                int C, int64_t tpc, HTargets tg, int ntarg,
-                                                float* __restrict__ mpart, float* __restrict__ apart,
-                                                float* __restrict__ spart) {
+__global__ __launch_bounds__(256) void k_xprep(const TX* __restrict__ X, int64_t ntok, int64_t ldx, int C,
+                                               bool vec_ok, uint16_t* __restrict__ XTr, int64_t ldt,
+                                               HTargets tg, int ntarg, float* __restrict__ sT, int64_t lds,
+                                               float* __restrict__ mpart, float* __restrict__ apart,
+                                               float* __restrict__ spart) {
+  __shared__ uint32_t tile[XPC][XPRS];
   __shared__ unsigned smx[HMAXT];
-  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int tid = threadIdx.x;
+  const int c0 = blockIdx.x * XPC;
   const int ch = blockIdx.y;
-  const int64_t t0 = (int64_t)ch * tpc;
-  const int64_t t1 = (t0 + tpc < ntok) ? t0 + tpc : ntok;
-  if (c < C) {
-    float m = 0.0f, a = 0.0f;
-    for (int64_t t = t0; t < t1; ++t) {
-      const float v = to_f32(X[t * ldx + c]);
-      m = fmaxf(m, fabsf(v));
-      a = a + v * v;                  // (inp ** 2).sum(0): square, then add
+  const int64_t t0 = (int64_t)ch * XTOK;
+  const uint16_t* Xb = reinterpret_cast<const uint16_t*>(X);
+  // load: 8 column groups (8 columns, 16 B) x 128 token pairs; lane = group + 8 * pair
+  for (int v = tid; v < 8 * (XTOK / 2); v += 256) {
+    const int grp = v & 7, tp = v >> 3;
+    const int cb = c0 + 8 * grp;
+    uint32_t e0[8], e1[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t t = t0 + 2 * tp + h;
+      uint32_t* e = h ? e1 : e0;
+      if (vec_ok && cb + 8 <= C && t < ntok) {
+        const uint4 q = *reinterpret_cast<const uint4*>(Xb + t * ldx + cb);
+        e[0] = q.x & 0xffffu; e[1] = q.x >> 16; e[2] = q.y & 0xffffu; e[3] = q.y >> 16;
+        e[4] = q.z & 0xffffu; e[5] = q.z >> 16; e[6] = q.w & 0xffffu; e[7] = q.w >> 16;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) e[k] = (t < ntok && cb + k < C) ? Xb[t * ldx + cb + k] : 0u;
+      }
     }
-    mpart[(int64_t)ch * C + c] = m;
-    apart[(int64_t)ch * C + c] = a;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) tile[8 * grp + k][tp] = e0[k] | (e1[k] << 16);
+  }
+  __syncthreads();
+  // store: row c of X^T, 16 B (8 tokens) per lane, 32 lanes per row
+  for (int v = tid; v < XPC * (XTOK / 8); v += 256) {
+    const int c = v >> 5, q = v & 31;
+    if (c0 + c < C) {
+      const uint32_t* src = &tile[c][4 * q];
+      *reinterpret_cast<uint4*>(XTr + (int64_t)(c0 + c) * ldt + t0 + 8 * q) =
+          make_uint4(src[0], src[1], src[2], src[3]);
+    }
+  }
+  if (tid < XPC && c0 + tid < C) {
+    float m = 0.0f, a = 0.0f;
+    for (int w = 0; w < XTOK / 2; ++w) {
+      const uint32_t u = tile[tid][w];
+      const float v0 = XType<TX>::lo(u), v1 = XType<TX>::hi(u);
+      m = fmaxf(m, fabsf(v0));
+      a = a + v0 * v0;                // (inp ** 2).sum(0): square, then add, in token order
+      m = fmaxf(m, fabsf(v1));
+      a = a + v1 * v1;
+    }
+    mpart[(int64_t)ch * C + c0 + tid] = m;
+    apart[(int64_t)ch * C + c0 + tid] = a;
   }
   if (blockIdx.x != 0) return;
-  if (threadIdx.x < HMAXT) smx[threadIdx.x] = 0u;
+  if (tid < HMAXT) smx[tid] = 0u;
   __syncthreads();
   for (int g = 0; g < ntarg; ++g) {
-    float m = 0.0f;
-    for (int64_t t = t0 + threadIdx.x; t < t1; t += 256) m = fmaxf(m, fabsf(tg.sal[g][t * tg.ld_sal[g]]));
-    atomicMax(&smx[g], __float_as_uint(m));
+    const int64_t t = t0 + tid;
+    const float s = (t < ntok) ? tg.sal[g][t * tg.ld_sal[g]] : 0.0f;
+    sT[(int64_t)g * lds + t] = s;
+    atomicMax(&smx[g], __float_as_uint(fabsf(s)));
   }
   __syncthreads();
-  if (threadIdx.x < ntarg) spart[(int64_t)ch * HMAXT + threadIdx.x] = __uint_as_float(smx[threadIdx.x]);
+  if (tid < ntarg) spart[(int64_t)ch * HMAXT + tid] = __uint_as_float(smx[tid]);
 }
 
-// Reduce the chunks: act_square += sum_t x^2 (chunks in order), and the per (target, column)
-// scale 2^e with e = 15 - E for max|x_c| * max|s_g| = f * 2^E, f in [0.5, 1).
+// Reduce the token blocks: act_square += sum_t x^2 (blocks in order), and the per (target,
+// column) scale 2^e with e = 15 - E for max|x_c| * max|s_g| = f * 2^E, f in [0.5, 1).
 __global__ __launch_bounds__(256) void k_xfinish(int C, int nchunk, HTargets tg, int ntarg,
                                                  const float* __restrict__ mpart,
                                                  const float* __restrict__ apart,
@@ -890,84 +925,86 @@ int64_t hessian_ws_bytes(int64_t tail, int S) {
 }
 
 struct SplitLayout {
-  int nchunk;
-  int64_t tpc, off_part, off_m, off_a, off_s, off_scale, bytes;
+  int64_t ntok_p, nchunk, off_part, off_xt, off_st, off_m, off_a, off_s, off_scale, bytes;
 };
 
 SplitLayout split_layout(int64_t ntok, int C, int ntarg, int64_t tail, int S) {
   SplitLayout L;
-  int64_t nch = (ntok + 63) / 64;
-  L.nchunk = (int)(nch < 1 ? 1 : (nch > 256 ? 256 : nch));
-  L.tpc = (ntok + L.nchunk - 1) / L.nchunk;
+  L.ntok_p = ((ntok + XTOK - 1) / XTOK) * XTOK;
+  L.nchunk = L.ntok_p / XTOK;
   L.off_part = hessian_cnt_bytes();
-  L.off_m = L.off_part + align256(tail * S * (int64_t)XPART * 4);
-  L.off_a = L.off_m + align256((int64_t)L.nchunk * C * 4);
-  L.off_s = L.off_a + align256((int64_t)L.nchunk * C * 4);
-  L.off_scale = L.off_s + align256((int64_t)L.nchunk * HMAXT * 4);
+  L.off_xt = L.off_part + align256(tail * S * (int64_t)XPART * 4);
+  L.off_st = L.off_xt + align256((int64_t)C * L.ntok_p * 2);
+  L.off_m = L.off_st + align256((int64_t)ntarg * L.ntok_p * 4);
+  L.off_a = L.off_m + align256(L.nchunk * C * 4);
+  L.off_s = L.off_a + align256(L.nchunk * C * 4);
+  L.off_scale = L.off_s + align256(L.nchunk * HMAXT * 4);
   L.bytes = L.off_scale + align256((int64_t)ntarg * C * 4);
   return L;
 }
 
-int64_t split_pairs(int C, int* nt_out, int* npr_out) {
-  const int nt = (C + XC - 1) / XC;
-  const int npr = (nt + 1) / 2;
-  int64_t n = 0;
-  for (int c = 0; c < nt; ++c) n += c / 2 + 1;
-  *nt_out = nt;
-  *npr_out = npr;
-  return n;
+void split_items(int C, int ntarg, int* nt, int* ntiles, int64_t* total) {
+  *nt = (C + XT - 1) / XT;
+  *ntiles = *nt * (*nt + 1) / 2;
+  *total = (int64_t)*ntiles * ntarg;
 }
 
 // Workspace bytes the split kernel needs for one launch of `ntarg` targets.
 int64_t split_ws_need(int64_t ntok, int C, int ntarg) {
-  int nt, npr;
-  const int64_t total = split_pairs(C, &nt, &npr) * ntarg;
+  int nt, ntiles;
+  int64_t total;
+  split_items(C, ntarg, &nt, &ntiles, &total);
   int tail = 0, S = 1;
-  tail_split(total, (ntok + XK - 1) / XK, split_slots(), &tail, &S);
+  const int64_t ntok_p = ((ntok + XTOK - 1) / XTOK) * XTOK;
+  tail_split(total, ntok_p / 16, split_slots(), &tail, &S);
   return split_layout(ntok, C, ntarg, tail, S).bytes;
 }
 
 int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, const HTargets& tg,
                  int ntarg, void* ws, int64_t ws_bytes, hipStream_t s) {
-  int nt, npr;
-  const int64_t npairs = split_pairs(C, &nt, &npr);
-  const int64_t total = npairs * ntarg;
+  int nt, ntiles;
+  int64_t total;
+  split_items(C, ntarg, &nt, &ntiles, &total);
   if (total > 0x7fffffff / 8) return RQ_EINVAL;
-  const bool vec_ok = ((reinterpret_cast<uintptr_t>(x) & 7) == 0) && (((size_t)ldx * 2) % 8 == 0);
-  const int slots = split_slots();
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (((size_t)ldx * 2) % 16 == 0);
   int tail = 0, S = 1;
-  tail_split(total, (ntok + XK - 1) / XK, slots, &tail, &S);
-  SplitLayout L = split_layout(ntok, C, ntarg, tail, S);
+  SplitLayout L = split_layout(ntok, C, ntarg, 0, 1);
+  const int64_t nks = L.ntok_p / 16;
+  tail_split(total, nks, split_slots(), &tail, &S);
+  L = split_layout(ntok, C, ntarg, tail, S);
   if (ws_bytes < L.bytes) {                       // no room for the slices: whole items only
     tail = 0;
     S = 1;
     L = split_layout(ntok, C, ntarg, 0, 1);
   }
   char* wb = reinterpret_cast<char*>(ws);
+  uint16_t* xt = reinterpret_cast<uint16_t*>(wb + L.off_xt);
+  float* sT = reinterpret_cast<float*>(wb + L.off_st);
   float* mpart = reinterpret_cast<float*>(wb + L.off_m);
   float* apart = reinterpret_cast<float*>(wb + L.off_a);
   float* spart = reinterpret_cast<float*>(wb + L.off_s);
   float* scale = reinterpret_cast<float*>(wb + L.off_scale);
-  dim3 sgrid((C + 255) / 256, L.nchunk), fgrid((C + 255) / 256);
+  dim3 pgrid((C + XPC - 1) / XPC, (unsigned)L.nchunk), fgrid((C + 255) / 256);
   if (x_dtype == RQ_F16)
-    hipLaunchKernelGGL(k_xstats<__half>, sgrid, dim3(256), 0, s, (const __half*)x, ntok, ldx, C, L.tpc,
-                       tg, ntarg, mpart, apart, spart);
+    hipLaunchKernelGGL(k_xprep<__half>, pgrid, dim3(256), 0, s, (const __half*)x, ntok, ldx, C, vec_ok, xt,
+                       L.ntok_p, tg, ntarg, sT, L.ntok_p, mpart, apart, spart);
   else
-    hipLaunchKernelGGL(k_xstats<__hip_bfloat16>, sgrid, dim3(256), 0, s, (const __hip_bfloat16*)x, ntok,
-                       ldx, C, L.tpc, tg, ntarg, mpart, apart, spart);
+    hipLaunchKernelGGL(k_xprep<__hip_bfloat16>, pgrid, dim3(256), 0, s, (const __hip_bfloat16*)x, ntok, ldx,
+                       C, vec_ok, xt, L.ntok_p, tg, ntarg, sT, L.ntok_p, mpart, apart, spart);
   RQ_CHECK_LAUNCH();
-  hipLaunchKernelGGL(k_xfinish, fgrid, dim3(256), 0, s, C, L.nchunk, tg, ntarg, mpart, apart, spart, scale);
+  hipLaunchKernelGGL(k_xfinish, fgrid, dim3(256), 0, s, C, (int)L.nchunk, tg, ntarg, mpart, apart, spart,
+                     scale);
   RQ_CHECK_LAUNCH();
   const int full = (int)(total - tail);
   int* cnt = tail > 0 ? reinterpret_cast<int*>(ws) : nullptr;
   float* wsf = tail > 0 ? reinterpret_cast<float*>(wb + L.off_part) : nullptr;
   dim3 grid((unsigned)(full + (int64_t)tail * S)), block(XTHREADS);
   if (x_dtype == RQ_F16)
-    hipLaunchKernelGGL(k_hessian_split<__half>, grid, block, 0, s, (const uint16_t*)x, ntok, ldx, C, tg,
-                       scale, ntarg, nt, npr, (int)npairs, vec_ok, full, S, wsf, cnt);
+    hipLaunchKernelGGL(k_hessian_split<__half>, grid, block, 0, s, xt, L.ntok_p, C, sT, L.ntok_p, scale, tg,
+                       ntarg, nt, ntiles, nks, full, S, wsf, cnt);
   else
-    hipLaunchKernelGGL(k_hessian_split<__hip_bfloat16>, grid, block, 0, s, (const uint16_t*)x, ntok, ldx,
-                       C, tg, scale, ntarg, nt, npr, (int)npairs, vec_ok, full, S, wsf, cnt);
+    hipLaunchKernelGGL(k_hessian_split<__hip_bfloat16>, grid, block, 0, s, xt, L.ntok_p, C, sT, L.ntok_p,
+                       scale, tg, ntarg, nt, ntiles, nks, full, S, wsf, cnt);
   RQ_CHECK_LAUNCH();
   return RQ_OK;
 }
