@@ -23,6 +23,7 @@
 #include "rq_common.h"
 
 #include <atomic>
+#include <type_traits>
 
 namespace {
 
@@ -349,19 +350,23 @@ __global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
 // applied, harmlessly.  The epilogue multiplies the tile by 2^-e (exact) before adding it
 // to H.
 //
-// Operands come straight from global memory.  A pre-pass (k_xprep) writes the chunk
-// transposed, X^T [C][ntok_p] (ntok_p = ntok rounded up to 256, zero padded), and each
-// target's saliency as a contiguous zero-padded vector, and reduces act_square and the
-// per-column / per-target maxima.  With tokens contiguous, one lane's MFMA fragment -- 8
-// consecutive tokens of one column -- is a single 16-byte load, so the product kernel needs
-// no LDS staging and no barriers.  A workgroup (4 waves, one per SIMD, one workgroup per CU)
-// owns a 256 x 256 tile of the upper triangle; wave w owns columns 64w..64w+63 against all
-// 256 rows (8 x 2 blocks of 32 x 32: 256 accumulators per lane).  Per 16 tokens a wave loads
-// 8 row fragments, 2 column fragments and 8 saliencies, splits the column fragments in
-// registers and issues 3 x 16 = 48 MFMAs, with the next 16 tokens' loads in flight.
+// Operands.  A pre-pass (k_xprep) writes the chunk in a fragment-blocked layout: for each
+// block of 32 columns and each 16-token step, one contiguous 1 KB holding exactly the
+// v_mfma_f32_32x32x16 operand of a wave (lane L = r + 32 h: tokens 8h..8h+7 of column r, zero
+// padded past ntok and C), so that every operand load of the product kernel reads whole cache
+// lines.  It also writes each target's saliency as a contiguous zero-padded vector and reduces
+// act_square and the per-column / per-target maxima.  A workgroup (8 waves, two per SIMD, one
+// workgroup per CU) owns a 256 x 256 tile of the upper triangle; wave w owns columns
+// 32w..32w+31 against all 256 rows (8 blocks of 32 x 32: 128 accumulators per lane, so two
+// waves fit a SIMD and the hardware interleaves one wave's loads and split with the other's
+// MFMAs).  Operands are staged into a ring of LDS stages by direct global->LDS loads (wave w
+// fetches row fragment w and its own column fragment, wave 0 the step's saliencies); per 16
+// tokens a wave reads 8 row fragments, splits its column fragment in registers and issues
+// 3 x 8 = 24 MFMAs.
 constexpr int XT = 256;          // workgroup tile edge
 constexpr int XNP = 3;           // pieces of the weighted operand
-constexpr int XTHREADS = 256;
+constexpr int XWAVES = 8;        // waves per workgroup, two per SIMD
+constexpr int XTHREADS = 64 * XWAVES;
 constexpr int XPART = XT * XT;   // floats of one partial tile
 constexpr int XTOK = 256;        // token padding of the transposed chunk / pre-pass block
 
@@ -399,6 +404,36 @@ struct XType<__hip_bfloat16> {
 // 8 tokens of one column: w = fl32(x * s) * 2^e split into three 16-bit fragments.
 // (fma(x, s, 0) is rn(x * s); fma(-p, 1, w) is the exact w - p.  Written as fma so that the
 // fp16 -> fp32 conversions can fold into v_fma_mix.)
+// One token pair of one column (x of tokens t, t+1 packed in xw): w = fl32(x * s) * 2^e for
+// both, split into three packed pieces.  fp16: each residual w - p is one v_fma_mix_f32
+// (-p as an fp16 operand, times 1, plus w: exact), written out because the compiler emits a
+// conversion and a subtraction for it.
+template <typename TX>
+__device__ __forceinline__ void split_pair(uint32_t xw, float s0, float s1, float sc, uint32_t& o0, uint32_t& o1,
+                                           uint32_t& o2) {
+  typedef XType<TX> T;
+  float a = __builtin_fmaf(T::lo(xw), s0, 0.0f) * sc;
+  float b = __builtin_fmaf(T::hi(xw), s1, 0.0f) * sc;
+  if constexpr (std::is_same<TX, __half>::value) {
+    asm("v_cvt_pk_f16_f32 %0, %3, %4\n\t"
+        "v_fma_mix_f32 %3, -%0, 1.0, %3 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mix_f32 %4, -%0, 1.0, %4 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_cvt_pk_f16_f32 %1, %3, %4\n\t"
+        "v_fma_mix_f32 %3, -%1, 1.0, %3 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mix_f32 %4, -%1, 1.0, %4 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_cvt_pk_f16_f32 %2, %3, %4"
+        : "=&v"(o0), "=&v"(o1), "=&v"(o2), "+v"(a), "+v"(b));
+  } else {
+    o0 = T::pack(a, b);
+    a = a - T::lo(o0);
+    b = b - T::hi(o0);
+    o1 = T::pack(a, b);
+    a = a - T::lo(o1);
+    b = b - T::hi(o1);
+    o2 = T::pack(a, b);
+  }
+}
+
 template <typename TX>
 __device__ __forceinline__ void split8(uint4 x, float4 s0, float4 s1, float sc, uint4 (&p)[XNP]) {
   typedef XType<TX> T;
@@ -426,17 +461,18 @@ __device__ __forceinline__ void split8(uint4 x, float4 s0, float4 s1, float sc, 
 }
 
 // LDS ring: XDEPTH stages (separate arrays) of one 16-token step each.  A stage holds the
-// workgroup's 8 row fragments (each wave fetches 2) and, per wave, its 2 raw column fragments
-// and its 8 saliencies (as two 16-byte loads per lane); every fragment is 64 lanes x 16 B,
-// placed by lane, so a lane reads back exactly its own MFMA operand.  Step k of a tile (or
-// token slice) starting at kbeg lives in stage (k - kbeg) % XDEPTH; the loop is unrolled by
-// XDEPTH so that every stage index is a compile-time constant: the LDS reads are ordinary
-// loads (the compiler places their lgkmcnt waits), and alias analysis can tell the staging
-// writes in flight to other stages from the stage being read.
+// workgroup's 8 row fragments (wave w fetches fragment w), each wave's column fragment, and the
+// step's 16 saliencies (wave 0, lanes 0-3); every fragment is 64 lanes x 16 B placed by lane,
+// so a lane reads back exactly its own MFMA operand.  Step k of a tile (or token slice)
+// starting at kbeg lives in stage (k - kbeg) % XDEPTH; the loop is unrolled by XDEPTH so that
+// every stage index is a compile-time constant: the LDS reads are ordinary loads (the compiler
+// places their lgkmcnt waits), and alias analysis can tell the staging writes in flight to
+// other stages from the stage being read.
 constexpr int XDEPTH = 4;
 constexpr int XA_BYTES = 8 * 1024;                  // row fragments of a stage
-constexpr int XW_BYTES = 4 * 1024;                  // per wave: 2 column fragments + 2 saliency blocks
-constexpr int XSTAGE = XA_BYTES + 4 * XW_BYTES;     // 24 KB
+constexpr int XB_OFF = XA_BYTES;                    // column fragment of wave w at XB_OFF + 1024 w
+constexpr int XS_OFF = XB_OFF + XWAVES * 1024;      // the step's 16 saliencies (64 B)
+constexpr int XSTAGE = XS_OFF + 256;
 
 struct XStages {
   uint8_t* s[XDEPTH];
@@ -449,164 +485,148 @@ __device__ __forceinline__ void lds_dma16(const void* g, uint8_t* l) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
 }
 
-// Stage step k into `st`: row fragments 2w, 2w+1, this wave's column fragments and saliencies.
-__device__ __forceinline__ void stage_step(uint8_t* st, const uint16_t* baseA, const uint32_t (&oa)[2],
-                                           const uint16_t* baseB, const uint32_t (&ob)[2], const float* sbase,
-                                           int wave, int64_t k) {
+// Stage step k into `st`: row fragment w and this wave's column fragment (each one contiguous
+// 1 KB of the fragment-blocked chunk), and -- wave 0, lanes 0-3 -- the step's 16 saliencies.
+// 2 staging loads per wave and step (wave 0: 3).
+__device__ __forceinline__ void stage_step(uint8_t* st, const uint16_t* pa, const uint16_t* pb, const float* sg,
+                                           int wave, int lane, int64_t k) {
   asm volatile("" : "+s"(k));
-  const uint16_t* pA = baseA + 16 * k;
-  const uint16_t* pB = baseB + 16 * k;
-  uint8_t* w = st + XA_BYTES + wave * XW_BYTES;
-  lds_dma16(pA + oa[0], st + (2 * wave) * 1024);
-  lds_dma16(pA + oa[1], st + (2 * wave + 1) * 1024);
-  lds_dma16(pB + ob[0], w);
-  lds_dma16(pB + ob[1], w + 1024);
-  lds_dma16(sbase + 16 * k, w + 2048);
-  lds_dma16(sbase + 16 * k + 4, w + 3072);
+  const int64_t off = k * 512;                      // 1 KB per step and fragment
+  lds_dma16(pa + off, st + wave * 1024);
+  lds_dma16(pb + off, st + XB_OFF + wave * 1024);
+  if (wave == 0 && lane < 4) lds_dma16(sg + 16 * k + 4 * lane, st + XS_OFF);
 }
 
-// This wave's column fragments and saliencies of a staged step, split into pieces.
+// This wave's column fragment and the saliencies of a staged step, split into pieces.
 template <typename TX>
-__device__ __forceinline__ void split_staged(const uint8_t* st, int wave, int lane, const float (&sc)[2],
-                                             uint4 (&p)[2][XNP]) {
-  const uint8_t* w = st + XA_BYTES + wave * XW_BYTES + lane * 16;
-  const uint4 b0 = *reinterpret_cast<const uint4*>(w);
-  const uint4 b1 = *reinterpret_cast<const uint4*>(w + 1024);
-  const float4 s0 = *reinterpret_cast<const float4*>(w + 2048);
-  const float4 s1 = *reinterpret_cast<const float4*>(w + 3072);
-  split8<TX>(b0, s0, s1, sc[0], p[0]);
-  split8<TX>(b1, s0, s1, sc[1], p[1]);
+__device__ __forceinline__ void split_staged(const uint8_t* st, int wave, int lane, float sc, uint4 (&p)[XNP]) {
+  const uint8_t* w = static_cast<const uint8_t*>(__builtin_assume_aligned(st + XB_OFF + wave * 1024 + lane * 16, 16));
+  const uint8_t* sp = static_cast<const uint8_t*>(__builtin_assume_aligned(st + XS_OFF + 32 * (lane >> 5), 16));
+  split8<TX>(*reinterpret_cast<const uint4*>(w), *reinterpret_cast<const float4*>(sp),
+             *reinterpret_cast<const float4*>(sp + 16), sc, p);
 }
 
-// One 16-token step k of a wave.  KP = (k - kbeg) % 2 selects the piece and row-fragment
-// buffers; CUR, NXT, FILL are the stages of steps k, k+1 and k+XDEPTH-1.  This wave's staging
-// of steps k and k+1 was issued XDEPTH-1 and XDEPTH-2 steps ago and is followed by the 6
-// staging loads of each step since, so vmcnt(6) covers both whatever the issue order within a
-// step; after the barrier the other waves' row fragments of steps k and k+1 are in LDS too (the
-// barrier also orders every read of the FILL stage, done in earlier steps, before its refill).
-// Then: stage step k+XDEPTH-1; read the row fragments of k+1 into the other buffer; split this
-// wave's column fragments of k+1 while the 48 MFMAs of step k run on the row fragments read one
-// step ago.  A bare s_barrier: the fence of __syncthreads would wait for every staging load in
-// flight.
+// One 16-token step k of a wave.  KP = (k - kbeg) % 2 selects the piece buffer; CUR, NXT, FILL
+// are the stages of steps k, k+1 and k+XDEPTH-1.  Every wave's staging of steps k and k+1 was
+// issued XDEPTH-1 and XDEPTH-2 steps ago and is followed by at least the 2 staging loads of each
+// of the XDEPTH-3 steps since, so vmcnt(2 * (XDEPTH - 3)) covers this wave's part of both
+// whatever the issue order within a step, and after the barrier the other waves' parts are in
+// LDS too (the barrier also orders every read of the FILL stage, done in earlier steps, before
+// its refill).  Then: stage step k+XDEPTH-1; read the row fragments of step k; split this
+// wave's column fragment of step k+1 under the 24 MFMAs of step k.  Two waves share a SIMD, so
+// one wave's reads, waits and split run while the other issues MFMAs.  A bare s_barrier: the
+// fence of __syncthreads would wait for every staging load in flight.
 template <typename TX, int KP, int CUR, int NXT, int FILL>
-__device__ __forceinline__ void split_step(uint4 (&p)[2][2][XNP], uint4 (&a)[2][8], floatx16 (&acc)[8][2],
-                                           const XStages& L, const uint16_t* baseA, const uint32_t (&oa)[2],
-                                           const uint16_t* baseB, const uint32_t (&ob)[2], const float* sbase,
-                                           const float (&sc)[2], int wave, int lane, int64_t k, int64_t last) {
+__device__ __forceinline__ void split_step(uint4 (&p)[2][XNP], floatx16 (&acc)[8], const XStages& L,
+                                           const uint16_t* pa, const uint16_t* pb, const float* sg, float sc,
+                                           int wave, int lane, int64_t k, int64_t last) {
   typedef XType<TX> T;
   typedef typename T::v8 v8;
   constexpr int NP = 1 - KP;
-  XWAIT_VM(6);
+  XWAIT_VM(2 * (XDEPTH - 3));
   __builtin_amdgcn_s_barrier();
-  stage_step(L.s[FILL], baseA, oa, baseB, ob, sbase, wave, min(k + XDEPTH - 1, last));
-  const uint8_t* nx = L.s[NXT] + lane * 16;
+  stage_step(L.s[FILL], pa, pb, sg, wave, lane, min(k + XDEPTH - 1, last));
+  const uint8_t* cur = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[CUR] + lane * 16, 16));
+  uint4 a[8];
 #pragma unroll
-  for (int bi = 0; bi < 8; ++bi) a[NP][bi] = *reinterpret_cast<const uint4*>(nx + bi * 1024);
-  split_staged<TX>(L.s[NXT], wave, lane, sc, p[NP]);
+  for (int bi = 0; bi < 8; ++bi) a[bi] = *reinterpret_cast<const uint4*>(cur + bi * 1024);
+  const uint8_t* w = static_cast<const uint8_t*>(
+      __builtin_assume_aligned(L.s[NXT] + XB_OFF + wave * 1024 + lane * 16, 16));
+  const uint8_t* sp = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[NXT] + XS_OFF + 32 * (lane >> 5), 16));
+  const uint4 b = *reinterpret_cast<const uint4*>(w);
+  const float4 s0 = *reinterpret_cast<const float4*>(sp);
+  const float4 s1 = *reinterpret_cast<const float4*>(sp + 16);
+  const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  const uint32_t xw[4] = {b.x, b.y, b.z, b.w};
+  uint32_t o[XNP][4];
 #pragma unroll
-  for (int q = XNP - 1; q >= 0; --q)
+  for (int bi = 0; bi < 8; ++bi)
+    acc[bi] = T::mfma(__builtin_bit_cast(v8, a[bi]), __builtin_bit_cast(v8, p[KP][XNP - 1]), acc[bi]);
 #pragma unroll
-    for (int bi = 0; bi < 8; ++bi)
+  for (int m = 0; m < 4; ++m) {
+    split_pair<TX>(xw[m], sv[2 * m], sv[2 * m + 1], sc, o[0][m], o[1][m], o[2][m]);
 #pragma unroll
-      for (int bj = 0; bj < 2; ++bj)
-        acc[bi][bj] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][bj][q]), acc[bi][bj]);
+    for (int i = 4 * m; i < 4 * m + 4; ++i) {
+      const int q = 1 - i / 8, bi = i % 8;
+      acc[bi] = T::mfma(__builtin_bit_cast(v8, a[bi]), __builtin_bit_cast(v8, p[KP][q]), acc[bi]);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < XNP; ++q) p[NP][q] = make_uint4(o[q][0], o[q][1], o[q][2], o[q][3]);
 }
 
 template <typename TX>
-__device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XTr, int64_t ldt, int C,
+__device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int64_t nks, int C,
                                            const float* __restrict__ sg, const float* __restrict__ scl,
                                            float* __restrict__ Hg, int R0, int C0, int64_t kbeg,
                                            int64_t kend, float* __restrict__ part, const XStages& L) {
+  typedef typename XType<TX>::v8 v8;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int fr = lane & 31, fh = lane >> 5;
-  const int Cw = C0 + 64 * wave;
-  const int Cb = min(Cw, C - 1);
+  const int Cw = C0 + 32 * wave;
+  const int ncb = (C + 31) / 32;
 
-  // Fragment sources: a uniform base per side plus a 32-bit lane offset (in elements, below
-  // 256 * ldt).  Rows / columns past C read column C-1; their products are discarded.
-  const uint16_t* baseA = XTr + (int64_t)R0 * ldt;
-  const uint16_t* baseB = XTr + (int64_t)Cb * ldt;
-  uint32_t oa[2], ob[2];
-  float sc[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-    oa[h] = (uint32_t)((min(R0 + 32 * (2 * wave + h) + fr, C - 1) - R0) * ldt + 8 * fh);
-#pragma unroll
-  for (int bj = 0; bj < 2; ++bj) {
-    const int c = min(Cw + 32 * bj + fr, C - 1);
-    ob[bj] = (uint32_t)((c - Cb) * ldt + 8 * fh);
-    sc[bj] = scl[c];
-  }
-  const float* sbase = sg + 8 * fh;
+  // Fragment sources in the fragment-blocked chunk: block cb of 32 columns, step k at
+  // ((cb * nks + k) * 64 + lane) * 8 halves.  Blocks past the last read the last one (zero
+  // padded past C); their products are discarded.
+  const uint16_t* pa = XB + ((int64_t)min(R0 / 32 + wave, ncb - 1) * nks * 64 + lane) * 8;
+  const uint16_t* pb = XB + ((int64_t)min(Cw / 32, ncb - 1) * nks * 64 + lane) * 8;
+  const float sc = scl[min(Cw + fr, C - 1)];
 
-  floatx16 acc[8][2];
+  floatx16 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
 
-  // Prologue: stage steps kbeg .. kbeg+XDEPTH-2 into stages 0 .. XDEPTH-2, read the row
-  // fragments and split the column fragments of kbeg.  Steps past the end re-read the last one;
-  // their values are never used.
+  // Prologue: stage steps kbeg .. kbeg+XDEPTH-2 into stages 0 .. XDEPTH-2 and split the column
+  // fragment of kbeg.  Steps past the end re-read the last one; their values are never used.
   const int64_t last = kend - 1;
 #pragma unroll
-  for (int h = 0; h < XDEPTH - 1; ++h) stage_step(L.s[h], baseA, oa, baseB, ob, sbase, wave, min(kbeg + h, last));
-  uint4 p[2][2][XNP];
-  uint4 a[2][8];
-  XWAIT_VM(6 * (XDEPTH - 2));         // this wave's staging of step kbeg
+  for (int h = 0; h < XDEPTH - 1; ++h) stage_step(L.s[h], pa, pb, sg, wave, lane, min(kbeg + h, last));
+  uint4 p[2][XNP];
+  XWAIT_VM(2 * (XDEPTH - 2));         // this wave's staging of step kbeg
   __builtin_amdgcn_s_barrier();       // and the other waves'
-  {
-    const uint8_t* c0 = L.s[0] + lane * 16;
-#pragma unroll
-    for (int bi = 0; bi < 8; ++bi) a[0][bi] = *reinterpret_cast<const uint4*>(c0 + bi * 1024);
-    split_staged<TX>(L.s[0], wave, lane, sc, p[0]);
-  }
+  split_staged<TX>(L.s[0], wave, lane, sc, p[0]);
 
   const int64_t n = kend - kbeg;
   int64_t k = kbeg;
+  static_assert(XDEPTH == 4, "unrolled stage schedule");
   for (; k + 4 <= kend; k += 4) {
-    split_step<TX, 0, 0, 1, 3>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k, last);
-    split_step<TX, 1, 1, 2, 0>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k + 1, last);
-    split_step<TX, 0, 2, 3, 1>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k + 2, last);
-    split_step<TX, 1, 3, 0, 2>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k + 3, last);
+    split_step<TX, 0, 0, 1, 3>(p, acc, L, pa, pb, sg, sc, wave, lane, k, last);
+    split_step<TX, 1, 1, 2, 0>(p, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last);
+    split_step<TX, 0, 2, 3, 1>(p, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last);
+    split_step<TX, 1, 3, 0, 2>(p, acc, L, pa, pb, sg, sc, wave, lane, k + 3, last);
   }
   const int rem = (int)(n & 3);
-  if (rem > 0) split_step<TX, 0, 0, 1, 3>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k, last);
-  if (rem > 1) split_step<TX, 1, 1, 2, 0>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k + 1, last);
-  if (rem > 2) split_step<TX, 0, 2, 3, 1>(p, a, acc, L, baseA, oa, baseB, ob, sbase, sc, wave, lane, k + 2, last);
+  if (rem > 0) split_step<TX, 0, 0, 1, 3>(p, acc, L, pa, pb, sg, sc, wave, lane, k, last);
+  if (rem > 1) split_step<TX, 1, 1, 2, 0>(p, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last);
+  if (rem > 2) split_step<TX, 0, 2, 3, 1>(p, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last);
   XWAIT_VM(0);                        // no staging left in flight when the workgroup moves on
-
 
   if (part) {
     // token slice: hand the (still scaled) partial tile to the workspace
 #pragma unroll
     for (int bi = 0; bi < 8; ++bi)
 #pragma unroll
-      for (int bj = 0; bj < 2; ++bj)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) part[((bi * 2 + bj) * 16 + e) * XTHREADS + tid] = acc[bi][bj][e];
+      for (int e = 0; e < 16; ++e) part[(bi * 16 + e) * XTHREADS + tid] = acc[bi][e];
     return;
   }
   // H[g][i][j] += acc * 2^-e_j   (32x32 block layout: i = 8*(e/4) + 4*(lane/32) + e%4, j = lane%32)
+  const int j = Cw + fr;
+  const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
 #pragma unroll
-  for (int bj = 0; bj < 2; ++bj) {
-    const int j = Cw + 32 * bj + fr;
-    const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
+  for (int bi = 0; bi < 8; ++bi)
 #pragma unroll
-    for (int bi = 0; bi < 8; ++bi)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
-        if (i < C && j < C) {
-          float* ph = Hg + (int64_t)i * C + j;
-          *ph = *ph + acc[bi][bj][e] * inv;
-        }
+    for (int e = 0; e < 16; ++e) {
+      const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
+      if (i < C && j < C) {
+        float* ph = Hg + (int64_t)i * C + j;
+        *ph = *ph + acc[bi][e] * inv;
       }
-  }
+    }
 }
 
 // The last slice of a split item adds the S partials (in slice order) to H.
@@ -617,31 +637,27 @@ __device__ __forceinline__ void reduce_split_slices(const float* __restrict__ pa
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int fr = lane & 31, fh = lane >> 5;
-#pragma unroll
-  for (int bj = 0; bj < 2; ++bj) {
-    const int j = C0 + 64 * wave + 32 * bj + fr;
-    const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
+  const int j = C0 + 32 * wave + fr;
+  const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
 #pragma unroll 1
-    for (int bi = 0; bi < 8; ++bi)
+  for (int bi = 0; bi < 8; ++bi)
 #pragma unroll 4
-      for (int e = 0; e < 16; ++e) {
-        const int slot = ((bi * 2 + bj) * 16 + e) * XTHREADS + tid;
-        float sum = __hip_atomic_load(part0 + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (int qq = 1; qq < S; ++qq)
-          sum += __hip_atomic_load(part0 + (int64_t)qq * XPART + slot, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
-        if (i < C && j < C) {
-          float* ph = Hg + (int64_t)i * C + j;
-          *ph = *ph + sum * inv;
-        }
+    for (int e = 0; e < 16; ++e) {
+      const int slot = (bi * 16 + e) * XTHREADS + tid;
+      float sum = __hip_atomic_load(part0 + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int qq = 1; qq < S; ++qq)
+        sum += __hip_atomic_load(part0 + (int64_t)qq * XPART + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
+      if (i < C && j < C) {
+        float* ph = Hg + (int64_t)i * C + j;
+        *ph = *ph + sum * inv;
       }
-  }
+    }
 }
 
 template <typename TX>
 __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
-    const uint16_t* __restrict__ XTr, int64_t ldt, int C, const float* __restrict__ sT, int64_t lds_stride,
+    const uint16_t* __restrict__ XB, int C, const float* __restrict__ sT, int64_t lds_stride,
     const float* __restrict__ scale, HTargets tg, int ntarg, int nt, int ntiles, int64_t nks, int full,
     int S, float* __restrict__ ws, int* __restrict__ cnt) {
   __shared__ __attribute__((aligned(16))) uint8_t lds0[XSTAGE];
@@ -677,7 +693,7 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
   const float* scl = scale + (int64_t)g * C;
   float* part0 = (slice >= 0) ? ws + (int64_t)(logical - full) * S * XPART : nullptr;
   float* part = part0 ? part0 + (int64_t)slice * XPART : nullptr;
-  split_tile<TX>(XTr, ldt, C, sT + (int64_t)g * lds_stride, scl, Hg, R0, C0, kbeg, kend, part, L);
+  split_tile<TX>(XB, nks, C, sT + (int64_t)g * lds_stride, scl, Hg, R0, C0, kbeg, kend, part, L);
   if (!part) return;
   __threadfence();
   __syncthreads();
@@ -693,8 +709,8 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
   reduce_split_slices(part0, S, Hg, scl, R0, C0, C);
 }
 
-// Pre-pass over one 64-column x 256-token block of X: the transposed block into X^T (zeros
-// past ntok), each column's max |x| and sum_t x^2 (in token order) for this token block, and
+// Pre-pass over one 64-column x 256-token block of X: the block in the fragment-blocked
+// layout read by k_hessian_split (zeros past ntok and past C), each column's max |x| and sum_t x^2 (in token order) for this token block, and
 // (first column block only) each target's saliency, contiguous and zero padded, with its
 // max |s|.  Two tokens of one column share a 32-bit LDS word; the row stride of 129 words
 // keeps the transposing writes free of bank conflicts.
@@ -702,7 +718,7 @@ constexpr int XPC = 64;            // columns per pre-pass block
 constexpr int XPRS = XTOK / 2 + 1; // LDS row stride in words
 template <typename TX>
 __global__ __launch_bounds__(256) void k_xprep(const TX* __restrict__ X, int64_t ntok, int64_t ldx, int C,
-                                               bool vec_ok, uint16_t* __restrict__ XTr, int64_t ldt,
+                                               bool vec_ok, uint16_t* __restrict__ XB, int64_t nks,
                                                HTargets tg, int ntarg, float* __restrict__ sT, int64_t lds,
                                                float* __restrict__ mpart, float* __restrict__ apart,
                                                float* __restrict__ spart) {
@@ -735,12 +751,15 @@ __global__ __launch_bounds__(256) void k_xprep(const TX* __restrict__ X, int64_t
     for (int k = 0; k < 8; ++k) tile[8 * grp + k][tp] = e0[k] | (e1[k] << 16);
   }
   __syncthreads();
-  // store: row c of X^T, 16 B (8 tokens) per lane, 32 lanes per row
-  for (int v = tid; v < XPC * (XTOK / 8); v += 256) {
-    const int c = v >> 5, q = v & 31;
-    if (c0 + c < C) {
-      const uint32_t* src = &tile[c][4 * q];
-      *reinterpret_cast<uint4*>(XTr + (int64_t)(c0 + c) * ldt + t0 + 8 * q) =
+  // store: the block's two 32-column groups x 16 steps, fragment-major: chunk (cb, kb) is 1 KB,
+  // lane L = fr + 32 fh holding tokens 16 kb + 8 fh .. +7 of column 32 cb + fr (zeros past C)
+  const int ncb = (C + 31) / 32;
+  for (int v = tid; v < 2 * (XTOK / 16) * 64; v += 256) {
+    const int L = v & 63, kbl = (v >> 6) & (XTOK / 16 - 1), cbl = v >> 10;
+    const int cb = c0 / 32 + cbl;
+    if (cb < ncb) {
+      const uint32_t* src = &tile[32 * cbl + (L & 31)][8 * kbl + 4 * (L >> 5)];
+      *reinterpret_cast<uint4*>(XB + (((int64_t)cb * nks + (int64_t)ch * (XTOK / 16) + kbl) * 64 + L) * 8) =
           make_uint4(src[0], src[1], src[2], src[3]);
     }
   }
@@ -934,7 +953,7 @@ SplitLayout split_layout(int64_t ntok, int C, int ntarg, int64_t tail, int S) {
   L.nchunk = L.ntok_p / XTOK;
   L.off_part = hessian_cnt_bytes();
   L.off_xt = L.off_part + align256(tail * S * (int64_t)XPART * 4);
-  L.off_st = L.off_xt + align256((int64_t)C * L.ntok_p * 2);
+  L.off_st = L.off_xt + align256((int64_t)((C + 31) / 32) * 32 * L.ntok_p * 2);
   L.off_m = L.off_st + align256((int64_t)ntarg * L.ntok_p * 4);
   L.off_a = L.off_m + align256(L.nchunk * C * 4);
   L.off_s = L.off_a + align256(L.nchunk * C * 4);
@@ -987,10 +1006,10 @@ int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, c
   dim3 pgrid((C + XPC - 1) / XPC, (unsigned)L.nchunk), fgrid((C + 255) / 256);
   if (x_dtype == RQ_F16)
     hipLaunchKernelGGL(k_xprep<__half>, pgrid, dim3(256), 0, s, (const __half*)x, ntok, ldx, C, vec_ok, xt,
-                       L.ntok_p, tg, ntarg, sT, L.ntok_p, mpart, apart, spart);
+                       nks, tg, ntarg, sT, L.ntok_p, mpart, apart, spart);
   else
     hipLaunchKernelGGL(k_xprep<__hip_bfloat16>, pgrid, dim3(256), 0, s, (const __hip_bfloat16*)x, ntok, ldx,
-                       C, vec_ok, xt, L.ntok_p, tg, ntarg, sT, L.ntok_p, mpart, apart, spart);
+                       C, vec_ok, xt, nks, tg, ntarg, sT, L.ntok_p, mpart, apart, spart);
   RQ_CHECK_LAUNCH();
   hipLaunchKernelGGL(k_xfinish, fgrid, dim3(256), 0, s, C, (int)L.nchunk, tg, ntarg, mpart, apart, spart,
                      scale);
@@ -1000,11 +1019,11 @@ int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, c
   float* wsf = tail > 0 ? reinterpret_cast<float*>(wb + L.off_part) : nullptr;
   dim3 grid((unsigned)(full + (int64_t)tail * S)), block(XTHREADS);
   if (x_dtype == RQ_F16)
-    hipLaunchKernelGGL(k_hessian_split<__half>, grid, block, 0, s, xt, L.ntok_p, C, sT, L.ntok_p, scale, tg,
-                       ntarg, nt, ntiles, nks, full, S, wsf, cnt);
+    hipLaunchKernelGGL(k_hessian_split<__half>, grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg, ntarg, nt,
+                       ntiles, nks, full, S, wsf, cnt);
   else
-    hipLaunchKernelGGL(k_hessian_split<__hip_bfloat16>, grid, block, 0, s, xt, L.ntok_p, C, sT, L.ntok_p,
-                       scale, tg, ntarg, nt, ntiles, nks, full, S, wsf, cnt);
+    hipLaunchKernelGGL(k_hessian_split<__hip_bfloat16>, grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg, ntarg,
+                       nt, ntiles, nks, full, S, wsf, cnt);
   RQ_CHECK_LAUNCH();
   return RQ_OK;
 }
