@@ -40,7 +40,7 @@ def hessian_roofline(flops, ms, math, extra):
     eq = flops / (ms * 1e-3) / 1e12
     if math == "split16":
         ach, peak = SPLIT_PIECES * eq, FP16_MFMA_PEAK_TFLOPS
-        kernel = "k_hessian_split<__half> (timed with its k_xstats + k_xfinish pre-pass)"
+        kernel = "k_hessian_split<__half> (timed with its k_xprep + k_xfinish pre-pass)"
     else:
         ach, peak = eq, FP32_MFMA_PEAK_TFLOPS
         kernel = "k_hessian_accum<__half>"

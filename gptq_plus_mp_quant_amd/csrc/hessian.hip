@@ -401,9 +401,6 @@ struct XType<__hip_bfloat16> {
   }
 };
 
-// 8 tokens of one column: w = fl32(x * s) * 2^e split into three 16-bit fragments.
-// (fma(x, s, 0) is rn(x * s); fma(-p, 1, w) is the exact w - p.  Written as fma so that the
-// fp16 -> fp32 conversions can fold into v_fma_mix.)
 // One token pair of one column (x of tokens t, t+1 packed in xw): w = fl32(x * s) * 2^e for
 // both, split into three packed pieces.  fp16: each residual w - p is one v_fma_mix_f32
 // (-p as an fp16 operand, times 1, plus w: exact), written out because the compiler emits a

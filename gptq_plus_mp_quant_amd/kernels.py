@@ -51,13 +51,16 @@ _HWS = {}
 
 
 def hessian_workspace(x, ntargets):
-    """Per-device, grow-only workspace for the Hessian launches' tail slices (zero-filled on
-    allocation; the kernels leave their counters zero).  Launches are stream-ordered, so the
-    calls of one process on one device share it."""
+    """Grow-only workspace of the Hessian launches, one per (device, stream): the
+    fragment-blocked copy of the chunk, the saliency copies, the pre-pass partials and the
+    tail slices' partial tiles and counters (zero-filled on allocation; the kernels leave the
+    counters zero).  Launches on one stream are ordered, so the calls on that stream share it;
+    calls on another stream get their own."""
     need = int(nat.load().rq_hessian_workspace_bytes(x.shape[0], x.shape[1], int(ntargets)))
     if need <= 0:
         return None, 0
-    key = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    dev = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    key = (dev, torch.cuda.current_stream(x.device).cuda_stream)
     ws = _HWS.get(key)
     if ws is None or ws.numel() < need:
         ws = torch.zeros(need, dtype=torch.uint8, device=x.device)
