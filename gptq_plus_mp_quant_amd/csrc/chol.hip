@@ -7,7 +7,7 @@
 // index-reversal permutation and L L^T = P H P,  U = P L^-1 P.  The factorisation and the
 // inverse L^-1 run together in one right-looking blocked pass in fp64 (64-wide blocks
 // inside 256-wide panels):
-//   per block k:  L_kk = chol(A_kk) and T = L_kk^-1 (one wavefront, rows in registers),
+//   per block k:  L_kk = chol(A_kk) and T = L_kk^-1 (one workgroup),
 //                 L_ik = A_ik T^T,  X_k = T B_k  (row block k of L^-1),
 //                 A_ij -= L_ik L_jk^T (lower tiles),  B_i -= L_ik X_k   (fp64 MFMA GEMMs),
 // where B accumulates I - sum_m L_im X_m; the updates of the trailing matrix and of the
@@ -77,81 +77,175 @@ __global__ __launch_bounds__(256) void k_reverse_to_f64(const float* __restrict_
   }
 }
 
-// Factor the nb x nb diagonal block of A at (k, k) and invert it: one wavefront, lane r owns
-// row r of the block in registers (rows >= nb are identity padding).  Step j broadcasts the
-// pivot and the scaled column through LDS; the inverse T = L^-1 is formed the same way row by
-// row (forward substitution).  Fully unrolled, so every register index is static.  Writes T
-// (lower, explicit zeros above) to Tbuf and to Linv's diagonal block.
-__global__ __launch_bounds__(64) void k_chol_diag(const double* __restrict__ A, int C, int k,
-                                                  int nb, double* __restrict__ Tbuf,
-                                                  double* __restrict__ Linv, int64_t ws,
-                                                  int* info_all) {
-  __shared__ __attribute__((aligned(16))) double buf[NB];
-  __shared__ double piv;
+// 1/sqrt(d) and sqrt(d) in fp64 from the hardware estimate and two Newton steps
+// y <- y (3 - d y^2) / 2 (the error squares each step: well below fp64 rounding after two).
+__device__ __forceinline__ void rsqrt_newton(double d, double& rs, double& sq) {
+  double y = __builtin_amdgcn_rsq(d);
+  const double h = 0.5 * d;
+  y = y * __builtin_fma(-h * y, y, 1.5);
+  y = y * __builtin_fma(-h * y, y, 1.5);
+  rs = y;
+  sq = d * y;
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Sum of a double over the 4 lanes of a quad (DPP quad_perm moves, no LDS).
+template <int CTRL>
+__device__ __forceinline__ double quad_mov_f64(double v) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double quad_sum_f64(double v) {
+  v = v + quad_mov_f64<0xB1>(v);   // lanes [1, 0, 3, 2]
+  return v + quad_mov_f64<0x4E>(v);   // lanes [2, 3, 0, 1]
+}
+
+// Factor the nb x nb diagonal block of A at (k, k) and invert it; one workgroup of 4 waves per
+// batch entry (rows >= nb are identity padding).
+//  - Factor: lane r of wave w holds L[r][16w .. 16w+15] (16 registers).  Step j: the wave
+//    holding column j takes the pivot from lane j (readlane), forms 1/sqrt and sqrt, scales
+//    its column (L[r][j], zero for r <= j) and publishes it in `col` (two buffers, alternating
+//    by step, so one barrier per step orders each write after the previous reads); then every
+//    wave subtracts L[r][j] L[l][j] from its 16 columns l (col is zero at l <= j, so the
+//    finished columns stay as they are).
+//  - Inverse: lane quad c of the workgroup computes column c of T = L^-1 by forward
+//    substitution t[i] = (delta_ic - sum_{m<i} L[i][m] t[m]) / L[i][i]; lane q of the quad
+//    holds the rows m = 4p + q and its part of each dot product, and the quad adds the four
+//    parts with DPP moves.  L is staged in LDS column-interleaved (element (i, 4p + q) at
+//    i * LS + 16 q + p), so a lane reads its operands of a row in 16-byte pieces, and the
+//    lanes of one q in a wave all read the same address (broadcast).
+// Writes T (lower, exact zeros above) to Tbuf and to Linv's diagonal block.
+constexpr int CD_THREADS = 256;
+__global__ __launch_bounds__(CD_THREADS) void k_chol_diag(const double* __restrict__ A, int C, int k,
+                                                          int nb, double* __restrict__ Tbuf,
+                                                          double* __restrict__ Linv, int64_t ws,
+                                                          int* info_all) {
+  constexpr int LS = NB + 2;                        // LDS row stride (16-byte aligned rows)
+  __shared__ __attribute__((aligned(16))) double S[NB * LS];
+  __shared__ __attribute__((aligned(16))) double col[2][NB];
+  __shared__ double dinv[NB];   // 1 / L[j][j]; NaN marks a failed pivot
   const int b = blockIdx.x;
   int* info = info_all + b;
   if (*info) return;
   A += b * ws;
   Tbuf += b * ws;
   Linv += b * ws;
-  const int r = threadIdx.x;
-  double a[NB];
+  const int tid = threadIdx.x;
+  const int r = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // columns 16 wave .. 16 wave + 15 of row r of the block's lower triangle (zeros above,
+  // identity on the padding rows).  Only rows < nb and columns < nb are read: a ragged last
+  // block reads with a clamped column index, and the mask clears those columns (they lie
+  // above the diagonal of every row that is read).  A full block with C even (k is a
+  // multiple of NB) has 16-byte aligned rows.
+  const int c0 = 16 * wave;
+  double a[16];
+  if (r < nb) {
+    const double* rowp = A + (int64_t)(k + r) * C + k + c0;
+    if (nb == NB && (C & 1) == 0) {
+      const double2* row = reinterpret_cast<const double2*>(rowp);
 #pragma unroll
-  for (int c = 0; c < NB; ++c) {
-    double v = (r >= nb && c == r) ? 1.0 : 0.0;
-    if (r < nb && c <= r) v = A[(int64_t)(k + r) * C + (k + c)];
-    a[c] = v;
+      for (int q = 0; q < 16; q += 2) {
+        const double2 v = row[q / 2];
+        a[q] = v.x;
+        a[q + 1] = v.y;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) a[q] = A[(int64_t)(k + r) * C + k + min(c0 + q, nb - 1)];
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      if (c0 + q > r) a[q] = 0.0;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) a[q] = (c0 + q == r) ? 1.0 : 0.0;
   }
+  __syncthreads();
+
   bool fail = false;
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
-    if (r == j) piv = a[j];
+    const int jw = j / 16, jq = j % 16;
+    double* cj = col[j & 1];
+    if (wave == jw) {
+      const double d = readlane_f64(a[jq], j);     // uniform pivot
+      double rd = 0.0, sq = 0.0;
+      const bool ok = d > 0.0 && rq_isfinite(d);
+      if (ok) rsqrt_newton(d, rd, sq);
+      const double lrj = (r > j) ? a[jq] * rd : 0.0;  // L[r][j]
+      a[jq] = (r == j) ? sq : lrj;
+      cj[r] = lrj;
+      if (r == 0) dinv[j] = ok ? rd : __builtin_nan("");
+    }
     __syncthreads();
-    const double d = piv;                           // uniform pivot
-    if (!(d > 0.0) || !rq_isfinite(d)) {
+    // dinv[j] is written once, before this barrier: every wave reads the same verdict.  The
+    // column is read before the verdict is tested (the reads are in bounds either way).
+    const double dj = dinv[j];
+    const double m = cj[r];
+    double cv[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cv[q] = cj[c0 + q];
+    if (!(dj == dj)) {
       fail = true;
       break;
     }
-    const double sq = sqrt(d);
-    const double rd = 1.0 / sq;
-    const double lrj = (r > j) ? a[j] * rd : 0.0;  // L[r][j]
-    a[j] = (r == j) ? sq : ((r > j) ? lrj : a[j]);
-    buf[r] = lrj;
-    __syncthreads();
 #pragma unroll
-    for (int l = j + 1; l < NB; ++l) a[l] = __builtin_fma(-lrj, buf[l], a[l]);
-    __syncthreads();
+    for (int q = 0; q < 16; ++q) a[q] = __builtin_fma(-m, cv[q], a[q]);
   }
   if (fail) {
-    if (r == 0) atomicExch(info, 1);
+    if (tid == 0) atomicExch(info, 1);
     return;
   }
-  // T = L^-1: t accumulates sum_{m < r} L[r][m] T[m][c]; row m is final at step m
-  double t[NB];
+  // L into LDS, column-interleaved; entries above the diagonal are zero
 #pragma unroll
-  for (int c = 0; c < NB; ++c) t[c] = 0.0;
-#pragma unroll
-  for (int m = 0; m < NB; ++m) {
-    if (r == m) {
-      const double rdm = 1.0 / a[m];
-#pragma unroll
-      for (int c = 0; c < m; ++c) t[c] = -t[c] * rdm;
-      t[m] = rdm;
-#pragma unroll
-      for (int c = 0; c <= m; ++c) buf[c] = t[c];
-    }
-    __syncthreads();
-    const double lrm = (r > m) ? a[m] : 0.0;
-#pragma unroll
-    for (int c = 0; c <= m; ++c) t[c] = __builtin_fma(lrm, buf[c], t[c]);
-    __syncthreads();
+  for (int q = 0; q < 16; ++q) {
+    const int c = c0 + q;
+    S[r * LS + 16 * (c & 3) + (c >> 2)] = (c <= r) ? a[q] : 0.0;
   }
+  __syncthreads();
+
+  const int cc = tid >> 2, qq = tid & 3;
+  const double* Sq = S + 16 * qq;
+  double t[16];
 #pragma unroll
-  for (int c = 0; c < NB; ++c) Tbuf[r * NB + c] = t[c];
-  if (r < nb) {
+  for (int p = 0; p < 16; ++p) t[p] = 0.0;
 #pragma unroll
-    for (int c = 0; c < NB; ++c)
-      if (c < nb) Linv[(int64_t)(k + r) * C + (k + c)] = t[c];
+  for (int i = 0; i < NB; ++i) {
+    // rows m = 4p + qq < i; L[i][m] = 0 for m >= i, so p runs to (i - 1) / 4 for every lane
+    double part = 0.0;
+    if (i > 0) {
+      const int np = (i - 1) / 4 + 1;
+      double s2[2] = {0.0, 0.0};
+#pragma unroll
+      for (int p = 0; p < np; p += 2) {
+        const double2 l = *reinterpret_cast<const double2*>(Sq + i * LS + p);
+        s2[0] = __builtin_fma(l.x, t[p], s2[0]);
+        if (p + 1 < np) s2[1] = __builtin_fma(l.y, t[p + 1], s2[1]);
+      }
+      part = s2[0] + s2[1];
+    }
+    const double di = dinv[i];
+    const double tot = quad_sum_f64(part);
+    const double ti = (((i == cc) ? 1.0 : 0.0) - tot) * di;
+    t[i >> 2] = ((i & 3) == qq) ? ti : t[i >> 2];   // a select, not a branch
+  }
+  // t[p] = T[4p + qq][cc]
+#pragma unroll
+  for (int p = 0; p < 16; ++p) Tbuf[(4 * p + qq) * NB + cc] = t[p];
+  if (cc < nb) {
+#pragma unroll
+    for (int p = 0; p < 16; ++p)
+      if (4 * p + qq < nb) Linv[(int64_t)(k + 4 * p + qq) * C + (k + cc)] = t[p];
   }
 }
 
@@ -296,7 +390,7 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
       const int jb = (pe - j < NB) ? (pe - j) : NB;
       const int below = C - j - jb;                      // rows below this block (whole matrix)
       const int pend = pe - j - jb;                      // panel columns right of this block
-      hipLaunchKernelGGL(k_chol_diag, dim3(nb), dim3(64), 0, s, A, C, j, jb, Tbuf, Linv, ws, info);
+      hipLaunchKernelGGL(k_chol_diag, dim3(nb), dim3(CD_THREADS), 0, s, A, C, j, jb, Tbuf, Linv, ws, info);
       RQ_CHECK_LAUNCH();
       int rc;
       if (below > 0) {
