@@ -707,9 +707,9 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
 }
 
 // Pre-pass over one 64-column x 256-token block of X: the block in the fragment-blocked
-// layout read by k_hessian_split (zeros past ntok and past C), each column's max |x| and sum_t x^2 (in token order) for this token block, and
-// (first column block only) each target's saliency, contiguous and zero padded, with its
-// max |s|.  Two tokens of one column share a 32-bit LDS word; the row stride of 129 words
+// layout read by k_hessian_split (zeros past ntok and past C), each column's max |x| and
+// sum_t x^2 for this token block, and (first column block only) each target's saliency,
+// contiguous and zero padded, with its max |s|.  Two tokens of one column share a 32-bit LDS word; the row stride of 129 words
 // keeps the transposing writes free of bank conflicts.
 constexpr int XPC = 64;            // columns per pre-pass block
 constexpr int XPRS = XTOK / 2 + 1; // LDS row stride in words
@@ -727,6 +727,7 @@ __global__ __launch_bounds__(256) void k_xprep(const TX* __restrict__ X, int64_t
   const int64_t t0 = (int64_t)ch * XTOK;
   const uint16_t* Xb = reinterpret_cast<const uint16_t*>(X);
   // load: 8 column groups (8 columns, 16 B) x 128 token pairs; lane = group + 8 * pair
+#pragma unroll
   for (int v = tid; v < 8 * (XTOK / 2); v += 256) {
     const int grp = v & 7, tp = v >> 3;
     const int cb = c0 + 8 * grp;
@@ -760,22 +761,31 @@ __global__ __launch_bounds__(256) void k_xprep(const TX* __restrict__ X, int64_t
           make_uint4(src[0], src[1], src[2], src[3]);
     }
   }
-  if (tid < XPC && c0 + tid < C) {
+  // column statistics: 4 threads per column, 64 tokens each in token order (square, then
+  // add), the four parts added in order
+  {
+    __shared__ float qm[4][XPC], qa[4][XPC];
+    const int cl = tid & (XPC - 1), part = tid >> 6;
     float m = 0.0f, a = 0.0f;
-    for (int w = 0; w < XTOK / 2; ++w) {
-      const uint32_t u = tile[tid][w];
+#pragma unroll 8
+    for (int w = part * (XTOK / 8); w < (part + 1) * (XTOK / 8); ++w) {
+      const uint32_t u = tile[cl][w];
       const float v0 = XType<TX>::lo(u), v1 = XType<TX>::hi(u);
       m = fmaxf(m, fabsf(v0));
-      a = a + v0 * v0;                // (inp ** 2).sum(0): square, then add, in token order
+      a = a + v0 * v0;
       m = fmaxf(m, fabsf(v1));
       a = a + v1 * v1;
     }
-    mpart[(int64_t)ch * C + c0 + tid] = m;
-    apart[(int64_t)ch * C + c0 + tid] = a;
+    qm[part][cl] = m;
+    qa[part][cl] = a;
+    if (tid < HMAXT) smx[tid] = 0u;
+    __syncthreads();
+    if (tid < XPC && c0 + tid < C) {
+      mpart[(int64_t)ch * C + c0 + tid] = fmaxf(fmaxf(qm[0][tid], qm[1][tid]), fmaxf(qm[2][tid], qm[3][tid]));
+      apart[(int64_t)ch * C + c0 + tid] = ((qa[0][tid] + qa[1][tid]) + qa[2][tid]) + qa[3][tid];
+    }
   }
   if (blockIdx.x != 0) return;
-  if (tid < HMAXT) smx[tid] = 0u;
-  __syncthreads();
   for (int g = 0; g < ntarg; ++g) {
     const int64_t t = t0 + tid;
     const float s = (t < ntok) ? tg.sal[g][t * tg.ld_sal[g]] : 0.0f;
@@ -786,30 +796,54 @@ __global__ __launch_bounds__(256) void k_xprep(const TX* __restrict__ X, int64_t
   if (tid < ntarg) spart[(int64_t)ch * HMAXT + tid] = __uint_as_float(smx[tid]);
 }
 
-// Reduce the token blocks: act_square += sum_t x^2 (blocks in order), and the per (target,
-// column) scale 2^e with e = 15 - E for max|x_c| * max|s_g| = f * 2^E, f in [0.5, 1).
+// Reduce the token blocks: act_square += sum_t x^2, and the per (target, column) scale 2^e
+// with e = 15 - E for max|x_c| * max|s_g| = f * 2^E, f in [0.5, 1).  A workgroup takes 32
+// columns; 8 threads per column each reduce one eighth of the blocks (in block order), and the
+// eight parts are added in a fixed order, so the sum is deterministic.  Every workgroup also
+// forms max|s_g| over all blocks (exact in any order).
+constexpr int XF_COLS = 32;
+constexpr int XF_SEG = 8;
 __global__ __launch_bounds__(256) void k_xfinish(int C, int nchunk, HTargets tg, int ntarg,
                                                  const float* __restrict__ mpart,
                                                  const float* __restrict__ apart,
                                                  const float* __restrict__ spart, float* __restrict__ scale) {
-  __shared__ float smax[HMAXT];
-  if (threadIdx.x < ntarg) {
+  __shared__ float smax[XF_SEG][HMAXT];
+  __shared__ float pm[XF_SEG][XF_COLS], pa[XF_SEG][XF_COLS];
+  const int t = threadIdx.x;
+  const int lane32 = t & 31, seg = t >> 5;
+  {
     float m = 0.0f;
-    for (int ch = 0; ch < nchunk; ++ch) m = fmaxf(m, spart[(int64_t)ch * HMAXT + threadIdx.x]);
-    smax[threadIdx.x] = m;
+    if (lane32 < ntarg)
+      for (int ch = seg; ch < nchunk; ch += XF_SEG) m = fmaxf(m, spart[(int64_t)ch * HMAXT + lane32]);
+    smax[seg][lane32] = m;
   }
-  __syncthreads();
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= C) return;
+  const int c = blockIdx.x * XF_COLS + lane32;
+  const int ch0 = (int)((int64_t)nchunk * seg / XF_SEG), ch1 = (int)((int64_t)nchunk * (seg + 1) / XF_SEG);
   float m = 0.0f, a = 0.0f;
-  for (int ch = 0; ch < nchunk; ++ch) {
-    m = fmaxf(m, mpart[(int64_t)ch * C + c]);
-    a = a + apart[(int64_t)ch * C + c];
+  if (c < C) {
+#pragma unroll 8
+    for (int ch = ch0; ch < ch1; ++ch) {
+      m = fmaxf(m, mpart[(int64_t)ch * C + c]);
+      a = a + apart[(int64_t)ch * C + c];
+    }
+  }
+  pm[seg][lane32] = m;
+  pa[seg][lane32] = a;
+  __syncthreads();
+  if (seg != 0 || c >= C) return;
+  float mt = pm[0][lane32], at = pa[0][lane32];
+#pragma unroll
+  for (int q = 1; q < XF_SEG; ++q) {
+    mt = fmaxf(mt, pm[q][lane32]);
+    at = at + pa[q][lane32];
   }
   for (int g = 0; g < ntarg; ++g)
-    if (tg.act[g]) tg.act[g][c] += a;
+    if (tg.act[g]) tg.act[g][c] += at;
   for (int g = 0; g < ntarg; ++g) {
-    const float mm = m * smax[g];
+    float sm = smax[0][g];
+#pragma unroll
+    for (int q = 1; q < XF_SEG; ++q) sm = fmaxf(sm, smax[q][g]);
+    const float mm = mt * sm;
     int e = 0;
     if (mm > 0.0f && mm <= 3.402823466e38f) {
       int E = 0;
@@ -1000,7 +1034,7 @@ int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, c
   float* apart = reinterpret_cast<float*>(wb + L.off_a);
   float* spart = reinterpret_cast<float*>(wb + L.off_s);
   float* scale = reinterpret_cast<float*>(wb + L.off_scale);
-  dim3 pgrid((C + XPC - 1) / XPC, (unsigned)L.nchunk), fgrid((C + 255) / 256);
+  dim3 pgrid((C + XPC - 1) / XPC, (unsigned)L.nchunk), fgrid((C + XF_COLS - 1) / XF_COLS);
   if (x_dtype == RQ_F16)
     hipLaunchKernelGGL(k_xprep<__half>, pgrid, dim3(256), 0, s, (const __half*)x, ntok, ldx, C, vec_ok, xt,
                        nks, tg, ntarg, sT, L.ntok_p, mpart, apart, spart);
