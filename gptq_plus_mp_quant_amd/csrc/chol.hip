@@ -393,50 +393,42 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
       hipLaunchKernelGGL(k_chol_diag, dim3(nb), dim3(CD_THREADS), 0, s, A, C, j, jb, Tbuf, Linv, ws, info);
       RQ_CHECK_LAUNCH();
       int rc;
-      if (below > 0) {
-        // L_ij = A_ij T^T  (in place, every row below the block)
-        GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)(j + jb) * C + j, C, Tbuf, NB,
-                                                       A + (int64_t)(j + jb) * C + j, C, below, jb,
-                                                       jb, 1.0, EPI_STORE));
-        if ((rc = launch_gemm(g, false, true, s, nb))) return rc;
-      }
-      if (j > 0) {
-        // X_j[:, 0:j] = T B_j[:, 0:j]  (in place, row block j of L^-1)
-        GemmArgs<double> g = batched(gemm_args<double>(Tbuf, NB, Linv + (int64_t)j * C, C,
-                                                       Linv + (int64_t)j * C, C, jb, j, jb, 1.0,
-                                                       EPI_STORE));
-        if ((rc = launch_gemm(g, false, false, s, nb))) return rc;
-      }
+      // one launch: L_ij = A_ij T^T (in place, every row below the block) and
+      // X_j[:, 0:j] = T B_j[:, 0:j] (in place, row block j of L^-1)
+      GemmArgs<double> lij = batched(gemm_args<double>(A + (int64_t)(j + jb) * C + j, C, Tbuf, NB,
+                                                       A + (int64_t)(j + jb) * C + j, C, below, jb, jb,
+                                                       1.0, EPI_STORE));
+      GemmArgs<double> xj = batched(gemm_args<double>(Tbuf, NB, Linv + (int64_t)j * C, C,
+                                                      Linv + (int64_t)j * C, C, jb, j, jb, 1.0, EPI_STORE));
+      if ((rc = launch_gemm_pair(lij, xj, s, nb))) return rc;
       if (pend > 0) {
-        // inside the panel: A[j+jb:, j+jb:pe] -= L[j+jb:, j] L[j+jb:pe, j]^T (lower tiles)
+        // one launch, inside the panel: A[j+jb:, j+jb:pe] -= L[j+jb:, j] L[j+jb:pe, j]^T (lower
+        // tiles) and the panel rows of L^-1: B[j+jb:pe, 0:j+jb] -= L[j+jb:pe, j] X_j
         GemmArgs<double> h = batched(gemm_args<double>(A + (int64_t)(j + jb) * C + j, C,
                                                        A + (int64_t)(j + jb) * C + j, C,
                                                        A + (int64_t)(j + jb) * C + (j + jb), C, below,
                                                        pend, jb, -1.0, EPI_ACCUM));
         h.lower_only = 1;
-        if ((rc = launch_gemm(h, false, true, s, nb))) return rc;
-        // and the panel rows of L^-1: B[j+jb:pe, 0:j+jb] -= L[j+jb:pe, j] X_j
         GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)(j + jb) * C + j, C,
                                                        Linv + (int64_t)j * C, C,
                                                        Linv + (int64_t)(j + jb) * C, C, pend, j + jb,
                                                        jb, -1.0, EPI_ACCUM));
-        if ((rc = launch_gemm(g, false, false, s, nb))) return rc;
+        if ((rc = launch_gemm_pair(h, g, s, nb))) return rc;
       }
     }
     const int rest = C - pe;
     if (rest > 0) {
-      int rc;
-      // trailing matrix: A[pe:, pe:] -= L[pe:, k:pe] L[pe:, k:pe]^T (lower tiles, K = kw)
+      // one launch: the trailing matrix A[pe:, pe:] -= L[pe:, k:pe] L[pe:, k:pe]^T (lower tiles,
+      // K = kw) and the rows of L^-1 below the panel: B[pe:, 0:pe] -= L[pe:, k:pe] X[k:pe, 0:pe]
       GemmArgs<double> h = batched(gemm_args<double>(A + (int64_t)pe * C + k, C, A + (int64_t)pe * C + k,
                                                      C, A + (int64_t)pe * C + pe, C, rest, rest, kw,
                                                      -1.0, EPI_ACCUM));
       h.lower_only = 1;
-      if ((rc = launch_gemm(h, false, true, s, nb))) return rc;
-      // rows of L^-1 below the panel: B[pe:, 0:pe] -= L[pe:, k:pe] X[k:pe, 0:pe]
       GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)pe * C + k, C, Linv + (int64_t)k * C,
                                                      C, Linv + (int64_t)pe * C, C, rest, pe, kw, -1.0,
                                                      EPI_ACCUM));
-      if ((rc = launch_gemm(g, false, false, s, nb))) return rc;
+      int rc;
+      if ((rc = launch_gemm_pair(h, g, s, nb))) return rc;
     }
   }
   hipLaunchKernelGGL(k_output_upper, gcol, blk, 0, s, Linv, C, Hinv, ws, info);

@@ -89,18 +89,16 @@ __device__ __forceinline__ void load_chunk(const T* __restrict__ src, bool vec, 
   }
 }
 
+// One 64x64 output tile (row tile ti, column tile tj) of batch entry bz.
 template <typename T, bool TA, bool TB>
-__global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
+__device__ __forceinline__ void gemm_tile_body(GemmArgs<T> p, int ti, int tj, int bz,
+                                               T (*__restrict__ As)[GT + GPAD],
+                                               T (*__restrict__ Bs)[GT + GPAD]) {
   using acc_t = typename Mfma16<T>::acc_t;
-  __shared__ T As[GKT][GT + GPAD];
-  __shared__ T Bs[GKT][GT + GPAD];
-
-  const int bz = blockIdx.z;
   if (p.abort_flag && p.abort_flag[bz]) return;
   p.A += bz * p.sA;
   p.B += bz * p.sB;
   p.Cm += bz * p.sC;
-  const int ti = blockIdx.y, tj = blockIdx.x;
   if (p.lower_only && tj > ti) return;
   const int i0 = ti * GT, j0 = tj * GT;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -230,6 +228,24 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
   if (p.nz_flag && nz) atomicOr(p.nz_flag, 1);
 }
 
+template <typename T, bool TA, bool TB>
+__global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
+  __shared__ T As[GKT][GT + GPAD];
+  __shared__ T Bs[GKT][GT + GPAD];
+  gemm_tile_body<T, TA, TB>(p, blockIdx.y, blockIdx.x, blockIdx.z, As, Bs);
+}
+
+// Two independent GEMMs in one launch: tiles [0, n1) of the flattened grid belong to p1
+// (A B^T), the rest to p2 (A B); grid.z is the batch entry of both.
+template <typename T>
+__global__ __launch_bounds__(256) void k_gemm_pair(GemmArgs<T> p1, GemmArgs<T> p2, int n1x, int n1, int n2x) {
+  __shared__ T As[GKT][GT + GPAD];
+  __shared__ T Bs[GKT][GT + GPAD];
+  const int b = blockIdx.x;
+  if (b < n1) gemm_tile_body<T, false, true>(p1, b / n1x, b % n1x, blockIdx.z, As, Bs);
+  else gemm_tile_body<T, false, false>(p2, (b - n1) / n2x, (b - n1) % n2x, blockIdx.z, As, Bs);
+}
+
 template <typename T>
 inline int launch_gemm(GemmArgs<T> a, bool ta, bool tb, hipStream_t s, int batch = 1) {
   if (a.M <= 0 || a.N <= 0 || batch <= 0) return RQ_OK;
@@ -241,6 +257,23 @@ inline int launch_gemm(GemmArgs<T> a, bool ta, bool tb, hipStream_t s, int batch
   else if (!ta && tb) hipLaunchKernelGGL((k_gemm_tile<T, false, true>), grid, block, 0, s, a);
   else if (ta && !tb) hipLaunchKernelGGL((k_gemm_tile<T, true, false>), grid, block, 0, s, a);
   else hipLaunchKernelGGL((k_gemm_tile<T, true, true>), grid, block, 0, s, a);
+  return hipGetLastError() == hipSuccess ? RQ_OK : RQ_EHIP;
+}
+
+// p1 = A B^T and p2 = A B (either may be empty: M or N <= 0) in one launch.
+template <typename T>
+inline int launch_gemm_pair(GemmArgs<T> p1, GemmArgs<T> p2, hipStream_t s, int batch = 1) {
+  const bool e1 = p1.M <= 0 || p1.N <= 0, e2 = p2.M <= 0 || p2.N <= 0;
+  if (batch <= 0 || (e1 && e2)) return RQ_OK;
+  if (e1) return launch_gemm(p2, false, false, s, batch);
+  if (e2) return launch_gemm(p1, false, true, s, batch);
+  auto al = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  auto ld_ok = [](int64_t ld) { return ((ld * (int64_t)sizeof(T)) & 15) == 0; };
+  p1.vec = al(p1.A) && al(p1.B) && ld_ok(p1.lda) && ld_ok(p1.ldb) && ld_ok(p1.sA) && ld_ok(p1.sB);
+  p2.vec = al(p2.A) && al(p2.B) && ld_ok(p2.lda) && ld_ok(p2.ldb) && ld_ok(p2.sA) && ld_ok(p2.sB);
+  const int n1x = (p1.N + GT - 1) / GT, n1 = n1x * ((p1.M + GT - 1) / GT);
+  const int n2x = (p2.N + GT - 1) / GT, n2 = n2x * ((p2.M + GT - 1) / GT);
+  hipLaunchKernelGGL(k_gemm_pair<T>, dim3(n1 + n2, 1, batch), dim3(256), 0, s, p1, p2, n1x, n1, n2x);
   return hipGetLastError() == hipSuccess ? RQ_OK : RQ_EHIP;
 }
 
