@@ -292,6 +292,49 @@ __global__ __launch_bounds__(256) void k_output_full(const double* __restrict__ 
   if (bad) atomicExch(info, 3);
 }
 
+// *out = max(*out, max_i |x_i|) as fp32 bit patterns (non-negative floats order like their
+// bits, and a NaN's bits exceed +inf's).  *out starts at 0.
+// 16-byte loads where x is 16-byte aligned; one atomic per workgroup.
+__global__ __launch_bounds__(256) void k_absmax_bits(const float* __restrict__ x, int64_t n,
+                                                     unsigned* __restrict__ out) {
+  __shared__ unsigned wm[4];
+  unsigned m = 0u;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  int64_t done = 0;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    const int64_t n4 = n / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    for (int64_t i = i0; i < n4; i += stride) {
+      const float4 v = x4[i];
+      m = max(m, max(max(__float_as_uint(fabsf(v.x)), __float_as_uint(fabsf(v.y))),
+                     max(__float_as_uint(fabsf(v.z)), __float_as_uint(fabsf(v.w)))));
+    }
+    done = 4 * n4;
+  }
+  for (int64_t i = done + i0; i < n; i += stride) m = max(m, __float_as_uint(fabsf(x[i])));
+  for (int o = 32; o > 0; o >>= 1) m = max(m, (unsigned)__shfl_xor((int)m, o, 64));
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    m = max(max(wm[0], wm[1]), max(wm[2], wm[3]));
+    if (m) atomicMax(out, m);
+  }
+}
+
+// need |= some row r with !(sum_k |G[r][k]| * mh < 3e38) (fp64 sums; a non-finite G or mh
+// fails the test).  One wavefront per row.
+__global__ __launch_bounds__(256) void k_z_rows_need(const float* __restrict__ G, int64_t ldg, int R,
+                                                     int C, const float* __restrict__ mh,
+                                                     int* __restrict__ need) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (r >= R) return;
+  double s = 0.0;
+  for (int k = lane; k < C; k += 64) s += (double)fabsf(G[(int64_t)r * ldg + k]);
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if (lane == 0 && !(s * (double)*mh < 3.0e38)) atomicOr(need, 1);
+}
+
 // compute_safe_beta_from_reference_loss row statistics (gptq_plus_utils.py:183-193).
 // One wavefront per row.
 __global__ __launch_bounds__(256) void k_safe_beta(const float* __restrict__ G, int64_t ldg,
@@ -483,6 +526,21 @@ extern "C" int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* H
   z.row_scale = beta;
   z.row_bcast = (beta_mode == 0);
   z.nz_flag = z_nonzero;
+  if (beta_mode == 0) {
+    // With beta = 0, Z is zero unless a product or a partial sum of G Hinv^T is not finite
+    // (then the reference's 0 * inf is NaN).  Every partial sum of row r is bounded by
+    // sum_k |G[r][k]| * max|Hinv|, so when that bound stays well inside the fp32 range for
+    // every row (and G is finite) Z is zero and the product is skipped: z_nonzero stays 0,
+    // and the Z launch only stores zeros.  Otherwise z_nonzero is raised and Z is formed.
+    // max|Hinv| passes through beta's storage (as bits), which is reset to 0 afterwards.
+    unsigned* mh = reinterpret_cast<unsigned*>(beta);
+    hipLaunchKernelGGL(k_absmax_bits, dim3(1024), dim3(256), 0, s, Hinv, (int64_t)C * C, mh);
+    hipLaunchKernelGGL(k_z_rows_need, dim3((R_s + 3) / 4), dim3(256), 0, s, G_sub, ldg, R_s, C,
+                       (const float*)beta, z_nonzero);
+    hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(1), 0, s, beta, 0.0f);
+    RQ_CHECK_LAUNCH();
+    z.skip_if_zero = z_nonzero;
+  }
   if ((rc = launch_gemm(z, false, true, s))) return rc;
   // GHinv = Z Hinv ; B(k, j) = Hinv[k][j] vanishes for k > j; all-zero Z -> zeros
   GemmArgs<float> h = gemm_args<float>(Z, ldz, Hinv, C, GHinv, ldz, R_s, C, C, 1.0f, EPI_STORE);

@@ -288,6 +288,40 @@ def test_gptqplus_terms(alpha, ref_loss):
         assert not Z.any() and not GH.any()
 
 
+def test_gptqplus_terms_zero_beta_nonfinite():
+    """beta = 0 (alpha = 0): Z = (G Hinv^T) * 0 is zero except where a product or partial sum
+    is not finite, where the reference yields NaN: rows with inf / NaN in G, and a row whose
+    (same-sign) products overflow fp32.  The kernel skips the product only when it can show Z
+    is zero.  Rows with finite G stay exactly zero; each bad row holds NaN in Z (the product
+    skips the structurally zero part of Hinv, so the NaN positions inside a bad row may be
+    fewer than the reference's) and is all NaN in GHinv = Z Hinv, as in the oracle."""
+    C, R_s = 192, 48
+    H = _spd(98, C)
+    Hinit_o, Hinv_o, *_ = hessian_inverse_with_fallback(H, 0.01)
+    Gs = torch.from_numpy(rng(5).standard_normal((R_s, C)).astype(np.float32))
+    Gs[3, 17] = float("inf")
+    Gs[10, 0] = float("nan")
+    h0 = Hinv_o[0].double()
+    Gs[20] = (torch.sign(h0) * min(3.0e38, 5.0e38 / float(h0.abs().sum()))).float()
+    bad = [3, 10, 20]
+    good = [r for r in range(R_s) if r not in bad]
+    beta_o, Z_o, GH_o, _ = gradient_terms(Gs, Hinit_o, Hinv_o, 0.0, 0.0, R_s * 2, C)
+    assert bool(Z_o[20, 0].isnan())                # the overflow row does overflow
+    beta = torch.empty(1, device=DEV)
+    Z = torch.empty(R_s, C, device=DEV)
+    GH = torch.empty(R_s, C, device=DEV)
+    nz = torch.zeros(1, dtype=torch.int32, device=DEV)
+    K.gptqplus_terms(Gs.to(DEV), None, Hinv_o.to(DEV), 0.0, 0.0, 0, beta, Z, GH, None, nz)
+    torch.cuda.synchronize()
+    Zc, GHc = Z.cpu(), GH.cpu()
+    assert float(beta[0]) == 0.0 and int(nz.item()) == 1
+    for z, gh in ((Zc, GHc), (Z_o, GH_o)):
+        assert not z[good].any() and not gh[good].any()
+        for r in bad:
+            assert z[r].isnan().any() and gh[r].isnan().all()
+    assert bool(Zc[20, 0].isnan())
+
+
 def test_trailing_update_matches_formula():
     r = rng(8)
     G, R_s, C, i1, cnt = 2, 96, 300, 64, 64
