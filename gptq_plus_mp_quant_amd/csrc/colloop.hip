@@ -2,20 +2,21 @@
 // (outer) update (:1500-1570), all subgroups in one launch each, for the frozen and the two
 // surrogate g_update modes.
 //
-// k_quant_block: rows are independent, so each row of the block is owned by a quad of 4
-// lanes; lane t of the quad holds columns t, t+4, t+8, ... of the row in registers (W1, GHinv1,
-// Z1), 64 rows per 256-thread workgroup, one subgroup per workgroup.  The B x B block of
-// Hinv (upper) sits in LDS.  Column i = 4m + r is quantised by lane r of every quad, its error
-// is broadcast inside the quad with a DPP quad_perm move, and every lane applies the rank-1
-// update to its own columns.  After each group of 4 columns the register slots rotate down
-// by one so every slot index is a compile-time constant.  Arithmetic follows the reference
-// op by op (no contraction, IEEE divide, round-half-even):
+// k_quant_block: rows are independent, so each row of the block is owned by 16 lanes (one DPP
+// row); lane t holds columns t, t+16, ..., t+112 of the row in 8 registers (W1, GHinv1, Z1),
+// 16 rows per 256-thread workgroup, one subgroup per workgroup, so 4096 rows keep every SIMD
+// busy.  The B x B block of Hinv (upper) sits in LDS as Hp[i][t][k] = Hinv1[i][16k + t], so a
+// lane reads its 8 entries of row i with two 16-byte loads.  Column i = 16m + r is quantised by
+// lane r of every row, its error is broadcast to the row with one DPP row_newbcast move, and
+// every lane applies the rank-1 update to its own columns.  The 128-column loop is fully
+// unrolled, so every register index is a compile-time constant.  Arithmetic follows the
+// reference op by op (no contraction, IEEE divide, round-half-even):
 //   code = clamp(rint(w / s), -(maxq+1), maxq); q = s * code
 //   err  = ((w - q) - gh_i) / Hinv1[i][i]
 //   w_j  = w_j - (err * Hinv1[i][j] + gh_j);   gh_j = gh_j - z_i * Hinv1[i][j]     (j >= i)
 // so with identical inputs codes and errors are bit-identical to the reference's CPU loop.
 // The atomic variant (:1238-1288) quantises the block start at once and solves
-// Err * Hinv1 = W - Q - GHinv1 by forward substitution with the same quad layout.
+// Err * Hinv1 = W - Q - GHinv1 by forward substitution with the same row layout.
 //
 // Surrogate modes (:580-584, :1190-1199, :1360-1367): the first-order term used in place of
 // gh is gh_eff = gh + beta_row * (W_cur - W_anchor), re-evaluated before every column, where
@@ -29,29 +30,33 @@
 // In the surrogate modes the GH[:, i2:] of the first term is GH + beta_row * (W - W_anchor)
 // (outer refresh "surrogate_block", :1500-1511), the GH update itself is unchanged; in
 // block_gd the whole W update is scaled by second_order_scale (:1546-1549).
+#include <type_traits>
+
 #include "rq_common.h"
 
 namespace {
 
 constexpr int QB_MAXB = 128;
 
-// LDS column of register slot s of lane t.  Every slot is updated every column, so the
-// compiler can batch the LDS reads without per-slot branches: slots past the block (column
-// >= count) hold zeros and meet zero Hinv entries, slots past column 127 (they only exist
-// late in the block, and never become live again) read a clamped, in-bounds column.
-__device__ __forceinline__ int hcol(int s, int t) { return min(4 * s + t, QB_MAXB - 1); }
-
-template <int CTRL>
-__device__ __forceinline__ float quad_bcast(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float quad_lane(float v, int r) {
-  switch (r) {
-    case 0: return quad_bcast<0x00>(v);
-    case 1: return quad_bcast<0x55>(v);
-    case 2: return quad_bcast<0xAA>(v);
-    default: return quad_bcast<0xFF>(v);
+// Compile-time loop: f(std::integral_constant<int, 0>) ... f(integral_constant<int, N - 1>).
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
   }
+}
+
+// Lanes per row in k_quant_block, and the broadcast of lane r of each 16-lane DPP row to the
+// whole row (row_newbcast).
+constexpr int QL = 16;
+template <int R>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + R, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
 struct QBArgs {
@@ -78,31 +83,47 @@ struct QBArgs {
 };
 
 // GM: 0 frozen, 1 surrogate_block, 2 surrogate_online, 3 frozen with every in-block update
-// scaled by second_order_scale (block_gd, :1344-1349)
-template <int SLOTS, int GM>
+// scaled by second_order_scale (block_gd, :1344-1349).  NS register slots per lane: lane t of
+// a row holds columns t, t + 16, ..., t + 16 (NS - 1) of the block (NS = 8 for 128 columns).
+template <int NS, int GM>
 __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
-  __shared__ float Hl[QB_MAXB][QB_MAXB];
+  constexpr int NB = QL * NS;             // widest block this instantiation takes
+  // Hp[i][t][k] = Hinv1[i][16 k + t] (upper; zeros below the diagonal and past the block):
+  // a lane reads its NS entries of row i as NS / 4 aligned 16-byte loads
+  __shared__ __attribute__((aligned(16))) float Hp[NB][QL][NS];
   const int tid = threadIdx.x;
-  const int t = tid & 3;
+  const int t = tid & (QL - 1);
   const int sub = blockIdx.y;
-  const int row_local = blockIdx.x * 64 + (tid >> 2);
+  const int row_local = blockIdx.x * (256 / QL) + (tid / QL);
   const bool valid = row_local < a.R_s;
   const int row = sub * a.R_s + (valid ? row_local : 0);
   const int count = a.count, i1 = a.i1;
   const float* Hs = a.Hinv + (int64_t)sub * a.C * a.C;
   const bool use_gh = (*a.z_nonzero != 0);
 
-  for (int e = tid; e < QB_MAXB * QB_MAXB; e += 256) {
-    const int i = e / QB_MAXB, j = e % QB_MAXB;
-    Hl[i][j] = (i < count && j < count && j >= i) ? Hs[(int64_t)(i1 + i) * a.C + (i1 + j)] : 0.0f;
+  {
+    // all NB * NB / 256 loads of a thread in flight at once: clamped (in-bounds) addresses,
+    // the mask applied to the values
+    constexpr int PER = NB * NB / 256;
+    float v[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = tid + 256 * q, i = e / NB, j = e % NB;
+      v[q] = Hs[(int64_t)(i1 + min(i, count - 1)) * a.C + (i1 + min(j, count - 1))];
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = tid + 256 * q, i = e / NB, j = e % NB;
+      Hp[i][j % QL][j / QL] = (i < count && j < count && j >= i) ? v[q] : 0.0f;
+    }
   }
 
   constexpr bool SURR = (GM == 1 || GM == 2);
-  float w[SLOTS], gh[SLOTS], zz[SLOTS], sc[SLOTS], xr[SURR ? SLOTS : 1];
+  float w[NS], gh[NS], zz[NS], sc[NS], xr[SURR ? NS : 1];
   const float brow = SURR ? a.beta[row] : 0.0f;
 #pragma unroll
-  for (int k = 0; k < SLOTS; ++k) {
-    const int col = 4 * k + t;
+  for (int k = 0; k < NS; ++k) {
+    const int col = QL * k + t;
     const bool in = valid && col < count;
     const int64_t off = (int64_t)row * a.ldw + i1 + col;
     w[k] = in ? a.Wp[off] : 0.0f;
@@ -117,7 +138,7 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
     if (a.qmode == RQ_QMODE_STATIC && in) sc[k] = a.scale[(int64_t)a.col_group[i1 + col] * a.R + row];
   }
   // gh_eff of slot k from the current registers: gh + beta * (W_cur - W_anchor)
-  auto geff = [&](int k) -> float {
+  auto geff = [&](int k) __attribute__((always_inline)) -> float {
     if constexpr (!SURR) return gh[k];
     const float dw = (GM == 1) ? xr[k] : (w[k] - xr[k]);
     return gh[k] + brow * dw;
@@ -127,19 +148,24 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
   if (a.qmode == RQ_QMODE_CHANNEL) {
     srow = a.scale[row];
   } else if (a.qmode == RQ_QMODE_DYNAMIC) {
-    // find_params on the block start (gptq_plus_utils.py:1208-1209): per-row min/max
+    // find_params on the block start (gptq_plus_utils.py:1208-1209): per-row min/max over
+    // the 16 lanes of the row (quad swaps, then rotations by 4 and 8 inside the row)
     float mn = __builtin_inff(), mx = -__builtin_inff();
 #pragma unroll
-    for (int k = 0; k < SLOTS; ++k) {
-      if (4 * k + t < count) {
+    for (int k = 0; k < NS; ++k) {
+      if (QL * k + t < count) {
         mn = rq_nan_min(mn, w[k]);
         mx = rq_nan_max(mx, w[k]);
       }
     }
-    mn = rq_nan_min(mn, quad_bcast<0xB1>(mn));
-    mx = rq_nan_max(mx, quad_bcast<0xB1>(mx));
-    mn = rq_nan_min(mn, quad_bcast<0x4E>(mn));
-    mx = rq_nan_max(mx, quad_bcast<0x4E>(mx));
+    mn = rq_nan_min(mn, dpp_mov<0xB1>(mn));
+    mx = rq_nan_max(mx, dpp_mov<0xB1>(mx));
+    mn = rq_nan_min(mn, dpp_mov<0x4E>(mn));
+    mx = rq_nan_max(mx, dpp_mov<0x4E>(mx));
+    mn = rq_nan_min(mn, dpp_mov<0x124>(mn));
+    mx = rq_nan_max(mx, dpp_mov<0x124>(mx));
+    mn = rq_nan_min(mn, dpp_mov<0x128>(mn));
+    mx = rq_nan_max(mx, dpp_mov<0x128>(mx));
     float z;
     rq_params_from_minmax(mn, mx, a.maxq, a.sym, &srow, &z);
     if (valid && t == 0) a.dyn_scale[row] = srow;
@@ -148,13 +174,23 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
 
   int16_t* crow = a.codes + (int64_t)row * a.C + i1;
   float* erow = a.err + (int64_t)row * count;
-  const int nmacro = (count + 3) / 4;
+  // row i of the block for this lane: h[k] = Hinv1[i][16 k + t]
+  auto hrow = [&](int i, float (&h)[NS]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < NS; k += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(&Hp[i][t][k]);
+      h[k] = v.x;
+      if (k + 1 < NS) h[k + 1] = v.y;
+      if (k + 2 < NS) h[k + 2] = v.z;
+      if (k + 3 < NS) h[k + 3] = v.w;
+    }
+  };
 
   if (a.atomic) {
     // Q1 = quant(W_block_start); res = W_block_start - Q1 - GHinv1   (:1243-1282)
 #pragma unroll
-    for (int k = 0; k < SLOTS; ++k) {
-      const int col = 4 * k + t;
+    for (int k = 0; k < NS; ++k) {
+      const int col = QL * k + t;
       const float s = (a.qmode == RQ_QMODE_STATIC) ? sc[k] : srow;
       const float code = rq_quant_code(w[k], s, lo, hi);
       const float q = s * code;
@@ -162,99 +198,76 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
       const float ge = geff(k);
       w[k] = (w[k] - q) - ge;
     }
-    // Err1 * Hinv1 = res, forward substitution (:1283-1288)
-    for (int m = 0; m < nmacro; ++m) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 4 * m + r;
+    // Err1 * Hinv1 = res, forward substitution (:1283-1288); column i = 16 m + r is owned by
+    // lane r, slot m
+    static_for<NS>([&](auto mc) __attribute__((always_inline)) {
+      static_for<QL>([&](auto rc) __attribute__((always_inline)) {
+        constexpr int m = decltype(mc)::value, r = decltype(rc)::value;
+        const int i = QL * m + r;
         if (i < count) {
-          const float d = Hl[i][i];
-          const float e_own = w[0] / d;
-          const float e = quad_lane(e_own, r);
+          float h[NS];
+          hrow(i, h);
+          const float e = row_bcast<r>(w[m] / h[m]);
           if (valid && t == r) erow[i] = e;
 #pragma unroll
-          for (int k = 0; k < SLOTS; ++k) {
-            {
-              const float h = Hl[i][hcol(m + k, t)];
-              w[k] = w[k] - e * h;
-            }
-          }
+          for (int k = 0; k < NS; ++k) w[k] = w[k] - e * h[k];
         }
-      }
-#pragma unroll
-      for (int k = 0; k + 1 < SLOTS; ++k) w[k] = w[k + 1];
-      w[SLOTS - 1] = 0.0f;
-    }
+      });
+    });
     return;
   }
 
-  // column-serial loop (:1296-1367)
-  for (int m = 0; m < nmacro; ++m) {
+  // column-serial loop (:1296-1367); column i = 16 m + r is quantised by lane r (slot m)
+  auto column = [&](auto mc, auto rc, bool with_gh) __attribute__((always_inline)) {
+    constexpr int m = decltype(mc)::value, r = decltype(rc)::value;
+    const int i = QL * m + r;
+    float h[NS];
+    hrow(i, h);
+    const float d = h[m];
+    const float s = (a.qmode == RQ_QMODE_STATIC) ? sc[m] : srow;
+    const float x = w[m];
+    const float code = rq_quant_code(x, s, lo, hi);
+    const float q = s * code;
+    const float e = row_bcast<r>(((x - q) - geff(m)) / d);
+    if (valid && t == r) {
+      crow[i] = (code != code) ? RQ_CODE_NAN : (int16_t)code;
+      erow[i] = e;
+    }
+    if constexpr (SURR) {
+      const float zi = with_gh ? row_bcast<r>(zz[m]) : 0.0f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 4 * m + r;
-      if (i < count) {
-        const float d = Hl[i][i];
-        const float s = (a.qmode == RQ_QMODE_STATIC) ? sc[0] : srow;
-        const float x = w[0];
-        const float code = rq_quant_code(x, s, lo, hi);
-        const float q = s * code;
-        const float e_own = ((x - q) - geff(0)) / d;
-        const float e = quad_lane(e_own, r);
-        if (valid && t == r) {
-          crow[i] = (code != code) ? RQ_CODE_NAN : (int16_t)code;
-          erow[i] = e;
-        }
-        if constexpr (SURR) {
-          const float zi = use_gh ? quad_lane(zz[0], r) : 0.0f;
+      for (int k = 0; k < NS; ++k) {
+        const float ge = geff(k);
+        const float upd = e * h[k];
+        w[k] = w[k] - (upd + ge);
+        gh[k] = gh[k] - zi * h[k];
+      }
+    } else if (with_gh) {
+      const float zi = row_bcast<r>(zz[m]);
 #pragma unroll
-          for (int k = 0; k < SLOTS; ++k) {
-            {
-              const float h = Hl[i][hcol(m + k, t)];
-              const float ge = geff(k);
-              const float upd = e * h;
-              w[k] = w[k] - (upd + ge);
-              gh[k] = gh[k] - zi * h;
-            }
-          }
-        } else if (use_gh) {
-          const float zi = quad_lane(zz[0], r);
+      for (int k = 0; k < NS; ++k) {
+        const float upd = e * h[k];
+        if constexpr (GM == 3) w[k] = w[k] - a.sos * (upd + gh[k]);
+        else w[k] = w[k] - (upd + gh[k]);
+        gh[k] = gh[k] - zi * h[k];
+      }
+    } else {
 #pragma unroll
-          for (int k = 0; k < SLOTS; ++k) {
-            {
-              const float h = Hl[i][hcol(m + k, t)];
-              const float upd = e * h;
-              if constexpr (GM == 3) w[k] = w[k] - a.sos * (upd + gh[k]);
-              else w[k] = w[k] - (upd + gh[k]);
-              gh[k] = gh[k] - zi * h;
-            }
-          }
-        } else {
-#pragma unroll
-          for (int k = 0; k < SLOTS; ++k) {
-            {
-              const float h = Hl[i][hcol(m + k, t)];
-              if constexpr (GM == 3) w[k] = w[k] - a.sos * (e * h + gh[k]);
-              else w[k] = w[k] - (e * h + gh[k]);
-            }
-          }
-        }
+      for (int k = 0; k < NS; ++k) {
+        if constexpr (GM == 3) w[k] = w[k] - a.sos * (e * h[k] + gh[k]);
+        else w[k] = w[k] - (e * h[k] + gh[k]);
       }
     }
-#pragma unroll
-    for (int k = 0; k + 1 < SLOTS; ++k) {
-      w[k] = w[k + 1];
-      gh[k] = gh[k + 1];
-      zz[k] = zz[k + 1];
-      sc[k] = sc[k + 1];
-      if constexpr (SURR) xr[k] = xr[k + 1];
-    }
-    w[SLOTS - 1] = 0.0f;
-    gh[SLOTS - 1] = 0.0f;
-    zz[SLOTS - 1] = 0.0f;
-    sc[SLOTS - 1] = 0.0f;
-    if constexpr (SURR) xr[SLOTS - 1] = 0.0f;
-  }
+  };
+  auto all_columns = [&](bool with_gh) __attribute__((always_inline)) {
+    static_for<NS>([&](auto mc) __attribute__((always_inline)) {
+      static_for<QL>([&](auto rc) __attribute__((always_inline)) {
+        if (QL * decltype(mc)::value + decltype(rc)::value < count) column(mc, rc, with_gh);
+      });
+    });
+  };
+  if (use_gh) all_columns(true);
+  else all_columns(false);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -400,24 +413,24 @@ extern "C" int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int
            dyn_scale, (float)maxq, sym, atomic, z_nonzero, codes, err, anchor, ld_anchor, beta,
            (float)second_order_scale};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  dim3 grid((R_s + 63) / 64, R / R_s), block(256);
-  const bool small = count <= 32;
+  dim3 grid((R_s + 256 / QL - 1) / (256 / QL), R / R_s), block(256);
+  const bool small = count <= 2 * QL;
   switch (gmode) {
     case 0:
-      if (small) hipLaunchKernelGGL((k_quant_block<8, 0>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((k_quant_block<32, 0>), grid, block, 0, s, a);
+      if (small) hipLaunchKernelGGL((k_quant_block<2, 0>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_quant_block<8, 0>), grid, block, 0, s, a);
       break;
     case 1:
-      if (small) hipLaunchKernelGGL((k_quant_block<8, 1>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((k_quant_block<32, 1>), grid, block, 0, s, a);
+      if (small) hipLaunchKernelGGL((k_quant_block<2, 1>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_quant_block<8, 1>), grid, block, 0, s, a);
       break;
     case 2:
-      if (small) hipLaunchKernelGGL((k_quant_block<8, 2>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((k_quant_block<32, 2>), grid, block, 0, s, a);
+      if (small) hipLaunchKernelGGL((k_quant_block<2, 2>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_quant_block<8, 2>), grid, block, 0, s, a);
       break;
     default:
-      if (small) hipLaunchKernelGGL((k_quant_block<8, 3>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((k_quant_block<32, 3>), grid, block, 0, s, a);
+      if (small) hipLaunchKernelGGL((k_quant_block<2, 3>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_quant_block<8, 3>), grid, block, 0, s, a);
   }
   RQ_CHECK_LAUNCH();
   return RQ_OK;

@@ -612,18 +612,23 @@ __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int6
     return;
   }
   // H[g][i][j] += acc * 2^-e_j   (32x32 block layout: i = 8*(e/4) + 4*(lane/32) + e%4, j = lane%32)
+  // The 16 loads of a block are issued together, then the 16 stores.
   const int j = Cw + fr;
   const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
 #pragma unroll
-  for (int bi = 0; bi < 8; ++bi)
+  for (int bi = 0; bi < 8; ++bi) {
+    float hv[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
-      if (i < C && j < C) {
-        float* ph = Hg + (int64_t)i * C + j;
-        *ph = *ph + acc[bi][e] * inv;
-      }
+      hv[e] = (i < C && j < C) ? Hg[(int64_t)i * C + j] : 0.0f;
     }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
+      if (i < C && j < C) Hg[(int64_t)i * C + j] = hv[e] + acc[bi][e] * inv;
+    }
+  }
 }
 
 // The last slice of a split item adds the S partials (in slice order) to H.
