@@ -371,6 +371,239 @@ __global__ __launch_bounds__(256) void k_safe_beta(const float* __restrict__ G, 
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// The two rank-K updates that follow each outer panel (K = NBW columns k .. k+K of L, rows
+// pe .. C), in one launch:
+//   SYRK part:  A[pe:, pe:] -= Lp Lp^T       (lower 128-tiles; Lp = L[pe:, k:k+K])
+//   row part:   Linv[pe:, 0:pe] -= Lp X      (X = Linv[k:k+K, 0:pe], row block of L^-1)
+// 128 x 128 output tiles, 4 waves of 64 x 64 (4 x 4 blocks of v_mfma_f64_16x16x4f64).  K
+// advances 8 at a time through a ring of PSTAGES LDS stages filled by direct global -> LDS
+// loads (16 bytes per lane) issued PSTAGES-1 steps ahead; one barrier per step.
+//  - Operands stored k-contiguous (Lp for both sides of the SYRK, Lp for the row part): a
+//    staging chunk is 16 rows x 8 k (1 KB); lane L fetches row L/4, k pair p = (L%4) ^
+//    ((row/4)%4) into LDS slot L, so the four lanes of a row read its 64 contiguous bytes and
+//    the 16 rows of one k pair sit in 16 different bank groups.
+//  - X (stored j-contiguous) is staged as 8 k-rows of 128 j (1 KB each, 64 B apart).
+//  - MFMA k order: in sub-step s of a stage the lanes of group g (= lane / 16) supply
+//    k = 2g + s on both operands, so a k-contiguous operand is one 16-byte LDS read per
+//    16 x 8 block for both sub-steps.
+// Edge rows / columns read clamped (in-bounds) addresses; their results are not stored.
+constexpr int PT = 128;
+constexpr int PKS = 8;                      // k per stage
+constexpr int PSTAGES = 4;
+constexpr int PCHUNK = 1024;
+constexpr int PXROW = PCHUNK + 64;          // X k-row stride in a stage
+constexpr int PA_BYTES = 8 * PCHUNK;
+constexpr int PSTAGE = PA_BYTES + 8 * PXROW;
+
+struct PanelArgs {
+  const double* Lp;    // Lp[i * ld + kk]: row i of the panel (i < rest), column kk < K
+  const double* X;     // X[kk * ld + j], j < pe
+  double* Atr;         // trailing matrix origin (row pe, column pe)
+  double* Brow;        // Linv row pe, column 0
+  int64_t ld;
+  int rest, pe, K;
+  int ntr;             // row tiles: ceil(rest / PT)
+  int nsy;             // SYRK tiles: ntr (ntr + 1) / 2
+  int nxc;             // row-part column tiles: ceil(pe / PT)
+  int per_batch;       // nsy + ntr * nxc
+  int64_t ws;          // batch stride (doubles)
+  const int* info;
+  int total;           // per_batch * nb
+};
+
+__device__ __forceinline__ void lds_dma16(const void* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+}
+
+// s_waitcnt with only the vector-memory counter limited (gfx9 encoding).
+#define PWAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+// The ring: PSTAGES separate __shared__ arrays.  The k loop is unrolled by PSTAGES so every
+// stage index is a compile-time constant: the compiler can then tell the global -> LDS loads in
+// flight to other stages from the stage being read, and does not wait for them.
+struct PStages {
+  uint8_t* s[PSTAGES];
+};
+
+template <bool SYRK>
+struct PanelTile {
+  const PanelArgs& p;
+  const double* srcA[2];
+  const double* srcB[2];
+  int wave, lane, wr, wc, g, r, slot, nk;
+  bool live;
+  doublex4 acc[4][4];
+
+  __device__ __forceinline__ PanelTile(const PanelArgs& pp, int64_t boff, int i0, int j0, int ti, int tj)
+      : p(pp) {
+    const int tid = threadIdx.x;
+    lane = tid & 63;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    wr = wave >> 1;
+    wc = wave & 1;
+    g = lane >> 4;
+    r = lane & 15;
+    slot = 4 * r + (g ^ ((r >> 2) & 3));
+    nk = p.K / PKS;
+    live = !(SYRK && ti == tj && wr < wc);   // a 64-block strictly above the diagonal
+    const int M = p.rest, N = SYRK ? p.rest : p.pe;
+    const double* Lp = p.Lp + boff;
+    // this wave's staging sources: chunks 2 wave and 2 wave + 1 of each operand
+    const int cr = lane >> 2, kp = (lane & 3) ^ ((cr >> 2) & 3);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 2 * wave + h;
+      srcA[h] = Lp + (int64_t)min(i0 + 16 * c + cr, M - 1) * p.ld + 2 * kp;
+      if (SYRK) srcB[h] = Lp + (int64_t)min(j0 + 16 * c + cr, N - 1) * p.ld + 2 * kp;
+      else srcB[h] = p.X + boff + (int64_t)c * p.ld + min(j0 + 2 * lane, N - 2);
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[a][b][e] = 0.0;
+  }
+
+  // 4 staging loads per wave: A chunks 2 wave, 2 wave + 1 and the same chunks of B
+  __device__ __forceinline__ void stage(uint8_t* st, int kt) {
+    const int64_t ka = (int64_t)kt * PKS;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 2 * wave + h;
+      lds_dma16(srcA[h] + ka, st + c * PCHUNK);
+      if (SYRK) lds_dma16(srcB[h] + ka, st + PA_BYTES + c * PCHUNK);
+      else lds_dma16(srcB[h] + ka * p.ld, st + PA_BYTES + c * PXROW);
+    }
+  }
+
+  // Step kt: wait for this wave's staging of kt (the PSTAGES-2 later steps may still be in
+  // flight), meet the other waves (their parts of kt are then in LDS, and every read of the
+  // FILL stage, done in step kt-1, is over), refill FILL with step kt+PSTAGES-1, multiply kt.
+  template <int CUR, int FILL>
+  __device__ __forceinline__ void step(const PStages& L, int kt) {
+    PWAIT_VM(4 * (PSTAGES - 2));
+    __builtin_amdgcn_s_barrier();
+    stage(L.s[FILL], min(kt + PSTAGES - 1, nk - 1));
+    if (!live) return;
+    const uint8_t* st = L.s[CUR];
+    double2 av[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+      av[rb] = *reinterpret_cast<const double2*>(st + (4 * wr + rb) * PCHUNK + 16 * slot);
+    double bv[2][4];
+    if (SYRK) {
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const double2 v = *reinterpret_cast<const double2*>(st + PA_BYTES + (4 * wc + cb) * PCHUNK + 16 * slot);
+        bv[0][cb] = v.x;
+        bv[1][cb] = v.y;
+      }
+    } else {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+          bv[s2][cb] = *reinterpret_cast<const double*>(st + PA_BYTES + (2 * g + s2) * PXROW +
+                                                        8 * (64 * wc + 16 * cb + r));
+    }
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+        acc[rb][cb] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[rb].x, bv[0][cb], acc[rb][cb], 0, 0, 0);
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+        acc[rb][cb] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[rb].y, bv[1][cb], acc[rb][cb], 0, 0, 0);
+  }
+};
+
+template <bool SYRK>
+__device__ __forceinline__ void panel_tile(const PanelArgs& p, int64_t boff, int ti, int tj, const PStages& L) {
+  const int i0 = ti * PT, j0 = tj * PT;
+  PanelTile<SYRK> t(p, boff, i0, j0, ti, tj);
+  const int nk = t.nk;
+  static_assert(PSTAGES == 4, "unrolled stage schedule");
+#pragma unroll
+  for (int s = 0; s < PSTAGES - 1; ++s) t.stage(L.s[s], min(s, nk - 1));
+  int kt = 0;
+  for (; kt + 4 <= nk; kt += 4) {
+    t.template step<0, 3>(L, kt);
+    t.template step<1, 0>(L, kt + 1);
+    t.template step<2, 1>(L, kt + 2);
+    t.template step<3, 2>(L, kt + 3);
+  }
+  const int rem = nk - kt;
+  if (rem > 0) t.template step<0, 3>(L, kt);
+  if (rem > 1) t.template step<1, 0>(L, kt + 1);
+  if (rem > 2) t.template step<2, 1>(L, kt + 2);
+  PWAIT_VM(0);   // no staging in flight when the workgroup moves on
+  if (!t.live) return;
+  const int M = p.rest, N = SYRK ? p.rest : p.pe;
+  double* Cm = (SYRK ? p.Atr : p.Brow) + boff;
+  // 16x16 f64 block layout: column lane % 16, row lane / 16 + 4 e.  Per 16-row block the 16
+  // loads are issued together (clamped in-bounds addresses), then the 16 stores.
+  const int ib = i0 + 64 * t.wr + t.g, jb = j0 + 64 * t.wc + t.r;
+  const bool full = (i0 + PT <= M) && (j0 + PT <= N);
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    double cv[4][4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = min(ib + 16 * rb + 4 * e, M - 1), j = min(jb + 16 * cb, N - 1);
+        cv[cb][e] = Cm[(int64_t)i * p.ld + j];
+      }
+    if (full) {   // interior tile: no per-element branches, so the stores wait once
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          Cm[(int64_t)(ib + 16 * rb + 4 * e) * p.ld + jb + 16 * cb] = cv[cb][e] - t.acc[rb][cb][e];
+    } else {
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = ib + 16 * rb + 4 * e, j = jb + 16 * cb;
+          if (i < M && j < N) Cm[(int64_t)i * p.ld + j] = cv[cb][e] - t.acc[rb][cb][e];
+        }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void k_panel_update(PanelArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds0[PSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds1[PSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds2[PSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds3[PSTAGE];
+  const PStages L{{lds0, lds1, lds2, lds3}};
+  // XCD-aware order: workgroup b runs on XCD b % 8; each XCD takes a contiguous range of
+  // tiles, so tiles that share panel rows meet in one L2.
+  const int b = blockIdx.x;
+  const int per = p.total / 8, rem8 = p.total % 8;
+  const int xcd = b % 8, idx = b / 8;
+  const int t = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
+  if (t >= p.total) return;
+  const int bz = t / p.per_batch, u = t % p.per_batch;
+  if (p.info[bz]) return;
+  const int64_t boff = (int64_t)bz * p.ws;
+  if (u < p.nsy) {
+    // lower-triangle tile u, row-major: ti (ti + 1) / 2 <= u < (ti + 1) (ti + 2) / 2
+    int ti = (int)((__builtin_sqrtf(8.0f * (float)u + 1.0f) - 1.0f) * 0.5f);
+    while ((ti + 1) * (ti + 2) / 2 <= u) ++ti;
+    while (ti * (ti + 1) / 2 > u) --ti;
+    panel_tile<true>(p, boff, ti, u - ti * (ti + 1) / 2, L);
+  } else {
+    const int v = u - p.nsy;
+    panel_tile<false>(p, boff, v / p.nxc, v % p.nxc, L);
+  }
+}
+
 }  // namespace
 
 extern "C" int64_t rq_chol_workspace_bytes(int C) {
@@ -460,9 +693,30 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
       }
     }
     const int rest = C - pe;
-    if (rest > 0) {
+    if (rest > 0 && (C & 1) == 0 && kw % PKS == 0) {
       // one launch: the trailing matrix A[pe:, pe:] -= L[pe:, k:pe] L[pe:, k:pe]^T (lower tiles,
       // K = kw) and the rows of L^-1 below the panel: B[pe:, 0:pe] -= L[pe:, k:pe] X[k:pe, 0:pe]
+      // (rows 16-byte aligned: C even; pe is a multiple of NBW, so X's column pairs stay inside)
+      PanelArgs pa;
+      pa.Lp = A + (int64_t)pe * C + k;
+      pa.X = Linv + (int64_t)k * C;
+      pa.Atr = A + (int64_t)pe * C + pe;
+      pa.Brow = Linv + (int64_t)pe * C;
+      pa.ld = C;
+      pa.rest = rest;
+      pa.pe = pe;
+      pa.K = kw;
+      pa.ntr = (rest + PT - 1) / PT;
+      pa.nsy = pa.ntr * (pa.ntr + 1) / 2;
+      pa.nxc = (pe + PT - 1) / PT;
+      pa.per_batch = pa.nsy + pa.ntr * pa.nxc;
+      pa.ws = ws;
+      pa.info = info;
+      pa.total = pa.per_batch * nb;
+      hipLaunchKernelGGL(k_panel_update, dim3(pa.total), dim3(256), 0, s, pa);
+      RQ_CHECK_LAUNCH();
+    } else if (rest > 0) {
+      // the same two updates on the 64-tile GEMM (odd C)
       GemmArgs<double> h = batched(gemm_args<double>(A + (int64_t)pe * C + k, C, A + (int64_t)pe * C + k,
                                                      C, A + (int64_t)pe * C + pe, C, rest, rest, kw,
                                                      -1.0, EPI_ACCUM));

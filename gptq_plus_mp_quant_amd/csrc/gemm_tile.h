@@ -207,6 +207,35 @@ __device__ __forceinline__ void gemm_tile_body(GemmArgs<T> p, int ti, int tj, in
   }
 
   // 16x16 block layout: col = lane % 16, row = Mfma16<T>::row(lane, e).
+  if (!p.nz_flag && i0 + GT <= p.M && j0 + GT <= p.N) {
+    // interior tile: the accumulate loads all in flight together, then the stores, with no
+    // per-element branches (so the compiler does not wait for each store)
+    T cv[2][2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = i0 + wr * 32 + a * 16 + Mfma16<T>::row(lane, e);
+          const int j = j0 + wc * 32 + b * 16 + (lane & 15);
+          cv[a][b][e] = (p.epi == EPI_ACCUM) ? p.Cm[(int64_t)i * p.ldc + j] : T(0);
+        }
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = i0 + wr * 32 + a * 16 + Mfma16<T>::row(lane, e);
+          const int j = j0 + wc * 32 + b * 16 + (lane & 15);
+          T v = p.alpha * acc[a][b][e];
+          if (p.row_scale) v = v * p.row_scale[p.row_bcast ? 0 : i];
+          if (p.epi == EPI_ACCUM) v = cv[a][b][e] + v;
+          p.Cm[(int64_t)i * p.ldc + j] = v;
+        }
+    return;
+  }
   int nz = 0;
 #pragma unroll
   for (int a = 0; a < 2; ++a)

@@ -503,49 +503,51 @@ __device__ __forceinline__ void split_staged(const uint8_t* st, int wave, int la
              *reinterpret_cast<const float4*>(sp + 16), sc, p);
 }
 
-// One 16-token step k of a wave.  KP = (k - kbeg) % 2 selects the piece buffer; CUR, NXT, FILL
-// are the stages of steps k, k+1 and k+XDEPTH-1.  Every wave's staging of steps k and k+1 was
-// issued XDEPTH-1 and XDEPTH-2 steps ago and is followed by at least the 2 staging loads of each
-// of the XDEPTH-3 steps since, so vmcnt(2 * (XDEPTH - 3)) covers this wave's part of both
+// One 16-token step k of a wave.  KP = (k - kbeg) % 2 selects the register buffers (row
+// fragments a and pieces p of step k, both read or made during step k-1); CUR, NXT, FILL are
+// the stages of steps k, k+1 and k+XDEPTH-1.  Every wave's staging of steps k and k+1 was
+// issued XDEPTH-1 and XDEPTH-2 steps ago and is followed by at least the 2 staging loads of
+// each of the XDEPTH-3 steps since, so vmcnt(2 * (XDEPTH - 3)) covers this wave's part of both
 // whatever the issue order within a step, and after the barrier the other waves' parts are in
-// LDS too (the barrier also orders every read of the FILL stage, done in earlier steps, before
-// its refill).  Then: stage step k+XDEPTH-1; read the row fragments of step k; split this
-// wave's column fragment of step k+1 under the 24 MFMAs of step k.  Two waves share a SIMD, so
-// one wave's reads, waits and split run while the other issues MFMAs.  A bare s_barrier: the
-// fence of __syncthreads would wait for every staging load in flight.
+// LDS too.  The barrier also orders every read of the FILL stage (the stage of step k-1, read
+// during step k-2) before its refill.  Then: stage step k+XDEPTH-1; issue the 24 MFMAs of
+// step k from registers, while the row fragments of step k+1 are read and this wave's column
+// fragment of step k+1 is split in between.  The MFMAs need no LDS read after the barrier, so
+// the two waves of a SIMD resume issuing as soon as it opens.  A bare s_barrier: the fence of
+// __syncthreads would wait for every staging load in flight.
 template <typename TX, int KP, int CUR, int NXT, int FILL>
-__device__ __forceinline__ void split_step(uint4 (&p)[2][XNP], floatx16 (&acc)[8], const XStages& L,
-                                           const uint16_t* pa, const uint16_t* pb, const float* sg, float sc,
-                                           int wave, int lane, int64_t k, int64_t last) {
+__device__ __forceinline__ void split_step(uint4 (&p)[2][XNP], uint4 (&a)[2][8], floatx16 (&acc)[8],
+                                           const XStages& L, const uint16_t* pa, const uint16_t* pb,
+                                           const float* sg, float sc, int wave, int lane, int64_t k,
+                                           int64_t last) {
   typedef XType<TX> T;
   typedef typename T::v8 v8;
   constexpr int NP = 1 - KP;
   XWAIT_VM(2 * (XDEPTH - 3));
   __builtin_amdgcn_s_barrier();
   stage_step(L.s[FILL], pa, pb, sg, wave, lane, min(k + XDEPTH - 1, last));
-  const uint8_t* cur = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[CUR] + lane * 16, 16));
-  uint4 a[8];
-#pragma unroll
-  for (int bi = 0; bi < 8; ++bi) a[bi] = *reinterpret_cast<const uint4*>(cur + bi * 1024);
+  const uint8_t* nxt = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[NXT] + lane * 16, 16));
   const uint8_t* w = static_cast<const uint8_t*>(
       __builtin_assume_aligned(L.s[NXT] + XB_OFF + wave * 1024 + lane * 16, 16));
   const uint8_t* sp = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[NXT] + XS_OFF + 32 * (lane >> 5), 16));
   const uint4 b = *reinterpret_cast<const uint4*>(w);
   const float4 s0 = *reinterpret_cast<const float4*>(sp);
   const float4 s1 = *reinterpret_cast<const float4*>(sp + 16);
+#pragma unroll
+  for (int bi = 0; bi < 8; ++bi) a[NP][bi] = *reinterpret_cast<const uint4*>(nxt + bi * 1024);
   const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
   const uint32_t xw[4] = {b.x, b.y, b.z, b.w};
   uint32_t o[XNP][4];
 #pragma unroll
   for (int bi = 0; bi < 8; ++bi)
-    acc[bi] = T::mfma(__builtin_bit_cast(v8, a[bi]), __builtin_bit_cast(v8, p[KP][XNP - 1]), acc[bi]);
+    acc[bi] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][XNP - 1]), acc[bi]);
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     split_pair<TX>(xw[m], sv[2 * m], sv[2 * m + 1], sc, o[0][m], o[1][m], o[2][m]);
 #pragma unroll
     for (int i = 4 * m; i < 4 * m + 4; ++i) {
       const int q = 1 - i / 8, bi = i % 8;
-      acc[bi] = T::mfma(__builtin_bit_cast(v8, a[bi]), __builtin_bit_cast(v8, p[KP][q]), acc[bi]);
+      acc[bi] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][q]), acc[bi]);
     }
   }
 #pragma unroll
@@ -583,24 +585,29 @@ __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int6
   const int64_t last = kend - 1;
 #pragma unroll
   for (int h = 0; h < XDEPTH - 1; ++h) stage_step(L.s[h], pa, pb, sg, wave, lane, min(kbeg + h, last));
-  uint4 p[2][XNP];
+  uint4 p[2][XNP], a[2][8];
   XWAIT_VM(2 * (XDEPTH - 2));         // this wave's staging of step kbeg
   __builtin_amdgcn_s_barrier();       // and the other waves'
   split_staged<TX>(L.s[0], wave, lane, sc, p[0]);
+  {
+    const uint8_t* cur = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[0] + lane * 16, 16));
+#pragma unroll
+    for (int bi = 0; bi < 8; ++bi) a[0][bi] = *reinterpret_cast<const uint4*>(cur + bi * 1024);
+  }
 
   const int64_t n = kend - kbeg;
   int64_t k = kbeg;
   static_assert(XDEPTH == 4, "unrolled stage schedule");
   for (; k + 4 <= kend; k += 4) {
-    split_step<TX, 0, 0, 1, 3>(p, acc, L, pa, pb, sg, sc, wave, lane, k, last);
-    split_step<TX, 1, 1, 2, 0>(p, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last);
-    split_step<TX, 0, 2, 3, 1>(p, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last);
-    split_step<TX, 1, 3, 0, 2>(p, acc, L, pa, pb, sg, sc, wave, lane, k + 3, last);
+    split_step<TX, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last);
+    split_step<TX, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last);
+    split_step<TX, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last);
+    split_step<TX, 1, 3, 0, 2>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 3, last);
   }
   const int rem = (int)(n & 3);
-  if (rem > 0) split_step<TX, 0, 0, 1, 3>(p, acc, L, pa, pb, sg, sc, wave, lane, k, last);
-  if (rem > 1) split_step<TX, 1, 1, 2, 0>(p, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last);
-  if (rem > 2) split_step<TX, 0, 2, 3, 1>(p, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last);
+  if (rem > 0) split_step<TX, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last);
+  if (rem > 1) split_step<TX, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last);
+  if (rem > 2) split_step<TX, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last);
   XWAIT_VM(0);                        // no staging left in flight when the workgroup moves on
 
   if (part) {
