@@ -391,6 +391,196 @@ __global__ __launch_bounds__(256) void k_trailing(TrArgs a) {
       }
 }
 
+// ---------------------------------------------------------------------------------------
+// k_trailing_w: the frozen-mode outer update when Z is identically zero (then GH is zero too):
+//   W[r, i2:] -= f * sum_k err[r, k] Hinv_s[i1 + k, i2:]       (f = 1, or second_order_scale)
+// The sum is formed like the reference's CPU matmul, a sequential fused multiply-add chain
+// c = fma(err[r, k], Hinv[k, c], c) for k = 0, 1, ..., count-1 starting from 0, so W is
+// bit-identical to `W - Err1 @ Hinv[i1:i2, i2:]` on CPU: every step is one
+// v_mfma_f32_32x32x1_2b_f32 (a 32x32 outer product per block, k = 1), which rounds exactly like
+// one fmaf per output, issued in k order.
+// 128 x 128 output tiles inside one subgroup, 4 waves of 64 x 64; per k a wave issues two of
+// them (column halves 0-31 and 32-63; in each, block b takes rows 32b .. 32b+31 of the wave, so
+// lane l supplies err of wave row l and Hinv of column l % 32 of the half).  K advances 8 at a
+// time through a ring of TSTAGES LDS stages (separate __shared__ arrays, the loop unrolled by
+// TSTAGES so stage indices are compile-time constants), filled by direct global -> LDS loads
+// (16 bytes per lane) issued TSTAGES-1 steps ahead; one barrier per step.  Per stage and wave:
+// one 1 KB chunk of err (32 rows x 8 k; lane L fetches row L/2, k quad (L%2) ^ ((row/8)%2), so
+// a lane's two 16-byte reads of its row are conflict-free) and one of Hinv (2 k-rows x 128
+// columns, chunks 64 bytes apart; both halves of the wave read the same word: a broadcast).
+constexpr int TT = 128;
+constexpr int TSTAGES = 4;
+constexpr int TCH = 1024;
+constexpr int THROW = TCH + 64;          // Hinv chunk stride in a stage
+constexpr int TA_BYTES = 4 * TCH;
+constexpr int TSTAGE = TA_BYTES + 4 * THROW;
+
+typedef float floatx32 __attribute__((ext_vector_type(32)));
+
+struct TwArgs {
+  float* Wp;
+  int64_t ldw;
+  const float* Hinv;
+  int C, R_s, i1, count;
+  const float* err;
+  float f;               // 1, or second_order_scale (RQ_GMODE_BLOCK_GD)
+  int nrt, nct;          // row tiles per subgroup, column tiles
+  int total;             // nrt * nct * subgroups
+};
+
+struct TStages {
+  uint8_t* s[TSTAGES];
+};
+
+__device__ __forceinline__ void lds_dma16(const void* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+}
+
+// s_waitcnt with only the vector-memory counter limited (gfx9 encoding).
+#define TWAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+struct TwTile {
+  const float* srcA;
+  const float* srcB;
+  int wave, wc, aoff0, aoff1, boff, nk;
+  int64_t ldh;
+  floatx32 acc[2];
+
+  __device__ __forceinline__ void stage(uint8_t* st, int kt) {
+    lds_dma16(srcA + kt * 8, st + wave * TCH);
+    lds_dma16(srcB + (int64_t)kt * 8 * ldh, st + TA_BYTES + wave * THROW);
+  }
+  // Step kt: wait for this wave's 2 staging loads of kt (the TSTAGES-2 later steps may be in
+  // flight), meet the other waves (their parts are in LDS, and every read of the FILL stage,
+  // done in step kt-1, is over), refill FILL with step kt+TSTAGES-1, then k = 8 kt .. 8 kt + 7.
+  template <int CUR, int FILL>
+  __device__ __forceinline__ void step(const TStages& L, int kt) {
+    TWAIT_VM(2 * (TSTAGES - 2));
+    __builtin_amdgcn_s_barrier();
+    stage(L.s[FILL], min(kt + TSTAGES - 1, nk - 1));
+    const uint8_t* st = L.s[CUR];
+    const float4 a0 = *reinterpret_cast<const float4*>(st + aoff0);   // k 0..3 of this lane's row
+    const float4 a1 = *reinterpret_cast<const float4*>(st + aoff1);   // k 4..7
+    const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    float bv[8][2];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        bv[k][h] = *reinterpret_cast<const float*>(st + TA_BYTES + (k >> 1) * THROW + (k & 1) * 512 +
+                                                    boff + 128 * h);
+    // all reads of the step issued before its MFMAs (otherwise the scheduler reuses one
+    // register pair for every Hinv read and each MFMA pair waits for an LDS round trip)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) acc[h] = __builtin_amdgcn_mfma_f32_32x32x1f32(av[k], bv[k][h], acc[h], 0, 0, 0);
+  }
+};
+
+__global__ __launch_bounds__(256) void k_trailing_w(TwArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds0[TSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds1[TSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds2[TSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds3[TSTAGE];
+  const TStages L{{lds0, lds1, lds2, lds3}};
+  // XCD-aware order: each XCD takes a contiguous range of tiles (row tile fastest), so the
+  // tiles of one Hinv column strip meet in one L2.
+  const int b = blockIdx.x;
+  const int per = a.total / 8, rem8 = a.total % 8;
+  const int xcd = b % 8, idx = b / 8;
+  const int t = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
+  if (t >= a.total) return;
+  const int per_sub = a.nrt * a.nct;
+  const int sub = t / per_sub, u = t % per_sub;
+  const int ct = u / a.nrt, rt = u % a.nrt;
+  const int i2 = a.i1 + a.count;
+  const int rl0 = rt * TT, c0 = i2 + ct * TT;
+  const int64_t rbase = (int64_t)sub * a.R_s;
+
+  TwTile w;
+  const int tid = threadIdx.x, lane = tid & 63;
+  w.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = w.wave >> 1;
+  w.wc = w.wave & 1;
+  w.nk = a.count / 8;
+  w.ldh = a.C;
+  {
+    // staging sources: err chunk `wave` (rows 32 wave .. +31 of the tile), Hinv k-rows
+    // 2 wave, 2 wave + 1 (columns clamped to a whole in-bounds quad)
+    const int rho = lane >> 1, q = (lane & 1) ^ ((rho >> 3) & 1);
+    const int rl = min(rl0 + 32 * w.wave + rho, a.R_s - 1);
+    w.srcA = a.err + (rbase + rl) * a.count + 4 * q;
+    const int kr = 2 * w.wave + (lane >> 5);
+    const int c = min(c0 + 4 * (lane & 31), a.C - 4);
+    w.srcB = a.Hinv + (int64_t)sub * a.C * a.C + (int64_t)(a.i1 + kr) * a.C + c;
+  }
+  // err of this lane: wave row `lane` = tile row 64 wr + lane, in chunk 2 wr + lane / 32 at
+  // in-chunk row rho = lane % 32; k quad q sits at slot 2 rho + (q ^ ((rho / 8) % 2))
+  {
+    const int rho = lane & 31, sw = (rho >> 3) & 1;
+    const int base = (2 * wr + (lane >> 5)) * TCH + 32 * rho;
+    w.aoff0 = base + 16 * (0 ^ sw);
+    w.aoff1 = base + 16 * (1 ^ sw);
+  }
+  // Hinv of this lane: column 64 wc + 32 h + lane % 32 of the tile
+  w.boff = 4 * (64 * w.wc + (lane & 31));
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 32; ++e) w.acc[h][e] = 0.0f;
+
+  static_assert(TSTAGES == 4, "unrolled stage schedule");
+#pragma unroll
+  for (int s = 0; s < TSTAGES - 1; ++s) w.stage(L.s[s], min(s, w.nk - 1));
+  int kt = 0;
+  for (; kt + 4 <= w.nk; kt += 4) {
+    w.step<0, 3>(L, kt);
+    w.step<1, 0>(L, kt + 1);
+    w.step<2, 1>(L, kt + 2);
+    w.step<3, 2>(L, kt + 3);
+  }
+  const int rem = w.nk - kt;
+  if (rem > 0) w.step<0, 3>(L, kt);
+  if (rem > 1) w.step<1, 0>(L, kt + 1);
+  if (rem > 2) w.step<2, 1>(L, kt + 2);
+  TWAIT_VM(0);   // no staging in flight when the workgroup ends
+
+  // Output e of half h: wave row 32 (e / 16) + 8 ((e % 16) / 4) + 4 (lane / 32) + e % 4, wave
+  // column 32 h + lane % 32.  Per group of 8 outputs the loads are issued together (clamped
+  // in-bounds addresses), then the stores.  W - tot, or W - f * tot (block_gd).
+  const int rw0 = rl0 + 64 * wr + 4 * (lane >> 5), cw0 = c0 + 64 * w.wc + (lane & 31);
+  const bool full = (rl0 + TT <= a.R_s) && (c0 + TT <= a.C);
+  const bool scaled = a.f != 1.0f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e0 = 0; e0 < 32; e0 += 8) {
+      float wv[8];
+#pragma unroll
+      for (int e = e0; e < e0 + 8; ++e) {
+        const int rl = min(rw0 + 32 * (e / 16) + 8 * ((e % 16) / 4) + (e % 4), a.R_s - 1);
+        wv[e - e0] = a.Wp[(rbase + rl) * a.ldw + min(cw0 + 32 * h, a.C - 1)];
+      }
+      if (full) {   // interior tile: no per-element branches, so the stores wait once
+#pragma unroll
+        for (int e = e0; e < e0 + 8; ++e) {
+          const int rl = rw0 + 32 * (e / 16) + 8 * ((e % 16) / 4) + (e % 4), c = cw0 + 32 * h;
+          const float tot = w.acc[h][e];
+          a.Wp[(rbase + rl) * a.ldw + c] = wv[e - e0] - (scaled ? a.f * tot : tot);
+        }
+      } else {
+#pragma unroll
+        for (int e = e0; e < e0 + 8; ++e) {
+          const int rl = rw0 + 32 * (e / 16) + 8 * ((e % 16) / 4) + (e % 4), c = cw0 + 32 * h;
+          const float tot = w.acc[h][e];
+          if (rl < a.R_s && c < a.C) a.Wp[(rbase + rl) * a.ldw + c] = wv[e - e0] - (scaled ? a.f * tot : tot);
+        }
+      }
+    }
+}
+
 }  // namespace
 
 extern "C" int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int C, const float* GH,
@@ -438,7 +628,7 @@ extern "C" int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int
 
 extern "C" int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float* Z, int64_t ldgh,
                                   const float* Hinv_all, int C, int R, int R_s, int i1, int count,
-                                  const float* err, const int* z_nonzero, int gmode,
+                                  const float* err, const int* z_nonzero, int z_zero, int gmode,
                                   const float* anchor, int64_t ld_anchor, const float* beta,
                                   double second_order_scale, void* stream) {
   if (!Wp || !GH || !Z || !Hinv_all || !err || !z_nonzero) return RQ_EINVAL;
@@ -448,9 +638,21 @@ extern "C" int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float
   if (count <= 0 || i1 < 0 || i1 + count > C) return RQ_EINVAL;
   const int i2 = i1 + count;
   if (i2 >= C) return RQ_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (z_zero && (gmode == RQ_GMODE_FROZEN || gmode == RQ_GMODE_BLOCK_GD) && count % 8 == 0 &&
+      C % 4 == 0 && i2 % 4 == 0 && al16(Hinv_all) && al16(err)) {
+    // Z (and with it GH) identically zero: only W -= f * err Hinv[i1:i2, i2:] remains
+    TwArgs w{Wp, ldw, Hinv_all, C, R_s, i1, count, err,
+             gmode == RQ_GMODE_BLOCK_GD ? (float)second_order_scale : 1.0f,
+             (R_s + TT - 1) / TT, (C - i2 + TT - 1) / TT, 0};
+    w.total = w.nrt * w.nct * (R / R_s);
+    hipLaunchKernelGGL(k_trailing_w, dim3(w.total), dim3(256), 0, s, w);
+    RQ_CHECK_LAUNCH();
+    return RQ_OK;
+  }
   TrArgs a{Wp, ldw, GH, Z, ldgh, Hinv_all, C, R, R_s, i1, count, err, z_nonzero, gmode,
            anchor, ld_anchor, beta, (float)second_order_scale};
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   dim3 grid((C - i2 + 63) / 64, (R_s + 63) / 64, R / R_s), block(256);
   hipLaunchKernelGGL(k_trailing, grid, block, 0, s, a);
   RQ_CHECK_LAUNCH();

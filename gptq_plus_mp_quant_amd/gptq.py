@@ -140,7 +140,7 @@ class GPTQ:
             K.quant_block(Wp, Hinv_all, Wp, Wp, R, i1, i2 - i1, qmode, scale_tab, col_group, None, maxq,
                           sym, False, z_off, codes, err)
             if i2 < C:
-                K.trailing_update(Wp, Wp, Wp, Hinv_all, R, i1, i2 - i1, err, z_off)
+                K.trailing_update(Wp, Wp, Wp, Hinv_all, R, i1, i2 - i1, err, z_off, z_zero=True)
 
         Q = torch.empty((R, C), dtype=W.dtype, device=dev)
         nan_flag = torch.zeros(1, dtype=torch.int32, device=dev)

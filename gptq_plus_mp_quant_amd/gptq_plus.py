@@ -359,6 +359,7 @@ class GPTQPlus:
                         beta_rows[sub * R_s:(sub + 1) * R_s].copy_(info["beta"])
             self.GHinv_initial = GH.clone() if keep_hinv else None
             z_any = torch.amax(z_flags).reshape(1).contiguous()
+            z_zero = not bool(z_any.item())      # one read-back: Z identically zero
 
             codes = torch.empty((R, C), dtype=torch.int16, device=dev)
             err = torch.empty((R, min(blocksize, C)), **f32)
@@ -413,13 +414,14 @@ class GPTQPlus:
                                 if beta_mode == 1 and self.reference_loss > 0:
                                     beta_rows[r0:r0 + R_s].copy_(beta)
                             z_any = torch.amax(z_flags).reshape(1).contiguous()
+                            z_zero = not bool(z_any.item())
                             K.current_weight(Wp, codes, i2, qmode, scale_tab, col_group, dyn_scale,
                                              blocksize, out=anchor)
                         if block_observer is not None:
                             block_observer(self._observer_record(i1, i2, blocksize, meta, block_gd=False))
                     if i2 < C:
                         K.trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_any, gm_out,
-                                          anchor, beta_rows, sos)
+                                          anchor, beta_rows, sos, z_zero=z_zero)
                     if block_gd and enable_gradient_update and i2 < C:
                         # block_gd (:1572-1834): one optimizer step on the trailing columns
                         if gradient_refresh_fn is None:

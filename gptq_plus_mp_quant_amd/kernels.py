@@ -245,7 +245,9 @@ def quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale, col_group, dy
 
 
 def trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_nonzero, gmode=nat.RQ_GMODE_FROZEN,
-                    anchor=None, beta=None, second_order_scale=1.0):
+                    anchor=None, beta=None, second_order_scale=1.0, z_zero=False):
+    """z_zero=True states that Z (and GH) are identically zero, i.e. that z_nonzero holds 0; the
+    frozen and block_gd modes then run the W-only kernel."""
     R, C = Wp.shape
     lda = _surrogate(gmode, anchor, beta, R, C)
     _cout(Wp, "Wp"), _cout(GH, "GH"), _cout(err, "err")
@@ -253,7 +255,8 @@ def trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_nonzero, gmode=n
         raise ValueError("trailing_update: Hinv_all must be contiguous, Z row-major")
     nat.call("rq_trailing_update", nat.ptr(Wp), Wp.stride(0), nat.ptr(GH), nat.ptr(Z), GH.stride(0),
              nat.ptr(Hinv_all), C, R, R_s, int(i1), int(count), nat.ptr(err), nat.ptr(z_nonzero),
-             int(gmode), nat.ptr(anchor), lda, nat.ptr(beta), float(second_order_scale), _stream(Wp))
+             int(bool(z_zero)), int(gmode), nat.ptr(anchor), lda, nat.ptr(beta), float(second_order_scale),
+             _stream(Wp))
 
 
 def writeback(codes, invperm, qmode, scale, col_group, dyn_scale, blocksize, q_out, w_int_out=None,

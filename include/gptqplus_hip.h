@@ -168,10 +168,13 @@ int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int C, const f
  * terms are skipped when *z_nonzero == 0.  fp32 MFMA.  For the surrogate gmodes the GH of
  * the first term is GH + beta[r] (Wp - anchor) (outer refresh "surrogate_block",
  * :1500-1511); the GH update is unchanged.  RQ_GMODE_BLOCK_GD scales the whole W update by
- * second_order_scale (:1546-1549); block_backward's outer update is RQ_GMODE_FROZEN. */
+ * second_order_scale (:1546-1549); block_backward's outer update is RQ_GMODE_FROZEN.
+ * z_zero != 0 is the caller's statement that Z (hence GH) is identically zero, i.e. that
+ * *z_nonzero == 0 (read back once after rq_gptqplus_terms): the frozen / block_gd modes then
+ * run a W-only kernel with 128x128 tiles.  Pass 0 when unknown; *z_nonzero then decides. */
 int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float* Z, int64_t ldgh,
                        const float* Hinv_all, int C, int R, int R_s, int i1, int count,
-                       const float* err, const int* z_nonzero, int gmode, const float* anchor,
+                       const float* err, const int* z_nonzero, int z_zero, int gmode, const float* anchor,
                        int64_t ld_anchor, const float* beta, double second_order_scale,
                        void* stream);
 

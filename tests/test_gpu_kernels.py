@@ -354,3 +354,41 @@ def test_trailing_update_matches_formula():
     for s in range(G):
         rows = slice(s * R_s, (s + 1) * R_s)
         assert rel_fro(Wd2[rows, i2:], W[rows, i2:] - err[rows] @ Hinv[s, i1:i2, i2:]) <= 1e-6
+
+
+@pytest.mark.parametrize("G,R_s,C,i1,cnt,gmode,sos", [
+    (2, 96, 300, 64, 64, 0, 1.0),        # ragged row and column tiles
+    (4, 256, 1024, 128, 128, 0, 1.0),    # interior 128x128 tiles only
+    (1, 200, 516, 0, 128, 3, 0.7),       # block_gd: the update scaled by second_order_scale
+    (3, 130, 392, 256, 8, 0, 1.0),       # a single 8-deep K step
+    (2, 64, 300, 100, 60, 0, 1.0),       # count % 8 != 0: the general kernel runs instead
+])
+def test_trailing_update_w_only(G, R_s, C, i1, cnt, gmode, sos):
+    """Z identically zero (z_zero=True): W[:, i2:] -= f err Hinv[i1:i2, i2:].  Where the W-only
+    kernel runs (count % 8 == 0) it forms the product as a k-ordered fused multiply-add chain,
+    like torch's CPU matmul, so W equals the reference expression evaluated on the CPU bit for
+    bit; the general kernel (and count % 8 != 0) is checked against float64 and that result."""
+    r = rng(10 + cnt)
+    Hinv = torch.from_numpy(np.triu(r.standard_normal((G, C, C))).astype(np.float32) * 0.1)
+    W = torch.from_numpy(r.standard_normal((G * R_s, C)).astype(np.float32))
+    err = torch.from_numpy(r.standard_normal((G * R_s, cnt)).astype(np.float32))
+    zero = torch.zeros_like(W).to(DEV)
+    nz0 = torch.zeros(1, dtype=torch.int32, device=DEV)
+    Hd, ed = Hinv.to(DEV), err.to(DEV)
+    Wf, Wg = W.to(DEV), W.to(DEV)
+    K.trailing_update(Wf, zero, zero, Hd, R_s, i1, cnt, ed, nz0, gmode, second_order_scale=sos, z_zero=True)
+    K.trailing_update(Wg, zero, zero, Hd, R_s, i1, cnt, ed, nz0, gmode, second_order_scale=sos)
+    torch.cuda.synchronize()
+    i2 = i1 + cnt
+    f = sos if gmode == 3 else 1.0
+    for s in range(G):
+        rows = slice(s * R_s, (s + 1) * R_s)
+        ref = W[rows, i2:].double() - f * (err[rows].double() @ Hinv[s, i1:i2, i2:].double())
+        assert rel_fro(Wf[rows, i2:], ref) <= 1e-6
+        assert rel_fro(Wf[rows, i2:], Wg[rows, i2:]) <= 1e-6
+        assert torch.equal(Wf[rows, :i2].cpu(), W[rows, :i2])
+        if cnt % 8 == 0:
+            second = err[rows].matmul(Hinv[s, i1:i2, i2:])                    # :1512-1519
+            exact = W[rows, i2:] - (f * second if gmode == 3 else second)
+            assert torch.equal(Wf[rows, i2:].cpu(), exact)
+    assert not zero.any()

@@ -44,15 +44,15 @@ def test_argument_validation_needs_no_device():
     assert lib.rq_chol_hinv_attempt(null, 4, 65, damp, null, null, null, null, null) == nat.RQ_EINVAL
     assert lib.rq_quant_block(null, 4, null, 4, null, null, 4, 4, 4, 0, 4, 0, null, null, null, 7, 1,
                               0, null, null, null, 0, null, 4, null, 1.0, null) == nat.RQ_EINVAL
-    assert lib.rq_trailing_update(null, 4, null, null, 4, null, 4, 4, 4, 0, 4, null, null, 0, null, 4,
+    assert lib.rq_trailing_update(null, 4, null, null, 4, null, 4, 4, 4, 0, 4, null, null, 0, 0, null, 4,
                                   null, 1.0, null) == nat.RQ_EINVAL
     # a surrogate g_update mode without its anchor / beta is refused before any launch
     fake = ctypes.c_void_p(16)
     assert lib.rq_quant_block(fake, 4, fake, 4, fake, fake, 4, 4, 4, 0, 4, 0, fake, null, null, 7, 1,
                               0, fake, fake, fake, 1, null, 4, null, 1.0, null) == nat.RQ_EINVAL
-    assert lib.rq_trailing_update(fake, 4, fake, fake, 4, fake, 4, 4, 4, 0, 2, fake, fake, 2, fake, 4,
+    assert lib.rq_trailing_update(fake, 4, fake, fake, 4, fake, 4, 4, 4, 0, 2, fake, fake, 0, 2, fake, 4,
                                   null, 1.0, null) == nat.RQ_EINVAL
-    assert lib.rq_trailing_update(fake, 4, fake, fake, 4, fake, 4, 4, 4, 0, 2, fake, fake, 4, fake, 4,
+    assert lib.rq_trailing_update(fake, 4, fake, fake, 4, fake, 4, 4, 4, 0, 2, fake, fake, 0, 4, fake, 4,
                                   fake, 1.0, null) == nat.RQ_EINVAL
     # refresh-mode entry points: missing optimizer state / regularizer inputs are refused
     D = ctypes.c_double
