@@ -199,7 +199,9 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
       w[k] = (w[k] - q) - ge;
     }
     // Err1 * Hinv1 = res, forward substitution (:1283-1288); column i = 16 m + r is owned by
-    // lane r, slot m
+    // lane r, slot m.  The operations are those of the CPU triangular solve (MKL strsm, which
+    // for blocks of up to 32 columns is this unblocked substitution): e_i = c_i * (1 / Hinv1[i][i])
+    // and c_k = fma(-e_i, Hinv1[i][k], c_k), applied to c_k for i = 0, 1, ... in order.
     static_for<NS>([&](auto mc) __attribute__((always_inline)) {
       static_for<QL>([&](auto rc) __attribute__((always_inline)) {
         constexpr int m = decltype(mc)::value, r = decltype(rc)::value;
@@ -207,10 +209,10 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
         if (i < count) {
           float h[NS];
           hrow(i, h);
-          const float e = row_bcast<r>(w[m] / h[m]);
+          const float e = row_bcast<r>(w[m] * (1.0f / h[m]));
           if (valid && t == r) erow[i] = e;
 #pragma unroll
-          for (int k = 0; k < NS; ++k) w[k] = w[k] - e * h[k];
+          for (int k = 0; k < NS; ++k) w[k] = __builtin_fmaf(-e, h[k], w[k]);
         }
       });
     });
