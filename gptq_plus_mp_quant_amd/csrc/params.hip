@@ -151,28 +151,37 @@ __device__ __forceinline__ bool same_key(float a, float b) {
 }
 
 // Stable descending rank sort: rank_i = #{j : key_j before key_i, or tie and j < i}.
-__global__ __launch_bounds__(256) void k_rank_desc(const float* __restrict__ key, int C,
-                                                   int64_t* __restrict__ perm,
-                                                   int64_t* __restrict__ invperm) {
-  __shared__ float tilek[1024];
+// Workgroup (x, y) counts, for the 64 keys i of chunk x (one per lane), the keys j of slice y
+// that come before them; its 4 waves take interleaved quarters of the slice and add their
+// counts in LDS, then one 64-bit atomic per key adds the slice's count into invperm (which
+// k_fill_i64 zeroed; integer sums do not depend on the order).  k_scatter_perm then writes perm.
+constexpr int RK_SLICE = 1024;
+__global__ void k_fill_i64(int64_t* __restrict__ p, int n) {
   const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+__global__ __launch_bounds__(256) void k_rank_desc(const float* __restrict__ key, int C,
+                                                   int64_t* __restrict__ rank) {
+  __shared__ int part[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = blockIdx.x * 64 + lane;
   const float ki = (i < C) ? key[i] : 0.0f;
-  int rank = 0;
-  for (int base = 0; base < C; base += 1024) {
-    __syncthreads();
-    for (int t = threadIdx.x; t < 1024; t += 256) tilek[t] = (base + t < C) ? key[base + t] : 0.0f;
-    __syncthreads();
-    const int n = min(1024, C - base);
-    for (int t = 0; t < n; ++t) {
-      const float kj = tilek[t];
-      const int j = base + t;
-      rank += (desc_before(kj, ki) || (same_key(kj, ki) && j < i)) ? 1 : 0;
-    }
+  const int j0 = blockIdx.y * RK_SLICE, j1 = min(j0 + RK_SLICE, C);
+  int cnt = 0;
+  for (int j = j0 + wave; j < j1; j += 4) {
+    const float kj = key[j];
+    cnt += (desc_before(kj, ki) || (same_key(kj, ki) && j < i)) ? 1 : 0;
   }
-  if (i < C) {
-    perm[rank] = i;
-    invperm[i] = rank;
+  part[wave][lane] = cnt;
+  __syncthreads();
+  if (wave == 0 && i < C) {
+    const int tot = part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane];
+    if (tot) atomicAdd(reinterpret_cast<unsigned long long*>(rank + i), (unsigned long long)tot);
   }
+}
+__global__ void k_scatter_perm(const int64_t* __restrict__ invperm, int C, int64_t* __restrict__ perm) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < C) perm[invperm[i]] = i;
 }
 
 template <typename TW>
@@ -302,7 +311,10 @@ extern "C" int rq_act_order_perm(const float* act_sq, int C, int64_t* perm, int6
                                  void* stream) {
   if (!act_sq || !perm || !invperm || C <= 0) return RQ_EINVAL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(k_rank_desc, dim3((C + 255) / 256), dim3(256), 0, s, act_sq, C, perm, invperm);
+  hipLaunchKernelGGL(k_fill_i64, dim3((C + 255) / 256), dim3(256), 0, s, invperm, C);
+  hipLaunchKernelGGL(k_rank_desc, dim3((C + 63) / 64, (C + RK_SLICE - 1) / RK_SLICE), dim3(256), 0, s,
+                     act_sq, C, invperm);
+  hipLaunchKernelGGL(k_scatter_perm, dim3((C + 255) / 256), dim3(256), 0, s, invperm, C, perm);
   RQ_CHECK_LAUNCH();
   return RQ_OK;
 }

@@ -186,6 +186,12 @@ def test_act_order_perm_stable_desc():
     # with distinct values the reference's (unstable) call gives the same order
     b = torch.from_numpy(r.standard_normal(4096).astype(np.float32))
     assert torch.equal(K.act_order_perm(b.to(DEV))[0].cpu(), torch.argsort(b, descending=True))
+    # the 70B down_proj width plus one (several key slices, a ragged last chunk), heavy ties
+    c = torch.from_numpy(r.integers(0, 300, size=28673).astype(np.float32))
+    c[r.choice(28673, 5, replace=False)] = float("nan")
+    perm, invperm = K.act_order_perm(c.to(DEV))
+    ref = torch.argsort(c, descending=True, stable=True)
+    assert torch.equal(perm.cpu(), ref) and torch.equal(invperm.cpu(), torch.argsort(ref))
 
 
 def _spd(seed, C, outlier=20.0):
