@@ -350,6 +350,31 @@ def copy_calibration(dev, nbytes=1 << 30, reps=3):
     print(json.dumps({"copy_calibration_bytes": nbytes, "reps": reps}), flush=True)
 
 
+def gemm_calibration(dev):
+    """Practical GEMM ceilings on this GPU: torch.matmul (hipBLASLt / rocBLAS) on large square
+    operands in fp16, fp32 (TF32 off) and fp64, as TFLOP/s.  The split Hessian kernel's products
+    run on the fp16 pipe, the Cholesky chain on the fp64 pipe, the trailing update on fp32."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    out = {}
+    for name, dt, n, reps in (("fp16", torch.float16, 8192, 20), ("fp32", torch.float32, 8192, 5),
+                              ("fp64", torch.float64, 8192, 3)):
+        a = torch.randn(n, n, device=dev).to(dt)
+        b = torch.randn(n, n, device=dev).to(dt)
+        for _ in range(2):
+            c = a @ b
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            c = a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out[name] = {"n": n, "ms": round(ms, 3), "tflops": round(2 * n ** 3 / ms / 1e9, 1)}
+        del a, b, c
+    print(json.dumps({"gemm_calibration": out}), flush=True)
+
+
 def load_traffic(math):
     """Calibrated HBM bytes per Hessian launch of the given kernel, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE measurement (None until measured)."""
@@ -380,6 +405,9 @@ def main():
                          "fp16 MFMA products; fp32: fp32 MFMA)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration for the traffic figure)")
+    ap.add_argument("--gemm-calibration", action="store_true",
+                    help="only time torch.matmul (hipBLASLt / rocBLAS) in fp16 / fp32 / fp64: the "
+                         "practical MFMA ceilings the kernels are compared with")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs the GPTQ+ hot path on one GPU only (asked for --gpus {args.gpus}); "
@@ -391,6 +419,9 @@ def main():
     nat.load().rq_hessian_math(nat.RQ_HMATH_SPLIT16 if args.hessian_math == "split16" else nat.RQ_HMATH_FP32)
     if args.copy_calibration:
         copy_calibration(dev)
+        return
+    if args.gemm_calibration:
+        gemm_calibration(dev)
         return
     if args.config in ("cfg3", "cfg4"):
         run_layer(args, dev)
