@@ -515,11 +515,13 @@ __device__ __forceinline__ void split_staged(const uint8_t* st, int wave, int la
 // fragment of step k+1 is split in between.  The MFMAs need no LDS read after the barrier, so
 // the two waves of a SIMD resume issuing as soon as it opens.  A bare s_barrier: the fence of
 // __syncthreads would wait for every staging load in flight.
-template <typename TX, int KP, int CUR, int NXT, int FILL>
+// DIAG (a diagonal tile): row blocks below this wave's column block hold only the discarded
+// lower triangle, so their row fragments are not read and their MFMAs not issued (bi < lim).
+template <typename TX, bool DIAG, int KP, int CUR, int NXT, int FILL>
 __device__ __forceinline__ void split_step(uint4 (&p)[2][XNP], uint4 (&a)[2][8], floatx16 (&acc)[8],
                                            const XStages& L, const uint16_t* pa, const uint16_t* pb,
                                            const float* sg, float sc, int wave, int lane, int64_t k,
-                                           int64_t last) {
+                                           int64_t last, int lim) {
   typedef XType<TX> T;
   typedef typename T::v8 v8;
   constexpr int NP = 1 - KP;
@@ -534,27 +536,35 @@ __device__ __forceinline__ void split_step(uint4 (&p)[2][XNP], uint4 (&a)[2][8],
   const float4 s0 = *reinterpret_cast<const float4*>(sp);
   const float4 s1 = *reinterpret_cast<const float4*>(sp + 16);
 #pragma unroll
-  for (int bi = 0; bi < 8; ++bi) a[NP][bi] = *reinterpret_cast<const uint4*>(nxt + bi * 1024);
+  for (int bi = 0; bi < 8; ++bi)
+    if (!DIAG || bi < lim) a[NP][bi] = *reinterpret_cast<const uint4*>(nxt + bi * 1024);
   const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
   const uint32_t xw[4] = {b.x, b.y, b.z, b.w};
   uint32_t o[XNP][4];
 #pragma unroll
   for (int bi = 0; bi < 8; ++bi)
-    acc[bi] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][XNP - 1]), acc[bi]);
+    if (!DIAG || bi < lim)
+      acc[bi] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][XNP - 1]), acc[bi]);
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     split_pair<TX>(xw[m], sv[2 * m], sv[2 * m + 1], sc, o[0][m], o[1][m], o[2][m]);
 #pragma unroll
     for (int i = 4 * m; i < 4 * m + 4; ++i) {
       const int q = 1 - i / 8, bi = i % 8;
-      acc[bi] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][q]), acc[bi]);
+      if (!DIAG || bi < lim)
+        acc[bi] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][q]), acc[bi]);
     }
   }
 #pragma unroll
   for (int q = 0; q < XNP; ++q) p[NP][q] = make_uint4(o[q][0], o[q][1], o[q][2], o[q][3]);
 }
 
-template <typename TX>
+// Column block of wave w: w for w < 4, 11 - w above, so the two waves that share a SIMD
+// (w and w + 4) own blocks c and 7 - c: on a diagonal tile, where wave w needs only the row
+// blocks up to its own, each SIMD then has 9 of the 16 blocks.
+__device__ __forceinline__ int split_colblock(int wave) { return wave < 4 ? wave : 11 - wave; }
+
+template <typename TX, bool DIAG>
 __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int64_t nks, int C,
                                            const float* __restrict__ sg, const float* __restrict__ scl,
                                            float* __restrict__ Hg, int R0, int C0, int64_t kbeg,
@@ -562,9 +572,13 @@ __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int6
   typedef typename XType<TX>::v8 v8;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave-uniform (an SGPR), so the DIAG row-block limit is a scalar branch: an MFMA under a
+  // zero exec mask would still update its accumulators
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, fh = lane >> 5;
-  const int Cw = C0 + 32 * wave;
+  const int cbw = split_colblock(wave);
+  const int Cw = C0 + 32 * cbw;
+  const int lim = DIAG ? cbw + 1 : 8;   // row blocks this wave computes
   const int ncb = (C + 31) / 32;
 
   // Fragment sources in the fragment-blocked chunk: block cb of 32 columns, step k at
@@ -592,30 +606,32 @@ __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int6
   {
     const uint8_t* cur = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[0] + lane * 16, 16));
 #pragma unroll
-    for (int bi = 0; bi < 8; ++bi) a[0][bi] = *reinterpret_cast<const uint4*>(cur + bi * 1024);
+    for (int bi = 0; bi < 8; ++bi)
+      if (!DIAG || bi < lim) a[0][bi] = *reinterpret_cast<const uint4*>(cur + bi * 1024);
   }
 
   const int64_t n = kend - kbeg;
   int64_t k = kbeg;
   static_assert(XDEPTH == 4, "unrolled stage schedule");
   for (; k + 4 <= kend; k += 4) {
-    split_step<TX, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last);
-    split_step<TX, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last);
-    split_step<TX, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last);
-    split_step<TX, 1, 3, 0, 2>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 3, last);
+    split_step<TX, DIAG, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last, lim);
+    split_step<TX, DIAG, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last, lim);
+    split_step<TX, DIAG, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last, lim);
+    split_step<TX, DIAG, 1, 3, 0, 2>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 3, last, lim);
   }
   const int rem = (int)(n & 3);
-  if (rem > 0) split_step<TX, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last);
-  if (rem > 1) split_step<TX, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last);
-  if (rem > 2) split_step<TX, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last);
+  if (rem > 0) split_step<TX, DIAG, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last, lim);
+  if (rem > 1) split_step<TX, DIAG, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last, lim);
+  if (rem > 2) split_step<TX, DIAG, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last, lim);
   XWAIT_VM(0);                        // no staging left in flight when the workgroup moves on
 
   if (part) {
-    // token slice: hand the (still scaled) partial tile to the workspace
+    // token slice: hand the (still scaled) partial tile to the workspace (zeros for the row
+    // blocks a diagonal tile does not compute)
 #pragma unroll
     for (int bi = 0; bi < 8; ++bi)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) part[(bi * 16 + e) * XTHREADS + tid] = acc[bi][e];
+      for (int e = 0; e < 16; ++e) part[(bi * 16 + e) * XTHREADS + tid] = (DIAG && bi >= lim) ? 0.0f : acc[bi][e];
     return;
   }
   // H[g][i][j] += acc * 2^-e_j   (32x32 block layout: i = 8*(e/4) + 4*(lane/32) + e%4, j = lane%32)
@@ -624,6 +640,7 @@ __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int6
   const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
 #pragma unroll
   for (int bi = 0; bi < 8; ++bi) {
+    if (DIAG && bi >= lim) continue;   // below the diagonal: nothing was accumulated
     float hv[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -646,7 +663,7 @@ __device__ __forceinline__ void reduce_split_slices(const float* __restrict__ pa
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int fr = lane & 31, fh = lane >> 5;
-  const int j = C0 + 32 * wave + fr;
+  const int j = C0 + 32 * split_colblock(wave) + fr;   // the column the slices' thread held
   const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
 #pragma unroll 1
   for (int bi = 0; bi < 8; ++bi)
@@ -702,7 +719,10 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
   const float* scl = scale + (int64_t)g * C;
   float* part0 = (slice >= 0) ? ws + (int64_t)(logical - full) * S * XPART : nullptr;
   float* part = part0 ? part0 + (int64_t)slice * XPART : nullptr;
-  split_tile<TX>(XB, nks, C, sT + (int64_t)g * lds_stride, scl, Hg, R0, C0, kbeg, kend, part, L);
+  if (R0 == C0)
+    split_tile<TX, true>(XB, nks, C, sT + (int64_t)g * lds_stride, scl, Hg, R0, C0, kbeg, kend, part, L);
+  else
+    split_tile<TX, false>(XB, nks, C, sT + (int64_t)g * lds_stride, scl, Hg, R0, C0, kbeg, kend, part, L);
   if (!part) return;
   __threadfence();
   __syncthreads();
