@@ -19,7 +19,10 @@
 namespace {
 
 constexpr int NB = 64;     // diagonal block (factored and inverted by one wavefront)
-constexpr int NBW = 256;   // outer panel width
+// Outer panel width: 256, or 512 from C = 8192 on.  The panel update re-reads and re-writes
+// its output tile once per panel, so wider panels halve that epilogue's share; the extra
+// in-panel work (C^2 NBW / 2 flops) stays ~1 % of the C^3 chain there.
+__host__ __device__ constexpr int panel_width(int C) { return C >= 8192 ? 512 : 256; }
 
 __global__ void k_fill_i32(int* p, int v) { *p = v; }
 __global__ void k_fill_f32(float* p, float v) { *p = v; }
@@ -372,13 +375,14 @@ __global__ __launch_bounds__(256) void k_safe_beta(const float* __restrict__ G, 
 }
 
 // ---------------------------------------------------------------------------------------------
-// The two rank-K updates that follow each outer panel (K = NBW columns k .. k+K of L, rows
+// The two rank-K updates that follow each outer panel (K = NBW = 256 or 512 columns k .. k+K of L, rows
 // pe .. C), in one launch:
 //   SYRK part:  A[pe:, pe:] -= Lp Lp^T       (lower 128-tiles; Lp = L[pe:, k:k+K])
 //   row part:   Linv[pe:, 0:pe] -= Lp X      (X = Linv[k:k+K, 0:pe], row block of L^-1)
-// 128 x 128 output tiles, 4 waves of 64 x 64 (4 x 4 blocks of v_mfma_f64_16x16x4f64).  K
-// advances 8 at a time through a ring of PSTAGES LDS stages filled by direct global -> LDS
-// loads (16 bytes per lane) issued PSTAGES-1 steps ahead; one barrier per step.
+// 128 x 128 output tiles, 8 waves of 32 x 64 (2 x 4 blocks of v_mfma_f64_16x16x4f64; two
+// workgroups per CU give 4 waves per SIMD).  K advances 8 at a time through a ring of PSTAGES
+// LDS stages filled by direct global -> LDS loads (16 bytes per lane) issued PSTAGES-1 steps
+// ahead; one barrier per step.
 //  - Operands stored k-contiguous (Lp for both sides of the SYRK, Lp for the row part): a
 //    staging chunk is 16 rows x 8 k (1 KB); lane L fetches row L/4, k pair p = (L%4) ^
 //    ((row/4)%4) into LDS slot L, so the four lanes of a row read its 64 contiguous bytes and
@@ -429,53 +433,46 @@ struct PStages {
 template <bool SYRK>
 struct PanelTile {
   const PanelArgs& p;
-  const double* srcA[2];
-  const double* srcB[2];
+  const double* srcA;
+  const double* srcB;
   int wave, lane, wr, wc, g, r, slot, nk;
   bool live;
-  doublex4 acc[4][4];
+  doublex4 acc[2][4];
 
   __device__ __forceinline__ PanelTile(const PanelArgs& pp, int64_t boff, int i0, int j0, int ti, int tj)
       : p(pp) {
     const int tid = threadIdx.x;
     lane = tid & 63;
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    wr = wave >> 1;
-    wc = wave & 1;
+    wr = wave >> 1;                          // rows 32 wr .. 32 wr + 31
+    wc = wave & 1;                           // columns 64 wc .. 64 wc + 63
     g = lane >> 4;
     r = lane & 15;
     slot = 4 * r + (g ^ ((r >> 2) & 3));
     nk = p.K / PKS;
-    live = !(SYRK && ti == tj && wr < wc);   // a 64-block strictly above the diagonal
+    live = !(SYRK && ti == tj && wr < 2 * wc);   // inside a 64-block strictly above the diagonal
     const int M = p.rest, N = SYRK ? p.rest : p.pe;
     const double* Lp = p.Lp + boff;
-    // this wave's staging sources: chunks 2 wave and 2 wave + 1 of each operand
+    // this wave's staging sources: chunk `wave` of each operand
     const int cr = lane >> 2, kp = (lane & 3) ^ ((cr >> 2) & 3);
+    const int c = wave;
+    srcA = Lp + (int64_t)min(i0 + 16 * c + cr, M - 1) * p.ld + 2 * kp;
+    if (SYRK) srcB = Lp + (int64_t)min(j0 + 16 * c + cr, N - 1) * p.ld + 2 * kp;
+    else srcB = p.X + boff + (int64_t)c * p.ld + min(j0 + 2 * lane, N - 2);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int c = 2 * wave + h;
-      srcA[h] = Lp + (int64_t)min(i0 + 16 * c + cr, M - 1) * p.ld + 2 * kp;
-      if (SYRK) srcB[h] = Lp + (int64_t)min(j0 + 16 * c + cr, N - 1) * p.ld + 2 * kp;
-      else srcB[h] = p.X + boff + (int64_t)c * p.ld + min(j0 + 2 * lane, N - 2);
-    }
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[a][b][e] = 0.0;
   }
 
-  // 4 staging loads per wave: A chunks 2 wave, 2 wave + 1 and the same chunks of B
+  // 2 staging loads per wave: chunk `wave` of A and of B
   __device__ __forceinline__ void stage(uint8_t* st, int kt) {
     const int64_t ka = (int64_t)kt * PKS;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int c = 2 * wave + h;
-      lds_dma16(srcA[h] + ka, st + c * PCHUNK);
-      if (SYRK) lds_dma16(srcB[h] + ka, st + PA_BYTES + c * PCHUNK);
-      else lds_dma16(srcB[h] + ka * p.ld, st + PA_BYTES + c * PXROW);
-    }
+    lds_dma16(srcA + ka, st + wave * PCHUNK);
+    if (SYRK) lds_dma16(srcB + ka, st + PA_BYTES + wave * PCHUNK);
+    else lds_dma16(srcB + ka * p.ld, st + PA_BYTES + wave * PXROW);
   }
 
   // Step kt: wait for this wave's staging of kt (the PSTAGES-2 later steps may still be in
@@ -483,15 +480,15 @@ struct PanelTile {
   // FILL stage, done in step kt-1, is over), refill FILL with step kt+PSTAGES-1, multiply kt.
   template <int CUR, int FILL>
   __device__ __forceinline__ void step(const PStages& L, int kt) {
-    PWAIT_VM(4 * (PSTAGES - 2));
+    PWAIT_VM(2 * (PSTAGES - 2));
     __builtin_amdgcn_s_barrier();
     stage(L.s[FILL], min(kt + PSTAGES - 1, nk - 1));
     if (!live) return;
     const uint8_t* st = L.s[CUR];
-    double2 av[4];
+    double2 av[2];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-      av[rb] = *reinterpret_cast<const double2*>(st + (4 * wr + rb) * PCHUNK + 16 * slot);
+    for (int rb = 0; rb < 2; ++rb)
+      av[rb] = *reinterpret_cast<const double2*>(st + (2 * wr + rb) * PCHUNK + 16 * slot);
     double bv[2][4];
     if (SYRK) {
 #pragma unroll
@@ -509,12 +506,12 @@ struct PanelTile {
                                                         8 * (64 * wc + 16 * cb + r));
     }
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb)
         acc[rb][cb] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[rb].x, bv[0][cb], acc[rb][cb], 0, 0, 0);
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb)
         acc[rb][cb] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[rb].y, bv[1][cb], acc[rb][cb], 0, 0, 0);
@@ -546,10 +543,10 @@ __device__ __forceinline__ void panel_tile(const PanelArgs& p, int64_t boff, int
   double* Cm = (SYRK ? p.Atr : p.Brow) + boff;
   // 16x16 f64 block layout: column lane % 16, row lane / 16 + 4 e.  Per 16-row block the 16
   // loads are issued together (clamped in-bounds addresses), then the 16 stores.
-  const int ib = i0 + 64 * t.wr + t.g, jb = j0 + 64 * t.wc + t.r;
+  const int ib = i0 + 32 * t.wr + t.g, jb = j0 + 64 * t.wc + t.r;
   const bool full = (i0 + PT <= M) && (j0 + PT <= N);
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
+  for (int rb = 0; rb < 2; ++rb) {
     double cv[4][4];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb)
@@ -576,7 +573,53 @@ __device__ __forceinline__ void panel_tile(const PanelArgs& p, int64_t boff, int
   }
 }
 
-__global__ __launch_bounds__(256, 2) void k_panel_update(PanelArgs p) {
+// Tile order.  Tiles are walked in bands of `band` tile rows, column by column inside a band
+// (then the band's rows): a column operand tile (128 panel rows x K) then serves `band` output
+// tiles while it is in L2, and the band's row operand (band x 128 x K doubles: 2 MB, 8 rows at
+// K = 256 or 4 at K = 512) stays there for the whole band.  Row-major order re-fetched every
+// column operand once per tile row: 3x the algorithmic bytes at C = 28672.
+__host__ __device__ constexpr int panel_band(int K) { return K > 256 ? 4 : 8; }
+
+// u-th tile of the lower triangle (tj <= ti < nt) in band order.
+__device__ __forceinline__ void lower_tile_banded(int u, int nt, int PBAND, int& ti, int& tj) {
+  int b0 = 0;
+  for (;;) {
+    const int h = min(PBAND, nt - b0);
+    const int cnt = b0 * h + h * (h + 1) / 2;   // b0 full columns of h rows, then the triangle
+    if (u < cnt || b0 + h >= nt) break;
+    u -= cnt;
+    b0 += h;
+  }
+  const int h = min(PBAND, nt - b0);
+  if (u < b0 * h) {
+    tj = u / h;
+    ti = b0 + u % h;
+    return;
+  }
+  u -= b0 * h;
+  for (int c = b0;; ++c) {           // column c holds rows c .. b0 + h - 1 of the band
+    const int k = b0 + h - c;
+    if (u < k) {
+      tj = c;
+      ti = c + u;
+      return;
+    }
+    u -= k;
+  }
+}
+
+// u-th tile of an nr x nc grid in band order.
+__device__ __forceinline__ void rect_tile_banded(int u, int nr, int nc, int PBAND, int& ti, int& tj) {
+  const int band = u / (PBAND * nc);
+  const int b0 = band * PBAND;
+  const int h = min(PBAND, nr - b0);
+  const int v = u - b0 * nc;
+  tj = v / h;
+  ti = b0 + v % h;
+}
+
+constexpr int PTHREADS = 512;
+__global__ __launch_bounds__(PTHREADS, 2) void k_panel_update(PanelArgs p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds0[PSTAGE];
   __shared__ __attribute__((aligned(16))) uint8_t lds1[PSTAGE];
   __shared__ __attribute__((aligned(16))) uint8_t lds2[PSTAGE];
@@ -592,15 +635,13 @@ __global__ __launch_bounds__(256, 2) void k_panel_update(PanelArgs p) {
   const int bz = t / p.per_batch, u = t % p.per_batch;
   if (p.info[bz]) return;
   const int64_t boff = (int64_t)bz * p.ws;
+  int ti, tj;
   if (u < p.nsy) {
-    // lower-triangle tile u, row-major: ti (ti + 1) / 2 <= u < (ti + 1) (ti + 2) / 2
-    int ti = (int)((__builtin_sqrtf(8.0f * (float)u + 1.0f) - 1.0f) * 0.5f);
-    while ((ti + 1) * (ti + 2) / 2 <= u) ++ti;
-    while (ti * (ti + 1) / 2 > u) --ti;
-    panel_tile<true>(p, boff, ti, u - ti * (ti + 1) / 2, L);
+    lower_tile_banded(u, p.ntr, panel_band(p.K), ti, tj);
+    panel_tile<true>(p, boff, ti, tj, L);
   } else {
-    const int v = u - p.nsy;
-    panel_tile<false>(p, boff, v / p.nxc, v % p.nxc, L);
+    rect_tile_banded(u - p.nsy, p.ntr, p.nxc, panel_band(p.K), ti, tj);
+    panel_tile<false>(p, boff, ti, tj, L);
   }
 }
 
@@ -659,6 +700,7 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
   // stay inside the panel; the trailing matrix (and the rows of L^-1 below the panel) get
   // one rank-NBW update per panel, so the big updates read and write the trailing matrix
   // NBW / NB times less often.
+  const int NBW = panel_width(C);
   for (int k = 0; k < C; k += NBW) {
     const int kw = (C - k < NBW) ? (C - k) : NBW;
     const int pe = k + kw;                               // panel end
@@ -713,7 +755,7 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
       pa.ws = ws;
       pa.info = info;
       pa.total = pa.per_batch * nb;
-      hipLaunchKernelGGL(k_panel_update, dim3(pa.total), dim3(256), 0, s, pa);
+      hipLaunchKernelGGL(k_panel_update, dim3(pa.total), dim3(PTHREADS), 0, s, pa);
       RQ_CHECK_LAUNCH();
     } else if (rest > 0) {
       // the same two updates on the 64-tile GEMM (odd C)

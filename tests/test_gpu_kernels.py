@@ -229,6 +229,31 @@ def test_cholesky_chain(C):
     assert rel_fro(Hw, Hd_ref) <= 1e-7
 
 
+@pytest.mark.parametrize("C", [8200])
+def test_cholesky_chain_wide_panels(C):
+    """C >= 8192 runs 512-wide panels (K = 512 panel updates, 4-row tile bands) with a ragged
+    last panel; checked against the float64 upper Cholesky factor of H_work^-1 (numpy / scipy
+    on the host)."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(C)
+    A = torch.randn(2 * C, C, device=DEV, generator=g)
+    A[:, :3] *= 20.0
+    H = (A.T @ (A * torch.rand(2 * C, 1, device=DEV, generator=g))) / (2 * C)
+    del A
+    Hw = H.clone()
+    ws = K.chol_workspace(C, DEV)
+    Hinv = torch.empty(C, C, device=DEV)
+    info = K.chol_hinv_attempt(Hw, 0.01, ws, Hinv, None)
+    torch.cuda.synchronize()
+    assert int(info.item()) == 0
+    assert torch.equal(Hinv, torch.triu(Hinv)) and bool((torch.diag(Hinv) > 0).all())
+    Hd = Hw.double().cpu().numpy()
+    U_true = torch.from_numpy(scipy.linalg.cholesky(np.linalg.inv(Hd), lower=False))
+    err = rel_fro(Hinv, U_true)
+    print(f"C={C}: rel-Frobenius vs float64 truth {err:.2e}")
+    assert err <= 1e-5
+
+
 @pytest.mark.parametrize("C", [200, 600])
 def test_cholesky_batch_independent_entries(C):
     """Batched attempt: each matrix gets its own damping, skipped entries stay untouched, and a
