@@ -400,17 +400,22 @@ constexpr int PXROW = PCHUNK + 64;          // X k-row stride in a stage
 constexpr int PA_BYTES = 8 * PCHUNK;
 constexpr int PSTAGE = PA_BYTES + 8 * PXROW;
 
+// SYRK part: Atr[i][j] -= sum_k Lp[i][k] Lp[j][k] for i < ms, j < ns <= ms, lower tiles
+// (tj <= ti); row part: Brow[i][j] -= sum_k Lp[i][k] X[k][j] for i < mr <= ms, j < nr.
+// After a panel: ms = ns = mr = C - pe, nr = pe.  Inside a panel (block j of width jb):
+// ms = rows below the block, ns = mr = panel columns right of it, nr = j + jb.
 struct PanelArgs {
-  const double* Lp;    // Lp[i * ld + kk]: row i of the panel (i < rest), column kk < K
-  const double* X;     // X[kk * ld + j], j < pe
-  double* Atr;         // trailing matrix origin (row pe, column pe)
-  double* Brow;        // Linv row pe, column 0
+  const double* Lp;    // Lp[i * ld + kk], column kk < K
+  const double* X;     // X[kk * ld + j]
+  double* Atr;
+  double* Brow;
   int64_t ld;
-  int rest, pe, K;
-  int ntr;             // row tiles: ceil(rest / PT)
-  int nsy;             // SYRK tiles: ntr (ntr + 1) / 2
-  int nxc;             // row-part column tiles: ceil(pe / PT)
-  int per_batch;       // nsy + ntr * nxc
+  int K;
+  int ms, ns, mr, nr;
+  int ntr, ntc;        // SYRK row / column tiles
+  int nsy;             // SYRK tiles (lower trapezoid)
+  int nrr, nrc;        // row-part row / column tiles
+  int per_batch;       // nsy + nrr * nrc
   int64_t ws;          // batch stride (doubles)
   const int* info;
   int total;           // per_batch * nb
@@ -451,7 +456,7 @@ struct PanelTile {
     slot = 4 * r + (g ^ ((r >> 2) & 3));
     nk = p.K / PKS;
     live = !(SYRK && ti == tj && wr < 2 * wc);   // inside a 64-block strictly above the diagonal
-    const int M = p.rest, N = SYRK ? p.rest : p.pe;
+    const int M = SYRK ? p.ms : p.mr, N = SYRK ? p.ns : p.nr;
     const double* Lp = p.Lp + boff;
     // this wave's staging sources: chunk `wave` of each operand
     const int cr = lane >> 2, kp = (lane & 3) ^ ((cr >> 2) & 3);
@@ -539,7 +544,7 @@ __device__ __forceinline__ void panel_tile(const PanelArgs& p, int64_t boff, int
   if (rem > 2) t.template step<2, 1>(L, kt + 2);
   PWAIT_VM(0);   // no staging in flight when the workgroup moves on
   if (!t.live) return;
-  const int M = p.rest, N = SYRK ? p.rest : p.pe;
+  const int M = SYRK ? p.ms : p.mr, N = SYRK ? p.ns : p.nr;
   double* Cm = (SYRK ? p.Atr : p.Brow) + boff;
   // 16x16 f64 block layout: column lane % 16, row lane / 16 + 4 e.  Per 16-row block the 16
   // loads are issued together (clamped in-bounds addresses), then the 16 stores.
@@ -580,23 +585,26 @@ __device__ __forceinline__ void panel_tile(const PanelArgs& p, int64_t boff, int
 // column operand once per tile row: 3x the algorithmic bytes at C = 28672.
 __host__ __device__ constexpr int panel_band(int K) { return K > 256 ? 4 : 8; }
 
-// u-th tile of the lower triangle (tj <= ti < nt) in band order.
-__device__ __forceinline__ void lower_tile_banded(int u, int nt, int PBAND, int& ti, int& tj) {
+// u-th tile of the lower trapezoid {(ti, tj): tj <= ti < ntr, tj < ntc} in band order.
+__device__ __forceinline__ void lower_tile_banded(int u, int ntr, int ntc, int PBAND, int& ti, int& tj) {
   int b0 = 0;
   for (;;) {
-    const int h = min(PBAND, nt - b0);
-    const int cnt = b0 * h + h * (h + 1) / 2;   // b0 full columns of h rows, then the triangle
-    if (u < cnt || b0 + h >= nt) break;
+    const int h = min(PBAND, ntr - b0);
+    const int ce = min(b0 + h, ntc);
+    int cnt = min(b0, ntc) * h;                 // columns left of the band: h rows each
+    for (int c = b0; c < ce; ++c) cnt += b0 + h - c;
+    if (u < cnt || b0 + h >= ntr) break;
     u -= cnt;
     b0 += h;
   }
-  const int h = min(PBAND, nt - b0);
-  if (u < b0 * h) {
+  const int h = min(PBAND, ntr - b0);
+  const int full = min(b0, ntc) * h;
+  if (u < full) {
     tj = u / h;
     ti = b0 + u % h;
     return;
   }
-  u -= b0 * h;
+  u -= full;
   for (int c = b0;; ++c) {           // column c holds rows c .. b0 + h - 1 of the band
     const int k = b0 + h - c;
     if (u < k) {
@@ -637,15 +645,46 @@ __global__ __launch_bounds__(PTHREADS, 2) void k_panel_update(PanelArgs p) {
   const int64_t boff = (int64_t)bz * p.ws;
   int ti, tj;
   if (u < p.nsy) {
-    lower_tile_banded(u, p.ntr, panel_band(p.K), ti, tj);
+    lower_tile_banded(u, p.ntr, p.ntc, panel_band(p.K), ti, tj);
     panel_tile<true>(p, boff, ti, tj, L);
   } else {
-    rect_tile_banded(u - p.nsy, p.ntr, p.nxc, panel_band(p.K), ti, tj);
+    rect_tile_banded(u - p.nsy, p.nrr, p.nrc, panel_band(p.K), ti, tj);
     panel_tile<false>(p, boff, ti, tj, L);
   }
 }
 
 }  // namespace
+
+// One k_panel_update launch over nb batch entries (see PanelArgs).  Requires C even and K a
+// multiple of PKS; returns false (nothing launched) otherwise.
+inline bool launch_panel(const double* Lp, const double* X, double* Atr, double* Brow, int C, int K,
+                         int ms, int ns, int mr, int nr, int64_t ws, const int* info, int nb,
+                         hipStream_t s) {
+  if ((C & 1) || K % PKS || K <= 0) return false;
+  PanelArgs pa;
+  pa.Lp = Lp;
+  pa.X = X;
+  pa.Atr = Atr;
+  pa.Brow = Brow;
+  pa.ld = C;
+  pa.K = K;
+  pa.ms = ms;
+  pa.ns = ns;
+  pa.mr = mr;
+  pa.nr = nr;
+  pa.ntr = ms > 0 ? (ms + PT - 1) / PT : 0;
+  pa.ntc = ns > 0 ? (ns + PT - 1) / PT : 0;
+  pa.nsy = 0;
+  for (int ti = 0; ti < pa.ntr; ++ti) pa.nsy += (ti + 1 < pa.ntc) ? ti + 1 : pa.ntc;
+  pa.nrr = (mr > 0 && nr > 0) ? (mr + PT - 1) / PT : 0;
+  pa.nrc = (mr > 0 && nr > 0) ? (nr + PT - 1) / PT : 0;
+  pa.per_batch = pa.nsy + pa.nrr * pa.nrc;
+  pa.ws = ws;
+  pa.info = info;
+  pa.total = pa.per_batch * nb;
+  if (pa.total > 0) hipLaunchKernelGGL(k_panel_update, dim3(pa.total), dim3(PTHREADS), 0, s, pa);
+  return true;
+}
 
 extern "C" int64_t rq_chol_workspace_bytes(int C) {
   if (C <= 0) return -1;
@@ -719,9 +758,15 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
       GemmArgs<double> xj = batched(gemm_args<double>(Tbuf, NB, Linv + (int64_t)j * C, C,
                                                       Linv + (int64_t)j * C, C, jb, j, jb, 1.0, EPI_STORE));
       if ((rc = launch_gemm_pair(lij, xj, s, nb))) return rc;
-      if (pend > 0) {
-        // one launch, inside the panel: A[j+jb:, j+jb:pe] -= L[j+jb:, j] L[j+jb:pe, j]^T (lower
-        // tiles) and the panel rows of L^-1: B[j+jb:pe, 0:j+jb] -= L[j+jb:pe, j] X_j
+      // one launch, inside the panel: A[j+jb:, j+jb:pe] -= L[j+jb:, j] L[j+jb:pe, j]^T (lower
+      // tiles) and the panel rows of L^-1: B[j+jb:pe, 0:j+jb] -= L[j+jb:pe, j] X_j.  On the
+      // 128-tile panel kernel with 512-wide panels (up to 448 columns); the narrower updates of
+      // 256-wide panels have too few 128-tiles and run faster on the 64-tile GEMM.
+      if (pend > 0 && NBW > 256 && launch_panel(A + (int64_t)(j + jb) * C + j, Linv + (int64_t)j * C,
+                                   A + (int64_t)(j + jb) * C + (j + jb), Linv + (int64_t)(j + jb) * C,
+                                   C, jb, below, pend, pend, j + jb, ws, info, nb, s)) {
+        RQ_CHECK_LAUNCH();
+      } else if (pend > 0) {
         GemmArgs<double> h = batched(gemm_args<double>(A + (int64_t)(j + jb) * C + j, C,
                                                        A + (int64_t)(j + jb) * C + j, C,
                                                        A + (int64_t)(j + jb) * C + (j + jb), C, below,
@@ -735,30 +780,13 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
       }
     }
     const int rest = C - pe;
-    if (rest > 0 && (C & 1) == 0 && kw % PKS == 0) {
-      // one launch: the trailing matrix A[pe:, pe:] -= L[pe:, k:pe] L[pe:, k:pe]^T (lower tiles,
-      // K = kw) and the rows of L^-1 below the panel: B[pe:, 0:pe] -= L[pe:, k:pe] X[k:pe, 0:pe]
-      // (rows 16-byte aligned: C even; pe is a multiple of NBW, so X's column pairs stay inside)
-      PanelArgs pa;
-      pa.Lp = A + (int64_t)pe * C + k;
-      pa.X = Linv + (int64_t)k * C;
-      pa.Atr = A + (int64_t)pe * C + pe;
-      pa.Brow = Linv + (int64_t)pe * C;
-      pa.ld = C;
-      pa.rest = rest;
-      pa.pe = pe;
-      pa.K = kw;
-      pa.ntr = (rest + PT - 1) / PT;
-      pa.nsy = pa.ntr * (pa.ntr + 1) / 2;
-      pa.nxc = (pe + PT - 1) / PT;
-      pa.per_batch = pa.nsy + pa.ntr * pa.nxc;
-      pa.ws = ws;
-      pa.info = info;
-      pa.total = pa.per_batch * nb;
-      hipLaunchKernelGGL(k_panel_update, dim3(pa.total), dim3(PTHREADS), 0, s, pa);
+    // one launch: the trailing matrix A[pe:, pe:] -= L[pe:, k:pe] L[pe:, k:pe]^T (lower tiles,
+    // K = kw) and the rows of L^-1 below the panel: B[pe:, 0:pe] -= L[pe:, k:pe] X[k:pe, 0:pe]
+    if (rest > 0 && launch_panel(A + (int64_t)pe * C + k, Linv + (int64_t)k * C, A + (int64_t)pe * C + pe,
+                                 Linv + (int64_t)pe * C, C, kw, rest, rest, rest, pe, ws, info, nb, s)) {
       RQ_CHECK_LAUNCH();
     } else if (rest > 0) {
-      // the same two updates on the 64-tile GEMM (odd C)
+      // the same two updates on the 64-tile GEMM (odd C, or a panel width not a multiple of 8)
       GemmArgs<double> h = batched(gemm_args<double>(A + (int64_t)pe * C + k, C, A + (int64_t)pe * C + k,
                                                      C, A + (int64_t)pe * C + pe, C, rest, rest, kw,
                                                      -1.0, EPI_ACCUM));
