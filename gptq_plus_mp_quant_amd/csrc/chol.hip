@@ -6,14 +6,16 @@
 // upper factor U of H^-1 (U^T U = H^-1) is obtained with ONE factorisation: with P the
 // index-reversal permutation and L L^T = P H P,  U = P L^-1 P.  The factorisation and the
 // inverse L^-1 run together in one right-looking blocked pass in fp64 (64-wide blocks
-// inside 256-wide panels):
-//   per block k:  L_kk = chol(A_kk) and T = L_kk^-1 (one workgroup),
+// inside 256-wide panels, 512-wide from C = 8192):
+//   per block k:  L_kk = chol(A_kk) and T = L_kk^-1 (k_chol_diag, one workgroup per matrix),
 //                 L_ik = A_ik T^T,  X_k = T B_k  (row block k of L^-1),
 //                 A_ij -= L_ik L_jk^T (lower tiles),  B_i -= L_ik X_k   (fp64 MFMA GEMMs),
-// where B accumulates I - sum_m L_im X_m; the updates of the trailing matrix and of the
-// rows of B below a panel are applied once per panel (rank 256) instead of once per block.  H^-1 itself (Hinv_init) is P (L^-T L^-1) P and is
-// only formed when asked for.  A non-positive or non-finite pivot, or a non-finite result,
-// raises the device `info` flag; later kernels of the same attempt exit early.
+// where B accumulates I - sum_m L_im X_m.  The updates of the trailing matrix and of the rows
+// of B below a panel are applied once per panel (rank 256 / 512) instead of once per block,
+// by k_panel_update (128x128 tiles, direct global->LDS staging).  H^-1 itself (Hinv_init) is
+// P (L^-T L^-1) P and is only formed when asked for.  A non-positive or non-finite pivot, or
+// a non-finite result, raises the device `info` flag; later kernels of the same attempt exit
+// early.
 #include "gemm_tile.h"
 
 namespace {

@@ -24,6 +24,9 @@
 // or the block start (surrogate_block).  A fifth register array per row holds the anchor
 // (online) or the constant difference W_block_start - W_anchor (block).
 //
+// k_trailing_w (Z identically zero, frozen / block_gd): W[:, i2:] -= Err Hinv[i1:i2, i2:] with
+// the product formed as a k-ordered fused multiply-add chain on the matrix cores, bit-identical
+// to the reference's CPU matmul (see the kernel).  Otherwise:
 // k_trailing: W[:, i2:] -= Err Hinv[i1:i2, i2:] + (count GH[:, i2:] - (Z1 D) Hinv[i1:i2, i2:])
 // and GH[:, i2:] -= Z1 Hinv[i1:i2, i2:], 64x64 output tiles, fp32 16x16x4 MFMA, K = count
 // streamed through LDS in slabs of 32.  The Z terms are skipped when Z is identically zero.
