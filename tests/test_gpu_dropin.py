@@ -281,3 +281,33 @@ def test_dropin_errors_and_side_effects():
     _accumulate(g3, X, 2)
     with pytest.raises(ValueError, match="NaN"):
         g3.fasterquant(blocksize=64)
+
+
+@pytest.mark.parametrize("gs,act", [(-1, True), (128, True), (128, False)],
+                         ids=["perchannel_act", "static_groups_act", "dynamic_groups"])
+def test_dropin_bf16_vs_oracle(gs, act):
+    """A bf16 checkpoint: bf16 layer and bf16 activations.  The Hessian runs on the split
+    kernel's bf16 path (pieces of 8 + 8 + 8 bits); with the oracle's H^-1 injected and Z = 0 the
+    block loop is bit-exact, so codes, scales and the bf16 weight equal the oracle's."""
+    R, C, G, N, T = 256, 384, 2, 8, 256
+    X, W, s, grad = synth(4242 + gs + int(act), R, C, G, N, T, x_dtype=torch.bfloat16)
+    W = W.to(torch.bfloat16)
+    o = GPTQPlusOracle(W, s, grad, G, 0.0, 0.0)
+    o.quantizer = make_quantizer(4, True)
+    for j in range(0, N, 4):
+        o.add_batch(X[j:j + 4])
+    o.finalize_hessian()
+    fq = dict(blocksize=128, percdamp=0.01, groupsize=gs, actorder=act, static_groups=act)
+    res = o.fasterquant(stable_ties=True, **fq)
+    g, layer = _gpu_obj(W, s, grad, G, 0.0, 0.0, 4, True)
+    _accumulate(g, X, 4)
+    assert rel_fro(g.H, o.H) <= 1e-5
+    g.H.copy_(o.H.to(DEV))
+    g.act_square.copy_(o.act_square.to(DEV))
+    inject = {"hinv": [(r.Hinv_init.to(DEV), r.Hinv.to(DEV)) for r in res.subgroups]}
+    g.fasterquant(export_to_et=True, inject=inject, **fq)
+    torch.cuda.synchronize()
+    assert layer.weight.dtype == torch.bfloat16
+    assert code_flips(layer.int_weight, res.W_int) == 0
+    assert torch.equal(layer.scale.cpu(), res.Scale)
+    assert torch.equal(layer.weight.data.cpu(), res.Q)
