@@ -130,17 +130,6 @@ __device__ __forceinline__ void split_tile_order(int t, int nt, int& ti, int& tj
   }
 }
 
-// Map a linear upper-triangle tile index to (ti, tj), ti <= tj, row-major.
-__device__ __forceinline__ void upper_tile(int t, int nt, int& ti, int& tj) {
-  int row = 0;
-  int rem = t;
-  while (rem >= nt - row) {
-    rem -= nt - row;
-    ++row;
-  }
-  ti = row;
-  tj = row + rem;
-}
 
 // Partial tile of one token slice: 64 accumulator floats per thread, stored e-major so each
 // store instruction of the workgroup writes 1 KB contiguously, then 128 act_square partials.
@@ -923,44 +912,63 @@ __global__ __launch_bounds__(256) void k_xfinish(int C, int nchunk, HTargets tg,
 namespace {
 
 // finalize_hessian (gptq_plus_utils.py:881-907): divide, symmetrise from the upper triangle,
-// sanitise non-finite entries.  One 32x32 upper tile pair per workgroup.
-__global__ __launch_bounds__(256) void k_hessian_finalize(float* __restrict__ H, int C, int nt,
-                                                          float h_div, float sal_scale,
-                                                          int apply_scale, int* nonfinite) {
-  __shared__ float tile[32][33];
+// sanitise non-finite entries.
+// t-th tile of the upper triangle (ti <= tj < nt), row-major, in closed form: row r starts at
+// r nt - r (r - 1) / 2.
+__device__ __forceinline__ void upper_tile_closed(int t, int nt, int& ti, int& tj) {
+  const float b = 2.0f * nt + 1.0f;
+  int r = (int)((b - __builtin_sqrtf(b * b - 8.0f * (float)t)) * 0.5f);
+  r = max(0, min(r, nt - 1));
+  auto start = [nt](int q) { return q * nt - q * (q - 1) / 2; };
+  while (r > 0 && start(r) > t) --r;
+  while (r + 1 < nt && start(r + 1) <= t) ++r;
+  ti = r;
+  tj = r + (t - start(r));
+}
+
+// The same per element, on 64x64 upper tile pairs: a thread's 16 loads are issued together,
+// then the symmetrised values are written to the tile and, through LDS, to its mirror.  (Many
+// 32x32 workgroups with 4 elements per thread kept too few loads in flight: ~1.5 TB/s.)
+__global__ __launch_bounds__(256) void k_hessian_finalize64(float* __restrict__ H, int C, int nt,
+                                                            float h_div, float sal_scale,
+                                                            int apply_scale, int* nonfinite) {
+  __shared__ float tile[64][65];
   __shared__ int cnt;
   const int g = blockIdx.y;
   int ti, tj;
-  upper_tile(blockIdx.x, nt, ti, tj);
+  upper_tile_closed(blockIdx.x, nt, ti, tj);
   float* Hg = H + (int64_t)g * C * C;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;   // 64 x 4
   if (threadIdx.x == 0) cnt = 0;
-  for (int y = ty; y < 32; y += 8) {
-    const int i = ti * 32 + y, j = tj * 32 + tx;
-    float v = 0.0f;
-    if (i < C && j < C) v = Hg[(int64_t)i * C + j];
-    tile[y][tx] = v;
+  float v[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int i = ti * 64 + ty + 4 * k, j = tj * 64 + tx;
+    v[k] = (i < C && j < C) ? Hg[(int64_t)i * C + j] : 0.0f;
   }
-  __syncthreads();
   int local = 0;
-  for (int y = ty; y < 32; y += 8) {
-    const int i = ti * 32 + y, j = tj * 32 + tx;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int y = ty + 4 * k;
+    const int i = ti * 64 + y, j = tj * 64 + tx;
     if (i >= C || j >= C) continue;
     if (ti == tj && y > tx) continue;            // lower half of a diagonal tile: mirrored below
-    float v = tile[y][tx] / h_div;
-    if (apply_scale) v = v / sal_scale;
-    v = 0.5f * (v + v);                           // 0.5 * (H + H^T) on the symmetric value
-    if (!rq_isfinite(v)) {
-      v = 0.0f;
+    float val = v[k] / h_div;
+    if (apply_scale) val = val / sal_scale;
+    val = 0.5f * (val + val);                     // 0.5 * (H + H^T) on the symmetric value
+    if (!rq_isfinite(val)) {
+      val = 0.0f;
       local += (i == j) ? 1 : 2;
     }
-    Hg[(int64_t)i * C + j] = v;
-    tile[y][tx] = v;
+    Hg[(int64_t)i * C + j] = val;
+    tile[y][tx] = val;
   }
   __syncthreads();
-  // mirror: H[j][i] = H[i][j]; write rows of the transposed tile for coalescing
-  for (int y = ty; y < 32; y += 8) {
-    const int j = tj * 32 + y, i = ti * 32 + tx;   // element (j, i) takes tile[tx][y]
+  // mirror: H[j][i] = H[i][j]; rows of the transposed tile, for coalescing
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int y = ty + 4 * k;
+    const int j = tj * 64 + y, i = ti * 64 + tx;   // element (j, i) takes tile[tx][y]
     if (i >= C || j >= C) continue;
     if (ti == tj && tx >= y) continue;            // diagonal tile: only strictly lower
     Hg[(int64_t)j * C + i] = tile[tx][y];
@@ -1231,10 +1239,10 @@ extern "C" int rq_hessian_finalize(float* H, float* act_sq, int G, int C, double
                                    double sal_scale, double seq_len, int* nonfinite, void* stream) {
   if (!H || C <= 0 || G <= 0 || !(h_div > 0) || !(seq_len > 0)) return RQ_EINVAL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int nt = (C + 31) / 32;
+  const int nt = (C + 63) / 64;
   const int ntiles = nt * (nt + 1) / 2;
   // torch divides a float tensor by a Python scalar in float: a / (float)b (CPU kernel).
-  hipLaunchKernelGGL(k_hessian_finalize, dim3(ntiles, G), dim3(256), 0, s, H, C, nt, (float)h_div,
+  hipLaunchKernelGGL(k_hessian_finalize64, dim3(ntiles, G), dim3(256), 0, s, H, C, nt, (float)h_div,
                      (float)sal_scale, sal_scale != 1.0 ? 1 : 0, nonfinite);
   RQ_CHECK_LAUNCH();
   if (act_sq) {

@@ -220,6 +220,61 @@ __global__ __launch_bounds__(256) void k_gather_h(const float* __restrict__ Hg, 
   }
 }
 
+// P H P by rows: workgroup i stages source row perm[i] in LDS with 16-byte loads (the whole
+// row, C floats), then writes output row i coalesced, column j taking LDS word perm[j].
+// Each source row is read from HBM once; the column-gather kernel above re-read every source
+// row's cache lines once per 256-column workgroup.  Dynamic LDS: C * 4 bytes (112 KB at
+// C = 28672, one workgroup per CU), so there both loops keep GR_U loads per thread in flight;
+// small rows run unrolled once with 256 threads and several workgroups per CU instead.
+template <int GR_THREADS, int GR_U>
+__global__ __launch_bounds__(GR_THREADS) void k_gather_h_rows(const float* __restrict__ Hg, int C,
+                                                              const int64_t* __restrict__ perm,
+                                                              float* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) float row[];
+  const int i = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t pi = perm ? perm[i] : i;
+  const float* src = Hg + pi * C;
+  if ((C & 3) == 0) {
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    const int n4 = C / 4;
+    for (int q0 = tid; q0 < n4; q0 += GR_THREADS * GR_U) {
+      float4 v[GR_U];
+#pragma unroll
+      for (int u = 0; u < GR_U; ++u) {
+        const int q = q0 + u * GR_THREADS;
+        if (q < n4) v[u] = s4[q];
+      }
+#pragma unroll
+      for (int u = 0; u < GR_U; ++u) {
+        const int q = q0 + u * GR_THREADS;
+        if (q < n4) reinterpret_cast<float4*>(row)[q] = v[u];
+      }
+    }
+  } else {
+    for (int q = tid; q < C; q += GR_THREADS) row[q] = src[q];
+  }
+  __syncthreads();
+  float* dst = out + (int64_t)i * C;
+  for (int j0 = tid; j0 < C; j0 += GR_THREADS * GR_U) {
+    int pj[GR_U];
+#pragma unroll
+    for (int u = 0; u < GR_U; ++u) {
+      const int j = j0 + u * GR_THREADS;
+      pj[u] = (j < C) ? (perm ? (int)perm[j] : j) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < GR_U; ++u) {
+      const int j = j0 + u * GR_THREADS;
+      if (j < C) {
+        float v = row[pj[u]];
+        if (j == i && v == 0.0f) v = 1.0f;        // H_sub[dead, dead] = 1
+        dst[j] = v;
+      }
+    }
+  }
+}
+
 template <typename TQ>
 __global__ __launch_bounds__(256) void k_writeback(const int16_t* __restrict__ codes, int R, int C,
                                                    const int64_t* __restrict__ invperm, int qmode,
@@ -343,7 +398,18 @@ extern "C" int rq_prepare_subgroup(const void* w, int w_dtype, int64_t ldw, cons
     hipLaunchKernelGGL(k_gather_g, gw, block, 0, s, grad, ldg, R_s, C, perm, G_sub, ld_gsub);
     RQ_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(k_gather_h, dim3((C + 255) / 256, rows_grid(C)), block, 0, s, H_g, C, perm, H_sub);
+  const size_t row_bytes = (size_t)C * sizeof(float);
+  if (row_bytes <= 64 * 1024 ||
+      (row_bytes <= 160 * 1024 &&
+       hipFuncSetAttribute((const void*)k_gather_h_rows<512, 8>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                           (int)row_bytes) == hipSuccess)) {
+    if (C >= 8192)
+      hipLaunchKernelGGL((k_gather_h_rows<512, 8>), dim3(C), dim3(512), row_bytes, s, H_g, C, perm, H_sub);
+    else
+      hipLaunchKernelGGL((k_gather_h_rows<256, 1>), dim3(C), dim3(256), row_bytes, s, H_g, C, perm, H_sub);
+  } else {
+    hipLaunchKernelGGL(k_gather_h, dim3((C + 255) / 256, rows_grid(C)), block, 0, s, H_g, C, perm, H_sub);
+  }
   RQ_CHECK_LAUNCH();
   return RQ_OK;
 }

@@ -102,6 +102,20 @@ def test_hessian_tail_slices_match_whole_items(C, G):
     # were left zero by the first)
 
 
+@pytest.mark.parametrize("C,G", [(300, 2), (64, 1), (129, 3)])
+def test_finalize_exact_on_symmetric_input(C, G):
+    """On a symmetric H the reference's 0.5 * (H + H^T) is the identity, so finalize must equal
+    (H / h_div) / hessian_saliency_scale evaluated on the CPU bit for bit (ragged 64-tiles)."""
+    r = rng(C + G)
+    A = torch.from_numpy(r.standard_normal((G, C, C)).astype(np.float32))
+    Hs = A + A.transpose(1, 2)
+    H = Hs.to(DEV).contiguous()
+    act = torch.ones(C, device=DEV)
+    K.hessian_finalize(H, act, 3.0, 7.0, 2.0)
+    torch.cuda.synchronize()
+    assert torch.equal(H.cpu(), (Hs / 3.0) / 7.0)
+
+
 def test_finalize_sanitises_nonfinite():
     H = torch.eye(70, device=DEV).repeat(2, 1, 1)
     H[1, 3, 40] = float("nan")
