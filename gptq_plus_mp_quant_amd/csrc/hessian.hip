@@ -98,37 +98,6 @@ __device__ __forceinline__ void upper_tile_blocked(int t, int nt, int& ti, int& 
   }
 }
 
-// Item order of the split kernel: the off-diagonal tiles in the super-row order of
-// upper_tile_blocked, then the nt diagonal tiles.  A diagonal tile skips its lower row blocks
-// and costs ~60 % of an off-diagonal one, so it belongs at the end of the launch, where the
-// token-sliced tail lets the CUs that finish early share the remaining work.
-__device__ __forceinline__ void split_tile_order(int t, int nt, int& ti, int& tj) {
-  const int noff = nt * (nt - 1) / 2;
-  if (t >= noff) {
-    ti = tj = t - noff;
-    return;
-  }
-  int r0 = 0;
-  int rem = t;
-  for (;;) {
-    const int h = min(HSR, nt - r0);
-    const int ncol = nt - r0;
-    const int cnt = ((ncol >= h) ? (h * (h + 1) / 2 + (ncol - h) * h) : (ncol * (ncol + 1) / 2)) - h;
-    if (rem < cnt) break;
-    rem -= cnt;
-    r0 += h;
-  }
-  const int h = min(HSR, nt - r0);
-  for (int c = r0;; ++c) {
-    const int k = min(h, c - r0 + 1) - (c < r0 + h ? 1 : 0);   // rows r0 .. of column c, above the diagonal
-    if (rem < k) {
-      ti = r0 + rem;
-      tj = c;
-      return;
-    }
-    rem -= k;
-  }
-}
 
 
 // Partial tile of one token slice: 64 accumulator floats per thread, stored e-major so each
@@ -734,7 +703,7 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
   if (logical >= total) return;
   const int g = logical % ntarg;
   int ti, tj;
-  split_tile_order(logical / ntarg, nt, ti, tj);
+  upper_tile_blocked(logical / ntarg, nt, ti, tj);
   const int R0 = ti * XT, C0 = tj * XT;
   float* Hg = tg.H[g];
   const float* scl = scale + (int64_t)g * C;
