@@ -484,7 +484,7 @@ struct TwTile {
   }
 };
 
-__global__ __launch_bounds__(256) void k_trailing_w(TwArgs a) {
+__global__ __launch_bounds__(256, 2) void k_trailing_w(TwArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds0[TSTAGE];
   __shared__ __attribute__((aligned(16))) uint8_t lds1[TSTAGE];
   __shared__ __attribute__((aligned(16))) uint8_t lds2[TSTAGE];
@@ -536,6 +536,19 @@ __global__ __launch_bounds__(256) void k_trailing_w(TwArgs a) {
 #pragma unroll
     for (int e = 0; e < 32; ++e) w.acc[h][e] = 0.0f;
 
+  // This lane's 64 outputs of W (clamped in-bounds addresses), loaded before the staging so
+  // their latency overlaps the first stage's: output e of half h is wave row
+  // 32 (e / 16) + 8 ((e % 16) / 4) + 4 (lane / 32) + e % 4, wave column 32 h + lane % 32.
+  const int rw0 = rl0 + 64 * wr + 4 * (lane >> 5), cw0 = c0 + 64 * w.wc + (lane & 31);
+  float wv[2][32];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const int rl = min(rw0 + 32 * (e / 16) + 8 * ((e % 16) / 4) + (e % 4), a.R_s - 1);
+      wv[h][e] = a.Wp[(rbase + rl) * a.ldw + min(cw0 + 32 * h, a.C - 1)];
+    }
+
   static_assert(TSTAGES == 4, "unrolled stage schedule");
 #pragma unroll
   for (int s = 0; s < TSTAGES - 1; ++s) w.stage(L.s[s], min(s, w.nk - 1));
@@ -552,37 +565,17 @@ __global__ __launch_bounds__(256) void k_trailing_w(TwArgs a) {
   if (rem > 2) w.step<2, 1>(L, kt + 2);
   TWAIT_VM(0);   // no staging in flight when the workgroup ends
 
-  // Output e of half h: wave row 32 (e / 16) + 8 ((e % 16) / 4) + 4 (lane / 32) + e % 4, wave
-  // column 32 h + lane % 32.  Per group of 8 outputs the loads are issued together (clamped
-  // in-bounds addresses), then the stores.  W - tot, or W - f * tot (block_gd).
-  const int rw0 = rl0 + 64 * wr + 4 * (lane >> 5), cw0 = c0 + 64 * w.wc + (lane & 31);
+  // W - tot, or W - f * tot (block_gd), into the prefetched outputs.
   const bool full = (rl0 + TT <= a.R_s) && (c0 + TT <= a.C);
   const bool scaled = a.f != 1.0f;
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int e0 = 0; e0 < 32; e0 += 8) {
-      float wv[8];
-#pragma unroll
-      for (int e = e0; e < e0 + 8; ++e) {
-        const int rl = min(rw0 + 32 * (e / 16) + 8 * ((e % 16) / 4) + (e % 4), a.R_s - 1);
-        wv[e - e0] = a.Wp[(rbase + rl) * a.ldw + min(cw0 + 32 * h, a.C - 1)];
-      }
-      if (full) {   // interior tile: no per-element branches, so the stores wait once
-#pragma unroll
-        for (int e = e0; e < e0 + 8; ++e) {
-          const int rl = rw0 + 32 * (e / 16) + 8 * ((e % 16) / 4) + (e % 4), c = cw0 + 32 * h;
-          const float tot = w.acc[h][e];
-          a.Wp[(rbase + rl) * a.ldw + c] = wv[e - e0] - (scaled ? a.f * tot : tot);
-        }
-      } else {
-#pragma unroll
-        for (int e = e0; e < e0 + 8; ++e) {
-          const int rl = rw0 + 32 * (e / 16) + 8 * ((e % 16) / 4) + (e % 4), c = cw0 + 32 * h;
-          const float tot = w.acc[h][e];
-          if (rl < a.R_s && c < a.C) a.Wp[(rbase + rl) * a.ldw + c] = wv[e - e0] - (scaled ? a.f * tot : tot);
-        }
-      }
+    for (int e = 0; e < 32; ++e) {
+      const int rl = rw0 + 32 * (e / 16) + 8 * ((e % 16) / 4) + (e % 4), c = cw0 + 32 * h;
+      const float tot = w.acc[h][e];
+      const float v = wv[h][e] - (scaled ? a.f * tot : tot);
+      if (full || (rl < a.R_s && c < a.C)) a.Wp[(rbase + rl) * a.ldw + c] = v;
     }
 }
 
