@@ -20,7 +20,8 @@
 
 namespace {
 
-constexpr int NB = 64;     // diagonal block (factored and inverted by one wavefront)
+constexpr int NB = 64;     // diagonal block (factored and inverted by one workgroup)
+constexpr int CG = 4;      // columns factored per barrier in the diagonal block
 // Outer panel width: 256, or 512 from C = 8192 on.  The panel update re-reads and re-writes
 // its output tile once per panel, so wider panels halve that epilogue's share; the extra
 // in-panel work (C^2 NBW / 2 flops) stays ~1 % of the C^3 chain there.
@@ -115,12 +116,15 @@ __device__ __forceinline__ double quad_sum_f64(double v) {
 
 // Factor the nb x nb diagonal block of A at (k, k) and invert it; one workgroup of 4 waves per
 // batch entry (rows >= nb are identity padding).
-//  - Factor: lane r of wave w holds L[r][16w .. 16w+15] (16 registers).  Step j: the wave
-//    holding column j takes the pivot from lane j (readlane), forms 1/sqrt and sqrt, scales
-//    its column (L[r][j], zero for r <= j) and publishes it in `col` (two buffers, alternating
-//    by step, so one barrier per step orders each write after the previous reads); then every
-//    wave subtracts L[r][j] L[l][j] from its 16 columns l (col is zero at l <= j, so the
-//    finished columns stay as they are).
+//  - Factor: lane r of wave w holds L[r][16w .. 16w+15] (16 registers).  Columns go in groups
+//    of CG = 4, all held by one wave.  For each column j of the group that wave takes the pivot
+//    from lane j (readlane), forms 1/sqrt and sqrt, scales its column (L[r][j], zero for
+//    r <= j) and subtracts L[r][j] L[l][j] from the group's later columns l itself (L[l][j] by
+//    readlane); then it publishes the group's columns in `col` (two buffers, alternating by
+//    group, so one barrier per group orders each write after the previous reads), and every
+//    wave subtracts L[r][j] L[l][j], j in the group in order, from its other columns l (col is
+//    zero at l <= j, so finished columns stay as they are).  Every entry sees the same fused
+//    multiply-adds in the same order as with one column per barrier.
 //  - Inverse: lane quad c of the workgroup computes column c of T = L^-1 by forward
 //    substitution t[i] = (delta_ic - sum_{m<i} L[i][m] t[m]) / L[i][i]; lane q of the quad
 //    holds the rows m = 4p + q and its part of each dot product, and the quad adds the four
@@ -135,7 +139,7 @@ __global__ __launch_bounds__(CD_THREADS) void k_chol_diag(const double* __restri
                                                           int* info_all) {
   constexpr int LS = NB + 2;                        // LDS row stride (16-byte aligned rows)
   __shared__ __attribute__((aligned(16))) double S[NB * LS];
-  __shared__ __attribute__((aligned(16))) double col[2][NB];
+  __shared__ __attribute__((aligned(16))) double col[2][CG][NB];
   __shared__ double dinv[NB];   // 1 / L[j][j]; NaN marks a failed pivot
   const int b = blockIdx.x;
   int* info = info_all + b;
@@ -179,33 +183,54 @@ __global__ __launch_bounds__(CD_THREADS) void k_chol_diag(const double* __restri
 
   bool fail = false;
 #pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const int jw = j / 16, jq = j % 16;
-    double* cj = col[j & 1];
+  for (int g = 0; g < NB / CG; ++g) {
+    const int j0 = CG * g, jw = j0 / 16, jq0 = j0 % 16;
+    double (*cg)[NB] = col[g & 1];
     if (wave == jw) {
-      const double d = readlane_f64(a[jq], j);     // uniform pivot
-      double rd = 0.0, sq = 0.0;
-      const bool ok = d > 0.0 && rq_isfinite(d);
-      if (ok) rsqrt_newton(d, rd, sq);
-      const double lrj = (r > j) ? a[jq] * rd : 0.0;  // L[r][j]
-      a[jq] = (r == j) ? sq : lrj;
-      cj[r] = lrj;
-      if (r == 0) dinv[j] = ok ? rd : __builtin_nan("");
+#pragma unroll
+      for (int u = 0; u < CG; ++u) {
+        const int j = j0 + u, jq = jq0 + u;
+        const double d = readlane_f64(a[jq], j);     // uniform pivot
+        double rd = 0.0, sq = 0.0;
+        const bool ok = d > 0.0 && rq_isfinite(d);
+        if (ok) rsqrt_newton(d, rd, sq);
+        const double lrj = (r > j) ? a[jq] * rd : 0.0;  // L[r][j]
+        a[jq] = (r == j) ? sq : lrj;
+        cg[u][r] = lrj;
+        if (r == 0) dinv[j] = ok ? rd : __builtin_nan("");
+#pragma unroll
+        for (int v = u + 1; v < CG; ++v)                  // the group's later columns
+          a[jq0 + v] = __builtin_fma(-lrj, readlane_f64(lrj, j0 + v), a[jq0 + v]);
+      }
     }
     __syncthreads();
     // dinv[j] is written once, before this barrier: every wave reads the same verdict.  The
-    // column is read before the verdict is tested (the reads are in bounds either way).
-    const double dj = dinv[j];
-    const double m = cj[r];
-    double cv[16];
+    // columns are read before the verdict is tested (the reads are in bounds either way).
+    bool bad = false;
+    double m[CG], cv[CG][16];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) cv[q] = cj[c0 + q];
-    if (!(dj == dj)) {
+    for (int u = 0; u < CG; ++u) {
+      const double dj = dinv[j0 + u];
+      bad |= !(dj == dj);
+      m[u] = cg[u][r];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) cv[u][q] = cg[u][c0 + q];
+    }
+    if (bad) {
       fail = true;
       break;
     }
+    // q-major, so the next group's columns are done first; the group's own columns were
+    // updated by their wave above
 #pragma unroll
-    for (int q = 0; q < 16; ++q) a[q] = __builtin_fma(-m, cv[q], a[q]);
+    for (int q = 0; q < 16; ++q) {
+      const bool own = (q >= jq0 && q < jq0 + CG) && wave == jw;
+#pragma unroll
+      for (int u = 0; u < CG; ++u) {
+        const double nv = __builtin_fma(-m[u], cv[u][q], a[q]);
+        a[q] = own ? a[q] : nv;
+      }
+    }
   }
   if (fail) {
     if (tid == 0) atomicExch(info, 1);
