@@ -11,8 +11,8 @@
 // into the B operand as it is written (the reference's `weighted` = fl32(x * s) is never
 // materialised).  Products run on v_mfma_f32_32x32x2f32 with fp32 accumulation; each 64x64
 // quarter of the tile belongs to one wave (2x2 MFMA blocks of 32x32); four workgroups share a
-// CU (<= 128 VGPRs, 37 KB LDS each).  The diagonal tiles of group 0 also accumulate
-// act_square = sum_t x^2, read back from the staged slab by the first 128 threads.
+// CU (<= 128 VGPRs, 37 KB LDS each).  act_square is reduced by its own kernels (below), in
+// the order of the reference's CPU reduction.
 //
 // Tail balancing: the (tile, target) items of a launch run in rounds of (CUs x 4) workgroups;
 // when the last round would be partly empty, its items are split along the tokens into S
@@ -101,15 +101,14 @@ __device__ __forceinline__ void upper_tile_blocked(int t, int nt, int& ti, int& 
 
 
 // Partial tile of one token slice: 64 accumulator floats per thread, stored e-major so each
-// store instruction of the workgroup writes 1 KB contiguously, then 128 act_square partials.
-constexpr int HPART = HT * HT + HT;
+// store instruction of the workgroup writes 1 KB contiguously.
+constexpr int HPART = HT * HT;
 
 template <typename TX, bool EDGE>
 __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t ntok, int64_t ldx,
                                              int C, const float* __restrict__ sal, int64_t ld_sal,
-                                             float* __restrict__ Hg,
-                                             float* __restrict__ act_sq, int I0, int J0, bool diag,
-                                             bool want_act, float (*As)[HS], float (*Bs)[HS],
+                                             float* __restrict__ Hg, int I0, int J0, bool diag,
+                                             float (*As)[HS], float (*Bs)[HS],
                                              int64_t sbeg, int64_t send, float* __restrict__ part) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -125,7 +124,6 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-  float actr = 0.0f;                  // act_square partial of column I0 + tid (tid < 128)
 
   RawSide<TX> ra, rb;
   load_side<TX, EDGE>(X, ntok, ldx, C, sbeg * HKC + sk, I0 + sc, ra);
@@ -146,16 +144,6 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
       Bs[sc + e][sk] = xb * s;        // fl32(x * s): the reference's `weighted`
     }
     __syncthreads();
-    if (want_act && tid < HT) {       // diagonal tiles: sum_t x^2 from the staged slab
-#pragma unroll
-      for (int q = 0; q < HKC; q += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(&As[tid][q]);
-        actr += v.x * v.x;
-        actr += v.y * v.y;
-        actr += v.z * v.z;
-        actr += v.w * v.w;
-      }
-    }
     if (sidx + 1 < send) {            // next slab in flight while this one is multiplied
       load_side<TX, EDGE>(X, ntok, ldx, C, t + HKC, I0 + sc, ra);
       if (!diag) load_side<TX, EDGE>(X, ntok, ldx, C, t + HKC, J0 + sc, rb);
@@ -190,7 +178,6 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
       for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
         for (int e = 0; e < 16; ++e) part[(bi * 32 + bj * 16 + e) * HTHREADS + tid] = acc[bi][bj][e];
-    if (want_act && tid < HT) part[HT * HT + tid] = actr;
     return;
   }
 
@@ -208,8 +195,6 @@ __device__ __forceinline__ void hessian_tile(const TX* __restrict__ X, int64_t n
           *p = *p + acc[bi][bj][e];
         }
       }
-
-  if (want_act && tid < HT && I0 + tid < C) act_sq[I0 + tid] += actr;
 }
 
 // One output of a launch: the Hessian of one (module, saliency group) pair.  Modules that
@@ -223,10 +208,9 @@ struct HTargets {
   float* act[HMAXT];         // act_square output (one target per module) or nullptr
 };
 
-// The last slice of a split item adds the S partials (in slice order) to H and act_square.
+// The last slice of a split item adds the S partials (in slice order) to H.
 __device__ __forceinline__ void reduce_slices(const float* __restrict__ part0, int S, float* __restrict__ Hg,
-                                              float* __restrict__ act_sq, int I0, int J0, int C,
-                                              bool want_act) {
+                                              int I0, int J0, int C) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -250,13 +234,6 @@ __device__ __forceinline__ void reduce_slices(const float* __restrict__ part0, i
           *p = *p + sum;
         }
       }
-  if (want_act && tid < HT && I0 + tid < C) {
-    float sum = __hip_atomic_load(part0 + HT * HT + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int q = 1; q < S; ++q)
-      sum += __hip_atomic_load(part0 + (int64_t)q * HPART + HT * HT + tid, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    act_sq[I0 + tid] += sum;
-  }
 }
 
 template <typename TX>
@@ -294,18 +271,16 @@ __global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
   upper_tile_blocked(logical / ntarg, nt, ti, tj);
   const int I0 = ti * HT, J0 = tj * HT;
   const bool diag = (ti == tj);
-  float* act_sq = tg.act[g];
-  const bool want_act = diag && (act_sq != nullptr);
   float* Hg = tg.H[g];
   const bool interior = vec_ok && (J0 + HT <= C);   // I0 <= J0
   float* part0 = (slice >= 0) ? ws + (int64_t)(logical - full) * S * HPART : nullptr;
   float* part = part0 ? part0 + (int64_t)slice * HPART : nullptr;
   if (interior)
-    hessian_tile<TX, false>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], Hg, act_sq, I0, J0, diag,
-                            want_act, As, Bs, sbeg, send, part);
+    hessian_tile<TX, false>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], Hg, I0, J0, diag, As, Bs, sbeg,
+                            send, part);
   else
-    hessian_tile<TX, true>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], Hg, act_sq, I0, J0, diag,
-                           want_act, As, Bs, sbeg, send, part);
+    hessian_tile<TX, true>(X, ntok, ldx, C, tg.sal[g], tg.ld_sal[g], Hg, I0, J0, diag, As, Bs, sbeg,
+                           send, part);
   if (!part) return;
   // publish this slice, and let the last of the S slices sum them in slice order
   __threadfence();
@@ -319,7 +294,7 @@ __global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
   __syncthreads();
   if (!last_slice) return;
   __threadfence();
-  reduce_slices(part0, S, Hg, act_sq, I0, J0, C, want_act);
+  reduce_slices(part0, S, Hg, I0, J0, C);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -783,28 +758,37 @@ __global__ __launch_bounds__(256) void k_xprep(const TX* __restrict__ X, int64_t
           make_uint4(src[0], src[1], src[2], src[3]);
     }
   }
-  // column statistics: 4 threads per column, 64 tokens each in token order (square, then
-  // add), the four parts added in order
+  // column statistics: 4 threads per column, 64 tokens each.  The 256 tokens are one level-2
+  // block of the reference's CPU reduction of act_square (act_square_l2 below): each thread
+  // forms its four level-1 sums (16 tokens, square then add, from zero), and one thread per
+  // column adds the 16 level-1 sums in order.  Tokens past ntok are zero: they add nothing.
   {
-    __shared__ float qm[4][XPC], qa[4][XPC];
+    __shared__ float qm[4][XPC], ql1[16][XPC];
     const int cl = tid & (XPC - 1), part = tid >> 6;
-    float m = 0.0f, a = 0.0f;
-#pragma unroll 8
-    for (int w = part * (XTOK / 8); w < (part + 1) * (XTOK / 8); ++w) {
-      const uint32_t u = tile[cl][w];
-      const float v0 = XType<TX>::lo(u), v1 = XType<TX>::hi(u);
-      m = fmaxf(m, fabsf(v0));
-      a = a + v0 * v0;
-      m = fmaxf(m, fabsf(v1));
-      a = a + v1 * v1;
+    float m = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      float a = 0.0f;
+#pragma unroll
+      for (int w = part * (XTOK / 8) + 8 * b; w < part * (XTOK / 8) + 8 * b + 8; ++w) {
+        const uint32_t u = tile[cl][w];
+        const float v0 = XType<TX>::lo(u), v1 = XType<TX>::hi(u);
+        m = fmaxf(m, fabsf(v0));
+        a = a + v0 * v0;
+        m = fmaxf(m, fabsf(v1));
+        a = a + v1 * v1;
+      }
+      ql1[4 * part + b][cl] = a;
     }
     qm[part][cl] = m;
-    qa[part][cl] = a;
     if (tid < HMAXT) smx[tid] = 0u;
     __syncthreads();
     if (tid < XPC && c0 + tid < C) {
       mpart[(int64_t)ch * C + c0 + tid] = fmaxf(fmaxf(qm[0][tid], qm[1][tid]), fmaxf(qm[2][tid], qm[3][tid]));
-      apart[(int64_t)ch * C + c0 + tid] = ((qa[0][tid] + qa[1][tid]) + qa[2][tid]) + qa[3][tid];
+      float l2 = 0.0f;
+#pragma unroll
+      for (int b = 0; b < 16; ++b) l2 = l2 + ql1[b][tid];
+      apart[(int64_t)ch * C + c0 + tid] = l2;
     }
   }
   if (blockIdx.x != 0) return;
@@ -818,19 +802,16 @@ __global__ __launch_bounds__(256) void k_xprep(const TX* __restrict__ X, int64_t
   if (tid < ntarg) spart[(int64_t)ch * HMAXT + tid] = __uint_as_float(smx[tid]);
 }
 
-// Reduce the token blocks: act_square += sum_t x^2, and the per (target, column) scale 2^e
-// with e = 15 - E for max|x_c| * max|s_g| = f * 2^E, f in [0.5, 1).  A workgroup takes 32
-// columns; 8 threads per column each reduce one eighth of the blocks (in block order), and the
-// eight parts are added in a fixed order, so the sum is deterministic.  Every workgroup also
-// forms max|s_g| over all blocks (exact in any order).
+// Reduce the token blocks' maxima into the per (target, column) scale 2^e with e = 15 - E for
+// max|x_c| * max|s_g| = f * 2^E, f in [0.5, 1).  A workgroup takes 32 columns; 8 threads per
+// column each take one eighth of the blocks (maxima are exact in any order).  act_square is
+// finished by k_act_finish.
 constexpr int XF_COLS = 32;
 constexpr int XF_SEG = 8;
-__global__ __launch_bounds__(256) void k_xfinish(int C, int nchunk, HTargets tg, int ntarg,
-                                                 const float* __restrict__ mpart,
-                                                 const float* __restrict__ apart,
+__global__ __launch_bounds__(256) void k_xfinish(int C, int nchunk, int ntarg, const float* __restrict__ mpart,
                                                  const float* __restrict__ spart, float* __restrict__ scale) {
   __shared__ float smax[XF_SEG][HMAXT];
-  __shared__ float pm[XF_SEG][XF_COLS], pa[XF_SEG][XF_COLS];
+  __shared__ float pm[XF_SEG][XF_COLS];
   const int t = threadIdx.x;
   const int lane32 = t & 31, seg = t >> 5;
   {
@@ -841,26 +822,17 @@ __global__ __launch_bounds__(256) void k_xfinish(int C, int nchunk, HTargets tg,
   }
   const int c = blockIdx.x * XF_COLS + lane32;
   const int ch0 = (int)((int64_t)nchunk * seg / XF_SEG), ch1 = (int)((int64_t)nchunk * (seg + 1) / XF_SEG);
-  float m = 0.0f, a = 0.0f;
+  float m = 0.0f;
   if (c < C) {
 #pragma unroll 8
-    for (int ch = ch0; ch < ch1; ++ch) {
-      m = fmaxf(m, mpart[(int64_t)ch * C + c]);
-      a = a + apart[(int64_t)ch * C + c];
-    }
+    for (int ch = ch0; ch < ch1; ++ch) m = fmaxf(m, mpart[(int64_t)ch * C + c]);
   }
   pm[seg][lane32] = m;
-  pa[seg][lane32] = a;
   __syncthreads();
   if (seg != 0 || c >= C) return;
-  float mt = pm[0][lane32], at = pa[0][lane32];
+  float mt = pm[0][lane32];
 #pragma unroll
-  for (int q = 1; q < XF_SEG; ++q) {
-    mt = fmaxf(mt, pm[q][lane32]);
-    at = at + pa[q][lane32];
-  }
-  for (int g = 0; g < ntarg; ++g)
-    if (tg.act[g]) tg.act[g][c] += at;
+  for (int q = 1; q < XF_SEG; ++q) mt = fmaxf(mt, pm[q][lane32]);
   for (int g = 0; g < ntarg; ++g) {
     float sm = smax[0][g];
 #pragma unroll
@@ -875,6 +847,160 @@ __global__ __launch_bounds__(256) void k_xfinish(int C, int nchunk, HTargets tg,
     }
     scale[(int64_t)g * C + c] = ldexpf(1.0f, e);
   }
+}
+
+// ---------------------------------------------------------------------------------------------
+// act_square += sum_t x_t^2 of one add_batch call (gptq_plus_utils.py:856:
+// `self.act_square.add_((inp ** 2).sum(0))` on the fp32 chunk), summed in the order of the
+// CPU reduction that line runs, so that act_order's argsort (:1046) sees the reference's values
+// bit for bit (near ties would otherwise swap columns).  That reduction (ATen's cascade sum of
+// a row-major [n, C] fp32 tensor over its rows) forms each column's sum over a sequence of
+// `count` elements in four levels.  With p = max(4, ceil(log2 count) / 4) and step = 2^p:
+// level 1 adds `step` consecutive elements from zero, level 2 adds `step` level-1 sums from
+// zero, level 3 adds `step` level-2 sums from zero, and level 4 adds every complete level-3
+// sum in order.  The partial sums an incomplete block leaves at levels 1-3 (a1, a2, a3) and
+// the level-4 sum a4 give ((a1 + a2) + a3) + a4.  Columns [0, 32 floor(C / 32)) (ATen's
+// four-vector inner loop) are one sequence of the n rows each.  The other columns are reduced
+// as four interleaved sequences, rows m, m + 4, m + 8, ... (n / 4 elements each, m < 4), the
+// n mod 4 leftover rows added to the first, then ((s0 + s1) + s2) + s3.  (For C mod 32 in
+// [4, 8) ATen reduces the first four of those columns either way, depending on n.)
+//
+// Work is split over "virtual columns": v = c for the first region (one lane), and
+// v = 4 (c - c_lo) + m for the interleaved region (four lanes).  k_act_l2 writes the level-2
+// sums (block b of step^2 elements, zero past the end, which adds nothing), k_act_finish
+// chains them per column and adds the result to every target's act_square.  For the usual
+// p = 4 the level-2 blocks of the first region are the 256-token blocks of k_xprep, which
+// writes them as it passes over the chunk.
+__host__ __device__ inline int act_level_power(int64_t count) {
+  int cl = 0;
+  while (cl < 62 && ((int64_t)1 << cl) < count) ++cl;     // ceil(log2 count); 0 for count <= 1
+  return cl / 4 > 4 ? cl / 4 : 4;
+}
+constexpr int ACT_MAXP = 6;                                 // step <= 64: count < 2^28
+
+template <typename TX>
+__device__ __forceinline__ float act_sq_elem(const TX* __restrict__ X, int64_t ldx, int64_t row, int c) {
+  const float v = rq_load_elem(X + row * ldx + c);
+  return v * v;
+}
+
+template <typename TX>
+__global__ __launch_bounds__(256) void k_act_l2(const TX* __restrict__ X, int64_t ldx, int c_lo, int V, int lanes,
+                                                int64_t count, int lp, float* __restrict__ out, int64_t ldo) {
+  __shared__ float l1s[1 << ACT_MAXP][64];
+  const int tid = threadIdx.x;
+  const int vl = tid & 63, part = tid >> 6;
+  const int v = blockIdx.x * 64 + vl;
+  const int step = 1 << lp;
+  const int64_t base = (int64_t)blockIdx.y << (2 * lp);
+  if (v < V) {
+    const int c = c_lo + v / lanes, m = v % lanes;
+    for (int k = part; k < step; k += 4) {
+      const int64_t i0 = base + (int64_t)k * step;
+      float s = 0.0f;
+      if (i0 + step <= count) {
+#pragma unroll 16
+        for (int j = 0; j < step; ++j) s = s + act_sq_elem(X, ldx, m + (i0 + j) * lanes, c);
+      } else {
+        for (int j = 0; j < step; ++j)
+          if (i0 + j < count) s = s + act_sq_elem(X, ldx, m + (i0 + j) * lanes, c);
+      }
+      l1s[k][vl] = s;
+    }
+  }
+  __syncthreads();
+  if (part != 0 || v >= V) return;
+  float l2 = 0.0f;
+  for (int k = 0; k < step; ++k) l2 = l2 + l1s[k][vl];
+  out[blockIdx.y * ldo + v] = l2;
+}
+
+// Levels 3 and 4 over the level-2 sums of virtual column v (in[b * ldi + v]).
+__device__ __forceinline__ float act_chain(const float* __restrict__ in, int64_t ldi, int v, int64_t count, int lp) {
+  const int64_t step = (int64_t)1 << lp;
+  const int64_t nfull = count >> (2 * lp);
+  const bool partial = (count & ((step << lp) - 1)) != 0;
+  float a4 = 0.0f;
+  int64_t j = 0;
+  for (; j + step <= nfull; j += step) {
+    float a3 = 0.0f;
+    for (int64_t k = 0; k < step; ++k) a3 = a3 + in[(j + k) * ldi + v];
+    a4 = a4 + a3;
+  }
+  float a3 = 0.0f;
+  for (; j < nfull; ++j) a3 = a3 + in[j * ldi + v];
+  const float a12 = partial ? in[nfull * ldi + v] : 0.0f;   // a1 + a2 of the incomplete block
+  return (a12 + a3) + a4;
+}
+
+template <typename TX>
+__device__ __forceinline__ void act_add(const HTargets& tg, int ntarg, int c, float v) {
+  for (int g = 0; g < ntarg; ++g)
+    if (tg.act[g]) tg.act[g][c] = tg.act[g][c] + v;
+}
+
+template <typename TX>
+__global__ __launch_bounds__(256) void k_act_finish(const float* __restrict__ in, int64_t ldi, int c_lo, int ncol,
+                                                    int lanes, int64_t count, int lp, const TX* __restrict__ X,
+                                                    int64_t ldx, int64_t ntok, HTargets tg, int ntarg) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= ncol) return;
+  const int c = c_lo + idx;
+  float r;
+  if (lanes == 1) {
+    r = act_chain(in, ldi, idx, count, lp);
+  } else {
+    float s0 = act_chain(in, ldi, 4 * idx, count, lp);
+    for (int64_t t = 4 * count; t < ntok; ++t) s0 = s0 + act_sq_elem(X, ldx, t, c);
+    const float s1 = act_chain(in, ldi, 4 * idx + 1, count, lp);
+    const float s2 = act_chain(in, ldi, 4 * idx + 2, count, lp);
+    const float s3 = act_chain(in, ldi, 4 * idx + 3, count, lp);
+    r = ((s0 + s1) + s2) + s3;
+  }
+  act_add<TX>(tg, ntarg, c, r);
+}
+
+// The same reduction without workspace: one thread per column walks its sequence(s) with the
+// four running partial sums (slow; used only when the caller gives no workspace).
+template <typename TX>
+__device__ float act_cascade_seq(const TX* __restrict__ X, int64_t ldx, int c, int m, int lanes, int64_t count) {
+  const int lp = act_level_power(count);
+  const int64_t step = (int64_t)1 << lp, mask = step - 1;
+  float a1 = 0.0f, a2 = 0.0f, a3 = 0.0f, a4 = 0.0f;
+  int64_t i = 0;
+  while (i + step <= count) {
+    for (int64_t j = 0; j < step; ++j, ++i) a1 = a1 + act_sq_elem(X, ldx, m + i * lanes, c);
+    a2 = a2 + a1;
+    a1 = 0.0f;
+    if ((i & (mask << lp)) != 0) continue;
+    a3 = a3 + a2;
+    a2 = 0.0f;
+    if ((i & (mask << (2 * lp))) != 0) continue;
+    a4 = a4 + a3;
+    a3 = 0.0f;
+  }
+  for (; i < count; ++i) a1 = a1 + act_sq_elem(X, ldx, m + i * lanes, c);
+  return ((a1 + a2) + a3) + a4;
+}
+
+template <typename TX>
+__global__ __launch_bounds__(256) void k_act_direct(const TX* __restrict__ X, int64_t ntok, int64_t ldx, int C,
+                                                    int ca, HTargets tg, int ntarg) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  float r;
+  if (c < ca) {
+    r = act_cascade_seq(X, ldx, c, 0, 1, ntok);
+  } else {
+    const int64_t k = ntok / 4;
+    float s0 = act_cascade_seq(X, ldx, c, 0, 4, k);
+    for (int64_t t = 4 * k; t < ntok; ++t) s0 = s0 + act_sq_elem(X, ldx, t, c);
+    const float s1 = act_cascade_seq(X, ldx, c, 1, 4, k);
+    const float s2 = act_cascade_seq(X, ldx, c, 2, 4, k);
+    const float s3 = act_cascade_seq(X, ldx, c, 3, 4, k);
+    r = ((s0 + s1) + s2) + s3;
+  }
+  act_add<TX>(tg, ntarg, c, r);
 }
 }  // namespace
 
@@ -1004,15 +1130,94 @@ int64_t align256(int64_t b) { return ((b + 255) / 256) * 256; }
 
 // Workspace layout: one int counter per possible tail item at a fixed place (the start, sized
 // for the larger slot count of the two kernels), so launches with different tails and either
-// kernel can share one workspace, then the partial tiles, then (split kernel) the X pass.
+// kernel can share one workspace; then the act_square level-2 sums; then the partial tiles;
+// then (split kernel) the X pass.
 int64_t hessian_cnt_bytes() {
   const int a = hessian_slots(), b = split_slots();
   return align256((int64_t)(a > b ? a : b) * 4);
 }
 
-int64_t hessian_ws_bytes(int64_t tail, int S) {
-  if (tail <= 0) return 0;
-  return hessian_cnt_bytes() + tail * S * (int64_t)HPART * 4;
+// act_square regions of a call: the one-sequence columns [0, ca) and the interleaved columns
+// [ca, C) (four sequences each).
+struct ActPlan {
+  int ca;
+  int lp_main, lp_tail;
+  int64_t nl2_main, nl2_tail, off_tail, bytes;
+};
+
+ActPlan act_plan(int64_t ntok, int C) {
+  ActPlan P;
+  P.ca = (C / 32) * 32;
+  P.lp_main = act_level_power(ntok);
+  P.lp_tail = act_level_power(ntok / 4);
+  P.nl2_main = (ntok + ((int64_t)1 << (2 * P.lp_main)) - 1) >> (2 * P.lp_main);
+  P.nl2_tail = (ntok / 4 + ((int64_t)1 << (2 * P.lp_tail)) - 1) >> (2 * P.lp_tail);
+  P.off_tail = align256(P.nl2_main * P.ca * 4);
+  P.bytes = P.off_tail + align256(P.nl2_tail * 4 * (int64_t)(C - P.ca) * 4);
+  return P;
+}
+
+int64_t act_off() { return hessian_cnt_bytes(); }
+
+// fp32-MFMA kernel: counters, act_square sums, then the tail slices' partial tiles.
+int64_t hessian_ws_bytes(int64_t ntok, int C, int64_t tail, int S) {
+  return act_off() + act_plan(ntok, C).bytes + (tail > 0 ? tail * S * (int64_t)HPART * 4 : 0);
+}
+
+// act_square of one call into every target's act pointer (no-op when none has one).
+// l2_main: the first region's level-2 sums already written by k_xprep (row stride C; only
+// valid for lp_main == 4), else nullptr.  ws_act: the act region of the workspace, or nullptr
+// (then the slow one-pass kernel runs).
+template <typename TX>
+int launch_act_square_t(const TX* x, int64_t ntok, int64_t ldx, int C, const HTargets& tg, int ntarg,
+                        const float* l2_main, char* ws_act, hipStream_t s) {
+  bool any = false;
+  for (int g = 0; g < ntarg; ++g) any = any || tg.act[g];
+  if (!any || ntok <= 0) return RQ_OK;
+  const ActPlan P = act_plan(ntok, C);
+  if (P.lp_main > ACT_MAXP) return RQ_EINVAL;
+  if (!ws_act) {
+    hipLaunchKernelGGL(k_act_direct<TX>, dim3((C + 255) / 256), dim3(256), 0, s, x, ntok, ldx, C, P.ca, tg, ntarg);
+    RQ_CHECK_LAUNCH();
+    return RQ_OK;
+  }
+  if (P.ca > 0) {
+    const float* l2 = l2_main;
+    int64_t ld = C;
+    if (!l2 || P.lp_main != 4) {
+      float* out = reinterpret_cast<float*>(ws_act);
+      hipLaunchKernelGGL(k_act_l2<TX>, dim3((P.ca + 63) / 64, (unsigned)P.nl2_main), dim3(256), 0, s, x, ldx, 0,
+                         P.ca, 1, ntok, P.lp_main, out, (int64_t)P.ca);
+      RQ_CHECK_LAUNCH();
+      l2 = out;
+      ld = P.ca;
+    }
+    hipLaunchKernelGGL(k_act_finish<TX>, dim3((P.ca + 255) / 256), dim3(256), 0, s, l2, ld, 0, P.ca, 1, ntok,
+                       P.lp_main, x, ldx, ntok, tg, ntarg);
+    RQ_CHECK_LAUNCH();
+  }
+  if (P.ca < C) {
+    const int nc = C - P.ca, V = 4 * nc;
+    float* out = reinterpret_cast<float*>(ws_act + P.off_tail);
+    if (P.nl2_tail > 0) {
+      hipLaunchKernelGGL(k_act_l2<TX>, dim3((V + 63) / 64, (unsigned)P.nl2_tail), dim3(256), 0, s, x, ldx, P.ca,
+                         V, 4, ntok / 4, P.lp_tail, out, (int64_t)V);
+      RQ_CHECK_LAUNCH();
+    }
+    hipLaunchKernelGGL(k_act_finish<TX>, dim3((nc + 255) / 256), dim3(256), 0, s, out, (int64_t)V, P.ca, nc, 4,
+                       ntok / 4, P.lp_tail, x, ldx, ntok, tg, ntarg);
+    RQ_CHECK_LAUNCH();
+  }
+  return RQ_OK;
+}
+
+int launch_act_square(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, const HTargets& tg, int ntarg,
+                      const float* l2_main, char* ws_act, hipStream_t s) {
+  if (x_dtype == RQ_F16)
+    return launch_act_square_t(static_cast<const __half*>(x), ntok, ldx, C, tg, ntarg, l2_main, ws_act, s);
+  if (x_dtype == RQ_BF16)
+    return launch_act_square_t(static_cast<const __hip_bfloat16*>(x), ntok, ldx, C, tg, ntarg, l2_main, ws_act, s);
+  return launch_act_square_t(static_cast<const float*>(x), ntok, ldx, C, tg, ntarg, l2_main, ws_act, s);
 }
 
 struct SplitLayout {
@@ -1023,7 +1228,7 @@ SplitLayout split_layout(int64_t ntok, int C, int ntarg, int64_t tail, int S) {
   SplitLayout L;
   L.ntok_p = ((ntok + XTOK - 1) / XTOK) * XTOK;
   L.nchunk = L.ntok_p / XTOK;
-  L.off_part = hessian_cnt_bytes();
+  L.off_part = act_off() + act_plan(ntok, C).bytes;
   L.off_xt = L.off_part + align256(tail * S * (int64_t)XPART * 4);
   L.off_st = L.off_xt + align256((int64_t)((C + 31) / 32) * 32 * L.ntok_p * 2);
   L.off_m = L.off_st + align256((int64_t)ntarg * L.ntok_p * 4);
@@ -1083,9 +1288,12 @@ int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, c
     hipLaunchKernelGGL(k_xprep<__hip_bfloat16>, pgrid, dim3(256), 0, s, (const __hip_bfloat16*)x, ntok, ldx,
                        C, vec_ok, xt, nks, tg, ntarg, sT, L.ntok_p, mpart, apart, spart);
   RQ_CHECK_LAUNCH();
-  hipLaunchKernelGGL(k_xfinish, fgrid, dim3(256), 0, s, C, (int)L.nchunk, tg, ntarg, mpart, apart, spart,
-                     scale);
+  hipLaunchKernelGGL(k_xfinish, fgrid, dim3(256), 0, s, C, (int)L.nchunk, ntarg, mpart, spart, scale);
   RQ_CHECK_LAUNCH();
+  {
+    const int rc = launch_act_square(x, x_dtype, ntok, ldx, C, tg, ntarg, apart, wb + act_off(), s);
+    if (rc) return rc;
+  }
   const int full = (int)(total - tail);
   int* cnt = tail > 0 ? reinterpret_cast<int*>(ws) : nullptr;
   float* wsf = tail > 0 ? reinterpret_cast<float*>(wb + L.off_part) : nullptr;
@@ -1112,15 +1320,21 @@ int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
   if (total > 0x7fffffff / 8) return RQ_EINVAL;
   const size_t esz = (x_dtype == RQ_F32) ? 4 : 2;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (((size_t)ldx * esz) % 16 == 0);
+  const bool have_act_ws = aligned && ws_bytes >= hessian_ws_bytes(ntok, C, 0, 1);
+  {
+    const int rc = launch_act_square(x, x_dtype, ntok, ldx, C, tg, ntarg, nullptr,
+                                     have_act_ws ? reinterpret_cast<char*>(ws) + act_off() : nullptr, s);
+    if (rc) return rc;
+  }
   int tail = 0, S = 1;
   if (aligned) tail_split(total, (ntok + HKC - 1) / HKC, hessian_slots(), &tail, &S);
-  if (tail > 0 && ws_bytes < hessian_ws_bytes(tail, S)) {
+  if (tail > 0 && ws_bytes < hessian_ws_bytes(ntok, C, tail, S)) {
     tail = 0;                                     // no room: whole items only
     S = 1;
   }
   const int full = (int)(total - tail);
   int* cnt = tail > 0 ? reinterpret_cast<int*>(ws) : nullptr;
-  float* wsf = tail > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + hessian_cnt_bytes())
+  float* wsf = tail > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + act_off() + act_plan(ntok, C).bytes)
                         : nullptr;
   dim3 grid((unsigned)(full + (int64_t)tail * S)), block(HTHREADS);
   if (x_dtype == RQ_F16)
@@ -1152,7 +1366,7 @@ extern "C" int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets)
     const int n = (ntargets - t0 < HMAXT) ? (ntargets - t0) : HMAXT;
     int tail = 0, S = 1;
     tail_split((int64_t)nt * (nt + 1) / 2 * n, (ntok + HKC - 1) / HKC, hessian_slots(), &tail, &S);
-    int64_t b = hessian_ws_bytes(tail, S);
+    int64_t b = hessian_ws_bytes(ntok, C, tail, S);
     const int64_t bs = split_ws_need(ntok, C, n);
     if (bs > b) b = bs;
     if (b > need) need = b;

@@ -1,7 +1,6 @@
-// Quantizer parameters, act_order permutation, per-subgroup gathers and the final write-back.
+// Quantizer parameters, per-subgroup gathers and the final write-back.
 //  - rq_find_params:      WeightQuantizer.find_params, per-channel min/max (utils/quant_utils.py:390-421),
 //                         also per static column group (gptq_utils/gptq_plus_utils.py:994-1002)
-//  - rq_act_order_perm:   argsort(act_square, descending) + argsort(perm) (gptq_plus_utils.py:1046-1050)
 //  - rq_prepare_subgroup: row slice, dead columns, act_order gathers of W, G and H (:1033-1050)
 //  - rq_writeback:        un-permute, dequantize, cast to the layer dtype, export buffers (:1850-1896)
 // All of these are HBM-bound gathers / reductions.
@@ -137,51 +136,6 @@ __global__ __launch_bounds__(256) void k_find_params_mse(const TW* __restrict__ 
     scale[(int64_t)grp * R + r] = bscale;
     zero[(int64_t)grp * R + r] = bzero;
   }
-}
-
-// a sorts strictly before b in a descending sort with NaN first (torch orders NaN as largest).
-__device__ __forceinline__ bool desc_before(float a, float b) {
-  const bool na = (a != a), nb = (b != b);
-  if (na) return !nb;
-  if (nb) return false;
-  return a > b;
-}
-__device__ __forceinline__ bool same_key(float a, float b) {
-  return ((a != a) && (b != b)) || (a == b);
-}
-
-// Stable descending rank sort: rank_i = #{j : key_j before key_i, or tie and j < i}.
-// Workgroup (x, y) counts, for the 64 keys i of chunk x (one per lane), the keys j of slice y
-// that come before them; its 4 waves take interleaved quarters of the slice and add their
-// counts in LDS, then one 64-bit atomic per key adds the slice's count into invperm (which
-// k_fill_i64 zeroed; integer sums do not depend on the order).  k_scatter_perm then writes perm.
-constexpr int RK_SLICE = 1024;
-__global__ void k_fill_i64(int64_t* __restrict__ p, int n) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
-__global__ __launch_bounds__(256) void k_rank_desc(const float* __restrict__ key, int C,
-                                                   int64_t* __restrict__ rank) {
-  __shared__ int part[4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int i = blockIdx.x * 64 + lane;
-  const float ki = (i < C) ? key[i] : 0.0f;
-  const int j0 = blockIdx.y * RK_SLICE, j1 = min(j0 + RK_SLICE, C);
-  int cnt = 0;
-  for (int j = j0 + wave; j < j1; j += 4) {
-    const float kj = key[j];
-    cnt += (desc_before(kj, ki) || (same_key(kj, ki) && j < i)) ? 1 : 0;
-  }
-  part[wave][lane] = cnt;
-  __syncthreads();
-  if (wave == 0 && i < C) {
-    const int tot = part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane];
-    if (tot) atomicAdd(reinterpret_cast<unsigned long long*>(rank + i), (unsigned long long)tot);
-  }
-}
-__global__ void k_scatter_perm(const int64_t* __restrict__ invperm, int C, int64_t* __restrict__ perm) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < C) perm[invperm[i]] = i;
 }
 
 template <typename TW>
@@ -358,18 +312,6 @@ extern "C" int rq_find_params_mse(const void* w, int w_dtype, int R, int C, int6
                        (float)maxq, sym, (float)norm, grid, steps, scale, zero);
   else
     return RQ_EINVAL;
-  RQ_CHECK_LAUNCH();
-  return RQ_OK;
-}
-
-extern "C" int rq_act_order_perm(const float* act_sq, int C, int64_t* perm, int64_t* invperm,
-                                 void* stream) {
-  if (!act_sq || !perm || !invperm || C <= 0) return RQ_EINVAL;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(k_fill_i64, dim3((C + 255) / 256), dim3(256), 0, s, invperm, C);
-  hipLaunchKernelGGL(k_rank_desc, dim3((C + 63) / 64, (C + RK_SLICE - 1) / RK_SLICE), dim3(256), 0, s,
-                     act_sq, C, invperm);
-  hipLaunchKernelGGL(k_scatter_perm, dim3((C + 255) / 256), dim3(256), 0, s, invperm, C, perm);
   RQ_CHECK_LAUNCH();
   return RQ_OK;
 }

@@ -44,7 +44,9 @@ int rq_version(void);
 /* GPTQPlus.add_batch -- gptq_utils/gptq_plus_utils.py:798-857.
  * H[g] (C x C, fp32, g < G) += X^T diag(sal[:, g]) X over `ntok` tokens, upper-triangle
  * 128x128 tiles only (the lower triangle is filled by rq_hessian_finalize);
- * act_sq[c] += sum_t x[t,c]^2.  X is [ntok, C] (row stride ldx) of type x_dtype,
+ * act_sq[c] += sum_t x[t,c]^2 (act_sq may be NULL), summed in the order of torch's CPU
+ * `(x.float() ** 2).sum(0)` (:856), so the result is the reference's bit for bit.
+ * X is [ntok, C] (row stride ldx) of type x_dtype,
  * sal is [ntok, G] fp32 (row stride ld_sal).  fp32 products accumulated in fp32
  * (rq_hessian_math), deterministic (bitwise reproducible).  workspace (optional, device, 256-byte aligned, zero-filled when first
  * allocated; the library leaves it reusable): with at least rq_hessian_workspace_bytes
@@ -99,9 +101,10 @@ int rq_find_params_mse(const void* w, int w_dtype, int R, int C, int64_t ldw, in
                        int maxq, int sym, double norm, int grid, double maxshrink, float* scale,
                        float* zero, void* stream);
 
-/* act_order permutation -- gptq_plus_utils.py:1046, 1050:
- * perm = argsort(act_sq, descending) with ties broken by ascending index (NaN first),
- * invperm = argsort(perm).  int64 outputs. */
+/* act_order permutation -- gptq_plus_utils.py:1046, 1050 (classic GPTQ: argsort of diag(H)):
+ * perm = torch.argsort(act_sq, descending=True) exactly as torch returns it on the CPU, ties
+ * included (the order libstdc++'s introsort leaves equal keys in; NaN first), and
+ * invperm = argsort(perm).  int64 outputs.  C <= 65536. */
 int rq_act_order_perm(const float* act_sq, int C, int64_t* perm, int64_t* invperm, void* stream);
 
 /* Per-subgroup slicing, dead columns and act_order gather -- gptq_plus_utils.py:1033-1050.

@@ -13,7 +13,6 @@ Follows ``gptq_utils/gptq_utils.py:23-180`` op for op on CPU tensors:
   group start, the trailing update, un-permute.  The quantizer left on the object is the one
   the reference leaves (the last dynamic fit, or the last static group used).
 
-``stable_ties`` (opt-in) makes the act_order argsort stable, like the GPU kernel.
 Pinned by golden vectors from the reference class itself (``tests/golden/make_golden.py``).
 """
 from __future__ import annotations
@@ -49,7 +48,7 @@ class GPTQOracle:
 
     # gptq_utils.py:45-171
     def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
-                    static_groups=False, stable_ties=False) -> FasterquantResult:
+                    static_groups=False) -> FasterquantResult:
         W = self.weight.clone().float()
         Scale = W.clone()
         W_int = W.clone()
@@ -71,10 +70,11 @@ class GPTQOracle:
                 groups.append(q)
         perm = invperm = None
         if actorder:
-            perm = torch.argsort(torch.diag(H), descending=True, stable=stable_ties)
+            perm = torch.argsort(torch.diag(H), descending=True)
             W = W[:, perm]
             H = H[perm][:, perm]
             invperm = torch.argsort(perm)
+        self.perm = perm
         Q = torch.zeros_like(W)
         damp_percent = percdamp
         while 1 > damp_percent > 0:

@@ -21,13 +21,8 @@ It restates, op for op and in the same torch call order on CPU tensors, the refe
   column loop, the block-atomic variant, the trailing (outer) update, un-permute and
   write-back -- ``gptq_plus_utils.py:910-1396, 1500-1570, 1850-1896``.
 
-Deviations, all opt-in:
-
-* ``dtype`` lets the same sequence run in float64 (used by the closed-form pinning tests).
-* ``stable_ties=True`` replaces ``torch.argsort(act_square, descending=True)`` (unstable on
-  exact ties on CPU) by its stable variant.  Among exactly tied ``act_square`` values the
-  reference's order is implementation-defined; the stable order (ties by ascending column
-  index) is one of the orders that call may return and is the one the HIP kernel uses.
+One deviation, opt-in: ``dtype`` lets the same sequence run in float64 (used by the
+closed-form pinning tests).
 
 Parity pinning (see ``tests/test_oracle_*.py``): golden vectors written by importing the
 reference (``tests/golden/make_golden.py``), fp64 brute-force Hessians, scipy fp64
@@ -423,7 +418,9 @@ class GPTQPlusOracle:
 
     # gptq_plus_utils.py:798-857
     @torch.no_grad()
-    def add_batch(self, inp, out=None):
+    def add_batch(self, inp, out=None, hessian=True):
+        """``hessian=False`` (test option) skips the H product and keeps everything else, for
+        full-size checks that take H from elsewhere."""
         if self._finalized:
             raise RuntimeError("add_batch called after finalize_hessian. Re-init GPTQPlus to reuse.")
         if inp.dim() == 2:
@@ -437,9 +434,10 @@ class GPTQPlusOracle:
         inp = inp.reshape(-1, inp.shape[-1]).to(self.dtype)
         sal = sal.reshape(-1, sal.shape[-1]).to(self.dtype)
         n_tokens = inp.shape[0]
-        weighted = inp.unsqueeze(0).mul(sal.transpose(0, 1).unsqueeze(-1))
-        block = torch.bmm(inp.transpose(0, 1).unsqueeze(0).expand(self.num_groups, -1, -1), weighted)
-        self.H.add_(block)
+        if hessian:
+            weighted = inp.unsqueeze(0).mul(sal.transpose(0, 1).unsqueeze(-1))
+            block = torch.bmm(inp.transpose(0, 1).unsqueeze(0).expand(self.num_groups, -1, -1), weighted)
+            self.H.add_(block)
         self.act_square.add_((inp ** 2).sum(0))
         self.token_count += n_tokens
 
@@ -466,7 +464,7 @@ class GPTQPlusOracle:
     @torch.no_grad()
     def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
                     static_groups=False, enable_gradient_update=True, g_update_mode="frozen",
-                    block_atomic_quant=False, stable_ties=False, gradient_refresh_fn=None,
+                    block_atomic_quant=False, gradient_refresh_fn=None,
                     grad_lr=1e-3, grad_optimizer="sgd", curvature_damping=0.1,
                     grad_reg_strategy="none", grad_reg_lambda=0.0, grad_gate_floor=0.1,
                     grad_gate_sharpness=1.0, grad_gate_sine_amp=0.0, second_order_scale=1.0,
@@ -533,7 +531,7 @@ class GPTQPlusOracle:
             W_sub[:, dead] = 0
             perm = invperm = None
             if actorder:
-                perm = torch.argsort(self.act_square, descending=True, stable=stable_ties)
+                perm = torch.argsort(self.act_square, descending=True)
                 W_sub = W_sub[:, perm]
                 H_sub = H_sub[perm][:, perm]
                 G_sub = G_sub[:, perm]
@@ -751,7 +749,7 @@ def make_quantizer(bits, sym=True, mse=False) -> WeightQuantizerOracle:
 
 def run_linear(weight, X, saliency, gradient, num_groups, bits=4, sym=True, alpha=0.0,
                reference_loss=0.0, accum_bsz=16, blocksize=128, percdamp=0.01, groupsize=-1,
-               actorder=True, static_groups=None, block_atomic_quant=False, stable_ties=False,
+               actorder=True, static_groups=None, block_atomic_quant=False,
                g_update_mode="frozen", dtype=torch.float32):
     """Drive one linear like ``build_gptq_for_subset`` + ``accumulate_hessian_for_gptq`` +
     ``fasterquant`` (gptq_plus_utils.py:6954-7039, 7467-7502).  X is (N, T, C)."""
@@ -764,7 +762,7 @@ def run_linear(weight, X, saliency, gradient, num_groups, bits=4, sym=True, alph
     g.finalize_hessian()
     res = g.fasterquant(blocksize=blocksize, percdamp=percdamp, groupsize=groupsize, actorder=actorder,
                         static_groups=static_groups, block_atomic_quant=block_atomic_quant,
-                        stable_ties=stable_ties, g_update_mode=g_update_mode)
+                        g_update_mode=g_update_mode)
     return g, res
 
 

@@ -3,7 +3,8 @@ vectors and the CPU oracle (oracle/gptq_cpu.py), driven like gptq_fwrd: one add_
 calibration sample, static_groups = act_order unless stated.
 
 Bars: H rel-Frobenius <= 1e-5 (the running mean is applied once instead of per sample);
-codes bit-exact up to rounding ties of the fp64-vs-fp32 inverse (<= 0.2 %, reported);
+codes within 0.01 % of the oracle's with the same H (rounding ties of the fp64-vs-fp32
+inverse, reported);
 reconstruction error within 0.5 % relative."""
 import pytest
 import torch
@@ -33,24 +34,27 @@ def _drop_in(W, X, bits, sym, mse=False):
     return g, layer
 
 
-def _expected(case):
-    """The golden arrays, or -- when act_order meets tied diag(H) entries, which the reference's
-    non-stable argsort orders in an unspecified way -- the oracle run with stable ties (the
-    oracle is pinned bit-exact to the reference where the orders agree)."""
+def _expected(case, H_gpu):
+    """The golden arrays when act_order's permutation from the kernel's own H equals the
+    reference's; otherwise (a near or exact tie of diag(H) resolved differently because the two
+    H differ by summation-order rounding) the oracle run on the kernel's H, which isolates the
+    quantization chain.  Returns (expected arrays, the permutation the kernel must produce)."""
     m = case.meta
     keys = ("W_int", "Scale", "Q", "qscale")
     if not m["act"]:
         return {k: case.t(k) for k in keys}, None
-    d = torch.diagonal(case.H()[0]).clone()
-    d[d == 0] = 1
-    p_ref = torch.argsort(d, descending=True)
-    p_stable = torch.argsort(d, descending=True, stable=True)
-    if torch.equal(p_ref, p_stable):
-        return {k: case.t(k) for k in keys}, p_ref
-    assert torch.equal(d[p_ref], d[p_stable])                    # the orders differ only in ties
-    g, _, res = run_gptq_oracle(case, stable_ties=True)
+
+    def perm_of(H):
+        d = torch.diagonal(H).clone()
+        d[d == 0] = 1
+        return torch.argsort(d, descending=True)
+
+    p_gpu = perm_of(H_gpu)
+    if torch.equal(perm_of(case.H()[0]), p_gpu):
+        return {k: case.t(k) for k in keys}, p_gpu
+    g, _, res = run_gptq_oracle(case, H=H_gpu)
     return {"W_int": res.W_int.to(torch.int8), "Scale": res.Scale, "Q": res.Q,
-            "qscale": g.quantizer.scale}, p_stable
+            "qscale": g.quantizer.scale}, p_gpu
 
 
 def _finalized_H(g):
@@ -63,19 +67,20 @@ def _finalized_H(g):
 def test_gptq_golden(case):
     m = case.meta
     g, layer = _drop_in(case.t("W"), case.t("X"), m["bits"], m["sym"], m.get("mse", False))
+    H_gpu = _finalized_H(g).cpu() if m["N"] > 0 else case.H()[0]
     if m["N"] > 0:
-        assert rel_fro(_finalized_H(g), case.H()[0]) <= 1e-5
+        assert rel_fro(H_gpu, case.H()[0]) <= 1e-5
     static = m.get("static", m["act"])
     g.fasterquant(blocksize=m["B"], percdamp=0.01, groupsize=m["gs"], actorder=m["act"],
                   static_groups=static, export_to_et=True)
     torch.cuda.synchronize()
-    exp, perm = _expected(case)
+    exp, perm = _expected(case, H_gpu)
     if perm is not None:
         assert torch.equal(g.perm.cpu(), perm)
     n = exp["W_int"].numel()
     flips = code_flips(layer.int_weight, exp["W_int"].float())
     print(f"{case.name}: code flips {flips}/{n}")
-    assert flips <= max(2, n // 500)
+    assert flips <= n // 10000
     same = layer.int_weight.cpu() == exp["W_int"].float()
     if m["gs"] == -1 or static:
         assert torch.equal(layer.scale.cpu(), exp["Scale"])            # permuted order, like the reference
@@ -119,30 +124,32 @@ def test_gptq_vs_oracle(cfg, tmp_path):
         if H is not None:
             o.H = H.clone()
         res = o.fasterquant(blocksize=cfg["B"], groupsize=cfg["gs"], actorder=cfg["act"],
-                            static_groups=cfg["act"], stable_ties=True)
-        return H_own, res
+                            static_groups=cfg["act"])
+        return H_own, res, o.perm
 
     g, layer = _drop_in(W, X, cfg["bits"], cfg["sym"])
     H_gpu = _finalized_H(g).cpu()
-    H_o, res_own = oracle()
+    H_o, res_own, _ = oracle()
     assert rel_fro(H_gpu, H_o) <= 1e-5
     if cfg["act"]:
         d_o, d_g = torch.diagonal(H_o), torch.diagonal(H_gpu)
-        p_o = torch.argsort(d_o, descending=True, stable=True)
-        p_g = torch.argsort(d_g, descending=True, stable=True)
+        p_o = torch.argsort(d_o, descending=True)
+        p_g = torch.argsort(d_g, descending=True)
         moved = p_o != p_g
         if moved.any():                              # only near ties may change places
             gap = (d_o[p_o[moved]] - d_o[p_g[moved]]).abs() / d_o[p_o[moved]]
             print(f"{cfg['name']}: act_order differs at {int(moved.sum())} positions, rel gap {float(gap.max()):.2e}")
             assert float(gap.max()) <= 1e-5
-    _, res = oracle(H_gpu)
+    _, res, perm_o = oracle(H_gpu)
     g.fasterquant(blocksize=cfg["B"], groupsize=cfg["gs"], actorder=cfg["act"], static_groups=cfg["act"],
                   export_to_et=True)
     torch.cuda.synchronize()
+    if cfg["act"]:
+        assert torch.equal(g.perm.cpu(), perm_o)             # the same keys give torch's order
     n = res.W_int.numel()
     flips = code_flips(layer.int_weight, res.W_int)
     print(f"{cfg['name']}: code flips {flips}/{n}")
-    assert flips <= n // 1000
+    assert flips <= n // 10000
     Xf = X.float().reshape(-1, cfg["C"])
     e_gpu = reconstruction_error(W.float(), layer.weight.data.float().cpu(), Xf)
     e_ref = reconstruction_error(W.float(), res_own.Q.float(), Xf)

@@ -11,16 +11,19 @@ from tests.golden.fixtures import GoldenSet
 CASES = GoldenSet.load().gptq_cases
 
 
-def run_gptq_oracle(case, stable_ties=False):
+def run_gptq_oracle(case, H=None):
+    """The oracle on a golden case; H (finalized, [C, C]) replaces the accumulated Hessian."""
     m = case.meta
     g = GPTQOracle(case.t("W"))
     g.quantizer = make_quantizer(m["bits"], m["sym"], m.get("mse", False))
     X = case.t("X")
     for j in range(X.shape[0]):
         g.add_batch(X[j].unsqueeze(0))
+    if H is not None:
+        g.H = H.clone()
     H = g.H.clone()
     res = g.fasterquant(blocksize=m["B"], percdamp=0.01, groupsize=m["gs"], actorder=m["act"],
-                        static_groups=m.get("static", m["act"]), stable_ties=stable_ties)
+                        static_groups=m.get("static", m["act"]))
     return g, H, res
 
 
