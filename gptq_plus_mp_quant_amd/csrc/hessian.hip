@@ -23,6 +23,7 @@
 #include "rq_common.h"
 
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 namespace {
@@ -1372,6 +1373,65 @@ extern "C" int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets)
     if (b > need) need = b;
   }
   return need;
+}
+
+// Scratch of the no-allocation variant: one array per device (the code object's own copy on
+// each GPU), held until the process ends.  Host code never passes the array's name to a
+// kernel: it takes the device address from hipGetSymbolAddress once per device.
+static __device__ __align__(256) uint8_t scratch[RQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+__global__ void k_zero_words(uint32_t* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+constexpr int SCRATCH_MAXDEV = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[SCRATCH_MAXDEV] = {};
+
+// Device address of the current device's scratch.  The first call on a device looks it up and
+// clears the tail-slice counters (the kernels return them to zero after every launch) with a
+// fill kernel on the caller's stream, ahead of the launches that use them.
+int scratch_of_current_device(hipStream_t s, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return RQ_EHIP;
+  if (dev < 0 || dev >= SCRATCH_MAXDEV) return RQ_EINVAL;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return RQ_EHIP;
+    const int64_t words = hessian_cnt_bytes() / 4;
+    hipLaunchKernelGGL(k_zero_words, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s,
+                       static_cast<uint32_t*>(p), words);
+    RQ_CHECK_LAUNCH();
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return RQ_OK;
+}
+
+}  // namespace
+
+extern "C" int rq_hessian_accum_noalloc(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
+                                        const float* sal, int64_t ld_sal, int G, float* H, float* act_sq,
+                                        void* stream) {
+  if (!x || !sal || !H || C <= 0 || G <= 0 || ntok < 0 || ldx < C || ld_sal < G) return RQ_EINVAL;
+  if (x_dtype != RQ_F16 && x_dtype != RQ_BF16 && x_dtype != RQ_F32) return RQ_EINVAL;
+  if (ntok == 0) return RQ_OK;
+  // the least scratch the kernel rq_hessian_accum would choose needs (whole items only)
+  const int n = G < HMAXT ? G : HMAXT;
+  const int64_t need = (x_dtype != RQ_F32 && g_hmath.load() == RQ_HMATH_SPLIT16)
+                           ? split_layout(ntok, C, n, 0, 1).bytes
+                           : hessian_ws_bytes(ntok, C, 0, 1);
+  if (need > (int64_t)RQ_NOALLOC_SCRATCH_BYTES) return RQ_EINVAL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(s, &ws);
+  if (rc) return rc;
+  return rq_hessian_accum(x, x_dtype, ntok, ldx, C, sal, ld_sal, G, H, act_sq, ws,
+                          (int64_t)RQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,

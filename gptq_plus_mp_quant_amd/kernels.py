@@ -100,6 +100,22 @@ def hessian_accum(x, sal, H, act_sq):
              nat.ptr(sal), sal.stride(0), G, nat.ptr(H), nat.ptr(act_sq), nat.ptr(ws), nbytes, _stream(x))
 
 
+def hessian_accum_noalloc(x, sal, H, act_sq):
+    """hessian_accum without a workspace: the library's per-GPU scratch array serves instead
+    (rq_hessian_accum_noalloc; RuntimeError when the chunk needs more than
+    RQ_NOALLOC_SCRATCH_BYTES of scratch).  Calls overlapping in time on one GPU race."""
+    _rowmajor(x, "x")
+    _rowmajor(sal, "sal")
+    G, C, C2 = H.shape
+    if C != C2 or x.shape[1] != C or sal.shape != (x.shape[0], G) or sal.dtype != _f32:
+        raise ValueError("hessian_accum_noalloc: shape mismatch")
+    if not (H.is_contiguous() and H.dtype == _f32 and (act_sq is None or
+                                                       (act_sq.is_contiguous() and act_sq.numel() == C))):
+        raise ValueError("hessian_accum_noalloc: H / act_sq must be contiguous fp32")
+    nat.call("rq_hessian_accum_noalloc", nat.ptr(x), nat.dtype_code(x.dtype), x.shape[0], x.stride(0), C,
+             nat.ptr(sal), sal.stride(0), G, nat.ptr(H), nat.ptr(act_sq), _stream(x))
+
+
 def hessian_accum_multi(x, sals, Hs, acts):
     """One launch for several (module, group) targets sharing x [n, C]: for module m,
     Hs[m][g] += x^T diag(sals[m][:, g]) x and acts[m] += sum x^2 (acts[m] may be None)."""

@@ -69,6 +69,20 @@ int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int 
                      const float* sal, int64_t ld_sal, int G, float* H, float* act_sq,
                      void* workspace, int64_t workspace_bytes, void* stream);
 
+/* rq_hessian_accum for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  Same arguments, kernels and results as rq_hessian_accum minus the workspace: a
+ * scratch array of the library (RQ_NOALLOC_SCRATCH_BYTES on every GPU the library runs on,
+ * held until the process ends) serves as the workspace, so the call allocates nothing.
+ * Returns RQ_EINVAL when the call needs more scratch than that (the split kernel needs about
+ * 2 * ntok * C bytes for its copy of the chunk: pass fewer tokens per call).  Every call on a
+ * GPU shares that GPU's array, which keeps the last call's contents: calls that overlap in time
+ * on one GPU race. */
+#define RQ_NOALLOC_SCRATCH_BYTES (128u << 20)
+int rq_hessian_accum_noalloc(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
+                             const float* sal, int64_t ld_sal, int G, float* H, float* act_sq,
+                             void* stream);
+
 /* Cross-module fused accumulation: the add_batch of several GPTQPlus objects whose modules read
  * the same input (q/k/v, gate/up; their forward hooks receive the same tensor,
  * gptq_plus_utils.py:6991-7003) in one launch, so X is streamed once for all of them.
