@@ -1,89 +1,112 @@
 """Benchmark: ms per linear (Hessian accumulation + GPTQ+ fasterquant) on one MI355X.
 
-Workload: one 4096x4096 q_proj linear, fp16 W ~ N(0, 0.02^2);
-calibration X = 128 samples x 2048 tokens x 4096 fp16 ~ N(0,1) with 8 outlier channels x20;
-NUM_GROUPS = 4 token saliencies ~ LogNormal(0,1) clipped at their 0.99 quantile; GPTQ+
-first-order term on with G ~ N(0, 1e-4^2) and alpha = 0; w4 asymmetric per-channel,
-act_order, BLOCKSIZE = 128, percdamp = 0.01; 16-sample add_batch chunks.
-A step = one linear: 8 add_batch calls + finalize_hessian + fasterquant, inputs resident in
-HBM.  Prints one JSON line.
+Default workload -- BASELINE.json configs[2], the configuration the metric and the target are
+stated on: a full Llama-3-8B-shaped decoder layer, 7 linears (q/o 4096x4096, k/v 1024x4096,
+gate/up 14336x4096, down 4096x14336), fp16 W ~ N(0, 0.02^2), calibration X = 128 samples x
+2048 tokens per input width (N(0,1), 8 seeded outlier channels x20), NUM_GROUPS = 4 token
+saliencies ~ LogNormal(0,1) clipped at their 0.99 quantile, GPTQ+ term on with
+G ~ N(0, 1e-4^2) and alpha = 0, w4 asymmetric per-channel, act_order, BLOCKSIZE = 128,
+percdamp = 0.01, 16-sample add_batch chunks; q/k/v and gate/up take their Hessians from one
+launch over their shared input (add_batch_shared).  A step = one layer (Hessians of the 7
+linears + finalize_hessian + fasterquant of each), inputs resident in HBM; value = layer / 7.
+Prints one JSON line.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-  python bench.py --config cfg3|cfg4 [--cpu-baseline-layer]   # a whole Llama-3-8B layer
-  python bench.py --config cfg5 [--cpu-baseline-sample]       # Llama-3-70B down_proj
+  python bench.py --config cfg1|cfg2          # configs[0] / configs[1]: one 4096x4096 q_proj
+  python bench.py --config cfg4               # configs[3]: the layer rotated, w4 sym, g128, atomic
+  python bench.py --config cfg5 [--cpu-baseline-sample]   # configs[4]: Llama-3-70B down_proj
+  python bench.py --alpha 0.05 --ref-loss 1e-3   # the GPTQ+ term with a non-zero beta
+
+Report helpers that run no GPU work (their outputs are the summaries under profiles/):
+  python bench.py --stats-table STATS_CSV --config cfgN --units U
+  python bench.py --traffic FETCH_CSV WRITE_CSV CAL_FETCH_CSV CAL_WRITE_CSV --config cfgN
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import hashlib
 import json
 import os
 import platform
+import re
+import subprocess
 import sys
 import time
-
-import torch
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 FP32_MFMA_PEAK_TFLOPS = 157.3
 FP16_MFMA_PEAK_TFLOPS = 2500.0      # dense fp16 / bf16 MFMA
-SPLIT_PIECES = 3                    # fp16 MFMA products per exact fp32 product (split16 kernel)
+FP64_MFMA_PEAK_TFLOPS = 78.6
+HBM_PEAK_GBS = 8000.0
+METRIC = "ms per linear (H-accum + fasterquant) at Llama-8B shapes; % fp32-MFMA peak"
+PIECES = {"split16": 2, "split16x3": 3, "fp32": 1}     # 16-bit MFMA products per fp32 product (fp16 X)
+KERNEL = {"split16": "k_hessian_split<__half, 2>", "split16x3": "k_hessian_split<__half, 3>",
+          "fp32": "k_hessian_accum<__half>"}
+HESSIAN_SRC = os.path.join(ROOT, "gptq_plus_mp_quant_amd", "csrc", "hessian.hip")
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "hessian_traffic.json")
+
+BASE = dict(R=4096, C=4096, G=4, N=128, T=2048, bsz=16, bits=4, sym=False, blocksize=128,
+            percdamp=0.01, alpha=0.0, ref_loss=0.0, outliers=8, seed=20251201, wscale=0.02)
+# BASELINE.md numbering: cfgK = BASELINE.json configs[K-1]
+CONFIGS = {
+    "cfg1": dict(BASE, G=1, gptq_plus=False, kind="linear"),
+    "cfg2": dict(BASE, kind="linear"),
+    "cfg3": dict(BASE, kind="layer"),
+    "cfg4": dict(BASE, sym=True, groupsize=128, actorder=False, atomic=True, rotate=True, kind="layer"),
+    "cfg5": dict(BASE, R=8192, C=28672, wscale=0.015, kind="linear"),
+}
+WORKLOAD = {
+    "cfg1": "configs[0]: q_proj 4096x4096, NUM_GROUPS=1, 128x2048 tokens, w4 asym per-channel, act_order, "
+            "B=128, GPTQ+ term off",
+    "cfg2": "configs[1]: q_proj 4096x4096, NUM_GROUPS=4, 128x2048 tokens, w4 asym per-channel, act_order, "
+            "B=128, GPTQ+ term on (alpha={alpha})",
+    "cfg3": "configs[2]: Llama-3-8B decoder layer, 7 linears (q/k/v and gate/up Hessians fused over their "
+            "shared input), NUM_GROUPS=4, 128x2048 tokens, w4 asym per-channel, act_order, B=128, GPTQ+ term on "
+            "(alpha={alpha}); value = layer time / 7, ms_per_step = layer",
+    "cfg4": "configs[3]: Llama-3-8B decoder layer, seeded orthogonal (Hadamard-based) rotation of W and X, w4 "
+            "sym, 128-column dynamic groups, BLOCK_ATOMIC_QUANT, NUM_GROUPS=4, 128x2048 tokens; value = layer "
+            "time / 7, ms_per_step = layer",
+    "cfg5": "configs[4]: Llama-3-70B down_proj 8192x28672, W ~ N(0, 0.015^2), NUM_GROUPS=4 (4 Hessians of "
+            "28672^2 fp32), 128x2048 tokens, w4 asym per-channel, act_order, B=128, GPTQ+ term on (alpha={alpha})",
+}
+# the modules of a Llama-3-8B decoder layer; modules that read the same input share one X
+LAYER8B = [("q_proj", 4096, 4096, "attn"), ("k_proj", 1024, 4096, "attn"), ("v_proj", 1024, 4096, "attn"),
+           ("o_proj", 4096, 4096, "o"), ("gate_proj", 14336, 4096, "mlp"), ("up_proj", 14336, 4096, "mlp"),
+           ("down_proj", 4096, 14336, "down")]
+INPUT_WIDTH = {"attn": 4096, "o": 4096, "mlp": 4096, "down": 14336}
 
 
-def hessian_roofline(flops, ms, math, extra):
-    """Roofline object for the Hessian accumulation.  `flops` counts 2 per (token, i <= j)
-    element of every Hessian.  split16 runs on the fp16 MFMA pipe and needs SPLIT_PIECES fp16
-    products per fp32 product, so its bound is the fp16 peak against SPLIT_PIECES x flops; the
-    fp32-equivalent rate (flops / time against the fp32 MFMA peak) is what the metric's
-    "% fp32-MFMA peak" reads."""
-    eq = flops / (ms * 1e-3) / 1e12
-    if math == "split16":
-        ach, peak = SPLIT_PIECES * eq, FP16_MFMA_PEAK_TFLOPS
-        kernel = "k_hessian_split<__half> (timed with its k_xprep + k_xfinish pre-pass)"
-    else:
-        ach, peak = eq, FP32_MFMA_PEAK_TFLOPS
-        kernel = "k_hessian_accum<__half>"
-    out = {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
-           "frac": round(ach / peak, 4), "kernel": kernel, "math": math,
-           "fp32_equivalent": {"achieved": round(eq, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
-                               "frac": round(eq / FP32_MFMA_PEAK_TFLOPS, 4)}}
-    out.update(extra)
-    return out
+# ---------------------------------------------------------------------------------------------
+# synthetic inputs (seeded, generated on the GPU)
 
-CFG = dict(R=4096, C=4096, G=4, N=128, T=2048, bsz=16, bits=4, sym=False, blocksize=128,
-           percdamp=0.01, alpha=0.0, outliers=8, seed=20251201, wscale=0.02)
-# the Llama-3-70B down_proj, one GPU's full share (4 Hessians of 28672^2 fp32)
-CFG5 = dict(CFG, R=8192, C=28672, wscale=0.015)
+def _saliency(gen, dev, N, T, G):
+    import torch
+    s = torch.exp(torch.randn((N, T, G), generator=gen, device=dev))
+    for g in range(G):
+        s[..., g].clamp_(max=float(torch.quantile(s[..., g].flatten(), 0.99)))   # linear interpolation
+    return s
 
 
 def make_inputs(dev, cfg):
-    """Synthetic inputs generated on the GPU from a fixed seed (torch Philox)."""
+    import torch
     gen = torch.Generator(device=dev)
     gen.manual_seed(cfg["seed"])
     N, T, C, R, G = cfg["N"], cfg["T"], cfg["C"], cfg["R"], cfg["G"]
     X = torch.empty((N, T, C), dtype=torch.float16, device=dev)
     for i in range(N):
         X[i] = torch.randn((T, C), generator=gen, device=dev, dtype=torch.float32).half()
-    out_ch = torch.randperm(C, generator=gen, device=dev)[: cfg["outliers"]]
-    X[:, :, out_ch] *= 20
+    X[:, :, torch.randperm(C, generator=gen, device=dev)[: cfg["outliers"]]] *= 20
     W = (torch.randn((R, C), generator=gen, device=dev) * cfg["wscale"]).half()
-    s = torch.exp(torch.randn((N, T, G), generator=gen, device=dev))
-    for g in range(G):
-        q = torch.quantile(s[..., g].flatten(), 0.99)          # linear interpolation
-        s[..., g].clamp_(max=float(q))
+    s = _saliency(gen, dev, N, T, G)
     grad = torch.randn((R, C), generator=gen, device=dev) * 1e-4
     return X, W, s, grad
 
 
-# a full Llama-3-8B decoder layer; modules that read the same input share one X
-LAYER8B = [("q_proj", 4096, 4096, "attn"), ("k_proj", 1024, 4096, "attn"), ("v_proj", 1024, 4096, "attn"),
-           ("o_proj", 4096, 4096, "o"), ("gate_proj", 14336, 4096, "mlp"), ("up_proj", 14336, 4096, "mlp"),
-           ("down_proj", 4096, 14336, "down")]
-
-
 def hadamard(n, dev):
-    """Sylvester Hadamard matrix of order n (a power of two), fp32."""
+    import torch
     H = torch.ones((1, 1), device=dev)
     while H.shape[0] < n:
         H = torch.cat([torch.cat([H, H], 1), torch.cat([H, -H], 1)], 0)
@@ -93,6 +116,7 @@ def hadamard(n, dev):
 def rotation(C, gen, dev):
     """configs[3]'s seeded orthogonal rotation: diag(+-1) H_C / sqrt(C) for a power of two,
     Q_k (x) (diag(+-1) H_m / sqrt(m)) for C = k * m (QuaRot-style; C = 14336 = 7 * 2048)."""
+    import torch
     m = 1 << (C.bit_length() - 1)
     while C % m:
         m >>= 1
@@ -105,242 +129,284 @@ def rotation(C, gen, dev):
     return torch.kron(Qk.contiguous().to(dev), Hm.contiguous())
 
 
-def rotate_(X, Rm):
-    """X <- X R in place, one calibration sample at a time (fp32 product, fp16 result)."""
-    for i in range(X.shape[0]):
-        X[i] = (X[i].float() @ Rm).half()
-
-
 def make_layer_inputs(dev, cfg):
+    import torch
     gen = torch.Generator(device=dev)
     gen.manual_seed(cfg["seed"] + 1)
     N, T, G = cfg["N"], cfg["T"], cfg["G"]
     xs, rots = {}, {}
-    for key, C in (("attn", 4096), ("o", 4096), ("mlp", 4096), ("down", 14336)):
+    for key, C in INPUT_WIDTH.items():
         X = torch.empty((N, T, C), dtype=torch.float16, device=dev)
         for i in range(N):
             X[i] = torch.randn((T, C), generator=gen, device=dev, dtype=torch.float32).half()
         X[:, :, torch.randperm(C, generator=gen, device=dev)[: cfg["outliers"]]] *= 20
         if cfg.get("rotate"):
             rots[key] = rotation(C, gen, dev)
-            rotate_(X, rots[key])
+            for i in range(N):                                  # X <- X R, one sample at a time
+                X[i] = (X[i].float() @ rots[key]).half()
         xs[key] = X
     mods = {}
     for name, R, C, key in LAYER8B:
-        W = (torch.randn((R, C), generator=gen, device=dev) * 0.02).half()
+        W = (torch.randn((R, C), generator=gen, device=dev) * cfg["wscale"]).half()
         if cfg.get("rotate"):
             W = (W.float() @ rots[key]).half()                 # W' = W R keeps X' W'^T = X W^T
-        s = torch.exp(torch.randn((N, T, G), generator=gen, device=dev))
-        for g in range(G):
-            s[..., g].clamp_(max=float(torch.quantile(s[..., g].flatten(), 0.99)))
-        grad = torch.randn((R, C), generator=gen, device=dev) * 1e-4
-        mods[name] = (W, s, grad, key)
+        mods[name] = (W, _saliency(gen, dev, N, T, G), torch.randn((R, C), generator=gen, device=dev) * 1e-4, key)
     return xs, mods
 
 
-def one_layer(xs, mods, cfg, layers, timer=None):
-    """Hessians of all 7 linears (shared inputs fused) + finalize + fasterquant of each."""
-    from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer, add_batch_shared
-    objs = {}
-    for name, (W, s, grad, key) in mods.items():
-        layers[name].weight.data.copy_(W)
-        g = GPTQPlus(layers[name], saliency=s, gradient=grad, num_groups=cfg["G"], alpha=cfg["alpha"],
-                     reference_loss=0.0)
-        g.quantizer = WeightQuantizer()
-        g.quantizer.configure(cfg["bits"], perchannel=True, sym=cfg["sym"], mse=False)
-        objs[name] = g
-    fq = fq_kwargs(cfg)
-    for key in ("attn", "o", "mlp", "down"):
-        group = [objs[n] for n, _, _, k in LAYER8B if k == key]
-        for j in range(0, cfg["N"], cfg["bsz"]):
-            if timer is not None:
-                timer.start()
-            add_batch_shared(group, xs[key][j:j + cfg["bsz"]])
-            if timer is not None:
-                timer.stop()
-    for g in objs.values():
-        g.finalize_hessian()
-    for g in objs.values():
-        g.fasterquant(**fq)
-        g.free()
-    return objs
+# ---------------------------------------------------------------------------------------------
+# the timed work
+
+class KernelTimer:
+    """HIP events recorded by the library around each Hessian product kernel
+    (rq_hessian_timing_events), on the stream that kernel runs on."""
+
+    def __init__(self):
+        self.pairs = []
+
+    def arm(self):
+        import torch
+        from gptq_plus_mp_quant_amd import _native as nat
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()          # creates the events; the library records them again around the kernel
+        b.record()
+        nat.call("rq_hessian_timing_events", a.cuda_event, b.cuda_event)
+        self.pairs.append((a, b))
+
+    def total_ms(self):
+        import torch
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in self.pairs), len(self.pairs)
 
 
 def fq_kwargs(cfg):
-    """fasterquant arguments of a config: configs[1..2] per-channel + act_order (static_groups
-    follows act_order like the driver, :7472); configs[3] dynamic 128-column groups + atomic."""
+    """fasterquant arguments: act_order with static_groups = act_order like the driver (:7472);
+    configs[3] dynamic 128-column groups + atomic; configs[0] without the GPTQ+ term."""
     act = cfg.get("actorder", True)
     return dict(blocksize=cfg["blocksize"], percdamp=cfg["percdamp"], groupsize=cfg.get("groupsize", -1),
-                actorder=act, static_groups=act, block_atomic_quant=cfg.get("atomic", False))
+                actorder=act, static_groups=act, block_atomic_quant=cfg.get("atomic", False),
+                enable_gradient_update=cfg.get("gptq_plus", True))
 
 
-def layer_hessian_flops(cfg):
-    ntok = cfg["N"] * cfg["T"]
-    return sum(cfg["G"] * ntok * C * (C + 1) for _, _, C, _ in LAYER8B)
-
-
-def cpu_baseline_layer(xs, mods, cfg):
-    """CPU oracle for configs[2]: per input width, one add_batch chunk is timed and scaled by
-    tokens (x N/bsz); every module's finalize_hessian + fasterquant is timed in full."""
-    from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
-    nchunks = cfg["N"] // cfg["bsz"]
-    total, parts = 0.0, []
-    for name, R, C, key in LAYER8B:
-        W, s, grad, _ = mods[name]
-        o = GPTQPlusOracle(W.cpu(), s.cpu(), grad.cpu(), cfg["G"], cfg["alpha"], 0.0)
-        o.quantizer = make_quantizer(cfg["bits"], cfg["sym"])
-        xc = xs[key][: cfg["bsz"]].cpu()
-        t0 = time.perf_counter()
-        o.add_batch(xc)
-        t_acc = time.perf_counter() - t0
-        o.index, o.token_count = cfg["N"], cfg["N"] * cfg["T"]
-        t1 = time.perf_counter()
-        o.finalize_hessian()
-        o.fasterquant(**fq_kwargs(cfg))
-        t_fq = time.perf_counter() - t1
-        total += t_acc * nchunks + t_fq
-        parts.append(f"{name}: 1/{nchunks} chunk {t_acc:.1f}s, fasterquant {t_fq:.1f}s")
-        print(f"cpu baseline {name}: add_batch chunk {t_acc:.1f} s, finalize+fasterquant {t_fq:.1f} s",
-              flush=True)
-    return dict(value=round(total * 1e3 / len(LAYER8B), 1), unit="ms per linear (layer / 7, extrapolated)",
-                cores=torch.get_num_threads(), kind="port",
-                sample="oracle on host CPU; " + "; ".join(parts) + f"; layer {total:.1f} s")
-
-
-CFG4 = dict(CFG, sym=True, groupsize=128, actorder=False, atomic=True, rotate=True)
-WORKLOAD = {
-    "cfg3": "configs[2]: Llama-3-8B decoder layer, 7 linears (q/k/v and gate/up Hessians fused over "
-            "their shared input), NUM_GROUPS=4, 128x2048 tokens, w4 asym per-channel, act_order, B=128; "
-            "value = layer time / 7, ms_per_step = layer",
-    "cfg4": "configs[3]: Llama-3-8B decoder layer, seeded orthogonal (Hadamard-based) rotation of W and X, "
-            "w4 sym, 128-column dynamic groups, BLOCK_ATOMIC_QUANT, NUM_GROUPS=4, 128x2048 tokens; "
-            "value = layer time / 7, ms_per_step = layer",
-}
-
-
-def run_layer(args, dev):
-    cfg = dict(CFG4 if args.config == "cfg4" else CFG)
-    xs, mods = make_layer_inputs(dev, cfg)
-    layers = {n: torch.nn.Linear(C, R, bias=False).to(dev, torch.float16) for n, R, C, _ in LAYER8B}
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        one_layer(xs, mods, cfg, layers)
-    timer = EventTimer()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        one_layer(xs, mods, cfg, layers, timer)
-    torch.cuda.synchronize()
-    layer_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    h_ms_mean, n_launch = timer.mean_ms()
-    h_ms_layer = h_ms_mean * n_launch / args.steps
-    line = {
-        "metric": "ms per linear (H-accum + fasterquant) at Llama-8B shapes; % fp32-MFMA peak",
-        "value": round(layer_ms / len(LAYER8B), 2), "unit": "ms", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(layer_ms, 2), "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32 (fp16 inputs; exact fp32 products)",
-        "data": "synthetic (seeded, generated on the GPU)",
-        "config": {"workload": WORKLOAD[args.config], "parallelism": "single GPU"},
-        "roofline": hessian_roofline(layer_hessian_flops(cfg), h_ms_layer, args.hessian_math,
-                                     {"traffic": None, "hessian_ms_per_layer": round(h_ms_layer, 2),
-                                      "launches_per_layer": n_launch // args.steps,
-                                      "flops_per_layer": layer_hessian_flops(cfg)}),
-    }
-    if args.cpu_baseline_layer:
-        line["cpu_baseline"] = cpu_baseline_layer(xs, mods, cfg)
-    print(json.dumps(line), flush=True)
+def new_gptq(layer, W, s, grad, cfg):
+    from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
+    layer.weight.data.copy_(W)
+    g = GPTQPlus(layer, saliency=s, gradient=grad, num_groups=cfg["G"], alpha=cfg["alpha"],
+                 reference_loss=cfg["ref_loss"])
+    g.quantizer = WeightQuantizer()
+    g.quantizer.configure(cfg["bits"], perchannel=True, sym=cfg["sym"], mse=False)
+    return g
 
 
 def one_linear(X, W, s, grad, cfg, layer, timer=None):
-    from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
-    layer.weight.data.copy_(W)
-    g = GPTQPlus(layer, saliency=s, gradient=grad, num_groups=cfg["G"], alpha=cfg["alpha"], reference_loss=0.0)
-    g.quantizer = WeightQuantizer()
-    g.quantizer.configure(cfg["bits"], perchannel=True, sym=cfg["sym"], mse=False)
+    g = new_gptq(layer, W, s, grad, cfg)
     for j in range(0, cfg["N"], cfg["bsz"]):
         if timer is not None:
-            timer.start()
+            timer.arm()
         g.add_batch(X[j:j + cfg["bsz"]], None)
-        if timer is not None:
-            timer.stop()
     g.finalize_hessian()
     g.fasterquant(**fq_kwargs(cfg))
     return g
 
 
-class EventTimer:
-    """HIP events on the stream the Hessian kernel is launched on (torch's current stream)."""
-
-    def __init__(self):
-        self.pairs = []
-
-    def start(self):
-        e = torch.cuda.Event(enable_timing=True)
-        e.record()
-        self.pairs.append([e, None])
-
-    def stop(self):
-        e = torch.cuda.Event(enable_timing=True)
-        e.record()
-        self.pairs[-1][1] = e
-
-    def mean_ms(self):
-        torch.cuda.synchronize()
-        ts = [a.elapsed_time(b) for a, b in self.pairs]
-        return sum(ts) / len(ts), len(ts)
+def one_layer(xs, mods, cfg, layers, timer=None, keep=False):
+    from gptq_plus_mp_quant_amd import add_batch_shared
+    objs = {name: new_gptq(layers[name], W, s, grad, cfg) for name, (W, s, grad, _) in mods.items()}
+    for key in INPUT_WIDTH:
+        group = [objs[n] for n, _, _, k in LAYER8B if k == key]
+        for j in range(0, cfg["N"], cfg["bsz"]):
+            if timer is not None:
+                timer.arm()
+            add_batch_shared(group, xs[key][j:j + cfg["bsz"]])
+    for g in objs.values():
+        g.finalize_hessian()
+    kept = {}
+    for name, g in objs.items():
+        if keep:
+            kept[name] = (g.H.clone(), g.act_square.clone())
+        g.fasterquant(**fq_kwargs(cfg))
+        g.free()
+    return kept
 
 
-def cpu_baseline(X, W, s, grad, cfg, chunks=2):
-    """Time the CPU oracle (the reference's torch op sequence) on a bounded sample:
-    `chunks` of the 8 add_batch calls (extrapolated linearly in tokens) plus the full
-    finalize_hessian + fasterquant of the same linear."""
+def hessian_flops(cfg):
+    """Algorithmic fp32 flops of one unit's Hessians: the upper triangle incl. the diagonal,
+    2 per (token, i <= j) element of every Hessian (G * N * T * C * (C + 1) per linear)."""
+    ntok = cfg["N"] * cfg["T"]
+    if cfg["kind"] == "layer":
+        return sum(cfg["G"] * ntok * C * (C + 1) for _, _, C, _ in LAYER8B)
+    return cfg["G"] * ntok * cfg["C"] * (cfg["C"] + 1)
+
+
+def load_traffic(math, config):
+    """Calibrated HBM bytes per product-kernel launch from the committed rocprofv3 measurement,
+    used only when it was taken on this configuration with the current hessian.hip."""
+    if not os.path.exists(TRAFFIC_JSON):
+        return None, "no measurement"
+    with open(TRAFFIC_JSON) as f:
+        rec = (json.load(f).get(math) or {})
+    if rec.get("config") != config:
+        return None, f"measured on {rec.get('config')}"
+    if rec.get("hessian_src_sha256") != source_sha():
+        return None, "hessian.hip changed since the measurement"
+    return rec.get("traffic_bytes_per_launch"), "profiles/hessian_traffic.json"
+
+
+def source_sha():
+    with open(HESSIAN_SRC, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
+def roofline(cfg, args, kernel_ms, launches, steps):
+    """The dominant kernel (the Hessian product kernel) against the fp32 MFMA peak that the
+    metric is stated on: algorithmic fp32 flops per launch / measured launch time.  The kernel
+    runs on the 16-bit MFMA pipe (PIECES products per fp32 product); that pipe's use is given
+    beside it."""
+    flops_unit = hessian_flops(cfg)
+    per_launch_flops = flops_unit * steps / launches
+    ms = kernel_ms / launches
+    ach = per_launch_flops / (ms * 1e-3) / 1e12
+    traffic, tsrc = load_traffic(args.hessian_math, args.config)
+    pieces = PIECES[args.hessian_math]
+    return {"bound": "mfma", "achieved": round(ach, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
+            "kernel": KERNEL[args.hessian_math], "launch_ms": round(ms, 4), "launches": launches // steps,
+            "flops_per_launch": int(per_launch_flops),
+            "algorithmic": "fp32 flops of H_g += X^T diag(s_g) X, upper triangle incl. diagonal "
+                           "(G*n*C*(C+1) per launch of n tokens)",
+            "pipe": {"name": "fp16 MFMA" if pieces > 1 else "fp32 MFMA", "products_per_fp32_product": pieces,
+                     "executed_tflops": round(ach * pieces, 2),
+                     "peak": FP16_MFMA_PEAK_TFLOPS if pieces > 1 else FP32_MFMA_PEAK_TFLOPS,
+                     "frac": round(ach * pieces / (FP16_MFMA_PEAK_TFLOPS if pieces > 1 else FP32_MFMA_PEAK_TFLOPS), 4)},
+            "traffic_source": tsrc}
+
+
+# ---------------------------------------------------------------------------------------------
+# the CPU baseline: the reference's op sequence (oracle/) on the host cores
+
+def host_cpu():
+    """Use every physical core this process may run on; describe the host."""
+    import torch
+    out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout if shutil_which("lscpu") else ""
+    field = lambda k: (re.search(rf"^{k}:\s*(.+)$", out, re.M) or [None, "?"])[1].strip()
+    model = field("Model name")
+    try:
+        sockets, cps, tpc = int(field(r"Socket\(s\)")), int(field(r"Core\(s\) per socket")), int(field(r"Thread\(s\) per core"))
+    except ValueError:
+        sockets, cps, tpc = 1, os.cpu_count() or 1, 1
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = max(1, min(sockets * cps, affinity // max(tpc, 1) if tpc > 1 else affinity))
+    torch.set_num_threads(threads)
+    cfg_txt = torch.__config__.show()
+    blas = (re.search(r"BLAS_INFO=(\w+)", cfg_txt) or [None, "?"])[1]
+    par = torch.__config__.parallel_info()
+    backend = (re.search(r"ATen parallel backend: (.+)", par) or [None, "?"])[1].strip()
+    return threads, {"model": model, "sockets": sockets, "cores_per_socket": cps, "threads_per_core": tpc,
+                     "cpus_available": affinity, "threads_used": threads, "blas": blas,
+                     "aten_parallel": backend, "isa": torch.backends.cpu.get_cpu_capability(),
+                     "torch": torch.__version__}
+
+
+def shutil_which(name):
+    from shutil import which
+    return which(name) is not None
+
+
+def cpu_baseline_linear(X, W, s, grad, cfg, chunks=2):
+    """`chunks` of the 8 add_batch calls timed (extrapolated by tokens)
+    plus the full finalize_hessian + fasterquant of the same linear."""
+    import torch
     from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
-    threads = torch.get_num_threads()
-    Xc = X[: chunks * cfg["bsz"]].cpu()
-    sc, Wc, gc = s.cpu(), W.cpu(), grad.cpu()
-    o = GPTQPlusOracle(Wc, sc, gc, cfg["G"], cfg["alpha"], 0.0)
+    threads, host = host_cpu()
+    o = GPTQPlusOracle(W.cpu(), s.cpu(), grad.cpu(), cfg["G"], cfg["alpha"], cfg["ref_loss"])
     o.quantizer = make_quantizer(cfg["bits"], cfg["sym"])
+    Xc = X[: chunks * cfg["bsz"]].cpu()
     t0 = time.perf_counter()
     for j in range(0, Xc.shape[0], cfg["bsz"]):
         o.add_batch(Xc[j:j + cfg["bsz"]])
     t_acc = time.perf_counter() - t0
-    # the remaining chunks only add to H; scale the measured accumulation time by tokens
-    o.index = cfg["N"]
-    o.token_count = cfg["N"] * cfg["T"]
+    o.index, o.token_count = cfg["N"], cfg["N"] * cfg["T"]
     t1 = time.perf_counter()
     o.finalize_hessian()
-    o.fasterquant(**fq_kwargs(cfg))
+    o.fasterquant(**{k: v for k, v in fq_kwargs(cfg).items()})
     t_fq = time.perf_counter() - t1
     nchunks = cfg["N"] // cfg["bsz"]
-    total_s = t_acc * nchunks / chunks + t_fq
-    return dict(value=round(total_s * 1e3, 1), unit="ms per linear (extrapolated)", cores=threads,
-                kind="port",
-                sample=(f"oracle (reference torch op sequence) on host CPU: {chunks}/{nchunks} add_batch "
-                        f"chunks timed ({t_acc:.1f} s, x{nchunks // chunks} by tokens) + full "
-                        f"finalize_hessian+fasterquant ({t_fq:.1f} s); {platform.processor() or platform.machine()}"))
+    total = t_acc * nchunks / chunks + t_fq
+    return dict(value=round(total * 1e3, 1), unit="ms per linear (extrapolated)", cores=threads, kind="port",
+                sample=(f"oracle (the reference's torch op sequence) on the host CPU: {chunks}/{nchunks} add_batch "
+                        f"chunks timed ({t_acc:.1f} s, x{nchunks // chunks} by tokens) + full finalize_hessian + "
+                        f"fasterquant ({t_fq:.1f} s)"), host=host)
+
+
+def cpu_baseline_layer(xs, mods, kept, cfg):
+    """configs[2] / configs[3] on a bounded sample.  add_batch: one calibration sample (2048 of the
+    262144 tokens) per input width, through the reference's per-module call (x 128 by tokens, per
+    module of that width).  finalize_hessian + fasterquant: one of the 4 row subgroups of each
+    distinct (rows, columns) shape, on the GPU run's finalized H_0 (the subgroups are independent
+    in the reference's loop, :1027-1162; x 4 per module).  The two parts make the layer."""
+    import torch
+    from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
+    threads, host = host_cpu()
+    N, G = cfg["N"], cfg["G"]
+    t_ab, parts = {}, []
+    for key, C in (("attn", 4096), ("down", 14336)):
+        name = next(n for n, _, c, k in LAYER8B if c == C)
+        W, s, grad, _ = mods[name]
+        o = GPTQPlusOracle(W.cpu(), s[:1].cpu(), grad.cpu(), G, cfg["alpha"], cfg["ref_loss"])
+        x = xs[key][:1].cpu()
+        t0 = time.perf_counter()
+        o.add_batch(x)
+        t_ab[C] = (time.perf_counter() - t0) * N
+        parts.append(f"add_batch C={C}: 1/{N} samples {t_ab[C] / N:.2f} s")
+    t_fq = {}
+    for name, R, C, key in LAYER8B:
+        if (R, C) in t_fq:
+            continue
+        W, s, grad, _ = mods[name]
+        Rs = R // G
+        H, act = kept[name]
+        o = GPTQPlusOracle(W[:Rs].cpu(), s[:, :, :1].cpu(), grad[:Rs].cpu(), 1, cfg["alpha"], cfg["ref_loss"])
+        o.quantizer = make_quantizer(cfg["bits"], cfg["sym"])
+        o.H = H[:1].cpu()
+        o.act_square = act.cpu()
+        o.index, o.token_count, o._finalized = N, N * cfg["T"], True
+        t0 = time.perf_counter()
+        o.fasterquant(**fq_kwargs(cfg))
+        t_fq[(R, C)] = (time.perf_counter() - t0) * G
+        parts.append(f"fasterquant {R}x{C}: 1/{G} subgroups {t_fq[(R, C)] / G:.2f} s")
+        print(f"cpu baseline fasterquant {R}x{C}: {t_fq[(R, C)] / G:.2f} s per subgroup", flush=True)
+    total = sum(t_ab[C] + t_fq[(R, C)] for _, R, C, _ in LAYER8B)
+    return dict(value=round(total * 1e3 / len(LAYER8B), 1), unit="ms per linear (layer / 7, extrapolated)",
+                cores=threads, kind="port",
+                sample=("oracle (the reference's torch op sequence) on the host CPU, extrapolated from a "
+                        "bounded sample: " + "; ".join(parts) + f"; layer {total:.1f} s"), host=host)
 
 
 def cpu_baseline_hessian_sample(X, s, cfg, samples=1):
-    """configs[4] on the host is hours of work; time the oracle's add_batch on `samples` of the
-    128 calibration samples and extrapolate by tokens.  A lower bound of the CPU path: the
-    CPU finalize_hessian + fasterquant (four 28672^2 Cholesky chains, the block loop) are left out."""
+    """configs[4] on the host is hours of work: the oracle's add_batch on `samples` of the 128
+    calibration samples, extrapolated by tokens; a lower bound (finalize + fasterquant left out)."""
+    import torch
     from oracle.gptqplus_cpu import GPTQPlusOracle
+    threads, host = host_cpu()
     C, G = cfg["C"], cfg["G"]
     o = GPTQPlusOracle(torch.zeros(G, C), s[:samples].cpu(), torch.zeros(G, C), G, 0.0, 0.0)
-    xc = X[:samples].cpu()
     t0 = time.perf_counter()
-    o.add_batch(xc)
+    o.add_batch(X[:samples].cpu())
     t = time.perf_counter() - t0
     scale = cfg["N"] // samples
     return dict(value=round(t * scale * 1e3, 1), unit="ms per linear (Hessian accumulation only, extrapolated)",
-                cores=torch.get_num_threads(), kind="port",
+                cores=threads, kind="port",
                 sample=(f"oracle add_batch on {samples}/{cfg['N']} samples ({t:.1f} s, x{scale} by tokens); "
-                        "finalize_hessian + fasterquant not timed, so this is a lower bound"))
+                        "finalize_hessian + fasterquant not timed, so this is a lower bound"), host=host)
 
+
+# ---------------------------------------------------------------------------------------------
+# report helpers (no GPU work)
 
 def copy_calibration(dev, nbytes=1 << 30, reps=3):
     """A plain device-to-device copy of known size, profiled with the same FETCH_SIZE /
     WRITE_SIZE counters to calibrate them (bytes moved = nbytes read + nbytes written)."""
+    import torch
     src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
@@ -351,9 +417,9 @@ def copy_calibration(dev, nbytes=1 << 30, reps=3):
 
 
 def gemm_calibration(dev):
-    """Practical GEMM ceilings on this GPU: torch.matmul (hipBLASLt / rocBLAS) on large square
-    operands in fp16, fp32 (TF32 off) and fp64, as TFLOP/s.  The split Hessian kernel's products
-    run on the fp16 pipe, the Cholesky chain on the fp64 pipe, the trailing update on fp32."""
+    """Practical GEMM ceilings: torch.matmul (hipBLASLt / rocBLAS) on large square operands in
+    fp16, fp32 (TF32 off) and fp64, as TFLOP/s."""
+    import torch
     torch.backends.cuda.matmul.allow_tf32 = False
     out = {}
     for name, dt, n, reps in (("fp16", torch.float16, 8192, 20), ("fp32", torch.float32, 8192, 5),
@@ -375,111 +441,208 @@ def gemm_calibration(dev):
     print(json.dumps({"gemm_calibration": out}), flush=True)
 
 
-def load_traffic(math):
-    """Calibrated HBM bytes per Hessian launch of the given kernel, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE measurement (None until measured)."""
-    path = os.path.join(ROOT, "profiles", "hessian_traffic.json")
-    if os.path.exists(path):
-        with open(path) as f:
-            return (json.load(f).get(math) or {}).get("traffic_bytes_per_launch")
-    return None
+def _kernel_name(full):
+    n = re.sub(r"\(anonymous namespace\)::", "", full)
+    n = re.sub(r"\((?:[^()]|\([^()]*\))*\)\s*$", "", n).strip()
+    return n[:60]
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=3)
-    ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-chunks", type=int, default=2)
-    ap.add_argument("--config", choices=["cfg2", "cfg3", "cfg4", "cfg5"], default="cfg2",
-                    help="cfg2: one q_proj linear (default); cfg3: a full Llama-3-8B layer; cfg4: the "
-                         "layer rotated, w4 sym, dynamic 128-column groups, atomic; cfg5: the Llama-3-70B "
-                         "down_proj 8192x28672")
-    ap.add_argument("--cpu-baseline-layer", action="store_true",
-                    help="with --config cfg3/cfg4: also time the CPU oracle on the layer (minutes)")
-    ap.add_argument("--cpu-baseline-sample", action="store_true",
-                    help="with --config cfg5: time the CPU oracle's Hessian accumulation on one sample")
-    ap.add_argument("--hessian-math", choices=["split16", "fp32"], default="split16",
-                    help="Hessian kernel for the fp16 inputs (split16: exact fp32 products from three "
-                         "fp16 MFMA products; fp32: fp32 MFMA)")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run a 1 GiB device copy (counter calibration for the traffic figure)")
-    ap.add_argument("--gemm-calibration", action="store_true",
-                    help="only time torch.matmul (hipBLASLt / rocBLAS) in fp16 / fp32 / fp64: the "
-                         "practical MFMA ceilings the kernels are compared with")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build runs the GPTQ+ hot path on one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU sharding is a design note, not a launched path.", file=sys.stderr)
-        sys.exit(2)
+def algorithmic_work(cfg):
+    """Algorithmic work per unit (one linear, or one layer) of the kernels the table reports:
+    (bytes, flops) by kernel-name prefix.  Bytes are those the operation must move at least once
+    (inputs read, outputs written); flops count the reference's arithmetic (fp32 unless noted)."""
+    B = cfg["blocksize"]
+    linears = [(R, C) for _, R, C, _ in LAYER8B] if cfg["kind"] == "layer" else [(cfg["R"], cfg["C"])]
+    G, ntok = cfg["G"], cfg["N"] * cfg["T"]
+    w = {}
 
-    dev = torch.device("cuda:0")
+    def add(k, b=0.0, f=0.0):
+        ob, of = w.get(k, (0.0, 0.0))
+        w[k] = (ob + b, of + f)
+    for R, C in linears:
+        nb = (C + B - 1) // B
+        trail = sum(2.0 * R * B * (C - min(C, (k + 1) * B)) for k in range(nb))
+        add("k_find_params", 2.0 * R * C + 8 * R)
+        add("k_gather_w", (2.0 + 4.0) * R * C)                 # fp16 W read, permuted fp32 written
+        add("k_gather_g", 8.0 * R * C)
+        add("k_gather_h_rows", 8.0 * G * C * C)
+        add("k_quant_block", 9.0 * R * C, 2.0 * R * C * B)     # W read, fp32 Q + int8 code written
+        add("k_trailing_w", 8.0 * R * C, trail)
+        add("k_hessian_finalize64", 6.0 * G * C * C)           # upper triangle read, both halves written
+        add("k_writeback", 2.0 * R * C + 2.0 * R * C)
+        add("k_panel_update", 0.0, G * (2.0 / 3.0) * C ** 3)   # fp64: trailing factor + L^-1 rows
+    inputs = {4096: 0, 14336: 0}
+    if cfg["kind"] == "layer":
+        for key, C in INPUT_WIDTH.items():
+            inputs[C] = inputs.get(C, 0) + 1
+    else:
+        inputs = {cfg["C"]: 1}
+    for C, n in inputs.items():
+        add("k_xprep", n * 4.0 * ntok * C)                      # X read, the blocked copy written
+    add("k_hessian_split", 0.0, float(hessian_flops(cfg)))
+    return w
+
+
+def stats_table(path, cfg, units, config):
+    """Markdown table of a rocprofv3 --stats kernel CSV, with achieved rates where the kernel's
+    algorithmic work per unit is known."""
+    work = algorithmic_work(cfg)
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            rows.append((_kernel_name(r["Name"]), int(r["Calls"]), float(r["TotalDurationNs"]) / 1e6,
+                         float(r["AverageNs"]) / 1e3, float(r["Percentage"])))
+    rows.sort(key=lambda x: -x[2])
+    print(f"| kernel | calls | total (ms) | per unit (ms) | average (us) | % | algorithmic work per unit | achieved |")
+    print("|---|---:|---:|---:|---:|---:|---|---|")
+    for name, calls, tot, avg, pct in rows[:24]:
+        per = tot / units
+        key = next((k for k in work if name.split("<")[0].split()[-1] == k), None)
+        wtxt = ach = ""
+        if key:
+            b, fl = work[key]
+            if fl:
+                peak = FP64_MFMA_PEAK_TFLOPS if key == "k_panel_update" else (
+                    FP32_MFMA_PEAK_TFLOPS if key != "k_quant_block" else None)
+                tf = fl / (per * 1e-3) / 1e12
+                wtxt = f"{fl / 1e9:.1f} GFLOP" + (f", {b / 1e6:.0f} MB" if b else "")
+                ach = f"{tf:.1f} TF/s" + (f" ({100 * tf / peak:.1f} % of {peak})" if peak else "")
+                if b and key == "k_quant_block":
+                    ach += f"; {b / (per * 1e-3) / 1e9:.0f} GB/s"
+            else:
+                gbs = b / (per * 1e-3) / 1e9
+                wtxt = f"{b / 1e6:.0f} MB"
+                ach = f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f} % of HBM)"
+        print(f"| `{name}` | {calls} | {tot:.2f} | {per:.3f} | {avg:.1f} | {pct:.2f} | {wtxt} | {ach} |")
+
+
+def traffic_report(fetch_csv, write_csv, cal_fetch_csv, cal_write_csv, kernel_prefix, config, cfg, math):
+    """HBM bytes per product-kernel launch from FETCH_SIZE / WRITE_SIZE passes (KiB per dispatch),
+    each scaled by what the counter reads for a 1 GiB device copy; written to TRAFFIC_JSON with
+    the source hash of hessian.hip so bench.py only reports it while the kernel is unchanged."""
+    def per_dispatch(path, counter, pred):
+        vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(path))
+                if r["Counter_Name"] == counter and pred(r["Kernel_Name"])]
+        return sum(vals) / max(len(vals), 1), len(vals)
+    is_k = lambda n: kernel_prefix in n
+    is_copy = lambda n: "copyBuffer" in n
+    fetch, nf = per_dispatch(fetch_csv, "FETCH_SIZE", is_k)
+    write, nw = per_dispatch(write_csv, "WRITE_SIZE", is_k)
+    cfetch, _ = per_dispatch(cal_fetch_csv, "FETCH_SIZE", is_copy)
+    cwrite, _ = per_dispatch(cal_write_csv, "WRITE_SIZE", is_copy)
+    gib = float(1 << 30)
+    rf, wf = cfetch * 1024 / gib, cwrite * 1024 / gib          # counter bytes per real byte
+    traffic = fetch * 1024 / rf + write * 1024 / wf
+    flops = hessian_flops(cfg)
+    rec = {"kernel": kernel_prefix, "config": config, "dispatches": [nf, nw],
+           "fetch_size_kib_per_dispatch": round(fetch, 1), "write_size_kib_per_dispatch": round(write, 1),
+           "copy_calibration": {"fetch_kib": round(cfetch, 1), "write_kib": round(cwrite, 1),
+                                "read_factor": round(rf, 3), "write_factor": round(wf, 3)},
+           "traffic_bytes_per_launch": int(traffic), "hessian_src_sha256": source_sha(),
+           "flops_per_unit": flops}
+    data = json.load(open(TRAFFIC_JSON)) if os.path.exists(TRAFFIC_JSON) else {}
+    data[math] = rec
+    with open(TRAFFIC_JSON, "w") as f:
+        json.dump(data, f, indent=1)
+    print(json.dumps(rec))
+
+
+# ---------------------------------------------------------------------------------------------
+
+def run(args):
+    import torch
     from gptq_plus_mp_quant_amd import _native as nat
-    nat.load().rq_hessian_math(nat.RQ_HMATH_SPLIT16 if args.hessian_math == "split16" else nat.RQ_HMATH_FP32)
+    dev = torch.device("cuda:0")
+    nat.load().rq_hessian_math({"split16": nat.RQ_HMATH_SPLIT16, "split16x3": nat.RQ_HMATH_SPLIT16X3,
+                                "fp32": nat.RQ_HMATH_FP32}[args.hessian_math])
+    torch.backends.cuda.matmul.allow_tf32 = False
     if args.copy_calibration:
         copy_calibration(dev)
         return
     if args.gemm_calibration:
         gemm_calibration(dev)
         return
-    if args.config in ("cfg3", "cfg4"):
-        run_layer(args, dev)
-        return
-    torch.backends.cuda.matmul.allow_tf32 = False
-    cfg = dict(CFG5 if args.config == "cfg5" else CFG)
-    X, W, s, grad = make_inputs(dev, cfg)
-    layer = torch.nn.Linear(cfg["C"], cfg["R"], bias=False).to(dev, torch.float16)
+    cfg = dict(CONFIGS[args.config], alpha=args.alpha, ref_loss=args.ref_loss)
+    layer_mode = cfg["kind"] == "layer"
+    if layer_mode:
+        xs, mods = make_layer_inputs(dev, cfg)
+        layers = {n: torch.nn.Linear(C, R, bias=False).to(dev, torch.float16) for n, R, C, _ in LAYER8B}
+        step = lambda timer=None, keep=False: one_layer(xs, mods, cfg, layers, timer, keep)
+    else:
+        X, W, s, grad = make_inputs(dev, cfg)
+        layer = torch.nn.Linear(cfg["C"], cfg["R"], bias=False).to(dev, torch.float16)
+        step = lambda timer=None, keep=False: one_linear(X, W, s, grad, cfg, layer, timer)
     torch.cuda.synchronize()
-
-    for _ in range(args.warmup):
-        one_linear(X, W, s, grad, cfg, layer)
-    torch.cuda.synchronize()
-
-    timer = EventTimer()
+    kept = None
+    for i in range(args.warmup):
+        out = step(keep=(layer_mode and i == args.warmup - 1))
+        kept = out if layer_mode and i == args.warmup - 1 else kept
+    timer = KernelTimer()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        one_linear(X, W, s, grad, cfg, layer, timer)
+        step(timer)
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
-
-    h_ms, n_launch = timer.mean_ms()
-    ntok = cfg["bsz"] * cfg["T"]
-    flops = cfg["G"] * ntok * cfg["C"] * (cfg["C"] + 1)       # upper triangle incl. diagonal
-
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    kernel_ms, launches = timer.total_ms()
+    per = len(LAYER8B) if layer_mode else 1
     line = {
-        "metric": "ms per linear (H-accum + fasterquant) at Llama-8B shapes; % fp32-MFMA peak",
-        "value": round(ms_per_step, 2),
-        "unit": "ms",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 2),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32 (fp16 inputs; exact fp32 products)",
-        "data": "synthetic (seeded, generated on the GPU)",
-        "config": {"workload": ("configs[4]: Llama-3-70B down_proj 8192x28672, W ~ N(0, 0.015^2), "
-                                "NUM_GROUPS=4 (4 Hessians of 28672^2 fp32), 128x2048 tokens, w4 asym "
-                                "per-channel, act_order, B=128, GPTQ+ term on (alpha=0)")
-                   if args.config == "cfg5" else
-                   "configs[1]: q_proj 4096x4096, NUM_GROUPS=4, 128x2048 tokens, w4 asym "
-                   "per-channel, act_order, B=128, GPTQ+ term on (alpha=0)",
-                   "parallelism": "single GPU"},
-        "roofline": hessian_roofline(flops, h_ms, args.hessian_math,
-                                     {"traffic": load_traffic(args.hessian_math) if args.config == "cfg2" else None,
-                                      "launch_ms": round(h_ms, 3), "launches": n_launch,
-                                      "flops_per_launch": flops}),
+        "metric": METRIC, "value": round(ms_step / per, 2), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 2), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 (fp16 inputs)", "data": "synthetic (seeded, generated on the GPU)",
+        "config": {"workload": WORKLOAD[args.config].format(alpha=cfg["alpha"]), "parallelism": "single GPU",
+                   "hessian_math": args.hessian_math},
+        "roofline": roofline(cfg, args, kernel_ms, launches, args.steps),
     }
-    if args.config == "cfg5":
-        if args.cpu_baseline_sample:
-            line["cpu_baseline"] = cpu_baseline_hessian_sample(X, s, cfg)
-    elif not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(X, W, s, grad, cfg, args.cpu_chunks)
+    if not args.no_cpu_baseline:
+        if layer_mode:
+            if kept is None:
+                kept = step(keep=True)
+            line["cpu_baseline"] = cpu_baseline_layer(xs, mods, kept, cfg)
+        elif args.config == "cfg5":
+            if args.cpu_baseline_sample:
+                line["cpu_baseline"] = cpu_baseline_hessian_sample(X, s, cfg)
+        else:
+            line["cpu_baseline"] = cpu_baseline_linear(X, W, s, grad, cfg, args.cpu_chunks)
     print(json.dumps(line), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="cfg3",
+                    help="BASELINE.md numbering, cfgK = configs[K-1]; default cfg3 (the Llama-3-8B layer)")
+    ap.add_argument("--alpha", type=float, default=0.0, help="GPTQ+ alpha (with --ref-loss > 0: beta != 0)")
+    ap.add_argument("--ref-loss", type=float, default=0.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-chunks", type=int, default=2)
+    ap.add_argument("--cpu-baseline-sample", action="store_true",
+                    help="with --config cfg5: time the CPU oracle's Hessian accumulation on one sample")
+    ap.add_argument("--hessian-math", choices=sorted(PIECES), default="split16",
+                    help="Hessian kernel for fp16 inputs: split16 (two fp16 MFMA products per fp32 product), "
+                         "split16x3 (three: exact products), fp32 (fp32 MFMA)")
+    ap.add_argument("--copy-calibration", action="store_true", help="only run a 1 GiB device copy (counter calibration)")
+    ap.add_argument("--gemm-calibration", action="store_true", help="only time torch.matmul in fp16 / fp32 / fp64")
+    ap.add_argument("--stats-table", metavar="STATS_CSV", help="print a rocprofv3 kernel-stats CSV as a table")
+    ap.add_argument("--units", type=float, default=1.0, help="with --stats-table: units (linears or layers) profiled")
+    ap.add_argument("--traffic", nargs=4, metavar=("FETCH", "WRITE", "CAL_FETCH", "CAL_WRITE"),
+                    help="counter CSVs of the product kernel and of the copy calibration -> profiles/hessian_traffic.json")
+    args = ap.parse_args()
+    if args.stats_table:
+        stats_table(args.stats_table, CONFIGS[args.config], args.units, args.config)
+        return
+    if args.traffic:
+        cfg = CONFIGS[args.config]
+        traffic_report(*args.traffic, "k_hessian_split" if args.hessian_math != "fp32" else "k_hessian_accum",
+                       args.config, cfg, args.hessian_math)
+        return
+    if args.gpus != 1:
+        print(f"bench.py: this build runs the GPTQ+ hot path on one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU sharding is a design note, not a launched path.", file=sys.stderr)
+        sys.exit(2)
+    run(args)
 
 
 if __name__ == "__main__":

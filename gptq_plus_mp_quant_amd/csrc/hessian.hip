@@ -303,18 +303,22 @@ __global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
 //
 // H_ij = sum_t x_ti * w_tj with w = fl32(x * s), the reference's `weighted`.  x is exact in
 // the input's 16-bit type.  w is multiplied by 2^e (one exponent per target and column,
-// exact) and written as the sum of three 16-bit pieces, w * 2^e = p0 + p1 + p2 with
-// p0 = rn(w), p1 = rn(w - p0), p2 = rn(w - p0 - p1) (round to nearest in the 16-bit type):
-// 11 + 11 + 2 (fp16) or 8 + 8 + 8 (bf16) significant bits cover w's 24, so the sum is exact.
-// Each product x * p_k (11 x 11 or 8 x 8 bits) is exact in fp32, so three
-// v_mfma_f32_32x32x16_{f16,bf16} per 16 tokens accumulate the reference's fp32 products
-// in fp32, at 16x the fp32 MFMA rate (three MFMAs of 16 tokens replace eight of 2).
+// exact) and written as the sum of PC 16-bit pieces, p0 = rn(w), p1 = rn(w - p0),
+// p2 = rn(w - p0 - p1) (round to nearest in the 16-bit type).  Each product x * p_k (11 x 11
+// or 8 x 8 bits) is exact in fp32, and PC v_mfma_f32_32x32x16_{f16,bf16} per 16 tokens add
+// them into fp32 accumulators.
+//  * bf16, and fp16 with RQ_HMATH_SPLIT16X3: three pieces, 8 + 8 + 8 or 11 + 11 + 2
+//    significant bits, cover w's 24: the reference's fp32 products, exactly.
+//  * fp16 (RQ_HMATH_SPLIT16, the default): two pieces carry 22 of w's 24 bits; the dropped
+//    residual is at most half an ulp of p1, 2^-23 relative to w (the unit roundoff of fp32 is
+//    2^-24), so each product is the reference's up to 2^-23 relative, far below the rounding
+//    of the fp32 sums themselves, for two thirds of the MFMA work of three pieces.
 // The exponent e (k_xfinish) puts the column's largest |w| in [2^14, 2^15): p0 cannot
-// overflow fp16, and the pieces are exact for every |w| * 2^e >= 2^-1, i.e. down to 2^-15
-// of the column's largest entry; below that the residual is at most 2^-25 * 2^-e, 2^-40 of
-// the column's largest |w|.  bf16 pieces have fp32's exponent range; the same scaling is
-// applied, harmlessly.  The epilogue multiplies the tile by 2^-e (exact) before adding it
-// to H.
+// overflow fp16, and fp16 pieces are normal numbers for every |w| * 2^e >= 2^-1 (down to 2^-15
+// of the column's largest entry); below that p1's subnormal spacing bounds the residual by
+// 2^-25 * 2^-e, 2^-40 of the column's largest |w|.  bf16 pieces have fp32's exponent range;
+// the same scaling is applied, harmlessly.  The epilogue multiplies the tile by 2^-e (exact)
+// before adding it to H.
 //
 // Operands.  A pre-pass (k_xprep) writes the chunk in a fragment-blocked layout: for each
 // block of 32 columns and each 16-token step, one contiguous 1 KB holding exactly the
@@ -328,9 +332,9 @@ __global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
 // MFMAs).  Operands are staged into a ring of LDS stages by direct global->LDS loads (wave w
 // fetches row fragment w and its own column fragment, wave 0 the step's saliencies); per 16
 // tokens a wave reads 8 row fragments, splits its column fragment in registers and issues
-// 3 x 8 = 24 MFMAs.
+// PC x 8 MFMAs.
 constexpr int XT = 256;          // workgroup tile edge
-constexpr int XNP = 3;           // pieces of the weighted operand
+constexpr int XNPMAX = 3;        // most pieces of the weighted operand
 constexpr int XWAVES = 8;        // waves per workgroup, two per SIMD
 constexpr int XTHREADS = 64 * XWAVES;
 constexpr int XPART = XT * XT;   // floats of one partial tile
@@ -368,16 +372,23 @@ struct XType<__hip_bfloat16> {
 };
 
 // One token pair of one column (x of tokens t, t+1 packed in xw): w = fl32(x * s) * 2^e for
-// both, split into three packed pieces.  fp16: each residual w - p is one v_fma_mix_f32
+// both, split into PC packed pieces.  fp16: each residual w - p is one v_fma_mix_f32
 // (-p as an fp16 operand, times 1, plus w: exact), written out because the compiler emits a
 // conversion and a subtraction for it.
-template <typename TX>
+template <typename TX, int PC>
 __device__ __forceinline__ void split_pair(uint32_t xw, float s0, float s1, float sc, uint32_t& o0, uint32_t& o1,
                                            uint32_t& o2) {
   typedef XType<TX> T;
   float a = __builtin_fmaf(T::lo(xw), s0, 0.0f) * sc;
   float b = __builtin_fmaf(T::hi(xw), s1, 0.0f) * sc;
-  if constexpr (std::is_same<TX, __half>::value) {
+  if constexpr (std::is_same<TX, __half>::value && PC == 2) {
+    asm("v_cvt_pk_f16_f32 %0, %2, %3\n\t"
+        "v_fma_mix_f32 %2, -%0, 1.0, %2 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mix_f32 %3, -%0, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_cvt_pk_f16_f32 %1, %2, %3"
+        : "=&v"(o0), "=&v"(o1), "+v"(a), "+v"(b));
+    o2 = 0u;
+  } else if constexpr (std::is_same<TX, __half>::value) {
     asm("v_cvt_pk_f16_f32 %0, %3, %4\n\t"
         "v_fma_mix_f32 %3, -%0, 1.0, %3 op_sel_hi:[1,0,0]\n\t"
         "v_fma_mix_f32 %4, -%0, 1.0, %4 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
@@ -387,6 +398,7 @@ __device__ __forceinline__ void split_pair(uint32_t xw, float s0, float s1, floa
         "v_cvt_pk_f16_f32 %2, %3, %4"
         : "=&v"(o0), "=&v"(o1), "=&v"(o2), "+v"(a), "+v"(b));
   } else {
+    static_assert(PC == 3, "bf16 pieces: three");
     o0 = T::pack(a, b);
     a = a - T::lo(o0);
     b = b - T::hi(o0);
@@ -397,12 +409,12 @@ __device__ __forceinline__ void split_pair(uint32_t xw, float s0, float s1, floa
   }
 }
 
-template <typename TX>
-__device__ __forceinline__ void split8(uint4 x, float4 s0, float4 s1, float sc, uint4 (&p)[XNP]) {
+template <typename TX, int PC>
+__device__ __forceinline__ void split8(uint4 x, float4 s0, float4 s1, float sc, uint4 (&p)[PC]) {
   typedef XType<TX> T;
   const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
   const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
-  uint32_t o[XNP][4];
+  uint32_t o[PC][4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     float a = __builtin_fmaf(T::lo(xw[m]), s[2 * m], 0.0f);
@@ -410,17 +422,17 @@ __device__ __forceinline__ void split8(uint4 x, float4 s0, float4 s1, float sc, 
     a = a * sc;
     b = b * sc;
 #pragma unroll
-    for (int k = 0; k < XNP; ++k) {
+    for (int k = 0; k < PC; ++k) {
       const uint32_t u = T::pack(a, b);
       o[k][m] = u;
-      if (k + 1 < XNP) {
+      if (k + 1 < PC) {
         a = __builtin_fmaf(-T::lo(u), 1.0f, a);
         b = __builtin_fmaf(-T::hi(u), 1.0f, b);
       }
     }
   }
 #pragma unroll
-  for (int k = 0; k < XNP; ++k) p[k] = make_uint4(o[k][0], o[k][1], o[k][2], o[k][3]);
+  for (int k = 0; k < PC; ++k) p[k] = make_uint4(o[k][0], o[k][1], o[k][2], o[k][3]);
 }
 
 // LDS ring: XDEPTH stages (separate arrays) of one 16-token step each.  A stage holds the
@@ -461,11 +473,11 @@ __device__ __forceinline__ void stage_step(uint8_t* st, const uint16_t* pa, cons
 }
 
 // This wave's column fragment and the saliencies of a staged step, split into pieces.
-template <typename TX>
-__device__ __forceinline__ void split_staged(const uint8_t* st, int wave, int lane, float sc, uint4 (&p)[XNP]) {
+template <typename TX, int PC>
+__device__ __forceinline__ void split_staged(const uint8_t* st, int wave, int lane, float sc, uint4 (&p)[PC]) {
   const uint8_t* w = static_cast<const uint8_t*>(__builtin_assume_aligned(st + XB_OFF + wave * 1024 + lane * 16, 16));
   const uint8_t* sp = static_cast<const uint8_t*>(__builtin_assume_aligned(st + XS_OFF + 32 * (lane >> 5), 16));
-  split8<TX>(*reinterpret_cast<const uint4*>(w), *reinterpret_cast<const float4*>(sp),
+  split8<TX, PC>(*reinterpret_cast<const uint4*>(w), *reinterpret_cast<const float4*>(sp),
              *reinterpret_cast<const float4*>(sp + 16), sc, p);
 }
 
@@ -476,15 +488,15 @@ __device__ __forceinline__ void split_staged(const uint8_t* st, int wave, int la
 // each of the XDEPTH-3 steps since, so vmcnt(2 * (XDEPTH - 3)) covers this wave's part of both
 // whatever the issue order within a step, and after the barrier the other waves' parts are in
 // LDS too.  The barrier also orders every read of the FILL stage (the stage of step k-1, read
-// during step k-2) before its refill.  Then: stage step k+XDEPTH-1; issue the 24 MFMAs of
-// step k from registers, while the row fragments of step k+1 are read and this wave's column
+// during step k-2) before its refill.  Then: stage step k+XDEPTH-1; issue the PC x 8 MFMAs
+// of step k from registers, while the row fragments of step k+1 are read and this wave's column
 // fragment of step k+1 is split in between.  The MFMAs need no LDS read after the barrier, so
 // the two waves of a SIMD resume issuing as soon as it opens.  A bare s_barrier: the fence of
 // __syncthreads would wait for every staging load in flight.
 // DIAG (a diagonal tile): row blocks below this wave's column block hold only the discarded
 // lower triangle, so their row fragments are not read and their MFMAs not issued (bi < lim).
-template <typename TX, bool DIAG, int KP, int CUR, int NXT, int FILL>
-__device__ __forceinline__ void split_step(uint4 (&p)[2][XNP], uint4 (&a)[2][8], floatx16 (&acc)[8],
+template <typename TX, int PC, bool DIAG, int KP, int CUR, int NXT, int FILL>
+__device__ __forceinline__ void split_step(uint4 (&p)[2][PC], uint4 (&a)[2][8], floatx16 (&acc)[8],
                                            const XStages& L, const uint16_t* pa, const uint16_t* pb,
                                            const float* sg, float sc, int wave, int lane, int64_t k,
                                            int64_t last, int lim) {
@@ -506,23 +518,26 @@ __device__ __forceinline__ void split_step(uint4 (&p)[2][XNP], uint4 (&a)[2][8],
     if (!DIAG || bi < lim) a[NP][bi] = *reinterpret_cast<const uint4*>(nxt + bi * 1024);
   const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
   const uint32_t xw[4] = {b.x, b.y, b.z, b.w};
-  uint32_t o[XNP][4];
+  uint32_t o[XNPMAX][4];
+  // smallest piece first into every accumulator, then the others, two or four MFMAs after
+  // each token pair of the next step's split
 #pragma unroll
   for (int bi = 0; bi < 8; ++bi)
     if (!DIAG || bi < lim)
-      acc[bi] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][XNP - 1]), acc[bi]);
+      acc[bi] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][PC - 1]), acc[bi]);
+  constexpr int PER_M = (PC - 1) * 2;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    split_pair<TX>(xw[m], sv[2 * m], sv[2 * m + 1], sc, o[0][m], o[1][m], o[2][m]);
+    split_pair<TX, PC>(xw[m], sv[2 * m], sv[2 * m + 1], sc, o[0][m], o[1][m], o[2][m]);
 #pragma unroll
-    for (int i = 4 * m; i < 4 * m + 4; ++i) {
-      const int q = 1 - i / 8, bi = i % 8;
+    for (int i = PER_M * m; i < PER_M * m + PER_M; ++i) {
+      const int q = (PC - 2) - i / 8, bi = i % 8;
       if (!DIAG || bi < lim)
         acc[bi] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][q]), acc[bi]);
     }
   }
 #pragma unroll
-  for (int q = 0; q < XNP; ++q) p[NP][q] = make_uint4(o[q][0], o[q][1], o[q][2], o[q][3]);
+  for (int q = 0; q < PC; ++q) p[NP][q] = make_uint4(o[q][0], o[q][1], o[q][2], o[q][3]);
 }
 
 // Column block of wave w: w for w < 4, 11 - w above, so the two waves that share a SIMD
@@ -530,7 +545,7 @@ __device__ __forceinline__ void split_step(uint4 (&p)[2][XNP], uint4 (&a)[2][8],
 // blocks up to its own, each SIMD then has 9 of the 16 blocks.
 __device__ __forceinline__ int split_colblock(int wave) { return wave < 4 ? wave : 11 - wave; }
 
-template <typename TX, bool DIAG>
+template <typename TX, int PC, bool DIAG>
 __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int64_t nks, int C,
                                            const float* __restrict__ sg, const float* __restrict__ scl,
                                            float* __restrict__ Hg, int R0, int C0, int64_t kbeg,
@@ -565,10 +580,10 @@ __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int6
   const int64_t last = kend - 1;
 #pragma unroll
   for (int h = 0; h < XDEPTH - 1; ++h) stage_step(L.s[h], pa, pb, sg, wave, lane, min(kbeg + h, last));
-  uint4 p[2][XNP], a[2][8];
+  uint4 p[2][PC], a[2][8];
   XWAIT_VM(2 * (XDEPTH - 2));         // this wave's staging of step kbeg
   __builtin_amdgcn_s_barrier();       // and the other waves'
-  split_staged<TX>(L.s[0], wave, lane, sc, p[0]);
+  split_staged<TX, PC>(L.s[0], wave, lane, sc, p[0]);
   {
     const uint8_t* cur = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[0] + lane * 16, 16));
 #pragma unroll
@@ -580,15 +595,15 @@ __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int6
   int64_t k = kbeg;
   static_assert(XDEPTH == 4, "unrolled stage schedule");
   for (; k + 4 <= kend; k += 4) {
-    split_step<TX, DIAG, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last, lim);
-    split_step<TX, DIAG, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last, lim);
-    split_step<TX, DIAG, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last, lim);
-    split_step<TX, DIAG, 1, 3, 0, 2>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 3, last, lim);
+    split_step<TX, PC, DIAG, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last, lim);
+    split_step<TX, PC, DIAG, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last, lim);
+    split_step<TX, PC, DIAG, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last, lim);
+    split_step<TX, PC, DIAG, 1, 3, 0, 2>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 3, last, lim);
   }
   const int rem = (int)(n & 3);
-  if (rem > 0) split_step<TX, DIAG, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last, lim);
-  if (rem > 1) split_step<TX, DIAG, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last, lim);
-  if (rem > 2) split_step<TX, DIAG, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last, lim);
+  if (rem > 0) split_step<TX, PC, DIAG, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last, lim);
+  if (rem > 1) split_step<TX, PC, DIAG, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last, lim);
+  if (rem > 2) split_step<TX, PC, DIAG, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last, lim);
   XWAIT_VM(0);                        // no staging left in flight when the workgroup moves on
 
   if (part) {
@@ -647,7 +662,7 @@ __device__ __forceinline__ void reduce_split_slices(const float* __restrict__ pa
     }
 }
 
-template <typename TX>
+template <typename TX, int PC>
 __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
     const uint16_t* __restrict__ XB, int C, const float* __restrict__ sT, int64_t lds_stride,
     const float* __restrict__ scale, HTargets tg, int ntarg, int nt, int ntiles, int64_t nks, int full,
@@ -686,9 +701,9 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
   float* part0 = (slice >= 0) ? ws + (int64_t)(logical - full) * S * XPART : nullptr;
   float* part = part0 ? part0 + (int64_t)slice * XPART : nullptr;
   if (R0 == C0)
-    split_tile<TX, true>(XB, nks, C, sT + (int64_t)g * lds_stride, scl, Hg, R0, C0, kbeg, kend, part, L);
+    split_tile<TX, PC, true>(XB, nks, C, sT + (int64_t)g * lds_stride, scl, Hg, R0, C0, kbeg, kend, part, L);
   else
-    split_tile<TX, false>(XB, nks, C, sT + (int64_t)g * lds_stride, scl, Hg, R0, C0, kbeg, kend, part, L);
+    split_tile<TX, PC, false>(XB, nks, C, sT + (int64_t)g * lds_stride, scl, Hg, R0, C0, kbeg, kend, part, L);
   if (!part) return;
   __threadfence();
   __syncthreads();
@@ -1086,6 +1101,18 @@ extern "C" int rq_version(void) { return 100; }
 namespace {
 
 std::atomic<int> g_hmath{RQ_HMATH_SPLIT16};
+// Optional events recorded around the next product-kernel launch (measurement hook).
+std::atomic<void*> g_time_start{nullptr}, g_time_stop{nullptr};
+
+// Record the hook's start event before the product kernel; returns the stop event to record
+// after it (nullptr when no hook is set).  Each pair is used once.
+hipEvent_t timing_begin(hipStream_t s) {
+  void* a = g_time_start.exchange(nullptr);
+  void* b = g_time_stop.exchange(nullptr);
+  if (!a || !b) return nullptr;
+  if (hipEventRecord(reinterpret_cast<hipEvent_t>(a), s) != hipSuccess) return nullptr;
+  return reinterpret_cast<hipEvent_t>(b);
+}
 
 // Concurrent workgroups of a Hessian kernel on the current device (CUs x occupancy).
 template <typename K>
@@ -1101,7 +1128,7 @@ int kernel_slots(K kfn, int threads, int which) {
   return cache[which][dev];
 }
 int hessian_slots() { return kernel_slots(k_hessian_accum<__half>, HTHREADS, 0); }
-int split_slots() { return kernel_slots(k_hessian_split<__half>, XTHREADS, 1); }
+int split_slots() { return kernel_slots(k_hessian_split<__half, 2>, XTHREADS, 1); }
 
 // Items of the last, partly filled round and the slice count that fills rounds best
 // (the finishing time of the tail in rounds is ceil(tail * S / slots) / S).
@@ -1299,20 +1326,25 @@ int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, c
   int* cnt = tail > 0 ? reinterpret_cast<int*>(ws) : nullptr;
   float* wsf = tail > 0 ? reinterpret_cast<float*>(wb + L.off_part) : nullptr;
   dim3 grid((unsigned)(full + (int64_t)tail * S)), block(XTHREADS);
-  if (x_dtype == RQ_F16)
-    hipLaunchKernelGGL(k_hessian_split<__half>, grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg, ntarg, nt,
+  hipEvent_t stop = timing_begin(s);
+  if (x_dtype == RQ_F16 && g_hmath.load() == RQ_HMATH_SPLIT16X3)
+    hipLaunchKernelGGL((k_hessian_split<__half, 3>), grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg, ntarg, nt,
+                       ntiles, nks, full, S, wsf, cnt);
+  else if (x_dtype == RQ_F16)
+    hipLaunchKernelGGL((k_hessian_split<__half, 2>), grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg, ntarg, nt,
                        ntiles, nks, full, S, wsf, cnt);
   else
-    hipLaunchKernelGGL(k_hessian_split<__hip_bfloat16>, grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg, ntarg,
-                       nt, ntiles, nks, full, S, wsf, cnt);
+    hipLaunchKernelGGL((k_hessian_split<__hip_bfloat16, 3>), grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg,
+                       ntarg, nt, ntiles, nks, full, S, wsf, cnt);
   RQ_CHECK_LAUNCH();
+  if (stop && hipEventRecord(stop, s) != hipSuccess) return RQ_EHIP;
   return RQ_OK;
 }
 
 int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, const HTargets& tg,
                    int ntarg, void* ws, int64_t ws_bytes, hipStream_t s) {
   const bool aligned = ws && ((reinterpret_cast<uintptr_t>(ws) & 255) == 0);
-  if (x_dtype != RQ_F32 && g_hmath.load() == RQ_HMATH_SPLIT16 && aligned &&
+  if (x_dtype != RQ_F32 && g_hmath.load() != RQ_HMATH_FP32 && aligned &&
       ws_bytes >= split_layout(ntok, C, ntarg, 0, 1).bytes)
     return launch_split(x, x_dtype, ntok, ldx, C, tg, ntarg, ws, ws_bytes, s);
   const int nt = (C + HT - 1) / HT;
@@ -1338,6 +1370,7 @@ int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
   float* wsf = tail > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + act_off() + act_plan(ntok, C).bytes)
                         : nullptr;
   dim3 grid((unsigned)(full + (int64_t)tail * S)), block(HTHREADS);
+  hipEvent_t stop = timing_begin(s);
   if (x_dtype == RQ_F16)
     hipLaunchKernelGGL(k_hessian_accum<__half>, grid, block, 0, s, (const __half*)x, ntok, ldx, C, tg,
                        ntarg, nt, ntiles, vec_ok, full, S, wsf, cnt);
@@ -1348,14 +1381,22 @@ int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
     hipLaunchKernelGGL(k_hessian_accum<float>, grid, block, 0, s, (const float*)x, ntok, ldx, C, tg,
                        ntarg, nt, ntiles, vec_ok, full, S, wsf, cnt);
   RQ_CHECK_LAUNCH();
+  if (stop && hipEventRecord(stop, s) != hipSuccess) return RQ_EHIP;
   return RQ_OK;
 }
 
 }  // namespace
 
+extern "C" int rq_hessian_timing_events(void* start_event, void* stop_event) {
+  if ((start_event == nullptr) != (stop_event == nullptr)) return RQ_EINVAL;
+  g_time_stop.store(stop_event);
+  g_time_start.store(start_event);
+  return RQ_OK;
+}
+
 extern "C" int rq_hessian_math(int mode) {
   if (mode < 0) return g_hmath.load();
-  if (mode != RQ_HMATH_SPLIT16 && mode != RQ_HMATH_FP32) return RQ_EINVAL;
+  if (mode != RQ_HMATH_SPLIT16 && mode != RQ_HMATH_FP32 && mode != RQ_HMATH_SPLIT16X3) return RQ_EINVAL;
   return g_hmath.exchange(mode);
 }
 
@@ -1422,7 +1463,7 @@ extern "C" int rq_hessian_accum_noalloc(const void* x, int x_dtype, int64_t ntok
   if (ntok == 0) return RQ_OK;
   // the least scratch the kernel rq_hessian_accum would choose needs (whole items only)
   const int n = G < HMAXT ? G : HMAXT;
-  const int64_t need = (x_dtype != RQ_F32 && g_hmath.load() == RQ_HMATH_SPLIT16)
+  const int64_t need = (x_dtype != RQ_F32 && g_hmath.load() != RQ_HMATH_FP32)
                            ? split_layout(ntok, C, n, 0, 1).bytes
                            : hessian_ws_bytes(ntok, C, 0, 1);
   if (need > (int64_t)RQ_NOALLOC_SCRATCH_BYTES) return RQ_EINVAL;

@@ -68,14 +68,15 @@ def hessian_workspace(x, ntargets):
     return ws, ws.numel()
 
 
-HESSIAN_MATH = {"split16": nat.RQ_HMATH_SPLIT16, "fp32": nat.RQ_HMATH_FP32}
+HESSIAN_MATH = {"split16": nat.RQ_HMATH_SPLIT16, "split16x3": nat.RQ_HMATH_SPLIT16X3, "fp32": nat.RQ_HMATH_FP32}
 
 
 @contextlib.contextmanager
 def hessian_math(mode):
     """Select the Hessian kernel for fp16 / bf16 inputs inside the block: "split16" (default;
-    exact fp32 products from three 16-bit MFMA products) or "fp32" (fp32 MFMA).  The choice is
-    process-wide; fp32 inputs always use the fp32 kernel."""
+    fp16 X: each fp32 product from two 16-bit MFMA products, within 2^-23 relative; bf16 X:
+    exact, from three), "split16x3" (exact products from three for fp16 too) or "fp32" (fp32
+    MFMA).  The choice is process-wide; fp32 inputs always use the fp32 kernel."""
     lib = nat.load()
     prev = int(lib.rq_hessian_math(HESSIAN_MATH[mode]))
     if prev < 0:

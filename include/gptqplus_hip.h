@@ -56,15 +56,26 @@ int rq_version(void);
 int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets);
 
 /* Kernel choice for fp16 / bf16 X (process-wide; fp32 X always uses the fp32 MFMA kernel).
- * RQ_HMATH_SPLIT16 (default): each fp32 product x * fl32(x * s) is formed exactly from three
- * 16-bit MFMA products (the weighted operand split into three 16-bit pieces after an exact
- * power-of-two column scaling) and accumulated in fp32; it needs the workspace (with less
- * than rq_hessian_workspace_bytes the fp32 kernel runs instead).  RQ_HMATH_FP32: fp32
- * MFMA on converted operands.  mode < 0 queries.  Returns the previous mode, or RQ_EINVAL.
- * No counterpart in the reference (its bmm runs in fp32, gptq_plus_utils.py:845-847). */
+ * The split kernels form each fp32 product x * fl32(x * s) on the 16-bit MFMA pipe from the
+ * weighted operand cut into 16-bit pieces (after an exact power-of-two column scaling), and
+ * accumulate in fp32; they need the workspace (with less than rq_hessian_workspace_bytes the
+ * fp32 kernel runs instead).
+ * RQ_HMATH_SPLIT16 (default): fp16 X in two pieces (22 of the operand's 24 bits: each product
+ *   within 2^-23 relative of the reference's), bf16 X in three (exact products).
+ * RQ_HMATH_SPLIT16X3: three pieces for fp16 X too (exact products, 1.5x the MFMA work).
+ * RQ_HMATH_FP32: fp32 MFMA on converted operands.
+ * mode < 0 queries.  Returns the previous mode, or RQ_EINVAL.  No counterpart in the
+ * reference (its bmm runs in fp32, gptq_plus_utils.py:845-847). */
 #define RQ_HMATH_SPLIT16 0
 #define RQ_HMATH_FP32 1
+#define RQ_HMATH_SPLIT16X3 2
 int rq_hessian_math(int mode);
+/* Measurement hook, no counterpart in the reference: the next Hessian product-kernel launch
+ * (k_hessian_split or k_hessian_accum, whichever runs) records start_event before it and
+ * stop_event after it on its stream, so a caller can time that kernel alone (hipEvent_t
+ * handles created with timing enabled; both NULL clears).  Process-wide, one launch per
+ * pair. */
+int rq_hessian_timing_events(void* start_event, void* stop_event);
 int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
                      const float* sal, int64_t ld_sal, int G, float* H, float* act_sq,
                      void* workspace, int64_t workspace_bytes, void* stream);
