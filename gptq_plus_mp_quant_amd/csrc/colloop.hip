@@ -26,13 +26,14 @@
 //
 // k_trailing_w (Z identically zero, frozen / block_gd): W[:, i2:] -= Err Hinv[i1:i2, i2:] with
 // the product formed as a k-ordered fused multiply-add chain on the matrix cores, bit-identical
-// to the reference's CPU matmul (see the kernel).  Otherwise:
-// k_trailing: W[:, i2:] -= Err Hinv[i1:i2, i2:] + (count GH[:, i2:] - (Z1 D) Hinv[i1:i2, i2:])
-// and GH[:, i2:] -= Z1 Hinv[i1:i2, i2:], 64x64 output tiles, fp32 16x16x4 MFMA, K = count
-// streamed through LDS in slabs of 32.  The Z terms are skipped when Z is identically zero.
-// In the surrogate modes the GH[:, i2:] of the first term is GH + beta_row * (W - W_anchor)
-// (outer refresh "surrogate_block", :1500-1511), the GH update itself is unchanged; in
-// block_gd the whole W update is scaled by second_order_scale (:1546-1549).
+// to the reference's CPU matmul (see the kernel).  Otherwise k_trailing_z:
+// W[:, i2:] -= Err Hinv[i1:i2, i2:] + (count GH[:, i2:] - (Z1 D) Hinv[i1:i2, i2:]) and
+// GH[:, i2:] -= Z1 Hinv[i1:i2, i2:], the three products formed the same way, so with equal
+// inputs W and GH are the reference's bit for bit.  In the surrogate modes the GH[:, i2:] of
+// the first term is GH + beta_row * (W - W_anchor) (outer refresh "surrogate_block",
+// :1500-1511), the GH update itself is unchanged; in block_gd the whole W update is scaled by
+// second_order_scale (:1546-1549).  k_trailing (fp32 16x16x4 MFMA, 64x64 tiles) takes the
+// shapes those two cannot (a block width that is not a multiple of 8, unaligned operands).
 #include <type_traits>
 
 #include "rq_common.h"
@@ -579,6 +580,176 @@ __global__ __launch_bounds__(256, 2) void k_trailing_w(TwArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// k_trailing_z: the outer update with the GPTQ+ terms (gptq_plus_utils.py:1500-1570), every
+// product a k-ordered fused multiply-add chain like the reference's CPU matmuls (K = count):
+//   second = Err1 @ Hinv[i1:i2, i2:]
+//   zd     = (Z1 * D) @ Hinv[i1:i2, i2:]      (torch's einsum("ij,j,jk->ik") on CPU is exactly
+//                                               this: the elementwise product, then the matmul)
+//   zz     = Z1 @ Hinv[i1:i2, i2:]
+//   W  -= second + (count * gh_eff - zd)      (block_gd: W -= sos * (...))
+//   GH -= zz
+// with gh_eff = GH, or GH + beta_r * (W - W_anchor) in the surrogate modes.  Each step is one
+// v_mfma_f32_32x32x1_2b_f32 per chain, so with equal inputs W and GH equal the reference's.
+// 64 x 128 output tiles: the 4 waves share the tile's 64 rows and take 32 columns each (three
+// 64 x 32 accumulators per wave).  The K ring is k_trailing_w's; per stage waves 0-1 fetch the
+// Err1 chunks of the two 32-row halves, waves 2-3 the Z1 chunks, every wave two Hinv k-rows.
+struct TzArgs {
+  float* Wp;
+  int64_t ldw;
+  float* GH;
+  const float* Z;
+  int64_t ldgh;
+  const float* Hinv;
+  int C, R_s, i1, count;
+  const float* err;
+  int gmode;
+  const float* anchor;
+  int64_t lda;
+  const float* beta;
+  float sos;
+  int nrt, nct, total;
+};
+
+constexpr int TZR = 64;    // tile rows
+constexpr int TZC = 128;   // tile columns
+
+struct TzTile {
+  const float* srcA;
+  const float* srcB;
+  int wave, eoff0, eoff1, boff, nk, count;
+  int64_t ldh;
+  floatx32 accE, accD, accZ;
+
+  __device__ __forceinline__ void stage(uint8_t* st, int kt) {
+    lds_dma16(srcA + kt * 8, st + wave * TCH);
+    lds_dma16(srcB + (int64_t)kt * 8 * ldh, st + TA_BYTES + wave * THROW);
+  }
+  template <int CUR, int FILL>
+  __device__ __forceinline__ void step(const TStages& L, int kt) {
+    TWAIT_VM(2 * (TSTAGES - 2));
+    __builtin_amdgcn_s_barrier();
+    stage(L.s[FILL], min(kt + TSTAGES - 1, nk - 1));
+    const uint8_t* st = L.s[CUR];
+    const float4 e0 = *reinterpret_cast<const float4*>(st + eoff0);
+    const float4 e1 = *reinterpret_cast<const float4*>(st + eoff1);
+    const float4 z0 = *reinterpret_cast<const float4*>(st + 2 * TCH + eoff0);
+    const float4 z1 = *reinterpret_cast<const float4*>(st + 2 * TCH + eoff1);
+    const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+    const float zv[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+    float bv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      bv[k] = *reinterpret_cast<const float*>(st + TA_BYTES + (k >> 1) * THROW + (k & 1) * 512 + boff);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float zd = zv[k] * (float)(count - 1 - (8 * kt + k));   // (Z1 * D)[r, k], one rounding
+      accE = __builtin_amdgcn_mfma_f32_32x32x1f32(ev[k], bv[k], accE, 0, 0, 0);
+      accD = __builtin_amdgcn_mfma_f32_32x32x1f32(zd, bv[k], accD, 0, 0, 0);
+      accZ = __builtin_amdgcn_mfma_f32_32x32x1f32(zv[k], bv[k], accZ, 0, 0, 0);
+    }
+  }
+};
+
+template <bool SURR>
+__global__ __launch_bounds__(256, 2) void k_trailing_z(TzArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds0[TSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds1[TSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds2[TSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds3[TSTAGE];
+  const TStages L{{lds0, lds1, lds2, lds3}};
+  const int b = blockIdx.x;
+  const int per = a.total / 8, rem8 = a.total % 8;
+  const int xcd = b % 8, idx = b / 8;
+  const int t = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
+  if (t >= a.total) return;
+  const int per_sub = a.nrt * a.nct;
+  const int sub = t / per_sub, u = t % per_sub;
+  const int ct = u / a.nrt, rt = u % a.nrt;
+  const int i2 = a.i1 + a.count;
+  const int rl0 = rt * TZR, c0 = i2 + ct * TZC;
+  const int64_t rbase = (int64_t)sub * a.R_s;
+  const int tid = threadIdx.x, lane = tid & 63;
+
+  TzTile w;
+  w.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  w.nk = a.count / 8;
+  w.count = a.count;
+  w.ldh = a.C;
+  {
+    // staging sources: waves 0-1 Err1 rows 32 w .. +31 of the tile, waves 2-3 Z1 rows
+    // 32 (w - 2) .. +31 (lane L: row L / 2, k quad (L % 2) ^ ((row / 8) % 2)); every wave the
+    // Hinv k-rows 2 w, 2 w + 1 (columns clamped to a whole in-bounds quad)
+    const int rho = lane >> 1, q = (lane & 1) ^ ((rho >> 3) & 1);
+    const int rl = min(rl0 + 32 * (w.wave & 1) + rho, a.R_s - 1);
+    w.srcA = (w.wave < 2) ? a.err + (rbase + rl) * a.count + 4 * q
+                          : a.Z + (rbase + rl) * a.ldgh + a.i1 + 4 * q;
+    const int kr = 2 * w.wave + (lane >> 5);
+    const int c = min(c0 + 4 * (lane & 31), a.C - 4);
+    w.srcB = a.Hinv + (int64_t)sub * a.C * a.C + (int64_t)(a.i1 + kr) * a.C + c;
+  }
+  {
+    // this lane's row is tile row `lane`: Err1 chunk lane / 32, Z1 chunk 2 + lane / 32
+    const int rho = lane & 31, sw = (rho >> 3) & 1;
+    const int base = (lane >> 5) * TCH + 32 * rho;
+    w.eoff0 = base + 16 * (0 ^ sw);
+    w.eoff1 = base + 16 * (1 ^ sw);
+  }
+  w.boff = 4 * (32 * w.wave + (lane & 31));
+#pragma unroll
+  for (int e = 0; e < 32; ++e) w.accE[e] = w.accD[e] = w.accZ[e] = 0.0f;
+
+  // this lane's 32 outputs: tile row 32 (e / 16) + 8 ((e % 16) / 4) + 4 (lane / 32) + e % 4,
+  // column 32 wave + lane % 32; W and GH loaded before the K loop (the surrogate modes' anchor
+  // after it, to stay within the register budget)
+  const int rw0 = rl0 + 4 * (lane >> 5), cw = c0 + 32 * w.wave + (lane & 31);
+  float wv[32], gv[32];
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const int rl = min(rw0 + 32 * (e / 16) + 8 * ((e % 16) / 4) + (e % 4), a.R_s - 1);
+    const int c = min(cw, a.C - 1);
+    wv[e] = a.Wp[(rbase + rl) * a.ldw + c];
+    gv[e] = a.GH[(rbase + rl) * a.ldgh + c];
+  }
+
+  static_assert(TSTAGES == 4, "unrolled stage schedule");
+#pragma unroll
+  for (int s = 0; s < TSTAGES - 1; ++s) w.stage(L.s[s], min(s, w.nk - 1));
+  int kt = 0;
+  for (; kt + 4 <= w.nk; kt += 4) {
+    w.step<0, 3>(L, kt);
+    w.step<1, 0>(L, kt + 1);
+    w.step<2, 1>(L, kt + 2);
+    w.step<3, 2>(L, kt + 3);
+  }
+  const int rem = w.nk - kt;
+  if (rem > 0) w.step<0, 3>(L, kt);
+  if (rem > 1) w.step<1, 0>(L, kt + 1);
+  if (rem > 2) w.step<2, 1>(L, kt + 2);
+  TWAIT_VM(0);   // no staging in flight when the workgroup ends
+
+  const float cnt = (float)a.count;
+  const bool scaled = a.gmode == 3;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const int rl = rw0 + 32 * (e / 16) + 8 * ((e % 16) / 4) + (e % 4);
+    if (rl >= a.R_s || cw >= a.C) continue;
+    const float g = gv[e];
+    float geff = g;
+    if constexpr (SURR) {
+      const float dw = wv[e] - a.anchor[(rbase + rl) * a.lda + cw];
+      const float bd = a.beta[rbase + rl] * dw;
+      geff = g + bd;
+    }
+    const float cg = cnt * geff;
+    const float gupd = cg - w.accD[e];
+    const float tot = w.accE[e] + gupd;
+    a.Wp[(rbase + rl) * a.ldw + cw] = wv[e] - (scaled ? a.sos * tot : tot);
+    a.GH[(rbase + rl) * a.ldgh + cw] = g - w.accZ[e];
+  }
+}
+
 }  // namespace
 
 extern "C" int rq_quant_block(float* Wp, int64_t ldw, const float* Hinv_all, int C, const float* GH,
@@ -646,6 +817,19 @@ extern "C" int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float
              (R_s + TT - 1) / TT, (C - i2 + TT - 1) / TT, 0};
     w.total = w.nrt * w.nct * (R / R_s);
     hipLaunchKernelGGL(k_trailing_w, dim3(w.total), dim3(256), 0, s, w);
+    RQ_CHECK_LAUNCH();
+    return RQ_OK;
+  }
+  if (count % 8 == 0 && C % 4 == 0 && i1 % 4 == 0 && ldgh % 4 == 0 && al16(Hinv_all) && al16(err) &&
+      al16(Z)) {
+    // the GPTQ+ terms present (or not known to be zero): three k-ordered chains per output
+    TzArgs z{Wp, ldw, GH, Z, ldgh, Hinv_all, C, R_s, i1, count, err, gmode, anchor, ld_anchor, beta,
+             (float)second_order_scale, (R_s + TZR - 1) / TZR, (C - i2 + TZC - 1) / TZC, 0};
+    z.total = z.nrt * z.nct * (R / R_s);
+    if (gmode == RQ_GMODE_SURROGATE_BLOCK || gmode == RQ_GMODE_SURROGATE_ONLINE)
+      hipLaunchKernelGGL(k_trailing_z<true>, dim3(z.total), dim3(256), 0, s, z);
+    else
+      hipLaunchKernelGGL(k_trailing_z<false>, dim3(z.total), dim3(256), 0, s, z);
     RQ_CHECK_LAUNCH();
     return RQ_OK;
   }

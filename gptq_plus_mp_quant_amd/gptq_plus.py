@@ -198,10 +198,11 @@ class GPTQPlus:
 
         Extra keyword arguments (not in the reference):
           keep_hinv -- keep ``Hinv_all``, ``Hinv_init_all``, ``Z`` and ``GHinv`` on the object.
-          inject    -- parity-test hook: ``{"perm": LongTensor[C], "hinv": [(Hinv_init, Hinv), ...]}``
-                       replaces the act_order permutation and/or each subgroup's inverse factors
-                       so the block loop can be compared against another implementation on
-                       identical inputs.
+          inject    -- parity-test hook: ``{"perm": LongTensor[C], "hinv": [(Hinv_init, Hinv), ...],
+                       "terms": [(beta, Z, GHinv), ...]}`` replaces the act_order permutation,
+                       each subgroup's inverse factors and/or its GPTQ+ terms (as the reference's
+                       _compute_gradient_terms returns them), so the block loop can be compared
+                       against another implementation on identical inputs.
         """
         rec = profile_recorder or self.profile_recorder
         inject = inject or {}
@@ -346,6 +347,13 @@ class GPTQPlus:
                                      Z[r0:r0 + R_s], GH[r0:r0 + R_s], GH0, z_flags[sub:sub + 1])
                 if beta_mode == 1 and self.reference_loss <= 0:
                     beta = torch.zeros(R_s, **f32)
+                if inject.get("terms") is not None:   # test hook: given (beta, Z, GHinv)
+                    b_in, z_in, gh_in = inject["terms"][sub]
+                    beta = b_in.to(**f32).reshape(-1).clone()
+                    Z[r0:r0 + R_s].copy_(z_in)
+                    GH[r0:r0 + R_s].copy_(gh_in)
+                    zs = Z[r0:r0 + R_s]
+                    z_flags[sub] = ((zs != 0) | torch.isnan(zs)).any().to(torch.int32)
                 damp, fallback, attempts = chain[sub]
                 self.subgroup_info.append(dict(damp_percent=damp, identity_fallback=fallback,
                                                attempts=attempts, beta=beta))

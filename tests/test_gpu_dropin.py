@@ -33,6 +33,17 @@ def _z_zero(m):
             and (not m["atomic"] or m["B"] <= 32))
 
 
+def _exact_with_terms(m):
+    """With the reference's H^-1 and its GPTQ+ terms (beta, Z, GHinv) injected, every later stage
+    of the frozen and surrogate modes is bit-exact: the column loop op for op, and the trailing
+    update's three products (Err1 Hinv, (Z1 D) Hinv, Z1 Hinv) as k-ordered fused multiply-add
+    chains like the CPU matmuls.  Not block_backward (its terms are recomputed from the refreshed
+    gradient by K = C GEMMs that MKL sums in K-chunks of its own choosing), not block_gd (the
+    optimizer step), and the atomic solve only for B <= 32."""
+    return (m.get("mode", "frozen") in ("frozen", "surrogate_block", "surrogate_online")
+            and (not m["atomic"] or m["B"] <= 32))
+
+
 def _gpu_obj(W, s, grad, G, alpha, ref_loss, bits, sym, mse=False):
     R, C = W.shape
     layer = torch.nn.Linear(C, R, bias=False).to(DEV, W.dtype)
@@ -81,6 +92,9 @@ def test_golden_fasterquant_same_inverse(case):
     g.act_square.copy_(case.t("act_square").to(DEV))
     inject = {"hinv": [(case.sub(s, "Hinv_init").to(DEV), case.sub(s, "Hinv_upper_cholesky").to(DEV))
                        for s in range(m["G"])]}
+    if m["alpha"] > 0:
+        inject["terms"] = [(case.sub(s, "beta").to(DEV), case.sub(s, "Z_initial").to(DEV),
+                            case.sub(s, "GHinv_initial").to(DEV)) for s in range(m["G"])]
     if m["act"]:
         inject["perm"] = case.sub(0, "perm")
     g.fasterquant(blocksize=m["B"], percdamp=0.01, groupsize=m["gs"], actorder=m["act"],
@@ -95,9 +109,9 @@ def test_golden_fasterquant_same_inverse(case):
     flips = code_flips(layer.int_weight, case.t("W_int").float())
     n = case.t("W_int").numel()
     print(f"{case.name}: code flips {flips}/{n}")
-    assert flips <= max(2, n // 1000)
+    assert flips <= n // 10000
     same = layer.int_weight.cpu() == case.t("W_int").float()
-    if _z_zero(m):
+    if _z_zero(m) or _exact_with_terms(m):
         assert flips == 0
         assert torch.equal(layer.scale.cpu(), case.t("Scale"))
         assert torch.equal(layer.weight.data.cpu(), case.t("Q"))
@@ -162,6 +176,13 @@ CFGS = [
 ]
 
 
+# Measured flips above 0.01 % (of 131072 codes), from sources named in test_dropin_vs_oracle:
+# the setup GEMMs' summation order under the GPTQ+ cancellation (static_gplus: 14,
+# surrogate_online: 34-36), block_backward's refreshed terms (63), block_gd (58).
+FLIP_BAR = {"g2_sym4_static_gplus": 30, "g4_asym4_surrogate_online": 60, "g4_sym4_block_backward": 100,
+            "g2_sym4_block_gd_adam_l2": 100}
+
+
 @pytest.mark.parametrize("cfg", CFGS, ids=[c["name"] for c in CFGS])
 def test_dropin_vs_oracle(cfg):
     R, C, G = cfg["R"], cfg["C"], cfg["G"]
@@ -193,11 +214,25 @@ def test_dropin_vs_oracle(cfg):
     n = res.W_int.numel()
     flips_same = code_flips(layer.int_weight, res.W_int)
     print(f"{cfg['name']}: flips with the oracle's H^-1 {flips_same}/{n}")
-    # beta > 0: Z = (G Hinv^T) beta enters as count*GHinv - (Z D) Hinv, whose cancellation
-    # amplifies the GEMMs' rounding, so the bar is 1e-3 there; with Z = 0 the codes are exact
-    assert flips_same <= max(2, n // 1000)
     if _z_zero(cfg):
         assert flips_same == 0
+    # (1b) the oracle's GPTQ+ terms too: frozen and surrogate modes are then bit-exact
+    terms_flips = None
+    if alpha > 0:
+        layer.weight.data.copy_(W.to(DEV))
+        gt, layer_t = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False))
+        gt.H, gt.act_square, gt._finalized = o.H.to(DEV).clone(), o.act_square.to(DEV).clone(), True
+        inject_t = dict(inject, terms=[(r.beta.to(DEV), r.Z.to(DEV), r.GHinv.to(DEV)) for r in res.subgroups])
+        gt.fasterquant(export_to_et=True, inject=inject_t, **fq)
+        torch.cuda.synchronize()
+        terms_flips = code_flips(layer_t.int_weight, res.W_int)
+        print(f"{cfg['name']}: flips with the oracle's H^-1 and GPTQ+ terms {terms_flips}/{n}")
+        if _exact_with_terms(cfg):
+            assert terms_flips == 0
+    # the remaining differences: the K = C setup GEMMs (G Hinv^T, Z Hinv) summed in another
+    # order than MKL's K-chunks, amplified by the count*GHinv - (Z D) Hinv cancellation
+    # (frozen / surrogate), the refreshed terms of block_backward, block_gd's optimizer step
+    assert flips_same <= FLIP_BAR.get(cfg["name"], n // 10000), flips_same
     # (2) own fp64 Cholesky chain
     layer.weight.data.copy_(W.to(DEV))
     g2, layer2 = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False))
@@ -210,7 +245,7 @@ def test_dropin_vs_oracle(cfg):
         assert rel_fro(g2.Hinv_all[sidx], rec.Hinv) <= 1e-4
     flips_own = code_flips(layer2.int_weight, res.W_int)
     print(f"{cfg['name']}: flips with its own H^-1 {flips_own}/{n}")
-    assert flips_own <= n // 1000
+    assert flips_own <= FLIP_BAR.get(cfg["name"], n // 10000), flips_own
     Xf = X.float().reshape(-1, C)
     e_gpu = reconstruction_error(W.float(), layer2.weight.data.float().cpu(), Xf)
     e_ref = reconstruction_error(W.float(), res.Q.float(), Xf)
