@@ -216,18 +216,26 @@ __device__ __forceinline__ void reduce_slices(const float* __restrict__ part0, i
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wr = wave >> 1, wc = wave & 1;
+  // partials of other workgroups: coherent loads, the S (<= 8) of 4 outputs issued together
+  // (within this kernel's register budget), then added in slice order
+#pragma unroll 1
+  for (int blk = 0; blk < 16; ++blk) {
+      const int bi = blk >> 3, bj = (blk >> 2) & 1, e0 = 4 * (blk & 3);
+      float v[4][8];
 #pragma unroll
-  for (int bi = 0; bi < 2; ++bi)
+      for (int e = 0; e < 4; ++e)
 #pragma unroll
-    for (int bj = 0; bj < 2; ++bj)
-#pragma unroll 4
-      for (int e = 0; e < 16; ++e) {
-        const int slot = (bi * 32 + bj * 16 + e) * HTHREADS + tid;
-        // partials of other workgroups: coherent (L1-bypassing) loads
-        float sum = __hip_atomic_load(part0 + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (int q = 1; q < S; ++q)
-          sum += __hip_atomic_load(part0 + (int64_t)q * HPART + slot, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        for (int q = 0; q < 8; ++q)
+          v[e][q] = (q < S) ? __hip_atomic_load(part0 + (int64_t)q * HPART + (bi * 32 + bj * 16 + e0 + e) * HTHREADS + tid,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                            : 0.0f;
+#pragma unroll
+      for (int ee = 0; ee < 4; ++ee) {
+        const int e = e0 + ee;
+        float sum = v[ee][0];
+#pragma unroll
+        for (int q = 1; q < 8; ++q)
+          if (q < S) sum += v[ee][q];
         const int i = I0 + wr * 64 + bi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
         const int j = J0 + wc * 64 + bj * 32 + (lane & 31);
         if (i < C && j < C) {
@@ -235,6 +243,7 @@ __device__ __forceinline__ void reduce_slices(const float* __restrict__ part0, i
           *p = *p + sum;
         }
       }
+    }
 }
 
 template <typename TX>
@@ -646,20 +655,40 @@ __device__ __forceinline__ void reduce_split_slices(const float* __restrict__ pa
   const int fr = lane & 31, fh = lane >> 5;
   const int j = C0 + 32 * split_colblock(wave) + fr;   // the column the slices' thread held
   const float inv = (j < C) ? 1.0f / scl[j] : 0.0f;
+  // per accumulator block: the S partials of its 16 outputs loaded 8 slices at a time (S
+  // uniform), added in slice order
 #pragma unroll 1
-  for (int bi = 0; bi < 8; ++bi)
-#pragma unroll 4
+  for (int bi = 0; bi < 8; ++bi) {
+    float sums[16];
+#pragma unroll 1
+    for (int q0 = 0; q0 < S; q0 += 8) {
+      float v[16][8];
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          v[e][q] = (q0 + q < S) ? __hip_atomic_load(part0 + (int64_t)(q0 + q) * XPART + (bi * 16 + e) * XTHREADS + tid,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                 : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float acc = q0 == 0 ? v[e][0] : sums[e] + v[e][0];
+#pragma unroll
+        for (int q = 1; q < 8; ++q)
+          if (q0 + q < S) acc += v[e][q];
+        sums[e] = acc;
+      }
+    }
+#pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int slot = (bi * 16 + e) * XTHREADS + tid;
-      float sum = __hip_atomic_load(part0 + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int qq = 1; qq < S; ++qq)
-        sum += __hip_atomic_load(part0 + (int64_t)qq * XPART + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float sum = sums[e];
       const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
       if (i < C && j < C) {
         float* ph = Hg + (int64_t)i * C + j;
         *ph = *ph + sum * inv;
       }
     }
+  }
 }
 
 template <typename TX, int PC>
@@ -1130,9 +1159,11 @@ int kernel_slots(K kfn, int threads, int which) {
 int hessian_slots() { return kernel_slots(k_hessian_accum<__half>, HTHREADS, 0); }
 int split_slots() { return kernel_slots(k_hessian_split<__half, 2>, XTHREADS, 1); }
 
-// Items of the last, partly filled round and the slice count that fills rounds best
-// (the finishing time of the tail in rounds is ceil(tail * S / slots) / S).
-void tail_split(int64_t total, int64_t nslab, int slots, int* tail, int* S) {
+// Items of the last, partly filled round and the slice count that fills rounds best: the
+// tail finishes in ceil(tail * S / slots) / S rounds, plus a little per slice for its partial
+// tile and the last slice's reduction (S <= maxS, at least 4 token slabs per slice).  The
+// split kernels reduce up to 16 slices, the fp32 kernel up to 8.
+void tail_split(int64_t total, int64_t nslab, int slots, int maxS, int* tail, int* S) {
   *tail = 0;
   *S = 1;
   if (slots <= 0 || total <= 0) return;
@@ -1140,9 +1171,9 @@ void tail_split(int64_t total, int64_t nslab, int slots, int* tail, int* S) {
   if (t == 0) return;
   double best = 1.0;
   int bestS = 1;
-  for (int cand = 2; cand <= 8; cand *= 2) {
-    if (nslab < 4 * cand) break;                  // keep >= 4 slabs per slice
-    const double rounds = (double)((t * cand + slots - 1) / slots) / cand;
+  for (int cand = 2; cand <= maxS; ++cand) {
+    if (nslab < 4 * cand) break;
+    const double rounds = (double)((t * cand + slots - 1) / slots) / cand + 0.003 * cand;
     if (rounds < best - 0.05) {
       best = rounds;
       bestS = cand;
@@ -1280,7 +1311,7 @@ int64_t split_ws_need(int64_t ntok, int C, int ntarg) {
   split_items(C, ntarg, &nt, &ntiles, &total);
   int tail = 0, S = 1;
   const int64_t ntok_p = ((ntok + XTOK - 1) / XTOK) * XTOK;
-  tail_split(total, ntok_p / 16, split_slots(), &tail, &S);
+  tail_split(total, ntok_p / 16, split_slots(), 16, &tail, &S);
   return split_layout(ntok, C, ntarg, tail, S).bytes;
 }
 
@@ -1294,7 +1325,7 @@ int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, c
   int tail = 0, S = 1;
   SplitLayout L = split_layout(ntok, C, ntarg, 0, 1);
   const int64_t nks = L.ntok_p / 16;
-  tail_split(total, nks, split_slots(), &tail, &S);
+  tail_split(total, nks, split_slots(), 16, &tail, &S);
   L = split_layout(ntok, C, ntarg, tail, S);
   if (ws_bytes < L.bytes) {                       // no room for the slices: whole items only
     tail = 0;
@@ -1360,7 +1391,7 @@ int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
     if (rc) return rc;
   }
   int tail = 0, S = 1;
-  if (aligned) tail_split(total, (ntok + HKC - 1) / HKC, hessian_slots(), &tail, &S);
+  if (aligned) tail_split(total, (ntok + HKC - 1) / HKC, hessian_slots(), 8, &tail, &S);
   if (tail > 0 && ws_bytes < hessian_ws_bytes(ntok, C, tail, S)) {
     tail = 0;                                     // no room: whole items only
     S = 1;
@@ -1407,7 +1438,7 @@ extern "C" int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets)
   for (int t0 = 0; t0 < ntargets; t0 += HMAXT) {   // per launch of at most 32 targets
     const int n = (ntargets - t0 < HMAXT) ? (ntargets - t0) : HMAXT;
     int tail = 0, S = 1;
-    tail_split((int64_t)nt * (nt + 1) / 2 * n, (ntok + HKC - 1) / HKC, hessian_slots(), &tail, &S);
+    tail_split((int64_t)nt * (nt + 1) / 2 * n, (ntok + HKC - 1) / HKC, hessian_slots(), 8, &tail, &S);
     int64_t b = hessian_ws_bytes(ntok, C, tail, S);
     const int64_t bs = split_ws_need(ntok, C, n);
     if (bs > b) b = bs;
