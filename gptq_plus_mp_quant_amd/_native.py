@@ -20,6 +20,7 @@ RQ_QMODE_CHANNEL, RQ_QMODE_STATIC, RQ_QMODE_DYNAMIC = 0, 1, 2
 RQ_GMODE_FROZEN, RQ_GMODE_SURROGATE_BLOCK, RQ_GMODE_SURROGATE_ONLINE, RQ_GMODE_BLOCK_GD = 0, 1, 2, 3
 RQ_HMATH_SPLIT16, RQ_HMATH_FP32, RQ_HMATH_SPLIT16X3 = 0, 1, 2
 RQ_NOALLOC_SCRATCH_BYTES = 128 << 20
+RQ_CHOL_MAXBATCH = 64          # matrices per rq_chol_hinv_attempt call
 # g_update_mode -> (kernel mode of the in-block loop, kernel mode of the trailing update);
 # gptq_plus_utils.py:1190 (inner) and :1500 (outer)
 GMODES = {"frozen": (RQ_GMODE_FROZEN, RQ_GMODE_FROZEN),
@@ -39,13 +40,13 @@ SIGNATURES = {
     "rq_hessian_math": (_I, [_I]),
     "rq_hessian_timing_events": (_I, [_P, _P]),
     "rq_hessian_accum_multi": (_I, [_P, _I, _L, _L, _I, _I, _P, _P, _P, _P, _P, _L, _P]),
-    "rq_hessian_finalize": (_I, [_P, _P, _I, _I, _D, _D, _D, _P, _P]),
+    "rq_hessian_finalize": (_I, [_P, _P, _I, _I, _D, _D, _D, _I, _P, _P]),
     "rq_find_params": (_I, [_P, _I, _I, _I, _L, _I, _I, _I, _P, _P, _P]),
     "rq_find_params_mse": (_I, [_P, _I, _I, _I, _L, _I, _I, _I, _D, _I, _D, _P, _P, _P]),
     "rq_act_order_perm": (_I, [_P, _I, _P, _P, _P]),
     "rq_prepare_subgroup": (_I, [_P, _I, _L, _P, _L, _P, _I, _I, _P, _P, _L, _P, _L, _P, _P]),
     "rq_chol_workspace_bytes": (_L, [_I]),
-    "rq_chol_hinv_attempt": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "rq_chol_hinv_attempt": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "rq_gptqplus_terms": (_I, [_P, _L, _P, _P, _I, _I, _D, _D, _I, _P, _P, _P, _L, _P, _P, _P]),
     "rq_quant_block": (_I, [_P, _L, _P, _I, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I,
                             _I, _P, _P, _P, _I, _P, _L, _P, _D, _P]),

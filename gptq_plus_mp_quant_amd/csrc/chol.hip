@@ -13,7 +13,8 @@
 // where B accumulates I - sum_m L_im X_m.  The updates of the trailing matrix and of the rows
 // of B below a panel are applied once per panel (rank 256 / 512) instead of once per block,
 // by k_panel_update (128x128 tiles, direct global->LDS staging).  H^-1 itself (Hinv_init) is
-// P (L^-T L^-1) P and is only formed when asked for.  A non-positive or non-finite pivot, or
+// P (L^-T L^-1) P and is only formed when asked for; its diagonal (all that the GPTQ+ step
+// size needs of it) comes from the column norms of L^-1.  A non-positive or non-finite pivot, or
 // a non-finite result, raises the device `info` flag; later kernels of the same attempt exit
 // early.
 #include "gemm_tile.h"
@@ -322,6 +323,62 @@ __global__ __launch_bounds__(256) void k_output_full(const double* __restrict__ 
   if (bad) atomicExch(info, 3);
 }
 
+// diag(H^-1)[i] = sum_{k >= p} Linv[k][p]^2 with p = C-1-i (the diagonal of P Linv^T Linv P),
+// in two passes: fp64 partial sums over nch = gridDim.y row chunks (`part`, nch x C doubles per
+// batch entry, at stride ws), then their sum in chunk order, rounded to fp32; non-finite ->
+// info 3 (as k_output_full).
+__host__ __device__ constexpr int diag_chunks(int C) { return C >= 256 ? 16 : 1; }   // nch * C <= C * C
+__global__ __launch_bounds__(256) void k_diag_partial(const double* __restrict__ Linv, int C,
+                                                      double* __restrict__ part, int64_t ws,
+                                                      const int* __restrict__ info_all) {
+  const int b = blockIdx.z;
+  if (info_all[b]) return;
+  Linv += b * ws;
+  part += b * ws;
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p >= C) return;
+  const int rows = (C + gridDim.y - 1) / gridDim.y;
+  const int k0 = blockIdx.y * rows, k1 = min(C, k0 + rows);
+  double s = 0.0;
+  for (int k = max(k0, p); k < k1; ++k) {
+    const double v = Linv[(int64_t)k * C + p];
+    s = __builtin_fma(v, v, s);
+  }
+  part[(int64_t)blockIdx.y * C + p] = s;
+}
+
+__global__ __launch_bounds__(256) void k_diag_final(const double* __restrict__ part, int C, int nch, int64_t ws,
+                                                    float* __restrict__ diag, int* info_all) {
+  const int b = blockIdx.z;
+  int* info = info_all + b;
+  if (*info) return;
+  part += b * ws;
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p >= C) return;
+  double s = 0.0;
+  for (int c = 0; c < nch; ++c) s += part[(int64_t)c * C + p];
+  const float v = (float)s;
+  diag[(int64_t)b * C + (C - 1 - p)] = v;
+  if (!rq_isfinite(v)) atomicExch(info, 3);
+}
+
+// Z[r][j] = Y[r][j] * beta[r] in place (fl32 of the fp32 product, as the reference's
+// `(G @ Hinv.T) * beta_view`); *nz = 1 when any result is non-zero or NaN.
+__global__ __launch_bounds__(256) void k_row_scale_flag(float* __restrict__ Z, int64_t ldz, int R, int C,
+                                                        const float* __restrict__ beta, int* __restrict__ nz) {
+  int any = 0;
+  for (int r = blockIdx.y; r < R; r += gridDim.y) {
+    const float bv = beta[r];
+    for (int j = blockIdx.x * 256 + threadIdx.x; j < C; j += gridDim.x * 256) {
+      float* z = Z + (int64_t)r * ldz + j;
+      const float v = *z * bv;
+      *z = v;
+      any |= (v != 0.0f) | (v != v);
+    }
+  }
+  if (__any(any) && (threadIdx.x & 63) == 0) atomicOr(nz, 1);
+}
+
 // *out = max(*out, max_i |x_i|) as fp32 bit patterns (non-negative floats order like their
 // bits, and a NaN's bits exceed +inf's).  *out starts at 0.
 // 16-byte loads where x is 16-byte aligned; one atomic per workgroup.
@@ -369,7 +426,7 @@ __global__ __launch_bounds__(256) void k_z_rows_need(const float* __restrict__ G
 // One wavefront per row.
 __global__ __launch_bounds__(256) void k_safe_beta(const float* __restrict__ G, int64_t ldg,
                                                    const float* __restrict__ GH0,
-                                                   const float* __restrict__ Hinit, int R, int C,
+                                                   const float* __restrict__ hdiag, int R, int C,
                                                    float target, float* __restrict__ beta) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -378,7 +435,7 @@ __global__ __launch_bounds__(256) void k_safe_beta(const float* __restrict__ G, 
   for (int j = lane; j < C; j += 64) {
     const float gh = GH0[(int64_t)r * C + j];
     s1 += G[(int64_t)r * ldg + j] * gh;
-    s2 += (gh * gh) / Hinit[(int64_t)j * C + j];
+    s2 += (gh * gh) / hdiag[j];
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -719,7 +776,8 @@ extern "C" int64_t rq_chol_workspace_bytes(int C) {
 }
 
 extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* damp_percent,
-                                    void* workspace, float* Hinv, float* Hinv_init, int* info,
+                                    void* workspace, float* Hinv, float* Hinv_init,
+                                    float* Hinv_diag, int* info,
                                     void* stream) {
   using namespace rq;
   if (!H_work || !workspace || !Hinv || !info || !damp_percent || C <= 0 || nb <= 0 ||
@@ -827,6 +885,14 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
   }
   hipLaunchKernelGGL(k_output_upper, gcol, blk, 0, s, Linv, C, Hinv, ws, info);
   RQ_CHECK_LAUNCH();
+  if (Hinv_diag) {
+    // partial column norms in A (free once the factorisation is done)
+    const int nch = diag_chunks(C);
+    const dim3 gd((C + 255) / 256, nch, nb), gf((C + 255) / 256, 1, nb);
+    hipLaunchKernelGGL(k_diag_partial, gd, blk, 0, s, Linv, C, A, ws, info);
+    hipLaunchKernelGGL(k_diag_final, gf, blk, 0, s, A, C, nch, ws, Hinv_diag, info);
+    RQ_CHECK_LAUNCH();
+  }
   if (Hinv_init) {
     // M = Linv^T Linv (lower tiles) into A, then Hinv_init = P M P.
     GemmArgs<double> g = batched(gemm_args<double>(Linv, C, Linv, C, A, C, C, C, C, 1.0, EPI_STORE));
@@ -840,7 +906,7 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
   return RQ_OK;
 }
 
-extern "C" int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* Hinv_init,
+extern "C" int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* hinv_diag,
                                  const float* Hinv, int R_s, int C, double alpha_eff,
                                  double reference_loss, int beta_mode, float* beta, float* Z,
                                  float* GHinv, int64_t ldz, float* GH0, int* z_nonzero,
@@ -849,7 +915,7 @@ extern "C" int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* H
   if (!G_sub || !Hinv || !beta || !Z || !GHinv || !z_nonzero || R_s <= 0 || C <= 0 || ldg < C ||
       ldz < C)
     return RQ_EINVAL;
-  if (beta_mode == 1 && (!Hinv_init || !GH0)) return RQ_EINVAL;
+  if (beta_mode == 1 && (!hinv_diag || !GH0)) return RQ_EINVAL;
   if (beta_mode != 0 && beta_mode != 1) return RQ_EINVAL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int rc;
@@ -859,12 +925,28 @@ extern "C" int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* H
       hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(1), 0, s, beta, 0.0f);
       beta_mode = 0;
     } else {
-      GemmArgs<float> g = gemm_args<float>(G_sub, ldg, Hinv_init, C, GH0, C, R_s, C, C, 1.0f, EPI_STORE);
+      // Y = G_sub Hinv^T (the reference's G Hinv^T before its beta scaling) into Z, then
+      // GH0 = Y Hinv = G Hinv^T Hinv = G Hinv_init, the reference's ghinv_init (:180), through
+      // the factor: two triangular products in place of the full one, and no H^-1 needed
+      // beyond its diagonal.
+      GemmArgs<float> y = gemm_args<float>(G_sub, ldg, Hinv, C, Z, ldz, R_s, C, C, 1.0f, EPI_STORE);
+      y.krange = KR_B_LOWER;
+      if ((rc = launch_gemm(y, false, true, s))) return rc;
+      GemmArgs<float> g = gemm_args<float>(Z, ldz, Hinv, C, GH0, C, R_s, C, C, 1.0f, EPI_STORE);
+      g.krange = KR_B_UPPER;
       if ((rc = launch_gemm(g, false, false, s))) return rc;
       const float target = (float)(2.0 * alpha_eff * reference_loss);
       hipLaunchKernelGGL(k_safe_beta, dim3((R_s + 3) / 4), dim3(256), 0, s, G_sub, ldg, GH0,
-                         Hinv_init, R_s, C, target, beta);
+                         hinv_diag, R_s, C, target, beta);
+      // Z = Y * beta (row-wise, in place), then GHinv = Z Hinv as below
+      hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(1), 0, s, z_nonzero, 0);
+      hipLaunchKernelGGL(k_row_scale_flag, dim3((C + 255) / 256 < 8 ? (C + 255) / 256 : 8, R_s < 65535 ? R_s : 65535),
+                         dim3(256), 0, s, Z, ldz, R_s, C, (const float*)beta, z_nonzero);
       RQ_CHECK_LAUNCH();
+      GemmArgs<float> h = gemm_args<float>(Z, ldz, Hinv, C, GHinv, ldz, R_s, C, C, 1.0f, EPI_STORE);
+      h.krange = KR_B_UPPER;
+      h.skip_if_zero = z_nonzero;
+      return launch_gemm(h, false, false, s);
     }
   } else {
     hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(1), 0, s, beta, 0.0f);

@@ -25,6 +25,7 @@
 #include <atomic>
 #include <mutex>
 #include <type_traits>
+#include <utility>
 
 namespace {
 
@@ -452,7 +453,7 @@ __device__ __forceinline__ void split8(uint4 x, float4 s0, float4 s1, float sc, 
 // every stage index is a compile-time constant: the LDS reads are ordinary loads (the compiler
 // places their lgkmcnt waits), and alias analysis can tell the staging writes in flight to
 // other stages from the stage being read.
-constexpr int XDEPTH = 4;
+constexpr int XDEPTH = 4;   // 8 stages measured no faster
 constexpr int XA_BYTES = 8 * 1024;                  // row fragments of a stage
 constexpr int XB_OFF = XA_BYTES;                    // column fragment of wave w at XB_OFF + 1024 w
 constexpr int XS_OFF = XB_OFF + XWAVES * 1024;      // the step's 16 saliencies (64 B)
@@ -549,6 +550,19 @@ __device__ __forceinline__ void split_step(uint4 (&p)[2][PC], uint4 (&a)[2][8], 
   for (int q = 0; q < PC; ++q) p[NP][q] = make_uint4(o[q][0], o[q][1], o[q][2], o[q][3]);
 }
 
+// Steps k .. k+nsteps-1 (nsteps <= XDEPTH) of the unrolled schedule: step k+J uses stage J,
+// reads stage J+1 and refills stage J-1 (mod XDEPTH), and register buffer J % 2.
+template <typename TX, int PC, bool DIAG, int... J>
+__device__ __forceinline__ void split_round(uint4 (&p)[2][PC], uint4 (&a)[2][8], floatx16 (&acc)[8],
+                                            const XStages& L, const uint16_t* pa, const uint16_t* pb,
+                                            const float* sg, float sc, int wave, int lane, int64_t k,
+                                            int64_t last, int lim, int nsteps, std::integer_sequence<int, J...>) {
+  ((J < nsteps ? split_step<TX, PC, DIAG, J % 2, J, (J + 1) % XDEPTH, (J + XDEPTH - 1) % XDEPTH>(
+                     p, a, acc, L, pa, pb, sg, sc, wave, lane, k + J, last, lim)
+               : void()),
+   ...);
+}
+
 // Column block of wave w: w for w < 4, 11 - w above, so the two waves that share a SIMD
 // (w and w + 4) own blocks c and 7 - c: on a diagonal tile, where wave w needs only the row
 // blocks up to its own, each SIMD then has 9 of the 16 blocks.
@@ -602,17 +616,11 @@ __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int6
 
   const int64_t n = kend - kbeg;
   int64_t k = kbeg;
-  static_assert(XDEPTH == 4, "unrolled stage schedule");
-  for (; k + 4 <= kend; k += 4) {
-    split_step<TX, PC, DIAG, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last, lim);
-    split_step<TX, PC, DIAG, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last, lim);
-    split_step<TX, PC, DIAG, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last, lim);
-    split_step<TX, PC, DIAG, 1, 3, 0, 2>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 3, last, lim);
-  }
-  const int rem = (int)(n & 3);
-  if (rem > 0) split_step<TX, PC, DIAG, 0, 0, 1, 3>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last, lim);
-  if (rem > 1) split_step<TX, PC, DIAG, 1, 1, 2, 0>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 1, last, lim);
-  if (rem > 2) split_step<TX, PC, DIAG, 0, 2, 3, 1>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k + 2, last, lim);
+  static_assert(XDEPTH % 2 == 0, "register buffers alternate by step");
+  constexpr auto round = std::make_integer_sequence<int, XDEPTH>();
+  for (; k + XDEPTH <= kend; k += XDEPTH)
+    split_round<TX, PC, DIAG>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last, lim, XDEPTH, round);
+  split_round<TX, PC, DIAG>(p, a, acc, L, pa, pb, sg, sc, wave, lane, k, last, lim, (int)(n % XDEPTH), round);
   XWAIT_VM(0);                        // no staging left in flight when the workgroup moves on
 
   if (part) {
@@ -1071,7 +1079,7 @@ __device__ __forceinline__ void upper_tile_closed(int t, int nt, int& ti, int& t
 // 32x32 workgroups with 4 elements per thread kept too few loads in flight: ~1.5 TB/s.)
 __global__ __launch_bounds__(256) void k_hessian_finalize64(float* __restrict__ H, int C, int nt,
                                                             float h_div, float sal_scale,
-                                                            int apply_scale, int* nonfinite) {
+                                                            int apply_scale, int sanitize, int* nonfinite) {
   __shared__ float tile[64][65];
   __shared__ int cnt;
   const int g = blockIdx.y;
@@ -1097,7 +1105,7 @@ __global__ __launch_bounds__(256) void k_hessian_finalize64(float* __restrict__ 
     if (apply_scale) val = val / sal_scale;
     val = 0.5f * (val + val);                     // 0.5 * (H + H^T) on the symmetric value
     if (!rq_isfinite(val)) {
-      val = 0.0f;
+      if (sanitize) val = 0.0f;
       local += (i == j) ? 1 : 2;
     }
     Hg[(int64_t)i * C + j] = val;
@@ -1551,14 +1559,15 @@ extern "C" int rq_hessian_accum_multi(const void* x, int x_dtype, int64_t ntok, 
 }
 
 extern "C" int rq_hessian_finalize(float* H, float* act_sq, int G, int C, double h_div,
-                                   double sal_scale, double seq_len, int* nonfinite, void* stream) {
+                                   double sal_scale, double seq_len, int sanitize, int* nonfinite,
+                                   void* stream) {
   if (!H || C <= 0 || G <= 0 || !(h_div > 0) || !(seq_len > 0)) return RQ_EINVAL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int nt = (C + 63) / 64;
   const int ntiles = nt * (nt + 1) / 2;
   // torch divides a float tensor by a Python scalar in float: a / (float)b (CPU kernel).
   hipLaunchKernelGGL(k_hessian_finalize64, dim3(ntiles, G), dim3(256), 0, s, H, C, nt, (float)h_div,
-                     (float)sal_scale, sal_scale != 1.0 ? 1 : 0, nonfinite);
+                     (float)sal_scale, sal_scale != 1.0 ? 1 : 0, sanitize ? 1 : 0, nonfinite);
   RQ_CHECK_LAUNCH();
   if (act_sq) {
     hipLaunchKernelGGL(k_scale_vec, dim3((C + 255) / 256), dim3(256), 0, s, act_sq, C, (float)seq_len);

@@ -82,12 +82,13 @@ class GPTQ:
             q.find_params(W)
         maxq, sym = int(q.maxq), int(bool(q.sym))
 
-        # H = 2/n * sum x x^T, mirrored; an all-zero H (no data) becomes the identity (RTN)
+        # H = 2/n * sum x x^T, mirrored and left unsanitised (a non-finite H fails every
+        # Cholesky retry and raises, :87-104); an all-zero H (no data) becomes the identity (RTN)
         H = self.H.view(1, C, C)
         self.H = None
         if self.nsamples > 0:
-            K.hessian_finalize(H, None, self.nsamples / 2.0, 1.0, 1.0)
-        if self.nsamples == 0 or int(torch.count_nonzero(torch.diagonal(H[0]))) == 0:
+            K.hessian_finalize(H, None, self.nsamples / 2.0, 1.0, 1.0, sanitize=False)
+        if self.nsamples == 0 or not bool(torch.any(H[0])):
             H[0].copy_(torch.eye(C, device=dev))
         # dead columns (:64-66), then act_order by the dead-fixed diag(H) (:75-80)
         Wp = torch.empty((R, C), **f32)
@@ -108,7 +109,7 @@ class GPTQ:
             cols = perm if perm is not None else torch.arange(C, device=dev)
             if static_groups:
                 # groups of the dead-fixed, unpermuted weight (:67-73)
-                scale_tab, zero_tab = q.params_on(Wd, groupsize)
+                scale_tab, zero_tab = q.params_grouped(Wd, groupsize)
                 col_group = (cols // groupsize).to(torch.int32).contiguous()
             else:
                 # re-fitted on the working weight at each group start (:121-125), in the
@@ -133,9 +134,9 @@ class GPTQ:
             if dyn_fit:
                 for g in range((i1 + groupsize - 1) // groupsize, (i2 + groupsize - 1) // groupsize):
                     s0 = g * groupsize
-                    sc, zc = q.params_on(Wp[:, s0:min(s0 + groupsize, C)])
-                    scale_tab[g].copy_(sc[0])
-                    zero_tab[g].copy_(zc[0])
+                    sc, zc = q.row_params(Wp[:, s0:min(s0 + groupsize, C)], R)
+                    scale_tab[g].copy_(sc)
+                    zero_tab[g].copy_(zc)
             # GH / Z are never read when the first-order flag is 0; Wp stands in for them
             K.quant_block(Wp, Hinv_all, Wp, Wp, R, i1, i2 - i1, qmode, scale_tab, col_group, None, maxq,
                           sym, False, z_off, codes, err)

@@ -38,16 +38,19 @@ def _section(rec, name):
 
 
 def hessian_inverse_chain(dev, H_work, Hinv_out, Hinv_init_out, workspace, percdamp,
-                          damp_auto_increment=0.0015, log_context="", identity_fallback=True):
+                          damp_auto_increment=0.0015, log_context="", identity_fallback=True,
+                          Hinv_diag_out=None):
     """The damped Cholesky chain with retries (gptq_plus_utils.py:494-561; classic GPTQ
     gptq_utils.py:87-106 has the same schedule but raises instead of the identity fallback).
-    H_work [nb, C, C] (or [C, C]) is damped in place; returns [(damp, fallback, attempts)]."""
+    H_work [nb, C, C] (or [C, C]) is damped in place; Hinv_init_out (H^-1) and Hinv_diag_out
+    (its diagonal, [nb, C]) are optional.  Returns [(damp, fallback, attempts)]."""
     damp0 = float(percdamp)
     if damp0 <= 0:
         raise ValueError(f"Quantization{log_context}: `damp_percent` must be positive. current is {damp0}")
     if H_work.dim() == 2:
         H_work, Hinv_out = H_work[None], Hinv_out[None]
         Hinv_init_out = None if Hinv_init_out is None else Hinv_init_out[None]
+        Hinv_diag_out = None if Hinv_diag_out is None else Hinv_diag_out.reshape(1, -1)
     nb, C = H_work.shape[0], H_work.shape[-1]
     damp = [damp0] * nb
     attempts = [0] * nb
@@ -57,7 +60,7 @@ def hessian_inverse_chain(dev, H_work, Hinv_out, Hinv_init_out, workspace, percd
         todo = [damp[b] if status[b] == "run" else 0.0 for b in range(nb)]
         for b in range(nb):
             attempts[b] += status[b] == "run"
-        K.chol_hinv_attempt(H_work, todo, workspace, Hinv_out, Hinv_init_out, info)
+        K.chol_hinv_attempt(H_work, todo, workspace, Hinv_out, Hinv_init_out, info, Hinv_diag_out)
         codes = info.tolist()
         for b in range(nb):
             if status[b] != "run":
@@ -81,6 +84,8 @@ def hessian_inverse_chain(dev, H_work, Hinv_out, Hinv_init_out, workspace, percd
             Hinv_out[b].copy_(eye)
             if Hinv_init_out is not None:
                 Hinv_init_out[b].copy_(eye)
+            if Hinv_diag_out is not None:
+                Hinv_diag_out[b].fill_(1.0)
             out.append((damp[b], True, attempts[b]))
         else:
             raise ValueError(f"Quantization{log_context}: `damp_percent` must between 0 and 1. "
@@ -179,9 +184,9 @@ class GPTQPlus:
 
     # gptq_plus_utils.py:494-561, for a batch of subgroups (each with its own schedule)
     def _hessian_inverse(self, H_work, Hinv_out, Hinv_init_out, workspace, percdamp,
-                         damp_auto_increment=0.0015, log_context=""):
+                         damp_auto_increment=0.0015, log_context="", Hinv_diag_out=None):
         return hessian_inverse_chain(self.dev, H_work, Hinv_out, Hinv_init_out, workspace, percdamp,
-                                     damp_auto_increment, log_context)
+                                     damp_auto_increment, log_context, Hinv_diag_out=Hinv_diag_out)
 
     # gptq_plus_utils.py:910-1896 (frozen mode)
     @torch.no_grad()
@@ -256,7 +261,7 @@ class GPTQPlus:
             elif static_groups:
                 qmode = nat.RQ_QMODE_STATIC
                 with _section(rec, "fasterquant.quantizer_build_groups"):
-                    scale_tab, zero_tab = q.params_on(W, groupsize)
+                    scale_tab, zero_tab = q.params_grouped(W, groupsize)
             else:
                 qmode = nat.RQ_QMODE_DYNAMIC
                 scale_tab = None
@@ -280,8 +285,9 @@ class GPTQPlus:
             Gs = torch.empty((R, C), **f32)
             Hinv_all = torch.empty((G, C, C), **f32)
             beta_mode = 1 if (enable_gradient_update and self.alpha > 0) else 0
-            want_init = beta_mode == 1 or keep_hinv
-            Hinit_all = torch.empty((G, C, C), **f32) if want_init else None
+            # H^-1 itself only for keep_hinv; the GPTQ+ step size needs just its diagonal
+            Hinit_all = torch.empty((G, C, C), **f32) if keep_hinv else None
+            hdiag_all = torch.empty((G, C), **f32) if beta_mode == 1 else None
             grads = self.gradients.to(**f32)
             if grads.stride(1) != 1:
                 grads = grads.contiguous()
@@ -324,7 +330,8 @@ class GPTQPlus:
                         b1 = min(G, b0 + nb)
                         chain += self._hessian_inverse(
                             H_work[b0:b1], Hinv_all[b0:b1],
-                            None if Hinit_all is None else Hinit_all[b0:b1], workspace, percdamp)
+                            None if Hinit_all is None else Hinit_all[b0:b1], workspace, percdamp,
+                            Hinv_diag_out=None if hdiag_all is None else hdiag_all[b0:b1])
                     del workspace
                 else:   # test hook: use given (Hinv_init, Hinv) pairs
                     chain = []
@@ -332,6 +339,8 @@ class GPTQPlus:
                         Hinv_all[sub].copy_(inject_hinv[sub][1])
                         if Hinit_all is not None:
                             Hinit_all[sub].copy_(inject_hinv[sub][0])
+                        if hdiag_all is not None:
+                            hdiag_all[sub].copy_(torch.diagonal(inject_hinv[sub][0]))
                         chain.append((float(percdamp), False, 0))
             del H_work
             GH0 = torch.empty((R_s, C), **f32) if beta_mode == 1 else None
@@ -342,7 +351,7 @@ class GPTQPlus:
                 r0 = sub * R_s
                 beta = torch.empty(R_s if beta_mode == 1 else 1, **f32)
                 with _section(rec, "fasterquant.subgroup.init_ghinv"):
-                    K.gptqplus_terms(Gs[r0:r0 + R_s], None if Hinit_all is None else Hinit_all[sub],
+                    K.gptqplus_terms(Gs[r0:r0 + R_s], None if hdiag_all is None else hdiag_all[sub],
                                      Hinv_all[sub], alpha_eff, float(self.reference_loss), beta_mode, beta,
                                      Z[r0:r0 + R_s], GH[r0:r0 + R_s], GH0, z_flags[sub:sub + 1])
                 if beta_mode == 1 and self.reference_loss <= 0:
@@ -391,11 +400,12 @@ class GPTQPlus:
                     i2 = min(i1 + blocksize, C)
                     count = i2 - i1
                     atomic = bool(block_atomic_quant) and i2 < C
-                    if qmode == nat.RQ_QMODE_DYNAMIC and q.mse:
-                        # dynamic groups + clip search: find_params on the block start
+                    if qmode == nat.RQ_QMODE_DYNAMIC and (q.mse or not q.perchannel):
+                        # dynamic groups with the clip search, or one scale per subgroup block
+                        # (perchannel=False): find_params on the block start
                         # (gptq_plus_utils.py:1208-1209), then quantize with those row scales
-                        bscale, _ = q.params_on(Wp[:, i1:i2])
-                        dyn_scale[bidx].copy_(bscale[0])
+                        bscale, _ = q.row_params(Wp[:, i1:i2], R_s)
+                        dyn_scale[bidx].copy_(bscale)
                         K.quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, nat.RQ_QMODE_CHANNEL,
                                       dyn_scale[bidx], None, None, maxq, sym, atomic, z_any, codes, err,
                                       gm_in, anchor, beta_rows, sos)
@@ -415,7 +425,7 @@ class GPTQPlus:
                             for sub in range(G):
                                 r0 = sub * R_s
                                 beta = torch.empty(R_s if beta_mode == 1 else 1, **f32)
-                                K.gptqplus_terms(Gs[r0:r0 + R_s], None if Hinit_all is None else Hinit_all[sub],
+                                K.gptqplus_terms(Gs[r0:r0 + R_s], None if hdiag_all is None else hdiag_all[sub],
                                                  Hinv_all[sub], alpha_eff, float(self.reference_loss),
                                                  beta_mode, beta, Z[r0:r0 + R_s], GH[r0:r0 + R_s], GH0,
                                                  z_flags[sub:sub + 1])
@@ -483,11 +493,12 @@ class GPTQPlus:
 
     @staticmethod
     def _chol_batch(C, G, dev):
-        """How many subgroups to factorise per launch: all of them when their fp64 workspaces
-        fit in 40 % of the free device memory, fewer otherwise."""
+        """How many subgroups to factorise per launch: all of them (at most
+        RQ_CHOL_MAXBATCH, the library's limit) when their fp64 workspaces fit in 40 % of the
+        free device memory, fewer otherwise."""
         per = int(nat.load().rq_chol_workspace_bytes(C))
         free, _ = torch.cuda.mem_get_info(dev)
-        return max(1, min(G, int(0.4 * free) // per))
+        return max(1, min(G, nat.RQ_CHOL_MAXBATCH, int(0.4 * free) // per))
 
     @property
     def codes(self):

@@ -143,10 +143,12 @@ def hessian_accum_multi(x, sals, Hs, acts):
              nbytes, _stream(x))
 
 
-def hessian_finalize(H, act_sq, h_div, sal_scale, seq_len, nonfinite=None):
+def hessian_finalize(H, act_sq, h_div, sal_scale, seq_len, nonfinite=None, sanitize=True):
+    """Mirror and scale H [G, C, C] in place; non-finite entries are counted into nonfinite
+    and, with sanitize, zeroed."""
     G, C, _ = H.shape
     nat.call("rq_hessian_finalize", nat.ptr(H), nat.ptr(act_sq), G, C, float(h_div), float(sal_scale),
-             float(seq_len), nat.ptr(nonfinite), _stream(H))
+             float(seq_len), int(bool(sanitize)), nat.ptr(nonfinite), _stream(H))
 
 
 def find_params(w, maxq, sym, group_size=-1):
@@ -197,14 +199,16 @@ def chol_workspace(C, device, nb=1):
     return torch.empty(nb * int(nat.load().rq_chol_workspace_bytes(C)), dtype=torch.uint8, device=device)
 
 
-def chol_hinv_attempt(H_work, damp_percent, workspace, Hinv, Hinv_init=None, info=None):
+def chol_hinv_attempt(H_work, damp_percent, workspace, Hinv, Hinv_init=None, info=None, Hinv_diag=None):
     """One damping attempt for H_work [C, C] or a batch [nb, C, C]; damp_percent is a float or a
-    list (entries <= 0 skip that matrix).  Returns the device info tensor [nb]."""
+    list (entries <= 0 skip that matrix).  Optional outputs: Hinv_init (H^-1) and Hinv_diag
+    (diag(H^-1), [C] or [nb, C]).  Returns the device info tensor [nb]."""
     batched = H_work.dim() == 3
     nb = H_work.shape[0] if batched else 1
     C = H_work.shape[-1]
-    _cout(H_work, "H_work"), _cout(Hinv, "Hinv"), _cout(Hinv_init, "Hinv_init")
-    if Hinv.numel() != nb * C * C or (Hinv_init is not None and Hinv_init.numel() != nb * C * C):
+    _cout(H_work, "H_work"), _cout(Hinv, "Hinv"), _cout(Hinv_init, "Hinv_init"), _cout(Hinv_diag, "Hinv_diag")
+    if Hinv.numel() != nb * C * C or (Hinv_init is not None and Hinv_init.numel() != nb * C * C) or \
+            (Hinv_diag is not None and Hinv_diag.numel() != nb * C):
         raise ValueError("chol_hinv_attempt: output shape mismatch")
     if workspace.numel() < nb * int(nat.load().rq_chol_workspace_bytes(C)):
         raise ValueError("chol_hinv_attempt: workspace too small")
@@ -215,19 +219,23 @@ def chol_hinv_attempt(H_work, damp_percent, workspace, Hinv, Hinv_init=None, inf
         info = torch.zeros(nb, dtype=torch.int32, device=H_work.device)
     arr = (ctypes.c_double * nb)(*[float(d) for d in damps])
     nat.call("rq_chol_hinv_attempt", nat.ptr(H_work), C, nb, arr, nat.ptr(workspace), nat.ptr(Hinv),
-             nat.ptr(Hinv_init), nat.ptr(info), _stream(H_work))
+             nat.ptr(Hinv_init), nat.ptr(Hinv_diag), nat.ptr(info), _stream(H_work))
     return info
 
 
-def gptqplus_terms(G_sub, Hinv_init, Hinv, alpha_eff, reference_loss, beta_mode, beta, Z, GHinv,
+def gptqplus_terms(G_sub, hinv_diag, Hinv, alpha_eff, reference_loss, beta_mode, beta, Z, GHinv,
                    GH0, z_nonzero):
+    """beta, Z = (G_sub Hinv^T) beta and GHinv = Z Hinv for one subgroup; hinv_diag = diag(H^-1)
+    [C] (beta_mode 1 only)."""
     R_s, C = G_sub.shape
     G_sub = _cin(G_sub, "G_sub")
-    Hinv_init = _cin(Hinv_init, "Hinv_init")
+    hinv_diag = _cin(hinv_diag, "hinv_diag")
+    if hinv_diag is not None and hinv_diag.numel() != C:
+        raise ValueError("gptqplus_terms: hinv_diag must hold C values")
     Hinv = _cin(Hinv, "Hinv")
     for t, n in ((beta, "beta"), (Z, "Z"), (GHinv, "GHinv"), (GH0, "GH0")):
         _cout(t, n)
-    nat.call("rq_gptqplus_terms", nat.ptr(G_sub), G_sub.stride(0), nat.ptr(Hinv_init), nat.ptr(Hinv),
+    nat.call("rq_gptqplus_terms", nat.ptr(G_sub), G_sub.stride(0), nat.ptr(hinv_diag), nat.ptr(Hinv),
              R_s, C, float(alpha_eff), float(reference_loss), int(beta_mode), nat.ptr(beta), nat.ptr(Z),
              nat.ptr(GHinv), Z.stride(0), nat.ptr(GH0), nat.ptr(z_nonzero), _stream(G_sub))
 

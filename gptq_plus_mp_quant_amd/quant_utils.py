@@ -74,6 +74,40 @@ class WeightQuantizer(torch.nn.Module):
                      nat.stream_of(w.device))
         return scale, zero
 
+    def params_grouped(self, w: torch.Tensor, group_size: int):
+        """(scale, zero) [ngroups, R] of the column groups of w, as ``find_params`` on each
+        slice ``w[:, g0:g0 + group_size]`` (static groups, gptq_plus_utils.py:994-1002): per row,
+        or with perchannel=False one value per group from the flattened slice, repeated over
+        the rows."""
+        if self.perchannel:
+            return self.params_on(w, group_size)
+        R, C = w.shape
+        ng = (C + group_size - 1) // group_size
+        scale = torch.empty((ng, R), device=w.device, dtype=torch.float32)
+        zero = torch.empty((ng, R), device=w.device, dtype=torch.float32)
+        for g in range(ng):
+            sg, zg = self.params_on(w[:, g * group_size:(g + 1) * group_size].reshape(1, -1))
+            scale[g].copy_(sg[0].expand(R))
+            zero[g].copy_(zg[0].expand(R))
+        return scale, zero
+
+    def row_params(self, w: torch.Tensor, rows_per_fit: int):
+        """(scale, zero) [R] for the block w [R, n] when ``find_params`` runs on each run of
+        rows_per_fit rows (a GPTQ+ subgroup's block start, gptq_plus_utils.py:1202-1209): per row,
+        or with perchannel=False one value per run of rows."""
+        if self.perchannel:
+            s, z = self.params_on(w)
+            return s[0], z[0]
+        R = w.shape[0]
+        scale = torch.empty(R, device=w.device, dtype=torch.float32)
+        zero = torch.empty(R, device=w.device, dtype=torch.float32)
+        for r0 in range(0, R, rows_per_fit):
+            r1 = min(R, r0 + rows_per_fit)
+            sg, zg = self.params_on(w[r0:r1].reshape(1, -1))
+            scale[r0:r1].copy_(sg[0].expand(r1 - r0))
+            zero[r0:r1].copy_(zg[0].expand(r1 - r0))
+        return scale, zero
+
     # utils/quant_utils.py:390-457
     def find_params(self, x) -> None:
         if self.bits == 16:

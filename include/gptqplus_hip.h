@@ -106,10 +106,12 @@ int rq_hessian_accum_multi(const void* x, int x_dtype, int64_t ntok, int64_t ldx
                            void* stream);
 
 /* GPTQPlus.finalize_hessian -- gptq_plus_utils.py:859-908 (world size 1).
- * H = sym(upper(H)) / h_div [/ sal_scale if != 1]; non-finite entries -> 0 and counted
- * into *nonfinite (device int, accumulated); act_sq /= seq_len. */
+ * H = sym(upper(H)) / h_div [/ sal_scale if != 1]; non-finite entries are counted into
+ * *nonfinite (device int, accumulated; may be NULL) and, with sanitize != 0 (GPTQPlus,
+ * :895-906), set to 0; sanitize = 0 keeps them (classic GPTQ, gptq_utils.py:63-106, whose
+ * Cholesky retries then fail and raise).  act_sq /= seq_len. */
 int rq_hessian_finalize(float* H, float* act_sq, int G, int C, double h_div, double sal_scale,
-                        double seq_len, int* nonfinite, void* stream);
+                        double seq_len, int sanitize, int* nonfinite, void* stream);
 
 /* WeightQuantizer.find_params, per-channel min/max -- utils/quant_utils.py:390-421
  * (static column groups: gptq_plus_utils.py:994-1002).  For each group k of `group_size`
@@ -141,28 +143,34 @@ int rq_prepare_subgroup(const void* w, int w_dtype, int64_t ldw, const float* gr
                         const float* H_g, int R_s, int C, const int64_t* perm, float* W_sub,
                         int64_t ld_wsub, float* G_sub, int64_t ld_gsub, float* H_sub, void* stream);
 
+/* Most matrices one rq_chol_hinv_attempt call factorises (nb). */
+#define RQ_CHOL_MAXBATCH 64
+
 /* Bytes of device workspace rq_chol_hinv_attempt needs per C x C matrix. */
 int64_t rq_chol_workspace_bytes(int C);
 
 /* One attempt of GPTQPlus._compute_hessian_inverse_with_fallback -- gptq_plus_utils.py:519-533,
- * for a batch of nb <= 64 subgroup matrices H_work[b] = H_work + b*C*C (one per row group):
+ * for a batch of nb <= RQ_CHOL_MAXBATCH subgroup matrices H_work[b] = H_work + b*C*C (one per row group):
  * H_work[b][i,i] += fl32(damp_percent[b]) * mean(diag(H_work[b]))  (in place: retries
  * accumulate, as in the reference), then Hinv[b] = upper Cholesky factor of H_work[b]^-1
- * (Hinv^T Hinv = H_work^-1) and, when Hinv_init != NULL, Hinv_init[b] = H_work[b]^-1.
- * damp_percent is a HOST array; entries <= 0 are skipped (left untouched).  Factorisation in
+ * (Hinv^T Hinv = H_work^-1), when Hinv_init != NULL, Hinv_init[b] = H_work[b]^-1, and when
+ * Hinv_diag != NULL, Hinv_diag[b] (C floats at b*C) = diag(H_work[b]^-1), the reference's
+ * torch.diagonal(hinv_init) (:184), without forming the matrix.  damp_percent is a HOST array; entries <= 0 are skipped (left untouched).  Factorisation in
  * fp64 (blocked, MFMA).  info (device int[nb]) is written per entry: 0 = done, > 0 = not
  * positive definite or non-finite result (caller raises the damping and retries that entry),
  * -1 = skipped.  workspace holds nb * rq_chol_workspace_bytes(C) bytes. */
 int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* damp_percent, void* workspace,
-                         float* Hinv, float* Hinv_init, int* info, void* stream);
+                         float* Hinv, float* Hinv_init, float* Hinv_diag, int* info, void* stream);
 
 /* GPTQPlus._compute_gradient_terms -- gptq_plus_utils.py:563-578 with
  * compute_safe_beta_from_reference_loss -- :174-194.
  * beta_mode 0: beta = 0 (alpha <= 0 or gradient update off; beta has 1 element);
- * beta_mode 1: beta[r] from G_sub, Hinv_init (needs GH0 workspace [R_s, C]).
+ * beta_mode 1: beta[r] from G_sub, hinv_diag = diag(H^-1) (C floats, from rq_chol_hinv_attempt)
+ * and the reference's G_sub Hinv_init (:180), formed as (G_sub Hinv^T) Hinv in the GH0
+ * workspace [R_s, C] (Hinv^T Hinv = Hinv_init: two triangular products, no full H^-1).
  * Z = (G_sub Hinv^T) * beta, GHinv = Z Hinv.  *z_nonzero (device int) is set to 1 when any Z
  * element is non-zero or NaN; 0 lets later kernels skip provably-zero first-order work. */
-int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* Hinv_init, const float* Hinv,
+int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* hinv_diag, const float* Hinv,
                       int R_s, int C, double alpha_eff, double reference_loss, int beta_mode,
                       float* beta, float* Z, float* GHinv, int64_t ldz, float* GH0,
                       int* z_nonzero, void* stream);

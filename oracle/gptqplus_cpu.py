@@ -741,9 +741,9 @@ class GPTQPlusOracle:
 # ---------------------------------------------------------------------------------------
 # Convenience drivers used by tests and the CPU baseline
 # ---------------------------------------------------------------------------------------
-def make_quantizer(bits, sym=True, mse=False) -> WeightQuantizerOracle:
+def make_quantizer(bits, sym=True, mse=False, perchannel=True) -> WeightQuantizerOracle:
     q = WeightQuantizerOracle()
-    q.configure(bits, perchannel=True, sym=sym, mse=mse)
+    q.configure(bits, perchannel=perchannel, sym=sym, mse=mse)
     return q
 
 

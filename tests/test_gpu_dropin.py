@@ -46,13 +46,13 @@ def _exact_with_terms(m):
             and (not m["atomic"] or m["B"] <= 32))
 
 
-def _gpu_obj(W, s, grad, G, alpha, ref_loss, bits, sym, mse=False):
+def _gpu_obj(W, s, grad, G, alpha, ref_loss, bits, sym, mse=False, perchannel=True):
     R, C = W.shape
     layer = torch.nn.Linear(C, R, bias=False).to(DEV, W.dtype)
     layer.weight.data.copy_(W.to(DEV))
     g = GPTQPlus(layer, saliency=s, gradient=grad, num_groups=G, alpha=alpha, reference_loss=ref_loss)
     g.quantizer = WeightQuantizer()
-    g.quantizer.configure(bits, perchannel=True, sym=sym, mse=mse)
+    g.quantizer.configure(bits, perchannel=perchannel, sym=sym, mse=mse)
     return g, layer
 
 
@@ -175,6 +175,11 @@ CFGS = [
     dict(name="g2_sym4_block_gd_sgd_gateopt_static", R=128, C=384, G=2, bits=4, sym=True, gs=128, act=True, B=128, atomic=False, alpha=0.05, ref_loss=100.0, gscale=1e-1, mode="block_gd",
          fq=dict(grad_optimizer="sgd", grad_lr=4e-3, grad_reg_strategy="quant_error_gate_optimized", grad_gate_floor=0.2, grad_gate_sharpness=2.0, grad_gate_sine_amp=0.001)),
     dict(name="g4_sym4_block_backward", R=256, C=512, G=4, bits=4, sym=True, gs=-1, act=True, B=128, atomic=False, alpha=0.05, ref_loss=100.0, gscale=1e-1, mode="block_backward"),
+    # perchannel=False: one scale per static group over all rows / per subgroup block
+    dict(name="g2_sym4_static_pertensor", R=256, C=512, G=2, bits=4, sym=True, gs=128, act=True, B=128, atomic=False, alpha=0.0, pc=False),
+    dict(name="g2_asym4_dynamic_pertensor", R=256, C=512, G=2, bits=4, sym=False, gs=128, act=False, B=128, atomic=False, alpha=0.0, pc=False),
+    # more subgroups than one Cholesky launch takes (RQ_CHOL_MAXBATCH = 64): two launches
+    dict(name="g80_sym4_many_subgroups", R=640, C=192, G=80, bits=4, sym=True, gs=-1, act=True, B=128, atomic=False, alpha=0.0),
 ]
 
 
@@ -192,7 +197,7 @@ def test_dropin_vs_oracle(cfg):
     X, W, s, grad = synth(sum(map(ord, cfg["name"])), R, C, G, N, T, gscale=cfg.get("gscale", 1e-4))
     alpha, ref_loss = cfg["alpha"], cfg.get("ref_loss", 0.0)
     o = GPTQPlusOracle(W, s, grad, G, alpha, ref_loss)
-    o.quantizer = make_quantizer(cfg["bits"], cfg["sym"], cfg.get("mse", False))
+    o.quantizer = make_quantizer(cfg["bits"], cfg["sym"], cfg.get("mse", False), cfg.get("pc", True))
     for j in range(0, N, 4):
         o.add_batch(X[j:j + 4])
     o.finalize_hessian()
@@ -201,7 +206,8 @@ def test_dropin_vs_oracle(cfg):
               **_mode_kwargs(cfg, X, W, grad))
     res = o.fasterquant(**fq)
 
-    g, layer = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False))
+    g, layer = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False),
+                          cfg.get("pc", True))
     _accumulate(g, X, 4)
     assert rel_fro(g.H, o.H) <= 1e-5
     assert torch.equal(g.act_square.cpu(), o.act_square)
@@ -222,7 +228,8 @@ def test_dropin_vs_oracle(cfg):
     terms_flips = None
     if alpha > 0:
         layer.weight.data.copy_(W.to(DEV))
-        gt, layer_t = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False))
+        gt, layer_t = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False),
+                          cfg.get("pc", True))
         gt.H, gt.act_square, gt._finalized = o.H.to(DEV).clone(), o.act_square.to(DEV).clone(), True
         inject_t = dict(inject, terms=[(r.beta.to(DEV), r.Z.to(DEV), r.GHinv.to(DEV)) for r in res.subgroups])
         gt.fasterquant(export_to_et=True, inject=inject_t, **fq)
@@ -237,7 +244,8 @@ def test_dropin_vs_oracle(cfg):
     assert flips_same <= FLIP_BAR.get(cfg["name"], n // 10000), flips_same
     # (2) own fp64 Cholesky chain
     layer.weight.data.copy_(W.to(DEV))
-    g2, layer2 = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False))
+    g2, layer2 = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False),
+                          cfg.get("pc", True))
     g2.H = o.H.to(DEV).clone()
     g2.act_square = o.act_square.to(DEV).clone()
     g2._finalized = True

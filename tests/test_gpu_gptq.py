@@ -22,13 +22,13 @@ DEV = torch.device("cuda:0")
 GOLD = GoldenSet.load().gptq_cases
 
 
-def _drop_in(W, X, bits, sym, mse=False):
+def _drop_in(W, X, bits, sym, mse=False, perchannel=True):
     R, C = W.shape
     layer = torch.nn.Linear(C, R, bias=False).to(DEV, W.dtype)
     layer.weight.data.copy_(W.to(DEV))
     g = GPTQ(layer)
     g.quantizer = WeightQuantizer()
-    g.quantizer.configure(bits, perchannel=True, sym=sym, mse=mse)
+    g.quantizer.configure(bits, perchannel=perchannel, sym=sym, mse=mse)
     for j in range(X.shape[0]):
         g.add_batch(X[j].unsqueeze(0).to(DEV), None)
     return g, layer
@@ -59,7 +59,7 @@ def _expected(case, H_gpu):
 
 def _finalized_H(g):
     H = g.H.clone().view(1, g.columns, g.columns)
-    K.hessian_finalize(H, None, g.nsamples / 2.0, 1.0, 1.0)
+    K.hessian_finalize(H, None, g.nsamples / 2.0, 1.0, 1.0, sanitize=False)
     return H[0]
 
 
@@ -104,6 +104,9 @@ CFGS = [
     dict(name="asym4_static_act", R=256, C=512, bits=4, sym=False, gs=128, act=True, B=128),
     dict(name="sym4_dynamic_gs64_B128", R=256, C=384, bits=4, sym=True, gs=64, act=False, B=128),
     dict(name="asym3_dynamic_gs256_B128", R=128, C=512, bits=3, sym=False, gs=256, act=False, B=128),
+    # perchannel=False: one (scale, zero) per column group over all rows
+    dict(name="asym4_static_act_pertensor", R=256, C=512, bits=4, sym=False, gs=128, act=True, B=128, pc=False),
+    dict(name="sym4_dynamic_gs64_pertensor", R=256, C=384, bits=4, sym=True, gs=64, act=False, B=128, pc=False),
 ]
 
 
@@ -117,7 +120,7 @@ def test_gptq_vs_oracle(cfg, tmp_path):
 
     def oracle(H=None):
         o = GPTQOracle(W)
-        o.quantizer = make_quantizer(cfg["bits"], cfg["sym"])
+        o.quantizer = make_quantizer(cfg["bits"], cfg["sym"], perchannel=cfg.get("pc", True))
         for j in range(X.shape[0]):
             o.add_batch(X[j].unsqueeze(0))
         H_own = o.H.clone()
@@ -127,7 +130,7 @@ def test_gptq_vs_oracle(cfg, tmp_path):
                             static_groups=cfg["act"])
         return H_own, res, o.perm
 
-    g, layer = _drop_in(W, X, cfg["bits"], cfg["sym"])
+    g, layer = _drop_in(W, X, cfg["bits"], cfg["sym"], perchannel=cfg.get("pc", True))
     H_gpu = _finalized_H(g).cpu()
     H_o, res_own, _ = oracle()
     assert rel_fro(H_gpu, H_o) <= 1e-5
@@ -156,3 +159,21 @@ def test_gptq_vs_oracle(cfg, tmp_path):
     assert abs(e_gpu - e_ref) <= 0.005 * e_ref
     # the packed export reproduces the layer weight for every group layout
     assert torch.equal(dequantize_packed(g.export_packed()).cpu(), layer.weight.data.cpu())
+
+
+def test_gptq_nonfinite_activation_raises():
+    """A NaN activation makes H non-finite.  The reference's GPTQ keeps it: every damped
+    Cholesky attempt fails and fasterquant raises ValueError once damp_percent reaches 1
+    (gptq_utils.py:87-104) -- the oracle does the same here.  (GPTQPlus instead sanitises H in
+    finalize_hessian.)"""
+    X, W, _, _ = synth(5, 64, 128, 1, 2, 64)
+    X[0, 3, 7] = float("nan")
+    o = GPTQOracle(W)
+    o.quantizer = make_quantizer(4, True)
+    for j in range(X.shape[0]):
+        o.add_batch(X[j].unsqueeze(0))
+    with pytest.raises(ValueError, match="damp_percent"):
+        o.fasterquant(blocksize=128, groupsize=-1, actorder=True, static_groups=True)
+    g, layer = _drop_in(W, X, 4, True)
+    with pytest.raises(ValueError, match="damp_percent"):
+        g.fasterquant(blocksize=128, groupsize=-1, actorder=True, static_groups=True)

@@ -129,6 +129,19 @@ def test_finalize_sanitises_nonfinite():
     assert H[1, 3, 40] == 0 and H[1, 40, 3] == 0 and H[0, 5, 5] == 0 and H[0, 6, 6] == 0.5
 
 
+def test_finalize_keeps_nonfinite_unsanitised():
+    """sanitize=False (classic GPTQ): the same count, the entries (and their mirrors) kept."""
+    H = torch.eye(70, device=DEV).repeat(2, 1, 1)
+    H[1, 3, 40] = float("nan")
+    H[0, 5, 5] = float("inf")
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    K.hessian_finalize(H, None, 2.0, 1.0, 1.0, bad, sanitize=False)
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 3
+    assert bool(H[1, 3, 40].isnan()) and bool(H[1, 40, 3].isnan()) and H[0, 5, 5] == float("inf")
+    assert int((~torch.isfinite(H)).sum()) == 3 and H[0, 6, 6] == 0.5
+
+
 @pytest.mark.parametrize("bits,sym", [(4, True), (4, False), (3, True), (2, False), (8, True), (8, False)])
 @pytest.mark.parametrize("gs", [-1, 32])
 def test_find_params_bitexact(bits, sym, gs):
@@ -224,11 +237,15 @@ def test_cholesky_chain(C):
     ws = K.chol_workspace(C, DEV)
     Hinv = torch.empty(C, C, device=DEV)
     Hinit = torch.empty(C, C, device=DEV)
-    info = K.chol_hinv_attempt(Hw, 0.01, ws, Hinv, Hinit)
+    hdiag = torch.empty(C, device=DEV)
+    info = K.chol_hinv_attempt(Hw, 0.01, ws, Hinv, Hinit, Hinv_diag=hdiag)
     torch.cuda.synchronize()
     assert int(info.item()) == 0
     assert rel_fro(Hinv, Hinv_o) <= 1e-4
     assert rel_fro(Hinit, Hinv_init_o) <= 1e-4
+    # the diagonal output (column norms of L^-1) against the formed H^-1: fp64 sums in two
+    # orders, rounded to fp32 -- equal up to one fp32 rounding step
+    assert float(((hdiag - torch.diagonal(Hinit)).abs() / torch.diagonal(Hinit)).max()) <= 2 ** -23
     assert torch.equal(Hinv, torch.triu(Hinv)) and (torch.diag(Hinv) > 0).all()
     assert torch.equal(Hinit, Hinit.T)
     # float64 truth on the same damped matrix
@@ -237,6 +254,8 @@ def test_cholesky_chain(C):
     U = scipy.linalg.cholesky(inv, lower=False)
     assert rel_fro(Hinit, torch.from_numpy(inv)) <= 1e-5
     assert rel_fro(Hinv, torch.from_numpy(U)) <= 1e-5
+    d_true = torch.from_numpy(np.diag(inv).copy())
+    assert float(((hdiag.double().cpu() - d_true).abs() / d_true).max()) <= 1e-5
     # damping applied in place exactly like the reference's first attempt
     Hd_ref = H.clone()
     idx = torch.arange(C)
@@ -258,15 +277,19 @@ def test_cholesky_chain_wide_panels(C):
     Hw = H.clone()
     ws = K.chol_workspace(C, DEV)
     Hinv = torch.empty(C, C, device=DEV)
-    info = K.chol_hinv_attempt(Hw, 0.01, ws, Hinv, None)
+    hdiag = torch.empty(C, device=DEV)
+    info = K.chol_hinv_attempt(Hw, 0.01, ws, Hinv, None, Hinv_diag=hdiag)
     torch.cuda.synchronize()
     assert int(info.item()) == 0
     assert torch.equal(Hinv, torch.triu(Hinv)) and bool((torch.diag(Hinv) > 0).all())
     Hd = Hw.double().cpu().numpy()
-    U_true = torch.from_numpy(scipy.linalg.cholesky(np.linalg.inv(Hd), lower=False))
+    inv = np.linalg.inv(Hd)
+    U_true = torch.from_numpy(scipy.linalg.cholesky(inv, lower=False))
     err = rel_fro(Hinv, U_true)
-    print(f"C={C}: rel-Frobenius vs float64 truth {err:.2e}")
-    assert err <= 1e-5
+    d_true = torch.from_numpy(np.diag(inv).copy())
+    derr = float(((hdiag.double().cpu() - d_true).abs() / d_true).max())
+    print(f"C={C}: rel-Frobenius vs float64 truth {err:.2e}, diag(H^-1) max rel {derr:.2e}")
+    assert err <= 1e-5 and derr <= 1e-5
 
 
 @pytest.mark.parametrize("C", [200, 600])
@@ -280,14 +303,16 @@ def test_cholesky_batch_independent_entries(C):
     ws = K.chol_workspace(C, DEV, 4)
     Hinv = torch.zeros(4, C, C, device=DEV)
     Hinit = torch.zeros(4, C, C, device=DEV)
-    info = K.chol_hinv_attempt(Hw, damps, ws, Hinv, Hinit)
+    hdiag = torch.zeros(4, C, device=DEV)
+    info = K.chol_hinv_attempt(Hw, damps, ws, Hinv, Hinit, Hinv_diag=hdiag)
     torch.cuda.synchronize()
     codes = info.tolist()
     assert codes[0] == 0 and codes[1] == 0 and codes[2] > 0 and codes[3] == -1
-    assert torch.equal(Hw[3], before[3]) and not Hinv[3].any()
+    assert torch.equal(Hw[3], before[3]) and not Hinv[3].any() and not hdiag[3].any()
     for b in (0, 1):
         Hi_o, Hv_o, *_ = hessian_inverse_with_fallback(Hs[b], damps[b])
         assert rel_fro(Hinv[b], Hv_o) <= 1e-4 and rel_fro(Hinit[b], Hi_o) <= 1e-4
+        assert rel_fro(hdiag[b], torch.diagonal(Hi_o)) <= 1e-5
 
 
 @pytest.mark.parametrize("neg", [0.05, 0.3, 5.0])
@@ -322,8 +347,10 @@ def test_gptqplus_terms(alpha, ref_loss):
     GH = torch.empty(R_s, C, device=DEV)
     GH0 = torch.empty(R_s, C, device=DEV) if mode else None
     nz = torch.zeros(1, dtype=torch.int32, device=DEV)
-    K.gptqplus_terms(Gs.to(DEV), Hinit_o.to(DEV) if mode else None, Hinv_o.to(DEV), a_eff, ref_loss, mode,
-                     beta, Z, GH, GH0, nz)
+    # beta_mode 1 takes diag(H^-1) and forms G Hinv_init as (G Hinv^T) Hinv (Hinv^T Hinv = Hinv_init
+    # up to the oracle's fp32 factorisation, so the bars below also bound that rewrite)
+    hdiag = torch.diagonal(Hinit_o).contiguous().to(DEV) if mode else None
+    K.gptqplus_terms(Gs.to(DEV), hdiag, Hinv_o.to(DEV), a_eff, ref_loss, mode, beta, Z, GH, GH0, nz)
     torch.cuda.synchronize()
     if alpha > 0 and ref_loss > 0:
         assert rel_fro(beta, beta_o) <= 1e-5 and beta_o.min() > 0.0

@@ -40,8 +40,8 @@ def test_argument_validation_needs_no_device():
     assert lib.rq_find_params(null, 0, 4, 4, 4, -1, 7, 1, null, null, null) == nat.RQ_EINVAL
     assert lib.rq_act_order_perm(null, 4, null, null, null) == nat.RQ_EINVAL
     damp = (ctypes.c_double * 1)(0.01)
-    assert lib.rq_chol_hinv_attempt(null, 4, 1, damp, null, null, null, null, null) == nat.RQ_EINVAL
-    assert lib.rq_chol_hinv_attempt(null, 4, 65, damp, null, null, null, null, null) == nat.RQ_EINVAL
+    assert lib.rq_chol_hinv_attempt(null, 4, 1, damp, null, null, null, null, null, null) == nat.RQ_EINVAL
+    assert lib.rq_chol_hinv_attempt(null, 4, 65, damp, null, null, null, null, null, null) == nat.RQ_EINVAL
     assert lib.rq_quant_block(null, 4, null, 4, null, null, 4, 4, 4, 0, 4, 0, null, null, null, 7, 1,
                               0, null, null, null, 0, null, 4, null, 1.0, null) == nat.RQ_EINVAL
     assert lib.rq_trailing_update(null, 4, null, null, 4, null, 4, 4, 4, 0, 4, null, null, 0, 0, null, 4,

@@ -81,6 +81,17 @@ def test_find_params_known_answers(row, bits, sym, scale, zero):
     assert q.zero.item() == zero
 
 
+@pytest.mark.parametrize("sym,scale,zero", [(True, 3.0 / 7, 0.0), (False, 4.0 / 15, 4.0)])
+def test_find_params_per_tensor_known_answer(sym, scale, zero):
+    """perchannel=False: one range over the whole tensor (min -1.0 in row 1, max 3.0 in row 0),
+    repeated for every row -- rows with their own ranges would give other values."""
+    q = make_quantizer(4, sym, perchannel=False)
+    q.find_params(torch.tensor([[0.5, 3.0], [-1.0, 0.25], [0.1, 0.2]], dtype=torch.float32))
+    assert q.scale.shape == (3, 1) and q.zero.shape == (3, 1)
+    assert torch.allclose(q.scale.flatten(), torch.full((3,), scale), rtol=1e-7, atol=0)
+    assert torch.equal(q.zero.flatten(), torch.full((3,), zero))
+
+
 @pytest.mark.parametrize("bits,sym", [(4, True), (4, False), (3, True), (2, False)])
 def test_fake_quantize_is_nearest_grid_point(bits, sym):
     """Brute force over every code: fake_quantize picks the nearest point of
