@@ -19,7 +19,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIBDIR = PKG / "_lib"
 LIB = LIBDIR / "libgptqplus_hip.so"
-SOURCES = ["hessian.hip", "params.hip", "argsort.hip", "chol.hip", "colloop.hip", "pack.hip", "blockgd.hip"]
+SOURCES = ["hessian.hip", "params.hip", "argsort.hip", "chol.hip", "terms.hip", "colloop.hip", "pack.hip",
+           "blockgd.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -55,7 +56,7 @@ def build(verbose: bool = False) -> Path:
             print(f"compiled {src}", flush=True)
         return out
 
-    with ThreadPoolExecutor(max_workers=min(7, len(SOURCES))) as ex:
+    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
         objs = list(ex.map(compile_one, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])

@@ -1,6 +1,5 @@
 // Damped Cholesky chain (GPTQPlus._compute_hessian_inverse_with_fallback,
-// gptq_utils/gptq_plus_utils.py:494-561) and the GPTQ+ first-order terms
-// (_compute_gradient_terms :563-578, compute_safe_beta_from_reference_loss :174-194).
+// gptq_utils/gptq_plus_utils.py:494-561).
 //
 // The reference computes chol(H) -> cholesky_inverse -> chol(H^-1, upper) in fp32.  Here the
 // upper factor U of H^-1 (U^T U = H^-1) is obtained with ONE factorisation: with P the
@@ -28,8 +27,6 @@ constexpr int CG = 4;      // columns factored per barrier in the diagonal block
 // in-panel work (C^2 NBW / 2 flops) stays ~1 % of the C^3 chain there.
 __host__ __device__ constexpr int panel_width(int C) { return C >= 8192 ? 512 : 256; }
 
-__global__ void k_fill_i32(int* p, int v) { *p = v; }
-__global__ void k_fill_f32(float* p, float v) { *p = v; }
 
 constexpr int MAXBATCH = 64;
 struct BatchCfg {
@@ -360,102 +357,6 @@ __global__ __launch_bounds__(256) void k_diag_final(const double* __restrict__ p
   const float v = (float)s;
   diag[(int64_t)b * C + (C - 1 - p)] = v;
   if (!rq_isfinite(v)) atomicExch(info, 3);
-}
-
-// Z[r][j] = Y[r][j] * beta[r] in place (fl32 of the fp32 product, as the reference's
-// `(G @ Hinv.T) * beta_view`); *nz = 1 when any result is non-zero or NaN.
-__global__ __launch_bounds__(256) void k_row_scale_flag(float* __restrict__ Z, int64_t ldz, int R, int C,
-                                                        const float* __restrict__ beta, int* __restrict__ nz) {
-  int any = 0;
-  for (int r = blockIdx.y; r < R; r += gridDim.y) {
-    const float bv = beta[r];
-    for (int j = blockIdx.x * 256 + threadIdx.x; j < C; j += gridDim.x * 256) {
-      float* z = Z + (int64_t)r * ldz + j;
-      const float v = *z * bv;
-      *z = v;
-      any |= (v != 0.0f) | (v != v);
-    }
-  }
-  if (__any(any) && (threadIdx.x & 63) == 0) atomicOr(nz, 1);
-}
-
-// *out = max(*out, max_i |x_i|) as fp32 bit patterns (non-negative floats order like their
-// bits, and a NaN's bits exceed +inf's).  *out starts at 0.
-// 16-byte loads where x is 16-byte aligned; one atomic per workgroup.
-__global__ __launch_bounds__(256) void k_absmax_bits(const float* __restrict__ x, int64_t n,
-                                                     unsigned* __restrict__ out) {
-  __shared__ unsigned wm[4];
-  unsigned m = 0u;
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  int64_t done = 0;
-  if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
-    const int64_t n4 = n / 4;
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    for (int64_t i = i0; i < n4; i += stride) {
-      const float4 v = x4[i];
-      m = max(m, max(max(__float_as_uint(fabsf(v.x)), __float_as_uint(fabsf(v.y))),
-                     max(__float_as_uint(fabsf(v.z)), __float_as_uint(fabsf(v.w)))));
-    }
-    done = 4 * n4;
-  }
-  for (int64_t i = done + i0; i < n; i += stride) m = max(m, __float_as_uint(fabsf(x[i])));
-  for (int o = 32; o > 0; o >>= 1) m = max(m, (unsigned)__shfl_xor((int)m, o, 64));
-  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    m = max(max(wm[0], wm[1]), max(wm[2], wm[3]));
-    if (m) atomicMax(out, m);
-  }
-}
-
-// need |= some row r with !(sum_k |G[r][k]| * mh < 3e38) (fp64 sums; a non-finite G or mh
-// fails the test).  One wavefront per row.
-__global__ __launch_bounds__(256) void k_z_rows_need(const float* __restrict__ G, int64_t ldg, int R,
-                                                     int C, const float* __restrict__ mh,
-                                                     int* __restrict__ need) {
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (r >= R) return;
-  double s = 0.0;
-  for (int k = lane; k < C; k += 64) s += (double)fabsf(G[(int64_t)r * ldg + k]);
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-  if (lane == 0 && !(s * (double)*mh < 3.0e38)) atomicOr(need, 1);
-}
-
-// compute_safe_beta_from_reference_loss row statistics (gptq_plus_utils.py:183-193).
-// One wavefront per row.
-__global__ __launch_bounds__(256) void k_safe_beta(const float* __restrict__ G, int64_t ldg,
-                                                   const float* __restrict__ GH0,
-                                                   const float* __restrict__ hdiag, int R, int C,
-                                                   float target, float* __restrict__ beta) {
-  const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= R) return;
-  float s1 = 0.0f, s2 = 0.0f;
-  for (int j = lane; j < C; j += 64) {
-    const float gh = GH0[(int64_t)r * C + j];
-    s1 += G[(int64_t)r * ldg + j] * gh;
-    s2 += (gh * gh) / hdiag[j];
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    s1 += __shfl_xor(s1, o, 64);
-    s2 += __shfl_xor(s2, o, 64);
-  }
-  if (lane == 0) {
-    float c = s1 - s2 / (float)C;
-    c = (c < target) ? target : c;                        // clamp(c, min=target)
-    float ratio = (c > 0.0f) ? target / c : 0.0f;         // where(c > 0, target / c, 0)
-    ratio = (ratio < 0.0f) ? 0.0f : ratio;
-    ratio = (ratio > 1.0f) ? 1.0f : ratio;
-    float om = 1.0f - ratio;
-    om = (om < 0.0f) ? 0.0f : om;
-    float b = 1.0f - sqrtf(om);
-    if (b != b) b = 0.0f;                                 // nan_to_num(nan=0, posinf=1, neginf=0)
-    else if (b == __builtin_inff()) b = 1.0f;
-    else if (b == -__builtin_inff()) b = 0.0f;
-    beta[r] = b;
-  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -903,82 +804,5 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
     hipLaunchKernelGGL(k_output_full, gcol, blk, 0, s, A, C, Hinv_init, ws, info);
     RQ_CHECK_LAUNCH();
   }
-  return RQ_OK;
-}
-
-extern "C" int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* hinv_diag,
-                                 const float* Hinv, int R_s, int C, double alpha_eff,
-                                 double reference_loss, int beta_mode, float* beta, float* Z,
-                                 float* GHinv, int64_t ldz, float* GH0, int* z_nonzero,
-                                 void* stream) {
-  using namespace rq;
-  if (!G_sub || !Hinv || !beta || !Z || !GHinv || !z_nonzero || R_s <= 0 || C <= 0 || ldg < C ||
-      ldz < C)
-    return RQ_EINVAL;
-  if (beta_mode == 1 && (!hinv_diag || !GH0)) return RQ_EINVAL;
-  if (beta_mode != 0 && beta_mode != 1) return RQ_EINVAL;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  int rc;
-  if (beta_mode == 1) {
-    if (reference_loss <= 0) {
-      // beta = zeros(R_s) (:181-183): the GEMMs below then produce exact zeros.
-      hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(1), 0, s, beta, 0.0f);
-      beta_mode = 0;
-    } else {
-      // Y = G_sub Hinv^T (the reference's G Hinv^T before its beta scaling) into Z, then
-      // GH0 = Y Hinv = G Hinv^T Hinv = G Hinv_init, the reference's ghinv_init (:180), through
-      // the factor: two triangular products in place of the full one, and no H^-1 needed
-      // beyond its diagonal.
-      GemmArgs<float> y = gemm_args<float>(G_sub, ldg, Hinv, C, Z, ldz, R_s, C, C, 1.0f, EPI_STORE);
-      y.krange = KR_B_LOWER;
-      if ((rc = launch_gemm(y, false, true, s))) return rc;
-      GemmArgs<float> g = gemm_args<float>(Z, ldz, Hinv, C, GH0, C, R_s, C, C, 1.0f, EPI_STORE);
-      g.krange = KR_B_UPPER;
-      if ((rc = launch_gemm(g, false, false, s))) return rc;
-      const float target = (float)(2.0 * alpha_eff * reference_loss);
-      hipLaunchKernelGGL(k_safe_beta, dim3((R_s + 3) / 4), dim3(256), 0, s, G_sub, ldg, GH0,
-                         hinv_diag, R_s, C, target, beta);
-      // Z = Y * beta (row-wise, in place), then GHinv = Z Hinv as below
-      hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(1), 0, s, z_nonzero, 0);
-      hipLaunchKernelGGL(k_row_scale_flag, dim3((C + 255) / 256 < 8 ? (C + 255) / 256 : 8, R_s < 65535 ? R_s : 65535),
-                         dim3(256), 0, s, Z, ldz, R_s, C, (const float*)beta, z_nonzero);
-      RQ_CHECK_LAUNCH();
-      GemmArgs<float> h = gemm_args<float>(Z, ldz, Hinv, C, GHinv, ldz, R_s, C, C, 1.0f, EPI_STORE);
-      h.krange = KR_B_UPPER;
-      h.skip_if_zero = z_nonzero;
-      return launch_gemm(h, false, false, s);
-    }
-  } else {
-    hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(1), 0, s, beta, 0.0f);
-  }
-  hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(1), 0, s, z_nonzero, 0);
-  RQ_CHECK_LAUNCH();
-  // Z = (G_sub Hinv^T) * beta ; Hinv upper => B(k, j) = Hinv[j][k] vanishes for k < j
-  GemmArgs<float> z = gemm_args<float>(G_sub, ldg, Hinv, C, Z, ldz, R_s, C, C, 1.0f, EPI_STORE);
-  z.krange = KR_B_LOWER;
-  z.row_scale = beta;
-  z.row_bcast = (beta_mode == 0);
-  z.nz_flag = z_nonzero;
-  if (beta_mode == 0) {
-    // With beta = 0, Z is zero unless a product or a partial sum of G Hinv^T is not finite
-    // (then the reference's 0 * inf is NaN).  Every partial sum of row r is bounded by
-    // sum_k |G[r][k]| * max|Hinv|, so when that bound stays well inside the fp32 range for
-    // every row (and G is finite) Z is zero and the product is skipped: z_nonzero stays 0,
-    // and the Z launch only stores zeros.  Otherwise z_nonzero is raised and Z is formed.
-    // max|Hinv| passes through beta's storage (as bits), which is reset to 0 afterwards.
-    unsigned* mh = reinterpret_cast<unsigned*>(beta);
-    hipLaunchKernelGGL(k_absmax_bits, dim3(1024), dim3(256), 0, s, Hinv, (int64_t)C * C, mh);
-    hipLaunchKernelGGL(k_z_rows_need, dim3((R_s + 3) / 4), dim3(256), 0, s, G_sub, ldg, R_s, C,
-                       (const float*)beta, z_nonzero);
-    hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(1), 0, s, beta, 0.0f);
-    RQ_CHECK_LAUNCH();
-    z.skip_if_zero = z_nonzero;
-  }
-  if ((rc = launch_gemm(z, false, true, s))) return rc;
-  // GHinv = Z Hinv ; B(k, j) = Hinv[k][j] vanishes for k > j; all-zero Z -> zeros
-  GemmArgs<float> h = gemm_args<float>(Z, ldz, Hinv, C, GHinv, ldz, R_s, C, C, 1.0f, EPI_STORE);
-  h.krange = KR_B_UPPER;
-  h.skip_if_zero = z_nonzero;
-  if ((rc = launch_gemm(h, false, false, s))) return rc;
   return RQ_OK;
 }

@@ -343,19 +343,21 @@ class GPTQPlus:
                             hdiag_all[sub].copy_(torch.diagonal(inject_hinv[sub][0]))
                         chain.append((float(percdamp), False, 0))
             del H_work
-            GH0 = torch.empty((R_s, C), **f32) if beta_mode == 1 else None
+            # GPTQ+ terms of every subgroup in one call (GH0 and Hinv^T: its workspaces)
+            GH0 = torch.empty((R, C), **f32) if beta_mode == 1 else None
+            HinvT = torch.empty((G, C, C), **f32) if beta_mode == 1 else None
             z_flags = torch.zeros(G, dtype=torch.int32, device=dev)
             alpha_eff = self.alpha / (R * C) if beta_mode == 1 else 0.0
+            beta_all = torch.empty(R if beta_mode == 1 else 1, **f32)
+            with _section(rec, "fasterquant.subgroup.init_ghinv"):
+                K.gptqplus_terms(Gs, hdiag_all, Hinv_all, alpha_eff, float(self.reference_loss), beta_mode,
+                                 beta_all, Z, GH, GH0, z_flags, HinvT)
+            if beta_mode == 1 and self.reference_loss <= 0:
+                beta_all = torch.zeros(R, **f32)
             self.subgroup_info = []
             for sub in range(G):
                 r0 = sub * R_s
-                beta = torch.empty(R_s if beta_mode == 1 else 1, **f32)
-                with _section(rec, "fasterquant.subgroup.init_ghinv"):
-                    K.gptqplus_terms(Gs[r0:r0 + R_s], None if hdiag_all is None else hdiag_all[sub],
-                                     Hinv_all[sub], alpha_eff, float(self.reference_loss), beta_mode, beta,
-                                     Z[r0:r0 + R_s], GH[r0:r0 + R_s], GH0, z_flags[sub:sub + 1])
-                if beta_mode == 1 and self.reference_loss <= 0:
-                    beta = torch.zeros(R_s, **f32)
+                beta = beta_all[r0:r0 + R_s] if beta_mode == 1 else beta_all
                 if inject.get("terms") is not None:   # test hook: given (beta, Z, GHinv)
                     b_in, z_in, gh_in = inject["terms"][sub]
                     beta = b_in.to(**f32).reshape(-1).clone()
@@ -367,7 +369,7 @@ class GPTQPlus:
                 self.subgroup_info.append(dict(damp_percent=damp, identity_fallback=fallback,
                                                attempts=attempts, beta=beta))
             if not block_bw:
-                del Gs, GH0
+                del Gs, GH0, HinvT
             beta_rows = None
             if surrogate:
                 beta_rows = torch.zeros(R, **f32)
@@ -421,16 +423,11 @@ class GPTQPlus:
                         with _section(rec, "fasterquant.block.true_gradient_refresh"):
                             grad, meta = gradient_refresh_fn(snapshot(i2))
                             K.gather_cols(refreshed(grad), perm, out=Gs)
-                            z_flags.zero_()
-                            for sub in range(G):
-                                r0 = sub * R_s
-                                beta = torch.empty(R_s if beta_mode == 1 else 1, **f32)
-                                K.gptqplus_terms(Gs[r0:r0 + R_s], None if hdiag_all is None else hdiag_all[sub],
-                                                 Hinv_all[sub], alpha_eff, float(self.reference_loss),
-                                                 beta_mode, beta, Z[r0:r0 + R_s], GH[r0:r0 + R_s], GH0,
-                                                 z_flags[sub:sub + 1])
-                                if beta_mode == 1 and self.reference_loss > 0:
-                                    beta_rows[r0:r0 + R_s].copy_(beta)
+                            beta_all = torch.empty(R if beta_mode == 1 else 1, **f32)
+                            K.gptqplus_terms(Gs, hdiag_all, Hinv_all, alpha_eff, float(self.reference_loss),
+                                             beta_mode, beta_all, Z, GH, GH0, z_flags, HinvT)
+                            if beta_mode == 1 and self.reference_loss > 0:
+                                beta_rows.copy_(beta_all)
                             z_any = torch.amax(z_flags).reshape(1).contiguous()
                             z_zero = not bool(z_any.item())
                             K.current_weight(Wp, codes, i2, qmode, scale_tab, col_group, dyn_scale,

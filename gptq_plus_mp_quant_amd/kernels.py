@@ -223,21 +223,34 @@ def chol_hinv_attempt(H_work, damp_percent, workspace, Hinv, Hinv_init=None, inf
     return info
 
 
-def gptqplus_terms(G_sub, hinv_diag, Hinv, alpha_eff, reference_loss, beta_mode, beta, Z, GHinv,
-                   GH0, z_nonzero):
-    """beta, Z = (G_sub Hinv^T) beta and GHinv = Z Hinv for one subgroup; hinv_diag = diag(H^-1)
-    [C] (beta_mode 1 only)."""
-    R_s, C = G_sub.shape
-    G_sub = _cin(G_sub, "G_sub")
+def gptqplus_terms(G, hinv_diag, Hinv, alpha_eff, reference_loss, beta_mode, beta, Z, GHinv,
+                   GH0, z_nonzero, HinvT=None):
+    """beta, Z = (G Hinv^T) beta and GHinv = Z Hinv for nsub = Hinv.shape[0] subgroups of
+    R_s = G.shape[0] / nsub rows: Hinv [nsub, C, C], hinv_diag = diag(H^-1) [nsub, C]
+    (beta_mode 1), GH0 [R, C] and HinvT [nsub, C, C] workspaces (beta_mode 1), z_nonzero [nsub]."""
+    R, C = G.shape
+    Hinv = Hinv.reshape(-1, C, C)
+    nsub = Hinv.shape[0]
+    if R % nsub:
+        raise ValueError("gptqplus_terms: rows must split evenly over the subgroups")
+    R_s = R // nsub
+    G = _cin(G, "G")
     hinv_diag = _cin(hinv_diag, "hinv_diag")
-    if hinv_diag is not None and hinv_diag.numel() != C:
-        raise ValueError("gptqplus_terms: hinv_diag must hold C values")
     Hinv = _cin(Hinv, "Hinv")
-    for t, n in ((beta, "beta"), (Z, "Z"), (GHinv, "GHinv"), (GH0, "GH0")):
+    if hinv_diag is not None and hinv_diag.numel() != nsub * C:
+        raise ValueError("gptqplus_terms: hinv_diag must hold C values per subgroup")
+    if GH0 is not None and GH0.numel() != R * C:
+        raise ValueError("gptqplus_terms: GH0 must be [R, C]")
+    if HinvT is not None and HinvT.numel() != nsub * C * C:
+        raise ValueError("gptqplus_terms: HinvT must be [nsub, C, C]")
+    if z_nonzero.numel() != nsub:
+        raise ValueError("gptqplus_terms: one z_nonzero flag per subgroup")
+    for t, n in ((beta, "beta"), (Z, "Z"), (GHinv, "GHinv"), (GH0, "GH0"), (HinvT, "HinvT")):
         _cout(t, n)
-    nat.call("rq_gptqplus_terms", nat.ptr(G_sub), G_sub.stride(0), nat.ptr(hinv_diag), nat.ptr(Hinv),
-             R_s, C, float(alpha_eff), float(reference_loss), int(beta_mode), nat.ptr(beta), nat.ptr(Z),
-             nat.ptr(GHinv), Z.stride(0), nat.ptr(GH0), nat.ptr(z_nonzero), _stream(G_sub))
+    _cout(z_nonzero, "z_nonzero", torch.int32)
+    nat.call("rq_gptqplus_terms", nat.ptr(G), G.stride(0), nat.ptr(hinv_diag), nat.ptr(Hinv), nat.ptr(HinvT),
+             R_s, nsub, C, float(alpha_eff), float(reference_loss), int(beta_mode), nat.ptr(beta), nat.ptr(Z),
+             nat.ptr(GHinv), Z.stride(0), nat.ptr(GH0), nat.ptr(z_nonzero), _stream(G))
 
 
 def _surrogate(gmode, anchor, beta, R, C):

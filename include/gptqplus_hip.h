@@ -163,16 +163,20 @@ int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* damp_percen
                          float* Hinv, float* Hinv_init, float* Hinv_diag, int* info, void* stream);
 
 /* GPTQPlus._compute_gradient_terms -- gptq_plus_utils.py:563-578 with
- * compute_safe_beta_from_reference_loss -- :174-194.
+ * compute_safe_beta_from_reference_loss -- :174-194, for nsub subgroups at once: subgroup b
+ * owns rows [b*R_s, (b+1)*R_s) of G (row stride ldg), Z and GHinv (row stride ldz), beta
+ * (beta_mode 1) and GH0, the upper factor Hinv + b*C*C (Hinv^T Hinv = Hinv_init), hinv_diag +
+ * b*C = diag(Hinv_init) (from rq_chol_hinv_attempt) and z_nonzero[b].
  * beta_mode 0: beta = 0 (alpha <= 0 or gradient update off; beta has 1 element);
- * beta_mode 1: beta[r] from G_sub, hinv_diag = diag(H^-1) (C floats, from rq_chol_hinv_attempt)
- * and the reference's G_sub Hinv_init (:180), formed as (G_sub Hinv^T) Hinv in the GH0
- * workspace [R_s, C] (Hinv^T Hinv = Hinv_init: two triangular products, no full H^-1).
- * Z = (G_sub Hinv^T) * beta, GHinv = Z Hinv.  *z_nonzero (device int) is set to 1 when any Z
- * element is non-zero or NaN; 0 lets later kernels skip provably-zero first-order work. */
-int rq_gptqplus_terms(const float* G_sub, int64_t ldg, const float* hinv_diag, const float* Hinv,
-                      int R_s, int C, double alpha_eff, double reference_loss, int beta_mode,
-                      float* beta, float* Z, float* GHinv, int64_t ldz, float* GH0,
+ * beta_mode 1: beta[r] from G, hinv_diag and the reference's G Hinv_init (:180), formed as
+ * (G Hinv^T) Hinv in the GH0 workspace [nsub*R_s, C] (two triangular products, no H^-1).
+ * Z = (G Hinv^T) * beta, GHinv = Z Hinv.  HinvT (optional workspace, nsub*C*C floats, used by
+ * beta_mode 1): with it, and C a multiple of 16, the products run as batched 128-tile NT GEMMs.
+ * z_nonzero[b] (device ints) is set to 1 when any Z element of subgroup b is non-zero or NaN;
+ * 0 lets later kernels skip provably-zero first-order work. */
+int rq_gptqplus_terms(const float* G, int64_t ldg, const float* hinv_diag, const float* Hinv,
+                      float* HinvT, int R_s, int nsub, int C, double alpha_eff, double reference_loss,
+                      int beta_mode, float* beta, float* Z, float* GHinv, int64_t ldz, float* GH0,
                       int* z_nonzero, void* stream);
 
 /* One block of the fasterquant loop for ALL subgroups -- gptq_plus_utils.py:1169-1372:

@@ -333,8 +333,24 @@ def test_cholesky_retry_schedule(neg):
         assert torch.equal(Hinv.cpu(), torch.eye(80))
 
 
+def _check_terms(G, Hinv, beta, Z, GH, beta_o):
+    """beta against the oracle's to an absolute 2^-21: the reference's 1 - sqrt(1 - ratio) in
+    fp32 cancels (beta ~ 1e-4 keeps ~10 of its 24 bits), so a last-bit difference of ratio --
+    from c summed in another order -- moves beta by up to an ulp of 1.  Z and GHinv follow beta
+    linearly, so they are checked against the oracle's products formed with the kernel's beta
+    (fp32 on the CPU: 1e-5)."""
+    beta_c = beta.cpu()
+    assert float((beta_c - beta_o).abs().max()) <= 2.0 ** -21
+    Z_o = G.matmul(Hinv.T) * beta_c.unsqueeze(1)
+    assert rel_fro(Z, Z_o) <= 1e-5
+    assert rel_fro(GH, Z.cpu().matmul(Hinv)) <= 1e-5
+
+
 @pytest.mark.parametrize("alpha,ref_loss", [(0.0, 0.0), (0.05, 3e5), (0.05, 0.0)])
-def test_gptqplus_terms(alpha, ref_loss):
+@pytest.mark.parametrize("nt", [False, True], ids=["tile64", "nt128"])
+def test_gptqplus_terms(alpha, ref_loss, nt):
+    """One subgroup against the oracle; nt: with the Hinv^T workspace the beta_mode 1 products
+    run on the batched 128-tile NT kernel (C = 192 is a multiple of 16), else on 64-tiles."""
     C, R_s = 192, 48
     H = _spd(99, C)
     Hinit_o, Hinv_o, *_ = hessian_inverse_with_fallback(H, 0.01)
@@ -346,19 +362,61 @@ def test_gptqplus_terms(alpha, ref_loss):
     Z = torch.empty(R_s, C, device=DEV)
     GH = torch.empty(R_s, C, device=DEV)
     GH0 = torch.empty(R_s, C, device=DEV) if mode else None
+    HinvT = torch.empty(C, C, device=DEV) if (mode and nt) else None
     nz = torch.zeros(1, dtype=torch.int32, device=DEV)
     # beta_mode 1 takes diag(H^-1) and forms G Hinv_init as (G Hinv^T) Hinv (Hinv^T Hinv = Hinv_init
     # up to the oracle's fp32 factorisation, so the bars below also bound that rewrite)
     hdiag = torch.diagonal(Hinit_o).contiguous().to(DEV) if mode else None
-    K.gptqplus_terms(Gs.to(DEV), hdiag, Hinv_o.to(DEV), a_eff, ref_loss, mode, beta, Z, GH, GH0, nz)
+    K.gptqplus_terms(Gs.to(DEV), hdiag, Hinv_o.to(DEV), a_eff, ref_loss, mode, beta, Z, GH, GH0, nz, HinvT)
     torch.cuda.synchronize()
     if alpha > 0 and ref_loss > 0:
-        assert rel_fro(beta, beta_o) <= 1e-5 and beta_o.min() > 0.0
-        assert rel_fro(Z, Z_o) <= 1e-5 and rel_fro(GH, GH_o) <= 1e-5
-        assert int(nz.item()) == 1
+        assert beta_o.min() > 0.0 and int(nz.item()) == 1
+        _check_terms(Gs, Hinv_o, beta, Z, GH, beta_o)
     else:
         assert float(beta[0]) == 0.0 and int(nz.item()) == 0
         assert not Z.any() and not GH.any()
+
+
+def test_gptqplus_terms_batched_nt():
+    """Three subgroups in one call (ragged R_s = 200 against the 128-row tiles, C = 400 with a
+    ragged last column tile): each against the oracle's terms of its own (H^-1, G rows), and
+    the NT-kernel results against the 64-tile path on the same inputs."""
+    C, R_s, nsub = 400, 200, 3
+    Gs = torch.from_numpy(rng(6).standard_normal((nsub * R_s, C)).astype(np.float32))
+    ref, hinvs, diags = [], [], []
+    for b in range(nsub):
+        Hinit_o, Hinv_o, *_ = hessian_inverse_with_fallback(_spd(120 + b, C), 0.01)
+        ref.append(gradient_terms(Gs[b * R_s:(b + 1) * R_s], Hinit_o, Hinv_o, 0.05, 3e5, nsub * R_s, C))
+        hinvs.append(Hinv_o)
+        diags.append(torch.diagonal(Hinit_o))
+    Hinv = torch.stack(hinvs).to(DEV).contiguous()
+    hdiag = torch.stack(diags).to(DEV).contiguous()
+    a_eff = 0.05 / (nsub * R_s * C)
+    outs, errs = [], []
+    for HinvT in (torch.empty(nsub, C, C, device=DEV), None):
+        beta = torch.empty(nsub * R_s, device=DEV)
+        Z = torch.empty(nsub * R_s, C, device=DEV)
+        GH = torch.empty(nsub * R_s, C, device=DEV)
+        GH0 = torch.empty(nsub * R_s, C, device=DEV)
+        nz = torch.full((nsub,), 7, dtype=torch.int32, device=DEV)
+        K.gptqplus_terms(Gs.to(DEV), hdiag, Hinv, a_eff, 3e5, 1, beta, Z, GH, GH0, nz, HinvT)
+        torch.cuda.synchronize()
+        assert nz.tolist() == [1] * nsub
+        if HinvT is not None:
+            assert torch.equal(HinvT.cpu(), Hinv.cpu().transpose(1, 2))
+        for b in range(nsub):
+            rows = slice(b * R_s, (b + 1) * R_s)
+            beta_o, Z_o, GH_o, GH0_o = ref[b]
+            errs.append(dict(nt=HinvT is not None, sub=b, gh0=rel_fro(GH0[rows], GH0_o),
+                             beta_abs=float((beta[rows].cpu() - beta_o).abs().max()), beta_max=float(beta_o.max())))
+            _check_terms(Gs[rows], hinvs[b], beta[rows], Z[rows], GH[rows], beta_o)
+        outs.append((beta, Z, GH, GH0))
+    for e in errs:
+        print(e)
+        assert e["gh0"] <= 1e-5, e
+    # the two kernel paths: GH0 (before the cancellation) to 1e-5, beta to the same 2^-21
+    assert rel_fro(outs[0][3], outs[1][3]) <= 1e-5
+    assert float((outs[0][0] - outs[1][0]).abs().max()) <= 2.0 ** -21
 
 
 def test_gptqplus_terms_zero_beta_nonfinite():
