@@ -41,8 +41,8 @@ SIGNATURES = {
     "rq_hessian_timing_events": (_I, [_P, _P]),
     "rq_hessian_accum_multi": (_I, [_P, _I, _L, _L, _I, _I, _P, _P, _P, _P, _P, _L, _P]),
     "rq_hessian_finalize": (_I, [_P, _P, _I, _I, _D, _D, _D, _I, _P, _P]),
-    "rq_find_params": (_I, [_P, _I, _I, _I, _L, _I, _I, _I, _P, _P, _P]),
-    "rq_find_params_mse": (_I, [_P, _I, _I, _I, _L, _I, _I, _I, _D, _I, _D, _P, _P, _P]),
+    "rq_find_params": (_I, [_P, _I, _I, _I, _L, _I, _I, _I, _I, _P, _P, _P]),
+    "rq_find_params_mse": (_I, [_P, _I, _I, _I, _L, _I, _I, _I, _I, _D, _I, _D, _P, _P, _P]),
     "rq_act_order_perm": (_I, [_P, _I, _P, _P, _P]),
     "rq_prepare_subgroup": (_I, [_P, _I, _L, _P, _L, _P, _I, _I, _P, _P, _L, _P, _L, _P, _P]),
     "rq_chol_workspace_bytes": (_L, [_I]),

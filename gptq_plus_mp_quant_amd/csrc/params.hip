@@ -1,6 +1,7 @@
 // Quantizer parameters, per-subgroup gathers and the final write-back.
 //  - rq_find_params:      WeightQuantizer.find_params, per-channel min/max (utils/quant_utils.py:390-421),
-//                         also per static column group (gptq_utils/gptq_plus_utils.py:994-1002)
+//                         also per static column group (gptq_utils/gptq_plus_utils.py:994-1002) and
+//                         find_params_weight_groupwise (utils/quant_utils.py:333-388, clip_zero = 0)
 //  - rq_prepare_subgroup: row slice, dead columns, act_order gathers of W, G and H (:1033-1050)
 //  - rq_writeback:        un-permute, dequantize, cast to the layer dtype, export buffers (:1850-1896)
 // All of these are HBM-bound gathers / reductions.
@@ -22,7 +23,7 @@ __device__ __forceinline__ float wave_max(float v) {
 // One wavefront per (row, group).
 template <typename TW>
 __global__ __launch_bounds__(256) void k_find_params(const TW* __restrict__ w, int R, int C,
-                                                     int64_t ldw, int gs, float maxq, int sym,
+                                                     int64_t ldw, int gs, float maxq, int sym, int clip_zero,
                                                      float* __restrict__ scale,
                                                      float* __restrict__ zero) {
   const int lane = threadIdx.x & 63;
@@ -42,7 +43,7 @@ __global__ __launch_bounds__(256) void k_find_params(const TW* __restrict__ w, i
   mx = wave_max(mx);
   if (lane == 0) {
     float s, z;
-    rq_params_from_minmax(mn, mx, maxq, sym, &s, &z);
+    rq_params_from_minmax(mn, mx, maxq, sym, &s, &z, clip_zero);
     scale[(int64_t)grp * R + r] = s;
     zero[(int64_t)grp * R + r] = z;
   }
@@ -50,12 +51,13 @@ __global__ __launch_bounds__(256) void k_find_params(const TW* __restrict__ w, i
 
 // WeightQuantizer.find_params with mse=True (utils/quant_utils.py:408-448): min/max start,
 // then a maxshrink*grid x maxshrink*grid shrink grid over (xmin, xmax); each candidate's row
-// error sum |q - x|^norm is reduced in a fixed order and the first strict minimum wins.
+// error sum |q - x|^norm is reduced in a fixed order and the first strict minimum wins
+// (clip_zero = 0: the groupwise search of :354-386, from the group's own min / max).
 // One 256-thread workgroup per (row, group).
 template <typename TW>
 __global__ __launch_bounds__(256) void k_find_params_mse(const TW* __restrict__ w, int R, int C,
                                                          int64_t ldw, int gs, float maxq, int sym,
-                                                         float norm, int grid, int steps,
+                                                         int clip_zero, float norm, int grid, int steps,
                                                          float* __restrict__ scale,
                                                          float* __restrict__ zero) {
   __shared__ float red[256];
@@ -81,14 +83,14 @@ __global__ __launch_bounds__(256) void k_find_params_mse(const TW* __restrict__ 
     }
     __syncthreads();
   }
-  float xmin = rq_nan_min(red[0], 0.0f);
-  float xmax = rq_nan_max(red2[0], 0.0f);
+  float xmin = clip_zero ? rq_nan_min(red[0], 0.0f) : red[0];
+  float xmax = clip_zero ? rq_nan_max(red2[0], 0.0f) : red2[0];
   if (!sym && xmin == 0.0f && xmax == 0.0f) {
     xmin = -1.0f;
     xmax = 1.0f;
   }
   float bscale, bzero;
-  rq_params_from_minmax(red[0], red2[0], maxq, sym, &bscale, &bzero);
+  rq_params_from_minmax(red[0], red2[0], maxq, sym, &bscale, &bzero, clip_zero);
   float best = __builtin_inff();
   for (int i = 0; i < steps; ++i) {
     const float fi = (float)(1.0 - (double)i / (double)grid);
@@ -270,7 +272,7 @@ inline int rows_grid(int rows) { return rows < 1024 ? rows : 1024; }
 }  // namespace
 
 extern "C" int rq_find_params(const void* w, int w_dtype, int R, int C, int64_t ldw, int group_size,
-                              int maxq, int sym, float* scale, float* zero, void* stream) {
+                              int maxq, int sym, int clip_zero, float* scale, float* zero, void* stream) {
   if (!w || !scale || !zero || R <= 0 || C <= 0 || ldw < C || maxq <= 0) return RQ_EINVAL;
   const int gs = group_size > 0 ? group_size : C;
   const int ng = (C + gs - 1) / gs;
@@ -278,13 +280,13 @@ extern "C" int rq_find_params(const void* w, int w_dtype, int R, int C, int64_t 
   dim3 grid((R + 3) / 4, ng), block(256);
   if (w_dtype == RQ_F16)
     hipLaunchKernelGGL(k_find_params<__half>, grid, block, 0, s, (const __half*)w, R, C, ldw, gs,
-                       (float)maxq, sym, scale, zero);
+                       (float)maxq, sym, clip_zero, scale, zero);
   else if (w_dtype == RQ_BF16)
     hipLaunchKernelGGL(k_find_params<__hip_bfloat16>, grid, block, 0, s, (const __hip_bfloat16*)w, R,
-                       C, ldw, gs, (float)maxq, sym, scale, zero);
+                       C, ldw, gs, (float)maxq, sym, clip_zero, scale, zero);
   else if (w_dtype == RQ_F32)
     hipLaunchKernelGGL(k_find_params<float>, grid, block, 0, s, (const float*)w, R, C, ldw, gs,
-                       (float)maxq, sym, scale, zero);
+                       (float)maxq, sym, clip_zero, scale, zero);
   else
     return RQ_EINVAL;
   RQ_CHECK_LAUNCH();
@@ -292,7 +294,7 @@ extern "C" int rq_find_params(const void* w, int w_dtype, int R, int C, int64_t 
 }
 
 extern "C" int rq_find_params_mse(const void* w, int w_dtype, int R, int C, int64_t ldw,
-                                  int group_size, int maxq, int sym, double norm, int grid,
+                                  int group_size, int maxq, int sym, int clip_zero, double norm, int grid,
                                   double maxshrink, float* scale, float* zero, void* stream) {
   if (!w || !scale || !zero || R <= 0 || C <= 0 || ldw < C || maxq <= 0 || grid <= 0) return RQ_EINVAL;
   const int gs = group_size > 0 ? group_size : C;
@@ -303,13 +305,13 @@ extern "C" int rq_find_params_mse(const void* w, int w_dtype, int R, int C, int6
   dim3 g(R, ng), block(256);
   if (w_dtype == RQ_F16)
     hipLaunchKernelGGL(k_find_params_mse<__half>, g, block, 0, s, (const __half*)w, R, C, ldw, gs,
-                       (float)maxq, sym, (float)norm, grid, steps, scale, zero);
+                       (float)maxq, sym, clip_zero, (float)norm, grid, steps, scale, zero);
   else if (w_dtype == RQ_BF16)
     hipLaunchKernelGGL(k_find_params_mse<__hip_bfloat16>, g, block, 0, s, (const __hip_bfloat16*)w, R,
-                       C, ldw, gs, (float)maxq, sym, (float)norm, grid, steps, scale, zero);
+                       C, ldw, gs, (float)maxq, sym, clip_zero, (float)norm, grid, steps, scale, zero);
   else if (w_dtype == RQ_F32)
     hipLaunchKernelGGL(k_find_params_mse<float>, g, block, 0, s, (const float*)w, R, C, ldw, gs,
-                       (float)maxq, sym, (float)norm, grid, steps, scale, zero);
+                       (float)maxq, sym, clip_zero, (float)norm, grid, steps, scale, zero);
   else
     return RQ_EINVAL;
   RQ_CHECK_LAUNCH();

@@ -41,11 +41,12 @@ __device__ __forceinline__ float rq_quant_code(float x, float scale, float lo, f
 }
 
 // WeightQuantizer.find_params per-channel branch (utils/quant_utils.py:408-421) for one row,
-// given the row's NaN-propagating min and max.
+// given the row's NaN-propagating min and max; clip_zero = 0: find_params_weight_groupwise
+// (:333-352), whose range is the group's min / max as they are (not widened to include 0).
 __device__ __forceinline__ void rq_params_from_minmax(float rmin, float rmax, float maxq, int sym,
-                                                      float* scale_out, float* zero_out) {
-  float xmin = rq_nan_min(rmin, 0.0f);
-  float xmax = rq_nan_max(rmax, 0.0f);
+                                                      float* scale_out, float* zero_out, int clip_zero = 1) {
+  float xmin = clip_zero ? rq_nan_min(rmin, 0.0f) : rmin;
+  float xmax = clip_zero ? rq_nan_max(rmax, 0.0f) : rmax;
   if (sym) {
     float m = rq_nan_max(fabsf(xmin), xmax);
     *scale_out = rq_clamp_min(m, 1e-5f) / maxq;

@@ -71,6 +71,10 @@ class GPTQ:
         q = self.quantizer
         if q is None or q.bits >= 16:
             raise ValueError("fasterquant needs a configured WeightQuantizer with bits < 16")
+        if getattr(q, "weight_groupsize", -1) > 0:
+            # one scale per weight element: the reference's column loop broadcasts it against a
+            # column (gptq_utils.py:135-136) and fails
+            raise ValueError("fasterquant: a quantizer with weight_groupsize > 0 has no per-row scale")
         if blocksize > 128 or blocksize <= 0:
             raise NotImplementedError("blocksize must be in [1, 128] on the HIP path")
         dev, R, C = self.dev, self.rows, self.columns

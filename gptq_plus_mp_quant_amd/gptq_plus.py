@@ -230,6 +230,10 @@ class GPTQPlus:
         q = self.quantizer
         if q is None or q.bits >= 16:
             raise ValueError("fasterquant needs a configured WeightQuantizer with bits < 16")
+        if getattr(q, "weight_groupsize", -1) > 0:
+            # one scale per weight element: the reference's column loop fails on it
+            # (gptq_plus_utils.py:1301-1315 broadcasts it against a column)
+            raise ValueError("fasterquant: a quantizer with weight_groupsize > 0 has no per-row scale")
         if blocksize > MAX_BLOCKSIZE or blocksize <= 0:
             raise NotImplementedError(f"blocksize must be in [1, {MAX_BLOCKSIZE}] on the HIP path")
 

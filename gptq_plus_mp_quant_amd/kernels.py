@@ -151,8 +151,9 @@ def hessian_finalize(H, act_sq, h_div, sal_scale, seq_len, nonfinite=None, sanit
              float(seq_len), int(bool(sanitize)), nat.ptr(nonfinite), _stream(H))
 
 
-def find_params(w, maxq, sym, group_size=-1):
-    """Per-row (or per column group) min/max scale and zero: returns ([ng, R], [ng, R])."""
+def find_params(w, maxq, sym, group_size=-1, clip_zero=True):
+    """Per-row (or per column group) min/max scale and zero: returns ([ng, R], [ng, R]).
+    clip_zero: the range includes 0 (find_params); False: the groupwise fit."""
     _rowmajor(w, "w")
     R, C = w.shape
     gs = group_size if group_size > 0 else C
@@ -160,11 +161,11 @@ def find_params(w, maxq, sym, group_size=-1):
     scale = torch.empty((ng, R), device=w.device, dtype=_f32)
     zero = torch.empty((ng, R), device=w.device, dtype=_f32)
     nat.call("rq_find_params", nat.ptr(w), nat.dtype_code(w.dtype), R, C, w.stride(0), gs, int(maxq),
-             int(bool(sym)), nat.ptr(scale), nat.ptr(zero), _stream(w))
+             int(bool(sym)), int(bool(clip_zero)), nat.ptr(scale), nat.ptr(zero), _stream(w))
     return scale, zero
 
 
-def find_params_mse(w, maxq, sym, norm=2.4, grid=50, maxshrink=0.5, group_size=-1):
+def find_params_mse(w, maxq, sym, norm=2.4, grid=50, maxshrink=0.5, group_size=-1, clip_zero=True):
     """find_params with the mse clip search: returns ([ng, R], [ng, R])."""
     _rowmajor(w, "w")
     R, C = w.shape
@@ -173,8 +174,8 @@ def find_params_mse(w, maxq, sym, norm=2.4, grid=50, maxshrink=0.5, group_size=-
     scale = torch.empty((ng, R), device=w.device, dtype=_f32)
     zero = torch.empty((ng, R), device=w.device, dtype=_f32)
     nat.call("rq_find_params_mse", nat.ptr(w), nat.dtype_code(w.dtype), R, C, w.stride(0), gs, int(maxq),
-             int(bool(sym)), float(norm), int(grid), float(maxshrink), nat.ptr(scale), nat.ptr(zero),
-             _stream(w))
+             int(bool(sym)), int(bool(clip_zero)), float(norm), int(grid), float(maxshrink), nat.ptr(scale),
+             nat.ptr(zero), _stream(w))
     return scale, zero
 
 

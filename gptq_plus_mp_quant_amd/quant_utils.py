@@ -4,8 +4,9 @@ runs the gfx950 ``rq_find_params`` kernel.
 Same constructor, ``configure`` arguments, attributes (``maxq``, ``scale``, ``zero``, ``bits``,
 ``perchannel``, ``sym``, ...) and method semantics as the reference.  ``find_params`` needs the
 tensor on the GPU; ``mse=True`` runs the clip grid search kernel (``rq_find_params_mse``).
-``weight_groupsize > 0`` (the activation-style grouping of ``find_params_weight_groupwise``,
-off the GPTQ+ path) raises ``NotImplementedError`` instead of diverging.
+``weight_groupsize > 0`` (``find_params_weight_groupwise``: one scale per run of columns,
+stored per element) runs the same kernels on the runs' own ranges, for fp32 tensors (the
+reference fits 16-bit tensors in their own dtype; those raise ``NotImplementedError``).
 """
 from __future__ import annotations
 
@@ -47,13 +48,10 @@ class WeightQuantizer(torch.nn.Module):
         self.weight_groupsize = weight_groupsize
         self.maxq = torch.tensor(2 ** (bits - 1) - 1) if sym else torch.tensor(2 ** bits - 1)
 
-    def _check_supported(self):
-        if getattr(self, "weight_groupsize", -1) > 0:
-            raise NotImplementedError("weight_groupsize > 0 has no HIP kernel yet")
-
-    def params_on(self, w: torch.Tensor, group_size: int = -1):
-        """Return (scale [ngroups, R], zero [ngroups, R]) for a 2-D weight without touching self."""
-        self._check_supported()
+    def params_on(self, w: torch.Tensor, group_size: int = -1, clip_zero: bool = True):
+        """Return (scale [ngroups, R], zero [ngroups, R]) for a 2-D weight without touching self
+        (clip_zero: the range of each (row, group) includes 0, as in find_params; False: the
+        group's own min / max, as in find_params_weight_groupwise)."""
         nat.require_gpu(w, "weight")
         if w.dim() != 2:
             raise ValueError("expected a 2-D weight")
@@ -66,11 +64,11 @@ class WeightQuantizer(torch.nn.Module):
         zero = torch.empty((ng, R), device=w.device, dtype=torch.float32)
         if self.mse:
             nat.call("rq_find_params_mse", nat.ptr(w), nat.dtype_code(w.dtype), R, C, w.stride(0), gs,
-                     int(self.maxq), int(bool(self.sym)), float(self.norm), int(self.grid),
+                     int(self.maxq), int(bool(self.sym)), int(bool(clip_zero)), float(self.norm), int(self.grid),
                      float(self.maxshrink), nat.ptr(scale), nat.ptr(zero), nat.stream_of(w.device))
         else:
             nat.call("rq_find_params", nat.ptr(w), nat.dtype_code(w.dtype), R, C, w.stride(0), gs,
-                     int(self.maxq), int(bool(self.sym)), nat.ptr(scale), nat.ptr(zero),
+                     int(self.maxq), int(bool(self.sym)), int(bool(clip_zero)), nat.ptr(scale), nat.ptr(zero),
                      nat.stream_of(w.device))
         return scale, zero
 
@@ -108,13 +106,35 @@ class WeightQuantizer(torch.nn.Module):
             zero[r0:r1].copy_(zg[0].expand(r1 - r0))
         return scale, zero
 
+    # utils/quant_utils.py:333-388
+    def find_params_weight_groupwise(self, x) -> None:
+        """One (scale, zero) per run of weight_groupsize columns of each row (x viewed as
+        [x.shape[-2], -1, weight_groupsize]), from the run's own min / max (mse: the shrink-grid
+        search per run), repeated over the run in x's shape."""
+        nat.require_gpu(x, "x")
+        wg = self.weight_groupsize
+        rows, cols = x.shape[-2], x.shape[-1]
+        if cols % wg or x.numel() != rows * cols:
+            raise RuntimeError(f"shape '[{rows}, {cols // wg}, {wg}]' is invalid for input of size {x.numel()}")
+        if x.dtype != torch.float32:
+            raise NotImplementedError("weight_groupsize > 0 for a 16-bit tensor: the reference fits it in "
+                                      "that dtype; pass a float32 tensor")
+        w = x.reshape(rows, cols)
+        if w.stride(1) != 1:
+            w = w.contiguous()
+        scale, zero = self.params_on(w, wg, clip_zero=False)          # [cols / wg, rows]
+        self.scale = scale.t().repeat_interleave(wg, dim=1).reshape(x.shape)
+        self.zero = zero.t().repeat_interleave(wg, dim=1).reshape(x.shape)
+
     # utils/quant_utils.py:390-457
     def find_params(self, x) -> None:
         if self.bits == 16:
             return
-        self._check_supported()
         nat.require_gpu(x, "x")
         self.maxq = self.maxq.to(x.device)
+        if getattr(self, "weight_groupsize", -1) > 0:
+            self.find_params_weight_groupwise(x)
+            return
         shape = x.shape
         x2 = x.flatten(1) if self.perchannel else x.flatten().unsqueeze(0)
         scale, zero = self.params_on(x2)

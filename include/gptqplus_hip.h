@@ -116,17 +116,19 @@ int rq_hessian_finalize(float* H, float* act_sq, int G, int C, double h_div, dou
 /* WeightQuantizer.find_params, per-channel min/max -- utils/quant_utils.py:390-421
  * (static column groups: gptq_plus_utils.py:994-1002).  For each group k of `group_size`
  * columns (group_size <= 0: one group of all C columns) and row r:
- * scale[k*R + r], zero[k*R + r]. */
+ * scale[k*R + r], zero[k*R + r].  clip_zero != 0: the range is widened to include 0
+ * (find_params); clip_zero = 0: the group's own min / max (find_params_weight_groupwise,
+ * :333-352). */
 int rq_find_params(const void* w, int w_dtype, int R, int C, int64_t ldw, int group_size,
-                   int maxq, int sym, float* scale, float* zero, void* stream);
+                   int maxq, int sym, int clip_zero, float* scale, float* zero, void* stream);
 
 /* WeightQuantizer.find_params with mse=True (the --w_clip grid search) -- utils/quant_utils.py:
- * 408-448: per (row, group) min/max start, then int(maxshrink*grid)^2 shrunken (xmin, xmax)
- * candidates scored by sum |q - x|^norm; the first strict minimum is kept.  Same layouts as
- * rq_find_params. */
+ * 408-448 (groupwise: :354-386): per (row, group) min/max start, then int(maxshrink*grid)^2
+ * shrunken (xmin, xmax) candidates scored by sum |q - x|^norm; the first strict minimum is
+ * kept.  Same layouts and clip_zero as rq_find_params. */
 int rq_find_params_mse(const void* w, int w_dtype, int R, int C, int64_t ldw, int group_size,
-                       int maxq, int sym, double norm, int grid, double maxshrink, float* scale,
-                       float* zero, void* stream);
+                       int maxq, int sym, int clip_zero, double norm, int grid, double maxshrink,
+                       float* scale, float* zero, void* stream);
 
 /* act_order permutation -- gptq_plus_utils.py:1046, 1050 (classic GPTQ: argsort of diag(H)):
  * perm = torch.argsort(act_sq, descending=True) exactly as torch returns it on the CPU, ties

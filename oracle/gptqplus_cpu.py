@@ -74,7 +74,8 @@ class WeightQuantizerOracle:
         if self.bits == 16:
             return
         if self.weight_groupsize > 0:
-            raise NotImplementedError("weight_groupsize>0 activation-style grouping is off the hot path")
+            self.find_params_weight_groupwise(x)
+            return
         self.maxq = self.maxq.to(x.device)
         shape = x.shape
         x = x.flatten(1) if self.perchannel else x.flatten().unsqueeze(0)
@@ -126,6 +127,57 @@ class WeightQuantizerOracle:
                     best[better] = err[better]
                     self.scale[better] = scale1[better]
                     self.zero[better] = zero1[better]
+
+    def find_params_weight_groupwise(self, x: torch.Tensor) -> None:
+        # quant_utils.py:333-388: per (row, run of weight_groupsize columns) min / max taken as
+        # they are (no widening to 0), in x's own dtype, optional shrink-grid search per run;
+        # scale / zero repeated over each run, in x's shape
+        wg = self.weight_groupsize
+        init_shape = x.shape
+        x = x.reshape(x.shape[-2], x.shape[-1] // wg, wg)
+        xmax = torch.amax(x, dim=-1, keepdim=True)
+        xmin = torch.amin(x, dim=-1, keepdim=True)
+        if self.sym:
+            self.scale = torch.maximum(torch.abs(xmin), xmax).clamp(min=1e-5) / self.maxq
+            self.zero = torch.zeros_like(self.scale)
+        else:
+            both_zero = (xmin == 0) & (xmax == 0)
+            xmin[both_zero] = -1
+            xmax[both_zero] = +1
+            self.scale = (xmax - xmin).clamp(min=1e-5) / self.maxq
+            self.zero = torch.round(-xmin / self.scale)
+        self.scale = self.scale.repeat(1, 1, wg)
+        self.zero = self.zero.repeat(1, 1, wg)
+        if self.mse:
+            best = torch.full([x.shape[0], x.shape[1]], float("inf"), device=x.device).type_as(x)
+            steps = int(self.maxshrink * self.grid)
+            for i in range(steps):
+                for j in range(steps):
+                    xmin1 = (1 - i / self.grid) * xmin
+                    xmax1 = (1 - j / self.grid) * xmax
+                    if self.sym:
+                        scale1 = torch.maximum(torch.abs(xmin1), xmax1).clamp(min=1e-5) / self.maxq
+                        zero1 = torch.zeros_like(scale1)
+                        scale1 = scale1.repeat(1, 1, wg)
+                        zero1 = zero1.repeat(1, 1, wg)
+                        q = scale1 * torch.clamp(torch.round(x / scale1), -(self.maxq + 1), self.maxq)
+                    else:
+                        scale1 = (xmax1 - xmin1) / self.maxq
+                        zero1 = torch.round(-xmin1 / scale1)
+                        scale1 = scale1.repeat(1, 1, wg)
+                        zero1 = zero1.repeat(1, 1, wg)
+                        q = scale1 * (torch.clamp(torch.round(x / scale1) + zero1, 0, self.maxq) - zero1)
+                    q -= x
+                    q.abs_()
+                    q.pow_(self.norm)
+                    err = torch.sum(q, -1)
+                    better = err < best
+                    if torch.any(better):
+                        best[better] = err[better]
+                        self.scale[better] = scale1[better]
+                        self.zero[better] = zero1[better]
+        self.scale = self.scale.reshape(init_shape)
+        self.zero = self.zero.reshape(init_shape)
 
     def fake_quantize(self, x, st_idx=None, end_idx=None):
         # quant_utils.py:471-480
@@ -741,9 +793,9 @@ class GPTQPlusOracle:
 # ---------------------------------------------------------------------------------------
 # Convenience drivers used by tests and the CPU baseline
 # ---------------------------------------------------------------------------------------
-def make_quantizer(bits, sym=True, mse=False, perchannel=True) -> WeightQuantizerOracle:
+def make_quantizer(bits, sym=True, mse=False, perchannel=True, weight_groupsize=-1) -> WeightQuantizerOracle:
     q = WeightQuantizerOracle()
-    q.configure(bits, perchannel=perchannel, sym=sym, mse=mse)
+    q.configure(bits, perchannel=perchannel, sym=sym, mse=mse, weight_groupsize=weight_groupsize)
     return q
 
 

@@ -357,3 +357,14 @@ def test_dropin_bf16_vs_oracle(gs, act):
     assert code_flips(layer.int_weight, res.W_int) == 0
     assert torch.equal(layer.scale.cpu(), res.Scale)
     assert torch.equal(layer.weight.data.cpu(), res.Q)
+
+
+def test_weight_groupsize_quantizer_rejected():
+    """A quantizer with weight_groupsize > 0 has one scale per weight element, which the column
+    loop cannot use (the reference's broadcast fails there too): fasterquant raises."""
+    X, W, s, grad = synth(3, 64, 128, 1, 2, 64)
+    g, layer = _gpu_obj(W, s, grad, 1, 0.0, 0.0, 4, True)
+    g.quantizer.configure(4, perchannel=True, sym=True, weight_groupsize=32)
+    _accumulate(g, X, 2)
+    with pytest.raises(ValueError, match="weight_groupsize"):
+        g.fasterquant(blocksize=128, percdamp=0.01, groupsize=-1, actorder=False)

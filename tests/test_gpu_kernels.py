@@ -142,6 +142,35 @@ def test_finalize_keeps_nonfinite_unsanitised():
     assert int((~torch.isfinite(H)).sum()) == 3 and H[0, 6, 6] == 0.5
 
 
+@pytest.mark.parametrize("sym", [True, False])
+@pytest.mark.parametrize("mse", [False, True])
+def test_find_params_weight_groupwise_matches_oracle(sym, mse):
+    """weight_groupsize > 0 on an fp32 weight: the per-run fit expanded per element equals the
+    oracle's find_params_weight_groupwise bit for bit (one-sign, all-zero and NaN runs
+    included); 16-bit tensors and ragged run lengths raise."""
+    from gptq_plus_mp_quant_amd import WeightQuantizer
+    r = rng(21 + sym + 2 * mse)
+    W = torch.from_numpy(r.standard_normal((40, 96)).astype(np.float32) * 0.03)
+    W[2, :16] = W[2, :16].abs() + 0.01
+    W[3, 16:32] = -W[3, 16:32].abs() - 0.01
+    W[5, 32:48] = 0
+    W[7, 50] = float("nan")
+    q = WeightQuantizer()
+    q.configure(4, perchannel=True, sym=sym, mse=mse, weight_groupsize=16)
+    q.find_params(W.to(DEV))
+    o = make_quantizer(4, sym, mse, weight_groupsize=16)
+    o.find_params(W.clone())
+    assert q.scale.shape == W.shape and q.zero.shape == W.shape
+    torch.testing.assert_close(q.scale.cpu(), o.scale, rtol=0, atol=0, equal_nan=True)
+    torch.testing.assert_close(q.zero.cpu(), o.zero, rtol=0, atol=0, equal_nan=True)
+    with pytest.raises(NotImplementedError):
+        q.find_params(W.to(DEV).half())
+    q2 = WeightQuantizer()
+    q2.configure(4, perchannel=True, sym=sym, weight_groupsize=7)
+    with pytest.raises(RuntimeError):
+        q2.find_params(W.to(DEV))
+
+
 @pytest.mark.parametrize("bits,sym", [(4, True), (4, False), (3, True), (2, False), (8, True), (8, False)])
 @pytest.mark.parametrize("gs", [-1, 32])
 def test_find_params_bitexact(bits, sym, gs):

@@ -37,7 +37,7 @@ def test_argument_validation_needs_no_device():
     null = ctypes.c_void_p(0)
     assert lib.rq_hessian_accum(null, 0, 10, 8, 8, null, 1, 1, null, null, null, 0, null) == nat.RQ_EINVAL
     assert lib.rq_hessian_workspace_bytes(10, 0, 1) < 0
-    assert lib.rq_find_params(null, 0, 4, 4, 4, -1, 7, 1, null, null, null) == nat.RQ_EINVAL
+    assert lib.rq_find_params(null, 0, 4, 4, 4, -1, 7, 1, 1, null, null, null) == nat.RQ_EINVAL
     assert lib.rq_act_order_perm(null, 4, null, null, null) == nat.RQ_EINVAL
     damp = (ctypes.c_double * 1)(0.01)
     assert lib.rq_chol_hinv_attempt(null, 4, 1, damp, null, null, null, null, null, null) == nat.RQ_EINVAL
@@ -91,7 +91,7 @@ def test_dropin_rejects_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU"):
         q.find_params(torch.ones(4, 8))
     q.configure(4, perchannel=True, sym=True, weight_groupsize=4)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="GPU"):
         q.find_params(torch.ones(4, 8))
 
 

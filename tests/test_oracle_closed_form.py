@@ -92,6 +92,37 @@ def test_find_params_per_tensor_known_answer(sym, scale, zero):
     assert torch.equal(q.zero.flatten(), torch.full((3,), zero))
 
 
+@pytest.mark.parametrize("sym,row,scale,zero", [
+    # asym: each run's own range, not widened to 0 (that would give 2/15, 0 and 5/15, 0)
+    (False, [1.0, 2.0, 3.0, 5.0], [1 / 15, 1 / 15, 2 / 15, 2 / 15], [-15.0, -15.0, -22.0, -22.0]),
+    # sym: max(|min|, max) of the run, also for an all-negative run
+    (True, [-1.0, -4.0, 0.5, 0.25], [4 / 7, 4 / 7, 0.5 / 7, 0.5 / 7], [0.0] * 4),
+])
+def test_find_params_weight_groupwise_known_answers(sym, row, scale, zero):
+    q = make_quantizer(4, sym, weight_groupsize=2)
+    q.find_params(torch.tensor([row, row], dtype=torch.float32))
+    assert q.scale.shape == (2, 4) and q.zero.shape == (2, 4)
+    assert torch.allclose(q.scale, torch.tensor([scale, scale]), rtol=1e-6, atol=0)
+    assert torch.equal(q.zero, torch.tensor([zero, zero]))
+
+
+@pytest.mark.parametrize("sym", [True, False])
+def test_find_params_weight_groupwise_mse_reduces_to_per_row(sym):
+    """Runs that hold both signs have the same range with or without the widening to 0, so the
+    groupwise clip search of a run equals the per-channel search (golden-pinned) on the run
+    taken as a row of its own."""
+    r = _rng(11)
+    x = torch.from_numpy(r.standard_normal((6, 32)).astype(np.float32))
+    x[:, 0::8] = -x[:, 0::8].abs() - 0.1
+    x[:, 1::8] = x[:, 1::8].abs() + 0.1
+    qg = make_quantizer(4, sym, mse=True, weight_groupsize=8)
+    qg.find_params(x)
+    qr = make_quantizer(4, sym, mse=True)
+    qr.find_params(x.reshape(-1, 8))
+    assert torch.equal(qg.scale.reshape(-1, 8), qr.scale.reshape(-1, 1).expand(-1, 8))
+    assert torch.equal(qg.zero.reshape(-1, 8), qr.zero.reshape(-1, 1).expand(-1, 8))
+
+
 @pytest.mark.parametrize("bits,sym", [(4, True), (4, False), (3, True), (2, False)])
 def test_fake_quantize_is_nearest_grid_point(bits, sym):
     """Brute force over every code: fake_quantize picks the nearest point of
