@@ -61,7 +61,7 @@ SIGNATURES = {
     "rq_kfac_curvature": (_I, [_P, _I, _I, _D, _P, _P]),
     "rq_hessian_reg_gemm": (_I, [_P, _L, _P, _I, _I, _I, _I, _P, _L, _P]),
     "rq_block_gd_step": (_I, [_P, _L, _I, _I, _I, _I, _P, _L, _P, _I, _I, _D, _D, _P, _P, _P, _I, _D,
-                              _P, _L, _P, _L, _I, _P, _P, _P, _I, _I, _D, _D, _D, _P]),
+                              _P, _L, _P, _L, _I, _P, _P, _P, _I, _I, _D, _D, _D, _P, _P]),
 }
 
 _lib = None

@@ -112,6 +112,9 @@ struct GdArgs {
   float maxq;
   int sym;
   float floor_, one_m_floor, neg_sharp, amp, two_pi;
+  // optional statistics planes [4][R][C - i2]: the optimizer step (after clipping), the applied
+  // update, the regularizer part (l2 / hessian term or gated - step) and the sine part
+  float* parts;
 };
 
 __global__ __launch_bounds__(256) void k_block_gd_step(GdArgs a) {
@@ -143,11 +146,15 @@ __global__ __launch_bounds__(256) void k_block_gd_step(GdArgs a) {
       }
       upd = a.step_size * (m / denom);
     }
+    const float raw = upd;
+    float reg_part = 0.0f, sine_part = 0.0f;
     const float w = a.Wp[ow];
     if (a.reg == 1) {
-      upd = upd + a.lr_lam * (w - a.w_fp[(int64_t)r * a.ld_fp + j]);
+      reg_part = a.lr_lam * (w - a.w_fp[(int64_t)r * a.ld_fp + j]);
+      upd = upd + reg_part;
     } else if (a.reg == 2) {
-      upd = upd + a.lr_lam * a.hreg[(int64_t)r * a.ld_hreg + jj];
+      reg_part = a.lr_lam * a.hreg[(int64_t)r * a.ld_hreg + jj];
+      upd = upd + reg_part;
     } else if (a.reg >= 3) {
       float s, z;
       if (a.gqmode == RQ_QMODE_CHANNEL) {
@@ -169,16 +176,25 @@ __global__ __launch_bounds__(256) void k_block_gd_step(GdArgs a) {
       const float dist = fabsf(w - qn) / sc;
       const float gate = a.floor_ + a.one_m_floor * (1.0f - expf(a.neg_sharp * dist));
       const float gated = upd * gate;
+      reg_part = gated - upd;
       if (a.reg == 4) {
         const float ws = w / sc;
         const float phase = a.sym ? a.two_pi * ws : a.two_pi * (ws + z);
         const float sine = (a.amp * (a.two_pi / sc)) * sinf(phase);
-        upd = gated + a.lr * sine;
+        sine_part = a.lr * sine;
+        upd = gated + sine_part;
       } else {
         upd = gated;
       }
     }
     a.Wp[ow] = w - upd;
+    if (a.parts) {
+      const int64_t n = (int64_t)a.R * (a.C - a.i2), e = (int64_t)r * (a.C - a.i2) + jj;
+      a.parts[e] = raw;
+      a.parts[n + e] = upd;
+      a.parts[2 * n + e] = reg_part;
+      a.parts[3 * n + e] = sine_part;
+    }
   }
 }
 
@@ -247,7 +263,8 @@ extern "C" int rq_block_gd_step(float* Wp, int64_t ldw, int R, int R_s, int C, i
                                 const float* hreg, int64_t ld_hreg, int gate_qmode,
                                 const float* gate_scale, const float* gate_zero,
                                 const int32_t* col_group, int maxq, int sym, double gate_floor,
-                                double gate_sharpness, double sine_amp, void* stream) {
+                                double gate_sharpness, double sine_amp, float* stats_parts,
+                                void* stream) {
   if (!Wp || !grad || R <= 0 || R_s <= 0 || R % R_s || C <= 0 || ldw < C || ldg < C) return RQ_EINVAL;
   if (i2 < 0 || i2 > C || optimizer < 0 || optimizer > 2 || reg_strategy < 0 || reg_strategy > 4)
     return RQ_EINVAL;
@@ -279,6 +296,7 @@ extern "C" int rq_block_gd_step(float* Wp, int64_t ldw, int R, int R_s, int C, i
   a.maxq = (float)maxq; a.sym = sym;
   a.floor_ = (float)gate_floor; a.one_m_floor = (float)(1.0 - gate_floor);
   a.neg_sharp = (float)(-gate_sharpness); a.amp = (float)sine_amp; a.two_pi = (float)(2.0 * M_PI);
+  a.parts = stats_parts;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   dim3 grid((C - i2 + 255) / 256, rows_grid(R)), block(256);
   hipLaunchKernelGGL(k_block_gd_step, grid, block, 0, s, a);

@@ -13,9 +13,10 @@ Every ``g_update_mode`` of the reference runs on the HIP path: ``"frozen"`` (def
 ``"surrogate_block"``, ``"surrogate_online"``, and the refresh modes ``"block_gd"`` /
 ``"block_backward"``, whose layer backward is the caller's ``gradient_refresh_fn`` (called
 with the current weight, on the GPU, like the reference does); the optimizer step,
-regularizers and GPTQ+ term refresh around it are kernels.  ``diagnostic_recorder`` dumps and
-``refresh_full_metrics`` statistics raise ``NotImplementedError`` rather than silently
-differing.
+regularizers and GPTQ+ term refresh around it are kernels; ``refresh_full_metrics`` fills the
+``block_observer`` statistics (means, row norms, max and 0.99 quantile of the refreshed
+gradient and of the update terms) with torch reductions on the GPU.  ``diagnostic_recorder``
+dumps raise ``NotImplementedError`` rather than silently differing.
 """
 from __future__ import annotations
 
@@ -92,6 +93,42 @@ def hessian_inverse_chain(dev, H_work, Hinv_out, Hinv_init_out, workspace, percd
                              f"current is {damp[b]}")
     return out
 
+
+
+def _quantile_large(t, q):
+    """gptq_plus_utils.py:46-60: torch.quantile, or the k-th value where quantile refuses the size."""
+    flat = t.reshape(-1)
+    n = flat.numel()
+    if n == 0:
+        return None
+    k = max(1, min(n, int(n * q + 0.5)))
+    try:
+        return torch.quantile(flat, q).item()
+    except RuntimeError:
+        return flat.kthvalue(k).values.item()
+
+
+def _update_stats(t, name, outliers=False):
+    """abs mean and mean row L2 norm of an update term (:1657-1668, :1759-1783); with outliers also
+    its abs max and 0.99 quantile.  Keys as in the observer record (``<name>_abs_mean`` ...)."""
+    t = t.float()
+    a = t.abs()
+    out = {f"{name}_abs_mean": a.mean().item(), f"{name}_mean_row_l2": torch.linalg.norm(t, dim=1).mean().item()}
+    if outliers:
+        out[f"{name}_abs_max"] = a.max().item()
+        out[f"{name}_abs_q99"] = _quantile_large(a, 0.99)
+    return out
+
+
+def _grad_stats(g, grad_clip):
+    """The refreshed gradient's trailing columns (:1448-1462, :1669-1681): abs mean, mean row L2
+    norm, and abs mean after clamping to +-grad_clip (the abs mean when there is no clip)."""
+    g = g.float()
+    a = g.abs().mean().item()
+    clipped = g.clamp(min=-grad_clip, max=grad_clip).abs().mean().item() \
+        if grad_clip is not None and grad_clip > 0 else a
+    return {"remaining_grad_abs_mean": a, "remaining_grad_mean_row_l2": torch.linalg.norm(g, dim=1).mean().item(),
+            "remaining_grad_clipped_abs_mean": clipped}
 
 
 class GPTQPlus:
@@ -219,8 +256,6 @@ class GPTQPlus:
         gm_in, gm_out = nat.GMODES[g_update_mode]
         block_gd = g_update_mode == "block_gd"
         block_bw = g_update_mode == "block_backward"
-        if (block_gd or block_bw) and refresh_full_metrics:
-            raise NotImplementedError("refresh_full_metrics statistics are not produced by the HIP path")
         if block_gd and grad_optimizer not in K.OPTIMIZERS:
             raise ValueError(f"Unsupported `grad_optimizer={grad_optimizer}`. Expected one of: sgd, adam, h_adam.")
         if diagnostic_recorder is not None:
@@ -436,8 +471,12 @@ class GPTQPlus:
                             z_zero = not bool(z_any.item())
                             K.current_weight(Wp, codes, i2, qmode, scale_tab, col_group, dyn_scale,
                                              blocksize, out=anchor)
+                        stats = {}
+                        if refresh_full_metrics and i2 < C:
+                            stats = _grad_stats(Gs[:, i2:], grad_clip)
                         if block_observer is not None:
-                            block_observer(self._observer_record(i1, i2, blocksize, meta, block_gd=False))
+                            block_observer(self._observer_record(i1, i2, blocksize, meta, block_gd=False,
+                                                                 stats=stats))
                     if i2 < C:
                         K.trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_any, gm_out,
                                           anchor, beta_rows, sos, z_zero=z_zero)
@@ -461,13 +500,33 @@ class GPTQPlus:
                                 del diff
                             if grad_optimizer != "sgd":
                                 opt_step += 1
+                            stats, parts = {}, None
+                            if refresh_full_metrics:
+                                # the applied second-order step (:1546-1553) and the refreshed
+                                # gradient's trailing columns, permuted (:1626-1681)
+                                second = torch.cat([sos * err[r0:r0 + R_s, :count].matmul(
+                                    Hinv_all[s_][i1:i2, i2:]) for s_, r0 in enumerate(range(0, R, R_s))])
+                                stats.update(_update_stats(second, "second_order_update", outliers=True))
+                                gperm = grad if perm is None else grad.index_select(1, perm)
+                                stats.update(_grad_stats(gperm[:, i2:], grad_clip))
+                                del second, gperm
+                                parts = torch.empty((4, R, C - i2), **f32)
                             K.block_gd_step(Wp, R_s, i2, grad, perm, grad_optimizer, opt_step, grad_lr,
                                             grad_clip, exp_avg, exp_avg_sq, curvature, reg,
                                             grad_reg_lambda, W_fp, hreg, gate_q or 0, gate_s, gate_z,
                                             col_group, maxq, sym, grad_gate_floor, grad_gate_sharpness,
-                                            grad_gate_sine_amp)
+                                            grad_gate_sine_amp, stats_parts=parts)
+                            if parts is not None:
+                                # :1759-1783: the optimizer step, the applied update, the
+                                # regularizer and sine parts
+                                stats.update(_update_stats(parts[0], "first_order_raw"))
+                                stats.update(_update_stats(parts[1], "first_order_update", outliers=True))
+                                stats.update(_update_stats(parts[2], "regularizer_update"))
+                                stats.update(_update_stats(parts[3], "sine_regularizer_update"))
+                                del parts
                         if block_observer is not None:
-                            block_observer(self._observer_record(i1, i2, blocksize, meta, block_gd=True))
+                            block_observer(self._observer_record(i1, i2, blocksize, meta, block_gd=True,
+                                                                 stats=stats))
 
             with _section(rec, "fasterquant.write_layer_weight"):
                 Q = torch.empty((R, C), dtype=W.dtype, device=dev)
@@ -508,9 +567,10 @@ class GPTQPlus:
             return None
         return self._codes_perm if self.invperm is None else self._codes_perm[:, self.invperm]
 
-    def _observer_record(self, i1, i2, blocksize, meta, block_gd):
+    def _observer_record(self, i1, i2, blocksize, meta, block_gd, stats=None):
         """The per-block dict the reference hands to ``block_observer`` (:1462-1496,
-        :1784-1817) without the refresh_full_metrics statistics (all None)."""
+        :1784-1817); the refresh_full_metrics statistics come from ``stats`` (None when absent,
+        as in the reference with the flag off)."""
         rec = {"block_idx": i1 // blocksize, "col_start": i1, "col_end": i2,
                "remaining_columns": self.columns - i2}
         for k in ("remaining_grad_abs_mean", "remaining_grad_clipped_abs_mean", "remaining_grad_mean_row_l2",
@@ -521,7 +581,7 @@ class GPTQPlus:
                   "first_order_update_abs_q99", "regularizer_update_abs_mean",
                   "regularizer_update_mean_row_l2", "sine_regularizer_update_abs_mean",
                   "sine_regularizer_update_mean_row_l2"):
-            rec[k] = None
+            rec[k] = (stats or {}).get(k)
         keys = ["mean_refresh_loss", "train_mean_refresh_loss", "val_mean_refresh_loss",
                 "refresh_subset_mean_refresh_loss"]
         if block_gd:

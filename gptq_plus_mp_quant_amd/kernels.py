@@ -428,7 +428,10 @@ def hessian_reg_gemm(diff, H_reg, R_s, i2):
 def block_gd_step(Wp, R_s, i2, grad, perm, optimizer, step, lr, grad_clip, exp_avg=None,
                   exp_avg_sq=None, curvature=None, reg="none", reg_lambda=0.0, w_fp=None, hreg=None,
                   gate_qmode=0, gate_scale=None, gate_zero=None, col_group=None, maxq=0, sym=True,
-                  gate_floor=0.1, gate_sharpness=1.0, sine_amp=0.0):
+                  gate_floor=0.1, gate_sharpness=1.0, sine_amp=0.0, stats_parts=None):
+    """One block_gd step on the trailing columns [i2, C); stats_parts (optional, contiguous
+    float32 [4, R, C - i2]) receives the optimizer step, the applied update, the regularizer
+    part and the sine part."""
     R, C = Wp.shape
     _cout(Wp, "Wp")
     grad = _cin(grad, "grad")
@@ -443,6 +446,9 @@ def block_gd_step(Wp, R_s, i2, grad, perm, optimizer, step, lr, grad_clip, exp_a
         raise ValueError("block_gd_step: curvature must be contiguous [G, C]")
     if hreg is not None and (hreg.shape != (R, C - i2) or hreg.stride(1) != 1):
         raise ValueError("block_gd_step: hreg must be row-major [R, C - i2]")
+    if stats_parts is not None and stats_parts.shape != (4, R, C - i2):
+        raise ValueError("block_gd_step: stats_parts must be [4, R, C - i2]")
+    _cout(stats_parts, "stats_parts")
     nat.call("rq_block_gd_step", nat.ptr(Wp), Wp.stride(0), R, R_s, C, int(i2), nat.ptr(grad),
              grad.stride(0), nat.ptr(perm), OPTIMIZERS[optimizer], int(step), float(lr),
              float(grad_clip if grad_clip is not None else 0.0), nat.ptr(exp_avg), nat.ptr(exp_avg_sq),
@@ -450,4 +456,4 @@ def block_gd_step(Wp, R_s, i2, grad, perm, optimizer, step, lr, grad_clip, exp_a
              w_fp.stride(0) if w_fp is not None else 0, nat.ptr(hreg),
              hreg.stride(0) if hreg is not None else 0, int(gate_qmode), nat.ptr(gate_scale),
              nat.ptr(gate_zero), nat.ptr(col_group), int(maxq), int(bool(sym)), float(gate_floor),
-             float(gate_sharpness), float(sine_amp), _stream(Wp))
+             float(gate_sharpness), float(sine_amp), nat.ptr(stats_parts), _stream(Wp))

@@ -294,14 +294,19 @@ int rq_hessian_reg_gemm(const float* diff, int64_t ldd, const float* H_reg, int 
  * 0.999, eps 1e-8.  reg_strategy 0 none, 1 l2 (w_fp [R, C]), 2 hessian (hreg from
  * rq_hessian_reg_gemm), 3 quant_error_gate, 4 quant_error_gate_optimized (gate maps:
  * gate_qmode RQ_QMODE_CHANNEL -> gate_scale[r] / gate_zero[r], RQ_QMODE_STATIC ->
- * [col_group[j] * R + r]). */
+ * [col_group[j] * R + r]).  stats_parts (optional, 4 * R * (C - i2) floats, the
+ * refresh_full_metrics statistics' inputs :1688-1770): planes [4][R][C - i2] of the
+ * optimizer step (optimizer_update_raw), the applied update (optimizer_update), the
+ * regularizer part (gate_regularizer_update: the l2 / hessian term, or gated - step) and the
+ * sine part (sine_regularizer_update). */
 int rq_block_gd_step(float* Wp, int64_t ldw, int R, int R_s, int C, int i2, const float* grad,
                      int64_t ldg, const int64_t* perm, int optimizer, int step, double lr,
                      double grad_clip, float* exp_avg, float* exp_avg_sq, const float* curvature,
                      int reg_strategy, double reg_lambda, const float* w_fp, int64_t ld_fp,
                      const float* hreg, int64_t ld_hreg, int gate_qmode, const float* gate_scale,
                      const float* gate_zero, const int32_t* col_group, int maxq, int sym,
-                     double gate_floor, double gate_sharpness, double sine_amp, void* stream);
+                     double gate_floor, double gate_sharpness, double sine_amp, float* stats_parts,
+                     void* stream);
 
 #ifdef __cplusplus
 }

@@ -411,6 +411,71 @@ def apply_regularizer(st, current, upd, c0, lr, strategy, lam, floor, sharp, sin
 
 
 # ---------------------------------------------------------------------------------------
+# refresh_full_metrics statistics and the block_observer record
+# ---------------------------------------------------------------------------------------
+def quantile_large(tensor, q):
+    """gptq_plus_utils.py:46-60."""
+    flat = tensor.reshape(-1)
+    n = flat.numel()
+    if n == 0:
+        return None
+    k = max(1, min(n, int(n * q + 0.5)))
+    try:
+        return torch.quantile(flat, q).item()
+    except RuntimeError:
+        return flat.kthvalue(k).values.item()
+
+
+def _update_term_stats(chunks, name, outliers):
+    """gptq_plus_utils.py:1657-1668, 1764-1798: abs mean and mean row L2 norm of the rows of all
+    subgroups, with outliers also the abs max and the 0.99 quantile."""
+    cat = torch.cat(chunks, dim=0).float()
+    a = cat.abs()
+    out = {f"{name}_abs_mean": a.mean().item(),
+           f"{name}_mean_row_l2": torch.linalg.norm(cat, dim=1).mean().item()}
+    if outliers:
+        out[f"{name}_abs_max"] = a.max().item()
+        out[f"{name}_abs_q99"] = quantile_large(a, 0.99)
+    return out
+
+
+def _trailing_grad_stats(chunks, grad_clip):
+    """gptq_plus_utils.py:1451-1467, 1669-1687."""
+    cat = torch.cat(chunks, dim=0).float()
+    out = {"remaining_grad_abs_mean": cat.abs().mean().item(),
+           "remaining_grad_mean_row_l2": torch.linalg.norm(cat, dim=1).mean().item()}
+    if grad_clip is not None and grad_clip > 0:
+        out["remaining_grad_clipped_abs_mean"] = cat.clamp(min=-grad_clip, max=grad_clip).abs().mean().item()
+    else:
+        out["remaining_grad_clipped_abs_mean"] = out["remaining_grad_abs_mean"]
+    return out
+
+
+_STAT_KEYS = ("remaining_grad_abs_mean", "remaining_grad_clipped_abs_mean", "remaining_grad_mean_row_l2",
+              "second_order_update_abs_mean", "second_order_update_mean_row_l2",
+              "second_order_update_abs_max", "second_order_update_abs_q99", "first_order_raw_abs_mean",
+              "first_order_raw_mean_row_l2", "first_order_update_abs_mean", "first_order_update_mean_row_l2",
+              "first_order_update_abs_max", "first_order_update_abs_q99", "regularizer_update_abs_mean",
+              "regularizer_update_mean_row_l2", "sine_regularizer_update_abs_mean",
+              "sine_regularizer_update_mean_row_l2")
+
+
+def _observer_record(i1, i2, blocksize, columns, meta, stats, block_gd):
+    """The dict handed to block_observer (gptq_plus_utils.py:1462-1496 block_backward,
+    1784-1817 block_gd); statistics not computed are None."""
+    rec = {"block_idx": i1 // blocksize, "col_start": i1, "col_end": i2, "remaining_columns": columns - i2}
+    for k in _STAT_KEYS:
+        rec[k] = stats.get(k)
+    keys = ["mean_refresh_loss", "train_mean_refresh_loss", "val_mean_refresh_loss",
+            "refresh_subset_mean_refresh_loss"]
+    if block_gd:
+        keys += ["slide_alpha", "mean_refresh_loss_current", "mean_refresh_loss_next"]
+    for k in keys:
+        rec[k] = None if meta is None else meta.get(k)
+    return rec
+
+
+# ---------------------------------------------------------------------------------------
 # GPTQPlus (all g_update modes; the layer backward comes from the caller's refresh fn)
 # ---------------------------------------------------------------------------------------
 @dataclass
@@ -521,7 +586,8 @@ class GPTQPlusOracle:
                     grad_reg_strategy="none", grad_reg_lambda=0.0, grad_gate_floor=0.1,
                     grad_gate_sharpness=1.0, grad_gate_sine_amp=0.0, second_order_scale=1.0,
                     grad_clip=1.0, slide_refresh_start=0,
-                    slide_refresh_block_total=None) -> FasterquantResult:
+                    slide_refresh_block_total=None, block_observer=None,
+                    refresh_full_metrics=False) -> FasterquantResult:
         # g_update modes: gptq_plus_utils.py:1190-1199, 1360-1367 (inner), 1408-1448
         # (block_backward refresh), 1500-1570 (outer), 1572-1848 (block_gd step)
         if g_update_mode not in ("frozen", "surrogate_block", "surrogate_online", "block_gd",
@@ -717,13 +783,16 @@ class GPTQPlusOracle:
             if block_bw and enable_gradient_update:                     # :1408-1448
                 if gradient_refresh_fn is None:
                     raise ValueError("`gradient_refresh_fn` must be provided for g_update_mode='block_backward'.")
-                grad, _meta = gradient_refresh_fn(snapshot(lambda st: st["current"]))
+                grad, meta = gradient_refresh_fn(snapshot(lambda st: st["current"]))
                 grad = grad.to(dt)
+                trailing = []
                 for bs in block_states:
                     st = bs[0]
                     g_sub = grad[st["r0"]:st["r1"], :]
                     if actorder:
                         g_sub = g_sub[:, st["perm"]]
+                    if refresh_full_metrics and g_sub[:, i2:].numel() > 0:
+                        trailing.append(g_sub[:, i2:])
                     beta, Z, GHinv, _ = gradient_terms(g_sub, st["Hinv_init"], st["Hinv"], self.alpha,
                                                        self.reference_loss, self.rows, self.columns,
                                                        enable_gradient_update)
@@ -731,7 +800,11 @@ class GPTQPlusOracle:
                     st["Z"], st["GHinv"] = Z, GHinv
                     st["anchor"] = st["current"].clone()
                     bs[2] = Z[:, i1:i2]
+                if block_observer is not None:                         # :1448-1496
+                    stats = _trailing_grad_stats(trailing, grad_clip) if trailing else {}
+                    block_observer(_observer_record(i1, i2, blocksize, self.columns, meta, stats, False))
 
+            second_chunks = []
             for st, Err1, Z1 in block_states:                          # :1500-1570
                 GHinv_rest = _current_ghinv(st["GHinv"][:, i2:], st["W_sub"][:, i2:], st["anchor"][:, i2:],
                                             st["beta_view"], outer_mode)
@@ -739,6 +812,8 @@ class GPTQPlusOracle:
                 second = Err1.matmul(st["Hinv"][i1:i2, i2:])
                 if block_gd:
                     st["W_sub"][:, i2:] -= sos * (second + G_Update)
+                    if refresh_full_metrics and second.numel() > 0:
+                        second_chunks.append(sos * second)
                 else:
                     st["W_sub"][:, i2:] -= second + G_Update
                 st["GHinv"][:, i2:] -= st["Z"][:, i1:i2].matmul(st["Hinv"][i1:i2, i2:])
@@ -757,17 +832,39 @@ class GPTQPlusOracle:
                 total = slide_refresh_block_total if slide_refresh_block_total is not None else n_refresh_total
                 idx = slide_refresh_start + refresh_idx
                 slide_alpha = 1.0 - idx / max(total - 1, 1) if total > 1 else 1.0
-                grad, _meta = gradient_refresh_fn(snapshot(effective), slide_alpha=slide_alpha)
+                grad, meta = gradient_refresh_fn(snapshot(effective), slide_alpha=slide_alpha)
                 grad = grad.to(dt)
+                trailing, parts = [], ([], [], [], [])
                 for st in states:                                      # :1688-1711
                     g_sub = grad[st["r0"]:st["r1"], :]
                     if actorder:
                         g_sub = g_sub[:, st["perm"]]
+                    if refresh_full_metrics and g_sub[:, i2:].numel() > 0:
+                        trailing.append(g_sub[:, i2:])
                     raw = opt_update(st["opt"], g_sub, i2, grad_lr, grad_clip=grad_clip)
-                    upd, _, _ = apply_regularizer(st, effective(st), raw, i2, grad_lr, grad_reg_strategy,
-                                                  grad_reg_lambda, grad_gate_floor, grad_gate_sharpness,
-                                                  grad_gate_sine_amp, maxq_int, quantizer.sym)
+                    upd, gate_part, sine_part = apply_regularizer(
+                        st, effective(st), raw, i2, grad_lr, grad_reg_strategy, grad_reg_lambda,
+                        grad_gate_floor, grad_gate_sharpness, grad_gate_sine_amp, maxq_int, quantizer.sym)
                     st["pending"] = upd
+                    if refresh_full_metrics:                           # :1757-1763
+                        if raw.numel() > 0:
+                            parts[0].append(raw)
+                        if upd.numel() > 0:
+                            parts[1].append(upd)
+                            parts[2].append(gate_part)
+                            parts[3].append(sine_part)
+                if block_observer is not None:                         # :1657-1817
+                    stats = {}
+                    if second_chunks:
+                        stats.update(_update_term_stats(second_chunks, "second_order_update", True))
+                    if trailing:
+                        stats.update(_trailing_grad_stats(trailing, grad_clip))
+                    for chunks, name, outl in zip(parts, ("first_order_raw", "first_order_update",
+                                                          "regularizer_update", "sine_regularizer_update"),
+                                                  (False, True, False, False)):
+                        if chunks:
+                            stats.update(_update_term_stats(chunks, name, outl))
+                    block_observer(_observer_record(i1, i2, blocksize, self.columns, meta, stats, True))
                 for st in states:                                      # :1828-1834
                     upd = st.pop("pending")
                     if upd.numel() > 0:

@@ -190,6 +190,26 @@ FLIP_BAR = {"g2_sym4_static_gplus": 30, "g4_asym4_surrogate_online": 60, "g4_sym
             "g2_sym4_block_gd_adam_l2": 100}
 
 
+def _compare_observer_records(name, recs_g, recs_o):
+    """block_observer records of the GPU run against the oracle's: the same blocks and keys,
+    None in the same places, every statistic within 1e-3 relative (the runs share H and H^-1;
+    their weights differ by the few code flips this case allows, which move the refreshed
+    gradients and the update terms by ~1e-5 relative)."""
+    assert len(recs_g) == len(recs_o)
+    worst = 0.0
+    for rg, ro in zip(recs_g, recs_o):
+        assert rg.keys() == ro.keys()
+        for k, vo in ro.items():
+            vg = rg[k]
+            if vo is None or isinstance(vo, int):
+                assert vg == vo, (k, vg, vo)
+                continue
+            d = abs(vg - vo) / max(abs(vo), 1e-30)
+            worst = max(worst, d)
+            assert d <= 1e-3, (k, rg["block_idx"], vg, vo)
+    print(f"{name}: observer statistics max rel diff {worst:.2e} over {len(recs_o)} blocks")
+
+
 @pytest.mark.parametrize("cfg", CFGS, ids=[c["name"] for c in CFGS])
 def test_dropin_vs_oracle(cfg):
     R, C, G = cfg["R"], cfg["C"], cfg["G"]
@@ -204,7 +224,10 @@ def test_dropin_vs_oracle(cfg):
     fq = dict(blocksize=cfg["B"], percdamp=0.01, groupsize=cfg["gs"], actorder=cfg["act"],
               static_groups=cfg["act"], block_atomic_quant=cfg["atomic"],
               **_mode_kwargs(cfg, X, W, grad))
-    res = o.fasterquant(**fq)
+    # the refresh modes also hand their refresh_full_metrics statistics to block_observer
+    refresh = fq["g_update_mode"] in ("block_gd", "block_backward")
+    recs_o, recs_g = [], []
+    res = o.fasterquant(**fq, **(dict(block_observer=recs_o.append, refresh_full_metrics=True) if refresh else {}))
 
     g, layer = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False),
                           cfg.get("pc", True))
@@ -215,8 +238,11 @@ def test_dropin_vs_oracle(cfg):
     g.H.copy_(o.H.to(DEV))
     g.act_square.copy_(o.act_square.to(DEV))
     inject = {"hinv": [(r.Hinv_init.to(DEV), r.Hinv.to(DEV)) for r in res.subgroups]}
-    g.fasterquant(export_to_et=True, inject=inject, **fq)
+    g.fasterquant(export_to_et=True, inject=inject, **fq,
+                  **(dict(block_observer=recs_g.append, refresh_full_metrics=True) if refresh else {}))
     torch.cuda.synchronize()
+    if refresh:
+        _compare_observer_records(cfg["name"], recs_g, recs_o)
     if cfg["act"]:
         assert torch.equal(g.perm.cpu(), res.subgroups[0].perm)
     n = res.W_int.numel()
@@ -300,8 +326,6 @@ def test_dropin_errors_and_side_effects():
         g.fasterquant(blocksize=64, groupsize=32, actorder=False, static_groups=False)
     with pytest.raises(NotImplementedError):
         g.fasterquant(g_update_mode="online")                       # not a mode of the reference
-    with pytest.raises(NotImplementedError):
-        g.fasterquant(blocksize=64, g_update_mode="block_gd", refresh_full_metrics=True)
     # a refresh mode without its layer backward fails at the first refresh, like the
     # reference (:1573-1574, :1409-1410), before the layer weight is touched
     w_before = layer.weight.data.clone()

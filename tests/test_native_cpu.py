@@ -58,10 +58,10 @@ def test_argument_validation_needs_no_device():
     D = ctypes.c_double
     assert lib.rq_block_gd_step(fake, 8, 4, 4, 8, 4, fake, 8, null, 1, 1, D(1e-3), D(1.0), null, null,
                                 null, 0, D(0.0), null, 0, null, 0, 0, null, null, null, 7, 1, D(0.1),
-                                D(1.0), D(0.0), null) == nat.RQ_EINVAL
+                                D(1.0), D(0.0), null, null) == nat.RQ_EINVAL
     assert lib.rq_block_gd_step(fake, 8, 4, 4, 8, 4, fake, 8, null, 0, 0, D(1e-3), D(1.0), null, null,
                                 null, 2, D(0.1), null, 0, null, 0, 0, null, null, null, 7, 1, D(0.1),
-                                D(1.0), D(0.0), null) == nat.RQ_EINVAL
+                                D(1.0), D(0.0), null, null) == nat.RQ_EINVAL
     assert lib.rq_current_weight(fake, 8, fake, 4, 8, 4, 1, fake, null, null, 8, null, null, 0, fake, 8,
                                  null) == nat.RQ_EINVAL
     assert lib.rq_hessian_reg_gemm(fake, 8, fake, 8, 4, 3, 0, fake, 8, null) == nat.RQ_EINVAL
