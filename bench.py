@@ -268,9 +268,14 @@ def roofline(cfg, args, kernel_ms, launches, steps):
     ach = per_launch_flops / (ms * 1e-3) / 1e12
     traffic, tsrc = load_traffic(args.hessian_math, args.config)
     pieces = PIECES[args.hessian_math]
+    kernel = KERNEL[args.hessian_math]
+    if args.x_fp32:   # fp32 activations: hi w0 + hi w1 + lo w0 on the split path
+        traffic, tsrc = None, "fp32 activations: not measured"
+        pieces = 3 if args.hessian_math != "fp32" else 1
+        kernel = "k_hessian_split32" if args.hessian_math != "fp32" else "k_hessian_accum<float>"
     return {"bound": "mfma", "achieved": round(ach, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
-            "kernel": KERNEL[args.hessian_math], "launch_ms": round(ms, 4), "launches": launches // steps,
+            "kernel": kernel, "launch_ms": round(ms, 4), "launches": launches // steps,
             "flops_per_launch": int(per_launch_flops),
             "algorithmic": "fp32 flops of H_g += X^T diag(s_g) X, upper triangle incl. diagonal "
                            "(G*n*C*(C+1) per launch of n tokens)",
@@ -566,10 +571,14 @@ def run(args):
     layer_mode = cfg["kind"] == "layer"
     if layer_mode:
         xs, mods = make_layer_inputs(dev, cfg)
+        if args.x_fp32:
+            xs = {k: v.float() for k, v in xs.items()}
         layers = {n: torch.nn.Linear(C, R, bias=False).to(dev, torch.float16) for n, R, C, _ in LAYER8B}
         step = lambda timer=None, keep=False: one_layer(xs, mods, cfg, layers, timer, keep)
     else:
         X, W, s, grad = make_inputs(dev, cfg)
+        if args.x_fp32:
+            X = X.float()
         layer = torch.nn.Linear(cfg["C"], cfg["R"], bias=False).to(dev, torch.float16)
         step = lambda timer=None, keep=False: one_linear(X, W, s, grad, cfg, layer, timer)
     torch.cuda.synchronize()
@@ -589,7 +598,7 @@ def run(args):
     line = {
         "metric": METRIC, "value": round(ms_step / per, 2), "unit": "ms", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 2), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32 (fp16 inputs)", "data": "synthetic (seeded, generated on the GPU)",
+        "vs_baseline": None, "dtype": "f32 (fp32 inputs)" if args.x_fp32 else "f32 (fp16 inputs)", "data": "synthetic (seeded, generated on the GPU)",
         "config": {"workload": WORKLOAD[args.config].format(alpha=cfg["alpha"]), "parallelism": "single GPU",
                    "hessian_math": args.hessian_math},
         "roofline": roofline(cfg, args, kernel_ms, launches, args.steps),
@@ -623,6 +632,9 @@ def main():
     ap.add_argument("--hessian-math", choices=sorted(PIECES), default="split16",
                     help="Hessian kernel for fp16 inputs: split16 (two fp16 MFMA products per fp32 product), "
                          "split16x3 (three: exact products), fp32 (fp32 MFMA)")
+    ap.add_argument("--x-fp32", action="store_true",
+                    help="fp32 activations (the reference's add_batch takes any float dtype): the same inputs "
+                         "converted to fp32")
     ap.add_argument("--copy-calibration", action="store_true", help="only run a 1 GiB device copy (counter calibration)")
     ap.add_argument("--gemm-calibration", action="store_true", help="only time torch.matmul in fp16 / fp32 / fp64")
     ap.add_argument("--stats-table", metavar="STATS_CSV", help="print a rocprofv3 kernel-stats CSV as a table")

@@ -36,7 +36,7 @@ SIGNATURES = {
     "rq_version": (_I, []),
     "rq_hessian_accum": (_I, [_P, _I, _L, _L, _I, _P, _L, _I, _P, _P, _P, _L, _P]),
     "rq_hessian_accum_noalloc": (_I, [_P, _I, _L, _L, _I, _P, _L, _I, _P, _P, _P]),
-    "rq_hessian_workspace_bytes": (_L, [_L, _I, _I]),
+    "rq_hessian_workspace_bytes": (_L, [_L, _I, _I, _I]),
     "rq_hessian_math": (_I, [_I]),
     "rq_hessian_timing_events": (_I, [_P, _P]),
     "rq_hessian_accum_multi": (_I, [_P, _I, _L, _L, _I, _I, _P, _P, _P, _P, _P, _L, _P]),

@@ -656,7 +656,7 @@ __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int6
 // The last slice of a split item adds the S partials (in slice order) to H.
 __device__ __forceinline__ void reduce_split_slices(const float* __restrict__ part0, int S,
                                                     float* __restrict__ Hg, const float* __restrict__ scl,
-                                                    int R0, int C0, int C) {
+                                                    int R0, int C0, int C, const float* __restrict__ rsc = nullptr) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -693,7 +693,10 @@ __device__ __forceinline__ void reduce_split_slices(const float* __restrict__ pa
       const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
       if (i < C && j < C) {
         float* ph = Hg + (int64_t)i * C + j;
-        *ph = *ph + sum * inv;
+        if (rsc)   // fp32 X: 2^-(ex_i + e_j), applied in fp64 (exact)
+          *ph = *ph + (float)((double)sum * ((double)inv / (double)rsc[i]));
+        else
+          *ph = *ph + sum * inv;
       }
     }
   }
@@ -754,6 +757,257 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
   if (!last_slice) return;
   __threadfence();
   reduce_split_slices(part0, S, Hg, scl, R0, C0, C);
+}
+
+// ---------------------------------------------------------------------------------------------
+// fp32 X (k_hessian_split32): the same 256 x 256 upper tiles, with x no longer exact in 16 bits.
+// The row operand is x 2^ex_i written as two fp16 pieces hi + lo (22 of x's 24 bits; k_xrows32),
+// the column operand w = fl32(x * s) 2^e_j is split in the kernel from the exact fp32 x (fp32
+// column fragments, k_xprep32) into w0 + w1 (as the two-piece fp16 mode), and each 16-token
+// step issues hi w1, hi w0 and lo w0: 3 MFMAs per product.  The terms left out (lo w1, and the
+// residuals of both splits) are each below 2^-22 of |x w|, so every product is the reference's
+// fp32 product within ~2^-20.5 relative, below the rounding of the fp32 sums themselves.  The
+// epilogue multiplies by 2^-(ex_i + e_j) (exact).
+//
+// LDS stage (one 16-token step): hi row fragments [0, 8 KB), lo row fragments [8, 16 KB), the
+// fp32 column fragment of wave w at 16 KB + 2 KB w (two 1 KB halves), the 16 saliencies.  A step
+// runs in two phases: (A) hi x (w1, w0) while the lo rows of this step are read and the next
+// step's column fragment is split; (B) lo x w0 while the next step's hi rows are read.
+constexpr int X3_HI = 0;
+constexpr int X3_LO = 8 * 1024;
+constexpr int X3_COL = 16 * 1024;
+constexpr int X3_SAL = X3_COL + XWAVES * 2048;
+constexpr int X3_STAGE = X3_SAL + 256;
+
+// Stage step k: hi and lo row fragment w, this wave's fp32 column fragment (two halves), and
+// -- wave 0, lanes 0-3 -- the step's 16 saliencies.  4 staging loads per wave (wave 0: 5).
+__device__ __forceinline__ void stage_step32(uint8_t* st, const uint16_t* ph, const uint16_t* pl,
+                                             const float* pc, const float* sg, int wave, int lane,
+                                             int64_t k) {
+  asm volatile("" : "+s"(k));
+  lds_dma16(ph + k * 512, st + X3_HI + wave * 1024);
+  lds_dma16(pl + k * 512, st + X3_LO + wave * 1024);
+  lds_dma16(pc + k * 512, st + X3_COL + wave * 2048);
+  lds_dma16(pc + k * 512 + 256, st + X3_COL + wave * 2048 + 1024);
+  if (wave == 0 && lane < 4) lds_dma16(sg + 16 * k + 4 * lane, st + X3_SAL);
+}
+
+// w = fl32(x * s) * sc for 8 tokens (exact x), split into two packed fp16 pieces.
+__device__ __forceinline__ void split8_f32(const float (&x)[8], const float (&sv)[8], float sc, uint4 (&p)[2]) {
+  uint32_t o0[4], o1[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    float a = __builtin_fmaf(x[2 * m], sv[2 * m], 0.0f) * sc;
+    float b = __builtin_fmaf(x[2 * m + 1], sv[2 * m + 1], 0.0f) * sc;
+    asm("v_cvt_pk_f16_f32 %0, %2, %3\n\t"
+        "v_fma_mix_f32 %2, -%0, 1.0, %2 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mix_f32 %3, -%0, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_cvt_pk_f16_f32 %1, %2, %3"
+        : "=&v"(o0[m]), "=&v"(o1[m]), "+v"(a), "+v"(b));
+  }
+  p[0] = make_uint4(o0[0], o0[1], o0[2], o0[3]);
+  p[1] = make_uint4(o1[0], o1[1], o1[2], o1[3]);
+}
+
+// This wave's fp32 column fragment and the saliencies of a staged step.
+__device__ __forceinline__ void read_col32(const uint8_t* st, int wave, int lane, float (&x)[8], float (&sv)[8]) {
+  const uint8_t* c = st + X3_COL + wave * 2048 + lane * 16;
+  const float4 a = *reinterpret_cast<const float4*>(__builtin_assume_aligned(c, 16));
+  const float4 b = *reinterpret_cast<const float4*>(__builtin_assume_aligned(c + 1024, 16));
+  const uint8_t* sp = st + X3_SAL + 32 * (lane >> 5);
+  const float4 s0 = *reinterpret_cast<const float4*>(__builtin_assume_aligned(sp, 16));
+  const float4 s1 = *reinterpret_cast<const float4*>(__builtin_assume_aligned(sp + 16, 16));
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w; sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
+}
+
+// One 16-token step k (stages CUR = k, NXT = k+1, FILL = k+XDEPTH-1).  Waits as split_step:
+// this step's and the next step's staging must be complete (phase A reads the lo rows of k and
+// the column fragment of k+1, phase B the hi rows of k+1), so vmcnt(4 * (XDEPTH - 3)).
+template <bool DIAG, int CUR, int NXT, int FILL>
+__device__ __forceinline__ void split_step32(uint4 (&p)[2], uint4 (&ah)[8], uint4 (&al)[8], floatx16 (&acc)[8],
+                                             const XStages& L, const uint16_t* ph, const uint16_t* pl,
+                                             const float* pc, const float* sg, float sc, int wave, int lane,
+                                             int64_t k, int64_t last, int lim) {
+  typedef XType<__half>::v8 v8;
+  XWAIT_VM(4 * (XDEPTH - 3));
+  __builtin_amdgcn_s_barrier();
+  stage_step32(L.s[FILL], ph, pl, pc, sg, wave, lane, min(k + XDEPTH - 1, last));
+  // phase A: hi rows x (w1, w0); the lo rows of this step and the next column fragment are read
+  const uint8_t* cur = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[CUR] + X3_LO + lane * 16, 16));
+#pragma unroll
+  for (int bi = 0; bi < 8; ++bi)
+    if (!DIAG || bi < lim) al[bi] = *reinterpret_cast<const uint4*>(cur + bi * 1024);
+  float x[8], sv[8];
+  read_col32(L.s[NXT], wave, lane, x, sv);
+#pragma unroll
+  for (int bi = 0; bi < 8; ++bi)
+    if (!DIAG || bi < lim)
+      acc[bi] = XType<__half>::mfma(__builtin_bit_cast(v8, ah[bi]), __builtin_bit_cast(v8, p[1]), acc[bi]);
+  uint4 pn[2];
+  split8_f32(x, sv, sc, pn);
+#pragma unroll
+  for (int bi = 0; bi < 8; ++bi)
+    if (!DIAG || bi < lim)
+      acc[bi] = XType<__half>::mfma(__builtin_bit_cast(v8, ah[bi]), __builtin_bit_cast(v8, p[0]), acc[bi]);
+  // phase B: lo rows x w0; the next step's hi rows are read
+  const uint8_t* nxt = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[NXT] + X3_HI + lane * 16, 16));
+#pragma unroll
+  for (int bi = 0; bi < 8; ++bi)
+    if (!DIAG || bi < lim)
+      acc[bi] = XType<__half>::mfma(__builtin_bit_cast(v8, al[bi]), __builtin_bit_cast(v8, p[0]), acc[bi]);
+#pragma unroll
+  for (int bi = 0; bi < 8; ++bi)
+    if (!DIAG || bi < lim) ah[bi] = *reinterpret_cast<const uint4*>(nxt + bi * 1024);
+  p[0] = pn[0];
+  p[1] = pn[1];
+}
+
+template <bool DIAG, int... J>
+__device__ __forceinline__ void split_round32(uint4 (&p)[2], uint4 (&ah)[8], uint4 (&al)[8], floatx16 (&acc)[8],
+                                              const XStages& L, const uint16_t* ph, const uint16_t* pl,
+                                              const float* pc, const float* sg, float sc, int wave, int lane,
+                                              int64_t k, int64_t last, int lim, int nsteps,
+                                              std::integer_sequence<int, J...>) {
+  ((J < nsteps ? split_step32<DIAG, J, (J + 1) % XDEPTH, (J + XDEPTH - 1) % XDEPTH>(
+                     p, ah, al, acc, L, ph, pl, pc, sg, sc, wave, lane, k + J, last, lim)
+               : void()),
+   ...);
+}
+
+// Tile (R0, C0) of one target over steps [kbeg, kend): as split_tile, with the fp32 operands.
+template <bool DIAG>
+__device__ __forceinline__ void split_tile32(const uint16_t* __restrict__ XH, const uint16_t* __restrict__ XL,
+                                             const float* __restrict__ XC, int64_t nks, int C,
+                                             const float* __restrict__ sg, const float* __restrict__ scl,
+                                             const float* __restrict__ rsc, float* __restrict__ Hg, int R0,
+                                             int C0, int64_t kbeg, int64_t kend, float* __restrict__ part,
+                                             const XStages& L) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 31, fh = lane >> 5;
+  const int cbw = split_colblock(wave);
+  const int Cw = C0 + 32 * cbw;
+  const int lim = DIAG ? cbw + 1 : 8;
+  const int ncb = (C + 31) / 32;
+  const int64_t rb = (int64_t)min(R0 / 32 + wave, ncb - 1) * nks * 64 + lane;
+  const uint16_t* ph = XH + rb * 8;
+  const uint16_t* pl = XL + rb * 8;
+  const float* pc = XC + ((int64_t)min(Cw / 32, ncb - 1) * nks * 128 + lane) * 4;
+  const float sc = scl[min(Cw + fr, C - 1)];
+
+  floatx16 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+
+  const int64_t last = kend - 1;
+#pragma unroll
+  for (int h = 0; h < XDEPTH - 1; ++h) stage_step32(L.s[h], ph, pl, pc, sg, wave, lane, min(kbeg + h, last));
+  uint4 p[2], ah[8], al[8];
+  XWAIT_VM(4 * (XDEPTH - 2));         // this wave's staging of step kbeg
+  __builtin_amdgcn_s_barrier();       // and the other waves'
+  {
+    float x[8], sv[8];
+    read_col32(L.s[0], wave, lane, x, sv);
+    split8_f32(x, sv, sc, p);
+    const uint8_t* cur = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[0] + X3_HI + lane * 16, 16));
+#pragma unroll
+    for (int bi = 0; bi < 8; ++bi)
+      if (!DIAG || bi < lim) ah[bi] = *reinterpret_cast<const uint4*>(cur + bi * 1024);
+  }
+  const int64_t n = kend - kbeg;
+  int64_t k = kbeg;
+  constexpr auto round = std::make_integer_sequence<int, XDEPTH>();
+  for (; k + XDEPTH <= kend; k += XDEPTH)
+    split_round32<DIAG>(p, ah, al, acc, L, ph, pl, pc, sg, sc, wave, lane, k, last, lim, XDEPTH, round);
+  split_round32<DIAG>(p, ah, al, acc, L, ph, pl, pc, sg, sc, wave, lane, k, last, lim, (int)(n % XDEPTH), round);
+  XWAIT_VM(0);
+
+  if (part) {
+#pragma unroll
+    for (int bi = 0; bi < 8; ++bi)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) part[(bi * 16 + e) * XTHREADS + tid] = (DIAG && bi >= lim) ? 0.0f : acc[bi][e];
+    return;
+  }
+  // H[g][i][j] += acc * 2^-(ex_i + e_j), the two exact scalings applied in fp64
+  const int j = Cw + fr;
+  const double inv = (j < C) ? 1.0 / (double)scl[j] : 0.0;
+#pragma unroll
+  for (int bi = 0; bi < 8; ++bi) {
+    if (DIAG && bi >= lim) continue;
+    float hv[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
+      hv[e] = (i < C && j < C) ? Hg[(int64_t)i * C + j] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int i = R0 + 32 * bi + 8 * (e >> 2) + 4 * fh + (e & 3);
+      if (i < C && j < C) Hg[(int64_t)i * C + j] = hv[e] + (float)((double)acc[bi][e] * (inv / (double)rsc[i]));
+    }
+  }
+}
+
+__global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split32(
+    const uint16_t* __restrict__ XH, const uint16_t* __restrict__ XL, const float* __restrict__ XC, int C,
+    const float* __restrict__ sT, int64_t lds_stride, const float* __restrict__ scale,
+    const float* __restrict__ rscale, HTargets tg, int ntarg, int nt, int ntiles, int64_t nks, int full, int S,
+    float* __restrict__ ws, int* __restrict__ cnt) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds0[X3_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds1[X3_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds2[X3_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds3[X3_STAGE];
+  __shared__ int last_slice;
+  static_assert(XDEPTH == 4, "stage arrays");
+  const XStages L{{lds0, lds1, lds2, lds3}};
+  const int total = ntiles * ntarg;
+  const int b = blockIdx.x;
+  int logical, slice = -1;
+  int64_t kbeg = 0, kend = nks;
+  if (b < full) {
+    const int per = full / 8, rem8 = full % 8;
+    const int xcd = b % 8, idx = b / 8;
+    logical = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
+  } else {
+    const int tb = b - full;
+    logical = full + tb / S;
+    slice = tb % S;
+    kbeg = nks * slice / S;
+    kend = nks * (slice + 1) / S;
+  }
+  if (logical >= total) return;
+  const int g = logical % ntarg;
+  int ti, tj;
+  upper_tile_blocked(logical / ntarg, nt, ti, tj);
+  const int R0 = ti * XT, C0 = tj * XT;
+  float* Hg = tg.H[g];
+  const float* scl = scale + (int64_t)g * C;
+  float* part0 = (slice >= 0) ? ws + (int64_t)(logical - full) * S * XPART : nullptr;
+  float* part = part0 ? part0 + (int64_t)slice * XPART : nullptr;
+  if (R0 == C0)
+    split_tile32<true>(XH, XL, XC, nks, C, sT + (int64_t)g * lds_stride, scl, rscale, Hg, R0, C0, kbeg, kend,
+                       part, L);
+  else
+    split_tile32<false>(XH, XL, XC, nks, C, sT + (int64_t)g * lds_stride, scl, rscale, Hg, R0, C0, kbeg, kend,
+                        part, L);
+  if (!part) return;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int* cp = cnt + (logical - full);
+    const int prev = atomicAdd(cp, 1);
+    last_slice = (prev == S - 1);
+    if (last_slice) atomicExch(cp, 0);
+  }
+  __syncthreads();
+  if (!last_slice) return;
+  __threadfence();
+  reduce_split_slices(part0, S, Hg, scl, R0, C0, C, rscale);
 }
 
 // Pre-pass over one 64-column x 256-token block of X: the block in the fragment-blocked
@@ -862,7 +1116,8 @@ __global__ __launch_bounds__(256) void k_xprep(const TX* __restrict__ X, int64_t
 constexpr int XF_COLS = 32;
 constexpr int XF_SEG = 8;
 __global__ __launch_bounds__(256) void k_xfinish(int C, int nchunk, int ntarg, const float* __restrict__ mpart,
-                                                 const float* __restrict__ spart, float* __restrict__ scale) {
+                                                 const float* __restrict__ spart, float* __restrict__ scale,
+                                                 float* __restrict__ rscale) {
   __shared__ float smax[XF_SEG][HMAXT];
   __shared__ float pm[XF_SEG][XF_COLS];
   const int t = threadIdx.x;
@@ -886,6 +1141,16 @@ __global__ __launch_bounds__(256) void k_xfinish(int C, int nchunk, int ntarg, c
   float mt = pm[0][lane32];
 #pragma unroll
   for (int q = 1; q < XF_SEG; ++q) mt = fmaxf(mt, pm[q][lane32]);
+  if (rscale) {   // fp32 X: the column's row-piece scale 2^ex, max|x_c| * 2^ex in [2^14, 2^15)
+    int ex = 0;
+    if (mt > 0.0f && mt <= 3.402823466e38f) {
+      int E = 0;
+      (void)frexpf(mt, &E);
+      ex = 15 - E;
+      ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
+    }
+    rscale[c] = ldexpf(1.0f, ex);
+  }
   for (int g = 0; g < ntarg; ++g) {
     float sm = smax[0][g];
 #pragma unroll
@@ -900,6 +1165,116 @@ __global__ __launch_bounds__(256) void k_xfinish(int C, int nchunk, int ntarg, c
     }
     scale[(int64_t)g * C + c] = ldexpf(1.0f, e);
   }
+}
+
+// fp32 X, pass 1 over one 64-column x 256-token block: the block as fp32 column fragments for
+// k_hessian_split32 (per 32 columns and 16-token step, 2 KB: half q in {0, 1}, lane
+// L = fr + 32 fh holding tokens 8 fh + 4 q .. +3 of column fr; zeros past ntok and C), each
+// column's max |x| and its level-2 act_square sum for this block (as k_xprep), and (first
+// column block only) the targets' saliencies.  LDS holds the block column-major, row stride 257
+// floats, so that the transposing writes and the fragment reads are free of bank conflicts.
+constexpr int XPRS32 = XTOK + 1;
+__global__ __launch_bounds__(256) void k_xprep32(const float* __restrict__ X, int64_t ntok, int64_t ldx, int C,
+                                                 bool vec_ok, float4* __restrict__ XC, int64_t nks,
+                                                 HTargets tg, int ntarg, float* __restrict__ sT, int64_t lds,
+                                                 float* __restrict__ mpart, float* __restrict__ apart,
+                                                 float* __restrict__ spart) {
+  __shared__ float tile[XPC][XPRS32];
+  __shared__ unsigned smx[HMAXT];
+  const int tid = threadIdx.x;
+  const int c0 = blockIdx.x * XPC;
+  const int ch = blockIdx.y;
+  const int64_t t0 = (int64_t)ch * XTOK;
+  // load: 16 float4 per token row, 16 rows per pass
+#pragma unroll 4
+  for (int v = tid; v < 16 * XTOK; v += 256) {
+    const int q = v & 15, tr = v >> 4;
+    const int cb = c0 + 4 * q;
+    const int64_t t = t0 + tr;
+    float e[4];
+    if (vec_ok && cb + 4 <= C && t < ntok) {
+      const float4 f = *reinterpret_cast<const float4*>(X + t * ldx + cb);
+      e[0] = f.x; e[1] = f.y; e[2] = f.z; e[3] = f.w;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) e[k] = (t < ntok && cb + k < C) ? X[t * ldx + cb + k] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) tile[4 * q + k][tr] = e[k];
+  }
+  __syncthreads();
+  const int ncb = (C + 31) / 32;
+  for (int v = tid; v < 2 * (XTOK / 16) * 2 * 64; v += 256) {
+    const int L = v & 63, q = (v >> 6) & 1, kbl = (v >> 7) & (XTOK / 16 - 1), cbl = v >> 11;
+    const int cb = c0 / 32 + cbl;
+    if (cb < ncb) {
+      const float* src = &tile[32 * cbl + (L & 31)][16 * kbl + 8 * (L >> 5) + 4 * q];
+      XC[(((int64_t)cb * nks + (int64_t)ch * (XTOK / 16) + kbl) * 2 + q) * 64 + L] =
+          make_float4(src[0], src[1], src[2], src[3]);
+    }
+  }
+  {
+    __shared__ float qm[4][XPC], ql1[16][XPC];
+    const int cl = tid & (XPC - 1), part = tid >> 6;
+    float m = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      float a = 0.0f;
+#pragma unroll
+      for (int w = part * (XTOK / 4) + 16 * b; w < part * (XTOK / 4) + 16 * b + 16; ++w) {
+        const float v0 = tile[cl][w];
+        m = fmaxf(m, fabsf(v0));
+        a = a + v0 * v0;
+      }
+      ql1[4 * part + b][cl] = a;
+    }
+    qm[part][cl] = m;
+    if (tid < HMAXT) smx[tid] = 0u;
+    __syncthreads();
+    if (tid < XPC && c0 + tid < C) {
+      mpart[(int64_t)ch * C + c0 + tid] = fmaxf(fmaxf(qm[0][tid], qm[1][tid]), fmaxf(qm[2][tid], qm[3][tid]));
+      float l2 = 0.0f;
+#pragma unroll
+      for (int b = 0; b < 16; ++b) l2 = l2 + ql1[b][tid];
+      apart[(int64_t)ch * C + c0 + tid] = l2;
+    }
+  }
+  if (blockIdx.x != 0) return;
+  for (int g = 0; g < ntarg; ++g) {
+    const int64_t t = t0 + tid;
+    const float s = (t < ntok) ? tg.sal[g][t * tg.ld_sal[g]] : 0.0f;
+    sT[(int64_t)g * lds + t] = s;
+    atomicMax(&smx[g], __float_as_uint(fabsf(s)));
+  }
+  __syncthreads();
+  if (tid < ntarg) spart[(int64_t)ch * HMAXT + tid] = __uint_as_float(smx[tid]);
+}
+
+// fp32 X, pass 2: the row pieces of every fragment, hi = rn16(x 2^ex) and lo = rn16(x 2^ex - hi)
+// (fp16, x 2^ex - hi exact in fp32), in the layout of k_xprep's fragments; 2^ex = rscale[c].
+__global__ __launch_bounds__(256) void k_xrows32(const float4* __restrict__ XC, int64_t nfrag, int C, int64_t nks,
+                                                 const float* __restrict__ rscale, uint4* __restrict__ XH,
+                                                 uint4* __restrict__ XL) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;   // (fragment, lane)
+  if (v >= nfrag * 64) return;
+  const int L = (int)(v & 63);
+  const int64_t f = v >> 6;
+  const int c = (int)(f / nks) * 32 + (L & 31);
+  const float rs = (c < C) ? rscale[c] : 1.0f;
+  const float4 a = XC[(f * 2) * 64 + L], b = XC[(f * 2 + 1) * 64 + L];
+  const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t hi[4], lo[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const float u0 = x[2 * m] * rs, u1 = x[2 * m + 1] * rs;
+    const h2 ph = {(_Float16)u0, (_Float16)u1};
+    const h2 pl = {(_Float16)(u0 - (float)ph.x), (_Float16)(u1 - (float)ph.y)};
+    hi[m] = __builtin_bit_cast(uint32_t, ph);
+    lo[m] = __builtin_bit_cast(uint32_t, pl);
+  }
+  XH[v] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+  XL[v] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1355,7 +1730,7 @@ int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, c
     hipLaunchKernelGGL(k_xprep<__hip_bfloat16>, pgrid, dim3(256), 0, s, (const __hip_bfloat16*)x, ntok, ldx,
                        C, vec_ok, xt, nks, tg, ntarg, sT, L.ntok_p, mpart, apart, spart);
   RQ_CHECK_LAUNCH();
-  hipLaunchKernelGGL(k_xfinish, fgrid, dim3(256), 0, s, C, (int)L.nchunk, ntarg, mpart, spart, scale);
+  hipLaunchKernelGGL(k_xfinish, fgrid, dim3(256), 0, s, C, (int)L.nchunk, ntarg, mpart, spart, scale, nullptr);
   RQ_CHECK_LAUNCH();
   {
     const int rc = launch_act_square(x, x_dtype, ntok, ldx, C, tg, ntarg, apart, wb + act_off(), s);
@@ -1380,12 +1755,100 @@ int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, c
   return RQ_OK;
 }
 
+// fp32 X workspace: the split layout plus the hi / lo row pieces, the fp32 column fragments and
+// the per-column row scales.
+struct SplitLayout32 {
+  SplitLayout base;
+  int64_t off_xh, off_xl, off_xc, off_rs, bytes;
+};
+
+SplitLayout32 split_layout32(int64_t ntok, int C, int ntarg, int64_t tail, int S) {
+  SplitLayout32 L;
+  L.base = split_layout(ntok, C, ntarg, tail, S);
+  const int64_t frag16 = align256((int64_t)((C + 31) / 32) * 32 * L.base.ntok_p * 2);
+  L.off_xh = L.base.bytes;
+  L.off_xl = L.off_xh + frag16;
+  L.off_xc = L.off_xl + frag16;
+  L.off_rs = L.off_xc + 2 * frag16;
+  L.bytes = L.off_rs + align256((int64_t)C * 4);
+  return L;
+}
+
+int split32_slots() { return kernel_slots(k_hessian_split32, XTHREADS, 1); }
+
+int64_t split32_ws_need(int64_t ntok, int C, int ntarg) {
+  int nt, ntiles;
+  int64_t total;
+  split_items(C, ntarg, &nt, &ntiles, &total);
+  int tail = 0, S = 1;
+  const int64_t ntok_p = ((ntok + XTOK - 1) / XTOK) * XTOK;
+  tail_split(total, ntok_p / 16, split32_slots(), 16, &tail, &S);
+  return split_layout32(ntok, C, ntarg, tail, S).bytes;
+}
+
+int launch_split32(const float* x, int64_t ntok, int64_t ldx, int C, const HTargets& tg, int ntarg, void* ws,
+                   int64_t ws_bytes, hipStream_t s) {
+  int nt, ntiles;
+  int64_t total;
+  split_items(C, ntarg, &nt, &ntiles, &total);
+  if (total > 0x7fffffff / 8) return RQ_EINVAL;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (((size_t)ldx * 4) % 16 == 0);
+  int tail = 0, S = 1;
+  SplitLayout32 L = split_layout32(ntok, C, ntarg, 0, 1);
+  const int64_t nks = L.base.ntok_p / 16;
+  tail_split(total, nks, split32_slots(), 16, &tail, &S);
+  L = split_layout32(ntok, C, ntarg, tail, S);
+  if (ws_bytes < L.bytes) {                       // no room for the slices: whole items only
+    tail = 0;
+    S = 1;
+    L = split_layout32(ntok, C, ntarg, 0, 1);
+  }
+  char* wb = reinterpret_cast<char*>(ws);
+  uint16_t* xh = reinterpret_cast<uint16_t*>(wb + L.off_xh);
+  uint16_t* xl = reinterpret_cast<uint16_t*>(wb + L.off_xl);
+  float* xc = reinterpret_cast<float*>(wb + L.off_xc);
+  float* rs = reinterpret_cast<float*>(wb + L.off_rs);
+  float* sT = reinterpret_cast<float*>(wb + L.base.off_st);
+  float* mpart = reinterpret_cast<float*>(wb + L.base.off_m);
+  float* apart = reinterpret_cast<float*>(wb + L.base.off_a);
+  float* spart = reinterpret_cast<float*>(wb + L.base.off_s);
+  float* scale = reinterpret_cast<float*>(wb + L.base.off_scale);
+  dim3 pgrid((C + XPC - 1) / XPC, (unsigned)L.base.nchunk), fgrid((C + XF_COLS - 1) / XF_COLS);
+  hipLaunchKernelGGL(k_xprep32, pgrid, dim3(256), 0, s, x, ntok, ldx, C, vec_ok, reinterpret_cast<float4*>(xc),
+                     nks, tg, ntarg, sT, L.base.ntok_p, mpart, apart, spart);
+  RQ_CHECK_LAUNCH();
+  hipLaunchKernelGGL(k_xfinish, fgrid, dim3(256), 0, s, C, (int)L.base.nchunk, ntarg, mpart, spart, scale, rs);
+  RQ_CHECK_LAUNCH();
+  const int64_t nfrag = (int64_t)((C + 31) / 32) * nks;
+  hipLaunchKernelGGL(k_xrows32, dim3((unsigned)((nfrag * 64 + 255) / 256)), dim3(256), 0, s,
+                     reinterpret_cast<const float4*>(xc), nfrag, C, nks, rs, reinterpret_cast<uint4*>(xh),
+                     reinterpret_cast<uint4*>(xl));
+  RQ_CHECK_LAUNCH();
+  {
+    const int rc = launch_act_square(x, RQ_F32, ntok, ldx, C, tg, ntarg, apart, wb + act_off(), s);
+    if (rc) return rc;
+  }
+  const int full = (int)(total - tail);
+  int* cnt = tail > 0 ? reinterpret_cast<int*>(ws) : nullptr;
+  float* wsf = tail > 0 ? reinterpret_cast<float*>(wb + L.base.off_part) : nullptr;
+  dim3 grid((unsigned)(full + (int64_t)tail * S)), block(XTHREADS);
+  hipEvent_t stop = timing_begin(s);
+  hipLaunchKernelGGL(k_hessian_split32, grid, block, 0, s, xh, xl, xc, C, sT, L.base.ntok_p, scale, rs, tg, ntarg,
+                     nt, ntiles, nks, full, S, wsf, cnt);
+  RQ_CHECK_LAUNCH();
+  if (stop && hipEventRecord(stop, s) != hipSuccess) return RQ_EHIP;
+  return RQ_OK;
+}
+
 int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, const HTargets& tg,
                    int ntarg, void* ws, int64_t ws_bytes, hipStream_t s) {
   const bool aligned = ws && ((reinterpret_cast<uintptr_t>(ws) & 255) == 0);
   if (x_dtype != RQ_F32 && g_hmath.load() != RQ_HMATH_FP32 && aligned &&
       ws_bytes >= split_layout(ntok, C, ntarg, 0, 1).bytes)
     return launch_split(x, x_dtype, ntok, ldx, C, tg, ntarg, ws, ws_bytes, s);
+  if (x_dtype == RQ_F32 && g_hmath.load() != RQ_HMATH_FP32 && aligned &&
+      ws_bytes >= split_layout32(ntok, C, ntarg, 0, 1).bytes)
+    return launch_split32(static_cast<const float*>(x), ntok, ldx, C, tg, ntarg, ws, ws_bytes, s);
   const int nt = (C + HT - 1) / HT;
   const int ntiles = nt * (nt + 1) / 2;
   const int64_t total = (int64_t)ntiles * ntarg;
@@ -1439,8 +1902,9 @@ extern "C" int rq_hessian_math(int mode) {
   return g_hmath.exchange(mode);
 }
 
-extern "C" int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets) {
+extern "C" int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets, int x_dtype) {
   if (ntok < 0 || C <= 0 || ntargets <= 0) return RQ_EINVAL;
+  if (x_dtype != RQ_F16 && x_dtype != RQ_BF16 && x_dtype != RQ_F32) return RQ_EINVAL;
   const int nt = (C + HT - 1) / HT;
   int64_t need = 0;
   for (int t0 = 0; t0 < ntargets; t0 += HMAXT) {   // per launch of at most 32 targets
@@ -1448,7 +1912,7 @@ extern "C" int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets)
     int tail = 0, S = 1;
     tail_split((int64_t)nt * (nt + 1) / 2 * n, (ntok + HKC - 1) / HKC, hessian_slots(), 8, &tail, &S);
     int64_t b = hessian_ws_bytes(ntok, C, tail, S);
-    const int64_t bs = split_ws_need(ntok, C, n);
+    const int64_t bs = x_dtype == RQ_F32 ? split32_ws_need(ntok, C, n) : split_ws_need(ntok, C, n);
     if (bs > b) b = bs;
     if (b > need) need = b;
   }

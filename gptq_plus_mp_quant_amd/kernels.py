@@ -56,7 +56,8 @@ def hessian_workspace(x, ntargets):
     tail slices' partial tiles and counters (zero-filled on allocation; the kernels leave the
     counters zero).  Launches on one stream are ordered, so the calls on that stream share it;
     calls on another stream get their own."""
-    need = int(nat.load().rq_hessian_workspace_bytes(x.shape[0], x.shape[1], int(ntargets)))
+    need = int(nat.load().rq_hessian_workspace_bytes(x.shape[0], x.shape[1], int(ntargets),
+                                                     nat.dtype_code(x.dtype)))
     if need <= 0:
         return None, 0
     dev = x.device.index if x.device.index is not None else torch.cuda.current_device()

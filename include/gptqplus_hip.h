@@ -52,18 +52,20 @@ int rq_version(void);
  * allocated; the library leaves it reusable): with at least rq_hessian_workspace_bytes
  * bytes the items of a partly filled last round are split along the tokens so the launch
  * ends with full rounds; NULL runs whole items only.  Calls that overlap in time on one
- * device need separate workspaces. */
-int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets);
+ * device need separate workspaces.  The size depends on x_dtype (fp32 X needs its 16-bit row
+ * pieces and fp32 column copy). */
+int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets, int x_dtype);
 
-/* Kernel choice for fp16 / bf16 X (process-wide; fp32 X always uses the fp32 MFMA kernel).
- * The split kernels form each fp32 product x * fl32(x * s) on the 16-bit MFMA pipe from the
- * weighted operand cut into 16-bit pieces (after an exact power-of-two column scaling), and
- * accumulate in fp32; they need the workspace (with less than rq_hessian_workspace_bytes the
- * fp32 kernel runs instead).
+/* Kernel choice (process-wide).  The split kernels form each fp32 product x * fl32(x * s) on
+ * the 16-bit MFMA pipe from the weighted operand cut into 16-bit pieces (after an exact
+ * power-of-two column scaling), and accumulate in fp32; they need the workspace (with less
+ * than rq_hessian_workspace_bytes the fp32 kernel runs instead).
  * RQ_HMATH_SPLIT16 (default): fp16 X in two pieces (22 of the operand's 24 bits: each product
- *   within 2^-23 relative of the reference's), bf16 X in three (exact products).
+ *   within 2^-23 relative of the reference's), bf16 X in three (exact products); fp32 X with x
+ *   itself in two fp16 pieces too, three MFMAs per product (hi w0, hi w1, lo w0: each product
+ *   within ~2^-20.5 relative).
  * RQ_HMATH_SPLIT16X3: three pieces for fp16 X too (exact products, 1.5x the MFMA work).
- * RQ_HMATH_FP32: fp32 MFMA on converted operands.
+ * RQ_HMATH_FP32: fp32 MFMA on converted operands (also for fp32 X).
  * mode < 0 queries.  Returns the previous mode, or RQ_EINVAL.  No counterpart in the
  * reference (its bmm runs in fp32, gptq_plus_utils.py:845-847). */
 #define RQ_HMATH_SPLIT16 0

@@ -1,5 +1,5 @@
-"""The split-operand Hessian kernel (default for fp16 / bf16 X) against exact arithmetic and
-the fp32-MFMA kernel.
+"""The split-operand Hessian kernels (the default for fp16, bf16 and fp32 X) against exact
+arithmetic and the fp32-MFMA kernel.
 
 The reference forms H = X^T (s * X) in fp32 (gptq_plus_utils.py:842-847): each product is
 x * fl32(x * s).  The exact value of that sum is computed here in float64 (each product of an
@@ -140,3 +140,82 @@ def test_multi_target_split_equals_separate():
         iu = torch.triu_indices(C, C)
         assert rel_fro(_upper(Hm[t], iu), _upper(H, iu)) <= 1e-6
         assert torch.equal(am[t], a)
+
+
+@pytest.mark.parametrize("n,C,G", [(4096, 512, 2), (2048, 1000, 3), (33, 385, 1), (5, 130, 2), (300, 17, 1)])
+def test_split_fp32_x_matches_exact_sum(n, C, G):
+    """fp32 X on the split path: x as two fp16 pieces (22 of its 24 bits) against the in-kernel
+    two-piece w, three MFMAs per product (each product within ~2^-20.5 relative of the
+    reference's).  The exact sums are still exact in float64 (24 x 24-bit products).  Bars:
+    rel-Frobenius <= 1e-6 like the other split modes, and act_square equal to the fp32 kernel's
+    bit for bit (both reproduce the reference's CPU summation order)."""
+    r = rng(3000 + n + C + G)
+    X = r.standard_normal((n, C), dtype=np.float32)
+    X[:, r.choice(C, min(8, C), replace=False)] *= 20.0
+    x = torch.from_numpy(X)
+    sal = torch.from_numpy(np.minimum(r.lognormal(size=(n, G)), 10.0).astype(np.float32))
+    ref, act_ref = _exact(x, sal)
+    Hs, acts, iu = _run(x, sal, "split16")
+    Hf, actf, _ = _run(x, sal, "fp32")
+    es = rel_fro(_upper(Hs, iu), _upper(ref, iu))
+    ef = rel_fro(_upper(Hf, iu), _upper(ref, iu))
+    print(f"fp32 X n={n} C={C} G={G}: rel err split {es:.3e}  fp32 {ef:.3e}")
+    assert es <= 1e-6 and ef <= 1e-6
+    assert torch.equal(acts, actf) and rel_fro(acts, act_ref) <= 1e-6
+
+
+def test_split_fp32_x_wide_dynamic_range():
+    """fp32 columns from 1e-15 to 1e15 and saliencies from 1e-3 to 1e3: the per-column
+    exponents of the row pieces and of w keep every entry at fp32 accuracy (normalised by
+    sqrt(|H_ii H_jj|), as for the 16-bit inputs)."""
+    r = rng(78)
+    n, C, G = 2048, 384, 2
+    mags = np.logspace(-15, 15, C).astype(np.float32)
+    r.shuffle(mags)
+    x = torch.from_numpy(r.standard_normal((n, C)).astype(np.float32) * mags)
+    sal = torch.from_numpy(np.exp(r.uniform(np.log(1e-3), np.log(1e3), size=(n, G))).astype(np.float32))
+    ref, _ = _exact(x, sal)
+    Hs, _, iu = _run(x, sal, "split16")
+    Hf, _, _ = _run(x, sal, "fp32")
+    d = torch.sqrt(torch.diagonal(ref, dim1=1, dim2=2).abs())
+    norm = d[:, :, None] * d[:, None, :]
+    es = float(((Hs.double() - ref).abs() / norm)[:, iu[0], iu[1]].max())
+    ef = float(((Hf.double() - ref).abs() / norm)[:, iu[0], iu[1]].max())
+    print(f"fp32 X wide range: max normalised entry error split {es:.3e}  fp32 {ef:.3e}")
+    assert es <= 1e-5 and ef <= 1e-5
+
+
+def test_split_fp32_x_deterministic_nonfinite_and_multi_target():
+    """Bitwise reproducible (C = 1000, G = 3 runs as token slices); an inf input gives
+    non-finite entries in the same places as the fp32 kernel; the multi-target launch agrees
+    with separate calls."""
+    r = rng(91)
+    n, C, G = 4096, 1000, 3
+    x = torch.from_numpy(r.standard_normal((n, C), dtype=np.float32))
+    sal = torch.from_numpy(r.lognormal(size=(n, G)).astype(np.float32))
+    a = _run(x, sal, "split16")
+    b = _run(x, sal, "split16")
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    X = r.standard_normal((256, 300), dtype=np.float32)
+    X[17, 5] = np.inf
+    X[200, 250] = -np.inf
+    xi = torch.from_numpy(X)
+    si = torch.from_numpy(r.lognormal(size=(256, 1)).astype(np.float32))
+    Hs, _, iu = _run(xi, si, "split16")
+    Hf, _, _ = _run(xi, si, "fp32")
+    bs, bf = ~torch.isfinite(_upper(Hs, iu)), ~torch.isfinite(_upper(Hf, iu))
+    assert bf.any() and torch.equal(bs, bf)
+    assert rel_fro(_upper(Hs, iu)[~bf], _upper(Hf, iu)[~bf]) <= 1e-6
+    xd = x[:1024, :640].contiguous().to(DEV)
+    sals = [torch.from_numpy(r.lognormal(size=(1024, 2)).astype(np.float32)).to(DEV) for _ in range(3)]
+    Hm = [torch.zeros(2, 640, 640, device=DEV) for _ in range(3)]
+    am = [torch.zeros(640, device=DEV) for _ in range(3)]
+    K.hessian_accum_multi(xd, sals, Hm, am)
+    for t in range(3):
+        H = torch.zeros(2, 640, 640, device=DEV)
+        ac = torch.zeros(640, device=DEV)
+        K.hessian_accum(xd, sals[t], H, ac)
+        torch.cuda.synchronize()
+        iu2 = torch.triu_indices(640, 640)
+        # (another target count splits the tail into other token slices: fp32 sums in another order)
+        assert rel_fro(_upper(Hm[t], iu2), _upper(H, iu2)) <= 1e-6 and torch.equal(am[t], ac)

@@ -36,7 +36,7 @@ def test_argument_validation_needs_no_device():
     lib = _lib()
     null = ctypes.c_void_p(0)
     assert lib.rq_hessian_accum(null, 0, 10, 8, 8, null, 1, 1, null, null, null, 0, null) == nat.RQ_EINVAL
-    assert lib.rq_hessian_workspace_bytes(10, 0, 1) < 0
+    assert lib.rq_hessian_workspace_bytes(10, 0, 1, nat.RQ_F16) < 0
     assert lib.rq_find_params(null, 0, 4, 4, 4, -1, 7, 1, 1, null, null, null) == nat.RQ_EINVAL
     assert lib.rq_act_order_perm(null, 4, null, null, null) == nat.RQ_EINVAL
     damp = (ctypes.c_double * 1)(0.01)

@@ -4,8 +4,8 @@ workspace is the library's per-GPU scratch array), through the C ABI against rq_
 - given a workspace of the scratch's size, rq_hessian_accum makes the same kernel choices, so
   H and act_square must be equal bit for bit;
 - against rq_hessian_accum with its full workspace (which may also split the last round of
-  tiles along the tokens) H must agree to rel. Frobenius 1e-5 (the suite's bar for H) and
-  act_square exactly;
+  tiles along the tokens, or pick another kernel) H's upper triangle must agree to rel.
+  Frobenius 1e-5 (the suite's bar for H) and act_square exactly;
 - two calls in a row on different shapes (the second smaller), each accumulated over two
   chunks, and fp16 / bf16 / fp32 inputs;
 - a chunk needing more than RQ_NOALLOC_SCRATCH_BYTES is refused with RQ_EINVAL before any
@@ -42,7 +42,8 @@ def _run(x, s, mode, ws_bytes=None):
         if mode == "noalloc":
             rc = lib.rq_hessian_accum_noalloc(*args, nat.stream_of(DEV))
         else:
-            need = int(lib.rq_hessian_workspace_bytes(ntok, C, G)) if ws_bytes is None else ws_bytes
+            need = int(lib.rq_hessian_workspace_bytes(ntok, C, G, nat.dtype_code(xk.dtype))) if ws_bytes is None \
+                else ws_bytes
             ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
             rc = lib.rq_hessian_accum(*args, nat.ptr(ws), need, nat.stream_of(DEV))
         assert rc == nat.RQ_OK, (mode, rc)
@@ -60,7 +61,12 @@ def test_noalloc_matches_workspace_entry(dtype):
         assert torch.equal(H_n, H_w) and torch.equal(a_n, a_w)
         H_f, a_f = _run(x, s, "workspace")
         assert torch.equal(a_n, a_f)
-        err = float((H_n.double() - H_f.double()).norm() / H_f.double().norm())
+        # the upper triangle (what rq_hessian_accum defines; finalize mirrors it): the two
+        # workspaces may choose different kernels (fp32 X: the split kernel needs more than the
+        # scratch at the first shape), whose lower triangles hold different partial values
+        iu = torch.triu_indices(C, C, device=DEV)
+        Hn_u, Hf_u = H_n[:, iu[0], iu[1]].double(), H_f[:, iu[0], iu[1]].double()
+        err = float((Hn_u - Hf_u).norm() / Hf_u.norm())
         assert err <= 1e-5, err
 
 
