@@ -34,7 +34,11 @@ __global__ __launch_bounds__(256) void k_row_scale_flag(float* __restrict__ Z, i
       *z = v;
       any |= (v != 0.0f) | (v != v);
     }
-    if (__any(any) && (threadIdx.x & 63) == 0) atomicOr(nz + r / R_s, 1);
+    // one atomic per wave only while the flag is still clear (its L2 copy is read first):
+    // nearly every row is non-zero, and atomics of all waves on the few flag words serialise
+    if (__any(any) && (threadIdx.x & 63) == 0 &&
+        __hip_atomic_load(nz + r / R_s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
+      atomicOr(nz + r / R_s, 1);
   }
 }
 
