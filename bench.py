@@ -521,6 +521,34 @@ def stats_table(path, cfg, units, config):
         print(f"| `{name}` | {calls} | {tot:.2f} | {per:.3f} | {avg:.1f} | {pct:.2f} | {wtxt} | {ach} |")
 
 
+def counters_table(path, top=16):
+    """Markdown table of a rocprofv3 --pmc CSV (one row per dispatch and counter), per kernel:
+    MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * 128) (the SQ counter sums the
+    1024 SIMDs, GRBM_GUI_ACTIVE the 8 XCDs' busy cycles: busy SIMD-cycles over SIMD-cycles),
+    VALU and LDS instructions per MFMA, LDS bank-conflict cycles per LDS instruction."""
+    agg, disp, dur = {}, {}, {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            k = _kernel_name(r["Kernel_Name"])
+            agg.setdefault(k, {}).setdefault(r["Counter_Name"], 0.0)
+            agg[k][r["Counter_Name"]] += float(r["Counter_Value"])
+            if (k, r["Dispatch_Id"]) not in disp:
+                disp[(k, r["Dispatch_Id"])] = 1
+                dur[k] = dur.get(k, 0.0) + (float(r["End_Timestamp"]) - float(r["Start_Timestamp"])) / 1e3
+    rows = sorted(agg.items(), key=lambda kv: -dur.get(kv[0], 0.0))
+    print("| kernel | dispatches | time (ms) | MFMA busy | VALU / MFMA | LDS / MFMA | LDS conflict cycles / LDS |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    for k, c in rows[:top]:
+        n = sum(1 for (kk, _d) in disp if kk == k)
+        busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / max(c.get("GRBM_GUI_ACTIVE", 0.0) * 128, 1.0)
+        mf = c.get("SQ_INSTS_MFMA", 0.0)
+        per_mfma = lambda key: f"{c.get(key, 0.0) / mf:.2f}" if mf else "-"
+        lds = c.get("SQ_INSTS_LDS", 0.0)
+        conf = f"{c.get('SQ_LDS_BANK_CONFLICT', 0.0) / lds:.2f}" if lds else "-"
+        print(f"| `{k}` | {n} | {dur.get(k, 0.0) / 1e3:.2f} | {100 * busy:.1f} % | {per_mfma('SQ_INSTS_VALU')} | "
+              f"{per_mfma('SQ_INSTS_LDS')} | {conf} |")
+
+
 def traffic_report(fetch_csv, write_csv, cal_fetch_csv, cal_write_csv, kernel_prefix, config, cfg, math):
     """HBM bytes per product-kernel launch from FETCH_SIZE / WRITE_SIZE passes (KiB per dispatch),
     each scaled by what the counter reads for a 1 GiB device copy; written to TRAFFIC_JSON with
@@ -639,11 +667,15 @@ def main():
     ap.add_argument("--gemm-calibration", action="store_true", help="only time torch.matmul in fp16 / fp32 / fp64")
     ap.add_argument("--stats-table", metavar="STATS_CSV", help="print a rocprofv3 kernel-stats CSV as a table")
     ap.add_argument("--units", type=float, default=1.0, help="with --stats-table: units (linears or layers) profiled")
+    ap.add_argument("--counters-table", metavar="PMC_CSV", help="print a rocprofv3 --pmc CSV as a per-kernel table")
     ap.add_argument("--traffic", nargs=4, metavar=("FETCH", "WRITE", "CAL_FETCH", "CAL_WRITE"),
                     help="counter CSVs of the product kernel and of the copy calibration -> profiles/hessian_traffic.json")
     args = ap.parse_args()
     if args.stats_table:
         stats_table(args.stats_table, CONFIGS[args.config], args.units, args.config)
+        return
+    if args.counters_table:
+        counters_table(args.counters_table)
         return
     if args.traffic:
         cfg = CONFIGS[args.config]
