@@ -21,7 +21,6 @@
 namespace {
 
 constexpr int NB = 64;     // diagonal block (factored and inverted by one workgroup)
-constexpr int CG = 4;      // columns factored per barrier in the diagonal block
 // Outer panel width: 256, or 512 from C = 8192 on.  The panel update re-reads and re-writes
 // its output tile once per panel, so wider panels halve that epilogue's share; the extra
 // in-panel work (C^2 NBW / 2 flops) stays ~1 % of the C^3 chain there.
@@ -81,199 +80,279 @@ __global__ __launch_bounds__(256) void k_reverse_to_f64(const float* __restrict_
   }
 }
 
-// 1/sqrt(d) and sqrt(d) in fp64 from the hardware estimate and two Newton steps
-// y <- y (3 - d y^2) / 2 (the error squares each step: well below fp64 rounding after two).
+// 1/sqrt(d) and sqrt(d) in fp64 from the hardware estimate (relative error 2^-24 on gfx950,
+// measured over 2^20 random inputs) and one Newton step y <- y (3 - d y^2) / 2, which squares
+// the error: 2^-47.8 measured, far below what the fp32 input and output resolve.
 __device__ __forceinline__ void rsqrt_newton(double d, double& rs, double& sq) {
   double y = __builtin_amdgcn_rsq(d);
   const double h = 0.5 * d;
-  y = y * __builtin_fma(-h * y, y, 1.5);
   y = y * __builtin_fma(-h * y, y, 1.5);
   rs = y;
   sq = d * y;
 }
 
-__device__ __forceinline__ double readlane_f64(double v, int lane) {
-  const uint64_t u = (uint64_t)__double_as_longlong(v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
-  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-}
-
-// Sum of a double over the 4 lanes of a quad (DPP quad_perm moves, no LDS).
-template <int CTRL>
-__device__ __forceinline__ double quad_mov_f64(double v) {
-  const uint64_t u = (uint64_t)__double_as_longlong(v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
-  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-}
-__device__ __forceinline__ double quad_sum_f64(double v) {
-  v = v + quad_mov_f64<0xB1>(v);   // lanes [1, 0, 3, 2]
-  return v + quad_mov_f64<0x4E>(v);   // lanes [2, 3, 0, 1]
-}
-
 // Factor the nb x nb diagonal block of A at (k, k) and invert it; one workgroup of 4 waves per
-// batch entry (rows >= nb are identity padding).
-//  - Factor: lane r of wave w holds L[r][16w .. 16w+15] (16 registers).  Columns go in groups
-//    of CG = 4, all held by one wave.  For each column j of the group that wave takes the pivot
-//    from lane j (readlane), forms 1/sqrt and sqrt, scales its column (L[r][j], zero for
-//    r <= j) and subtracts L[r][j] L[l][j] from the group's later columns l itself (L[l][j] by
-//    readlane); then it publishes the group's columns in `col` (two buffers, alternating by
-//    group, so one barrier per group orders each write after the previous reads), and every
-//    wave subtracts L[r][j] L[l][j], j in the group in order, from its other columns l (col is
-//    zero at l <= j, so finished columns stay as they are).  Every entry sees the same fused
-//    multiply-adds in the same order as with one column per barrier.
-//  - Inverse: lane quad c of the workgroup computes column c of T = L^-1 by forward
-//    substitution t[i] = (delta_ic - sum_{m<i} L[i][m] t[m]) / L[i][i]; lane q of the quad
-//    holds the rows m = 4p + q and its part of each dot product, and the quad adds the four
-//    parts with DPP moves.  L is staged in LDS column-interleaved (element (i, 4p + q) at
-//    i * LS + 16 q + p), so a lane reads its operands of a row in 16-byte pieces, and the
-//    lanes of one q in a wave all read the same address (broadcast).
+// batch entry (rows >= nb are identity padding).  Blocked by 16, in LDS:
+//   for b = 0..3:  D = A_bb:  L_bb = chol(D) and T_bb = L_bb^-1            (16 x 16, in-wave)
+//                  L_ib = A_ib T_bb^T (i > b),  X_b = T_bb B_b[:, 0:16b]   (MFMA)
+//                  A_ij -= L_ib L_jb^T (b < j <= i),  B_i[:, 0:16b+16] -= L_ib X_b  (i > b)
+// with B = I at the start; row block b of B becomes X_b, row block b of T = L^-1 (its diagonal
+// block T_bb).  The block products are 16 x 16 x 16 on v_mfma_f64_16x16x4f64, spread over the 4
+// waves, two barriers per block column.
+//  - The 16 x 16 factorisation runs in every wave on the same LDS data (no barrier; the waves
+//    reach the same verdict on the pivots).  Lane 4r + q holds D[r][4q .. 4q+3] and the same
+//    entries of the running inverse W (= I at the start).  Columns go in groups of 4: the
+//    lanes of the group's rows publish those rows of D and W in a per-wave LDS buffer (one
+//    wave's LDS accesses complete in order); every lane factors the 4 x 4 pivot block
+//    (L_P, with 1/sqrt of each pivot), solves for the L entries of its own row and of its 4
+//    columns in the group (D is symmetric, so the published rows are also the columns), forms
+//    the group's rows of T, X = L_P^-1 W_group, and rows below the group subtract their rank-4
+//    products from D and W.  After 4 groups W = T_bb.
 // Writes T (lower, exact zeros above) to Tbuf and to Linv's diagonal block.
 constexpr int CD_THREADS = 256;
+constexpr int DLS = NB + 2;                 // LDS row stride of the block and of B (doubles)
+constexpr int OPS = 17;                     // row stride of a wave's T_bb operand copy
+
+__device__ __forceinline__ doublex4 mfma_f64(double a, double b, doublex4 c) {
+  return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
 __global__ __launch_bounds__(CD_THREADS) void k_chol_diag(const double* __restrict__ A, int C, int k,
                                                           int nb, double* __restrict__ Tbuf,
                                                           double* __restrict__ Linv, int64_t ws,
                                                           int* info_all) {
-  constexpr int LS = NB + 2;                        // LDS row stride (16-byte aligned rows)
-  __shared__ __attribute__((aligned(16))) double S[NB * LS];
-  __shared__ __attribute__((aligned(16))) double col[2][CG][NB];
-  __shared__ double dinv[NB];   // 1 / L[j][j]; NaN marks a failed pivot
+  __shared__ __attribute__((aligned(16))) double Am[NB * DLS];
+  __shared__ __attribute__((aligned(16))) double Bm[NB * DLS];
+  __shared__ __attribute__((aligned(16))) double pub[4][4 * 32];
+  __shared__ __attribute__((aligned(16))) double opnd[4][16 * OPS];
   const int b = blockIdx.x;
   int* info = info_all + b;
-  if (*info) return;
+  const int skip = *info;             // tested after the block's loads are issued
   A += b * ws;
   Tbuf += b * ws;
   Linv += b * ws;
   const int tid = threadIdx.x;
-  const int r = tid & 63;
+  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // columns 16 wave .. 16 wave + 15 of row r of the block's lower triangle (zeros above,
-  // identity on the padding rows).  Only rows < nb and columns < nb are read: a ragged last
-  // block reads with a clamped column index, and the mask clears those columns (they lie
-  // above the diagonal of every row that is read).  A full block with C even (k is a
-  // multiple of NB) has 16-byte aligned rows.
-  const int c0 = 16 * wave;
-  double a[16];
-  if (r < nb) {
-    const double* rowp = A + (int64_t)(k + r) * C + k + c0;
-    if (nb == NB && (C & 1) == 0) {
-      const double2* row = reinterpret_cast<const double2*>(rowp);
+  // The block, symmetric, from its lower triangle (only rows and columns < nb are read; the
+  // padding is the identity), and B = I.  A wave reads two whole rows per instruction: thread
+  // t, step q takes the column pair 2 (t % 32) of row (t + 256 q) / 32 (16-byte loads when the
+  // rows are aligned and whole, else clamped column indices); all loads go out before the
+  // LDS writes.
+  {
+    double2 v[8];
+    const bool vec = (nb == NB) && (C & 1) == 0;
 #pragma unroll
-      for (int q = 0; q < 16; q += 2) {
-        const double2 v = row[q / 2];
-        a[q] = v.x;
-        a[q + 1] = v.y;
+    for (int q = 0; q < 8; ++q) {
+      const int e = tid + 256 * q, r = e >> 5, c = 2 * (e & 31);
+      const double* rowp = A + (int64_t)(k + min(r, nb - 1)) * C + k;
+      if (vec) {
+        v[q] = *reinterpret_cast<const double2*>(rowp + c);
+      } else {
+        v[q].x = rowp[min(c, nb - 1)];
+        v[q].y = rowp[min(c + 1, nb - 1)];
       }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 16; ++q) a[q] = A[(int64_t)(k + r) * C + k + min(c0 + q, nb - 1)];
     }
+    if (skip) return;
 #pragma unroll
-    for (int q = 0; q < 16; ++q)
-      if (c0 + q > r) a[q] = 0.0;
-  } else {
+    for (int q = 0; q < 8; ++q) {
+      const int e = tid + 256 * q, r = e >> 5, c = 2 * (e & 31);
 #pragma unroll
-    for (int q = 0; q < 16; ++q) a[q] = (c0 + q == r) ? 1.0 : 0.0;
+      for (int h = 0; h < 2; ++h) {
+        const int cc = c + h;
+        Bm[r * DLS + cc] = (r == cc) ? 1.0 : 0.0;
+        if (cc <= r) {
+          const double x = (r < nb) ? (h ? v[q].y : v[q].x) : ((r == cc) ? 1.0 : 0.0);
+          Am[r * DLS + cc] = x;
+          Am[cc * DLS + r] = x;
+        }
+      }
+    }
   }
   __syncthreads();
 
-  bool fail = false;
+  const int fr = lane >> 2, fq = lane & 3;      // in-wave 16 x 16 layout: row fr, columns 4 fq ..
+  const int mi = lane & 15, mk = lane >> 4;     // MFMA operand: row / column mi, k mk
+  double* pw = pub[wave];
+  double* ow = opnd[wave];
+  bool bad = false;
+  for (int bb = 0; bb < 4; ++bb) {
+    const int o = 16 * bb;
+    // (1) L_bb and T_bb = W, in every wave
+    double d[4], w[4];
 #pragma unroll
-  for (int g = 0; g < NB / CG; ++g) {
-    const int j0 = CG * g, jw = j0 / 16, jq0 = j0 % 16;
-    double (*cg)[NB] = col[g & 1];
-    if (wave == jw) {
+    for (int i = 0; i < 4; ++i) {
+      d[i] = Am[(o + fr) * DLS + o + 4 * fq + i];
+      w[i] = (fr == 4 * fq + i) ? 1.0 : 0.0;
+    }
 #pragma unroll
-      for (int u = 0; u < CG; ++u) {
-        const int j = j0 + u, jq = jq0 + u;
-        const double d = readlane_f64(a[jq], j);     // uniform pivot
-        double rd = 0.0, sq = 0.0;
-        const bool ok = d > 0.0 && rq_isfinite(d);
-        if (ok) rsqrt_newton(d, rd, sq);
-        const double lrj = (r > j) ? a[jq] * rd : 0.0;  // L[r][j]
-        a[jq] = (r == j) ? sq : lrj;
-        cg[u][r] = lrj;
-        if (r == 0) dinv[j] = ok ? rd : __builtin_nan("");
+    for (int g = 0; g < 4; ++g) {
+      // columns j0 .. j0+3: the group's 4 rows of D and W are published, every lane factors
+      // the 4 x 4 pivot block P, forms the L entries of its row and of its columns in the
+      // group, the group's rows of T (X = L_P^-1 W_group) and applies the rank-4 updates
+      const int j0 = 4 * g, own = fr - j0;
+      if (own >= 0 && own < 4) {
 #pragma unroll
-        for (int v = u + 1; v < CG; ++v)                  // the group's later columns
-          a[jq0 + v] = __builtin_fma(-lrj, readlane_f64(lrj, j0 + v), a[jq0 + v]);
+        for (int i = 0; i < 4; ++i) {
+          pw[own * 32 + 4 * fq + i] = d[i];
+          pw[own * 32 + 16 + 4 * fq + i] = w[i];
+        }
+      }
+      // lanes read what other lanes wrote: keep the compiler from moving the reads above the
+      // writes (the hardware runs a wave's LDS accesses in order)
+      __builtin_amdgcn_wave_barrier();
+      double P[4][4], u[4][4], wv[4][4], ur[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          P[m][i] = pw[m * 32 + j0 + i];
+          u[m][i] = pw[m * 32 + 4 * fq + i];
+          wv[m][i] = pw[m * 32 + 16 + 4 * fq + i];
+        }
+        ur[m] = pw[m * 32 + fr];
+      }
+      __builtin_amdgcn_wave_barrier();   // the next group's writes stay after these reads
+      double Lp[4][4], rs[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        double dm = P[m][m];
+#pragma unroll
+        for (int q = 0; q < m; ++q) dm = __builtin_fma(-Lp[m][q], Lp[m][q], dm);
+        const bool ok = dm > 0.0 && rq_isfinite(dm);
+        bad |= !ok;
+        double r1, sq;
+        rsqrt_newton(ok ? dm : 1.0, r1, sq);    // no branch: a failed pivot ends the block anyway
+        rs[m] = r1;
+        Lp[m][m] = sq;
+#pragma unroll
+        for (int m2 = m + 1; m2 < 4; ++m2) {
+          double v = P[m2][m];
+#pragma unroll
+          for (int q = 0; q < m; ++q) v = __builtin_fma(-Lp[m2][q], Lp[m][q], v);
+          Lp[m2][m] = v * rs[m];
+        }
+      }
+      double lr[4], lc[4][4], X[4][4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        double v = ur[m];
+#pragma unroll
+        for (int q = 0; q < m; ++q) v = __builtin_fma(-lr[q], Lp[m][q], v);
+        lr[m] = v * rs[m];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          double c = u[m][i], x = wv[m][i];
+#pragma unroll
+          for (int q = 0; q < m; ++q) {
+            c = __builtin_fma(-lc[i][q], Lp[m][q], c);
+            x = __builtin_fma(-Lp[m][q], X[q][i], x);
+          }
+          lc[i][m] = c * rs[m];
+          X[m][i] = x * rs[m];
+        }
+      }
+      const bool below = fr >= j0 + 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        double nd = d[i], nw = w[i];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          nd = __builtin_fma(-lr[m], lc[i][m], nd);
+          nw = __builtin_fma(-lr[m], X[m][i], nw);
+        }
+        double wn = below ? nw : w[i];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) wn = (own == m) ? X[m][i] : wn;
+        d[i] = below ? nd : d[i];
+        w[i] = wn;
+      }
+    }
+    if (bad) break;                            // the same in every wave
+    // (2) T_bb as an MFMA operand (element [mi][4 kk + mk]), this wave's copy
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ow[fr * OPS + 4 * fq + i] = w[i];
+    __builtin_amdgcn_wave_barrier();
+    double top[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) top[kk] = ow[mi * OPS + 4 * kk + mk];
+    if (wave == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Bm[(o + fr) * DLS + o + 4 * fq + i] = w[i];
+    } else {
+      // three tasks per block column: L_ib = A_ib T_bb^T for i = bb+1 .. 3, then
+      // X_b[:, 16m ..] = T_bb B_b[:, 16m ..] for m = 0 .. bb-1 (both in place)
+      const int t = wave - 1;
+      doublex4 acc = {0.0, 0.0, 0.0, 0.0};
+      if (t < 3 - bb) {
+        const int i0 = 16 * (bb + 1 + t);
+        double av[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) av[kk] = Am[(i0 + mi) * DLS + o + 4 * kk + mk];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) acc = mfma_f64(av[kk], top[kk], acc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Am[(i0 + mk + 4 * e) * DLS + o + mi] = acc[e];
+      } else {
+        const int m0 = 16 * (t - (3 - bb));
+        double bv[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) bv[kk] = Bm[(o + 4 * kk + mk) * DLS + m0 + mi];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) acc = mfma_f64(top[kk], bv[kk], acc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Bm[(o + mk + 4 * e) * DLS + m0 + mi] = acc[e];
       }
     }
     __syncthreads();
-    // dinv[j] is written once, before this barrier: every wave reads the same verdict.  The
-    // columns are read before the verdict is tested (the reads are in bounds either way).
-    bool bad = false;
-    double m[CG], cv[CG][16];
-#pragma unroll
-    for (int u = 0; u < CG; ++u) {
-      const double dj = dinv[j0 + u];
-      bad |= !(dj == dj);
-      m[u] = cg[u][r];
-#pragma unroll
-      for (int q = 0; q < 16; ++q) cv[u][q] = cg[u][c0 + q];
-    }
-    if (bad) {
-      fail = true;
-      break;
-    }
-    // q-major, so the next group's columns are done first; the group's own columns were
-    // updated by their wave above
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const bool own = (q >= jq0 && q < jq0 + CG) && wave == jw;
-#pragma unroll
-      for (int u = 0; u < CG; ++u) {
-        const double nv = __builtin_fma(-m[u], cv[u][q], a[q]);
-        a[q] = own ? a[q] : nv;
+    if (bb == 3) break;
+    // (3) trailing blocks: A_ij (b < j <= i, the next diagonal block first), then B_i[:, m]
+    const int nA = (3 - bb) * (4 - bb) / 2, nT = nA + (3 - bb) * (bb + 1);
+    for (int t = wave; t < nT; t += 4) {
+      int bi, bj;
+      bool isA = t < nA;
+      if (isA) {           // j = bb+1 .. 3, i = j .. 3, column by column
+        int u = t;
+        bj = bb + 1;
+        while (u >= 4 - bj) {
+          u -= 4 - bj;
+          ++bj;
+        }
+        bi = bj + u;
+      } else {             // i = bb+1 .. 3, m = 0 .. bb
+        const int u = t - nA;
+        bi = bb + 1 + u / (bb + 1);
+        bj = u % (bb + 1);
       }
+      double* Cm = isA ? Am : Bm;
+      doublex4 acc;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = Cm[(16 * bi + mk + 4 * e) * DLS + 16 * bj + mi];
+      double av[4], bv[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        av[kk] = -Am[(16 * bi + mi) * DLS + o + 4 * kk + mk];
+        bv[kk] = isA ? Am[(16 * bj + mi) * DLS + o + 4 * kk + mk] : Bm[(o + 4 * kk + mk) * DLS + 16 * bj + mi];
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc = mfma_f64(av[kk], bv[kk], acc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Cm[(16 * bi + mk + 4 * e) * DLS + 16 * bj + mi] = acc[e];
     }
+    __syncthreads();
   }
-  if (fail) {
+  if (bad) {
     if (tid == 0) atomicExch(info, 1);
     return;
   }
-  // L into LDS, column-interleaved; entries above the diagonal are zero
+  // T = B (lower; zeros above), one whole row per wave and instruction
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
-    const int c = c0 + q;
-    S[r * LS + 16 * (c & 3) + (c >> 2)] = (c <= r) ? a[q] : 0.0;
-  }
-  __syncthreads();
-
-  const int cc = tid >> 2, qq = tid & 3;
-  const double* Sq = S + 16 * qq;
-  double t[16];
-#pragma unroll
-  for (int p = 0; p < 16; ++p) t[p] = 0.0;
-#pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    // rows m = 4p + qq < i; L[i][m] = 0 for m >= i, so p runs to (i - 1) / 4 for every lane
-    double part = 0.0;
-    if (i > 0) {
-      const int np = (i - 1) / 4 + 1;
-      double s2[2] = {0.0, 0.0};
-#pragma unroll
-      for (int p = 0; p < np; p += 2) {
-        const double2 l = *reinterpret_cast<const double2*>(Sq + i * LS + p);
-        s2[0] = __builtin_fma(l.x, t[p], s2[0]);
-        if (p + 1 < np) s2[1] = __builtin_fma(l.y, t[p + 1], s2[1]);
-      }
-      part = s2[0] + s2[1];
-    }
-    const double di = dinv[i];
-    const double tot = quad_sum_f64(part);
-    const double ti = (((i == cc) ? 1.0 : 0.0) - tot) * di;
-    t[i >> 2] = ((i & 3) == qq) ? ti : t[i >> 2];   // a select, not a branch
-  }
-  // t[p] = T[4p + qq][cc]
-#pragma unroll
-  for (int p = 0; p < 16; ++p) Tbuf[(4 * p + qq) * NB + cc] = t[p];
-  if (cc < nb) {
-#pragma unroll
-    for (int p = 0; p < 16; ++p)
-      if (4 * p + qq < nb) Linv[(int64_t)(k + 4 * p + qq) * C + (k + cc)] = t[p];
+    const int e = tid + 256 * q, r = e >> 6, c = e & 63;
+    const double v = Bm[r * DLS + c];
+    Tbuf[e] = v;
+    if (r < nb && c < nb) Linv[(int64_t)(k + r) * C + (k + c)] = v;
   }
 }
 
@@ -471,7 +550,7 @@ struct PanelTile {
   template <int CUR, int FILL>
   __device__ __forceinline__ void step(const PStages& L, int kt) {
     PWAIT_VM(2 * (PSTAGES - 2));
-    __builtin_amdgcn_s_barrier();
+    RQ_STAGE_BARRIER();
     stage(L.s[FILL], min(kt + PSTAGES - 1, nk - 1));
     if (!live) return;
     const uint8_t* st = L.s[CUR];
@@ -726,16 +805,17 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
   // one rank-NBW update per panel, so the big updates read and write the trailing matrix
   // NBW / NB times less often.
   const int NBW = panel_width(C);
-  for (int k = 0; k < C; k += NBW) {
-    const int kw = (C - k < NBW) ? (C - k) : NBW;
-    const int pe = k + kw;                               // panel end
+  int rc;
+  // The factorisation of one panel: per NB block the diagonal factor and inverse, the block
+  // column of L and row block of L^-1, and the update of the panel's later columns.
+  auto factor_panel = [&](int k, int pe) -> int {
     for (int j = k; j < pe; j += NB) {
       const int jb = (pe - j < NB) ? (pe - j) : NB;
       const int below = C - j - jb;                      // rows below this block (whole matrix)
       const int pend = pe - j - jb;                      // panel columns right of this block
       hipLaunchKernelGGL(k_chol_diag, dim3(nb), dim3(CD_THREADS), 0, s, A, C, j, jb, Tbuf, Linv, ws, info);
       RQ_CHECK_LAUNCH();
-      int rc;
+      int r;
       // one launch: L_ij = A_ij T^T (in place, every row below the block) and
       // X_j[:, 0:j] = T B_j[:, 0:j] (in place, row block j of L^-1)
       GemmArgs<double> lij = batched(gemm_args<double>(A + (int64_t)(j + jb) * C + j, C, Tbuf, NB,
@@ -743,7 +823,7 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
                                                        1.0, EPI_STORE));
       GemmArgs<double> xj = batched(gemm_args<double>(Tbuf, NB, Linv + (int64_t)j * C, C,
                                                       Linv + (int64_t)j * C, C, jb, j, jb, 1.0, EPI_STORE));
-      if ((rc = launch_gemm_pair(lij, xj, s, nb))) return rc;
+      if ((r = launch_gemm_pair(lij, xj, s, nb))) return r;
       // one launch, inside the panel: A[j+jb:, j+jb:pe] -= L[j+jb:, j] L[j+jb:pe, j]^T (lower
       // tiles) and the panel rows of L^-1: B[j+jb:pe, 0:j+jb] -= L[j+jb:pe, j] X_j.  On the
       // 128-tile panel kernel with 512-wide panels (up to 448 columns); the narrower updates of
@@ -762,27 +842,68 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
                                                        Linv + (int64_t)j * C, C,
                                                        Linv + (int64_t)(j + jb) * C, C, pend, j + jb,
                                                        jb, -1.0, EPI_ACCUM));
-        if ((rc = launch_gemm_pair(h, g, s, nb))) return rc;
+        if ((r = launch_gemm_pair(h, g, s, nb))) return r;
       }
     }
-    const int rest = C - pe;
-    // one launch: the trailing matrix A[pe:, pe:] -= L[pe:, k:pe] L[pe:, k:pe]^T (lower tiles,
-    // K = kw) and the rows of L^-1 below the panel: B[pe:, 0:pe] -= L[pe:, k:pe] X[k:pe, 0:pe]
-    if (rest > 0 && launch_panel(A + (int64_t)pe * C + k, Linv + (int64_t)k * C, A + (int64_t)pe * C + pe,
-                                 Linv + (int64_t)pe * C, C, kw, rest, rest, rest, pe, ws, info, nb, s)) {
+    return RQ_OK;
+  };
+  // The update by panel [k, k + kw) of the trailing rows r0 ..: A[r0:r0+ms, r0:r0+ns] -=
+  // L[r0:, k:k+kw] L[r0:, k:k+kw]^T (lower tiles) and B[r0:r0+mr, 0:nr] -= L[r0:r0+mr, k:k+kw]
+  // X[k:k+kw, 0:nr], on the 128-tile panel kernel, or on the 64-tile GEMM when `small` (fewer,
+  // shorter tiles: lower latency) or when the panel kernel does not take the shape.
+  auto trailing = [&](int k, int kw, int r0, int ms, int ns, int mr, int nr, hipStream_t st, bool small) -> int {
+    if (!small && launch_panel(A + (int64_t)r0 * C + k, Linv + (int64_t)k * C, A + (int64_t)r0 * C + r0,
+                               Linv + (int64_t)r0 * C, C, kw, ms, ns, mr, nr, ws, info, nb, st)) {
       RQ_CHECK_LAUNCH();
-    } else if (rest > 0) {
-      // the same two updates on the 64-tile GEMM (odd C, or a panel width not a multiple of 8)
-      GemmArgs<double> h = batched(gemm_args<double>(A + (int64_t)pe * C + k, C, A + (int64_t)pe * C + k,
-                                                     C, A + (int64_t)pe * C + pe, C, rest, rest, kw,
-                                                     -1.0, EPI_ACCUM));
-      h.lower_only = 1;
-      GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)pe * C + k, C, Linv + (int64_t)k * C,
-                                                     C, Linv + (int64_t)pe * C, C, rest, pe, kw, -1.0,
-                                                     EPI_ACCUM));
-      int rc;
-      if ((rc = launch_gemm_pair(h, g, s, nb))) return rc;
+      return RQ_OK;
     }
+    GemmArgs<double> h = batched(gemm_args<double>(A + (int64_t)r0 * C + k, C, A + (int64_t)r0 * C + k, C,
+                                                   A + (int64_t)r0 * C + r0, C, ms, ns, kw, -1.0, EPI_ACCUM));
+    h.lower_only = 1;
+    GemmArgs<double> g = batched(gemm_args<double>(A + (int64_t)r0 * C + k, C, Linv + (int64_t)k * C, C,
+                                                   Linv + (int64_t)r0 * C, C, mr, nr, kw, -1.0, EPI_ACCUM));
+    return launch_gemm_pair(h, g, st, nb);
+  };
+
+  // Look-ahead over two streams.  After panel p the trailing update is split: the near part
+  // (the next panel's columns, all rows below, and its rows of L^-1) runs on the caller's
+  // stream, and the next panel's factorisation follows it at once; the far part (the columns
+  // and L^-1 rows past the next panel) runs on the side stream meanwhile.  The near part of
+  // panel p+1 waits for the far part of panel p, which updated the same columns; a far part
+  // starts after the panel that produced its operands and after the previous far part.  The
+  // two parts write disjoint tiles and read only finished panels.
+  std::unique_lock<std::mutex> side_lock;
+  RqSideJoin join;
+  join.s = s;
+  for (int k = 0; k < C; k += NBW) {
+    const int kw = (C - k < NBW) ? (C - k) : NBW;
+    const int pe = k + kw;                               // panel end
+    if ((rc = factor_panel(k, pe))) return rc;
+    const int rest = C - pe;
+    if (rest <= 0) break;
+    const int w2 = (rest < NBW) ? rest : NBW;            // the next panel's width
+    const int rest2 = rest - w2;
+    if (rest2 > 0) {
+      if (!join.sd && (rc = rq_side_stream(&join.sd, side_lock))) return rc;
+      RqSide* sd = join.sd;
+      if (hipEventRecord(sd->fork, s) != hipSuccess) return RQ_EHIP;
+      if (join.busy && hipStreamWaitEvent(s, sd->join, 0) != hipSuccess) return RQ_EHIP;
+      if (hipStreamWaitEvent(sd->s, sd->fork, 0) != hipSuccess) return RQ_EHIP;
+      if ((rc = trailing(k, kw, pe + w2, rest2, rest2, rest2, pe, sd->s, false))) return rc;
+      if (hipEventRecord(sd->join, sd->s) != hipSuccess) return RQ_EHIP;
+      join.busy = true;
+      if ((rc = trailing(k, kw, pe, rest, w2, w2, pe, s, NBW <= 256))) return rc;
+    } else {
+      if (join.busy) {
+        if (hipStreamWaitEvent(s, join.sd->join, 0) != hipSuccess) return RQ_EHIP;
+        join.busy = false;
+      }
+      if ((rc = trailing(k, kw, pe, rest, rest, rest, pe, s, false))) return rc;
+    }
+  }
+  if (join.busy) {
+    if (hipStreamWaitEvent(s, join.sd->join, 0) != hipSuccess) return RQ_EHIP;
+    join.busy = false;
   }
   hipLaunchKernelGGL(k_output_upper, gcol, blk, 0, s, Linv, C, Hinv, ws, info);
   RQ_CHECK_LAUNCH();
@@ -799,7 +920,7 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
     GemmArgs<double> g = batched(gemm_args<double>(Linv, C, Linv, C, A, C, C, C, C, 1.0, EPI_STORE));
     g.krange = KR_AB_LOWER;
     g.lower_only = 1;
-    int rc = launch_gemm(g, true, false, s, nb);
+    rc = launch_gemm(g, true, false, s, nb);
     if (rc) return rc;
     hipLaunchKernelGGL(k_output_full, gcol, blk, 0, s, A, C, Hinv_init, ws, info);
     RQ_CHECK_LAUNCH();

@@ -462,7 +462,7 @@ struct TwTile {
   template <int CUR, int FILL>
   __device__ __forceinline__ void step(const TStages& L, int kt) {
     TWAIT_VM(2 * (TSTAGES - 2));
-    __builtin_amdgcn_s_barrier();
+    RQ_STAGE_BARRIER();
     stage(L.s[FILL], min(kt + TSTAGES - 1, nk - 1));
     const uint8_t* st = L.s[CUR];
     const float4 a0 = *reinterpret_cast<const float4*>(st + aoff0);   // k 0..3 of this lane's row
@@ -628,7 +628,7 @@ struct TzTile {
   template <int CUR, int FILL>
   __device__ __forceinline__ void step(const TStages& L, int kt) {
     TWAIT_VM(2 * (TSTAGES - 2));
-    __builtin_amdgcn_s_barrier();
+    RQ_STAGE_BARRIER();
     stage(L.s[FILL], min(kt + TSTAGES - 1, nk - 1));
     const uint8_t* st = L.s[CUR];
     const float4 e0 = *reinterpret_cast<const float4*>(st + eoff0);

@@ -514,7 +514,7 @@ __device__ __forceinline__ void split_step(uint4 (&p)[2][PC], uint4 (&a)[2][8], 
   typedef typename T::v8 v8;
   constexpr int NP = 1 - KP;
   XWAIT_VM(2 * (XDEPTH - 3));
-  __builtin_amdgcn_s_barrier();
+  RQ_STAGE_BARRIER();
   stage_step(L.s[FILL], pa, pb, sg, wave, lane, min(k + XDEPTH - 1, last));
   const uint8_t* nxt = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[NXT] + lane * 16, 16));
   const uint8_t* w = static_cast<const uint8_t*>(
@@ -605,7 +605,7 @@ __device__ __forceinline__ void split_tile(const uint16_t* __restrict__ XB, int6
   for (int h = 0; h < XDEPTH - 1; ++h) stage_step(L.s[h], pa, pb, sg, wave, lane, min(kbeg + h, last));
   uint4 p[2][PC], a[2][8];
   XWAIT_VM(2 * (XDEPTH - 2));         // this wave's staging of step kbeg
-  __builtin_amdgcn_s_barrier();       // and the other waves'
+  RQ_STAGE_BARRIER();       // and the other waves'
   split_staged<TX, PC>(L.s[0], wave, lane, sc, p[0]);
   {
     const uint8_t* cur = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[0] + lane * 16, 16));
@@ -831,7 +831,7 @@ __device__ __forceinline__ void split_step32(uint4 (&p)[2], uint4 (&ah)[8], uint
                                              int64_t k, int64_t last, int lim) {
   typedef XType<__half>::v8 v8;
   XWAIT_VM(4 * (XDEPTH - 3));
-  __builtin_amdgcn_s_barrier();
+  RQ_STAGE_BARRIER();
   stage_step32(L.s[FILL], ph, pl, pc, sg, wave, lane, min(k + XDEPTH - 1, last));
   // phase A: hi rows x (w1, w0); the lo rows of this step and the next column fragment are read
   const uint8_t* cur = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[CUR] + X3_LO + lane * 16, 16));
@@ -908,7 +908,7 @@ __device__ __forceinline__ void split_tile32(const uint16_t* __restrict__ XH, co
   for (int h = 0; h < XDEPTH - 1; ++h) stage_step32(L.s[h], ph, pl, pc, sg, wave, lane, min(kbeg + h, last));
   uint4 p[2], ah[8], al[8];
   XWAIT_VM(4 * (XDEPTH - 2));         // this wave's staging of step kbeg
-  __builtin_amdgcn_s_barrier();       // and the other waves'
+  RQ_STAGE_BARRIER();       // and the other waves'
   {
     float x[8], sv[8];
     read_col32(L.s[0], wave, lane, x, sv);

@@ -5,6 +5,8 @@
 #include <hip/hip_bf16.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/gptqplus_hip.h"
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -14,6 +16,61 @@ typedef double doublex4 __attribute__((ext_vector_type(4)));
 #define RQ_CHECK_LAUNCH()                                   \
   do {                                                      \
     if (hipGetLastError() != hipSuccess) return RQ_EHIP;    \
+  } while (0)
+
+// A second stream of the current device for work that overlaps the caller's stream: forked
+// from it and joined back through the two events.  Created on first use (non-blocking,
+// default priority) and kept until the process ends.  An entry point that uses it holds
+// `lock` for the whole call, so calls from several host threads on one device enqueue their
+// fork / join pairs one call at a time.
+struct RqSide {
+  hipStream_t s;
+  hipEvent_t fork, join;
+};
+inline int rq_side_stream(RqSide** out, std::unique_lock<std::mutex>& lock) {
+  constexpr int MAXDEV = 64;
+  static std::mutex mu[MAXDEV];
+  static RqSide side[MAXDEV];
+  static bool made[MAXDEV];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) return RQ_EHIP;
+  lock = std::unique_lock<std::mutex>(mu[dev]);
+  if (!made[dev]) {
+    if (hipStreamCreateWithFlags(&side[dev].s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&side[dev].fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&side[dev].join, hipEventDisableTiming) != hipSuccess)
+      return RQ_EHIP;
+    made[dev] = true;
+  }
+  *out = &side[dev];
+  return RQ_OK;
+}
+
+// Makes `s` wait for the last work queued on the side stream when it goes out of scope (every
+// return path of an entry point that forked work there, errors included), so the caller's
+// buffers outlive that work.
+struct RqSideJoin {
+  RqSide* sd = nullptr;
+  hipStream_t s = nullptr;
+  bool busy = false;
+  ~RqSideJoin() {
+    if (busy) (void)hipStreamWaitEvent(s, sd->join, 0);
+  }
+};
+
+// Workgroup barrier for the direct-to-LDS staging rings: the stage a ring refills after the
+// barrier was read before it, so every wave first waits for its own LDS reads to complete
+// (lgkmcnt(0): a read only issued before the barrier could otherwise still be pending when
+// another wave's direct-to-LDS load lands on the same bytes), then s_barrier, with no wait on
+// the vector-memory counter (the loads of later stages stay in flight).  A compiler memory
+// barrier on both sides keeps the LDS accesses of a stage on their side of the barrier (the
+// builtins alone do not order memory accesses for the compiler).
+#define RQ_STAGE_BARRIER()                                                              \
+  do {                                                                                  \
+    asm volatile("" ::: "memory");                                                      \
+    __builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0); vmcnt, expcnt not limited */    \
+    __builtin_amdgcn_s_barrier();                                                       \
+    asm volatile("" ::: "memory");                                                      \
   } while (0)
 
 __device__ __forceinline__ float rq_load_elem(const __half* p) { return __half2float(*p); }

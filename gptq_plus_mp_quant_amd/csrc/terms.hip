@@ -227,7 +227,7 @@ struct NtTile {
   template <int CUR, int FILL>
   __device__ __forceinline__ void step(const NtStages& L, int kt, int nk) {
     NT_WAIT_VM(4 * (NT_STAGES - 2));
-    __builtin_amdgcn_s_barrier();
+    RQ_STAGE_BARRIER();
     stage(L.s[FILL], min(kt + NT_STAGES - 1, nk - 1));
     const uint8_t* st = L.s[CUR];
     float a[2][8], b[2][8];
