@@ -6,17 +6,21 @@
 // index-reversal permutation and L L^T = P H P,  U = P L^-1 P.  The factorisation and the
 // inverse L^-1 run together in one right-looking blocked pass in fp64 (64-wide blocks
 // inside 256-wide panels, 512-wide from C = 8192):
-//   per block k:  L_kk = chol(A_kk) and T = L_kk^-1 (k_chol_diag, one workgroup per matrix),
-//                 L_ik = A_ik T^T,  X_k = T B_k  (row block k of L^-1),
+//   per block k:  L_kk = chol(A_kk), T = L_kk^-1, L_ik = A_ik T^T and X_k = T B_k (row block k
+//                 of L^-1) in one launch (k_chol_step: every workgroup factors the 64 x 64
+//                 block itself, then does its GEMM tiles),
 //                 A_ij -= L_ik L_jk^T (lower tiles),  B_i -= L_ik X_k   (fp64 MFMA GEMMs),
 // where B accumulates I - sum_m L_im X_m.  The updates of the trailing matrix and of the rows
 // of B below a panel are applied once per panel (rank 256 / 512) instead of once per block,
-// by k_panel_update (128x128 tiles, direct global->LDS staging).  H^-1 itself (Hinv_init) is
+// by k_panel_update (128x128 tiles, direct global->LDS staging); the part of that update past
+// the next panel runs on a second stream while the next panel is factored (look-ahead).  H^-1 itself (Hinv_init) is
 // P (L^-T L^-1) P and is only formed when asked for; its diagonal (all that the GPTQ+ step
 // size needs of it) comes from the column norms of L^-1.  A non-positive or non-finite pivot, or
 // a non-finite result, raises the device `info` flag; later kernels of the same attempt exit
 // early.
 #include "gemm_tile.h"
+
+#include <algorithm>
 
 namespace {
 
@@ -108,7 +112,6 @@ __device__ __forceinline__ void rsqrt_newton(double d, double& rs, double& sq) {
 //    columns in the group (D is symmetric, so the published rows are also the columns), forms
 //    the group's rows of T, X = L_P^-1 W_group, and rows below the group subtract their rank-4
 //    products from D and W.  After 4 groups W = T_bb.
-// Writes T (lower, exact zeros above) to Tbuf and to Linv's diagonal block.
 constexpr int CD_THREADS = 256;
 constexpr int DLS = NB + 2;                 // LDS row stride of the block and of B (doubles)
 constexpr int OPS = 17;                     // row stride of a wave's T_bb operand copy
@@ -117,20 +120,12 @@ __device__ __forceinline__ doublex4 mfma_f64(double a, double b, doublex4 c) {
   return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(CD_THREADS) void k_chol_diag(const double* __restrict__ A, int C, int k,
-                                                          int nb, double* __restrict__ Tbuf,
-                                                          double* __restrict__ Linv, int64_t ws,
-                                                          int* info_all) {
-  __shared__ __attribute__((aligned(16))) double Am[NB * DLS];
-  __shared__ __attribute__((aligned(16))) double Bm[NB * DLS];
-  __shared__ __attribute__((aligned(16))) double pub[4][4 * 32];
-  __shared__ __attribute__((aligned(16))) double opnd[4][16 * OPS];
-  const int b = blockIdx.x;
-  int* info = info_all + b;
-  const int skip = *info;             // tested after the block's loads are issued
-  A += b * ws;
-  Tbuf += b * ws;
-  Linv += b * ws;
+// Leaves T in Bm (lower, exact zeros above, the identity on the padding) and returns 0, or
+// returns 1 when a pivot is not positive and finite (every wave of the workgroup sees the same),
+// or 2 when `skip` is set (the entry's attempt has already failed).
+__device__ __forceinline__ int chol_diag_lds(const double* __restrict__ A, int C, int k, int nb, int skip,
+                                             double* __restrict__ Am, double* __restrict__ Bm,
+                                             double (*pub)[4 * 32], double (*opnd)[16 * OPS]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -154,7 +149,7 @@ __global__ __launch_bounds__(CD_THREADS) void k_chol_diag(const double* __restri
         v[q].y = rowp[min(c + 1, nb - 1)];
       }
     }
-    if (skip) return;
+    if (skip) return 2;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int e = tid + 256 * q, r = e >> 5, c = 2 * (e & 31);
@@ -342,17 +337,105 @@ __global__ __launch_bounds__(CD_THREADS) void k_chol_diag(const double* __restri
     }
     __syncthreads();
   }
-  if (bad) {
-    if (tid == 0) atomicExch(info, 1);
+  return bad ? 1 : 0;
+}
+
+// One diagonal block step of the chain, in one launch: every workgroup factors and inverts the
+// 64 x 64 diagonal block at (j, j) (chol_diag_lds: the same arithmetic in each, so the same T),
+// then computes its share of the 64-wide GEMM tiles that use T:
+//   tiles u < n1:   L_ij = A_ij T^T   (rows j+jb+64u .. of the block column, in place)
+//   tiles u >= n1:  X_j[:, 64v ..] = T B_j[:, 64v ..]   (v = u - n1: row block j of L^-1, in place)
+// The tile is staged in LDS (the block's buffer, free once T is formed) and multiplied on
+// v_mfma_f64_16x16x4f64, 4 waves of 32 x 32.  Workgroup 0 of each entry writes T to Linv's
+// diagonal block; a failed pivot is recorded by workgroup 0 in `info`.  Redundant factoring in
+// every workgroup replaces a separate launch per block: the factorisation is latency-bound and
+// the GEMM tiles need only T.
+constexpr int STEP_SLOTS = 512;   // workgroups of k_chol_step resident at once (2 per CU)
+struct StepArgs {
+  double* A;
+  double* Linv;
+  int C, j, jb;
+  int n1, n2;       // lij tiles (rows below the block, 64 at a time), xj tiles (64 columns of 0 .. j)
+  int64_t ws;
+  int* info;
+};
+
+__global__ __launch_bounds__(CD_THREADS) void k_chol_step(StepArgs p) {
+  __shared__ __attribute__((aligned(16))) double Am[NB * DLS];
+  __shared__ __attribute__((aligned(16))) double Bm[NB * DLS];
+  __shared__ __attribute__((aligned(16))) double pub[4][4 * 32];
+  __shared__ __attribute__((aligned(16))) double opnd[4][16 * OPS];
+  const int b = blockIdx.z;
+  int* info = p.info + b;
+  const int skip = *info;
+  double* A = p.A + b * p.ws;
+  double* Linv = p.Linv + b * p.ws;
+  const int C = p.C, j = p.j, jb = p.jb;
+  const int rc = chol_diag_lds(A, C, j, jb, skip, Am, Bm, pub, opnd);
+  if (rc) {
+    if (rc == 1 && blockIdx.x == 0 && threadIdx.x == 0) atomicExch(info, 1);
     return;
   }
-  // T = B (lower; zeros above), one whole row per wave and instruction
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (blockIdx.x == 0) {
+    // T into Linv's diagonal block, one whole row per wave and instruction
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const int e = tid + 256 * q, r = e >> 6, c = e & 63;
-    const double v = Bm[r * DLS + c];
-    Tbuf[e] = v;
-    if (r < nb && c < nb) Linv[(int64_t)(k + r) * C + (k + c)] = v;
+    for (int q = 0; q < 16; ++q) {
+      const int e = tid + 256 * q, r = e >> 6, c = e & 63;
+      if (r < jb && c < jb) Linv[(int64_t)(j + r) * C + (j + c)] = Bm[r * DLS + c];
+    }
+  }
+  const int mi = lane & 15, mk = lane >> 4;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int ntiles = p.n1 + p.n2;
+  for (int u = blockIdx.x; u < ntiles; u += gridDim.x) {
+    const bool lij = u < p.n1;
+    // the tile: lij rows j+jb+64u .., columns j .. j+jb; xj rows j .. j+jb, columns 64v ..
+    // (clamped in-bounds reads: a padding row or column only meets a zero of T)
+    const int r0 = lij ? j + jb + 64 * u : j;
+    const int c0 = lij ? j : 64 * (u - p.n1);
+    const int rmax = lij ? C - 1 : j + jb - 1;
+    const int cmax = lij ? j + jb - 1 : j - 1;
+    __syncthreads();                  // the previous tile's reads of Am are done
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int e = tid + 256 * q, r = e >> 5, c = 2 * (e & 31);
+      const double* src = (lij ? A : Linv) + (int64_t)min(r0 + r, rmax) * C;
+      Am[r * DLS + c] = src[min(c0 + c, cmax)];
+      Am[r * DLS + c + 1] = src[min(c0 + c + 1, cmax)];
+    }
+    __syncthreads();
+    doublex4 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) acc[a][q] = doublex4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      const int kx = 4 * kk + mk;
+      double av[2], bv[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int rr = 32 * wr + 16 * a + mi, cc = 32 * wc + 16 * a + mi;
+        av[a] = lij ? Am[rr * DLS + kx] : Bm[rr * DLS + kx];          // A_ij[r][k] / T[r][k]
+        bv[a] = lij ? Bm[cc * DLS + kx] : Am[kx * DLS + cc];          // T[c][k] / B_j[k][c]
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) acc[a][q] = mfma_f64(av[a], bv[q], acc[a][q]);
+    }
+    double* dst = lij ? A : Linv;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = r0 + 32 * wr + 16 * a + mk + 4 * e, c = c0 + 32 * wc + 16 * q + mi;
+          if (r <= rmax && c <= cmax) dst[(int64_t)r * C + c] = acc[a][q][e];
+        }
   }
 }
 
@@ -785,7 +868,6 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
   const int64_t ws = 2 * (int64_t)C * C + (int64_t)NB * NB;   // doubles per batch entry
   double* A = reinterpret_cast<double*>(workspace);
   double* Linv = A + (int64_t)C * C;
-  double* Tbuf = Linv + (int64_t)C * C;
   const dim3 blk(256);
   const dim3 gcol((C + 255) / 256, C < 1024 ? C : 1024, nb);
 
@@ -813,17 +895,14 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
       const int jb = (pe - j < NB) ? (pe - j) : NB;
       const int below = C - j - jb;                      // rows below this block (whole matrix)
       const int pend = pe - j - jb;                      // panel columns right of this block
-      hipLaunchKernelGGL(k_chol_diag, dim3(nb), dim3(CD_THREADS), 0, s, A, C, j, jb, Tbuf, Linv, ws, info);
+      // one launch: T = L_jj^-1, then L_ij = A_ij T^T (in place, every row below the block) and
+      // X_j[:, 0:j] = T B_j[:, 0:j] (in place, row block j of L^-1)
+      StepArgs sa{A, Linv, C, j, jb, (below + NB - 1) / NB, (j + NB - 1) / NB, ws, info};
+      const int ntiles = sa.n1 + sa.n2;
+      const int per_entry = std::max(1, std::min(ntiles, std::max(1, STEP_SLOTS / nb)));
+      hipLaunchKernelGGL(k_chol_step, dim3(per_entry, 1, nb), dim3(CD_THREADS), 0, s, sa);
       RQ_CHECK_LAUNCH();
       int r;
-      // one launch: L_ij = A_ij T^T (in place, every row below the block) and
-      // X_j[:, 0:j] = T B_j[:, 0:j] (in place, row block j of L^-1)
-      GemmArgs<double> lij = batched(gemm_args<double>(A + (int64_t)(j + jb) * C + j, C, Tbuf, NB,
-                                                       A + (int64_t)(j + jb) * C + j, C, below, jb, jb,
-                                                       1.0, EPI_STORE));
-      GemmArgs<double> xj = batched(gemm_args<double>(Tbuf, NB, Linv + (int64_t)j * C, C,
-                                                      Linv + (int64_t)j * C, C, jb, j, jb, 1.0, EPI_STORE));
-      if ((r = launch_gemm_pair(lij, xj, s, nb))) return r;
       // one launch, inside the panel: A[j+jb:, j+jb:pe] -= L[j+jb:, j] L[j+jb:pe, j]^T (lower
       // tiles) and the panel rows of L^-1: B[j+jb:pe, 0:j+jb] -= L[j+jb:pe, j] X_j.  On the
       // 128-tile panel kernel with 512-wide panels (up to 448 columns); the narrower updates of
