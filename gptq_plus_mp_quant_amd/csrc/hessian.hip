@@ -453,7 +453,7 @@ __device__ __forceinline__ void split8(uint4 x, float4 s0, float4 s1, float sc, 
 // every stage index is a compile-time constant: the LDS reads are ordinary loads (the compiler
 // places their lgkmcnt waits), and alias analysis can tell the staging writes in flight to
 // other stages from the stage being read.
-constexpr int XDEPTH = 4;   // 8 stages measured no faster
+constexpr int XDEPTH = 4;   // 8 stages measured no faster, also with one barrier per two steps
 constexpr int XA_BYTES = 8 * 1024;                  // row fragments of a stage
 constexpr int XB_OFF = XA_BYTES;                    // column fragment of wave w at XB_OFF + 1024 w
 constexpr int XS_OFF = XB_OFF + XWAVES * 1024;      // the step's 16 saliencies (64 B)
@@ -501,8 +501,8 @@ __device__ __forceinline__ void split_staged(const uint8_t* st, int wave, int la
 // during step k-2) before its refill.  Then: stage step k+XDEPTH-1; issue the PC x 8 MFMAs
 // of step k from registers, while the row fragments of step k+1 are read and this wave's column
 // fragment of step k+1 is split in between.  The MFMAs need no LDS read after the barrier, so
-// the two waves of a SIMD resume issuing as soon as it opens.  A bare s_barrier: the fence of
-// __syncthreads would wait for every staging load in flight.
+// the two waves of a SIMD resume issuing as soon as it opens.  RQ_STAGE_BARRIER, not
+// __syncthreads, whose fence would wait for every staging load in flight.
 // DIAG (a diagonal tile): row blocks below this wave's column block hold only the discarded
 // lower triangle, so their row fragments are not read and their MFMAs not issued (bi < lim).
 template <typename TX, int PC, bool DIAG, int KP, int CUR, int NXT, int FILL>

@@ -321,6 +321,36 @@ def test_cholesky_chain_wide_panels(C):
     assert err <= 1e-5 and derr <= 1e-5
 
 
+def test_cholesky_lookahead_repeatable():
+    """The chain overlaps each panel's far trailing update (second stream) with the next panel's
+    factorisation; the results must not depend on how the two interleave.  C = 14336 (28
+    panels of 512, the down_proj width): six attempts on the same matrices give the same bits.
+    Regression check for a staging-ring race (a stage refilled by one wave's direct-to-LDS
+    load before another wave's read of it had completed) that concurrent kernels exposed."""
+    C, nb = 14336, 4
+    g = torch.Generator(device=DEV)
+    g.manual_seed(5)
+    A = torch.randn(2 * C, C, device=DEV, generator=g)
+    H = (A.T @ A) / (2 * C)
+    del A
+    Hs = H.unsqueeze(0).repeat(nb, 1, 1).contiguous()
+    del H
+    ws = K.chol_workspace(C, DEV, nb)
+    Hinv = torch.empty(nb, C, C, device=DEV)
+    hd = torch.empty(nb, C, device=DEV)
+    ref = None
+    for rep in range(6):
+        Hw = Hs.clone()
+        info = K.chol_hinv_attempt(Hw, [0.01] * nb, ws, Hinv, None, Hinv_diag=hd)
+        torch.cuda.synchronize()
+        assert info.tolist() == [0] * nb
+        if ref is None:
+            ref = (Hinv.clone(), hd.clone())
+        else:
+            assert torch.equal(Hinv, ref[0]) and torch.equal(hd, ref[1]), f"attempt {rep} differs"
+        del Hw
+
+
 @pytest.mark.parametrize("C", [200, 600])
 def test_cholesky_batch_independent_entries(C):
     """Batched attempt: each matrix gets its own damping, skipped entries stay untouched, and a
