@@ -928,10 +928,10 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
   };
   // The update by panel [k, k + kw) of the trailing rows r0 ..: A[r0:r0+ms, r0:r0+ns] -=
   // L[r0:, k:k+kw] L[r0:, k:k+kw]^T (lower tiles) and B[r0:r0+mr, 0:nr] -= L[r0:r0+mr, k:k+kw]
-  // X[k:k+kw, 0:nr], on the 128-tile panel kernel, or on the 64-tile GEMM when `small` (fewer,
-  // shorter tiles: lower latency) or when the panel kernel does not take the shape.
-  auto trailing = [&](int k, int kw, int r0, int ms, int ns, int mr, int nr, hipStream_t st, bool small) -> int {
-    if (!small && launch_panel(A + (int64_t)r0 * C + k, Linv + (int64_t)k * C, A + (int64_t)r0 * C + r0,
+  // X[k:k+kw, 0:nr], on the 128-tile panel kernel, or on the 64-tile GEMM when the panel kernel
+  // does not take the shape.
+  auto trailing = [&](int k, int kw, int r0, int ms, int ns, int mr, int nr, hipStream_t st) -> int {
+    if (launch_panel(A + (int64_t)r0 * C + k, Linv + (int64_t)k * C, A + (int64_t)r0 * C + r0,
                                Linv + (int64_t)r0 * C, C, kw, ms, ns, mr, nr, ws, info, nb, st)) {
       RQ_CHECK_LAUNCH();
       return RQ_OK;
@@ -944,7 +944,9 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
     return launch_gemm_pair(h, g, st, nb);
   };
 
-  // Look-ahead over two streams.  After panel p the trailing update is split: the near part
+  // Look-ahead over two streams, for the 512-wide panels (C >= 8192: at C = 4096 the overlap
+  // gains less than the latency-bound factorisation kernels lose while the far update holds the
+  // CUs).  After panel p the trailing update is split: the near part
   // (the next panel's columns, all rows below, and its rows of L^-1) runs on the caller's
   // stream, and the next panel's factorisation follows it at once; the far part (the columns
   // and L^-1 rows past the next panel) runs on the side stream meanwhile.  The near part of
@@ -962,22 +964,22 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
     if (rest <= 0) break;
     const int w2 = (rest < NBW) ? rest : NBW;            // the next panel's width
     const int rest2 = rest - w2;
-    if (rest2 > 0) {
+    if (rest2 > 0 && NBW > 256) {
       if (!join.sd && (rc = rq_side_stream(&join.sd, side_lock))) return rc;
       RqSide* sd = join.sd;
       if (hipEventRecord(sd->fork, s) != hipSuccess) return RQ_EHIP;
       if (join.busy && hipStreamWaitEvent(s, sd->join, 0) != hipSuccess) return RQ_EHIP;
       if (hipStreamWaitEvent(sd->s, sd->fork, 0) != hipSuccess) return RQ_EHIP;
-      if ((rc = trailing(k, kw, pe + w2, rest2, rest2, rest2, pe, sd->s, false))) return rc;
+      if ((rc = trailing(k, kw, pe + w2, rest2, rest2, rest2, pe, sd->s))) return rc;
       if (hipEventRecord(sd->join, sd->s) != hipSuccess) return RQ_EHIP;
       join.busy = true;
-      if ((rc = trailing(k, kw, pe, rest, w2, w2, pe, s, NBW <= 256))) return rc;
+      if ((rc = trailing(k, kw, pe, rest, w2, w2, pe, s))) return rc;
     } else {
       if (join.busy) {
         if (hipStreamWaitEvent(s, join.sd->join, 0) != hipSuccess) return RQ_EHIP;
         join.busy = false;
       }
-      if ((rc = trailing(k, kw, pe, rest, rest, rest, pe, s, false))) return rc;
+      if ((rc = trailing(k, kw, pe, rest, rest, rest, pe, s))) return rc;
     }
   }
   if (join.busy) {
