@@ -50,6 +50,8 @@ SIGNATURES = {
     "rq_gptqplus_terms": (_I, [_P, _L, _P, _P, _P, _I, _I, _I, _D, _D, _I, _P, _P, _P, _L, _P, _P, _P]),
     "rq_quant_block": (_I, [_P, _L, _P, _I, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I,
                             _I, _P, _P, _P, _I, _P, _L, _P, _D, _P]),
+    "rq_quant_block_lookahead": (_I, [_P, _L, _P, _I, _I, _I, _I, _I, _P, _I, _I, _P, _P, _P, _I, _I, _I, _P,
+                                      _P, _P]),
     "rq_trailing_update": (_I, [_P, _L, _P, _P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _I, _I, _P, _L,
                                 _P, _D, _P]),
     "rq_writeback": (_I, [_P, _I, _I, _P, _I, _P, _P, _P, _I, _P, _I, _L, _P, _P, _P, _P]),

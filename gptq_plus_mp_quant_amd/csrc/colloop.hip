@@ -84,26 +84,98 @@ struct QBArgs {
   int64_t lda;
   const float* beta;
   float sos;
+  // Look-ahead launch (k_block_lookahead): the previous block's update of this block's
+  // columns, applied by each workgroup to its own rows before the column loop; zero_terms: Z
+  // (hence GH) is identically zero, z_nonzero is not read.
+  const float* near_err;      // err of the previous block [R, near_count], or NULL
+  int near_i1, near_count;
+  int zero_terms;
 };
+
+// Bytes of LDS the column loop uses: the block of Hinv ([16 NS][16][NS] floats), and in a
+// look-ahead launch the previous block's rows of Hinv ([QB_MAXB][16][NS], the same buffer)
+// and err of the workgroup's 16 rows after it.
+template <int NS>
+constexpr int qb_hbytes(bool near) {
+  return (near ? QB_MAXB : QL * NS) * QL * NS * 4;
+}
+template <int NS>
+constexpr int qb_lds_bytes(bool near) {
+  return qb_hbytes<NS>(near) + (near ? (256 / QL) * QB_MAXB * 4 : 0);
+}
 
 // GM: 0 frozen, 1 surrogate_block, 2 surrogate_online, 3 frozen with every in-block update
 // scaled by second_order_scale (block_gd, :1344-1349).  NS register slots per lane: lane t of
 // a row holds columns t, t + 16, ..., t + 16 (NS - 1) of the block (NS = 8 for 128 columns).
 template <int NS, int GM>
-__global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
+__device__ __forceinline__ void quant_block_body(const QBArgs& a, int bx, int by, uint8_t* lds) {
   constexpr int NB = QL * NS;             // widest block this instantiation takes
   // Hp[i][t][k] = Hinv1[i][16 k + t] (upper; zeros below the diagonal and past the block):
   // a lane reads its NS entries of row i as NS / 4 aligned 16-byte loads
-  __shared__ __attribute__((aligned(16))) float Hp[NB][QL][NS];
+  float (*Hp)[QL][NS] = reinterpret_cast<float (*)[QL][NS]>(lds);
   const int tid = threadIdx.x;
   const int t = tid & (QL - 1);
-  const int sub = blockIdx.y;
-  const int row_local = blockIdx.x * (256 / QL) + (tid / QL);
+  const int sub = by;
+  const int rloc = tid / QL;
+  const int row_local = bx * (256 / QL) + rloc;
   const bool valid = row_local < a.R_s;
   const int row = sub * a.R_s + (valid ? row_local : 0);
   const int count = a.count, i1 = a.i1;
   const float* Hs = a.Hinv + (int64_t)sub * a.C * a.C;
-  const bool use_gh = (*a.z_nonzero != 0);
+  const bool use_gh = !a.zero_terms && (*a.z_nonzero != 0);
+
+  // Look-ahead launch: W[r, i1 + c] -= sum_k err_prev[r, k] Hinv[p1 + k, i1 + c] for this
+  // workgroup's rows, formed like rq_trailing_update (a sequential fused multiply-add chain in k
+  // from 0, then one subtraction: the CPU matmul's order), and written back to Wp.  The
+  // previous block's rows of Hinv go through the same LDS as Hp (Hoff[k][t][s] =
+  // Hinv[p1 + k][i1 + 16 s + t]), the err rows after it.
+  float wn[NS];                         // the block's weights after the look-ahead update
+  if (a.near_err) {
+    const int pc = a.near_count, p1 = a.near_i1;
+    float* Ep = reinterpret_cast<float*>(lds + qb_hbytes<NS>(true));   // [16][QB_MAXB]
+    constexpr int PER = QB_MAXB * NB / 256;
+    float v[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = tid + 256 * q, i = e / NB, j = e % NB;
+      v[q] = Hs[(int64_t)(p1 + min(i, pc - 1)) * a.C + (i1 + min(j, count - 1))];
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = tid + 256 * q, i = e / NB, j = e % NB;
+      Hp[i][j % QL][j / QL] = (i < pc && j < count) ? v[q] : 0.0f;
+    }
+    for (int e = tid; e < (256 / QL) * pc; e += 256) {
+      const int rl = e / pc, kk = e % pc;
+      const int rr = bx * (256 / QL) + rl;
+      Ep[rl * QB_MAXB + kk] = (rr < a.R_s) ? a.near_err[(int64_t)(sub * a.R_s + rr) * pc + kk] : 0.0f;
+    }
+    __syncthreads();
+    float acc[NS];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) acc[k] = 0.0f;
+    const float* er = Ep + rloc * QB_MAXB;
+    for (int kk = 0; kk < pc; ++kk) {
+      const float e = er[kk];
+#pragma unroll
+      for (int k = 0; k < NS; k += 4) {
+        const float4 h = *reinterpret_cast<const float4*>(&Hp[kk][t][k]);
+        acc[k] = __builtin_fmaf(e, h.x, acc[k]);
+        if (k + 1 < NS) acc[k + 1] = __builtin_fmaf(e, h.y, acc[k + 1]);
+        if (k + 2 < NS) acc[k + 2] = __builtin_fmaf(e, h.z, acc[k + 2]);
+        if (k + 3 < NS) acc[k + 3] = __builtin_fmaf(e, h.w, acc[k + 3]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const int col = QL * k + t;
+      const bool in = valid && col < count;
+      float* wp = a.Wp + (int64_t)row * a.ldw + i1 + col;
+      wn[k] = in ? *wp - acc[k] : 0.0f;
+      if (in) *wp = wn[k];
+    }
+    __syncthreads();                  // Hp is refilled below
+  }
 
   {
     // all NB * NB / 256 loads of a thread in flight at once: clamped (in-bounds) addresses,
@@ -130,7 +202,7 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
     const int col = QL * k + t;
     const bool in = valid && col < count;
     const int64_t off = (int64_t)row * a.ldw + i1 + col;
-    w[k] = in ? a.Wp[off] : 0.0f;
+    w[k] = a.near_err ? wn[k] : (in ? a.Wp[off] : 0.0f);
     if constexpr (SURR) {
       const float wr = in ? a.anchor[(int64_t)row * a.lda + i1 + col] : 0.0f;
       xr[k] = (GM == 1) ? (w[k] - wr) : wr;
@@ -274,6 +346,12 @@ __global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
   };
   if (use_gh) all_columns(true);
   else all_columns(false);
+}
+
+template <int NS, int GM>
+__global__ __launch_bounds__(256) void k_quant_block(QBArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[qb_lds_bytes<NS>(false)];
+  quant_block_body<NS, GM>(a, blockIdx.x, blockIdx.y, lds);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -432,6 +510,7 @@ struct TwArgs {
   float f;               // 1, or second_order_scale (RQ_GMODE_BLOCK_GD)
   int nrt, nct;          // row tiles per subgroup, column tiles
   int total;             // nrt * nct * subgroups
+  int cbeg;              // first updated column (i1 + count; later in a look-ahead launch)
 };
 
 struct TStages {
@@ -485,15 +564,9 @@ struct TwTile {
   }
 };
 
-__global__ __launch_bounds__(256, 2) void k_trailing_w(TwArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds0[TSTAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t lds1[TSTAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t lds2[TSTAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t lds3[TSTAGE];
-  const TStages L{{lds0, lds1, lds2, lds3}};
+__device__ __forceinline__ void trailing_w_body(const TwArgs& a, int b, const TStages& L) {
   // XCD-aware order: each XCD takes a contiguous range of tiles (row tile fastest), so the
   // tiles of one Hinv column strip meet in one L2.
-  const int b = blockIdx.x;
   const int per = a.total / 8, rem8 = a.total % 8;
   const int xcd = b % 8, idx = b / 8;
   const int t = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
@@ -501,8 +574,7 @@ __global__ __launch_bounds__(256, 2) void k_trailing_w(TwArgs a) {
   const int per_sub = a.nrt * a.nct;
   const int sub = t / per_sub, u = t % per_sub;
   const int ct = u / a.nrt, rt = u % a.nrt;
-  const int i2 = a.i1 + a.count;
-  const int rl0 = rt * TT, c0 = i2 + ct * TT;
+  const int rl0 = rt * TT, c0 = a.cbeg + ct * TT;
   const int64_t rbase = (int64_t)sub * a.R_s;
 
   TwTile w;
@@ -578,6 +650,35 @@ __global__ __launch_bounds__(256, 2) void k_trailing_w(TwArgs a) {
       const float v = wv[h][e] - (scaled ? a.f * tot : tot);
       if (full || (rl < a.R_s && c < a.C)) a.Wp[(rbase + rl) * a.ldw + c] = v;
     }
+}
+
+__global__ __launch_bounds__(256, 2) void k_trailing_w(TwArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds0[TSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds1[TSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds2[TSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds3[TSTAGE];
+  const TStages L{{lds0, lds1, lds2, lds3}};
+  trailing_w_body(a, blockIdx.x, L);
+}
+
+// One launch per block k of the frozen column loop with Z identically zero: workgroups
+// [0, nq) quantise block k+1 (each first applies block k's update to its own rows of block
+// k+1's columns), the others update the columns past block k+1 with block k's err
+// (k_trailing_w's tiles).  The two parts touch disjoint columns and different err buffers,
+// so block k+1's column loop runs while block k's wide update does.  The quantising
+// workgroups come first in the grid, so they are dispatched first.
+template <int NS>
+__global__ __launch_bounds__(256, 2) void k_block_lookahead(QBArgs q, TwArgs w, int nqx, int nq) {
+  constexpr int QBYTES = qb_lds_bytes<NS>(true);
+  constexpr int LBYTES = QBYTES > TSTAGES * TSTAGE ? QBYTES : TSTAGES * TSTAGE;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LBYTES];
+  const int b = blockIdx.x;
+  if (b < nq) {
+    quant_block_body<NS, 0>(q, b % nqx, b / nqx, lds);
+    return;
+  }
+  const TStages L{{lds, lds + TSTAGE, lds + 2 * TSTAGE, lds + 3 * TSTAGE}};
+  trailing_w_body(w, b - nq, L);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -814,7 +915,7 @@ extern "C" int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float
     // Z (and with it GH) identically zero: only W -= f * err Hinv[i1:i2, i2:] remains
     TwArgs w{Wp, ldw, Hinv_all, C, R_s, i1, count, err,
              gmode == RQ_GMODE_BLOCK_GD ? (float)second_order_scale : 1.0f,
-             (R_s + TT - 1) / TT, (C - i2 + TT - 1) / TT, 0};
+             (R_s + TT - 1) / TT, (C - i2 + TT - 1) / TT, 0, i2};
     w.total = w.nrt * w.nct * (R / R_s);
     hipLaunchKernelGGL(k_trailing_w, dim3(w.total), dim3(256), 0, s, w);
     RQ_CHECK_LAUNCH();
@@ -837,6 +938,65 @@ extern "C" int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float
            anchor, ld_anchor, beta, (float)second_order_scale};
   dim3 grid((C - i2 + 63) / 64, (R_s + 63) / 64, R / R_s), block(256);
   hipLaunchKernelGGL(k_trailing, grid, block, 0, s, a);
+  RQ_CHECK_LAUNCH();
+  return RQ_OK;
+}
+
+extern "C" int rq_quant_block_lookahead(float* Wp, int64_t ldw, const float* Hinv_all, int C, int R, int R_s,
+                                        int i1, int count, const float* err, int count_next, int qmode,
+                                        const float* scale, const int32_t* col_group, float* dyn_scale,
+                                        int maxq, int sym, int atomic, int16_t* codes, float* err_next,
+                                        void* stream) {
+  if (!Wp || !Hinv_all || !err || !codes || !err_next || err == err_next) return RQ_EINVAL;
+  if (R <= 0 || R_s <= 0 || R % R_s != 0 || C <= 0 || ldw < C) return RQ_EINVAL;
+  if (count <= 0 || count > QB_MAXB || i1 < 0 || count_next <= 0 || count_next > QB_MAXB) return RQ_EINVAL;
+  const int i1n = i1 + count, cbeg = i1n + count_next;
+  if (cbeg > C || maxq <= 0 || qmode < 0 || qmode > 2) return RQ_EINVAL;
+  if (qmode == RQ_QMODE_CHANNEL && !scale) return RQ_EINVAL;
+  if (qmode == RQ_QMODE_STATIC && (!scale || !col_group)) return RQ_EINVAL;
+  if (qmode == RQ_QMODE_DYNAMIC && !dyn_scale) return RQ_EINVAL;
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  // the wide part runs k_trailing_w's tiles: its shape conditions
+  if (count % 8 || C % 4 || cbeg % 4 || !al16(Hinv_all) || !al16(err)) return RQ_EINVAL;
+  QBArgs q{};
+  q.Wp = Wp;
+  q.ldw = ldw;
+  q.Hinv = Hinv_all;
+  q.C = C;
+  q.GH = nullptr;
+  q.Z = nullptr;
+  q.ldgh = C;
+  q.R = R;
+  q.R_s = R_s;
+  q.i1 = i1n;
+  q.count = count_next;
+  q.qmode = qmode;
+  q.scale = scale;
+  q.col_group = col_group;
+  q.dyn_scale = dyn_scale;
+  q.maxq = (float)maxq;
+  q.sym = sym;
+  q.atomic = atomic;
+  q.z_nonzero = nullptr;
+  q.codes = codes;
+  q.err = err_next;
+  q.anchor = nullptr;
+  q.lda = C;
+  q.beta = nullptr;
+  q.sos = 1.0f;
+  q.near_err = err;
+  q.near_i1 = i1;
+  q.near_count = count;
+  q.zero_terms = 1;
+  TwArgs w{Wp, ldw, Hinv_all, C, R_s, i1, count, err, 1.0f, (R_s + TT - 1) / TT, (C - cbeg + TT - 1) / TT, 0,
+           cbeg};
+  w.total = (cbeg < C) ? w.nrt * w.nct * (R / R_s) : 0;
+  const int nqx = (R_s + 256 / QL - 1) / (256 / QL), nq = nqx * (R / R_s);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (count_next <= 2 * QL)
+    hipLaunchKernelGGL(k_block_lookahead<2>, dim3(nq + w.total), dim3(256), 0, s, q, w, nqx, nq);
+  else
+    hipLaunchKernelGGL(k_block_lookahead<8>, dim3(nq + w.total), dim3(256), 0, s, q, w, nqx, nq);
   RQ_CHECK_LAUNCH();
   return RQ_OK;
 }

@@ -436,8 +436,33 @@ class GPTQPlus:
                 grad = grad.to(dev).float().reshape(R, C)
                 return grad if grad.is_contiguous() else grad.contiguous()
 
+            # Frozen mode with the GPTQ+ terms identically zero and no refresh between blocks: one
+            # launch per block quantises block k+1 while block k's wide update runs
+            # (rq_quant_block_lookahead; equal bit for bit to the two calls per block below)
+            lookahead = (gm_in == nat.RQ_GMODE_FROZEN and gm_out == nat.RQ_GMODE_FROZEN and z_zero
+                         and not (block_bw or block_gd) and nblocks > 1 and blocksize % 8 == 0
+                         and C % 4 == 0
+                         and not (qmode == nat.RQ_QMODE_DYNAMIC and (q.mse or not q.perchannel)))
+            if lookahead:
+                with _section(rec, "fasterquant.block_loop"):
+                    errs = (err, torch.empty_like(err))
+                    for bidx, i1 in enumerate(range(0, C, blocksize)):
+                        i2 = min(i1 + blocksize, C)
+                        atomic = bool(block_atomic_quant) and i2 < C
+                        ds = dyn_scale[bidx] if dyn_scale is not None else None
+                        if bidx == 0:
+                            K.quant_block(Wp, Hinv_all, GH, Z, R_s, i1, i2 - i1, qmode, scale_tab, col_group,
+                                          ds, maxq, sym, atomic, z_any, codes, errs[0], gm_in, anchor,
+                                          beta_rows, sos)
+                        if i2 < C:
+                            n2 = min(i2 + blocksize, C)
+                            K.quant_block_lookahead(Wp, Hinv_all, R_s, i1, i2 - i1, errs[bidx % 2], n2 - i2,
+                                                    qmode, scale_tab, col_group,
+                                                    dyn_scale[bidx + 1] if dyn_scale is not None else None,
+                                                    maxq, sym, bool(block_atomic_quant) and n2 < C, codes,
+                                                    errs[(bidx + 1) % 2])
             with _section(rec, "fasterquant.block_loop"):
-                for bidx, i1 in enumerate(range(0, C, blocksize)):
+                for bidx, i1 in enumerate(range(0, C, blocksize) if not lookahead else ()):
                     i2 = min(i1 + blocksize, C)
                     count = i2 - i1
                     atomic = bool(block_atomic_quant) and i2 < C

@@ -284,6 +284,22 @@ def quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale, col_group, dy
              float(second_order_scale), _stream(Wp))
 
 
+def quant_block_lookahead(Wp, Hinv_all, R_s, i1, count, err, count_next, qmode, scale, col_group, dyn_scale,
+                          maxq, sym, atomic, codes, err_next):
+    """Block k's trailing update (W-only: frozen mode, Z identically zero) and block k+1's
+    quantisation in one launch; equal bit for bit to trailing_update(k) then quant_block(k+1)."""
+    R, C = Wp.shape
+    if Hinv_all.shape != (R // R_s, C, C) or not Hinv_all.is_contiguous():
+        raise ValueError("quant_block_lookahead: Hinv_all must be contiguous [G, C, C]")
+    _cout(Wp, "Wp"), _cout(err_next, "err_next"), _cin(err, "err")
+    if err.data_ptr() == err_next.data_ptr():
+        raise ValueError("quant_block_lookahead: err and err_next must be different buffers")
+    nat.call("rq_quant_block_lookahead", nat.ptr(Wp), Wp.stride(0), nat.ptr(Hinv_all), C, R, R_s, int(i1),
+             int(count), nat.ptr(err), int(count_next), int(qmode), nat.ptr(scale), nat.ptr(col_group),
+             nat.ptr(dyn_scale), int(maxq), int(bool(sym)), int(bool(atomic)), nat.ptr(codes),
+             nat.ptr(err_next), _stream(Wp))
+
+
 def trailing_update(Wp, GH, Z, Hinv_all, R_s, i1, count, err, z_nonzero, gmode=nat.RQ_GMODE_FROZEN,
                     anchor=None, beta=None, second_order_scale=1.0, z_zero=False):
     """z_zero=True states that Z (and GH) are identically zero, i.e. that z_nonzero holds 0; the

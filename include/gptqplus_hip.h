@@ -222,6 +222,23 @@ int rq_trailing_update(float* Wp, int64_t ldw, float* GH, const float* Z, int64_
                        int64_t ld_anchor, const float* beta, double second_order_scale,
                        void* stream);
 
+/* The frozen-mode column loop's per-block pair -- rq_trailing_update for block k
+ * (gptq_plus_utils.py:1512-1519) and rq_quant_block for block k+1 (:1296-1367) -- in one
+ * launch, for Z (hence GH) identically zero; equal to the two calls bit for bit.  Block k =
+ * columns [i1, i1+count) with its err [R, count]; block k+1 = [i1+count, i1+count+count_next).
+ * The workgroups that quantise block k+1 first apply block k's update to their own rows of
+ * its columns (the CPU matmul's order, written back to Wp); the rest apply block k's update to
+ * the columns past block k+1 meanwhile.  Writes block k+1's codes and its err to err_next
+ * ([R, count_next], a different buffer from err); dyn_scale is block k+1's, atomic applies
+ * to block k+1.  Needs count % 8 == 0, C % 4 == 0, (i1 + count + count_next) % 4 == 0 and
+ * Hinv_all, err 16-byte aligned (else RQ_EINVAL: use the two calls).  No single counterpart in
+ * the reference: it fuses two of its steps for the look-ahead over blocks. */
+int rq_quant_block_lookahead(float* Wp, int64_t ldw, const float* Hinv_all, int C, int R, int R_s,
+                             int i1, int count, const float* err, int count_next, int qmode,
+                             const float* scale, const int32_t* col_group, float* dyn_scale,
+                             int maxq, int sym, int atomic, int16_t* codes, float* err_next,
+                             void* stream);
+
 /* Un-permute and write back -- gptq_plus_utils.py:1850-1875:
  * natural column c of row r takes permuted column j = invperm[c] (identity if NULL):
  * Q = scale(r, j) * code[r, j]; q_out (layer dtype q_dtype, [R, C] row stride ldq) = Q;

@@ -567,6 +567,78 @@ def test_trailing_update_with_z(G, R_s, C, i1, cnt, gmode, sos):
         assert torch.equal(GHd[rows, :i2].cpu(), GH[rows, :i2])
 
 
+@pytest.mark.parametrize("G,R_s,C,B,qmode,atomic", [
+    (2, 96, 328, 128, "channel", False),     # last block 72 wide
+    (1, 200, 280, 128, "static", False),     # last block 24 wide (the narrow column loop)
+    (3, 48, 384, 128, "dynamic", False),
+    (2, 64, 264, 64, "channel", True),       # atomic blocks, 64 wide
+    (4, 40, 256, 32, "static", True),
+])
+def test_quant_block_lookahead_equals_two_calls(G, R_s, C, B, qmode, atomic):
+    """rq_quant_block_lookahead (block k's W-only trailing update and block k+1's column loop in
+    one launch) against rq_trailing_update + rq_quant_block over a whole column loop: codes,
+    every block's err and the working weight equal bit for bit."""
+    r = rng(70 + C + B)
+    R = G * R_s
+    Hs = torch.stack([_spd(80 + g, C) for g in range(G)]).to(DEV).contiguous()
+    ws = K.chol_workspace(C, DEV, G)
+    Hinv = torch.empty(G, C, C, device=DEV)
+    info = K.chol_hinv_attempt(Hs.clone(), [0.01] * G, ws, Hinv)
+    assert info.tolist() == [0] * G
+    W0 = torch.from_numpy(r.standard_normal((R, C)).astype(np.float32)).to(DEV)
+    maxq, sym = 7, 0
+    nblocks = (C + B - 1) // B
+    scale = col_group = dyn = None
+    qm = {"channel": nat.RQ_QMODE_CHANNEL, "static": nat.RQ_QMODE_STATIC, "dynamic": nat.RQ_QMODE_DYNAMIC}[qmode]
+    if qmode == "channel":
+        scale = (W0.abs().amax(1) / maxq).contiguous()
+    elif qmode == "static":
+        ng = (C + 63) // 64
+        scale = torch.from_numpy(r.uniform(0.2, 0.6, (ng, R)).astype(np.float32)).to(DEV).reshape(-1)
+        col_group = (torch.arange(C, device=DEV) // 64).to(torch.int32)
+    zero = torch.zeros_like(W0)
+    nz0 = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = {}
+    for mode in ("two_calls", "lookahead"):
+        Wp = W0.clone()
+        codes = torch.zeros((R, C), dtype=torch.int16, device=DEV)
+        errs = [torch.empty((R, B), device=DEV) for _ in range(2)]
+        dyn = torch.zeros((nblocks, R), device=DEV) if qmode == "dynamic" else None
+        seen = []
+        for b, i1 in enumerate(range(0, C, B)):
+            i2 = min(i1 + B, C)
+            at = atomic and i2 < C
+            ds = dyn[b] if dyn is not None else None
+            e = errs[b % 2]
+            if mode == "two_calls" or b == 0:
+                K.quant_block(Wp, Hinv, zero, zero, R_s, i1, i2 - i1, qm, scale, col_group, ds, maxq, sym, at,
+                              nz0, codes, e)
+            if i2 < C:
+                if mode == "two_calls":
+                    K.trailing_update(Wp, zero, zero, Hinv, R_s, i1, i2 - i1, e, nz0, z_zero=True)
+                else:
+                    n2 = min(i2 + B, C)
+                    K.quant_block_lookahead(Wp, Hinv, R_s, i1, i2 - i1, e, n2 - i2, qm, scale, col_group,
+                                            dyn[b + 1] if dyn is not None else None, maxq, sym,
+                                            atomic and n2 < C, codes, errs[(b + 1) % 2])
+            if mode == "two_calls" or b == 0:
+                seen.append(e.reshape(-1)[:R * (i2 - i1)].clone())
+            if mode == "lookahead" and i2 < C:
+                n2 = min(i2 + B, C)
+                seen.append(errs[(b + 1) % 2].reshape(-1)[:R * (n2 - i2)].clone())
+        torch.cuda.synchronize()
+        out[mode] = (Wp, codes, seen, dyn)
+    a, b = out["two_calls"], out["lookahead"]
+    assert torch.equal(a[1], b[1]), "codes"
+    assert len(a[2]) == len(b[2]) == nblocks
+    for k, (x, y) in enumerate(zip(a[2], b[2])):
+        assert torch.equal(x, y), f"err of block {k}"
+    assert torch.equal(a[0], b[0]), "working weight"
+    if qmode == "dynamic":
+        assert torch.equal(a[3], b[3])
+    assert not zero.any()
+
+
 @pytest.mark.parametrize("G,R_s,C,i1,cnt,gmode,sos", [
     (2, 96, 300, 64, 64, 0, 1.0),        # ragged row and column tiles
     (4, 256, 1024, 128, 128, 0, 1.0),    # interior 128x128 tiles only
