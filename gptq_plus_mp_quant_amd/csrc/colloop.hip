@@ -295,7 +295,16 @@ __device__ __forceinline__ void quant_block_body(const QBArgs& a, int bx, int by
     return;
   }
 
-  // column-serial loop (:1296-1367); column i = 16 m + r is quantised by lane r (slot m)
+  // column-serial loop (:1296-1367); column i = 16 m + r is quantised by lane r (slot m).  The
+  // updates of a column reach the slots k >= m only: slots below hold finished columns, which
+  // the reference no longer updates either (W1[:, i:]).  Each lane keeps the codes and errors
+  // of its own slots in registers and stores them after the loop.
+  float ccode[NS], cerr[NS];
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    ccode[k] = 0.0f;
+    cerr[k] = 0.0f;
+  }
   auto column = [&](auto mc, auto rc, bool with_gh) __attribute__((always_inline)) {
     constexpr int m = decltype(mc)::value, r = decltype(rc)::value;
     const int i = QL * m + r;
@@ -307,14 +316,12 @@ __device__ __forceinline__ void quant_block_body(const QBArgs& a, int bx, int by
     const float code = rq_quant_code(x, s, lo, hi);
     const float q = s * code;
     const float e = row_bcast<r>(((x - q) - geff(m)) / d);
-    if (valid && t == r) {
-      crow[i] = (code != code) ? RQ_CODE_NAN : (int16_t)code;
-      erow[i] = e;
-    }
+    ccode[m] = (t == r) ? code : ccode[m];
+    cerr[m] = (t == r) ? e : cerr[m];
     if constexpr (SURR) {
       const float zi = with_gh ? row_bcast<r>(zz[m]) : 0.0f;
 #pragma unroll
-      for (int k = 0; k < NS; ++k) {
+      for (int k = m; k < NS; ++k) {
         const float ge = geff(k);
         const float upd = e * h[k];
         w[k] = w[k] - (upd + ge);
@@ -323,7 +330,7 @@ __device__ __forceinline__ void quant_block_body(const QBArgs& a, int bx, int by
     } else if (with_gh) {
       const float zi = row_bcast<r>(zz[m]);
 #pragma unroll
-      for (int k = 0; k < NS; ++k) {
+      for (int k = m; k < NS; ++k) {
         const float upd = e * h[k];
         if constexpr (GM == 3) w[k] = w[k] - a.sos * (upd + gh[k]);
         else w[k] = w[k] - (upd + gh[k]);
@@ -331,7 +338,7 @@ __device__ __forceinline__ void quant_block_body(const QBArgs& a, int bx, int by
       }
     } else {
 #pragma unroll
-      for (int k = 0; k < NS; ++k) {
+      for (int k = m; k < NS; ++k) {
         if constexpr (GM == 3) w[k] = w[k] - a.sos * (e * h[k] + gh[k]);
         else w[k] = w[k] - (e * h[k] + gh[k]);
       }
@@ -346,6 +353,16 @@ __device__ __forceinline__ void quant_block_body(const QBArgs& a, int bx, int by
   };
   if (use_gh) all_columns(true);
   else all_columns(false);
+  if (valid) {
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const int col = QL * k + t;
+      if (col < count) {
+        crow[col] = (ccode[k] != ccode[k]) ? RQ_CODE_NAN : (int16_t)ccode[k];
+        erow[col] = cerr[k];
+      }
+    }
+  }
 }
 
 template <int NS, int GM>
