@@ -1542,29 +1542,25 @@ int kernel_slots(K kfn, int threads, int which) {
 int hessian_slots() { return kernel_slots(k_hessian_accum<__half>, HTHREADS, 0); }
 int split_slots() { return kernel_slots(k_hessian_split<__half, 2>, XTHREADS, 1); }
 
-// Items of the last, partly filled round and the slice count that fills rounds best: the
-// tail finishes in ceil(tail * S / slots) / S rounds, plus a little per slice for its partial
-// tile and the last slice's reduction (S <= maxS, at least 4 token slabs per slice).  The
-// split kernels reduce up to 16 slices, the fp32 kernel up to 8.
+// Items of the last, partly filled round and their slice count: the most slices that still
+// fit the tail into one round (S = slots / tail, S <= maxS, at least 4 token slabs per slice).
+// Measured at C = 4096 (tails of 32, 64, 96 and 136 items on 256 slots: best S = 6-8, 3-4, 2 and
+// 1-3) and 14336 (240 items: 1).  Splitting further, into more rounds, loses: besides each
+// slice's partial tile and the last slice's reduction, the power-limited clock rises when fewer
+// CUs are busy, so a tail on part of the GPU costs less than its idle share.  The split kernels
+// reduce up to 16 slices, the fp32 kernel up to 8.
 void tail_split(int64_t total, int64_t nslab, int slots, int maxS, int* tail, int* S) {
   *tail = 0;
   *S = 1;
   if (slots <= 0 || total <= 0) return;
   const int64_t t = total % slots;
   if (t == 0) return;
-  double best = 1.0;
-  int bestS = 1;
-  for (int cand = 2; cand <= maxS; ++cand) {
-    if (nslab < 4 * cand) break;
-    const double rounds = (double)((t * cand + slots - 1) / slots) / cand + 0.003 * cand;
-    if (rounds < best - 0.05) {
-      best = rounds;
-      bestS = cand;
-    }
-  }
-  if (bestS > 1) {
+  int64_t s = slots / t;
+  if (s > maxS) s = maxS;
+  while (s > 1 && nslab < 4 * s) --s;
+  if (s > 1) {
     *tail = (int)t;
-    *S = bestS;
+    *S = (int)s;
   }
 }
 
