@@ -452,10 +452,13 @@ def _kernel_name(full):
     return n[:60]
 
 
-def algorithmic_work(cfg):
+def algorithmic_work(cfg, lookahead=False):
     """Algorithmic work per unit (one linear, or one layer) of the kernels the table reports:
     (bytes, flops) by kernel-name prefix.  Bytes are those the operation must move at least once
-    (inputs read, outputs written); flops count the reference's arithmetic (fp32 unless noted)."""
+    (inputs read, outputs written); flops count the reference's arithmetic (fp32 unless noted).
+    With `lookahead` (the run used k_block_lookahead), k_quant_block quantises only each linear's
+    first block, and k_block_lookahead does every other block's column loop plus the whole
+    trailing update."""
     B = cfg["blocksize"]
     linears = [(R, C) for _, R, C, _ in LAYER8B] if cfg["kind"] == "layer" else [(cfg["R"], cfg["C"])]
     G, ntok = cfg["G"], cfg["N"] * cfg["T"]
@@ -470,9 +473,14 @@ def algorithmic_work(cfg):
         add("k_find_params", 2.0 * R * C + 8 * R)
         add("k_gather_w", (2.0 + 4.0) * R * C)                 # fp16 W read, permuted fp32 written
         add("k_gather_g", 8.0 * R * C)
-        add("k_gather_h_rows", 8.0 * G * C * C)
-        add("k_quant_block", 9.0 * R * C, 2.0 * R * C * B)     # W read, fp32 Q + int8 code written
-        add("k_trailing_w", 8.0 * R * C, trail)
+        # one H row per workgroup: 512 threads x 8 rows in flight from C = 8192 on (params.hip)
+        add("k_gather_h_rows<512, 8>" if C >= 8192 else "k_gather_h_rows<256, 1>", 8.0 * G * C * C)
+        f0 = min(B, C) / C if lookahead else 1.0             # share of the columns k_quant_block runs
+        add("k_quant_block", 9.0 * R * C * f0, 2.0 * R * C * B * f0)   # W read, fp32 Q + int8 code written
+        if lookahead:
+            add("k_block_lookahead", 9.0 * R * C * (1.0 - f0) + 8.0 * R * C, trail + 2.0 * R * C * B * (1.0 - f0))
+        else:
+            add("k_trailing_w", 8.0 * R * C, trail)
         add("k_hessian_finalize64", 6.0 * G * C * C)           # upper triangle read, both halves written
         add("k_writeback", 2.0 * R * C + 2.0 * R * C)
         add("k_panel_update", 0.0, G * (2.0 / 3.0) * C ** 3)   # fp64: trailing factor + L^-1 rows
@@ -491,18 +499,19 @@ def algorithmic_work(cfg):
 def stats_table(path, cfg, units, config):
     """Markdown table of a rocprofv3 --stats kernel CSV, with achieved rates where the kernel's
     algorithmic work per unit is known."""
-    work = algorithmic_work(cfg)
     rows = []
     with open(path) as f:
         for r in csv.DictReader(f):
             rows.append((_kernel_name(r["Name"]), int(r["Calls"]), float(r["TotalDurationNs"]) / 1e6,
                          float(r["AverageNs"]) / 1e3, float(r["Percentage"])))
+    work = algorithmic_work(cfg, lookahead=any("k_block_lookahead" in r[0] for r in rows))
     rows.sort(key=lambda x: -x[2])
     print(f"| kernel | calls | total (ms) | per unit (ms) | average (us) | % | algorithmic work per unit | achieved |")
     print("|---|---:|---:|---:|---:|---:|---|---|")
     for name, calls, tot, avg, pct in rows[:24]:
         per = tot / units
-        key = next((k for k in work if name.split("<")[0].split()[-1] == k), None)
+        bare = name[5:] if name.startswith("void ") else name
+        key = bare if bare in work else next((k for k in work if bare.split("<")[0] == k), None)
         wtxt = ach = ""
         if key:
             b, fl = work[key]
@@ -512,7 +521,7 @@ def stats_table(path, cfg, units, config):
                 tf = fl / (per * 1e-3) / 1e12
                 wtxt = f"{fl / 1e9:.1f} GFLOP" + (f", {b / 1e6:.0f} MB" if b else "")
                 ach = f"{tf:.1f} TF/s" + (f" ({100 * tf / peak:.1f} % of {peak})" if peak else "")
-                if b and key == "k_quant_block":
+                if b and key in ("k_quant_block", "k_block_lookahead"):
                     ach += f"; {b / (per * 1e-3) / 1e9:.0f} GB/s"
             else:
                 gbs = b / (per * 1e-3) / 1e9
