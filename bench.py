@@ -471,8 +471,10 @@ def algorithmic_work(cfg, lookahead=False):
         nb = (C + B - 1) // B
         trail = sum(2.0 * R * B * (C - min(C, (k + 1) * B)) for k in range(nb))
         add("k_find_params", 2.0 * R * C + 8 * R)
-        add("k_gather_w", (2.0 + 4.0) * R * C)                 # fp16 W read, permuted fp32 written
-        add("k_gather_g", 8.0 * R * C)
+        # row-staged gathers (params.hip): 1024 threads per workgroup for rows above 32 KB
+        nt = lambda esize: 1024 if C * esize > 32 * 1024 else 256
+        add(f"k_gather_rows<{nt(2)}, __half>", (2.0 + 4.0) * R * C)   # fp16 W read, permuted fp32 written
+        add(f"k_gather_rows<{nt(4)}, float>", 8.0 * R * C)            # G read, permuted copy written
         # one H row per workgroup: 512 threads x 8 rows in flight from C = 8192 on (params.hip)
         add("k_gather_h_rows<512, 8>" if C >= 8192 else "k_gather_h_rows<256, 1>", 8.0 * G * C * C)
         f0 = min(B, C) / C if lookahead else 1.0             # share of the columns k_quant_block runs
@@ -482,7 +484,7 @@ def algorithmic_work(cfg, lookahead=False):
         else:
             add("k_trailing_w", 8.0 * R * C, trail)
         add("k_hessian_finalize64", 6.0 * G * C * C)           # upper triangle read, both halves written
-        add("k_writeback", 2.0 * R * C + 2.0 * R * C)
+        add(f"k_writeback_rows<{nt(2)}, __half>", 2.0 * R * C + 2.0 * R * C)   # int16 codes read, fp16 out
         add("k_panel_update", 0.0, G * (2.0 / 3.0) * C ** 3)   # fp64: trailing factor + L^-1 rows
     inputs = {4096: 0, 14336: 0}
     if cfg["kind"] == "layer":
