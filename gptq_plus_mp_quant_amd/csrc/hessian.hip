@@ -1030,27 +1030,54 @@ __global__ __launch_bounds__(256) void k_xprep(const TX* __restrict__ X, int64_t
   const int ch = blockIdx.y;
   const int64_t t0 = (int64_t)ch * XTOK;
   const uint16_t* Xb = reinterpret_cast<const uint16_t*>(X);
-  // load: 8 column groups (8 columns, 16 B) x 128 token pairs; lane = group + 8 * pair
-#pragma unroll
-  for (int v = tid; v < 8 * (XTOK / 2); v += 256) {
+  // load: 8 column groups (8 columns, 16 B) x 128 token pairs; lane = group + 8 * pair.  A
+  // block inside the chunk (every workgroup but the edge ones) issues its 8 loads per thread
+  // before using any; the edge blocks load element by element with bounds checks.
+  auto put = [&](int v, uint4 q0, uint4 q1) __attribute__((always_inline)) {
     const int grp = v & 7, tp = v >> 3;
-    const int cb = c0 + 8 * grp;
-    uint32_t e0[8], e1[8];
+    const uint32_t a[4] = {q0.x, q0.y, q0.z, q0.w}, b[4] = {q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int64_t t = t0 + 2 * tp + h;
-      uint32_t* e = h ? e1 : e0;
-      if (vec_ok && cb + 8 <= C && t < ntok) {
-        const uint4 q = *reinterpret_cast<const uint4*>(Xb + t * ldx + cb);
-        e[0] = q.x & 0xffffu; e[1] = q.x >> 16; e[2] = q.y & 0xffffu; e[3] = q.y >> 16;
-        e[4] = q.z & 0xffffu; e[5] = q.z >> 16; e[6] = q.w & 0xffffu; e[7] = q.w >> 16;
-      } else {
+    for (int k = 0; k < 4; ++k) {
+      tile[8 * grp + 2 * k][tp] = (a[k] & 0xffffu) | (b[k] << 16);
+      tile[8 * grp + 2 * k + 1][tp] = (a[k] >> 16) | (b[k] & 0xffff0000u);
+    }
+  };
+  if (vec_ok && c0 + XPC <= C && t0 + XTOK <= ntok) {
+    uint4 q[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) e[k] = (t < ntok && cb + k < C) ? Xb[t * ldx + cb + k] : 0u;
-      }
+    for (int it = 0; it < 4; ++it) {
+      const int v = tid + 256 * it;
+      const int grp = v & 7, tp = v >> 3;
+      const uint16_t* src = Xb + (t0 + 2 * tp) * ldx + c0 + 8 * grp;
+      q[2 * it] = *reinterpret_cast<const uint4*>(src);
+      q[2 * it + 1] = *reinterpret_cast<const uint4*>(src + ldx);
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) tile[8 * grp + k][tp] = e0[k] | (e1[k] << 16);
+    for (int it = 0; it < 4; ++it) put(tid + 256 * it, q[2 * it], q[2 * it + 1]);
+  } else {
+#pragma unroll
+    for (int v = tid; v < 8 * (XTOK / 2); v += 256) {
+      const int grp = v & 7, tp = v >> 3;
+      const int cb = c0 + 8 * grp;
+      uint32_t e[2][8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t t = t0 + 2 * tp + h;
+        if (vec_ok && cb + 8 <= C && t < ntok) {
+          const uint4 q = *reinterpret_cast<const uint4*>(Xb + t * ldx + cb);
+          e[h][0] = q.x & 0xffffu; e[h][1] = q.x >> 16; e[h][2] = q.y & 0xffffu; e[h][3] = q.y >> 16;
+          e[h][4] = q.z & 0xffffu; e[h][5] = q.z >> 16; e[h][6] = q.w & 0xffffu; e[h][7] = q.w >> 16;
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) e[h][k] = (t < ntok && cb + k < C) ? Xb[t * ldx + cb + k] : 0u;
+        }
+      }
+      const uint4 q0 = make_uint4(e[0][0] | (e[0][1] << 16), e[0][2] | (e[0][3] << 16), e[0][4] | (e[0][5] << 16),
+                                  e[0][6] | (e[0][7] << 16));
+      const uint4 q1 = make_uint4(e[1][0] | (e[1][1] << 16), e[1][2] | (e[1][3] << 16), e[1][4] | (e[1][5] << 16),
+                                  e[1][6] | (e[1][7] << 16));
+      put(v, q0, q1);
+    }
   }
   __syncthreads();
   // store: the block's two 32-column groups x 16 steps, fragment-major: chunk (cb, kb) is 1 KB,
@@ -1185,22 +1212,44 @@ __global__ __launch_bounds__(256) void k_xprep32(const float* __restrict__ X, in
   const int c0 = blockIdx.x * XPC;
   const int ch = blockIdx.y;
   const int64_t t0 = (int64_t)ch * XTOK;
-  // load: 16 float4 per token row, 16 rows per pass
-#pragma unroll 4
-  for (int v = tid; v < 16 * XTOK; v += 256) {
-    const int q = v & 15, tr = v >> 4;
-    const int cb = c0 + 4 * q;
-    const int64_t t = t0 + tr;
-    float e[4];
-    if (vec_ok && cb + 4 <= C && t < ntok) {
-      const float4 f = *reinterpret_cast<const float4*>(X + t * ldx + cb);
-      e[0] = f.x; e[1] = f.y; e[2] = f.z; e[3] = f.w;
-    } else {
+  // load: 16 float4 per token row, 16 rows per pass.  A block inside the chunk issues 8 loads
+  // per thread before using any; the edge blocks check every element.
+  if (vec_ok && c0 + XPC <= C && t0 + XTOK <= ntok) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) e[k] = (t < ntok && cb + k < C) ? X[t * ldx + cb + k] : 0.0f;
+    for (int v0 = tid; v0 < 16 * XTOK; v0 += 256 * 8) {
+      float4 f[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int v = v0 + 256 * u;
+        f[u] = *reinterpret_cast<const float4*>(X + (t0 + (v >> 4)) * ldx + c0 + 4 * (v & 15));
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int v = v0 + 256 * u;
+        const int q = v & 15, tr = v >> 4;
+        tile[4 * q][tr] = f[u].x;
+        tile[4 * q + 1][tr] = f[u].y;
+        tile[4 * q + 2][tr] = f[u].z;
+        tile[4 * q + 3][tr] = f[u].w;
+      }
     }
+  } else {
+#pragma unroll 4
+    for (int v = tid; v < 16 * XTOK; v += 256) {
+      const int q = v & 15, tr = v >> 4;
+      const int cb = c0 + 4 * q;
+      const int64_t t = t0 + tr;
+      float e[4];
+      if (vec_ok && cb + 4 <= C && t < ntok) {
+        const float4 f = *reinterpret_cast<const float4*>(X + t * ldx + cb);
+        e[0] = f.x; e[1] = f.y; e[2] = f.z; e[3] = f.w;
+      } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) tile[4 * q + k][tr] = e[k];
+        for (int k = 0; k < 4; ++k) e[k] = (t < ntok && cb + k < C) ? X[t * ldx + cb + k] : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) tile[4 * q + k][tr] = e[k];
+    }
   }
   __syncthreads();
   const int ncb = (C + 31) / 32;
