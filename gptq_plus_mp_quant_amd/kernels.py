@@ -274,7 +274,11 @@ def quant_block(Wp, Hinv_all, GH, Z, R_s, i1, count, qmode, scale, col_group, dy
     if Hinv_all.shape != (R // R_s, C, C):
         raise ValueError("quant_block: Hinv_all must be [G, C, C]")
     lda = _surrogate(gmode, anchor, beta, R, C)
-    _cout(Wp, "Wp"), _cin(Hinv_all, "Hinv_all"), _cin(GH, "GH"), _cin(Z, "Z")
+    _cout(Wp, "Wp")
+    for t, n in ((Hinv_all, "Hinv_all"), (GH, "GH"), (Z, "Z")):
+        nat.require_gpu(t, n)
+        if t.dtype != _f32:
+            raise ValueError(f"{n} must be {_f32}")
     if not (Hinv_all.is_contiguous() and GH.stride(1) == 1 and Z.stride(1) == 1):
         raise ValueError("quant_block: Hinv_all must be contiguous, GH / Z row-major")
     nat.call("rq_quant_block", nat.ptr(Wp), Wp.stride(0), nat.ptr(Hinv_all), C, nat.ptr(GH), nat.ptr(Z),
@@ -291,7 +295,8 @@ def quant_block_lookahead(Wp, Hinv_all, R_s, i1, count, err, count_next, qmode, 
     R, C = Wp.shape
     if Hinv_all.shape != (R // R_s, C, C) or not Hinv_all.is_contiguous():
         raise ValueError("quant_block_lookahead: Hinv_all must be contiguous [G, C, C]")
-    _cout(Wp, "Wp"), _cout(err_next, "err_next"), _cin(err, "err")
+    _cout(Wp, "Wp"), _cout(err_next, "err_next")
+    err = _cin(err, "err")
     if err.data_ptr() == err_next.data_ptr():
         raise ValueError("quant_block_lookahead: err and err_next must be different buffers")
     nat.call("rq_quant_block_lookahead", nat.ptr(Wp), Wp.stride(0), nat.ptr(Hinv_all), C, R, R_s, int(i1),

@@ -392,6 +392,46 @@ def test_cholesky_retry_schedule(neg):
         assert torch.equal(Hinv.cpu(), torch.eye(80))
 
 
+def test_cholesky_near_singular_dense():
+    """A dense H whose damped working copy is positive definite by a margin of ~1e-8 of its
+    norm: the reference's fp32 chain (potrf, cholesky_inverse, potrf) breaks down at
+    damp_percent 0.01 and succeeds on the retry at 0.0115; the fp64 factorisation succeeds at
+    0.01 (the documented difference in the number of retries).  Pinned: the oracle's attempt
+    count, this build's, the factor at 0.01 against fp64 truth on the same damped matrix, and
+    the factor at the oracle's damping against the oracle's."""
+    from gptq_plus_mp_quant_amd import GPTQPlus
+    C = 64
+    r = rng(0)
+    Q, _ = np.linalg.qr(r.standard_normal((C, C)))
+    lam = np.linspace(1.0, 2.0, C)
+    delta = 1e-6
+    lam[0] = -0.01 * (1 - delta) * lam[1:].sum() / (C + 0.01 * (1 - delta))   # lam_min = -(1 - delta) damp
+    H = torch.from_numpy((Q * lam) @ Q.T).float()
+    _, Hv_o, p_o, fb_o, att_o = hessian_inverse_with_fallback(H, 0.01)
+    # 2 attempts on the x86 hosts measured (MKL); the breakdown depends on the LAPACK build
+    print(f"near-singular C={C}: fp32 reference chain attempts {att_o} (damp {p_o:.4f})", flush=True)
+    assert not fb_o
+
+    layer = torch.nn.Linear(C, 8, bias=False).to(DEV)
+    g = GPTQPlus(layer, torch.ones(1, 1, 1), torch.zeros(8, C), 1, 0.0, 0.0)
+    ws = K.chol_workspace(C, DEV)
+    Hw = H.to(DEV).clone()
+    Hinv = torch.empty(C, C, device=DEV)
+    (p, fb, att), = g._hessian_inverse(Hw, Hinv, None, ws, 0.01)
+    assert (att, fb) == (1, False) and abs(p - 0.01) < 1e-12 and att_o >= att
+    Hd = Hw.double().cpu()                            # the damped working copy the chain factored
+    assert float(torch.linalg.eigvalsh(Hd)[0]) > 0.0
+    U = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(Hd)), upper=True)
+    assert rel_fro(Hinv, U.float()) <= 1e-5
+
+    if att_o > 1:                                     # at the reference's final damping both agree
+        Hw2 = H.to(DEV).clone()
+        Hinv2 = torch.empty(C, C, device=DEV)
+        (p2, fb2, att2), = g._hessian_inverse(Hw2, Hinv2, None, ws, p_o)
+        assert (att2, fb2) == (1, False)
+        assert rel_fro(Hinv2, Hv_o) <= 1e-4
+
+
 def _check_terms(G, Hinv, beta, Z, GH, beta_o):
     """beta against the oracle's to an absolute 2^-21: the reference's 1 - sqrt(1 - ratio) in
     fp32 cancels (beta ~ 1e-4 keeps ~10 of its 24 bits), so a last-bit difference of ratio --
