@@ -715,3 +715,72 @@ def test_trailing_update_w_only(G, R_s, C, i1, cnt, gmode, sos):
             exact = W[rows, i2:] - (f * second if gmode == 3 else second)
             assert torch.equal(Wf[rows, i2:].cpu(), exact)
     assert not zero.any()
+
+
+@pytest.mark.parametrize("R_s,C,wdt,ldpad,perm_on", [
+    (40, 136, torch.float16, 0, True),      # 16-byte rows, 256 threads
+    (33, 130, torch.bfloat16, 3, True),     # row length / stride not whole 16 bytes: element loads
+    (9, 20000, torch.float16, 0, True),     # fp16 rows above 32 KB (1024 threads), fp32 G rows above 64 KB
+    (6, 45000, torch.float32, 0, False),    # fp32 rows above 160 KB: the column kernels
+    (5, 1, torch.float32, 0, True),         # C = 1: no index scratch in H_sub
+])
+def test_prepare_subgroup_gathers_exact(R_s, C, wdt, ldpad, perm_on):
+    """rq_prepare_subgroup against torch indexing, bit for bit: W_sub = W[:, perm] with dead
+    columns (H_g[p, p] == 0) zeroed, G_sub = G[:, perm], H_sub = H_g[perm][:, perm] with a dead
+    diagonal set to 1; then rq_writeback's un-permute of int16 codes against torch."""
+    r = rng(R_s + C)
+    ld = C + ldpad
+    Wfull = torch.from_numpy(r.standard_normal((R_s, ld)).astype(np.float32)).to(wdt)
+    W = Wfull.to(DEV)[:, :C] if ldpad else Wfull.to(DEV)
+    G = torch.from_numpy(r.standard_normal((R_s, C)).astype(np.float32)).to(DEV)
+    d = torch.from_numpy(r.standard_normal(C).astype(np.float32) ** 2 + 0.5)
+    dead = torch.from_numpy(r.random(C) < 0.1)
+    d[dead] = 0.0
+    if C <= 2048:
+        A = torch.from_numpy(r.standard_normal((C, C)).astype(np.float32)) * 0.01
+        Hg = (A + A.T)
+        Hg[torch.arange(C), torch.arange(C)] = d
+        Hg[dead, :] = 0.0
+        Hg[:, dead] = 0.0
+    else:
+        Hg = None
+    perm = torch.from_numpy(r.permutation(C)).to(torch.int64) if perm_on else torch.arange(C)
+    W_sub = torch.full((R_s, C), 7.0, device=DEV)
+    G_sub = torch.full((R_s, C), 7.0, device=DEV)
+    if Hg is not None:
+        Hg_d = Hg.to(DEV).contiguous()
+        H_sub = torch.empty(C, C, device=DEV)
+    else:                                             # diagonal H: the W / G gathers are the point
+        Hg_d = torch.zeros(C, C, device=DEV)
+        Hg_d[torch.arange(C), torch.arange(C)] = d.to(DEV)
+        H_sub = torch.empty(C, C, device=DEV)
+    K.prepare_subgroup(W, G, Hg_d, perm.to(DEV) if perm_on else None, W_sub, G_sub, H_sub)
+    torch.cuda.synchronize()
+    Wc = W.float().cpu()
+    pd = perm
+    exp_W = Wc[:, pd].clone()
+    exp_W[:, dead[pd]] = 0.0
+    assert torch.equal(W_sub.cpu(), exp_W)
+    assert torch.equal(G_sub.cpu(), G.cpu()[:, pd])
+    if C <= 20000:                                    # H_sub checked where the host copies stay small
+        pg = pd.to(DEV)
+        exp_H = Hg_d[pg][:, pg]
+        dd = dead[pd].nonzero().flatten().to(DEV)
+        exp_H[dd, dd] = 1.0
+        assert torch.equal(H_sub, exp_H)
+    del Hg_d, H_sub
+
+    # write-back: codes in the permuted order -> q[:, c] = fp16(scale[r] * codes[r, invperm[c]])
+    codes = torch.from_numpy(r.integers(-8, 8, size=(R_s, C)).astype(np.int16)).to(DEV)
+    codes[0, 0] = -32768                              # a NaN weight
+    scale = torch.from_numpy(r.random(R_s).astype(np.float32) * 0.1 + 0.01).to(DEV)
+    invperm = torch.argsort(perm).to(DEV)
+    q = torch.empty(R_s, C, dtype=torch.float16, device=DEV)
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    K.writeback(codes, invperm, nat.RQ_QMODE_CHANNEL, scale, None, None, 128, q, nan_flag=flag)
+    torch.cuda.synchronize()
+    cf = codes.cpu().float()
+    cf[codes.cpu() == -32768] = float("nan")
+    exp_q = (scale.cpu().unsqueeze(1) * cf[:, invperm.cpu()]).to(torch.float16)
+    torch.testing.assert_close(q.cpu(), exp_q, rtol=0, atol=0, equal_nan=True)
+    assert int(flag.item()) == 1
