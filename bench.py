@@ -483,6 +483,7 @@ def algorithmic_work(cfg, lookahead=False):
             add("k_block_lookahead", 9.0 * R * C * (1.0 - f0) + 8.0 * R * C, trail + 2.0 * R * C * B * (1.0 - f0))
         else:
             add("k_trailing_w", 8.0 * R * C, trail)
+        add("k_trailing_z", 20.0 * R * C, 3.0 * trail)         # GPTQ+ terms: three chains; W, GH, Z
         add("k_hessian_finalize64", 6.0 * G * C * C)           # upper triangle read, both halves written
         add(f"k_writeback_rows<{nt(2)}, __half>", 2.0 * R * C + 2.0 * R * C)   # int16 codes read, fp16 out
         add("k_panel_update", 0.0, G * (2.0 / 3.0) * C ** 3)   # fp64: trailing factor + L^-1 rows
