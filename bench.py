@@ -50,7 +50,7 @@ TRAFFIC_JSON = os.path.join(ROOT, "profiles", "hessian_traffic.json")
 
 BASE = dict(R=4096, C=4096, G=4, N=128, T=2048, bsz=16, bits=4, sym=False, blocksize=128,
             percdamp=0.01, alpha=0.0, ref_loss=0.0, outliers=8, seed=20251201, wscale=0.02)
-# BASELINE.md numbering: cfgK = BASELINE.json configs[K-1]
+# cfgK = BASELINE.json configs[K-1] (numbered from 1)
 CONFIGS = {
     "cfg1": dict(BASE, G=1, gptq_plus=False, kind="linear"),
     "cfg2": dict(BASE, kind="linear"),
@@ -662,7 +662,7 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", choices=sorted(CONFIGS), default="cfg3",
-                    help="BASELINE.md numbering, cfgK = configs[K-1]; default cfg3 (the Llama-3-8B layer)")
+                    help="cfgK = BASELINE.json configs[K-1]; default cfg3 (the Llama-3-8B layer)")
     ap.add_argument("--alpha", type=float, default=0.0, help="GPTQ+ alpha (with --ref-loss > 0: beta != 0)")
     ap.add_argument("--ref-loss", type=float, default=0.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
