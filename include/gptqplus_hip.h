@@ -142,7 +142,8 @@ int rq_act_order_perm(const float* act_sq, int C, int64_t* perm, int64_t* invper
  * dead[c] = (H_g[c,c] == 0).  W_sub[r,j] = dead[p_j] ? 0 : w[r, p_j] (fp32),
  * G_sub[r,j] = grad[r, p_j] (skipped when grad == NULL), H_sub[i,j] = H_g[p_i, p_j] with
  * H_sub[i,i] = 1 where dead[p_i]; p = perm (identity when perm == NULL).  w/grad point at the
- * subgroup's first row. */
+ * subgroup's first row.  H_sub must not overlap H_g, w, grad, W_sub or G_sub: its first 2*C
+ * words carry the gathers' column indices on the stream before the H gather writes it. */
 int rq_prepare_subgroup(const void* w, int w_dtype, int64_t ldw, const float* grad, int64_t ldg,
                         const float* H_g, int R_s, int C, const int64_t* perm, float* W_sub,
                         int64_t ld_wsub, float* G_sub, int64_t ld_gsub, float* H_sub, void* stream);
