@@ -1,0 +1,84 @@
+"""bench.py's report helpers on synthetic rocprofv3 CSVs (no GPU): the kernel-statistics table
+credits each kernel with its algorithmic work (the look-ahead column loop with the trailing
+update and every block but the first, the row gathers by variant), and the counter table's
+MFMA-busy arithmetic."""
+import contextlib
+import csv
+import io
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+import bench  # noqa: E402
+
+
+def _stats_csv(path, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage"])
+        tot = sum(r[2] for r in rows)
+        for name, calls, ns in rows:
+            w.writerow([name, calls, ns, ns / calls, 100.0 * ns / tot])
+
+
+def _table(path, cfg, units):
+    buf = io.StringIO()
+    with contextlib.redirect_stdout(buf):
+        bench.stats_table(path, bench.CONFIGS[cfg], units, cfg)
+    return {line.split("|")[1].strip().strip("`"): line for line in buf.getvalue().splitlines()[2:]}
+
+
+def test_stats_table_credits_lookahead_and_gathers(tmp_path):
+    cfg = bench.CONFIGS["cfg2"]
+    R, C, B = cfg["R"], cfg["C"], cfg["blocksize"]
+    p = str(tmp_path / "stats.csv")
+    ms = 1e6
+    _stats_csv(p, [("void (anonymous namespace)::k_block_lookahead<8>(QBArgs, TwArgs, int, int)", 31, 1.8 * ms),
+                   ("void (anonymous namespace)::k_quant_block<8, 0>(QBArgs)", 1, 0.03 * ms),
+                   ("void (anonymous namespace)::k_gather_rows<256, __half>(args)", 4, 0.036 * ms),
+                   ("void (anonymous namespace)::k_gather_h_rows<256, 1>(args)", 4, 0.134 * ms)])
+    t = _table(p, "cfg2", 1)
+    nb = (C + B - 1) // B
+    trail = sum(2.0 * R * B * (C - min(C, (k + 1) * B)) for k in range(nb))
+    f_la = trail + 2.0 * R * C * B * (1 - B / C)
+    assert f"{f_la / 1e9:.1f} GFLOP" in t["void k_block_lookahead<8>"]
+    assert f"{f_la / 1.8e-3 / 1e12:.1f} TF/s" in t["void k_block_lookahead<8>"]
+    # k_quant_block then runs only the first block of each linear
+    assert f"{2.0 * R * C * B * (B / C) / 1e9:.1f} GFLOP" in t["void k_quant_block<8, 0>"]
+    assert f"{6.0 * R * C / 1e6:.0f} MB" in t["void k_gather_rows<256, __half>"]
+    assert f"{8.0 * cfg['G'] * C * C / 1e6:.0f} MB" in t["void k_gather_h_rows<256, 1>"]
+
+
+def test_stats_table_without_lookahead(tmp_path):
+    cfg = bench.CONFIGS["cfg2"]
+    R, C, B = cfg["R"], cfg["C"], cfg["blocksize"]
+    p = str(tmp_path / "stats.csv")
+    _stats_csv(p, [("void (anonymous namespace)::k_quant_block<8, 0>(QBArgs)", 32, 0.9e6),
+                   ("void (anonymous namespace)::k_trailing_z<false>(TzArgs)", 31, 2.5e6)])
+    t = _table(p, "cfg2", 1)
+    assert f"{2.0 * R * C * B / 1e9:.1f} GFLOP" in t["void k_quant_block<8, 0>"]
+    nb = (C + B - 1) // B
+    trail = sum(2.0 * R * B * (C - min(C, (k + 1) * B)) for k in range(nb))
+    assert f"{3 * trail / 1e9:.1f} GFLOP" in t["void k_trailing_z<false>"]
+
+
+def test_counters_table_mfma_busy(tmp_path):
+    p = str(tmp_path / "pmc.csv")
+    with open(p, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"])
+        for d in (1, 2):
+            for name, v in (("SQ_VALU_MFMA_BUSY_CYCLES", 640.0), ("GRBM_GUI_ACTIVE", 10.0),
+                            ("SQ_INSTS_MFMA", 100.0), ("SQ_INSTS_VALU", 350.0), ("SQ_INSTS_LDS", 70.0),
+                            ("SQ_LDS_BANK_CONFLICT", 0.0)):
+                w.writerow([d, "void k_hessian_split<__half, 2>(args)", name, v, 0, 1000])
+    buf = io.StringIO()
+    with contextlib.redirect_stdout(buf):
+        bench.counters_table(p)
+    row = buf.getvalue().splitlines()[2]
+    # 1280 busy SIMD-cycles over 20 x 128 SIMD-cycles = 50 %
+    assert "| 2 |" in row and "50.0 %" in row and "| 3.50 | 0.70 | 0.00 |" in row
