@@ -443,6 +443,25 @@ def gemm_calibration(dev):
         ms = e0.elapsed_time(e1) / reps
         out[name] = {"n": n, "ms": round(ms, 3), "tflops": round(2 * n ** 3 / ms / 1e9, 1)}
         del a, b, c
+    # fp64 rank-K updates C -= A B of the Cholesky chain's panel shapes (trailing rows x rows,
+    # K = panel width): the practical ceiling the panel-update kernel is measured against
+    out["fp64_rank_k"] = []
+    for m, k in ((4096, 256), (13824, 512), (13824, 256), (27648, 512)):
+        a = torch.randn(m, k, device=dev, dtype=torch.float64)
+        b = torch.randn(k, m, device=dev, dtype=torch.float64)
+        c = torch.randn(m, m, device=dev, dtype=torch.float64)
+        for _ in range(2):
+            c.addmm_(a, b, alpha=-1.0)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            c.addmm_(a, b, alpha=-1.0)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 5
+        out["fp64_rank_k"].append({"m": m, "k": k, "ms": round(ms, 3), "tflops": round(2 * m * m * k / ms / 1e9, 1)})
+        del a, b, c
     print(json.dumps({"gemm_calibration": out}), flush=True)
 
 
