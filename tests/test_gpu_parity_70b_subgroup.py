@@ -1,0 +1,120 @@
+"""Parity against the oracle at the full width of BASELINE configs[4] (Llama-3-70B down_proj,
+C = 28672): one subgroup's share of the rows (R = 2048 = 8192 / NUM_GROUPS), NUM_GROUPS = 1 on
+it, 16 x 2048 tokens with outlier channels, w4 asymmetric per-channel, act_order, B = 128.  The
+oracle (the reference's op sequence on the host CPU) runs act_square and fasterquant on the GPU's
+finalized H; its fp32 LAPACK chain at this width takes tens of seconds, the whole test about two
+minutes.
+
+- act_square bit for bit and the act_order permutation equal to the oracle's argsort;
+- with the oracle's fp32 H^-1 injected: codes and the written weight equal (Z = 0);
+- with the GPU's fp64 chain: H^-1 within 1e-4 of the oracle's and the reconstruction error
+  within 0.5 % of the oracle's.  At this width the reference's fp32 LAPACK chain is ~3e-6 from an
+  fp64 factorisation of the same damped matrix (checked here with torch's fp64 factorisation on
+  the GPU), the GPU's chain within fp32 rounding of it, so every code near a rounding boundary
+  follows the reference's chain error: 0.25 % of the codes flip (measured), while the two
+  reconstruction errors agree within 4e-5 relative.  The GPU's factor must be the closer one;
+  the flips are reported and bounded at 0.5 %.
+The case's numbers are printed and appended to RQ_PARITY_LOG (JSON lines) when it is set.
+"""
+import json
+import os
+
+import pytest
+import torch
+
+from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
+from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
+from tests._util import rel_fro
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+R, C, G, N, T, BSZ = 2048, 28672, 1, 16, 2048, 8
+FQ = dict(blocksize=128, percdamp=0.01, groupsize=-1, actorder=True, static_groups=True)
+
+
+def test_70b_width_subgroup_parity():
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(35)
+    X = torch.randn((N, T, C), generator=gen, device=DEV).half()
+    X[:, :, torch.randperm(C, generator=gen, device=DEV)[:8]] *= 20
+    W = (torch.randn((R, C), generator=gen, device=DEV) * 0.015).half()
+    s = torch.exp(torch.randn((N, T, G), generator=gen, device=DEV))
+    s[..., 0].clamp_(max=float(torch.quantile(s[..., 0].flatten(), 0.99)))
+    grad = torch.zeros((R, C), device=DEV)
+    layer = torch.nn.Linear(C, R, bias=False).to(DEV, torch.float16)
+    layer.weight.data.copy_(W)
+    g = GPTQPlus(layer, saliency=s, gradient=grad, num_groups=G, alpha=0.0, reference_loss=0.0)
+    g.quantizer = WeightQuantizer()
+    g.quantizer.configure(4, perchannel=True, sym=False, mse=False)
+    for j in range(0, N, BSZ):
+        g.add_batch(X[j:j + BSZ], None)
+    g.finalize_hessian()
+    torch.cuda.synchronize()
+
+    o = GPTQPlusOracle(W.cpu(), s.cpu(), grad.cpu(), G, 0.0, 0.0)
+    o.quantizer = make_quantizer(4, False)
+    for j in range(0, N, BSZ):
+        o.add_batch(X[j:j + BSZ].cpu(), hessian=False)
+    o.finalize_hessian()
+    o.H = g.H.cpu()
+    act_bad = int((g.act_square.cpu() != o.act_square).sum())
+    res = o.fasterquant(**FQ)
+
+    H_keep, act_keep = g.H.clone(), g.act_square.clone()
+    g.fasterquant(export_to_et=True, inject={"hinv": [(r.Hinv_init.to(DEV), r.Hinv.to(DEV)) for r in res.subgroups]},
+                  **FQ)
+    torch.cuda.synchronize()
+    perm_bad = int((g.perm.cpu() != res.subgroups[0].perm).sum())
+    flips_inj = int((layer.int_weight.cpu() != res.W_int).sum())
+    q_equal = torch.equal(layer.weight.data.cpu(), res.Q)
+
+    layer.weight.data.copy_(W)
+    g2 = GPTQPlus(layer, saliency=s, gradient=grad, num_groups=G, alpha=0.0, reference_loss=0.0)
+    g2.quantizer = WeightQuantizer()
+    g2.quantizer.configure(4, perchannel=True, sym=False, mse=False)
+    g2.H, g2.act_square = H_keep, act_keep
+    g2.index, g2.token_count, g2._finalized = g.index, g.token_count, True
+    g2.fasterquant(export_to_et=True, keep_hinv=True, **FQ)
+    torch.cuda.synchronize()
+    hinv_err = rel_fro(g2.Hinv_all[0], res.subgroups[0].Hinv)
+    flips_own = int((layer.int_weight.cpu() != res.W_int).sum())
+    # the damped working matrix (P H P, dead columns as the chain handles them) in fp64 on the GPU
+    p = g2.perm
+    Hw = H_keep[0][p][:, p].double()
+    dead = torch.diagonal(Hw) == 0
+    Hw[dead, dead] = 1
+    damp = float(torch.tensor(g2.subgroup_info[0]["damp_percent"], dtype=torch.float32))
+    Hw32 = Hw.float()
+    idx = torch.arange(C, device=DEV)
+    Hw32[idx, idx] += damp * torch.mean(torch.diagonal(Hw32))
+    del Hw
+    U64 = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(Hw32.double())), upper=True)
+    del Hw32
+    gpu_vs_64 = rel_fro(g2.Hinv_all[0], U64)
+    ref_vs_64 = rel_fro(res.subgroups[0].Hinv.to(DEV), U64)
+    del U64
+    n = res.W_int.numel()
+    D_g = W.float() - layer.weight.data.float()
+    D_o = W.float() - res.Q.to(DEV).float()
+    x = X.reshape(-1, C).float()
+    Wx = float((W.float() @ x.T).double().pow(2).sum())
+    e_gpu = float((D_g @ x.T).double().pow(2).sum()) / Wx
+    e_ref = float((D_o @ x.T).double().pow(2).sum()) / Wx
+    rec = dict(case="configs4_width_subgroup", R=R, C=C, G=G, tokens=N * T, act_square_mismatch=act_bad,
+               perm_mismatch=perm_bad, flips_with_oracle_hinv=flips_inj, q_equal_with_oracle_hinv=q_equal,
+               flips_own_chain=flips_own, codes=n, hinv_rel_fro=hinv_err, hinv_vs_fp64=gpu_vs_64,
+               oracle_hinv_vs_fp64=ref_vs_64, recon_gpu=e_gpu, recon_oracle=e_ref,
+               recon_rel_diff=abs(e_gpu - e_ref) / e_ref)
+    print(json.dumps(rec), flush=True)
+    path = os.environ.get("RQ_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(rec) + "\n")
+    assert act_bad == 0 and perm_bad == 0
+    assert flips_inj == 0 and q_equal
+    assert hinv_err <= 1e-4
+    assert gpu_vs_64 <= 1e-6 and gpu_vs_64 < ref_vs_64
+    assert abs(e_gpu - e_ref) <= 0.005 * e_ref
+    assert flips_own <= n // 200
+    g.free()
+    g2.free()
