@@ -82,3 +82,14 @@ def test_counters_table_mfma_busy(tmp_path):
     row = buf.getvalue().splitlines()[2]
     # 1280 busy SIMD-cycles over 20 x 128 SIMD-cycles = 50 %
     assert "| 2 |" in row and "50.0 %" in row and "| 3.50 | 0.70 | 0.00 |" in row
+
+
+def test_more_than_one_gpu_is_refused_before_any_device_work():
+    """`bench.py --gpus N` with N > 1 exits with status 2 and says the build runs on one GPU;
+    it touches no device (this runs on a host without one)."""
+    import subprocess
+    res = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2", "--steps", "1",
+                          "--warmup", "0"], capture_output=True, text=True, timeout=120, cwd=ROOT)
+    assert res.returncode == 2
+    assert "one GPU only" in res.stdout + res.stderr
+    assert not res.stdout.strip().startswith("{")
