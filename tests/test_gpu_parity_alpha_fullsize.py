@@ -1,6 +1,8 @@
 """Parity of the GPTQ+ first-order term at a full BASELINE linear shape: q_proj 4096 x 4096,
-NUM_GROUPS = 4, w4 asym per-channel, act_order, B = 128, the term on (alpha = 0.05,
-reference_loss = 1e-3, gradient ~ N(0, 1e-4^2)), 16 x 2048 tokens with outlier channels.  The
+NUM_GROUPS = 4, w4 asym per-channel, act_order, B = 128, the term on (alpha = 0.05, gradient
+~ N(0, 1e-4^2)), 16 x 2048 tokens with outlier channels.  Two cases: the frozen mode with
+reference_loss = 1e-3 (beta ~ 1e-7), and surrogate_online (the first-order term re-evaluated
+before every column, :580-584) with reference_loss = 50 (beta ~ 5e-3).  The
 oracle (the reference's op sequence on the host CPU) runs act_square and fasterquant on the
 GPU's finalized H (gptq_plus_utils.py:174-194, 563-578 for the terms, :1500-1570 for the
 trailing update with Z != 0).
@@ -11,7 +13,9 @@ trailing update with Z != 0).
   op for op);
 - with only the oracle's H^-1 injected: the GPU's beta equal to the reference formula
   (:183-193) evaluated in IEEE fp32 with numpy on the oracle's row statistic c, and within one
-  rounding step of the oracle's own beta; Z and GHinv within 1e-5 (rel. Frobenius) of the
+  rounding step of the oracle's own beta (1e-5 relative, or 2^-23; at most 1 % of the rows
+  off the IEEE value by more than 1e-5, from c's summation order); Z and GHinv within 1e-5
+  (rel. Frobenius) of the
   oracle's once rescaled by the two betas' ratio; code flips <= 0.01 %.
   At this shape beta = 1 - sqrt(1 - ratio) with ratio ~ 2e-7, where fp32 resolves beta only
   in steps of 2^-24: the reference's own value depends on the host.  1 - ratio rounds to
@@ -36,20 +40,21 @@ from tests._util import rel_fro
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 R, C, G, N, T, BSZ = 4096, 4096, 4, 16, 2048, 8
-ALPHA, REF_LOSS = 0.05, 1e-3
+ALPHA = 0.05
+CASES = {"frozen_refloss_1e-3": ("frozen", 1e-3), "surrogate_online_refloss_50": ("surrogate_online", 50.0)}
 FQ = dict(blocksize=128, percdamp=0.01, groupsize=-1, actorder=True, static_groups=True)
 
 
-def _obj(layer, W, s, grad):
+def _obj(layer, W, s, grad, ref_loss):
     layer.weight.data.copy_(W)
-    g = GPTQPlus(layer, saliency=s, gradient=grad, num_groups=G, alpha=ALPHA, reference_loss=REF_LOSS)
+    g = GPTQPlus(layer, saliency=s, gradient=grad, num_groups=G, alpha=ALPHA, reference_loss=ref_loss)
     g.quantizer = WeightQuantizer()
     g.quantizer.configure(4, perchannel=True, sym=False, mse=False)
     return g
 
 
-def _rerun(layer, W, s, grad, src, H, act, **kw):
-    g = _obj(layer, W, s, grad)
+def _rerun(layer, W, s, grad, ref_loss, src, H, act, **kw):
+    g = _obj(layer, W, s, grad, ref_loss)
     g.H, g.act_square = H.clone(), act.clone()
     g.index, g.token_count, g._finalized = src.index, src.token_count, True
     g.fasterquant(export_to_et=True, keep_hinv=True, **FQ, **kw)
@@ -57,7 +62,9 @@ def _rerun(layer, W, s, grad, src, H, act, **kw):
     return g
 
 
-def test_gptqplus_term_parity_full_linear():
+@pytest.mark.parametrize("case", list(CASES))
+def test_gptqplus_term_parity_full_linear(case):
+    mode, REF_LOSS = CASES[case]
     gen = torch.Generator(device=DEV)
     gen.manual_seed(36)
     X = torch.randn((N, T, C), generator=gen, device=DEV).half()
@@ -68,7 +75,7 @@ def test_gptqplus_term_parity_full_linear():
         s[..., k].clamp_(max=float(torch.quantile(s[..., k].flatten(), 0.99)))
     grad = torch.randn((R, C), generator=gen, device=DEV) * 1e-4
     layer = torch.nn.Linear(C, R, bias=False).to(DEV, torch.float16)
-    g = _obj(layer, W, s, grad)
+    g = _obj(layer, W, s, grad, REF_LOSS)
     for j in range(0, N, BSZ):
         g.add_batch(X[j:j + BSZ], None)
     g.finalize_hessian()
@@ -82,20 +89,21 @@ def test_gptqplus_term_parity_full_linear():
     o.finalize_hessian()
     o.H = H_keep.cpu()
     act_bad = int((act_keep.cpu() != o.act_square).sum())
-    res = o.fasterquant(**FQ)
+    res = o.fasterquant(g_update_mode=mode, **FQ)
     subs = res.subgroups
     hinv = [(r.Hinv_init.to(DEV), r.Hinv.to(DEV)) for r in subs]
     terms = [(r.beta.to(DEV), r.Z.to(DEV), r.GHinv.to(DEV)) for r in subs]
     R_s = R // G
     z_rel = max(float(r.Z.abs().max()) for r in subs) / float(W.float().abs().max())
 
-    g1 = _rerun(layer, W, s, grad, g, H_keep, act_keep, inject={"hinv": hinv, "terms": terms})
+    g1 = _rerun(layer, W, s, grad, REF_LOSS, g, H_keep, act_keep, g_update_mode=mode,
+                inject={"hinv": hinv, "terms": terms})
     perm_bad = int((g1.perm.cpu() != subs[0].perm).sum())
     flips_all = int((layer.int_weight.cpu() != res.W_int).sum())
     q_equal = torch.equal(layer.weight.data.cpu(), res.Q)
     g1.free()
 
-    g2 = _rerun(layer, W, s, grad, g, H_keep, act_keep, inject={"hinv": hinv})
+    g2 = _rerun(layer, W, s, grad, REF_LOSS, g, H_keep, act_keep, g_update_mode=mode, inject={"hinv": hinv})
     target = 2 * (ALPHA / (R * C)) * REF_LOSS
     beta_ieee_bad = beta_step_bad = 0
     beta_err = z_err = gh_err = 0.0
@@ -108,7 +116,7 @@ def test_gptqplus_term_parity_full_linear():
         ratio = np.clip(np.where(c > 0, np.float32(target) / c, np.float32(0)), 0, 1).astype(np.float32)
         b_ieee = (np.float32(1) - np.sqrt(np.maximum(np.float32(1) - ratio, np.float32(0)))).astype(np.float32)
         gb, ob = info["beta"].cpu(), r.beta
-        beta_ieee_bad += int((gb.numpy() != b_ieee).sum())
+        beta_ieee_bad += int((np.abs(gb.numpy() - b_ieee) > 1e-5 * np.abs(b_ieee)).sum())
         beta_step_bad += int(((gb - ob).abs() > torch.maximum(1e-5 * ob.abs(), torch.tensor(2.0 ** -23))).sum())
         beta_err = max(beta_err, rel_fro(gb, ob))
         scale = torch.where(ob != 0, gb.double() / ob.double(), torch.ones_like(ob, dtype=torch.float64))[:, None]
@@ -117,7 +125,7 @@ def test_gptqplus_term_parity_full_linear():
     flips_terms = int((layer.int_weight.cpu() != res.W_int).sum())
     g2.free()
 
-    g3 = _rerun(layer, W, s, grad, g, H_keep, act_keep)
+    g3 = _rerun(layer, W, s, grad, REF_LOSS, g, H_keep, act_keep, g_update_mode=mode)
     hinv_err = max(rel_fro(g3.Hinv_all[k], r.Hinv) for k, r in enumerate(subs))
     flips_own = int((layer.int_weight.cpu() != res.W_int).sum())
     n = res.W_int.numel()
@@ -127,7 +135,7 @@ def test_gptqplus_term_parity_full_linear():
     e_ref = float(((W.float() - res.Q.to(DEV).float()) @ x.T).double().pow(2).sum()) / Wx
     g3.free()
     g.free()
-    rec = dict(case="configs1_q_proj_G4_alpha", R=R, C=C, G=G, tokens=N * T, alpha=ALPHA, ref_loss=REF_LOSS,
+    rec = dict(case=f"configs1_q_proj_G4_alpha_{case}", mode=mode, R=R, C=C, G=G, tokens=N * T, alpha=ALPHA, ref_loss=REF_LOSS,
                z_max_over_w_max=z_rel, act_square_mismatch=act_bad, perm_mismatch=perm_bad,
                flips_with_oracle_hinv_and_terms=flips_all, q_equal_with_oracle_hinv_and_terms=q_equal,
                beta_rel_fro=beta_err, beta_rows_not_ieee=beta_ieee_bad, beta_rows_beyond_one_step=beta_step_bad,
