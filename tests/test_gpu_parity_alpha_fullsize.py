@@ -1,8 +1,10 @@
 """Parity of the GPTQ+ first-order term at a full BASELINE linear shape: q_proj 4096 x 4096,
 NUM_GROUPS = 4, w4 asym per-channel, act_order, B = 128, the term on (alpha = 0.05, gradient
-~ N(0, 1e-4^2)), 16 x 2048 tokens with outlier channels.  Two cases: the frozen mode with
-reference_loss = 1e-3 (beta ~ 1e-7), and surrogate_online (the first-order term re-evaluated
-before every column, :580-584) with reference_loss = 50 (beta ~ 5e-3).  The
+~ N(0, 1e-4^2)), 16 x 2048 tokens with outlier channels.  Three cases: the frozen mode with
+reference_loss = 1e-3 (beta ~ 1e-7); surrogate_online (the first-order term re-evaluated
+before every column, :580-584) with reference_loss = 50 (beta ~ 5e-3); block_gd with SGD
+(:1572-1848) and reference_loss = 50, whose layer backward is an elementwise quadratic that
+both devices evaluate identically (_diag_refresh).  The
 oracle (the reference's op sequence on the host CPU) runs act_square and fasterquant on the
 GPU's finalized H (gptq_plus_utils.py:174-194, 563-578 for the terms, :1500-1570 for the
 trailing update with Z != 0).
@@ -41,7 +43,24 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 R, C, G, N, T, BSZ = 4096, 4096, 4, 16, 2048, 8
 ALPHA = 0.05
-CASES = {"frozen_refloss_1e-3": ("frozen", 1e-3), "surrogate_online_refloss_50": ("surrogate_online", 50.0)}
+CASES = {"frozen_refloss_1e-3": ("frozen", 1e-3), "surrogate_online_refloss_50": ("surrogate_online", 50.0),
+         "block_gd_sgd_refloss_50": ("block_gd", 50.0)}
+BLOCK_GD = dict(grad_optimizer="sgd", grad_lr=0.008, grad_reg_strategy="none", second_order_scale=1.0, grad_clip=1.0)
+
+
+def _diag_refresh(a, W0, G0):
+    """A layer backward for block_gd that both devices evaluate identically: the gradient of
+    0.5 sum_j a_j ||W[:, j] - W0[:, j]||^2 + <G0, W>, elementwise in float64, returned float32
+    (scaled by (1 + slide_alpha) / 2 when the caller passes slide_alpha)."""
+    def fn(weight_snapshot, slide_alpha=None):
+        dev = weight_snapshot.device
+        D = weight_snapshot.double() - W0.to(dev)
+        grad = D * a.to(dev) + G0.to(dev)
+        if slide_alpha is not None:
+            grad = grad * (0.5 + 0.5 * float(slide_alpha))
+        return grad.float(), {"mean_refresh_loss": float(0.5 * (D * D * a.to(dev)).sum().cpu()),
+                              "slide_alpha": slide_alpha}
+    return fn
 FQ = dict(blocksize=128, percdamp=0.01, groupsize=-1, actorder=True, static_groups=True)
 
 
@@ -74,6 +93,10 @@ def test_gptqplus_term_parity_full_linear(case):
     for k in range(G):
         s[..., k].clamp_(max=float(torch.quantile(s[..., k].flatten(), 0.99)))
     grad = torch.randn((R, C), generator=gen, device=DEV) * 1e-4
+    extra = {}
+    if mode == "block_gd":
+        a = X.reshape(-1, C).double().pow(2).mean(0).cpu()
+        extra = dict(BLOCK_GD, gradient_refresh_fn=_diag_refresh(a, W.double().cpu(), grad.double().cpu()))
     layer = torch.nn.Linear(C, R, bias=False).to(DEV, torch.float16)
     g = _obj(layer, W, s, grad, REF_LOSS)
     for j in range(0, N, BSZ):
@@ -89,7 +112,7 @@ def test_gptqplus_term_parity_full_linear(case):
     o.finalize_hessian()
     o.H = H_keep.cpu()
     act_bad = int((act_keep.cpu() != o.act_square).sum())
-    res = o.fasterquant(g_update_mode=mode, **FQ)
+    res = o.fasterquant(g_update_mode=mode, **FQ, **extra)
     subs = res.subgroups
     hinv = [(r.Hinv_init.to(DEV), r.Hinv.to(DEV)) for r in subs]
     terms = [(r.beta.to(DEV), r.Z.to(DEV), r.GHinv.to(DEV)) for r in subs]
@@ -97,13 +120,14 @@ def test_gptqplus_term_parity_full_linear(case):
     z_rel = max(float(r.Z.abs().max()) for r in subs) / float(W.float().abs().max())
 
     g1 = _rerun(layer, W, s, grad, REF_LOSS, g, H_keep, act_keep, g_update_mode=mode,
-                inject={"hinv": hinv, "terms": terms})
+                inject={"hinv": hinv, "terms": terms}, **extra)
     perm_bad = int((g1.perm.cpu() != subs[0].perm).sum())
     flips_all = int((layer.int_weight.cpu() != res.W_int).sum())
     q_equal = torch.equal(layer.weight.data.cpu(), res.Q)
     g1.free()
 
-    g2 = _rerun(layer, W, s, grad, REF_LOSS, g, H_keep, act_keep, g_update_mode=mode, inject={"hinv": hinv})
+    g2 = _rerun(layer, W, s, grad, REF_LOSS, g, H_keep, act_keep, g_update_mode=mode, inject={"hinv": hinv},
+                **extra)
     target = 2 * (ALPHA / (R * C)) * REF_LOSS
     beta_ieee_bad = beta_step_bad = 0
     beta_err = z_err = gh_err = 0.0
@@ -125,7 +149,7 @@ def test_gptqplus_term_parity_full_linear(case):
     flips_terms = int((layer.int_weight.cpu() != res.W_int).sum())
     g2.free()
 
-    g3 = _rerun(layer, W, s, grad, REF_LOSS, g, H_keep, act_keep, g_update_mode=mode)
+    g3 = _rerun(layer, W, s, grad, REF_LOSS, g, H_keep, act_keep, g_update_mode=mode, **extra)
     hinv_err = max(rel_fro(g3.Hinv_all[k], r.Hinv) for k, r in enumerate(subs))
     flips_own = int((layer.int_weight.cpu() != res.W_int).sum())
     n = res.W_int.numel()
