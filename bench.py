@@ -43,6 +43,19 @@ FP64_MFMA_PEAK_TFLOPS = 78.6
 HBM_PEAK_GBS = 8000.0
 METRIC = "ms per linear (H-accum + fasterquant) at Llama-8B shapes; % fp32-MFMA peak"
 PIECES = {"split16": 2, "split16x3": 3, "fp32": 1}     # 16-bit MFMA products per fp32 product (fp16 X)
+# the arithmetic the Hessian (the dominant kernel) computes in, by --hessian-math and fp32 X;
+# the Cholesky chain runs in fp64, every other kernel in fp32
+DTYPE_TEXT = {
+    ("split16x3", False): "f32 (fp16 inputs; Hessian: exact fp32 products, 3 fp16 MFMA products each, fp32 sums)",
+    ("split16", False): "f32 (fp16 inputs; Hessian: fp32 products within 2^-23 relative, 2 fp16 MFMA products "
+                        "each, fp32 sums)",
+    ("fp32", False): "f32 (fp16 inputs; Hessian: fp32 MFMA)",
+    ("split16x3", True): "f32 (fp32 inputs; Hessian: fp32 products within 2^-20.5 relative, 3 fp16 MFMA "
+                         "products each, fp32 sums)",
+    ("split16", True): "f32 (fp32 inputs; Hessian: fp32 products within 2^-20.5 relative, 3 fp16 MFMA "
+                       "products each, fp32 sums)",
+    ("fp32", True): "f32 (fp32 inputs; Hessian: fp32 MFMA)",
+}
 KERNEL = {"split16": "k_hessian_split<__half, 2>", "split16x3": "k_hessian_split<__half, 3>",
           "fp32": "k_hessian_accum<__half>"}
 HESSIAN_SRC = os.path.join(ROOT, "gptq_plus_mp_quant_amd", "csrc", "hessian.hip")
@@ -198,19 +211,63 @@ def new_gptq(layer, W, s, grad, cfg):
     return g
 
 
-def one_linear(X, W, s, grad, cfg, layer, timer=None):
+class PhaseMarks:
+    """Events recorded on the current stream at the boundaries of a step's phases (no host
+    synchronisation), read after the timed region: per-step times and per-phase means."""
+
+    def __init__(self):
+        self.steps = []
+
+    def begin(self):
+        import torch
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.steps.append([("begin", e)])
+
+    def mark(self, name):
+        import torch
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.steps[-1].append((name, e))
+
+    def report(self):
+        import torch
+        torch.cuda.synchronize()
+        per_step, phases = [], {}
+        for marks in self.steps:
+            per_step.append(marks[0][1].elapsed_time(marks[-1][1]))
+            for (_, a), (name, b) in zip(marks, marks[1:]):
+                phases[name] = phases.get(name, 0.0) + a.elapsed_time(b)
+        n = max(len(self.steps), 1)
+        return per_step, {k: v / n for k, v in phases.items()}
+
+
+def one_linear(X, W, s, grad, cfg, layer, timer=None, keep=False, marks=None):
+    if marks is not None:
+        marks.begin()
     g = new_gptq(layer, W, s, grad, cfg)
     for j in range(0, cfg["N"], cfg["bsz"]):
         if timer is not None:
             timer.arm()
         g.add_batch(X[j:j + cfg["bsz"]], None)
+    if marks is not None:
+        marks.mark("hessian")
     g.finalize_hessian()
+    if marks is not None:
+        marks.mark("finalize")
     g.fasterquant(**fq_kwargs(cfg))
+    if marks is not None:
+        marks.mark("fasterquant")
+    g.free()
+    if marks is not None:
+        marks.mark("free")
     return g
 
 
-def one_layer(xs, mods, cfg, layers, timer=None, keep=False):
+def one_layer(xs, mods, cfg, layers, timer=None, keep=False, marks=None):
     from gptq_plus_mp_quant_amd import add_batch_shared
+    if marks is not None:
+        marks.begin()
     objs = {name: new_gptq(layers[name], W, s, grad, cfg) for name, (W, s, grad, _) in mods.items()}
     for key in INPUT_WIDTH:
         group = [objs[n] for n, _, _, k in LAYER8B if k == key]
@@ -218,14 +275,22 @@ def one_layer(xs, mods, cfg, layers, timer=None, keep=False):
             if timer is not None:
                 timer.arm()
             add_batch_shared(group, xs[key][j:j + cfg["bsz"]])
+    if marks is not None:
+        marks.mark("hessian")
     for g in objs.values():
         g.finalize_hessian()
+    if marks is not None:
+        marks.mark("finalize")
     kept = {}
     for name, g in objs.items():
         if keep:
             kept[name] = (g.H.clone(), g.act_square.clone())
         g.fasterquant(**fq_kwargs(cfg))
+        if marks is not None:
+            marks.mark(f"fasterquant {name}")
         g.free()
+        if marks is not None:
+            marks.mark(f"free {name}")
     return kept
 
 
@@ -258,10 +323,13 @@ def source_sha():
 
 
 def roofline(cfg, args, kernel_ms, launches, steps):
-    """The dominant kernel (the Hessian product kernel) against the fp32 MFMA peak that the
-    metric is stated on: algorithmic fp32 flops per launch / measured launch time.  The kernel
-    runs on the 16-bit MFMA pipe (PIECES products per fp32 product); that pipe's use is given
-    beside it."""
+    """The dominant kernel (the Hessian product kernel) against the peak of the MFMA pipe it
+    runs on: algorithmic fp32 flops per launch (the upper triangle of the reference's fp32
+    products, each counted once) / measured launch time.  The split kernels form each fp32
+    product from PIECES 16-bit MFMA products, so they are held to the fp16 / bf16 peak (2.5
+    PF/s) and `executed` gives the pipe's use counting every product issued; the fp32 MFMA kernel
+    is held to the fp32 peak.  `fp32_equivalent` states the same rate against the fp32 MFMA
+    peak the metric names (a ratio, not a fraction of a pipe)."""
     flops_unit = hessian_flops(cfg)
     per_launch_flops = flops_unit * steps / launches
     ms = kernel_ms / launches
@@ -273,16 +341,17 @@ def roofline(cfg, args, kernel_ms, launches, steps):
         traffic, tsrc = None, "fp32 activations: not measured"
         pieces = 3 if args.hessian_math != "fp32" else 1
         kernel = "k_hessian_split32" if args.hessian_math != "fp32" else "k_hessian_accum<float>"
-    return {"bound": "mfma", "achieved": round(ach, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
+    peak = FP16_MFMA_PEAK_TFLOPS if pieces > 1 else FP32_MFMA_PEAK_TFLOPS
+    return {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(ach / peak, 4), "traffic": traffic,
+            "pipe": "fp16 MFMA (v_mfma_f32_32x32x16_f16)" if pieces > 1 else "fp32 MFMA (v_mfma_f32_32x32x2_f32)",
             "kernel": kernel, "launch_ms": round(ms, 4), "launches": launches // steps,
             "flops_per_launch": int(per_launch_flops),
             "algorithmic": "fp32 flops of H_g += X^T diag(s_g) X, upper triangle incl. diagonal "
                            "(G*n*C*(C+1) per launch of n tokens)",
-            "pipe": {"name": "fp16 MFMA" if pieces > 1 else "fp32 MFMA", "products_per_fp32_product": pieces,
-                     "executed_tflops": round(ach * pieces, 2),
-                     "peak": FP16_MFMA_PEAK_TFLOPS if pieces > 1 else FP32_MFMA_PEAK_TFLOPS,
-                     "frac": round(ach * pieces / (FP16_MFMA_PEAK_TFLOPS if pieces > 1 else FP32_MFMA_PEAK_TFLOPS), 4)},
+            "executed": {"products_per_fp32_product": pieces, "tflops": round(ach * pieces, 2),
+                         "frac": round(ach * pieces / peak, 4)},
+            "fp32_equivalent": {"peak": FP32_MFMA_PEAK_TFLOPS, "ratio": round(ach / FP32_MFMA_PEAK_TFLOPS, 4)},
             "traffic_source": tsrc}
 
 
@@ -344,42 +413,50 @@ def cpu_baseline_linear(X, W, s, grad, cfg, chunks=2):
 
 
 def cpu_baseline_layer(xs, mods, kept, cfg):
-    """configs[2] / configs[3] on a bounded sample.  add_batch: one calibration sample (2048 of the
-    262144 tokens) per input width, through the reference's per-module call (x 128 by tokens, per
-    module of that width).  finalize_hessian + fasterquant: one of the 4 row subgroups of each
-    distinct (rows, columns) shape, on the GPU run's finalized H_0 (the subgroups are independent
-    in the reference's loop, :1027-1162; x 4 per module).  The two parts make the layer."""
+    """configs[2] / configs[3] on a bounded sample.  add_batch: one full 16-sample chunk
+    (32768 tokens, the reference's HESSIAN_ACCUM_BSZ call with its (G, 32768, C) fp32 `weighted`)
+    per input width, through the reference's per-module call (x 8 chunks by tokens, per module
+    of that width).  finalize_hessian + fasterquant: all 4 row subgroups of q_proj (4096 x 4096)
+    and one of the 4 of each other distinct (rows, columns) shape (x 4: the subgroups are
+    independent in the reference's loop, :1027-1162), on the GPU run's finalized Hessians.  The
+    two parts make the layer."""
     import torch
     from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
     threads, host = host_cpu()
-    N, G = cfg["N"], cfg["G"]
+    N, G, bsz = cfg["N"], cfg["G"], cfg["bsz"]
     t_ab, parts = {}, []
     for key, C in (("attn", 4096), ("down", 14336)):
         name = next(n for n, _, c, k in LAYER8B if c == C)
         W, s, grad, _ = mods[name]
-        o = GPTQPlusOracle(W.cpu(), s[:1].cpu(), grad.cpu(), G, cfg["alpha"], cfg["ref_loss"])
-        x = xs[key][:1].cpu()
+        o = GPTQPlusOracle(W.cpu(), s[:bsz].cpu(), grad.cpu(), G, cfg["alpha"], cfg["ref_loss"])
+        x = xs[key][:bsz].cpu()
         t0 = time.perf_counter()
         o.add_batch(x)
-        t_ab[C] = (time.perf_counter() - t0) * N
-        parts.append(f"add_batch C={C}: 1/{N} samples {t_ab[C] / N:.2f} s")
+        t_ab[C] = (time.perf_counter() - t0) * (N // bsz)
+        parts.append(f"add_batch C={C}: 1 of {N // bsz} {bsz}-sample chunks {t_ab[C] / (N // bsz):.2f} s")
+        print(f"cpu baseline add_batch C={C}: {t_ab[C] / (N // bsz):.2f} s per {bsz}-sample chunk", flush=True)
+        del o, x
     t_fq = {}
     for name, R, C, key in LAYER8B:
         if (R, C) in t_fq:
             continue
         W, s, grad, _ = mods[name]
+        nsub = G if (R, C) == (4096, 4096) else 1
         Rs = R // G
         H, act = kept[name]
-        o = GPTQPlusOracle(W[:Rs].cpu(), s[:, :, :1].cpu(), grad[:Rs].cpu(), 1, cfg["alpha"], cfg["ref_loss"])
+        o = GPTQPlusOracle(W[:nsub * Rs].cpu(), s[:, :, :nsub].cpu(), grad[:nsub * Rs].cpu(), nsub,
+                           cfg["alpha"], cfg["ref_loss"])
         o.quantizer = make_quantizer(cfg["bits"], cfg["sym"])
-        o.H = H[:1].cpu()
+        o.H = H[:nsub].cpu()
         o.act_square = act.cpu()
         o.index, o.token_count, o._finalized = N, N * cfg["T"], True
         t0 = time.perf_counter()
         o.fasterquant(**fq_kwargs(cfg))
-        t_fq[(R, C)] = (time.perf_counter() - t0) * G
-        parts.append(f"fasterquant {R}x{C}: 1/{G} subgroups {t_fq[(R, C)] / G:.2f} s")
-        print(f"cpu baseline fasterquant {R}x{C}: {t_fq[(R, C)] / G:.2f} s per subgroup", flush=True)
+        t_fq[(R, C)] = (time.perf_counter() - t0) * G / nsub
+        parts.append(f"fasterquant {R}x{C}: {nsub}/{G} subgroups {t_fq[(R, C)] * nsub / G:.2f} s")
+        print(f"cpu baseline fasterquant {R}x{C}: {t_fq[(R, C)] / G:.2f} s per subgroup ({nsub} timed)",
+              flush=True)
+        del o
     total = sum(t_ab[C] + t_fq[(R, C)] for _, R, C, _ in LAYER8B)
     return dict(value=round(total * 1e3 / len(LAYER8B), 1), unit="ms per linear (layer / 7, extrapolated)",
                 cores=threads, kind="port",
@@ -633,34 +710,43 @@ def run(args):
         if args.x_fp32:
             xs = {k: v.float() for k, v in xs.items()}
         layers = {n: torch.nn.Linear(C, R, bias=False).to(dev, torch.float16) for n, R, C, _ in LAYER8B}
-        step = lambda timer=None, keep=False: one_layer(xs, mods, cfg, layers, timer, keep)
+        step = lambda timer=None, keep=False, marks=None: one_layer(xs, mods, cfg, layers, timer, keep, marks)
     else:
         X, W, s, grad = make_inputs(dev, cfg)
         if args.x_fp32:
             X = X.float()
         layer = torch.nn.Linear(cfg["C"], cfg["R"], bias=False).to(dev, torch.float16)
-        step = lambda timer=None, keep=False: one_linear(X, W, s, grad, cfg, layer, timer)
+        step = lambda timer=None, keep=False, marks=None: one_linear(X, W, s, grad, cfg, layer, timer, keep, marks)
     torch.cuda.synchronize()
     kept = None
     for i in range(args.warmup):
         out = step(keep=(layer_mode and i == args.warmup - 1))
         kept = out if layer_mode and i == args.warmup - 1 else kept
     timer = KernelTimer()
+    marks = PhaseMarks()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step(timer)
+        step(timer, marks=marks)
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
     kernel_ms, launches = timer.total_ms()
+    step_ms, phase_ms = marks.report()
     per = len(LAYER8B) if layer_mode else 1
+    print("per-step ms: " + " ".join(f"{t:.1f}" for t in step_ms), file=sys.stderr, flush=True)
+    print("per-phase ms (mean per step): " + "; ".join(f"{k} {v:.2f}" for k, v in phase_ms.items()),
+          file=sys.stderr, flush=True)
+    srt = sorted(step_ms)
     line = {
         "metric": METRIC, "value": round(ms_step / per, 2), "unit": "ms", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 2), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32 (fp32 inputs)" if args.x_fp32 else "f32 (fp16 inputs)", "data": "synthetic (seeded, generated on the GPU)",
+        "vs_baseline": None, "dtype": DTYPE_TEXT[(args.hessian_math, bool(args.x_fp32))],
+        "data": "synthetic (seeded, generated on the GPU)",
         "config": {"workload": WORKLOAD[args.config].format(alpha=cfg["alpha"]), "parallelism": "single GPU",
                    "hessian_math": args.hessian_math},
         "roofline": roofline(cfg, args, kernel_ms, launches, args.steps),
+        "step_ms": {"min": round(srt[0], 2), "median": round(srt[len(srt) // 2], 2), "max": round(srt[-1], 2)},
+        "phase_ms": {k: round(v, 2) for k, v in phase_ms.items()},
     }
     if not args.no_cpu_baseline:
         if layer_mode:
@@ -688,9 +774,9 @@ def main():
     ap.add_argument("--cpu-chunks", type=int, default=2)
     ap.add_argument("--cpu-baseline-sample", action="store_true",
                     help="with --config cfg5: time the CPU oracle's Hessian accumulation on one sample")
-    ap.add_argument("--hessian-math", choices=sorted(PIECES), default="split16",
-                    help="Hessian kernel for fp16 inputs: split16 (two fp16 MFMA products per fp32 product), "
-                         "split16x3 (three: exact products), fp32 (fp32 MFMA)")
+    ap.add_argument("--hessian-math", choices=sorted(PIECES), default="split16x3",
+                    help="Hessian kernel for fp16 inputs: split16x3 (default: three fp16 MFMA products per fp32 "
+                         "product, exact), split16 (two: within 2^-23 relative), fp32 (fp32 MFMA)")
     ap.add_argument("--x-fp32", action="store_true",
                     help="fp32 activations (the reference's add_batch takes any float dtype): the same inputs "
                          "converted to fp32")

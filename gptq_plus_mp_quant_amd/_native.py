@@ -1,17 +1,20 @@
 """ctypes binding of the C ABI in ``include/gptqplus_hip.h`` (library ``_lib/libgptqplus_hip.so``).
 
 The library is the only compute path: if it is missing or cannot be loaded every call raises
-``RuntimeError`` -- there is no silent fallback.
+``RuntimeError`` -- there is no silent fallback.  ``GPTQPLUS_HIP_LIB`` (environment) names
+another build of the same library to load instead (e.g. a variant built for an A/B timing).
 """
 from __future__ import annotations
 
 import ctypes
+import os
 import re
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgptqplus_hip.so"
+LIB_PATH = Path(os.environ.get("GPTQPLUS_HIP_LIB") or
+                Path(__file__).resolve().parent / "_lib" / "libgptqplus_hip.so").resolve()
 HEADER = Path(__file__).resolve().parent.parent / "include" / "gptqplus_hip.h"
 
 RQ_OK, RQ_EINVAL, RQ_EHIP, RQ_ENOTSUP = 0, -1, -2, -3
@@ -21,6 +24,7 @@ RQ_GMODE_FROZEN, RQ_GMODE_SURROGATE_BLOCK, RQ_GMODE_SURROGATE_ONLINE, RQ_GMODE_B
 RQ_HMATH_SPLIT16, RQ_HMATH_FP32, RQ_HMATH_SPLIT16X3 = 0, 1, 2
 RQ_NOALLOC_SCRATCH_BYTES = 128 << 20
 RQ_CHOL_MAXBATCH = 64          # matrices per rq_chol_hinv_attempt call
+RQ_ACT_ORDER_MAXC = 65536      # widest rq_act_order_perm
 # g_update_mode -> (kernel mode of the in-block loop, kernel mode of the trailing update);
 # gptq_plus_utils.py:1190 (inner) and :1500 (outer)
 GMODES = {"frozen": (RQ_GMODE_FROZEN, RQ_GMODE_FROZEN),

@@ -317,12 +317,12 @@ __global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
 // p2 = rn(w - p0 - p1) (round to nearest in the 16-bit type).  Each product x * p_k (11 x 11
 // or 8 x 8 bits) is exact in fp32, and PC v_mfma_f32_32x32x16_{f16,bf16} per 16 tokens add
 // them into fp32 accumulators.
-//  * bf16, and fp16 with RQ_HMATH_SPLIT16X3: three pieces, 8 + 8 + 8 or 11 + 11 + 2
-//    significant bits, cover w's 24: the reference's fp32 products, exactly.
-//  * fp16 (RQ_HMATH_SPLIT16, the default): two pieces carry 22 of w's 24 bits; the dropped
+//  * bf16, and fp16 with RQ_HMATH_SPLIT16X3 (the default): three pieces, 8 + 8 + 8 or
+//    11 + 11 + 2 significant bits, cover w's 24: the reference's fp32 products, exactly.
+//  * fp16 with RQ_HMATH_SPLIT16 (opt-in): two pieces carry 22 of w's 24 bits; the dropped
 //    residual is at most half an ulp of p1, 2^-23 relative to w (the unit roundoff of fp32 is
-//    2^-24), so each product is the reference's up to 2^-23 relative, far below the rounding
-//    of the fp32 sums themselves, for two thirds of the MFMA work of three pieces.
+//    2^-24), so each product is the reference's up to 2^-23 relative, for two thirds of the
+//    MFMA work of three pieces.
 // The exponent e (k_xfinish) puts the column's largest |w| in [2^14, 2^15): p0 cannot
 // overflow fp16, and fp16 pieces are normal numbers for every |w| * 2^e >= 2^-1 (down to 2^-15
 // of the column's largest entry); below that p1's subnormal spacing bounds the residual by
@@ -1577,7 +1577,7 @@ extern "C" int rq_version(void) { return 100; }
 
 namespace {
 
-std::atomic<int> g_hmath{RQ_HMATH_SPLIT16};
+std::atomic<int> g_hmath{RQ_HMATH_SPLIT16X3};   // exact fp32 products by default
 // Optional events recorded around the next product-kernel launch (measurement hook).
 std::atomic<void*> g_time_start{nullptr}, g_time_stop{nullptr};
 

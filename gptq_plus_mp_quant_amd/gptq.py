@@ -77,6 +77,8 @@ class GPTQ:
             raise ValueError("fasterquant: a quantizer with weight_groupsize > 0 has no per-row scale")
         if blocksize > 128 or blocksize <= 0:
             raise NotImplementedError("blocksize must be in [1, 128] on the HIP path")
+        if actorder:
+            K.check_act_order_width(self.columns)
         dev, R, C = self.dev, self.rows, self.columns
         f32 = dict(device=dev, dtype=torch.float32)
         W = self.layer.weight.data
@@ -179,4 +181,5 @@ class GPTQ:
         self.H = None
         self.Losses = None
         self._codes_perm = None
+        K.release_hessian_workspace(self.dev)
         torch.cuda.empty_cache()

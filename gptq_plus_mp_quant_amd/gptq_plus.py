@@ -271,6 +271,8 @@ class GPTQPlus:
             raise ValueError("fasterquant: a quantizer with weight_groupsize > 0 has no per-row scale")
         if blocksize > MAX_BLOCKSIZE or blocksize <= 0:
             raise NotImplementedError(f"blocksize must be in [1, {MAX_BLOCKSIZE}] on the HIP path")
+        if actorder:
+            K.check_act_order_width(self.columns)
 
         dev, R, C, G = self.dev, self.rows, self.columns, self.num_groups
         R_s = R // G
@@ -639,10 +641,13 @@ class GPTQPlus:
         return export_packed(self)
 
     def free(self):
+        # gptq_plus_utils.py:2357-2361: drop the Hessians and return cached device memory
+        # (the library's cached Hessian workspace included) to the device
         self.H = None
         self.Losses = None
         self._codes_perm = None
         self.Hinv_all = None
+        K.release_hessian_workspace(self.dev)
         torch.cuda.empty_cache()
 
 

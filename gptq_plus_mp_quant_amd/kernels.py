@@ -64,9 +64,20 @@ def hessian_workspace(x, ntargets):
     key = (dev, torch.cuda.current_stream(x.device).cuda_stream)
     ws = _HWS.get(key)
     if ws is None or ws.numel() < need:
+        _HWS.pop(key, None)                       # the old one is released before the new one is made
+        del ws
         ws = torch.zeros(need, dtype=torch.uint8, device=x.device)
         _HWS[key] = ws
     return ws, ws.numel()
+
+
+def release_hessian_workspace(device=None):
+    """Drop the cached Hessian workspaces (all devices, or one), e.g. when a linear is freed;
+    the next launch allocates a new one of the size it needs.  Work already queued on a stream
+    keeps its workspace alive through the caching allocator's stream semantics."""
+    dev = None if device is None else (device.index if device.index is not None else torch.cuda.current_device())
+    for key in [k for k in _HWS if dev is None or k[0] == dev]:
+        del _HWS[key]
 
 
 HESSIAN_MATH = {"split16": nat.RQ_HMATH_SPLIT16, "split16x3": nat.RQ_HMATH_SPLIT16X3, "fp32": nat.RQ_HMATH_FP32}
@@ -74,10 +85,11 @@ HESSIAN_MATH = {"split16": nat.RQ_HMATH_SPLIT16, "split16x3": nat.RQ_HMATH_SPLIT
 
 @contextlib.contextmanager
 def hessian_math(mode):
-    """Select the Hessian kernel for fp16 / bf16 inputs inside the block: "split16" (default;
-    fp16 X: each fp32 product from two 16-bit MFMA products, within 2^-23 relative; bf16 X:
-    exact, from three), "split16x3" (exact products from three for fp16 too) or "fp32" (fp32
-    MFMA).  The choice is process-wide; fp32 inputs always use the fp32 kernel."""
+    """Select the Hessian kernel inside the block: "split16x3" (default; fp16 / bf16 X: each
+    fp32 product exactly, from three 16-bit MFMA products), "split16" (fp16 X: from two, within
+    2^-23 relative; bf16 X as the default) or "fp32" (fp32 MFMA).  The choice is process-wide.
+    fp32 inputs take the fp32-X split kernel (three MFMAs per product, each within ~2^-20.5
+    relative) under both split modes, and the fp32 MFMA kernel under "fp32"."""
     lib = nat.load()
     prev = int(lib.rq_hessian_math(HESSIAN_MATH[mode]))
     if prev < 0:
@@ -180,8 +192,17 @@ def find_params_mse(w, maxq, sym, norm=2.4, grid=50, maxshrink=0.5, group_size=-
     return scale, zero
 
 
+def check_act_order_width(C):
+    """act_order sorts at most RQ_ACT_ORDER_MAXC columns (rq_act_order_perm); the fasterquant
+    entry points call this before any device work, so a wider linear is refused up front."""
+    if C > nat.RQ_ACT_ORDER_MAXC:
+        raise NotImplementedError(f"actorder=True supports at most {nat.RQ_ACT_ORDER_MAXC} input columns "
+                                  f"on the HIP path (got {C})")
+
+
 def act_order_perm(act_sq):
     C = act_sq.numel()
+    check_act_order_width(C)
     perm = torch.empty(C, dtype=torch.int64, device=act_sq.device)
     invperm = torch.empty(C, dtype=torch.int64, device=act_sq.device)
     nat.call("rq_act_order_perm", nat.ptr(act_sq), C, nat.ptr(perm), nat.ptr(invperm), _stream(act_sq))

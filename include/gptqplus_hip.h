@@ -1,9 +1,13 @@
 /*
  * C ABI of the MI355X (gfx950) GPTQ+ per-linear quantization hot path.
  *
- * Every entry point takes device pointers allocated by the caller (no allocation happens
- * inside the library), a hipStream_t passed as `void*`, launches asynchronously on that
- * stream and returns an int status:  0 = ok, <0 = argument / HIP error (RQ_E*).  Shapes are
+ * Every entry point takes device pointers allocated by the caller (no entry point allocates
+ * device memory), a hipStream_t passed as `void*`, launches asynchronously on that stream and
+ * returns an int status:  0 = ok, <0 = argument / HIP error (RQ_E*).  The one static device
+ * allocation is the scratch array of rq_hessian_accum_noalloc: RQ_NOALLOC_SCRATCH_BYTES
+ * (128 MiB) of `__device__` memory that the loader places on every GPU the library's code
+ * object is loaded on, held until the process ends, whether or not that entry point is
+ * called.  Shapes are
  * validated on the host before any launch.  Matrices are row-major with explicit leading
  * dimensions (in elements).  The reference implementation is Python; the citations name
  * the reference code each call replaces (file:line in Mrluxianseng/gptq_plus_mp_quant).
@@ -60,12 +64,14 @@ int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets, int x_dtyp
  * the 16-bit MFMA pipe from the weighted operand cut into 16-bit pieces (after an exact
  * power-of-two column scaling), and accumulate in fp32; they need the workspace (with less
  * than rq_hessian_workspace_bytes the fp32 kernel runs instead).
- * RQ_HMATH_SPLIT16 (default): fp16 X in two pieces (22 of the operand's 24 bits: each product
- *   within 2^-23 relative of the reference's), bf16 X in three (exact products); fp32 X with x
- *   itself in two fp16 pieces too, three MFMAs per product (hi w0, hi w1, lo w0: each product
- *   within ~2^-20.5 relative).
- * RQ_HMATH_SPLIT16X3: three pieces for fp16 X too (exact products, 1.5x the MFMA work).
- * RQ_HMATH_FP32: fp32 MFMA on converted operands (also for fp32 X).
+ * RQ_HMATH_SPLIT16X3 (default): fp16 and bf16 X with the weighted operand in three pieces
+ *   (11 + 11 + 2 or 8 + 8 + 8 bits): the reference's fp32 products exactly (for fp16, every
+ *   operand within 2^15 of its column's largest; below that within 2^-40 of the largest).
+ * RQ_HMATH_SPLIT16 (opt-in, faster): fp16 X in two pieces (22 of the operand's 24 bits: each
+ *   product within 2^-23 relative of the reference's, 2/3 of the MFMA work), bf16 X in three.
+ * Both split modes take fp32 X with x itself in two fp16 pieces, three MFMAs per product
+ * (hi w0, hi w1, lo w0: each product within ~2^-20.5 relative; k_hessian_split32).
+ * RQ_HMATH_FP32: fp32 MFMA on converted operands (exact fp32 products, also for fp32 X).
  * mode < 0 queries.  Returns the previous mode, or RQ_EINVAL.  No counterpart in the
  * reference (its bmm runs in fp32, gptq_plus_utils.py:845-847). */
 #define RQ_HMATH_SPLIT16 0
@@ -135,7 +141,9 @@ int rq_find_params_mse(const void* w, int w_dtype, int R, int C, int64_t ldw, in
 /* act_order permutation -- gptq_plus_utils.py:1046, 1050 (classic GPTQ: argsort of diag(H)):
  * perm = torch.argsort(act_sq, descending=True) exactly as torch returns it on the CPU, ties
  * included (the order libstdc++'s introsort leaves equal keys in; NaN first), and
- * invperm = argsort(perm).  int64 outputs.  C <= 65536. */
+ * invperm = argsort(perm).  int64 outputs.  C <= RQ_ACT_ORDER_MAXC (the widest linear of
+ * today's models has 53248 input columns), else RQ_EINVAL. */
+#define RQ_ACT_ORDER_MAXC 65536
 int rq_act_order_perm(const float* act_sq, int C, int64_t* perm, int64_t* invperm, void* stream);
 
 /* Per-subgroup slicing, dead columns and act_order gather -- gptq_plus_utils.py:1033-1050.

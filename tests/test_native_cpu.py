@@ -100,3 +100,25 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(nat, "_lib", None)
     with pytest.raises(RuntimeError, match="not built"):
         nat.load()
+
+
+def test_act_order_width_refused_before_device_work():
+    """rq_act_order_perm sorts at most RQ_ACT_ORDER_MAXC columns; both fasterquant entry points
+    refuse a wider act_order linear with NotImplementedError before any device work (the
+    objects here carry CPU tensors only, so any launch would fail differently)."""
+    lib = _lib()
+    from gptq_plus_mp_quant_amd import GPTQ, GPTQPlus, WeightQuantizer
+    from gptq_plus_mp_quant_amd import kernels as K
+    fake = ctypes.c_void_p(16)
+    assert lib.rq_act_order_perm(fake, nat.RQ_ACT_ORDER_MAXC + 1, fake, fake, None) == nat.RQ_EINVAL
+    K.check_act_order_width(nat.RQ_ACT_ORDER_MAXC)
+    with pytest.raises(NotImplementedError, match="at most 65536"):
+        K.check_act_order_width(nat.RQ_ACT_ORDER_MAXC + 1)
+    q = WeightQuantizer()
+    q.configure(4, perchannel=True, sym=False)
+    for cls in (GPTQPlus, GPTQ):
+        g = object.__new__(cls)
+        g.rows, g.columns, g.quantizer, g.profile_recorder, g._finalized = 4, nat.RQ_ACT_ORDER_MAXC + 1, q, None, True
+        g.layer = torch.nn.Linear(4, 4, bias=False)
+        with pytest.raises(NotImplementedError, match="at most 65536"):
+            g.fasterquant(blocksize=128, actorder=True)

@@ -71,12 +71,15 @@ def test_noalloc_matches_workspace_entry(dtype):
 
 
 def test_noalloc_rejects_oversize():
-    x = torch.zeros((8, 64), dtype=torch.float16, device=DEV)
-    s = torch.ones((8, 1), device=DEV)
-    H = torch.zeros((1, 64, 64), device=DEV)
-    lib = nat.load()
-    C = 8192
+    """Buffers sized for the shape the call states (x [ntok, C] of ones, s [ntok, 1], H [1, C, C]),
+    so that a guard that let the call through would compute a non-zero H within bounds and fail
+    the assertions, rather than touch memory past the tensors."""
+    C = 1024
     ntok = (nat.RQ_NOALLOC_SCRATCH_BYTES // (2 * C)) + 4096          # the chunk copy alone is larger
+    x = torch.ones((ntok, C), dtype=torch.float16, device=DEV)
+    s = torch.ones((ntok, 1), device=DEV)
+    H = torch.zeros((1, C, C), device=DEV)
+    lib = nat.load()
     rc = lib.rq_hessian_accum_noalloc(nat.ptr(x), nat.RQ_F16, ntok, C, C, nat.ptr(s), 1, 1, nat.ptr(H), None,
                                       nat.stream_of(DEV))
     assert rc == nat.RQ_EINVAL
