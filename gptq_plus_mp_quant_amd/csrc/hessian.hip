@@ -498,11 +498,19 @@ __device__ __forceinline__ void split_staged(const uint8_t* st, int wave, int la
 // each of the XDEPTH-3 steps since, so vmcnt(2 * (XDEPTH - 3)) covers this wave's part of both
 // whatever the issue order within a step, and after the barrier the other waves' parts are in
 // LDS too.  The barrier also orders every read of the FILL stage (the stage of step k-1, read
-// during step k-2) before its refill.  Then: stage step k+XDEPTH-1; issue the PC x 8 MFMAs
-// of step k from registers, while the row fragments of step k+1 are read and this wave's column
-// fragment of step k+1 is split in between.  The MFMAs need no LDS read after the barrier, so
-// the two waves of a SIMD resume issuing as soon as it opens.  RQ_STAGE_BARRIER, not
-// __syncthreads, whose fence would wait for every staging load in flight.
+// during step k-2) before its refill.  RQ_STAGE_BARRIER, not __syncthreads, whose fence would
+// wait for every staging load in flight.
+// After the barrier: stage step k+XDEPTH-1 (row fragment w, this wave's column fragment), read
+// the next step's column fragment and saliencies, then work through the row blocks in pairs:
+// the pair's PC x 2 MFMAs (smallest piece first into each accumulator, the two accumulators
+// alternating), the split of one token pair of the next step's column fragment, then the pair's
+// row fragments of the next step, which this step no longer reads.  The pairs are pinned with
+// sched_barrier: left alone, the compiler sinks all the next step's LDS reads behind the last
+// MFMA, so every wave then waits on a burst of LDS reads right before the barrier (measured:
+// MFMA busy 67 / 72 % -> 71 / 76 % at C = 4096 / 14336 with the reads spread).  The saliency
+// staging (wave 0, lanes 0-3, a branch) comes last, so the step's main work is one scheduling
+// region.  Its vmcnt accounting is unchanged: wave 0's saliency load of step k+XDEPTH-1 still
+// follows that step's row / column loads.
 // DIAG (a diagonal tile): row blocks below this wave's column block hold only the discarded
 // lower triangle, so their row fragments are not read and their MFMAs not issued (bi < lim).
 template <typename TX, int PC, bool DIAG, int KP, int CUR, int NXT, int FILL>
@@ -515,7 +523,14 @@ __device__ __forceinline__ void split_step(uint4 (&p)[2][PC], uint4 (&a)[2][8], 
   constexpr int NP = 1 - KP;
   XWAIT_VM(2 * (XDEPTH - 3));
   RQ_STAGE_BARRIER();
-  stage_step(L.s[FILL], pa, pb, sg, wave, lane, min(k + XDEPTH - 1, last));
+  const int64_t kf = min(k + XDEPTH - 1, last);
+  {
+    int64_t kk = kf;
+    asm volatile("" : "+s"(kk));
+    const int64_t off = kk * 512;                     // 1 KB per step and fragment
+    lds_dma16(pa + off, L.s[FILL] + wave * 1024);
+    lds_dma16(pb + off, L.s[FILL] + XB_OFF + wave * 1024);
+  }
   const uint8_t* nxt = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[NXT] + lane * 16, 16));
   const uint8_t* w = static_cast<const uint8_t*>(
       __builtin_assume_aligned(L.s[NXT] + XB_OFF + wave * 1024 + lane * 16, 16));
@@ -523,31 +538,29 @@ __device__ __forceinline__ void split_step(uint4 (&p)[2][PC], uint4 (&a)[2][8], 
   const uint4 b = *reinterpret_cast<const uint4*>(w);
   const float4 s0 = *reinterpret_cast<const float4*>(sp);
   const float4 s1 = *reinterpret_cast<const float4*>(sp + 16);
-#pragma unroll
-  for (int bi = 0; bi < 8; ++bi)
-    if (!DIAG || bi < lim) a[NP][bi] = *reinterpret_cast<const uint4*>(nxt + bi * 1024);
   const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
   const uint32_t xw[4] = {b.x, b.y, b.z, b.w};
   uint32_t o[XNPMAX][4];
-  // smallest piece first into every accumulator, then the others, two or four MFMAs after
-  // each token pair of the next step's split
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int bi = 0; bi < 8; ++bi)
-    if (!DIAG || bi < lim)
-      acc[bi] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][PC - 1]), acc[bi]);
-  constexpr int PER_M = (PC - 1) * 2;
+  for (int j = 0; j < 4; ++j) {
+    const int b0 = 2 * j, b1 = 2 * j + 1;
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    split_pair<TX, PC>(xw[m], sv[2 * m], sv[2 * m + 1], sc, o[0][m], o[1][m], o[2][m]);
-#pragma unroll
-    for (int i = PER_M * m; i < PER_M * m + PER_M; ++i) {
-      const int q = (PC - 2) - i / 8, bi = i % 8;
-      if (!DIAG || bi < lim)
-        acc[bi] = T::mfma(__builtin_bit_cast(v8, a[KP][bi]), __builtin_bit_cast(v8, p[KP][q]), acc[bi]);
+    for (int q = PC - 1; q >= 0; --q) {
+      if (!DIAG || b0 < lim)
+        acc[b0] = T::mfma(__builtin_bit_cast(v8, a[KP][b0]), __builtin_bit_cast(v8, p[KP][q]), acc[b0]);
+      if (!DIAG || b1 < lim)
+        acc[b1] = T::mfma(__builtin_bit_cast(v8, a[KP][b1]), __builtin_bit_cast(v8, p[KP][q]), acc[b1]);
     }
+    split_pair<TX, PC>(xw[j], sv[2 * j], sv[2 * j + 1], sc, o[0][j], o[1][j], o[2][j]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!DIAG || b0 < lim) a[NP][b0] = *reinterpret_cast<const uint4*>(nxt + b0 * 1024);
+    if (!DIAG || b1 < lim) a[NP][b1] = *reinterpret_cast<const uint4*>(nxt + b1 * 1024);
+    __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
   for (int q = 0; q < PC; ++q) p[NP][q] = make_uint4(o[q][0], o[q][1], o[q][2], o[q][3]);
+  if (wave == 0 && lane < 4) lds_dma16(sg + 16 * kf + 4 * lane, L.s[FILL] + XS_OFF);
 }
 
 // Steps k .. k+nsteps-1 (nsteps <= XDEPTH) of the unrolled schedule: step k+J uses stage J,
@@ -1605,7 +1618,7 @@ int kernel_slots(K kfn, int threads, int which) {
   return cache[which][dev];
 }
 int hessian_slots() { return kernel_slots(k_hessian_accum<__half>, HTHREADS, 0); }
-int split_slots() { return kernel_slots(k_hessian_split<__half, 2>, XTHREADS, 1); }
+int split_slots() { return kernel_slots(k_hessian_split<__half, 3>, XTHREADS, 1); }
 
 // Items of the last, partly filled round and their slice count: the most slices that still
 // fit the tail into one round (S = slots / tail, S <= maxS, at least 4 token slabs per slice).
@@ -1800,8 +1813,9 @@ int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, c
   const int full = (int)(total - tail);
   int* cnt = tail > 0 ? reinterpret_cast<int*>(ws) : nullptr;
   float* wsf = tail > 0 ? reinterpret_cast<float*>(wb + L.off_part) : nullptr;
-  dim3 grid((unsigned)(full + (int64_t)tail * S)), block(XTHREADS);
+  dim3 grid((unsigned)(full + (int64_t)tail * S));
   hipEvent_t stop = timing_begin(s);
+  const dim3 block(XTHREADS);
   if (x_dtype == RQ_F16 && g_hmath.load() == RQ_HMATH_SPLIT16X3)
     hipLaunchKernelGGL((k_hessian_split<__half, 3>), grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg, ntarg, nt,
                        ntiles, nks, full, S, wsf, cnt);

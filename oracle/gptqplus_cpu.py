@@ -22,7 +22,11 @@ It restates, op for op and in the same torch call order on CPU tensors, the refe
   write-back -- ``gptq_plus_utils.py:910-1396, 1500-1570, 1850-1896``.
 
 One deviation, opt-in: ``dtype`` lets the same sequence run in float64 (used by the
-closed-form pinning tests).
+closed-form pinning tests).  One report, opt-in: ``fasterquant(record_ratio=True)`` also
+returns the value ``w / scale`` that each code rounds (the operand of ``torch.round`` at
+quant_utils.py:477 / gptq_plus_utils.py:1306-1310), computed by the same division, so code
+flips against another implementation can be classified as exact rounding ties or
+near-boundary flips; it changes no computed value.
 
 Parity pinning (see ``tests/test_oracle_*.py``): golden vectors written by importing the
 reference (``tests/golden/make_golden.py``), fp64 brute-force Hessians, scipy fp64
@@ -502,6 +506,7 @@ class FasterquantResult:
     W_int: torch.Tensor        # (R, C) integer-valued codes (compute dtype), natural order
     Scale: torch.Tensor        # (R, C) per-element scale, natural order
     subgroups: List[SubgroupRecord] = field(default_factory=list)
+    ratio: Optional[torch.Tensor] = None   # (R, C) w / scale each code rounds (record_ratio)
 
 
 class GPTQPlusOracle:
@@ -587,7 +592,7 @@ class GPTQPlusOracle:
                     grad_gate_sharpness=1.0, grad_gate_sine_amp=0.0, second_order_scale=1.0,
                     grad_clip=1.0, slide_refresh_start=0,
                     slide_refresh_block_total=None, block_observer=None,
-                    refresh_full_metrics=False) -> FasterquantResult:
+                    refresh_full_metrics=False, record_ratio=False) -> FasterquantResult:
         # g_update modes: gptq_plus_utils.py:1190-1199, 1360-1367 (inner), 1408-1448
         # (block_backward refresh), 1500-1570 (outer), 1572-1848 (block_gd step)
         if g_update_mode not in ("frozen", "surrogate_block", "surrogate_online", "block_gd",
@@ -675,6 +680,7 @@ class GPTQPlusOracle:
                                if block_gd else None,
                                invperm=invperm, Q=torch.zeros_like(W_sub),
                                W_int=torch.zeros_like(W_sub), Scale=torch.zeros_like(W_sub),
+                               Ratio=torch.zeros_like(W_sub) if record_ratio else None,
                                fast_scale=fast_scale_full[r0:r1] if fast else None))
 
         n_blocks = (self.columns + blocksize - 1) // blocksize         # :1165-1167
@@ -731,6 +737,8 @@ class GPTQPlusOracle:
                         Q1.copy_(q)
                         W_int1.copy_(iw)
                         Scale1.copy_(sc.expand_as(W_block_start))
+                        if record_ratio:
+                            st["Ratio"][:, i1:i2] = W_block_start / sc
                     else:
                         for i in range(count):
                             qz, a, b = column_quantizer(i)
@@ -738,6 +746,8 @@ class GPTQPlusOracle:
                             Q1[:, i] = q.flatten()
                             W_int1[:, i] = iw.flatten()
                             Scale1[:, i] = sc.flatten()
+                            if record_ratio:
+                                st["Ratio"][:, i1 + i] = (W_block_start[:, i].unsqueeze(1) / sc).flatten()
                     residual = W_block_start - Q1 - GHinv1_eff
                     Err1.copy_(torch.linalg.solve_triangular(Hinv1.T, residual.T, upper=False).T)
                 else:                                                  # :1296-1367
@@ -753,6 +763,8 @@ class GPTQPlusOracle:
                         else:
                             qz, a, b = column_quantizer(i)
                             q_fake, iw, sc = qz.fake_quantize(w_col, st_idx=a, end_idx=b)
+                        if record_ratio:
+                            st["Ratio"][:, i1 + i] = (w_col / sc).flatten()
                         q = q_fake.flatten()
                         Q1[:, i] = q
                         W_int1[:, i] = iw.flatten()
@@ -870,6 +882,7 @@ class GPTQPlusOracle:
                     if upd.numel() > 0:
                         st["W_sub"][:, i2:] -= upd
 
+        Ratio_final = torch.zeros_like(W) if record_ratio else None
         for st in states:                                              # :1850-1864
             Q, W_int_sub, Scale_sub = st["Q"], st["W_int"], st["Scale"]
             if actorder:
@@ -879,12 +892,14 @@ class GPTQPlusOracle:
             Q_final[st["r0"]:st["r1"], :] = Q
             W_int_final[st["r0"]:st["r1"], :] = W_int_sub
             Scale_final[st["r0"]:st["r1"], :] = Scale_sub
+            if record_ratio:
+                Ratio_final[st["r0"]:st["r1"], :] = st["Ratio"][:, st["invperm"]] if actorder else st["Ratio"]
 
         Q_out = Q_final.reshape(self.weight.shape).to(self.weight.dtype)   # :1873-1875
         if torch.any(torch.isnan(Q_out)):
             raise ValueError("NaN in weights")
         return FasterquantResult(Q=Q_out, Q_fp32=Q_final, W_int=W_int_final, Scale=Scale_final,
-                                 subgroups=records)
+                                 subgroups=records, ratio=Ratio_final)
 
 
 # ---------------------------------------------------------------------------------------

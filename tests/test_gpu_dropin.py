@@ -13,18 +13,28 @@ own choosing), amplified by the count*GHinv - (Z D) Hinv cancellation, and block
 refreshed terms.  Flips are held to 0.01 % except in the cases FLIP_BAR lists with their
 measured counts; the layer reconstruction error stays within 0.5 % relative.
 """
+import json
+import os
+
 import numpy as np
 import pytest
 import torch
 
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer, reconstruction_error
-from tests._util import code_flips, rel_fro, synth
+from tests._util import code_flips, flip_report, rel_fro, synth
 from tests.golden.fixtures import GoldenSet, quadratic_refresh
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 GOLD = GoldenSet.load().cases
+
+
+def _log(rec):
+    path = os.environ.get("RQ_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(rec) + "\n")
 
 
 def _z_zero(m):
@@ -227,7 +237,9 @@ def test_dropin_vs_oracle(cfg):
     # the refresh modes also hand their refresh_full_metrics statistics to block_observer
     refresh = fq["g_update_mode"] in ("block_gd", "block_backward")
     recs_o, recs_g = [], []
-    res = o.fasterquant(**fq, **(dict(block_observer=recs_o.append, refresh_full_metrics=True) if refresh else {}))
+    res = o.fasterquant(record_ratio=True, **fq,
+                        **(dict(block_observer=recs_o.append, refresh_full_metrics=True) if refresh else {}))
+    perm = res.subgroups[0].perm if cfg["act"] else None
 
     g, layer = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"], cfg.get("mse", False),
                           cfg.get("pc", True))
@@ -247,6 +259,7 @@ def test_dropin_vs_oracle(cfg):
         assert torch.equal(g.perm.cpu(), res.subgroups[0].perm)
     n = res.W_int.numel()
     flips_same = code_flips(layer.int_weight, res.W_int)
+    rep_same = flip_report(layer.int_weight, res.W_int, res.ratio, perm)
     print(f"{cfg['name']}: flips with the oracle's H^-1 {flips_same}/{n}")
     if _z_zero(cfg):
         assert flips_same == 0
@@ -281,11 +294,74 @@ def test_dropin_vs_oracle(cfg):
         assert rel_fro(g2.Hinv_all[sidx], rec.Hinv) <= 1e-4
     flips_own = code_flips(layer2.int_weight, res.W_int)
     print(f"{cfg['name']}: flips with its own H^-1 {flips_own}/{n}")
+    _log(dict(case=f"oracle_cfg_{cfg['name']}", R=R, C=C, G=G, mode=cfg.get("mode", "frozen"), codes=n,
+              flips_oracle_hinv=rep_same, flips_oracle_hinv_and_terms=terms_flips,
+              flips_own_chain=flip_report(layer2.int_weight, res.W_int, res.ratio, perm)))
     assert flips_own <= FLIP_BAR.get(cfg["name"], n // 10000), flips_own
     Xf = X.float().reshape(-1, C)
     e_gpu = reconstruction_error(W.float(), layer2.weight.data.float().cpu(), Xf)
     e_ref = reconstruction_error(W.float(), res.Q.float(), Xf)
     assert abs(e_gpu - e_ref) <= 0.005 * e_ref
+
+
+TERM_CASES = ["g2_sym4_static_gplus", "g2_sym4_surrogate_block_static", "g4_asym4_surrogate_online"]
+
+
+@pytest.mark.parametrize("name", TERM_CASES)
+def test_gplus_term_flip_sources(name):
+    """Which GPTQ+ term moves the codes when Z != 0 (gptq_plus_utils.py:174-194, 563-578).  Both
+    sides share H and the reference's H^-1; the GPU's own beta / Z / GHinv are then swapped for
+    the reference's one at a time.  Reported per case: each term's difference, the flips with
+    each single term injected, and the own-terms flips classified by the reference's
+    pre-rounding value (exact ties; the first flip of each row against the later ones, which
+    follow that row's changed error feedback).  With all three injected the codes are equal."""
+    cfg = next(c for c in CFGS if c["name"] == name)
+    R, C, G = cfg["R"], cfg["C"], cfg["G"]
+    N, T = 8, 256
+    X, W, s, grad = synth(sum(map(ord, name)), R, C, G, N, T, gscale=cfg.get("gscale", 1e-4))
+    alpha, ref_loss = cfg["alpha"], cfg.get("ref_loss", 0.0)
+    o = GPTQPlusOracle(W, s, grad, G, alpha, ref_loss)
+    o.quantizer = make_quantizer(cfg["bits"], cfg["sym"])
+    for j in range(0, N, 4):
+        o.add_batch(X[j:j + 4])
+    o.finalize_hessian()
+    fq = dict(blocksize=cfg["B"], percdamp=0.01, groupsize=cfg["gs"], actorder=cfg["act"],
+              static_groups=cfg["act"], block_atomic_quant=cfg["atomic"], **_mode_kwargs(cfg, X, W, grad))
+    res = o.fasterquant(record_ratio=True, **fq)
+    perm = res.subgroups[0].perm if cfg["act"] else None
+    hinv = [(r.Hinv_init.to(DEV), r.Hinv.to(DEV)) for r in res.subgroups]
+    Rs = R // G
+
+    def run(terms=None, keep=False):
+        g, layer = _gpu_obj(W, s, grad, G, alpha, ref_loss, cfg["bits"], cfg["sym"])
+        g.H, g.act_square, g._finalized = o.H.to(DEV).clone(), o.act_square.to(DEV).clone(), True
+        inj = dict(hinv=hinv) if terms is None else dict(hinv=hinv, terms=terms)
+        g.fasterquant(export_to_et=True, keep_hinv=keep, inject=inj, **fq)
+        torch.cuda.synchronize()
+        return g, layer.int_weight.cpu()
+
+    g0, codes0 = run(keep=True)
+    own = [(g0.subgroup_info[k]["beta"].reshape(-1).clone(), g0.Z[k * Rs:(k + 1) * Rs].clone(),
+            g0.GHinv_initial[k * Rs:(k + 1) * Rs].clone()) for k in range(G)]
+    ref = [(r.beta.to(DEV).reshape(-1), r.Z.to(DEV), r.GHinv.to(DEV)) for r in res.subgroups]
+    beta_err = max(float((a[0] - b[0]).abs().max() / b[0].abs().max().clamp_min(1e-30)) for a, b in zip(own, ref))
+    z_err = max(rel_fro(a[1], b[1]) for a, b in zip(own, ref))
+    gh_err = max(rel_fro(a[2], b[2]) for a, b in zip(own, ref))
+    flips = {}
+    for label, pick in (("beta", (1, 0, 0)), ("Z", (0, 1, 0)), ("GHinv", (0, 0, 1)), ("Z+GHinv", (0, 1, 1)),
+                        ("all", (1, 1, 1))):
+        terms = [tuple(rf[i] if pick[i] else ow[i] for i in range(3)) for ow, rf in zip(own, ref)]
+        flips[label] = code_flips(run(terms)[1], res.W_int)
+    n = res.W_int.numel()
+    rep = flip_report(codes0, res.W_int, res.ratio, perm)
+    rec = dict(case=f"terms_{name}", R=R, C=C, G=G, mode=cfg.get("mode", "frozen"), codes=n,
+               beta_max_rel_diff=beta_err, z_rel_fro=z_err, ghinv_rel_fro=gh_err,
+               flips_own_terms=rep, flips_with_ref_term=flips)
+    print(rec, flush=True)
+    _log(rec)
+    assert flips["all"] == 0
+    assert z_err <= 1e-4 and gh_err <= 1e-4
+    assert rep["flips"] <= FLIP_BAR.get(name, n // 10000)
 
 
 @pytest.mark.parametrize("groups", [(4, 4, 4), (12, 12, 12), (48, 1, 2)])

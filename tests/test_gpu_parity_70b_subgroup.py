@@ -24,7 +24,7 @@ import torch
 
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
-from tests._util import rel_fro
+from tests._util import flip_report, rel_fro
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -58,7 +58,7 @@ def test_70b_width_subgroup_parity():
     o.finalize_hessian()
     o.H = g.H.cpu()
     act_bad = int((g.act_square.cpu() != o.act_square).sum())
-    res = o.fasterquant(**FQ)
+    res = o.fasterquant(record_ratio=True, **FQ)
 
     H_keep, act_keep = g.H.clone(), g.act_square.clone()
     g.fasterquant(export_to_et=True, inject={"hinv": [(r.Hinv_init.to(DEV), r.Hinv.to(DEV)) for r in res.subgroups]},
@@ -78,6 +78,7 @@ def test_70b_width_subgroup_parity():
     torch.cuda.synchronize()
     hinv_err = rel_fro(g2.Hinv_all[0], res.subgroups[0].Hinv)
     flips_own = int((layer.int_weight.cpu() != res.W_int).sum())
+    rep_own = flip_report(g2.codes, res.W_int, res.ratio, res.subgroups[0].perm)
     # the damped working matrix (P H P, dead columns as the chain handles them) in fp64 on the GPU
     p = g2.perm
     Hw = H_keep[0][p][:, p].double()
@@ -104,7 +105,7 @@ def test_70b_width_subgroup_parity():
                perm_mismatch=perm_bad, flips_with_oracle_hinv=flips_inj, q_equal_with_oracle_hinv=q_equal,
                flips_own_chain=flips_own, codes=n, hinv_rel_fro=hinv_err, hinv_vs_fp64=gpu_vs_64,
                oracle_hinv_vs_fp64=ref_vs_64, recon_gpu=e_gpu, recon_oracle=e_ref,
-               recon_rel_diff=abs(e_gpu - e_ref) / e_ref)
+               recon_rel_diff=abs(e_gpu - e_ref) / e_ref, own_chain_flip_report=rep_own)
     print(json.dumps(rec), flush=True)
     path = os.environ.get("RQ_PARITY_LOG")
     if path:

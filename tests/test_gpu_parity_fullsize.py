@@ -3,16 +3,22 @@ configs[0] (q_proj 4096 x 4096, NUM_GROUPS = 1, w4 asym per-channel, act_order, 
 term off) and configs[1] (the same with NUM_GROUPS = 4 and the GPTQ+ term on at alpha = 0),
 128 x 2048 calibration tokens fed in add_batch chunks of 16 samples.
 
-The CPU oracle cannot form the 4 x 4096^2 Hessians from 262144 tokens in a test's time, so:
-- act_square is computed by the oracle from the same chunks (gptq_plus_utils.py:856, 889) and
-  must equal the GPU's bit for bit, and the act_order permutation must equal the oracle's
-  torch.argsort of it (:1046) exactly;
-- the GPU's finalized H is handed to the oracle, which then runs the reference's fasterquant
-  (fp32 LAPACK chain, column loop, trailing update) on the CPU;
-- with the oracle's H^-1 injected the codes must be equal (Z = 0: every later stage is
-  bit-exact); with the GPU's own fp64 chain, H^-1 within 1e-4 (rel. Frobenius) of the
-  oracle's, code flips <= 0.01 %, and the layer reconstruction error
-  ||(W - Q) X^T||^2 / ||W X^T||^2 over all tokens within 0.5 % of the oracle's.
+Three comparisons per case:
+- each side end to end on its own: the oracle accumulates its Hessians from the same chunks
+  (the reference's fp32 `weighted` and bmm, gptq_plus_utils.py:846-850) and runs its own fp32
+  LAPACK chain; the GPU runs its exact-product Hessian (the default) and its own fp64 chain.
+  H within 1e-4 (rel. Frobenius, per group) of the oracle's, act_square bit for bit, the
+  act_order permutation equal, the layer reconstruction error ||(W - Q) X^T||^2 / ||W X^T||^2
+  over all tokens within 0.5 % of the oracle's, code flips <= 0.01 %.  Every flip is classified
+  by the oracle's pre-rounding value w / scale: exact rounding ties, and the distance of the
+  others from the rounding midpoint (tests/_util.flip_report).  The first flip of each row
+  ("primary"; the later ones follow the row's changed error feedback) must be an exact tie or
+  within 256 fp32 ulps of one, and at most 0.001 % of the codes.  The same holds for the opt-in
+  two-piece Hessian ("split16");
+- the GPU's finalized H handed to the oracle: with the oracle's H^-1 injected the codes must be
+  equal (Z = 0: every later stage is bit-exact);
+- the GPU's own fp64 chain on that H: H^-1 within 1e-4 of the oracle's, flips <= 0.01 %, and
+  the reconstruction error within 0.5 %.
 Each case's numbers are printed and, when RQ_PARITY_LOG names a file, appended to it as JSON.
 """
 import json
@@ -22,8 +28,9 @@ import pytest
 import torch
 
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
+from gptq_plus_mp_quant_amd import kernels as K
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
-from tests._util import rel_fro
+from tests._util import flip_report, rel_fro
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -87,12 +94,22 @@ def test_full_shape_parity(name):
     H_gpu = g.H.clone()
     fq = dict(blocksize=128, percdamp=0.01, groupsize=-1, actorder=True, static_groups=True)
 
-    # oracle: act_square from the same chunks, H from the GPU
+    # the oracle end to end: its own Hessians from the same chunks, its own chain
+    o_own = GPTQPlusOracle(W.cpu(), s.cpu(), grad.cpu(), G, 0.0, 0.0)
+    o_own.quantizer = make_quantizer(4, False)
+    for j in range(0, N, BSZ):
+        print(f"{name}: oracle add_batch chunk {j // BSZ}", flush=True)
+        o_own.add_batch(X[j:j + BSZ].cpu())
+    o_own.finalize_hessian()
+    h_err = [rel_fro(H_gpu[k], o_own.H[k]) for k in range(G)]
+    res_own = o_own.fasterquant(record_ratio=True, **fq)
+    print(f"{name}: H rel-Frobenius per group {h_err}", flush=True)
+
+    # the oracle on the GPU's H (act_square: its own, from the same chunks)
     o = GPTQPlusOracle(W.cpu(), s.cpu(), grad.cpu(), G, 0.0, 0.0)
     o.quantizer = make_quantizer(4, False)
-    for j in range(0, N, BSZ):
-        o.add_batch(X[j:j + BSZ].cpu(), hessian=False)
-    o.finalize_hessian()
+    o.act_square = o_own.act_square.clone()
+    o.index, o.token_count, o._finalized = o_own.index, o_own.token_count, True
     o.H = H_gpu.cpu()
     act_bad = int((g.act_square.cpu() != o.act_square).sum())
     print(f"{name}: act_square entries differing from the CPU sum: {act_bad}/{C}", flush=True)
@@ -121,12 +138,30 @@ def test_full_shape_parity(name):
     n = res.W_int.numel()
     e_gpu = _recon(W, layer.weight.data, X)
     e_ref = _recon(W, res.Q.to(DEV), X)
+    # (3) each side's own Hessian and chain: the GPU's default H (g2's) against the oracle's
+    # own; then the opt-in two-piece Hessian, accumulated again
+    own = flip_report(g2.codes, res_own.W_int, res_own.ratio, res_own.subgroups[0].perm)
+    e_own_ref = _recon(W, res_own.Q.to(DEV), X)
+    g3 = gpu_obj()
+    with K.hessian_math("split16"):
+        for j in range(0, N, BSZ):
+            g3.add_batch(X[j:j + BSZ], None)
+    g3.finalize_hessian()
+    h2_err = [rel_fro(g3.H[k], o_own.H[k]) for k in range(G)]
+    g3.fasterquant(**fq)
+    torch.cuda.synchronize()
+    own2 = flip_report(g3.codes, res_own.W_int, res_own.ratio, res_own.subgroups[0].perm)
+    e_own2_gpu = _recon(W, layer.weight.data, X)
     rec = dict(case=name, R=R, C=C, G=G, tokens=N * T, act_square_mismatch=act_bad, exact_ties_in_act_square=ties,
                perm_mismatch=perm_bad, flips_with_oracle_hinv=flips_inj, q_equal_with_oracle_hinv=q_equal,
                flips_own_chain=flips_own, codes=n, hinv_rel_fro=hinv_err, hinv_init_rel_fro=hinit_err,
                recon_gpu=e_gpu, recon_oracle=e_ref, recon_rel_diff=abs(e_gpu - e_ref) / e_ref,
                damp=[i["damp_percent"] for i in g2.subgroup_info],
-               oracle_damp=[r.damp_percent for r in res.subgroups])
+               oracle_damp=[r.damp_percent for r in res.subgroups],
+               own_h_rel_fro=h_err, own_flips=own, own_recon_gpu=e_gpu, own_recon_oracle=e_own_ref,
+               own_recon_rel_diff=abs(e_gpu - e_own_ref) / e_own_ref,
+               split16_h_rel_fro=h2_err, split16_own_flips=own2, split16_own_recon_gpu=e_own2_gpu,
+               split16_own_recon_rel_diff=abs(e_own2_gpu - e_own_ref) / e_own_ref)
     _log(rec)
     assert act_bad == 0
     assert perm_bad == 0
@@ -134,3 +169,9 @@ def test_full_shape_parity(name):
     assert hinv_err <= 1e-4 and hinit_err <= 1e-4
     assert flips_own <= n // 10000
     assert abs(e_gpu - e_ref) <= 0.005 * e_ref
+    assert max(h_err) <= 1e-4 and max(h2_err) <= 1e-4
+    for r in (own, own2):
+        assert r["flips"] <= n // 10000
+        assert r["primary"] <= n // 100000 and r.get("primary_ulps_le_256", 0) == r["primary"]
+    assert abs(e_gpu - e_own_ref) <= 0.005 * e_own_ref
+    assert abs(e_own2_gpu - e_own_ref) <= 0.005 * e_own_ref

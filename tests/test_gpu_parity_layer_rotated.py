@@ -29,7 +29,7 @@ import torch
 
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer, add_batch_shared
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
-from tests._util import rel_fro
+from tests._util import flip_report, rel_fro
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -129,13 +129,14 @@ def test_rotated_layer_linear_parity(rotated_layer, name):
     o.finalize_hessian()
     o.H = g.H.cpu()
     act_bad = int((g.act_square.cpu() != o.act_square).sum())
-    res = o.fasterquant(**FQ)
+    res = o.fasterquant(record_ratio=True, **FQ)
 
     H_keep, act_keep = g.H.clone(), g.act_square.clone()
     g.fasterquant(export_to_et=True, inject={"hinv": [(r.Hinv_init.to(DEV), r.Hinv.to(DEV)) for r in res.subgroups]},
                   **FQ)
     torch.cuda.synchronize()
     flips_inj = int((layer.int_weight.cpu() != res.W_int).sum())
+    rep_inj = flip_report(layer.int_weight, res.W_int, res.ratio)
 
     layer.weight.data.copy_(W)
     g2 = GPTQPlus(layer, saliency=s, gradient=grad, num_groups=G, alpha=0.0, reference_loss=0.0)
@@ -147,6 +148,7 @@ def test_rotated_layer_linear_parity(rotated_layer, name):
     torch.cuda.synchronize()
     hinv_err = max(rel_fro(g2.Hinv_all[k], r.Hinv) for k, r in enumerate(res.subgroups))
     flips_own = int((layer.int_weight.cpu() != res.W_int).sum())
+    rep_own = flip_report(layer.int_weight, res.W_int, res.ratio)
     n = res.W_int.numel()
     e_gpu = _recon(W, layer.weight.data, xs[key])
     e_ref = _recon(W, res.Q.to(DEV), xs[key])
@@ -167,7 +169,8 @@ def test_rotated_layer_linear_parity(rotated_layer, name):
     _log(dict(case=f"configs3_rotated_{name}", R=R, C=C, G=G, tokens=N * T, act_square_mismatch=act_bad,
               flips_with_oracle_hinv=flips_inj, flips_own_chain=flips_own, codes=n, hinv_rel_fro=hinv_err,
               hinv_vs_fp64_host=gpu_vs_64, oracle_hinv_vs_fp64_host=ref_vs_64,
-              recon_gpu=e_gpu, recon_oracle=e_ref, recon_rel_diff=abs(e_gpu - e_ref) / e_ref))
+              recon_gpu=e_gpu, recon_oracle=e_ref, recon_rel_diff=abs(e_gpu - e_ref) / e_ref,
+              oracle_hinv_flip_report=rep_inj, own_chain_flip_report=rep_own))
     assert act_bad == 0
     assert flips_inj <= n // 10000
     assert hinv_err <= 1e-4
