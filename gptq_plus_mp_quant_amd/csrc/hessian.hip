@@ -72,31 +72,63 @@ __device__ __forceinline__ void load_side(const TX* __restrict__ X, int64_t ntok
   }
 }
 
-// Map a linear index to an upper-triangle tile (ti <= tj) in super-row order: rows are taken
-// HSR at a time and each super-row is walked column by column, so tiles that run at the same
-// time on one XCD share a few I strips and a few J strips of X (L2 reuse in both operands).
+// Super-row order of the off-diagonal upper-triangle tiles: tile rows are taken HSR at a time
+// and each super-row is walked column by column, so tiles that run at the same time on one XCD
+// share a few I strips and a few J strips of X (L2 reuse in both operands).
 constexpr int HSR = 4;
-__device__ __forceinline__ void upper_tile_blocked(int t, int nt, int& ti, int& tj) {
+// The t-th off-diagonal tile (ti < tj) in super-row order.
+__device__ __forceinline__ void offdiag_tile(int t, int nt, int& ti, int& tj) {
   int r0 = 0;
   int rem = t;
   for (;;) {
     const int h = min(HSR, nt - r0);
-    // tiles in this super-row: sum over tj >= r0 of min(h, tj - r0 + 1)
-    const int ncol = nt - r0;
-    const int cnt = (ncol >= h) ? (h * (h + 1) / 2 + (ncol - h) * h) : (ncol * (ncol + 1) / 2);
+    const int cnt = h * (h + 1) / 2 + (nt - r0 - h) * h - h;   // the super-row's tiles minus its h diagonal ones
     if (rem < cnt) break;
     rem -= cnt;
     r0 += h;
   }
   const int h = min(HSR, nt - r0);
   for (int c = r0;; ++c) {
-    const int k = min(h, c - r0 + 1);
+    const int k = min(h, c - r0 + 1) - (c < r0 + h ? 1 : 0);
     if (rem < k) {
       ti = r0 + rem;
       tj = c;
       return;
     }
     rem -= k;
+  }
+}
+
+// Item order of the Hessian kernels.  The item list holds every off-diagonal tile (in
+// super-row order) before every diagonal tile, the
+// targets of a tile consecutive.  The whole items (blocks b < full; block b runs on XCD b % 8)
+// are dealt to the 8 XCDs as contiguous runs of that list, each XCD taking its proportional share
+// of the off-diagonal items first and of the diagonal ones after.  The items that run side by side
+// on an XCD then do equal work per step (a diagonal tile computes only its upper half), so the
+// targets of a tile, which read the same X strips, start together and stay in step, and share
+// those strips through the XCD's L2.  The tail's token-slice items are the list's last items
+// (position = logical index).  Returns the list position of whole-item block b.
+__device__ __forceinline__ int item_position(int b, int full, int od_items) {
+  const int per = full / 8, rem8 = full % 8;
+  const int x = b % 8, idx = b / 8;
+  const int64_t len0 = (int64_t)x * per + min(x, rem8);        // whole items of the XCDs before x
+  const int64_t len1 = len0 + per + (x < rem8 ? 1 : 0);
+  const int64_t od_full = min((int64_t)od_items, (int64_t)full);
+  const int64_t od0 = od_full * len0 / full, od1 = od_full * len1 / full;
+  if (idx < od1 - od0) return (int)(od0 + idx);
+  return (int)(od_full + (len0 - od0) + (idx - (od1 - od0)));
+}
+
+// Target and tile of list position pos.
+__device__ __forceinline__ void item_tile(int pos, int ntarg, int nt, int& g, int& ti, int& tj) {
+  const int od_items = nt * (nt - 1) / 2 * ntarg;
+  if (pos < od_items) {
+    g = pos % ntarg;
+    offdiag_tile(pos / ntarg, nt, ti, tj);
+  } else {
+    const int p2 = pos - od_items;
+    g = p2 % ntarg;
+    ti = tj = p2 / ntarg;
   }
 }
 
@@ -266,9 +298,7 @@ __global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
   int logical, slice = -1;
   int64_t sbeg = 0, send = nslab;
   if (b < full) {
-    const int per = full / 8, rem8 = full % 8;
-    const int xcd = b % 8, idx = b / 8;
-    logical = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
+    logical = item_position(b, full, nt * (nt - 1) / 2 * ntarg);
   } else {
     const int tb = b - full;
     logical = full + tb / S;
@@ -277,9 +307,8 @@ __global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
     send = nslab * (slice + 1) / S;
   }
   if (logical >= total) return;
-  const int g = logical % ntarg;
-  int ti, tj;
-  upper_tile_blocked(logical / ntarg, nt, ti, tj);
+  int g, ti, tj;
+  item_tile(logical, ntarg, nt, g, ti, tj);
   const int I0 = ti * HT, J0 = tj * HT;
   const bool diag = (ti == tj);
   float* Hg = tg.H[g];
@@ -734,9 +763,7 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
   int logical, slice = -1;
   int64_t kbeg = 0, kend = nks;
   if (b < full) {
-    const int per = full / 8, rem8 = full % 8;
-    const int xcd = b % 8, idx = b / 8;
-    logical = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
+    logical = item_position(b, full, nt * (nt - 1) / 2 * ntarg);
   } else {
     const int tb = b - full;
     logical = full + tb / S;
@@ -745,9 +772,8 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
     kend = nks * (slice + 1) / S;
   }
   if (logical >= total) return;
-  const int g = logical % ntarg;
-  int ti, tj;
-  upper_tile_blocked(logical / ntarg, nt, ti, tj);
+  int g, ti, tj;
+  item_tile(logical, ntarg, nt, g, ti, tj);
   const int R0 = ti * XT, C0 = tj * XT;
   float* Hg = tg.H[g];
   const float* scl = scale + (int64_t)g * C;
@@ -983,9 +1009,7 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split32(
   int logical, slice = -1;
   int64_t kbeg = 0, kend = nks;
   if (b < full) {
-    const int per = full / 8, rem8 = full % 8;
-    const int xcd = b % 8, idx = b / 8;
-    logical = (xcd < rem8) ? xcd * (per + 1) + idx : rem8 * (per + 1) + (xcd - rem8) * per + idx;
+    logical = item_position(b, full, nt * (nt - 1) / 2 * ntarg);
   } else {
     const int tb = b - full;
     logical = full + tb / S;
@@ -994,9 +1018,8 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split32(
     kend = nks * (slice + 1) / S;
   }
   if (logical >= total) return;
-  const int g = logical % ntarg;
-  int ti, tj;
-  upper_tile_blocked(logical / ntarg, nt, ti, tj);
+  int g, ti, tj;
+  item_tile(logical, ntarg, nt, g, ti, tj);
   const int R0 = ti * XT, C0 = tj * XT;
   float* Hg = tg.H[g];
   const float* scl = scale + (int64_t)g * C;
