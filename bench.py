@@ -265,7 +265,7 @@ def one_linear(X, W, s, grad, cfg, layer, timer=None, keep=False, marks=None):
 
 
 def one_layer(xs, mods, cfg, layers, timer=None, keep=False, marks=None):
-    from gptq_plus_mp_quant_amd import add_batch_shared
+    from gptq_plus_mp_quant_amd import add_batch_shared, fasterquant_shared
     if marks is not None:
         marks.begin()
     objs = {name: new_gptq(layers[name], W, s, grad, cfg) for name, (W, s, grad, _) in mods.items()}
@@ -282,15 +282,25 @@ def one_layer(xs, mods, cfg, layers, timer=None, keep=False, marks=None):
     if marks is not None:
         marks.mark("finalize")
     kept = {}
-    for name, g in objs.items():
-        if keep:
-            kept[name] = (g.H.clone(), g.act_square.clone())
-        g.fasterquant(**fq_kwargs(cfg))
+    if keep:
+        kept = {name: (g.H.clone(), g.act_square.clone()) for name, g in objs.items()}
+    # one fasterquant per linear, free() after each group (the reference's loop, free() emptying
+    # the allocator cache like gptq_plus_utils.py:2357-2361); --shared-fasterquant runs the chains
+    # of the linears that share an input as one batch (fasterquant_shared, bit-identical results)
+    for key in INPUT_WIDTH:
+        names = [n for n, _, _, k in LAYER8B if k == key]
+        group = [objs[n] for n in names]
+        if len(group) > 1 and cfg.get("shared_fq"):
+            fasterquant_shared(group, **fq_kwargs(cfg))
+        else:
+            for g in group:
+                g.fasterquant(**fq_kwargs(cfg))
         if marks is not None:
-            marks.mark(f"fasterquant {name}")
-        g.free()
+            marks.mark(f"fasterquant {'/'.join(names)}")
+        for g in group:
+            g.free()
         if marks is not None:
-            marks.mark(f"free {name}")
+            marks.mark(f"free {'/'.join(names)}")
     return kept
 
 
@@ -703,7 +713,7 @@ def run(args):
     if args.gemm_calibration:
         gemm_calibration(dev)
         return
-    cfg = dict(CONFIGS[args.config], alpha=args.alpha, ref_loss=args.ref_loss)
+    cfg = dict(CONFIGS[args.config], alpha=args.alpha, ref_loss=args.ref_loss, shared_fq=args.shared_fasterquant)
     layer_mode = cfg["kind"] == "layer"
     if layer_mode:
         xs, mods = make_layer_inputs(dev, cfg)
@@ -777,6 +787,9 @@ def main():
     ap.add_argument("--hessian-math", choices=sorted(PIECES), default="split16x3",
                     help="Hessian kernel for fp16 inputs: split16x3 (default: three fp16 MFMA products per fp32 "
                          "product, exact), split16 (two: within 2^-23 relative), fp32 (fp32 MFMA)")
+    ap.add_argument("--shared-fasterquant", action="store_true",
+                    help="layer configs: fasterquant_shared for the linears that share an input (their Cholesky "
+                         "chains as one batch) instead of one fasterquant call per linear")
     ap.add_argument("--x-fp32", action="store_true",
                     help="fp32 activations (the reference's add_batch takes any float dtype): the same inputs "
                          "converted to fp32")

@@ -5,9 +5,10 @@ same names; all arithmetic runs in the HIP library built by ``gptq_plus_mp_quant
 """
 from .export import dequantize_packed, export_packed, load_packed, save_packed
 from .gptq import GPTQ
-from .gptq_plus import GPTQPlus, add_batch_shared
+from .gptq_plus import GPTQPlus, add_batch_shared, fasterquant_shared
 from .quant_utils import WeightQuantizer, get_minq_maxq
 
-__all__ = ["GPTQPlus", "GPTQ", "WeightQuantizer", "add_batch_shared", "get_minq_maxq", "export_packed",
+__all__ = ["GPTQPlus", "GPTQ", "WeightQuantizer", "add_batch_shared", "fasterquant_shared", "get_minq_maxq",
+           "export_packed",
            "dequantize_packed", "save_packed", "load_packed"]
 __version__ = "0.1.0"

@@ -21,6 +21,7 @@ dumps raise ``NotImplementedError`` rather than silently differing.
 from __future__ import annotations
 
 import contextlib
+import inspect
 import logging
 from typing import Optional
 
@@ -219,12 +220,6 @@ class GPTQPlus:
                             n_bad, self.layer.__class__.__name__)
         self._finalized = True
 
-    # gptq_plus_utils.py:494-561, for a batch of subgroups (each with its own schedule)
-    def _hessian_inverse(self, H_work, Hinv_out, Hinv_init_out, workspace, percdamp,
-                         damp_auto_increment=0.0015, log_context="", Hinv_diag_out=None):
-        return hessian_inverse_chain(self.dev, H_work, Hinv_out, Hinv_init_out, workspace, percdamp,
-                                     damp_auto_increment, log_context, Hinv_diag_out=Hinv_diag_out)
-
     # gptq_plus_utils.py:910-1896 (frozen mode)
     @torch.no_grad()
     def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
@@ -246,6 +241,26 @@ class GPTQPlus:
                        _compute_gradient_terms returns them), so the block loop can be compared
                        against another implementation on identical inputs.
         """
+        kw = {k: v for k, v in locals().items() if k != "self"}
+        steps = self._fasterquant_steps(**kw)
+        req = next(steps)
+        if req is not None:
+            req.run([req])
+        for _ in steps:
+            pass
+
+    def _fasterquant_steps(self, blocksize, percdamp, groupsize, actorder, static_groups,
+                           enable_gradient_update, g_update_mode, export_to_et, profile_recorder,
+                           gradient_refresh_fn, grad_lr, grad_optimizer, curvature_damping,
+                           grad_reg_strategy, grad_reg_lambda, grad_gate_floor, grad_gate_sharpness,
+                           grad_gate_sine_amp, second_order_scale, block_atomic_quant, block_observer,
+                           grad_clip, diagnostic_recorder, slide_refresh_start, slide_refresh_block_total,
+                           refresh_full_metrics, keep_hinv, inject, alloc=None):
+        """fasterquant as a generator that pauses once, at the damped Cholesky chain: it yields a
+        ChainRequest (or None when inject supplies H^-1), whose chain the caller runs -- alone
+        (fasterquant) or batched with other linears' (fasterquant_shared) -- and is then driven to
+        the end.  ``alloc`` supplies this linear's H_work / Hinv_all / Hinv_init_all / diag(H^-1)
+        as views into the caller's batched buffers."""
         rec = profile_recorder or self.profile_recorder
         inject = inject or {}
         inject_hinv = inject.get("hinv")
@@ -324,16 +339,19 @@ class GPTQPlus:
             Z = torch.empty((R, C), **f32)
             GH = torch.empty((R, C), **f32)
             Gs = torch.empty((R, C), **f32)
-            Hinv_all = torch.empty((G, C, C), **f32)
             beta_mode = 1 if (enable_gradient_update and self.alpha > 0) else 0
+            alloc = alloc or {}
+            Hinv_all = alloc["Hinv_all"] if "Hinv_all" in alloc else torch.empty((G, C, C), **f32)
             # H^-1 itself only for keep_hinv; the GPTQ+ step size needs just its diagonal
-            Hinit_all = torch.empty((G, C, C), **f32) if keep_hinv else None
-            hdiag_all = torch.empty((G, C), **f32) if beta_mode == 1 else None
+            Hinit_all = (alloc["Hinv_init_all"] if "Hinv_init_all" in alloc else torch.empty((G, C, C), **f32)) \
+                if keep_hinv else None
+            hdiag_all = (alloc["Hinv_diag"] if "Hinv_diag" in alloc else torch.empty((G, C), **f32)) \
+                if beta_mode == 1 else None
             grads = self.gradients.to(**f32)
             if grads.stride(1) != 1:
                 grads = grads.contiguous()
             # slice, dead-column fix and act_order gathers of every subgroup
-            H_work = torch.empty((G, C, C), **f32)
+            H_work = alloc["H_work"] if "H_work" in alloc else torch.empty((G, C, C), **f32)
             with _section(rec, "fasterquant.subgroup.slice_inputs"):
                 for sub in range(G):
                     r0 = sub * R_s
@@ -361,20 +379,15 @@ class GPTQPlus:
                     gate_q = nat.RQ_QMODE_CHANNEL
                     gate_s = q.scale.reshape(-1).to(**f32).contiguous()
                     gate_z = q.zero.reshape(-1).to(**f32).contiguous()
-            # damped Cholesky chain, subgroups batched through every launch
+            # damped Cholesky chain, subgroups batched through every launch (the caller runs it:
+            # this linear's alone, or batched with other linears')
             with _section(rec, "fasterquant.subgroup.compute_hinv"):
                 if inject_hinv is None:
-                    nb = self._chol_batch(C, G, dev)
-                    workspace = K.chol_workspace(C, dev, nb)
-                    chain = []
-                    for b0 in range(0, G, nb):
-                        b1 = min(G, b0 + nb)
-                        chain += self._hessian_inverse(
-                            H_work[b0:b1], Hinv_all[b0:b1],
-                            None if Hinit_all is None else Hinit_all[b0:b1], workspace, percdamp,
-                            Hinv_diag_out=None if hdiag_all is None else hdiag_all[b0:b1])
-                    del workspace
+                    req = ChainRequest(dev, H_work, Hinv_all, Hinit_all, hdiag_all, percdamp)
+                    yield req
+                    chain = req.chain
                 else:   # test hook: use given (Hinv_init, Hinv) pairs
+                    yield None
                     chain = []
                     for sub in range(G):
                         Hinv_all[sub].copy_(inject_hinv[sub][1])
@@ -580,12 +593,7 @@ class GPTQPlus:
 
     @staticmethod
     def _chol_batch(C, G, dev):
-        """How many subgroups to factorise per launch: all of them (at most
-        RQ_CHOL_MAXBATCH, the library's limit) when their fp64 workspaces fit in 40 % of the
-        free device memory, fewer otherwise."""
-        per = int(nat.load().rq_chol_workspace_bytes(C))
-        free, _ = torch.cuda.mem_get_info(dev)
-        return max(1, min(G, nat.RQ_CHOL_MAXBATCH, int(0.4 * free) // per))
+        return _chol_batch(C, G, dev)
 
     @property
     def codes(self):
@@ -649,6 +657,123 @@ class GPTQPlus:
         self.Hinv_all = None
         K.release_hessian_workspace(self.dev)
         torch.cuda.empty_cache()
+
+
+def _chol_batch(C, G, dev):
+    """How many subgroup matrices to factorise per launch sequence: all of them (at most
+    RQ_CHOL_MAXBATCH, the library's limit) when their fp64 workspaces fit in 40 % of the device
+    memory not yet held by PyTorch's caching allocator, fewer otherwise.  Memory the allocator
+    caches but does not use counts as free (mem_get_info alone would count it as used)."""
+    per = int(nat.load().rq_chol_workspace_bytes(C))
+    free, _ = torch.cuda.mem_get_info(dev)
+    free += torch.cuda.memory_reserved(dev) - torch.cuda.memory_allocated(dev)
+    return max(1, min(G, nat.RQ_CHOL_MAXBATCH, int(0.4 * free) // per))
+
+
+class ChainRequest:
+    """One linear's damped Cholesky chain, as fasterquant pauses for it: H_work [G, C, C] (damped
+    in place), Hinv_all [G, C, C] (the upper factors), optional Hinv_init_all and diag(H^-1)
+    outputs.  ``run`` factorises a list of requests with the same C as one batch of launch
+    sequences (gptq_plus_utils.py:494-561 per subgroup: each keeps its own damping schedule) and
+    leaves each request's [(damp, identity_fallback, attempts)] in ``chain``."""
+
+    def __init__(self, dev, H_work, Hinv_all, Hinv_init_all, Hinv_diag, percdamp):
+        self.dev, self.H_work, self.Hinv_all = dev, H_work, Hinv_all
+        self.Hinv_init_all, self.Hinv_diag, self.percdamp = Hinv_init_all, Hinv_diag, percdamp
+        self.chain = None
+
+    @staticmethod
+    def run(reqs):
+        reqs = [r for r in reqs if r is not None]
+        if not reqs:
+            return
+        dev, C = reqs[0].dev, reqs[0].H_work.shape[-1]
+        # one batch when the requests' buffers are consecutive views of one allocation
+        # (fasterquant_shared), else one batch per request
+        groups, cur = [], [reqs[0]]
+        for r in reqs[1:]:
+            prev = cur[-1]
+            same = all((getattr(r, a) is None) == (getattr(prev, a) is None)
+                       for a in ("Hinv_init_all", "Hinv_diag")) and r.percdamp == prev.percdamp
+            contiguous = same and all(
+                getattr(r, a) is None or
+                getattr(r, a).data_ptr() == getattr(prev, a).data_ptr() + getattr(prev, a).numel() * 4
+                for a in ("H_work", "Hinv_all", "Hinv_init_all", "Hinv_diag"))
+            if contiguous:
+                cur.append(r)
+            else:
+                groups.append(cur)
+                cur = [r]
+        groups.append(cur)
+        for grp in groups:
+            G = sum(r.H_work.shape[0] for r in grp)
+            view = lambda a: None if getattr(grp[0], a) is None else \
+                getattr(grp[0], a).as_strided((G,) + tuple(getattr(grp[0], a).shape[1:]),
+                                              getattr(grp[0], a).stride())
+            H_work, Hinv_all, Hinit, hdiag = (view(a) for a in ("H_work", "Hinv_all", "Hinv_init_all",
+                                                                 "Hinv_diag"))
+            nb = _chol_batch(C, G, dev)
+            workspace = K.chol_workspace(C, dev, nb)
+            chain = []
+            for b0 in range(0, G, nb):
+                b1 = min(G, b0 + nb)
+                chain += hessian_inverse_chain(dev, H_work[b0:b1], Hinv_all[b0:b1],
+                                               None if Hinit is None else Hinit[b0:b1], workspace,
+                                               grp[0].percdamp,
+                                               Hinv_diag_out=None if hdiag is None else hdiag[b0:b1])
+            del workspace
+            o = 0
+            for r in grp:
+                g = r.H_work.shape[0]
+                r.chain = chain[o:o + g]
+                o += g
+
+
+@torch.no_grad()
+def fasterquant_shared(gptqs, **kwargs):
+    """``fasterquant(**kwargs)`` for several GPTQPlus objects of the same in_features (q/k/v, or
+    gate/up), their damped Cholesky chains run as one batch: each linear's work up to the chain
+    (find_params, act_order, the subgroup gathers) runs first, then the chains of all their
+    subgroups go through the same launch sequences (each subgroup keeps its own damping schedule,
+    gptq_plus_utils.py:494-561), then each linear's block loop and write-back.  The results are
+    those of calling fasterquant on each object in turn, bit for bit."""
+    gptqs = list(gptqs)
+    if not gptqs:
+        return
+    C, dev = gptqs[0].columns, gptqs[0].dev
+    if any(g.columns != C or g.dev != dev for g in gptqs):
+        raise ValueError("fasterquant_shared: all modules must share in_features and device")
+    inject = kwargs.get("inject") or {}
+    if inject.get("hinv") is not None:
+        for g in gptqs:
+            g.fasterquant(**kwargs)
+        return
+    keep = bool(kwargs.get("keep_hinv", False))
+    Gt = sum(g.num_groups for g in gptqs)
+    f32 = dict(device=dev, dtype=torch.float32)
+    H_work = torch.empty((Gt, C, C), **f32)
+    Hinv_all = torch.empty((Gt, C, C), **f32)
+    Hinit = torch.empty((Gt, C, C), **f32) if keep else None
+    hdiag = torch.empty((Gt, C), **f32)
+    sig = inspect.signature(GPTQPlus.fasterquant)
+    sig.bind(None, **kwargs)                     # unknown arguments fail here, as in fasterquant
+    full = {k: p.default for k, p in sig.parameters.items() if k != "self"}
+    full.update(kwargs)
+    steps, reqs, o = [], [], 0
+    for g in gptqs:
+        G = g.num_groups
+        alloc = dict(H_work=H_work[o:o + G], Hinv_all=Hinv_all[o:o + G], Hinv_diag=hdiag[o:o + G])
+        if Hinit is not None:
+            alloc["Hinv_init_all"] = Hinit[o:o + G]
+        o += G
+        st = g._fasterquant_steps(alloc=alloc, **full)
+        steps.append(st)
+        reqs.append(next(st))
+    ChainRequest.run(reqs)
+    del H_work
+    for st in steps:
+        for _ in st:
+            pass
 
 
 @torch.no_grad()

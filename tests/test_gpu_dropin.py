@@ -390,6 +390,45 @@ def test_add_batch_shared_equals_separate(groups):
         assert torch.equal(a.H, b.H)
 
 
+@pytest.mark.parametrize("alpha,ref_loss,keep", [(0.0, 0.0, False), (0.05, 3e4, True)])
+def test_fasterquant_shared_equals_separate(alpha, ref_loss, keep):
+    """q/k/v-style modules quantized with their Cholesky chains in one batch (fasterquant_shared)
+    give bitwise the codes, weights, damping records and (keep_hinv) factors of separate
+    fasterquant calls, with the GPTQ+ term off and on (diag(H^-1) from the batched chain)."""
+    from gptq_plus_mp_quant_amd import add_batch_shared, fasterquant_shared
+    C, N, T = 384, 4, 64
+    X, _, _, _ = synth(61, 8, C, 1, N, T)
+    fq = dict(blocksize=128, percdamp=0.01, groupsize=-1, actorder=True, static_groups=True, keep_hinv=keep)
+    runs = []
+    for fused in (False, True):
+        objs = []
+        for m, (R, G) in enumerate(((128, 4), (64, 4), (96, 2))):
+            _, W, s, grad = synth(70 + m, R, C, G, N, T, gscale=1e-1)
+            objs.append(_gpu_obj(W, s, grad, G, alpha, ref_loss, 4, False))
+        gs = [o[0] for o in objs]
+        for j in range(0, N, 2):
+            add_batch_shared(gs, X[j:j + 2].to(DEV))
+        for g in gs:
+            g.finalize_hessian()
+        if fused:
+            fasterquant_shared(gs, **fq)
+        else:
+            for g in gs:
+                g.fasterquant(**fq)
+        torch.cuda.synchronize()
+        runs.append(objs)
+    for (ga, la), (gb, lb) in zip(*runs):
+        assert torch.equal(ga.codes, gb.codes) and torch.equal(la.weight.data, lb.weight.data)
+        for ia, ib in zip(ga.subgroup_info, gb.subgroup_info):
+            assert (ia["damp_percent"], ia["attempts"], ia["identity_fallback"]) == \
+                (ib["damp_percent"], ib["attempts"], ib["identity_fallback"])
+            assert torch.equal(ia["beta"], ib["beta"])
+        if keep:
+            assert torch.equal(ga.Hinv_all, gb.Hinv_all) and torch.equal(ga.Hinv_init_all, gb.Hinv_init_all)
+    with pytest.raises(ValueError):
+        fasterquant_shared([runs[0][0][0], _gpu_obj(*synth(1, 16, 256, 1, 1, 8)[1:], 1, 0.0, 0.0, 4, True)[0]])
+
+
 def test_dropin_errors_and_side_effects():
     X, W, s, grad = synth(1, 64, 128, 2, 2, 64)
     g, layer = _gpu_obj(W, s, grad, 2, 0.0, 0.0, 4, True)
