@@ -482,7 +482,7 @@ __device__ __forceinline__ void split8(uint4 x, float4 s0, float4 s1, float sc, 
 // every stage index is a compile-time constant: the LDS reads are ordinary loads (the compiler
 // places their lgkmcnt waits), and alias analysis can tell the staging writes in flight to
 // other stages from the stage being read.
-constexpr int XDEPTH = 4;   // 8 stages measured no faster, also with one barrier per two steps
+constexpr int XDEPTH = 8;   // 8 stages (133 KB of LDS, one workgroup per CU): 2 % faster than 4 at cfg3
 constexpr int XA_BYTES = 8 * 1024;                  // row fragments of a stage
 constexpr int XB_OFF = XA_BYTES;                    // column fragment of wave w at XB_OFF + 1024 w
 constexpr int XS_OFF = XB_OFF + XWAVES * 1024;      // the step's 16 saliencies (64 B)
@@ -753,9 +753,13 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
   __shared__ __attribute__((aligned(16))) uint8_t lds1[XSTAGE];
   __shared__ __attribute__((aligned(16))) uint8_t lds2[XSTAGE];
   __shared__ __attribute__((aligned(16))) uint8_t lds3[XSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds4[XSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds5[XSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds6[XSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds7[XSTAGE];
   __shared__ int last_slice;
-  static_assert(XDEPTH == 4, "stage arrays");
-  const XStages L{{lds0, lds1, lds2, lds3}};
+  static_assert(XDEPTH == 8, "stage arrays");
+  const XStages L{{lds0, lds1, lds2, lds3, lds4, lds5, lds6, lds7}};
   // Same schedule as k_hessian_accum: XCD-aware order for whole items, then the token
   // slices of the tail items.
   const int total = ntiles * ntarg;
@@ -812,6 +816,7 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
 // fp32 column fragment of wave w at 16 KB + 2 KB w (two 1 KB halves), the 16 saliencies.  A step
 // runs in two phases: (A) hi x (w1, w0) while the lo rows of this step are read and the next
 // step's column fragment is split; (B) lo x w0 while the next step's hi rows are read.
+constexpr int X32DEPTH = 4;   // stages of 32.25 KB: 4 fit the LDS
 constexpr int X3_HI = 0;
 constexpr int X3_LO = 8 * 1024;
 constexpr int X3_COL = 16 * 1024;
@@ -860,18 +865,18 @@ __device__ __forceinline__ void read_col32(const uint8_t* st, int wave, int lane
   sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w; sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
 }
 
-// One 16-token step k (stages CUR = k, NXT = k+1, FILL = k+XDEPTH-1).  Waits as split_step:
+// One 16-token step k (stages CUR = k, NXT = k+1, FILL = k+X32DEPTH-1).  Waits as split_step:
 // this step's and the next step's staging must be complete (phase A reads the lo rows of k and
-// the column fragment of k+1, phase B the hi rows of k+1), so vmcnt(4 * (XDEPTH - 3)).
+// the column fragment of k+1, phase B the hi rows of k+1), so vmcnt(4 * (X32DEPTH - 3)).
 template <bool DIAG, int CUR, int NXT, int FILL>
 __device__ __forceinline__ void split_step32(uint4 (&p)[2], uint4 (&ah)[8], uint4 (&al)[8], floatx16 (&acc)[8],
                                              const XStages& L, const uint16_t* ph, const uint16_t* pl,
                                              const float* pc, const float* sg, float sc, int wave, int lane,
                                              int64_t k, int64_t last, int lim) {
   typedef XType<__half>::v8 v8;
-  XWAIT_VM(4 * (XDEPTH - 3));
+  XWAIT_VM(4 * (X32DEPTH - 3));
   RQ_STAGE_BARRIER();
-  stage_step32(L.s[FILL], ph, pl, pc, sg, wave, lane, min(k + XDEPTH - 1, last));
+  stage_step32(L.s[FILL], ph, pl, pc, sg, wave, lane, min(k + X32DEPTH - 1, last));
   // phase A: hi rows x (w1, w0); the lo rows of this step and the next column fragment are read
   const uint8_t* cur = static_cast<const uint8_t*>(__builtin_assume_aligned(L.s[CUR] + X3_LO + lane * 16, 16));
 #pragma unroll
@@ -908,7 +913,7 @@ __device__ __forceinline__ void split_round32(uint4 (&p)[2], uint4 (&ah)[8], uin
                                               const float* pc, const float* sg, float sc, int wave, int lane,
                                               int64_t k, int64_t last, int lim, int nsteps,
                                               std::integer_sequence<int, J...>) {
-  ((J < nsteps ? split_step32<DIAG, J, (J + 1) % XDEPTH, (J + XDEPTH - 1) % XDEPTH>(
+  ((J < nsteps ? split_step32<DIAG, J, (J + 1) % X32DEPTH, (J + X32DEPTH - 1) % X32DEPTH>(
                      p, ah, al, acc, L, ph, pl, pc, sg, sc, wave, lane, k + J, last, lim)
                : void()),
    ...);
@@ -944,9 +949,9 @@ __device__ __forceinline__ void split_tile32(const uint16_t* __restrict__ XH, co
 
   const int64_t last = kend - 1;
 #pragma unroll
-  for (int h = 0; h < XDEPTH - 1; ++h) stage_step32(L.s[h], ph, pl, pc, sg, wave, lane, min(kbeg + h, last));
+  for (int h = 0; h < X32DEPTH - 1; ++h) stage_step32(L.s[h], ph, pl, pc, sg, wave, lane, min(kbeg + h, last));
   uint4 p[2], ah[8], al[8];
-  XWAIT_VM(4 * (XDEPTH - 2));         // this wave's staging of step kbeg
+  XWAIT_VM(4 * (X32DEPTH - 2));         // this wave's staging of step kbeg
   RQ_STAGE_BARRIER();       // and the other waves'
   {
     float x[8], sv[8];
@@ -959,10 +964,10 @@ __device__ __forceinline__ void split_tile32(const uint16_t* __restrict__ XH, co
   }
   const int64_t n = kend - kbeg;
   int64_t k = kbeg;
-  constexpr auto round = std::make_integer_sequence<int, XDEPTH>();
-  for (; k + XDEPTH <= kend; k += XDEPTH)
-    split_round32<DIAG>(p, ah, al, acc, L, ph, pl, pc, sg, sc, wave, lane, k, last, lim, XDEPTH, round);
-  split_round32<DIAG>(p, ah, al, acc, L, ph, pl, pc, sg, sc, wave, lane, k, last, lim, (int)(n % XDEPTH), round);
+  constexpr auto round = std::make_integer_sequence<int, X32DEPTH>();
+  for (; k + X32DEPTH <= kend; k += X32DEPTH)
+    split_round32<DIAG>(p, ah, al, acc, L, ph, pl, pc, sg, sc, wave, lane, k, last, lim, X32DEPTH, round);
+  split_round32<DIAG>(p, ah, al, acc, L, ph, pl, pc, sg, sc, wave, lane, k, last, lim, (int)(n % X32DEPTH), round);
   XWAIT_VM(0);
 
   if (part) {
@@ -1002,7 +1007,7 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split32(
   __shared__ __attribute__((aligned(16))) uint8_t lds2[X3_STAGE];
   __shared__ __attribute__((aligned(16))) uint8_t lds3[X3_STAGE];
   __shared__ int last_slice;
-  static_assert(XDEPTH == 4, "stage arrays");
+  static_assert(X32DEPTH == 4, "stage arrays");
   const XStages L{{lds0, lds1, lds2, lds3}};
   const int total = ntiles * ntarg;
   const int b = blockIdx.x;

@@ -378,15 +378,13 @@ def test_cholesky_batch_independent_entries(C):
 def test_cholesky_retry_schedule(neg):
     """Indefinite diagonal H: the damping retries (cumulative on the same working copy)
     must stop at the same attempt as the reference's loop, or fall back to identity."""
-    from gptq_plus_mp_quant_amd import GPTQPlus
+    from gptq_plus_mp_quant_amd.gptq_plus import hessian_inverse_chain
     d = torch.tensor([-neg, 1.0, 1.0, 1.0, 2.0] * 16)
     H = torch.diag(d)
     _, _, p_o, fb_o, att_o = hessian_inverse_with_fallback(H, 0.01)
-    layer = torch.nn.Linear(80, 8, bias=False).to(DEV)
-    g = GPTQPlus(layer, torch.ones(1, 1, 1), torch.zeros(8, 80), 1, 0.0, 0.0)
     Hw = H.to(DEV).clone()
     Hinv = torch.empty(80, 80, device=DEV)
-    (p, fb, att), = g._hessian_inverse(Hw, Hinv, None, K.chol_workspace(80, DEV), 0.01)
+    (p, fb, att), = hessian_inverse_chain(DEV, Hw, Hinv, None, K.chol_workspace(80, DEV), 0.01)
     assert (att, fb) == (att_o, fb_o) and abs(p - p_o) < 1e-12
     if fb:
         assert torch.equal(Hinv.cpu(), torch.eye(80))
@@ -399,7 +397,7 @@ def test_cholesky_near_singular_dense():
     0.01 (the documented difference in the number of retries).  Pinned: the oracle's attempt
     count, this build's, the factor at 0.01 against fp64 truth on the same damped matrix, and
     the factor at the oracle's damping against the oracle's."""
-    from gptq_plus_mp_quant_amd import GPTQPlus
+    from gptq_plus_mp_quant_amd.gptq_plus import hessian_inverse_chain
     C = 64
     r = rng(0)
     Q, _ = np.linalg.qr(r.standard_normal((C, C)))
@@ -412,12 +410,10 @@ def test_cholesky_near_singular_dense():
     print(f"near-singular C={C}: fp32 reference chain attempts {att_o} (damp {p_o:.4f})", flush=True)
     assert not fb_o
 
-    layer = torch.nn.Linear(C, 8, bias=False).to(DEV)
-    g = GPTQPlus(layer, torch.ones(1, 1, 1), torch.zeros(8, C), 1, 0.0, 0.0)
     ws = K.chol_workspace(C, DEV)
     Hw = H.to(DEV).clone()
     Hinv = torch.empty(C, C, device=DEV)
-    (p, fb, att), = g._hessian_inverse(Hw, Hinv, None, ws, 0.01)
+    (p, fb, att), = hessian_inverse_chain(DEV, Hw, Hinv, None, ws, 0.01)
     assert (att, fb) == (1, False) and abs(p - 0.01) < 1e-12 and att_o >= att
     Hd = Hw.double().cpu()                            # the damped working copy the chain factored
     assert float(torch.linalg.eigvalsh(Hd)[0]) > 0.0
@@ -427,7 +423,7 @@ def test_cholesky_near_singular_dense():
     if att_o > 1:                                     # at the reference's final damping both agree
         Hw2 = H.to(DEV).clone()
         Hinv2 = torch.empty(C, C, device=DEV)
-        (p2, fb2, att2), = g._hessian_inverse(Hw2, Hinv2, None, ws, p_o)
+        (p2, fb2, att2), = hessian_inverse_chain(DEV, Hw2, Hinv2, None, ws, p_o)
         assert (att2, fb2) == (1, False)
         assert rel_fro(Hinv2, Hv_o) <= 1e-4
 

@@ -11,9 +11,11 @@ minutes.
   within 0.5 % of the oracle's.  At this width the reference's fp32 LAPACK chain is ~3e-6 from an
   fp64 factorisation of the same damped matrix (checked here with torch's fp64 factorisation on
   the GPU), the GPU's chain within fp32 rounding of it, so every code near a rounding boundary
-  follows the reference's chain error: 0.25 % of the codes flip (measured), while the two
+  follows the reference's chain error: 0.2-0.25 % of the codes flip (measured), while the two
   reconstruction errors agree within 4e-5 relative.  The GPU's factor must be the closer one;
-  the flips are reported and bounded at 0.5 %.
+  the first differing code of each row must be an exact tie or within 256 fp32 ulps of one (52
+  such rows measured, 3 exact ties, at most 88 ulps; the rest of a row follows its changed
+  error feedback), and the total is bounded at 0.5 %.
 The case's numbers are printed and appended to RQ_PARITY_LOG (JSON lines) when it is set.
 """
 import json
@@ -116,6 +118,9 @@ def test_70b_width_subgroup_parity():
     assert hinv_err <= 1e-4
     assert gpu_vs_64 <= 1e-6 and gpu_vs_64 < ref_vs_64
     assert abs(e_gpu - e_ref) <= 0.005 * e_ref
+    # every row's first differing code an exact tie or within 256 fp32 ulps of one (the rest of
+    # such a row follows its changed error feedback); totals bounded at 0.5 %
+    assert rep_own["primary"] <= n // 100000 and rep_own.get("primary_ulps_le_256", 0) == rep_own["primary"]
     assert flips_own <= n // 200
     g.free()
     g2.free()

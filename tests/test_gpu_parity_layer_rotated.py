@@ -8,17 +8,19 @@ add_batch_shared, gptq_plus_utils.py:6990-7039).
 
 Per linear, against the CPU oracle given the GPU's finalized H:
 - act_square bit for bit;
-- with the oracle's fp32 H^-1 injected: code flips <= 0.01 %.  The atomic block solve
-  (Err1 Hinv1 = W1 - Q1, gptq_plus_utils.py:1283-1288) is the CPU's unblocked substitution op
-  for op, but MKL solves a 128-column block in sub-blocks of its own choosing, so its errors
-  differ from the GPU's in the last bits and a few codes near a rounding boundary follow;
+- with the oracle's fp32 H^-1 injected: the atomic block solve (Err1 Hinv1 = W1 - Q1,
+  gptq_plus_utils.py:1283-1288) is the CPU's unblocked substitution op for op, but MKL solves a
+  128-column block in sub-blocks of its own choosing, so its errors differ from the GPU's in the
+  last bits and a few codes at a rounding boundary follow.  Every row's first differing code
+  ("primary") must be an exact tie or within 256 fp32 ulps of one, and at most 0.001 % of the
+  codes; the later flips of such a row follow its changed error feedback (sanity bound 0.1 %);
 - with the GPU's fp64 chain: H^-1 within 1e-4, reconstruction error within 0.5 % of the
   oracle's.  The rotated Hessians are harder for the reference's fp32 LAPACK chain than the
   unrotated ones: its factor is ~4e-6 from an fp64 factorisation of the same damped matrix on
   the host (checked here on subgroup 0 of every linear), the GPU's within fp32 rounding of it,
   so the codes that sit near a rounding boundary follow the reference's chain error.  The GPU's
-  factor must be the closer one to fp64; code flips are bounded at 0.02 % (C = 4096) and 0.1 %
-  (C = 14336, 0.06 % measured) and reported.
+  factor must be the closer one to fp64; the flips are classified as above (primary flips exact
+  ties or within 256 ulps of one, at most 0.001 %; totals reported, sanity bound 0.1 %).
 Each case's numbers are printed and appended to RQ_PARITY_LOG (JSON lines) when it is set.
 """
 import json
@@ -172,10 +174,13 @@ def test_rotated_layer_linear_parity(rotated_layer, name):
               recon_gpu=e_gpu, recon_oracle=e_ref, recon_rel_diff=abs(e_gpu - e_ref) / e_ref,
               oracle_hinv_flip_report=rep_inj, own_chain_flip_report=rep_own))
     assert act_bad == 0
-    assert flips_inj <= n // 10000
     assert hinv_err <= 1e-4
     assert gpu_vs_64 <= 1e-6 and gpu_vs_64 < ref_vs_64
     assert abs(e_gpu - e_ref) <= 0.005 * e_ref
-    assert flips_own <= (n // 1000 if C == 14336 else n // 5000)
+    # every row's first differing code an exact tie or within 256 fp32 ulps of one; the rest of
+    # such a row follows its changed error feedback (totals: sanity bound 0.1 %)
+    for r in (rep_inj, rep_own):
+        assert r["primary"] <= n // 100000 and r.get("primary_ulps_le_256", 0) == r["primary"]
+        assert r["flips"] <= n // 1000
     g.free()
     g2.free()
