@@ -602,12 +602,13 @@ def algorithmic_work(cfg, lookahead=False):
     for C, n in inputs.items():
         add("k_xprep", n * 4.0 * ntok * C)                      # X read, the blocked copy written
     add("k_hessian_split", 0.0, float(hessian_flops(cfg)))
+    add("k_hessian_accum", 0.0, float(hessian_flops(cfg)))
     return w
 
 
 def stats_table(path, cfg, units, config):
-    """Markdown table of a rocprofv3 --stats kernel CSV, with achieved rates where the kernel's
-    algorithmic work per unit is known."""
+    """Markdown table of a rocprofv3 --stats kernel CSV (the 24 longest kernels and every kernel
+    whose algorithmic work per unit is known), with achieved rates where that work is known."""
     rows = []
     with open(path) as f:
         for r in csv.DictReader(f):
@@ -617,16 +618,21 @@ def stats_table(path, cfg, units, config):
     rows.sort(key=lambda x: -x[2])
     print(f"| kernel | calls | total (ms) | per unit (ms) | average (us) | % | algorithmic work per unit | achieved |")
     print("|---|---:|---:|---:|---:|---:|---|---|")
-    for name, calls, tot, avg, pct in rows[:24]:
+    for rank, (name, calls, tot, avg, pct) in enumerate(rows):
         per = tot / units
         bare = name[5:] if name.startswith("void ") else name
         key = bare if bare in work else next((k for k in work if bare.split("<")[0] == k), None)
+        if rank >= 24 and not key:     # the 24 longest kernels, then those with a known rate
+            continue
         wtxt = ach = ""
         if key:
             b, fl = work[key]
             if fl:
+                # the split Hessian kernels run on the fp16 pipe (algorithmic fp32 flops against
+                # its peak), the fp32 one on the fp32 pipe, the Cholesky update on the fp64 pipe
                 peak = FP64_MFMA_PEAK_TFLOPS if key == "k_panel_update" else (
-                    FP32_MFMA_PEAK_TFLOPS if key != "k_quant_block" else None)
+                    FP16_MFMA_PEAK_TFLOPS if key == "k_hessian_split" else (
+                        FP32_MFMA_PEAK_TFLOPS if key != "k_quant_block" else None))
                 tf = fl / (per * 1e-3) / 1e12
                 wtxt = f"{fl / 1e9:.1f} GFLOP" + (f", {b / 1e6:.0f} MB" if b else "")
                 ach = f"{tf:.1f} TF/s" + (f" ({100 * tf / peak:.1f} % of {peak})" if peak else "")
@@ -643,7 +649,9 @@ def counters_table(path, top=16):
     """Markdown table of a rocprofv3 --pmc CSV (one row per dispatch and counter), per kernel:
     MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * 128) (the SQ counter sums the
     1024 SIMDs, GRBM_GUI_ACTIVE the 8 XCDs' busy cycles: busy SIMD-cycles over SIMD-cycles),
-    VALU and LDS instructions per MFMA, LDS bank-conflict cycles per LDS instruction."""
+    VALU and LDS instructions per MFMA, LDS bank-conflict cycles per LDS instruction, and the
+    sustained clock: GRBM_GUI_ACTIVE / 8 XCDs over the dispatches' summed durations (for kernels
+    averaging 1 ms or more per dispatch)."""
     agg, disp, dur = {}, {}, {}
     with open(path) as f:
         for r in csv.DictReader(f):
@@ -654,8 +662,8 @@ def counters_table(path, top=16):
                 disp[(k, r["Dispatch_Id"])] = 1
                 dur[k] = dur.get(k, 0.0) + (float(r["End_Timestamp"]) - float(r["Start_Timestamp"])) / 1e3
     rows = sorted(agg.items(), key=lambda kv: -dur.get(kv[0], 0.0))
-    print("| kernel | dispatches | time (ms) | MFMA busy | VALU / MFMA | LDS / MFMA | LDS conflict cycles / LDS |")
-    print("|---|---:|---:|---:|---:|---:|---:|")
+    print("| kernel | dispatches | time (ms) | MFMA busy | clock (GHz) | VALU / MFMA | LDS / MFMA | LDS conflict cycles / LDS |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|")
     for k, c in rows[:top]:
         n = sum(1 for (kk, _d) in disp if kk == k)
         busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / max(c.get("GRBM_GUI_ACTIVE", 0.0) * 128, 1.0)
@@ -663,7 +671,10 @@ def counters_table(path, top=16):
         per_mfma = lambda key: f"{c.get(key, 0.0) / mf:.2f}" if mf else "-"
         lds = c.get("SQ_INSTS_LDS", 0.0)
         conf = f"{c.get('SQ_LDS_BANK_CONFLICT', 0.0) / lds:.2f}" if lds else "-"
-        print(f"| `{k}` | {n} | {dur.get(k, 0.0) / 1e3:.2f} | {100 * busy:.1f} % | {per_mfma('SQ_INSTS_VALU')} | "
+        # cycles per ns; the counter window exceeds a short dispatch, so only from 1 ms on average
+        clk = c.get("GRBM_GUI_ACTIVE", 0.0) / 8 / max(dur.get(k, 0.0) * 1e3, 1.0)
+        clk = f"{clk:.3f}" if dur.get(k, 0.0) >= 1e3 * n else "-"
+        print(f"| `{k}` | {n} | {dur.get(k, 0.0) / 1e3:.2f} | {100 * busy:.1f} % | {clk} | {per_mfma('SQ_INSTS_VALU')} | "
               f"{per_mfma('SQ_INSTS_LDS')} | {conf} |")
 
 

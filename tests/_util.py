@@ -1,6 +1,9 @@
 """Shared helpers for the parity tests (seeded synthetic inputs, error metrics)."""
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 import torch
 
@@ -78,3 +81,12 @@ def flip_report(codes_gpu, codes_ref, ratio, perm=None):
         all_ulps_median=float(np.median(u_all)), all_dist_max=float(d_all.max()),
         code_delta_max=int((a - b).abs().max()))
     return out
+
+
+def log_parity(rec):
+    """Print one case's numbers and, when RQ_PARITY_LOG names a file, append them to it as JSON."""
+    print(json.dumps(rec), flush=True)
+    path = os.environ.get("RQ_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(rec) + "\n")

@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
+from tests._util import log_parity
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -88,6 +89,7 @@ def test_configs4_full_shape_properties():
     got = torch.stack([(U * (H[g].double() @ V)).sum(0) for g in range(G)])
     perr = ((got - exp).abs() / mag).max().item()
     print(f"H probes: max |u'Hv - fp64| / sum|.| = {perr:.3g}", flush=True)
+    rec = dict(case="configs4_full_shape_properties", R=R, C=C, G=G, tokens=N * T, h_probe_max_rel=perr)
     assert perr <= 1e-5
 
     # the damped Cholesky chain of two subgroups against torch fp64 on the GPU
@@ -111,6 +113,7 @@ def test_configs4_full_shape_properties():
         resid = float(((Ud.T @ Ud) @ Hw - torch.eye(C, device=DEV, dtype=torch.float64)).norm()) / C ** 0.5
         print(f"subgroup {sub}: U vs fp64 {e_u:.3g}, H^-1 vs fp64 {e_i:.3g}, ||U'U H - I||_F/sqrt(C) {resid:.3g}",
               flush=True)
+        rec[f"subgroup{sub}"] = dict(u_vs_fp64=e_u, hinv_vs_fp64=e_i, resid=resid)
         assert e_u <= 1e-6 and e_i <= 1e-6
         assert resid <= 1e-2
         del Hw, Hinv64, U64, Ud
@@ -131,9 +134,13 @@ def test_configs4_full_shape_properties():
         return sum(float(((D[g] @ H[g].double()) * D[g]).sum()) for g in range(G))
     e_q, e_r = proxy(a["Q"]), proxy(rtn)
     print(f"proxy loss: GPTQ+ {e_q:.6g}  RTN {e_r:.6g}  ratio {e_q / e_r:.3f}", flush=True)
+    rec.update(proxy_gptqplus=e_q, proxy_rtn=e_r)
     assert e_q < e_r
 
     # determinism
     b = _run(X, W, s, grad, keep_hinv=False)
-    for k in ("H", "codes", "Q"):
-        assert torch.equal(a[k], b[k]), k
+    same = {k: bool(torch.equal(a[k], b[k])) for k in ("H", "codes", "Q")}
+    rec["second_run_identical"] = same
+    log_parity(rec)
+    for k, v in same.items():
+        assert v, k
