@@ -50,8 +50,7 @@ DTYPE_TEXT = {
     ("split16", False): "f32 (fp16 inputs; Hessian: fp32 products within 2^-23 relative, 2 fp16 MFMA products "
                         "each, fp32 sums)",
     ("fp32", False): "f32 (fp16 inputs; Hessian: fp32 MFMA)",
-    ("split16x3", True): "f32 (fp32 inputs; Hessian: fp32 products within 2^-20.5 relative, 3 fp16 MFMA "
-                         "products each, fp32 sums)",
+    ("split16x3", True): "f32 (fp32 inputs; Hessian: fp32 MFMA)",
     ("split16", True): "f32 (fp32 inputs; Hessian: fp32 products within 2^-20.5 relative, 3 fp16 MFMA "
                        "products each, fp32 sums)",
     ("fp32", True): "f32 (fp32 inputs; Hessian: fp32 MFMA)",
@@ -347,10 +346,10 @@ def roofline(cfg, args, kernel_ms, launches, steps):
     traffic, tsrc = load_traffic(args.hessian_math, args.config)
     pieces = PIECES[args.hessian_math]
     kernel = KERNEL[args.hessian_math]
-    if args.x_fp32:   # fp32 activations: hi w0 + hi w1 + lo w0 on the split path
+    if args.x_fp32:   # fp32 activations: exact on the fp32 kernel, or hi w0 + hi w1 + lo w0 (split16)
         traffic, tsrc = None, "fp32 activations: not measured"
-        pieces = 3 if args.hessian_math != "fp32" else 1
-        kernel = "k_hessian_split32" if args.hessian_math != "fp32" else "k_hessian_accum<float>"
+        pieces = 3 if args.hessian_math == "split16" else 1
+        kernel = "k_hessian_split32" if args.hessian_math == "split16" else "k_hessian_accum<float>"
     peak = FP16_MFMA_PEAK_TFLOPS if pieces > 1 else FP32_MFMA_PEAK_TFLOPS
     return {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
             "frac": round(ach / peak, 4), "traffic": traffic,

@@ -803,7 +803,8 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
 }
 
 // ---------------------------------------------------------------------------------------------
-// fp32 X (k_hessian_split32): the same 256 x 256 upper tiles, with x no longer exact in 16 bits.
+// fp32 X (k_hessian_split32, run in the opt-in RQ_HMATH_SPLIT16 mode; by default fp32 X runs on
+// the fp32 MFMA kernel): the same 256 x 256 upper tiles, with x no longer exact in 16 bits.
 // The row operand is x 2^ex_i written as two fp16 pieces hi + lo (22 of x's 24 bits; k_xrows32),
 // the column operand w = fl32(x * s) 2^e_j is split in the kernel from the exact fp32 x (fp32
 // column fragments, k_xprep32) into w0 + w1 (as the two-piece fp16 mode), and each 16-token
@@ -1949,7 +1950,9 @@ int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
   if (x_dtype != RQ_F32 && g_hmath.load() != RQ_HMATH_FP32 && aligned &&
       ws_bytes >= split_layout(ntok, C, ntarg, 0, 1).bytes)
     return launch_split(x, x_dtype, ntok, ldx, C, tg, ntarg, ws, ws_bytes, s);
-  if (x_dtype == RQ_F32 && g_hmath.load() != RQ_HMATH_FP32 && aligned &&
+  // fp32 X: the split kernel (products within ~2^-20.5) only in the opt-in two-piece mode; by
+  // default the fp32 MFMA kernel below forms the reference's products exactly
+  if (x_dtype == RQ_F32 && g_hmath.load() == RQ_HMATH_SPLIT16 && aligned &&
       ws_bytes >= split_layout32(ntok, C, ntarg, 0, 1).bytes)
     return launch_split32(static_cast<const float*>(x), ntok, ldx, C, tg, ntarg, ws, ws_bytes, s);
   const int nt = (C + HT - 1) / HT;

@@ -85,11 +85,12 @@ HESSIAN_MATH = {"split16": nat.RQ_HMATH_SPLIT16, "split16x3": nat.RQ_HMATH_SPLIT
 
 @contextlib.contextmanager
 def hessian_math(mode):
-    """Select the Hessian kernel inside the block: "split16x3" (default; fp16 / bf16 X: each
-    fp32 product exactly, from three 16-bit MFMA products), "split16" (fp16 X: from two, within
-    2^-23 relative; bf16 X as the default) or "fp32" (fp32 MFMA).  The choice is process-wide.
-    fp32 inputs take the fp32-X split kernel (three MFMAs per product, each within ~2^-20.5
-    relative) under both split modes, and the fp32 MFMA kernel under "fp32"."""
+    """Select the Hessian kernel inside the block: "split16x3" (default: each fp32 product
+    exactly; fp16 / bf16 X from three 16-bit MFMA products, fp32 X on the fp32 MFMA kernel),
+    "split16" (faster, narrower products: fp16 X from two 16-bit products, within 2^-23
+    relative; bf16 X as the default; fp32 X on the fp32-X split kernel, three MFMAs per product,
+    each within ~2^-20.5 relative) or "fp32" (fp32 MFMA for every input type).  The choice is
+    process-wide."""
     lib = nat.load()
     prev = int(lib.rq_hessian_math(HESSIAN_MATH[mode]))
     if prev < 0:

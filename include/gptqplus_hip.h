@@ -64,14 +64,16 @@ int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets, int x_dtyp
  * the 16-bit MFMA pipe from the weighted operand cut into 16-bit pieces (after an exact
  * power-of-two column scaling), and accumulate in fp32; they need the workspace (with less
  * than rq_hessian_workspace_bytes the fp32 kernel runs instead).
- * RQ_HMATH_SPLIT16X3 (default): fp16 and bf16 X with the weighted operand in three pieces
- *   (11 + 11 + 2 or 8 + 8 + 8 bits): the reference's fp32 products exactly (for fp16, every
- *   operand within 2^15 of its column's largest; below that within 2^-40 of the largest).
- * RQ_HMATH_SPLIT16 (opt-in, faster): fp16 X in two pieces (22 of the operand's 24 bits: each
- *   product within 2^-23 relative of the reference's, 2/3 of the MFMA work), bf16 X in three.
- * Both split modes take fp32 X with x itself in two fp16 pieces, three MFMAs per product
- * (hi w0, hi w1, lo w0: each product within ~2^-20.5 relative; k_hessian_split32).
- * RQ_HMATH_FP32: fp32 MFMA on converted operands (exact fp32 products, also for fp32 X).
+ * RQ_HMATH_SPLIT16X3 (default): the reference's fp32 products exactly.  fp16 and bf16 X with
+ *   the weighted operand in three pieces (11 + 11 + 2 or 8 + 8 + 8 bits; for fp16, every
+ *   operand within 2^15 of its column's largest, below that within 2^-40 of the largest);
+ *   fp32 X on the fp32 MFMA kernel.
+ * RQ_HMATH_SPLIT16 (opt-in, faster, narrower products): fp16 X in two pieces (22 of the
+ *   operand's 24 bits: each product within 2^-23 relative of the reference's, 2/3 of the MFMA
+ *   work), bf16 X in three; fp32 X with x itself in two fp16 pieces, three MFMAs per product
+ *   (hi w0, hi w1, lo w0: each product within ~2^-20.5 relative; k_hessian_split32, about 3x
+ *   the fp32 MFMA kernel's speed).
+ * RQ_HMATH_FP32: fp32 MFMA on converted operands for every input type (exact fp32 products).
  * mode < 0 queries.  Returns the previous mode, or RQ_EINVAL.  No counterpart in the
  * reference (its bmm runs in fp32, gptq_plus_utils.py:845-847). */
 #define RQ_HMATH_SPLIT16 0

@@ -1,4 +1,5 @@
-"""The split-operand Hessian kernels (the default for fp16, bf16 and fp32 X) against exact
+"""The split-operand Hessian kernels (the default for fp16 and bf16 X; for fp32 X the opt-in
+"split16" mode's kernel, the default there being the fp32-MFMA kernel) against exact
 arithmetic and the fp32-MFMA kernel.
 
 The reference forms H = X^T (s * X) in fp32 (gptq_plus_utils.py:842-847): each product is
@@ -159,11 +160,14 @@ def test_split_fp32_x_matches_exact_sum(n, C, G):
     ref, act_ref = _exact(x, sal)
     Hs, acts, iu = _run(x, sal, "split16")
     Hf, actf, _ = _run(x, sal, "fp32")
+    Hd, actd, _ = _run(x, sal, "split16x3")
     es = rel_fro(_upper(Hs, iu), _upper(ref, iu))
     ef = rel_fro(_upper(Hf, iu), _upper(ref, iu))
     print(f"fp32 X n={n} C={C} G={G}: rel err split {es:.3e}  fp32 {ef:.3e}")
     assert es <= 1e-6 and ef <= 1e-6
     assert torch.equal(acts, actf) and rel_fro(acts, act_ref) <= 1e-6
+    # the default mode runs fp32 X on the fp32 MFMA kernel: the same bits
+    assert torch.equal(_upper(Hd, iu), _upper(Hf, iu)) and torch.equal(actd, actf)
 
 
 def test_split_fp32_x_wide_dynamic_range():

@@ -7,7 +7,7 @@ workspace is the library's per-GPU scratch array), through the C ABI against rq_
   tiles along the tokens, or pick another kernel) H's upper triangle must agree to rel.
   Frobenius 1e-5 (the suite's bar for H) and act_square exactly;
 - two calls in a row on different shapes (the second smaller), each accumulated over two
-  chunks, and fp16 / bf16 / fp32 inputs;
+  chunks, and fp16 / bf16 / fp32 inputs, in the default and the opt-in split16 Hessian mode;
 - a chunk needing more than RQ_NOALLOC_SCRATCH_BYTES is refused with RQ_EINVAL before any
   launch.
 """
@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from gptq_plus_mp_quant_amd import _native as nat
+from gptq_plus_mp_quant_amd import kernels as K
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -51,19 +52,23 @@ def _run(x, s, mode, ws_bytes=None):
     return H, act
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-def test_noalloc_matches_workspace_entry(dtype):
+@pytest.mark.parametrize("dtype,math", [(torch.float16, "split16x3"), (torch.bfloat16, "split16x3"),
+                                        (torch.float32, "split16x3"), (torch.float16, "split16"),
+                                        (torch.float32, "split16")])
+def test_noalloc_matches_workspace_entry(dtype, math):
     for ntok, C, G, seed in ((9000, 1536, 4, 1), (700, 200, 3, 2)):
-        print(f"noalloc: ntok={ntok} C={C} G={G} {dtype}", flush=True)
+        print(f"noalloc: ntok={ntok} C={C} G={G} {dtype} {math}", flush=True)
         x, s = _inputs(ntok, C, G, dtype, seed)
-        H_n, a_n = _run(x, s, "noalloc")
-        H_w, a_w = _run(x, s, "workspace", ws_bytes=nat.RQ_NOALLOC_SCRATCH_BYTES)
+        with K.hessian_math(math):
+            H_n, a_n = _run(x, s, "noalloc")
+            H_w, a_w = _run(x, s, "workspace", ws_bytes=nat.RQ_NOALLOC_SCRATCH_BYTES)
+            H_f, a_f = _run(x, s, "workspace")
         assert torch.equal(H_n, H_w) and torch.equal(a_n, a_w)
-        H_f, a_f = _run(x, s, "workspace")
         assert torch.equal(a_n, a_f)
         # the upper triangle (what rq_hessian_accum defines; finalize mirrors it): the two
-        # workspaces may choose different kernels (fp32 X: the split kernel needs more than the
-        # scratch at the first shape), whose lower triangles hold different partial values
+        # workspaces may choose different kernels (fp32 X in the split16 mode: its split kernel
+        # needs more than the scratch at the first shape), whose lower triangles hold different
+        # partial values
         iu = torch.triu_indices(C, C, device=DEV)
         Hn_u, Hf_u = H_n[:, iu[0], iu[1]].double(), H_f[:, iu[0], iu[1]].double()
         err = float((Hn_u - Hf_u).norm() / Hf_u.norm())
