@@ -5,7 +5,8 @@
 // upper factor U of H^-1 (U^T U = H^-1) is obtained with ONE factorisation: with P the
 // index-reversal permutation and L L^T = P H P,  U = P L^-1 P.  The factorisation and the
 // inverse L^-1 run together in one right-looking blocked pass in fp64 (64-wide blocks
-// inside 256-wide panels, 512-wide from C = 8192):
+// inside 256-wide panels; from C = 8192 512-wide panels, each factored as two 256-wide
+// halves):
 //   per block k:  L_kk = chol(A_kk), T = L_kk^-1, L_ik = A_ik T^T and X_k = T B_k (row block k
 //                 of L^-1) in one launch (k_chol_step: every workgroup factors the 64 x 64
 //                 block itself, then does its GEMM tiles),
@@ -888,9 +889,9 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
   // NBW / NB times less often.
   const int NBW = panel_width(C);
   int rc;
-  // The factorisation of one panel: per NB block the diagonal factor and inverse, the block
-  // column of L and row block of L^-1, and the update of the panel's later columns.
-  auto factor_panel = [&](int k, int pe) -> int {
+  // The factorisation of columns [k, pe): per NB block the diagonal factor and inverse, the
+  // block column of L and row block of L^-1, and the update of the later columns up to pe.
+  auto factor_cols = [&](int k, int pe) -> int {
     for (int j = k; j < pe; j += NB) {
       const int jb = (pe - j < NB) ? (pe - j) : NB;
       const int below = C - j - jb;                      // rows below this block (whole matrix)
@@ -903,11 +904,11 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
       hipLaunchKernelGGL(k_chol_step, dim3(per_entry, 1, nb), dim3(CD_THREADS), 0, s, sa);
       RQ_CHECK_LAUNCH();
       int r;
-      // one launch, inside the panel: A[j+jb:, j+jb:pe] -= L[j+jb:, j] L[j+jb:pe, j]^T (lower
-      // tiles) and the panel rows of L^-1: B[j+jb:pe, 0:j+jb] -= L[j+jb:pe, j] X_j.  On the
-      // 128-tile panel kernel with 512-wide panels (up to 448 columns); the narrower updates of
-      // 256-wide panels have too few 128-tiles and run faster on the 64-tile GEMM.
-      if (pend > 0 && NBW > 256 && launch_panel(A + (int64_t)(j + jb) * C + j, Linv + (int64_t)j * C,
+      // one launch, inside [k, pe): A[j+jb:, j+jb:pe] -= L[j+jb:, j] L[j+jb:pe, j]^T (lower
+      // tiles) and those rows of L^-1: B[j+jb:pe, 0:j+jb] -= L[j+jb:pe, j] X_j.  On the 128-tile
+      // panel kernel when [k, pe) is wider than 256 (up to 448 columns); the narrower updates
+      // have too few 128-tiles and run faster on the 64-tile GEMM.
+      if (pend > 0 && pe - k > 256 && launch_panel(A + (int64_t)(j + jb) * C + j, Linv + (int64_t)j * C,
                                    A + (int64_t)(j + jb) * C + (j + jb), Linv + (int64_t)(j + jb) * C,
                                    C, jb, below, pend, pend, j + jb, ws, info, nb, s)) {
         RQ_CHECK_LAUNCH();
@@ -944,6 +945,22 @@ extern "C" int rq_chol_hinv_attempt(float* H_work, int C, int nb, const double* 
     return launch_gemm_pair(h, g, st, nb);
   };
 
+  // One panel [k, pe).  A 512-wide panel is factored as two 256-wide halves: the first half's
+  // blocks update only its own later columns (rank 64 each), one rank-256 update then carries
+  // the first half into the second half's columns (all rows below) and rows of L^-1, and the
+  // second half follows.  The same operations as one pass over the panel, grouped so that
+  // more of the in-panel work runs at the rank-256 rate (C = 14336, 4 subgroups: 143.3 ->
+  // 141.0 ms per chain).
+  auto factor_panel = [&](int k, int pe) -> int {
+    if (pe - k > 256) {
+      const int h = k + 256;
+      int r;
+      if ((r = factor_cols(k, h))) return r;
+      if ((r = trailing(k, 256, h, C - h, pe - h, pe - h, h, s))) return r;
+      return factor_cols(h, pe);
+    }
+    return factor_cols(k, pe);
+  };
   // Look-ahead over two streams, for the 512-wide panels (C >= 8192: at C = 4096 the overlap
   // gains less than the latency-bound factorisation kernels lose while the far update holds the
   // CUs).  After panel p the trailing update is split: the near part

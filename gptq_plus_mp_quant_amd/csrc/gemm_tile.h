@@ -73,8 +73,19 @@ struct GemmArgs {
 
 constexpr int GT = 64;
 constexpr int GKT = 32;
-constexpr int GPAD = 4;
 constexpr int GCH = 8;   // consecutive elements per thread in a slab fetch
+// LDS row padding of the 64-wide slabs.  fp64: a row of 65 doubles (130 dwords, 2 banks past
+// a multiple of 32) spreads every access pattern below evenly over the 32 banks: the MFMA
+// operand reads (4 rows x 16 consecutive doubles per instruction) and all four slab stores
+// (8 rows x 8 threads 8 doubles apart, or 4 rows x 16 consecutive threads).  fp32 keeps 68.
+template <typename T>
+struct GPad {
+  static constexpr int v = 4;
+};
+template <>
+struct GPad<double> {
+  static constexpr int v = 1;
+};
 
 template <typename T>
 __device__ __forceinline__ void load_chunk(const T* __restrict__ src, bool vec, T (&r)[GCH]) {
@@ -92,8 +103,8 @@ __device__ __forceinline__ void load_chunk(const T* __restrict__ src, bool vec, 
 // One 64x64 output tile (row tile ti, column tile tj) of batch entry bz.
 template <typename T, bool TA, bool TB>
 __device__ __forceinline__ void gemm_tile_body(GemmArgs<T> p, int ti, int tj, int bz,
-                                               T (*__restrict__ As)[GT + GPAD],
-                                               T (*__restrict__ Bs)[GT + GPAD]) {
+                                               T (*__restrict__ As)[GT + GPad<T>::v],
+                                               T (*__restrict__ Bs)[GT + GPad<T>::v]) {
   using acc_t = typename Mfma16<T>::acc_t;
   if (p.abort_flag && p.abort_flag[bz]) return;
   p.A += bz * p.sA;
@@ -259,8 +270,8 @@ __device__ __forceinline__ void gemm_tile_body(GemmArgs<T> p, int ti, int tj, in
 
 template <typename T, bool TA, bool TB>
 __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
-  __shared__ T As[GKT][GT + GPAD];
-  __shared__ T Bs[GKT][GT + GPAD];
+  __shared__ T As[GKT][GT + GPad<T>::v];
+  __shared__ T Bs[GKT][GT + GPad<T>::v];
   gemm_tile_body<T, TA, TB>(p, blockIdx.y, blockIdx.x, blockIdx.z, As, Bs);
 }
 
@@ -268,8 +279,8 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs<T> p) {
 // (A B^T), the rest to p2 (A B); grid.z is the batch entry of both.
 template <typename T>
 __global__ __launch_bounds__(256) void k_gemm_pair(GemmArgs<T> p1, GemmArgs<T> p2, int n1x, int n1, int n2x) {
-  __shared__ T As[GKT][GT + GPAD];
-  __shared__ T Bs[GKT][GT + GPAD];
+  __shared__ T As[GKT][GT + GPad<T>::v];
+  __shared__ T Bs[GKT][GT + GPad<T>::v];
   const int b = blockIdx.x;
   if (b < n1) gemm_tile_body<T, false, true>(p1, b / n1x, b % n1x, blockIdx.z, As, Bs);
   else gemm_tile_body<T, false, false>(p2, (b - n1) / n2x, (b - n1) % n2x, blockIdx.z, As, Bs);
