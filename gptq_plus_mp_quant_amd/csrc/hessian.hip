@@ -279,8 +279,13 @@ __device__ __forceinline__ void reduce_slices(const float* __restrict__ part0, i
     }
 }
 
+// Four workgroups per CU for 16-bit X; three for fp32 X, whose twice larger prefetch registers
+// would otherwise spill at the four-workgroup budget of 128 VGPRs.
 template <typename TX>
-__global__ __launch_bounds__(HTHREADS, 4) void k_hessian_accum(
+constexpr int accum_wgs() { return sizeof(TX) == 4 ? 3 : 4; }
+
+template <typename TX>
+__global__ __launch_bounds__(HTHREADS, accum_wgs<TX>()) void k_hessian_accum(
     const TX* __restrict__ X, int64_t ntok, int64_t ldx, int C, HTargets tg, int ntarg, int nt,
     int ntiles, bool vec_ok, int full, int S, float* __restrict__ ws, int* __restrict__ cnt) {
   __shared__ __attribute__((aligned(16))) float As[HT][HS];
@@ -1636,7 +1641,7 @@ hipEvent_t timing_begin(hipStream_t s) {
 // Concurrent workgroups of a Hessian kernel on the current device (CUs x occupancy).
 template <typename K>
 int kernel_slots(K kfn, int threads, int which) {
-  static int cache[2][64];
+  static int cache[3][64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   if (cache[which][dev] > 0) return cache[which][dev];
@@ -1647,6 +1652,8 @@ int kernel_slots(K kfn, int threads, int which) {
   return cache[which][dev];
 }
 int hessian_slots() { return kernel_slots(k_hessian_accum<__half>, HTHREADS, 0); }
+int hessian_slots32() { return kernel_slots(k_hessian_accum<float>, HTHREADS, 2); }
+int accum_slots(int x_dtype) { return x_dtype == RQ_F32 ? hessian_slots32() : hessian_slots(); }
 int split_slots() { return kernel_slots(k_hessian_split<__half, 3>, XTHREADS, 1); }
 
 // Items of the last, partly filled round and their slice count: the most slices that still
@@ -1968,7 +1975,7 @@ int launch_hessian(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
     if (rc) return rc;
   }
   int tail = 0, S = 1;
-  if (aligned) tail_split(total, (ntok + HKC - 1) / HKC, hessian_slots(), 8, &tail, &S);
+  if (aligned) tail_split(total, (ntok + HKC - 1) / HKC, accum_slots(x_dtype), 8, &tail, &S);
   if (tail > 0 && ws_bytes < hessian_ws_bytes(ntok, C, tail, S)) {
     tail = 0;                                     // no room: whole items only
     S = 1;
@@ -2016,7 +2023,7 @@ extern "C" int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets,
   for (int t0 = 0; t0 < ntargets; t0 += HMAXT) {   // per launch of at most 32 targets
     const int n = (ntargets - t0 < HMAXT) ? (ntargets - t0) : HMAXT;
     int tail = 0, S = 1;
-    tail_split((int64_t)nt * (nt + 1) / 2 * n, (ntok + HKC - 1) / HKC, hessian_slots(), 8, &tail, &S);
+    tail_split((int64_t)nt * (nt + 1) / 2 * n, (ntok + HKC - 1) / HKC, accum_slots(x_dtype), 8, &tail, &S);
     int64_t b = hessian_ws_bytes(ntok, C, tail, S);
     const int64_t bs = x_dtype == RQ_F32 ? split32_ws_need(ntok, C, n) : split_ws_need(ntok, C, n);
     if (bs > b) b = bs;
