@@ -292,11 +292,12 @@ def test_cholesky_chain(C):
     assert rel_fro(Hw, Hd_ref) <= 1e-7
 
 
-@pytest.mark.parametrize("C", [8200])
+@pytest.mark.parametrize("C", [8200, 8520])
 def test_cholesky_chain_wide_panels(C):
-    """C >= 8192 runs 512-wide panels (K = 512 panel updates, 4-row tile bands) with a ragged
-    last panel; checked against the float64 upper Cholesky factor of H_work^-1 (numpy / scipy
-    on the host)."""
+    """C >= 8192 runs 512-wide panels (K = 512 panel updates, 4-row tile bands), each factored
+    as two 256-wide halves joined by a rank-256 update, with a ragged last panel (C = 8200: 8
+    columns, one pass; C = 8520: 328 columns, halves of 256 and 72); checked against the float64
+    upper Cholesky factor of H_work^-1 (numpy / scipy on the host)."""
     g = torch.Generator(device=DEV)
     g.manual_seed(C)
     A = torch.randn(2 * C, C, device=DEV, generator=g)
