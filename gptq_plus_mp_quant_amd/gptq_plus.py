@@ -697,7 +697,8 @@ class ChainRequest:
                        for a in ("Hinv_init_all", "Hinv_diag")) and r.percdamp == prev.percdamp
             contiguous = same and all(
                 getattr(r, a) is None or
-                getattr(r, a).data_ptr() == getattr(prev, a).data_ptr() + getattr(prev, a).numel() * 4
+                getattr(r, a).data_ptr() == getattr(prev, a).data_ptr() +
+                getattr(prev, a).numel() * getattr(prev, a).element_size()
                 for a in ("H_work", "Hinv_all", "Hinv_init_all", "Hinv_diag"))
             if contiguous:
                 cur.append(r)
