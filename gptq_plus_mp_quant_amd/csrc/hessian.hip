@@ -537,11 +537,14 @@ __device__ __forceinline__ void split_staged(const uint8_t* st, int wave, int la
 // After the barrier: stage step k+XDEPTH-1 (row fragment w, this wave's column fragment), read
 // the next step's column fragment and saliencies, then work through the row blocks in pairs:
 // the pair's PC x 2 MFMAs (smallest piece first into each accumulator, the two accumulators
-// alternating), the split of one token pair of the next step's column fragment, then the pair's
-// row fragments of the next step, which this step no longer reads.  The pairs are pinned with
-// sched_barrier: left alone, the compiler sinks all the next step's LDS reads behind the last
-// MFMA, so every wave then waits on a burst of LDS reads right before the barrier (measured:
-// MFMA busy 67 / 72 % -> 71 / 76 % at C = 4096 / 14336 with the reads spread).  The saliency
+// alternating), with the pair's row fragments of the next step (which this step no longer
+// reads) issued after its first two MFMAs and the split of one token pair of the next step's
+// column fragment after the next two.  Each piece of work is pinned between sched_barriers:
+// left alone, the compiler sinks all the next step's LDS reads behind the last MFMA, so every
+// wave then waits on a burst of LDS reads right before the barrier (measured: MFMA busy
+// 67 / 72 % -> 71 / 76 % at C = 4096 / 14336 with the reads spread after each pair's six
+// MFMAs; placing them after its first two instead, and the split after the next two, gained
+// another 1-1.5 % over that; groups of 4 or 8 row blocks lost 2 / 7 %).  The saliency
 // staging (wave 0, lanes 0-3, a branch) comes last, so the step's main work is one scheduling
 // region.  Its vmcnt accounting is unchanged: wave 0's saliency load of step k+XDEPTH-1 still
 // follows that step's row / column loads.
@@ -585,12 +588,15 @@ __device__ __forceinline__ void split_step(uint4 (&p)[2][PC], uint4 (&a)[2][8], 
         acc[b0] = T::mfma(__builtin_bit_cast(v8, a[KP][b0]), __builtin_bit_cast(v8, p[KP][q]), acc[b0]);
       if (!DIAG || b1 < lim)
         acc[b1] = T::mfma(__builtin_bit_cast(v8, a[KP][b1]), __builtin_bit_cast(v8, p[KP][q]), acc[b1]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (q == PC - 1) {            // after the first MFMA pair: the pair's next-step row fragments
+        if (!DIAG || b0 < lim) a[NP][b0] = *reinterpret_cast<const uint4*>(nxt + b0 * 1024);
+        if (!DIAG || b1 < lim) a[NP][b1] = *reinterpret_cast<const uint4*>(nxt + b1 * 1024);
+      }
+      if (q == PC - 2)              // after the second: the split of token pair j
+        split_pair<TX, PC>(xw[j], sv[2 * j], sv[2 * j + 1], sc, o[0][j], o[1][j], o[2][j]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    split_pair<TX, PC>(xw[j], sv[2 * j], sv[2 * j + 1], sc, o[0][j], o[1][j], o[2][j]);
-    __builtin_amdgcn_sched_barrier(0);
-    if (!DIAG || b0 < lim) a[NP][b0] = *reinterpret_cast<const uint4*>(nxt + b0 * 1024);
-    if (!DIAG || b1 < lim) a[NP][b1] = *reinterpret_cast<const uint4*>(nxt + b1 * 1024);
-    __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
   for (int q = 0; q < PC; ++q) p[NP][q] = make_uint4(o[q][0], o[q][1], o[q][2], o[q][3]);
