@@ -1,7 +1,10 @@
 """Parity with the reference's op sequence at the full BASELINE shapes of one linear:
 configs[0] (q_proj 4096 x 4096, NUM_GROUPS = 1, w4 asym per-channel, act_order, B = 128, GPTQ+
 term off) and configs[1] (the same with NUM_GROUPS = 4 and the GPTQ+ term on at alpha = 0),
-128 x 2048 calibration tokens fed in add_batch chunks of 16 samples.
+128 x 2048 calibration tokens fed in add_batch chunks of 16 samples; configs[1] also with bf16
+activations and weights (the reference's add_batch casts any float input to fp32, so the
+products are the same kind; the GPU forms them from three bf16 pieces of 8 bits each in every
+Hessian mode, and writes the weight back rounded to bf16).
 
 Three comparisons per case:
 - each side end to end on its own: the oracle accumulates its Hessians from the same chunks
@@ -36,17 +39,18 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 R = C = 4096
 N, T, BSZ = 128, 2048, 16
-CASES = {"configs0_q_proj_G1": dict(G=1, seed=11), "configs1_q_proj_G4": dict(G=4, seed=12)}
+CASES = {"configs0_q_proj_G1": dict(G=1, seed=11), "configs1_q_proj_G4": dict(G=4, seed=12),
+         "configs1_q_proj_G4_bf16": dict(G=4, seed=13, dtype=torch.bfloat16)}
 
 
-def _inputs(seed, G):
+def _inputs(seed, G, dtype=torch.float16):
     gen = torch.Generator(device=DEV)
     gen.manual_seed(seed)
-    X = torch.empty((N, T, C), dtype=torch.float16, device=DEV)
+    X = torch.empty((N, T, C), dtype=dtype, device=DEV)
     for i in range(N):
-        X[i] = torch.randn((T, C), generator=gen, device=DEV).half()
+        X[i] = torch.randn((T, C), generator=gen, device=DEV).to(dtype)
     X[:, :, torch.randperm(C, generator=gen, device=DEV)[:8]] *= 20
-    W = (torch.randn((R, C), generator=gen, device=DEV) * 0.02).half()
+    W = (torch.randn((R, C), generator=gen, device=DEV) * 0.02).to(dtype)
     s = torch.exp(torch.randn((N, T, G), generator=gen, device=DEV))
     for g in range(G):
         s[..., g].clamp_(max=float(torch.quantile(s[..., g].flatten(), 0.99)))
@@ -77,8 +81,9 @@ def _log(rec):
 def test_full_shape_parity(name):
     G, seed = CASES[name]["G"], CASES[name]["seed"]
     print(f"{name}: generating inputs", flush=True)
-    X, W, s, grad = _inputs(seed, G)
-    layer = torch.nn.Linear(C, R, bias=False).to(DEV, torch.float16)
+    dtype = CASES[name].get("dtype", torch.float16)
+    X, W, s, grad = _inputs(seed, G, dtype)
+    layer = torch.nn.Linear(C, R, bias=False).to(DEV, dtype)
 
     def gpu_obj():
         layer.weight.data.copy_(W)
