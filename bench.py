@@ -312,6 +312,15 @@ def hessian_flops(cfg):
     return cfg["G"] * ntok * cfg["C"] * (cfg["C"] + 1)
 
 
+def hessian_calls(cfg):
+    """add_batch product launches per unit (layer or linear): one per HESSIAN_ACCUM_BSZ-sample chunk
+    and distinct input (the layer's q/k/v and gate/up read one X each).  The split kernel issues
+    each call as several dispatches (one per round of whole items), so per-call figures are
+    totals over the call's dispatches."""
+    chunks = cfg["N"] // cfg["bsz"]
+    return chunks * (len(INPUT_WIDTH) if cfg["kind"] == "layer" else 1)
+
+
 def load_traffic(math, config):
     """Calibrated HBM bytes per product-kernel launch from the committed rocprofv3 measurement,
     used only when it was taken on this configuration with the current hessian.hip."""
@@ -635,6 +644,9 @@ def stats_table(path, cfg, units, config):
                 tf = fl / (per * 1e-3) / 1e12
                 wtxt = f"{fl / 1e9:.1f} GFLOP" + (f", {b / 1e6:.0f} MB" if b else "")
                 ach = f"{tf:.1f} TF/s" + (f" ({100 * tf / peak:.1f} % of {peak})" if peak else "")
+                if key in ("k_hessian_split", "k_hessian_accum"):
+                    # the live launch time covers one add_batch call, which may span dispatches
+                    ach += f"; {per / hessian_calls(cfg):.3f} ms per add_batch call"
                 if b and key in ("k_quant_block", "k_block_lookahead"):
                     ach += f"; {b / (per * 1e-3) / 1e9:.0f} GB/s"
             else:
@@ -681,22 +693,24 @@ def traffic_report(fetch_csv, write_csv, cal_fetch_csv, cal_write_csv, kernel_pr
     """HBM bytes per product-kernel launch from FETCH_SIZE / WRITE_SIZE passes (KiB per dispatch),
     each scaled by what the counter reads for a 1 GiB device copy; written to TRAFFIC_JSON with
     the source hash of hessian.hip so bench.py only reports it while the kernel is unchanged."""
-    def per_dispatch(path, counter, pred):
+    def per_dispatch(path, counter, pred, calls=None):
         vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(path))
                 if r["Counter_Name"] == counter and pred(r["Kernel_Name"])]
-        return sum(vals) / max(len(vals), 1), len(vals)
+        return sum(vals) / max(calls or len(vals), 1), len(vals)
     is_k = lambda n: kernel_prefix in n
     is_copy = lambda n: "copyBuffer" in n
-    fetch, nf = per_dispatch(fetch_csv, "FETCH_SIZE", is_k)
-    write, nw = per_dispatch(write_csv, "WRITE_SIZE", is_k)
+    # per add_batch call (one profiled step: hessian_calls(cfg) calls, each one or more dispatches)
+    ncalls = hessian_calls(cfg)
+    fetch, nf = per_dispatch(fetch_csv, "FETCH_SIZE", is_k, ncalls)
+    write, nw = per_dispatch(write_csv, "WRITE_SIZE", is_k, ncalls)
     cfetch, _ = per_dispatch(cal_fetch_csv, "FETCH_SIZE", is_copy)
     cwrite, _ = per_dispatch(cal_write_csv, "WRITE_SIZE", is_copy)
     gib = float(1 << 30)
     rf, wf = cfetch * 1024 / gib, cwrite * 1024 / gib          # counter bytes per real byte
     traffic = fetch * 1024 / rf + write * 1024 / wf
     flops = hessian_flops(cfg)
-    rec = {"kernel": kernel_prefix, "config": config, "dispatches": [nf, nw],
-           "fetch_size_kib_per_dispatch": round(fetch, 1), "write_size_kib_per_dispatch": round(write, 1),
+    rec = {"kernel": kernel_prefix, "config": config, "dispatches": [nf, nw], "calls": ncalls,
+           "fetch_size_kib_per_call": round(fetch, 1), "write_size_kib_per_call": round(write, 1),
            "copy_calibration": {"fetch_kib": round(cfetch, 1), "write_kib": round(cwrite, 1),
                                 "read_factor": round(rf, 3), "write_factor": round(wf, 3)},
            "traffic_bytes_per_launch": int(traffic), "hessian_src_sha256": source_sha(),

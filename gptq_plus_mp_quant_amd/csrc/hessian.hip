@@ -22,6 +22,7 @@
 // fixed summation order, and results are bitwise reproducible run to run.
 #include "rq_common.h"
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <type_traits>
@@ -755,11 +756,14 @@ __device__ __forceinline__ void reduce_split_slices(const float* __restrict__ pa
   }
 }
 
+// One launch covers a segment of the item list: its `segn` whole items from list position seg0
+// on (od_seg of them off-diagonal), dealt to the XCDs as item_position describes, followed in the
+// last segment by the tail's token slices (the list's items from `full` on, S slices each).
 template <typename TX, int PC>
 __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
     const uint16_t* __restrict__ XB, int C, const float* __restrict__ sT, int64_t lds_stride,
-    const float* __restrict__ scale, HTargets tg, int ntarg, int nt, int ntiles, int64_t nks, int full,
-    int S, float* __restrict__ ws, int* __restrict__ cnt) {
+    const float* __restrict__ scale, HTargets tg, int ntarg, int nt, int ntiles, int64_t nks, int seg0,
+    int segn, int od_seg, int full, int S, float* __restrict__ ws, int* __restrict__ cnt) {
   __shared__ __attribute__((aligned(16))) uint8_t lds0[XSTAGE];
   __shared__ __attribute__((aligned(16))) uint8_t lds1[XSTAGE];
   __shared__ __attribute__((aligned(16))) uint8_t lds2[XSTAGE];
@@ -777,10 +781,10 @@ __global__ __launch_bounds__(XTHREADS, 1) void k_hessian_split(
   const int b = blockIdx.x;
   int logical, slice = -1;
   int64_t kbeg = 0, kend = nks;
-  if (b < full) {
-    logical = item_position(b, full, nt * (nt - 1) / 2 * ntarg);
+  if (b < segn) {
+    logical = seg0 + item_position(b, segn, od_seg);
   } else {
-    const int tb = b - full;
+    const int tb = b - segn;
     logical = full + tb / S;
     slice = tb % S;
     kbeg = nks * slice / S;
@@ -1814,6 +1818,16 @@ int64_t split_ws_need(int64_t ntok, int C, int ntarg) {
   return split_layout(ntok, C, ntarg, tail, S).bytes;
 }
 
+// Whole items per launch of the split kernel, in rounds of `slots` workgroups (see launch_split).
+// One round per launch: all its workgroups start together and do equal work, so the targets of
+// a tile and the tiles of a super-row read their X strips through the XCD's L2 in step.  In one
+// launch of many rounds the workgroups' start times drift apart from round to round (25 rounds
+// per configs[2] down_proj call), and they re-read the strips from HBM.  Measured on the
+// configs[2] layer (two boxes, two A/B passes each): HBM fetch of the split kernel -40 % per
+// layer; layer time -2.0 / -1.8 / -1.5 / -1.6 % with 1 / 2 / 3 / 4 rounds per launch, -1.0 /
+// -0.2 % with 3 / 5 rounds on the other box.
+constexpr int XSEG_ROUNDS = 1;
+
 int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, const HTargets& tg,
                  int ntarg, void* ws, int64_t ws_bytes, hipStream_t s) {
   int nt, ntiles;
@@ -1855,19 +1869,31 @@ int launch_split(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C, c
   const int full = (int)(total - tail);
   int* cnt = tail > 0 ? reinterpret_cast<int*>(ws) : nullptr;
   float* wsf = tail > 0 ? reinterpret_cast<float*>(wb + L.off_part) : nullptr;
-  dim3 grid((unsigned)(full + (int64_t)tail * S));
+  const int od_items = nt * (nt - 1) / 2 * ntarg;
+  // Segments of XSEG_ROUNDS rounds of whole items, each a launch of its own (the tail's slices
+  // ride with the last): the kernel boundary brings every XCD's workgroups back in step.
+  const int slots = split_slots();
+  const int rounds = slots > 0 ? full / slots : 0;
+  const int nseg = (XSEG_ROUNDS > 0 && rounds > XSEG_ROUNDS) ? (rounds + XSEG_ROUNDS - 1) / XSEG_ROUNDS : 1;
   hipEvent_t stop = timing_begin(s);
   const dim3 block(XTHREADS);
-  if (x_dtype == RQ_F16 && g_hmath.load() == RQ_HMATH_SPLIT16X3)
-    hipLaunchKernelGGL((k_hessian_split<__half, 3>), grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg, ntarg, nt,
-                       ntiles, nks, full, S, wsf, cnt);
-  else if (x_dtype == RQ_F16)
-    hipLaunchKernelGGL((k_hessian_split<__half, 2>), grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg, ntarg, nt,
-                       ntiles, nks, full, S, wsf, cnt);
-  else
-    hipLaunchKernelGGL((k_hessian_split<__hip_bfloat16, 3>), grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg,
-                       ntarg, nt, ntiles, nks, full, S, wsf, cnt);
-  RQ_CHECK_LAUNCH();
+  for (int q = 0; q < nseg; ++q) {
+    const int p0 = (nseg == 1) ? 0 : (int)((int64_t)rounds * q / nseg) * slots;
+    const int p1 = (q + 1 == nseg) ? full : (int)((int64_t)rounds * (q + 1) / nseg) * slots;
+    const int segn = p1 - p0;
+    const int od_seg = std::min(segn, std::max(0, od_items - p0));
+    const dim3 grid((unsigned)(segn + (q + 1 == nseg ? (int64_t)tail * S : 0)));
+    if (x_dtype == RQ_F16 && g_hmath.load() == RQ_HMATH_SPLIT16X3)
+      hipLaunchKernelGGL((k_hessian_split<__half, 3>), grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg, ntarg,
+                         nt, ntiles, nks, p0, segn, od_seg, full, S, wsf, cnt);
+    else if (x_dtype == RQ_F16)
+      hipLaunchKernelGGL((k_hessian_split<__half, 2>), grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg, ntarg,
+                         nt, ntiles, nks, p0, segn, od_seg, full, S, wsf, cnt);
+    else
+      hipLaunchKernelGGL((k_hessian_split<__hip_bfloat16, 3>), grid, block, 0, s, xt, C, sT, L.ntok_p, scale, tg,
+                         ntarg, nt, ntiles, nks, p0, segn, od_seg, full, S, wsf, cnt);
+    RQ_CHECK_LAUNCH();
+  }
   if (stop && hipEventRecord(stop, s) != hipSuccess) return RQ_EHIP;
   return RQ_OK;
 }
