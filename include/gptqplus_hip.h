@@ -81,10 +81,11 @@ int64_t rq_hessian_workspace_bytes(int64_t ntok, int C, int ntargets, int x_dtyp
 #define RQ_HMATH_SPLIT16X3 2
 int rq_hessian_math(int mode);
 /* Measurement hook, no counterpart in the reference: the next Hessian product-kernel launch
- * (k_hessian_split or k_hessian_accum, whichever runs) records start_event before it and
- * stop_event after it on its stream, so a caller can time that kernel alone (hipEvent_t
- * handles created with timing enabled; both NULL clears).  Process-wide, one launch per
- * pair. */
+ * (k_hessian_split or k_hessian_accum, whichever runs; k_hessian_split issues one call's
+ * items as one dispatch per round of whole items, and the pair brackets all of them) records
+ * start_event before it and stop_event after it on its stream, so a caller can time that
+ * kernel alone (hipEvent_t handles created with timing enabled; both NULL clears).
+ * Process-wide, one call per pair. */
 int rq_hessian_timing_events(void* start_event, void* stop_event);
 int rq_hessian_accum(const void* x, int x_dtype, int64_t ntok, int64_t ldx, int C,
                      const float* sal, int64_t ld_sal, int G, float* H, float* act_sq,
