@@ -127,6 +127,29 @@ def test_split_nonfinite_like_fp32(mode):
     assert rel_fro(_upper(Hs, iu)[ok], _upper(Hf, iu)[ok]) <= 1e-6
 
 
+@pytest.mark.parametrize("n,C,G", [(256, 4096, 4), (512, 6000, 2)])
+def test_split_multi_round_matches_exact_sum(n, C, G):
+    """Calls whose whole items span several rounds of the GPU's workgroup slots, which the split
+    kernel issues as one dispatch per round with the tail's token slices in the last: at C = 4096,
+    G = 4, 544 items (two rounds and 32 items in 4 slices each); at C = 6000 (a ragged last tile),
+    G = 2, 600 items (two rounds and 88 items in 2 slices each).  Every tile must be formed once:
+    a missing or repeated tile would move H by far more than the fp32 bar."""
+    r = rng(2000 + n + C + G)
+    X = r.standard_normal((n, C), dtype=np.float32)
+    X[:, r.choice(C, 8, replace=False)] *= 20.0
+    x = torch.from_numpy(X).half()
+    sal = torch.from_numpy(np.minimum(r.lognormal(size=(n, G)), 10.0).astype(np.float32))
+    H, a, iu = _run(x, sal, "split16x3")
+    xd = x.to(DEV).double()
+    for g in range(G):
+        w = (x.to(DEV).float() * sal[:, g:g + 1].to(DEV)).double()     # fl32(x * s), exact in fp64
+        ref = (xd.T @ w).cpu()
+        err = rel_fro(H[g][iu[0], iu[1]], ref[iu[0], iu[1]])
+        print(f"multi-round n={n} C={C} G={G} group {g}: rel-Frobenius {err:.2e}", flush=True)
+        assert err <= 1e-6, (g, err)
+    assert torch.equal(a, (x.float() ** 2).sum(0)) or rel_fro(a, (x.double() ** 2).sum(0)) <= 1e-6
+
+
 def test_multi_target_split_equals_separate():
     r = rng(21)
     n, C = 1024, 640
