@@ -34,6 +34,15 @@ def rel_fro(a, b):
     return float((a - b).norm() / (den if den > 0 else 1.0))
 
 
+def w_rel_fro(a, b):
+    """||a - b||_F / ||b||_F of two weight tensors in float64, on a's device (the dequantized weights
+    the north star compares; each flipped code moves one weight by a quantisation step)."""
+    a = a.detach()
+    b = b.detach().to(a.device)
+    den = b.double().norm()
+    return float((a.double() - b.double()).norm() / (den if den > 0 else 1.0))
+
+
 def code_flips(a, b):
     a = a.double().cpu()
     b = b.double().cpu()

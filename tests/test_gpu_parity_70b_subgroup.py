@@ -34,7 +34,7 @@ import torch
 
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
-from tests._util import flip_report, rel_fro
+from tests._util import flip_report, rel_fro, w_rel_fro
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -132,7 +132,8 @@ def test_70b_width_subgroup_parity(width_case):
     n = res.W_int.numel()
     e_gpu = _recon(W, layer.weight.data, X)
     e_ref = _recon(W, res.Q.to(DEV), X)
-    rec = dict(case="configs4_width_subgroup", R=R, C=C, G=G, tokens=N * T, act_square_mismatch=act_bad,
+    w_own = w_rel_fro(layer.weight.data, res.Q)
+    rec = dict(case="configs4_width_subgroup", w_rel_fro_own_chain=w_own, R=R, C=C, G=G, tokens=N * T, act_square_mismatch=act_bad,
                perm_mismatch=perm_bad, flips_with_oracle_hinv=flips_inj, q_equal_with_oracle_hinv=q_equal,
                flips_own_chain=flips_own, codes=n, hinv_rel_fro=hinv_err, hinv_vs_fp64=gpu_vs_64,
                oracle_hinv_vs_fp64=ref_vs_64, recon_gpu=e_gpu, recon_oracle=e_ref,
@@ -178,7 +179,8 @@ def test_70b_width_subgroup_own_hessian(width_case):
     n = res.W_int.numel()
     e_gpu = _recon(W, layer.weight.data, X)
     e_ref = _recon(W, res.Q.to(DEV), X)
-    _log(dict(case="configs4_width_subgroup_own_hessian", R=R, C=C, G=G, tokens=N * T, codes=n,
+    w_own = w_rel_fro(layer.weight.data, res.Q)
+    _log(dict(case="configs4_width_subgroup_own_hessian", w_rel_fro=w_own, R=R, C=C, G=G, tokens=N * T, codes=n,
               act_square_mismatch=act_bad, perm_mismatch=perm_bad, h_rel_fro=h_err, flips=rep,
               recon_gpu=e_gpu, recon_oracle=e_ref, recon_rel_diff=abs(e_gpu - e_ref) / e_ref,
               oracle_damp=res.subgroups[0].damp_percent))

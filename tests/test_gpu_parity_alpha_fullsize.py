@@ -37,7 +37,7 @@ import torch
 
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
-from tests._util import rel_fro
+from tests._util import rel_fro, w_rel_fro
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -157,6 +157,7 @@ def test_gptqplus_term_parity_full_linear(case):
     Wx = float((W.float() @ x.T).double().pow(2).sum())
     e_gpu = float(((W.float() - layer.weight.data.float()) @ x.T).double().pow(2).sum()) / Wx
     e_ref = float(((W.float() - res.Q.to(DEV).float()) @ x.T).double().pow(2).sum()) / Wx
+    w_own = w_rel_fro(layer.weight.data, res.Q)
     g3.free()
     g.free()
     rec = dict(case=f"configs1_q_proj_G4_alpha_{case}", mode=mode, R=R, C=C, G=G, tokens=N * T, alpha=ALPHA, ref_loss=REF_LOSS,
@@ -165,7 +166,8 @@ def test_gptqplus_term_parity_full_linear(case):
                beta_rel_fro=beta_err, beta_rows_not_ieee=beta_ieee_bad, beta_rows_beyond_one_step=beta_step_bad,
                z_rel_fro_beta_rescaled=z_err, ghinv_rel_fro_beta_rescaled=gh_err,
                flips_with_oracle_hinv=flips_terms, flips_own_chain=flips_own, codes=n, hinv_rel_fro=hinv_err,
-               recon_gpu=e_gpu, recon_oracle=e_ref, recon_rel_diff=abs(e_gpu - e_ref) / e_ref)
+               recon_gpu=e_gpu, recon_oracle=e_ref, recon_rel_diff=abs(e_gpu - e_ref) / e_ref,
+               w_rel_fro_own_chain=w_own)
     print(json.dumps(rec), flush=True)
     path = os.environ.get("RQ_PARITY_LOG")
     if path:

@@ -33,7 +33,7 @@ import torch
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
 from gptq_plus_mp_quant_amd import kernels as K
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
-from tests._util import flip_report, rel_fro
+from tests._util import flip_report, rel_fro, w_rel_fro
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -143,6 +143,8 @@ def test_full_shape_parity(name):
     n = res.W_int.numel()
     e_gpu = _recon(W, layer.weight.data, X)
     e_ref = _recon(W, res.Q.to(DEV), X)
+    w_own_chain = w_rel_fro(layer.weight.data, res.Q)
+    w_own_h = w_rel_fro(layer.weight.data, res_own.Q)
     # (3) each side's own Hessian and chain: the GPU's default H (g2's) against the oracle's
     # own; then the opt-in two-piece Hessian, accumulated again
     own = flip_report(g2.codes, res_own.W_int, res_own.ratio, res_own.subgroups[0].perm)
@@ -157,6 +159,7 @@ def test_full_shape_parity(name):
     torch.cuda.synchronize()
     own2 = flip_report(g3.codes, res_own.W_int, res_own.ratio, res_own.subgroups[0].perm)
     e_own2_gpu = _recon(W, layer.weight.data, X)
+    w_own2 = w_rel_fro(layer.weight.data, res_own.Q)
     rec = dict(case=name, R=R, C=C, G=G, tokens=N * T, act_square_mismatch=act_bad, exact_ties_in_act_square=ties,
                perm_mismatch=perm_bad, flips_with_oracle_hinv=flips_inj, q_equal_with_oracle_hinv=q_equal,
                flips_own_chain=flips_own, codes=n, hinv_rel_fro=hinv_err, hinv_init_rel_fro=hinit_err,
@@ -166,7 +169,8 @@ def test_full_shape_parity(name):
                own_h_rel_fro=h_err, own_flips=own, own_recon_gpu=e_gpu, own_recon_oracle=e_own_ref,
                own_recon_rel_diff=abs(e_gpu - e_own_ref) / e_own_ref,
                split16_h_rel_fro=h2_err, split16_own_flips=own2, split16_own_recon_gpu=e_own2_gpu,
-               split16_own_recon_rel_diff=abs(e_own2_gpu - e_own_ref) / e_own_ref)
+               split16_own_recon_rel_diff=abs(e_own2_gpu - e_own_ref) / e_own_ref,
+               w_rel_fro_own_chain=w_own_chain, w_rel_fro_own_hessian=w_own_h, split16_w_rel_fro_own_hessian=w_own2)
     _log(rec)
     assert act_bad == 0
     assert perm_bad == 0

@@ -37,7 +37,7 @@ import torch
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer, add_batch_shared
 from gptq_plus_mp_quant_amd import kernels as K
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
-from tests._util import flip_report, rel_fro
+from tests._util import flip_report, rel_fro, w_rel_fro
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -157,7 +157,8 @@ def test_layer_linear_parity(layer_state, name):
     n = res.W_int.numel()
     e_gpu = _recon(W, layer.weight.data, xs[key])
     e_ref = _recon(W, res.Q.to(DEV), xs[key])
-    rec = dict(case=f"configs2_layer_{name}", R=R, C=C, G=G, tokens=N * T, act_square_mismatch=act_bad,
+    w_own = w_rel_fro(layer.weight.data, res.Q)
+    rec = dict(case=f"configs2_layer_{name}", R=R, C=C, G=G, tokens=N * T, act_square_mismatch=act_bad, w_rel_fro_own_chain=w_own,
                exact_ties_in_act_square=int(C - torch.unique(o.act_square).numel()), perm_mismatch=perm_bad,
                flips_with_oracle_hinv=flips_inj, q_equal_with_oracle_hinv=q_equal, flips_own_chain=flips_own,
                codes=n, hinv_rel_fro=hinv_err, hinv_init_rel_fro=hinit_err, recon_gpu=e_gpu, recon_oracle=e_ref,
@@ -224,15 +225,16 @@ def test_layer_linear_own_hessian(layer_state, name):
         g = _new_gpu(mods[name], layer, H, act, index, tokens)
         g.fasterquant(**FQ)
         torch.cuda.synchronize()
-        out[mode] = (flip_report(g.codes, res.W_int, res.ratio, perm), _recon(W, layer.weight.data, xs[key]))
+        out[mode] = (flip_report(g.codes, res.W_int, res.ratio, perm), _recon(W, layer.weight.data, xs[key]),
+                     w_rel_fro(layer.weight.data, res.Q))
         g.free()
-    rep3, e3 = out["split16x3"]
-    rep2, e2 = out["split16"]
+    rep3, e3, w3 = out["split16x3"]
+    rep2, e2, w2 = out["split16"]
     rec = dict(case=f"configs2_layer_{name}_own_hessian", R=R, C=C, G=G, tokens=N * T, codes=n,
                act_square_mismatch=act_bad, h_rel_fro=h_err, split16_h_rel_fro=h2_err,
                flips=rep3, recon_gpu=e3, recon_oracle=e_ref, recon_rel_diff=abs(e3 - e_ref) / e_ref,
                split16_flips=rep2, split16_recon_gpu=e2, split16_recon_rel_diff=abs(e2 - e_ref) / e_ref,
-               oracle_damp=[r.damp_percent for r in res.subgroups])
+               oracle_damp=[r.damp_percent for r in res.subgroups], w_rel_fro=w3, split16_w_rel_fro=w2)
     _log(rec)
     assert act_bad == 0
     assert max(h_err) <= 1e-4 and max(h2_err) <= 1e-4

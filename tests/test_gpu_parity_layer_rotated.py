@@ -42,7 +42,7 @@ import torch
 
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer, add_batch_shared
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
-from tests._util import flip_report, rel_fro
+from tests._util import flip_report, rel_fro, w_rel_fro
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -167,6 +167,7 @@ def test_rotated_layer_linear_parity(rotated_layer, name):
     n = res.W_int.numel()
     e_gpu = _recon(W, layer.weight.data, xs[key])
     e_ref = _recon(W, res.Q.to(DEV), xs[key])
+    w_own = w_rel_fro(layer.weight.data, res.Q)
     # subgroup 0's damped working matrix factorised in fp64 on the host (no act_order: no
     # permutation; dead columns as the chain handles them)
     sub = 0
@@ -185,7 +186,7 @@ def test_rotated_layer_linear_parity(rotated_layer, name):
               flips_with_oracle_hinv=flips_inj, flips_own_chain=flips_own, codes=n, hinv_rel_fro=hinv_err,
               hinv_vs_fp64_host=gpu_vs_64, oracle_hinv_vs_fp64_host=ref_vs_64,
               recon_gpu=e_gpu, recon_oracle=e_ref, recon_rel_diff=abs(e_gpu - e_ref) / e_ref,
-              oracle_hinv_flip_report=rep_inj, own_chain_flip_report=rep_own))
+              oracle_hinv_flip_report=rep_inj, own_chain_flip_report=rep_own, w_rel_fro_own_chain=w_own))
     assert act_bad == 0
     assert hinv_err <= 1e-4
     assert gpu_vs_64 <= 1e-6 and gpu_vs_64 < ref_vs_64
@@ -230,7 +231,8 @@ def test_rotated_layer_linear_own_hessian(rotated_layer, name):
     n = res.W_int.numel()
     e_gpu = _recon(W, layer.weight.data, xs[key])
     e_ref = _recon(W, res.Q.to(DEV), xs[key])
-    _log(dict(case=f"configs3_rotated_{name}_own_hessian", R=R, C=C, G=G, tokens=N * T, codes=n,
+    w_own = w_rel_fro(layer.weight.data, res.Q)
+    _log(dict(case=f"configs3_rotated_{name}_own_hessian", w_rel_fro=w_own, R=R, C=C, G=G, tokens=N * T, codes=n,
               act_square_mismatch=act_bad, h_rel_fro=h_err, flips=rep, recon_gpu=e_gpu, recon_oracle=e_ref,
               recon_rel_diff=abs(e_gpu - e_ref) / e_ref, oracle_damp=[r.damp_percent for r in res.subgroups]))
     g.free()
