@@ -1,7 +1,8 @@
 """bench.py's report helpers on synthetic rocprofv3 CSVs (no GPU): the kernel-statistics table
 credits each kernel with its algorithmic work (the look-ahead column loop with the trailing
-update and every block but the first, the row gathers by variant), and the counter table's
-MFMA-busy arithmetic."""
+update and every block but the first, the row gathers by variant), the counter table's
+MFMA-busy arithmetic, and the traffic record's per-call accounting (a split-kernel call spans
+several dispatches) with the copy calibration."""
 import contextlib
 import csv
 import io
@@ -93,3 +94,35 @@ def test_more_than_one_gpu_is_refused_before_any_device_work():
     assert res.returncode == 2
     assert "one GPU only" in res.stdout + res.stderr
     assert not res.stdout.strip().startswith("{")
+
+
+def _pmc_csv(path, kernel, counter, values):
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        for i, v in enumerate(values):
+            w.writerow([i, kernel, counter, v])
+
+
+def test_traffic_report_per_add_batch_call(tmp_path, monkeypatch):
+    """8 add_batch calls per linear; 3 dispatches per call of 1000 KiB FETCH_SIZE and
+    one of 100 KiB WRITE_SIZE; the copy reads as half its bytes (FETCH) and all of them (WRITE).
+    Per call: 3000 KiB / 0.5 + 100 KiB / 1.0 = 6 144 000 + 102 400 bytes."""
+    out = tmp_path / "traffic.json"
+    monkeypatch.setattr(bench, "TRAFFIC_JSON", str(out))      # never the committed record
+    k = "void k_hessian_split<__half, 3>(...)"
+    _pmc_csv(tmp_path / "f.csv", k, "FETCH_SIZE", [1000.0] * 24)
+    _pmc_csv(tmp_path / "w.csv", k, "WRITE_SIZE", [100.0] * 8)
+    _pmc_csv(tmp_path / "cf.csv", "__amd_rocclr_copyBuffer", "FETCH_SIZE", [524288.0])
+    _pmc_csv(tmp_path / "cw.csv", "__amd_rocclr_copyBuffer", "WRITE_SIZE", [1048576.0])
+    assert bench.hessian_calls(bench.CONFIGS["cfg2"]) == 8
+    assert bench.hessian_calls(bench.CONFIGS["cfg3"]) == 32
+    with contextlib.redirect_stdout(io.StringIO()):
+        bench.traffic_report(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"), str(tmp_path / "cf.csv"),
+                             str(tmp_path / "cw.csv"), "k_hessian_split", "cfg2", bench.CONFIGS["cfg2"], "split16x3")
+    import json
+    rec = json.load(open(out))["split16x3"]
+    assert rec["calls"] == 8 and rec["dispatches"] == [24, 8]
+    assert rec["fetch_size_kib_per_call"] == 3000.0 and rec["write_size_kib_per_call"] == 100.0
+    assert rec["traffic_bytes_per_launch"] == 6144000 + 102400
+    assert rec["hessian_src_sha256"] == bench.source_sha()
