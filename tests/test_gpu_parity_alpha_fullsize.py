@@ -26,7 +26,13 @@ trailing update with Z != 0).
   GPU host gives 2^-24.  Z and GHinv scale with beta row by row;
 - with the GPU's own fp64 chain: H^-1 within 1e-4, reconstruction error within 0.5 % of the
   oracle's, code flips <= 0.02 %.
-The case's numbers are printed and appended to RQ_PARITY_LOG (JSON lines) when it is set.
+- each side end to end on its own (test_gptqplus_term_own_hessian, frozen mode, reference_loss
+  = 50 so that beta ~ 5e-3 is resolved well above fp32's step): the oracle forms its own H from
+  the same chunks and runs its own chain and terms; H within 1e-4 (rel. Frobenius, per group),
+  act_square and the permutation equal, reconstruction error within 0.5 %, the first flip of
+  each row an exact tie or within 4096 fp32 ulps of one (the two chains start from Hessians
+  that differ by the fp32 summation orders), at most 0.001 % of the codes, total below 0.1 %.
+The cases' numbers are printed and appended to RQ_PARITY_LOG (JSON lines) when it is set.
 """
 import json
 import os
@@ -37,7 +43,7 @@ import torch
 
 from gptq_plus_mp_quant_amd import GPTQPlus, WeightQuantizer
 from oracle.gptqplus_cpu import GPTQPlusOracle, make_quantizer
-from tests._util import rel_fro, w_rel_fro
+from tests._util import flip_report, rel_fro, w_rel_fro
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -181,3 +187,60 @@ def test_gptqplus_term_parity_full_linear(case):
     assert hinv_err <= 1e-4
     assert abs(e_gpu - e_ref) <= 0.005 * e_ref
     assert flips_own <= n // 5000
+
+
+def test_gptqplus_term_own_hessian():
+    ref_loss = 50.0
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(37)
+    X = torch.randn((N, T, C), generator=gen, device=DEV).half()
+    X[:, :, torch.randperm(C, generator=gen, device=DEV)[:8]] *= 20
+    W = (torch.randn((R, C), generator=gen, device=DEV) * 0.02).half()
+    s = torch.exp(torch.randn((N, T, G), generator=gen, device=DEV))
+    for k in range(G):
+        s[..., k].clamp_(max=float(torch.quantile(s[..., k].flatten(), 0.99)))
+    grad = torch.randn((R, C), generator=gen, device=DEV) * 1e-4
+    layer = torch.nn.Linear(C, R, bias=False).to(DEV, torch.float16)
+    g = _obj(layer, W, s, grad, ref_loss)
+    for j in range(0, N, BSZ):
+        g.add_batch(X[j:j + BSZ], None)
+    g.finalize_hessian()
+    torch.cuda.synchronize()
+    print("GPTQ+ term, own Hessians: oracle add_batch", flush=True)
+    o = GPTQPlusOracle(W.cpu(), s.cpu(), grad.cpu(), G, ALPHA, ref_loss)
+    o.quantizer = make_quantizer(4, False)
+    for j in range(0, N, BSZ):
+        o.add_batch(X[j:j + BSZ].cpu())
+    o.finalize_hessian()
+    h_err = [rel_fro(g.H[k], o.H[k]) for k in range(G)]
+    act_bad = int((g.act_square.cpu() != o.act_square).sum())
+    print(f"GPTQ+ term, own Hessians: H rel-Frobenius {h_err}; oracle fasterquant", flush=True)
+    res = o.fasterquant(record_ratio=True, **FQ)
+    g.fasterquant(**FQ)
+    torch.cuda.synchronize()
+    perm = res.subgroups[0].perm
+    perm_bad = int((g.perm.cpu() != perm).sum())
+    rep = flip_report(g.codes, res.W_int, res.ratio, perm)
+    n = res.W_int.numel()
+    x = X.reshape(-1, C).float()
+    Wx = float((W.float() @ x.T).double().pow(2).sum())
+    e_gpu = float(((W.float() - layer.weight.data.float()) @ x.T).double().pow(2).sum()) / Wx
+    e_ref = float(((W.float() - res.Q.to(DEV).float()) @ x.T).double().pow(2).sum()) / Wx
+    w_own = w_rel_fro(layer.weight.data, res.Q)
+    beta_g = torch.cat([i["beta"].reshape(-1).cpu() for i in g.subgroup_info])
+    beta_o = torch.cat([r.beta.reshape(-1) for r in res.subgroups])
+    rec = dict(case="configs1_q_proj_G4_alpha_frozen_refloss_50_own_hessian", R=R, C=C, G=G, tokens=N * T,
+               alpha=ALPHA, ref_loss=ref_loss, codes=n, act_square_mismatch=act_bad, perm_mismatch=perm_bad,
+               h_rel_fro=h_err, beta_rel_fro=rel_fro(beta_g, beta_o), beta_mean=float(beta_o.mean()), flips=rep,
+               recon_gpu=e_gpu, recon_oracle=e_ref, recon_rel_diff=abs(e_gpu - e_ref) / e_ref, w_rel_fro=w_own)
+    print(json.dumps(rec), flush=True)
+    path = os.environ.get("RQ_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(rec) + "\n")
+    g.free()
+    assert act_bad == 0 and perm_bad == 0
+    assert max(h_err) <= 1e-4
+    assert abs(e_gpu - e_ref) <= 0.005 * e_ref
+    assert rep["primary"] <= n // 100000 and rep.get("primary_ulps_le_4096", 0) == rep["primary"]
+    assert rep["flips"] <= n // 1000
